@@ -1,0 +1,240 @@
+"""Benchmark: BitNet-2B-shaped greedy decode on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload (one "step" = one greedy decode token: embedding, 30 layers with
+the KV cache, output norm, Q6_K lm-head, argmax): random-init BitNet
+b1.58-2B-shaped weights (30 layers, 2560/6912, 20/5 heads, vocab 128256),
+the KV cache pre-filled to 1024 positions with N(0,1) values, start token
+15339 at position 1024.  W warm-up tokens run first and are rolled back, so
+the K timed tokens occupy positions 1024..1024+K-1 (K = 64 by default: the
+64-token decode).  Inputs are resident in HBM before timing starts.
+
+Printed JSON line: decode tokens/s (value) plus, for the dominant kernel
+(the Q6_K lm-head matvec, one launch over 269.3 MB), achieved HBM GB/s
+against the 8 TB/s peak, measured with HIP events on the library's stream;
+the i2_s matvec's streaming GB/s over weight copies rotated through more
+than the 256 MB Infinity Cache; and the oracle's CPU time on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "project-willamette_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "i2_s/Q6_K matvec GB/s (% HBM peak) + decode tok/s, BitNet-2B shape, 1 GPU"
+HBM_PEAK_GBPS = 8000.0
+PREFILL, START_TOKEN = 1024, 15339
+
+
+class HipTimer:
+    """hipEvent pairs on a given stream (the library's own stream)."""
+
+    def __init__(self, stream: int):
+        self.hip = C.CDLL("libamdhip64.so")
+        self.stream = C.c_void_p(stream)
+        for n in ("hipEventCreate", "hipEventRecord", "hipEventSynchronize", "hipEventElapsedTime",
+                  "hipEventDestroy"):
+            getattr(self.hip, n).restype = C.c_int
+        self.a, self.b = C.c_void_p(), C.c_void_p()
+        assert self.hip.hipEventCreate(C.byref(self.a)) == 0
+        assert self.hip.hipEventCreate(C.byref(self.b)) == 0
+
+    def start(self):
+        assert self.hip.hipEventRecord(self.a, self.stream) == 0
+
+    def stop_ms(self) -> float:
+        assert self.hip.hipEventRecord(self.b, self.stream) == 0
+        assert self.hip.hipEventSynchronize(self.b) == 0
+        ms = C.c_float()
+        assert self.hip.hipEventElapsedTime(C.byref(ms), self.a, self.b) == 0
+        return float(ms.value)
+
+
+def log(msg: str):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def decode_tokens(dkv, n: int, tok: int, pos: int):
+    ids = []
+    for _ in range(n):
+        _, _, nxt = dkv.decode_step(tok, pos, want_logits=False)
+        ids.append(nxt)
+        tok, pos = nxt, pos + 1
+    return ids
+
+
+def lm_head_kernel(ctx, wh, hm, cfg, reps: int):
+    """Average duration of one Q6_K logits launch (no argmax kernel)."""
+    t = ctx.upload_q6k(hm.token_embd, cfg.n_embd, cfg.vocab)
+    h = ctx.to_device(wh.synth_normal(0x5749_4C4C_0000_0002, 2, cfg.n_embd))
+    logits = ctx.alloc(cfg.vocab * 4)
+    for _ in range(3):
+        ctx.check(wh.lib.wm_logits_argmax_dev(ctx.h, t.h, h.ptr, logits.ptr, None))
+    timer = HipTimer(ctx.stream)
+    timer.start()
+    for _ in range(reps):
+        ctx.check(wh.lib.wm_logits_argmax_dev(ctx.h, t.h, h.ptr, logits.ptr, None))
+    ms = timer.stop_ms() / reps
+    bytes_per = cfg.vocab * (cfg.n_embd // 256) * 210 + cfg.n_embd * 4 + cfg.vocab * 4
+    t.close()
+    return ms, bytes_per
+
+
+def i2s_stream(ctx, wh, copies: int, reps: int):
+    """i2_s 2560x2560 matvec over `copies` distinct device copies (rotated
+    through > 256 MB so the Infinity Cache cannot hold them), 64 per launch."""
+    seed = 0x5749_4C4C_0000_0001
+    packed = wh.synth_i2s(seed, 1, 2560, 2560)
+    ws = [ctx.upload_i2s(packed, 1.25, 2560, 2560) for _ in range(copies)]
+    x = ctx.to_device(wh.synth_normal(seed, 3, 2560))
+    y = ctx.alloc(copies * 2560 * 4)
+    arr = (wh._vp * copies)(*[w.h.value for w in ws])
+    ctx.check(wh.lib.wm_bitlinear_i2s_matvec_f32_multi_dev(ctx.h, arr, copies, x.ptr, y.ptr))
+    timer = HipTimer(ctx.stream)
+    timer.start()
+    for _ in range(reps):
+        ctx.check(wh.lib.wm_bitlinear_i2s_matvec_f32_multi_dev(ctx.h, arr, copies, x.ptr, y.ptr))
+    ms = timer.stop_ms() / reps
+    per_matvec = 2560 * 640 + 4 + 2560 * 4 * 2  # weights + scale + x + y (f32)
+    for w in ws:
+        w.close()
+    return ms, per_matvec * copies
+
+
+def cpu_baseline(hm, cfg, n_tokens: int, threads: int):
+    """The oracle (C restatement of the reference's x86 SSE2 path) on this
+    host: BitLinear single-threaded, lm-head rows over `threads` threads
+    (src/model/bitlinear_sse2.rs:329-340, src/model/lm_head.rs:87-88)."""
+    import bitnet_synth as bs
+    from oracle.oracle_model import OracleModel
+    orm = OracleModel(hm, threads=threads)
+    okv = orm.kv(cfg.context_length)
+    k, v = bs.kv_prefill(cfg, bs.master_seed(4), PREFILL)
+    okv.append_positions(k, v)
+    del k, v
+    tok, pos = START_TOKEN, PREFILL
+    t0 = time.perf_counter()
+    for _ in range(n_tokens):
+        h = okv.forward(tok, pos)
+        _, tok = okv.logits_argmax(h)
+        pos += 1
+    dt = time.perf_counter() - t0
+    orm.close()
+    return n_tokens / dt, dt
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--cpu-tokens", type=int, default=4)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the decode path runs on a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+    if PREFILL + args.warmup + args.steps > 4096 or args.steps < 1:
+        sys.exit("steps/warmup exceed the 4096-position context")
+
+    import willamette_hip as wh
+    import bitnet_synth as bs
+
+    cfg = bs.BITNET_2B
+    seed = bs.master_seed(4)
+    t0 = time.time()
+    hm = bs.make_host_model(cfg, seed)
+    ctx = wh.Context(0)
+    dev = bs.load_device_model(ctx, hm)
+    dkv = dev.kv_cache(cfg.context_length)
+    k, v = bs.kv_prefill(cfg, seed, PREFILL)
+    dkv.append_positions(k, v)
+    del k, v
+    log(f"model + KV prefill ready in {time.time() - t0:.1f}s")
+
+    decode_tokens(dkv, args.warmup, START_TOKEN, PREFILL)
+    dkv.rollback(PREFILL)
+    ctx.synchronize()
+    timer = HipTimer(ctx.stream)
+    w0 = time.perf_counter()
+    timer.start()
+    ids = decode_tokens(dkv, args.steps, START_TOKEN, PREFILL)
+    gpu_ms = timer.stop_ms()
+    ctx.synchronize()
+    wall_ms = (time.perf_counter() - w0) * 1000.0
+    ms_tok = wall_ms / args.steps
+    tok_s = args.steps / (wall_ms / 1000.0)
+    log(f"decode: {tok_s:.1f} tok/s ({ms_tok:.3f} ms/token wall, {gpu_ms / args.steps:.3f} ms/token events)")
+
+    lm_ms, lm_bytes = lm_head_kernel(ctx, wh, hm, cfg, reps=50)
+    lm_gbps = lm_bytes / (lm_ms / 1000.0) / 1e9
+    log(f"lm-head kernel: {lm_ms * 1000:.1f} us, {lm_gbps:.0f} GB/s")
+    copies = 320  # 320 x 1.64 MB = 524 MB > 256 MB Infinity Cache
+    mv_ms, mv_bytes = i2s_stream(ctx, wh, copies, reps=10)
+    mv_gbps = mv_bytes / (mv_ms / 1000.0) / 1e9
+    log(f"i2_s 2560x2560 x{copies}: {mv_ms * 1000 / copies:.2f} us/matvec, {mv_gbps:.0f} GB/s")
+
+    wb = cfg.weight_bytes()
+    kv_read = sum(cfg.n_layers * (p + 1) * cfg.kv_dim * 2 * 1 + cfg.n_layers * (p + 1) * 8
+                  for p in range(PREFILL, PREFILL + args.steps)) / args.steps
+    token_bytes = wb["i2s"] + wb["norms"] + wb["lm_head"] + kv_read
+    decode_gbps = token_bytes * tok_s / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        cpu_tok_s, cpu_s = cpu_baseline(hm, cfg, args.cpu_tokens, threads)
+        cpu = {"value": round(cpu_tok_s, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"{args.cpu_tokens} greedy tokens of the same workload (positions 1024..), "
+                         f"{cpu_s:.1f} s; BitLinear single-threaded, lm-head over {threads} threads"}
+        log(f"cpu baseline: {cpu_tok_s:.3f} tok/s")
+
+    out = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_tok, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i8",
+        "data": "synthetic: seeded random-init BitNet-2B-shaped weights, N(0,1) KV prefill",
+        "config": {"workload": "bitnet2b_greedy_decode", "n_layers": cfg.n_layers,
+                   "n_embd": cfg.n_embd, "n_ff": cfg.n_ff, "heads": cfg.n_heads,
+                   "kv_heads": cfg.n_kv_heads, "vocab": cfg.vocab, "kv_prefill": PREFILL,
+                   "decode_tokens": args.steps, "start_token": START_TOKEN, "exact": True},
+        "roofline": {"bound": "hbm", "achieved": round(lm_gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(lm_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "k_q6k_logits (Q6_K lm-head 128256x2560)",
+                     "us_per_launch": round(lm_ms * 1000, 2)},
+        "cpu_baseline": cpu,
+        "matvec": {
+            "q6k_lm_head_128256x2560": {"gbps": round(lm_gbps, 1), "frac": round(lm_gbps / HBM_PEAK_GBPS, 4)},
+            "i2s_2560x2560_rotated": {"gbps": round(mv_gbps, 1), "frac": round(mv_gbps / HBM_PEAK_GBPS, 4),
+                                      "us_per_matvec": round(mv_ms * 1000 / copies, 3),
+                                      "copies": copies},
+        },
+        "decode_effective_gbps": round(decode_gbps, 1),
+        "gpu_event_ms_per_token": round(gpu_ms / args.steps, 4),
+        "token_checksum": int(np.bitwise_xor.reduce(np.array(ids, np.uint64))),
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

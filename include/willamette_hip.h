@@ -1,0 +1,232 @@
+/*
+ * willamette_hip.h — C ABI of the MI355X (gfx950) BitNet b1.58 decode path.
+ *
+ * Drop-in boundary for project-willamette's CPU kernels: every entry point
+ * below names the reference function it replaces (file:line in
+ * project-willamette).  Plain pointers and sizes only; no HIP or torch types.
+ *
+ * Conventions
+ *  - Host-pointer entry points (no suffix) take the same slices the Rust API
+ *    takes (`&[f32]`, `&mut [f32]`), copy them to the device, run, and copy
+ *    results back before returning.  `_dev` entry points take device pointers
+ *    (from wm_dev_alloc) and are asynchronous on the context's stream.
+ *  - Every call validates all arguments before touching the device; on a
+ *    validation error nothing is written to any output (the reference's
+ *    `Err(..)` before any work, src/model/bitlinear.rs:150-199).
+ *  - A context is single-threaded: callers serialise calls on one context
+ *    (the reference decode loop is single-threaded, src/model/stage_timing.rs:32-36).
+ *  - Numerics: the device path reproduces the reference's x86_64 arithmetic
+ *    bit for bit (int8 activations, i32 dots, Q6_K values, f32 reductions in
+ *    the reference's sequential order, glibc-identical expf).
+ */
+#ifndef WILLAMETTE_HIP_H
+#define WILLAMETTE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes; the Rust shim maps them onto WillametteError (src/error.rs:9-57). */
+typedef enum wm_status {
+    WM_OK = 0,
+    WM_E_UNSUPPORTED_TYPE = 1, /* WillametteError::UnsupportedTensorType (src/error.rs:29) */
+    WM_E_SHAPE = 2,            /* WillametteError::GgufParse shape/length errors (src/error.rs:14) */
+    WM_E_NONFINITE = 3,        /* non-finite scale (src/gguf/tensor.rs:302-307) or hidden
+                                  (src/model/cached_forward.rs:511-521) */
+    WM_E_OOM = 4,              /* device allocation failed */
+    WM_E_HIP = 5,              /* HIP runtime error; wm_last_error() has the text */
+    WM_E_ARG = 6,              /* null pointer / out-of-range argument */
+    WM_E_STATE = 7             /* call out of protocol order (e.g. KV position mismatch,
+                                  src/model/cached_forward.rs:271-305) */
+} wm_status;
+
+typedef enum wm_tensor_type {
+    WM_TYPE_I2S = 36, /* GgmlType::BitNetI2S raw id (src/gguf/types.rs:14-60) */
+    WM_TYPE_Q6K = 14  /* GgmlType::Q6K raw id */
+} wm_tensor_type;
+
+typedef struct wm_ctx wm_ctx;
+typedef struct wm_tensor wm_tensor;
+typedef struct wm_model wm_model;
+typedef struct wm_kv_cache wm_kv_cache;
+
+/* ---- context --------------------------------------------------------- */
+
+/* One device, one stream.  Replaces the process-wide kernel selection
+ * (src/model/dispatch.rs:111-114, :159-184) for a `Kernel::Hip` arm. */
+wm_status wm_ctx_create(int device, wm_ctx **out);
+void wm_ctx_destroy(wm_ctx *ctx);
+/* Text of the last error on this context ("" if none).  Owned by ctx. */
+const char *wm_last_error(const wm_ctx *ctx);
+/* The context's hipStream_t, as an opaque pointer, for callers that time or
+ * order their own work against the library's. */
+void *wm_ctx_stream(wm_ctx *ctx);
+wm_status wm_ctx_synchronize(wm_ctx *ctx);
+const char *wm_version(void);
+
+/* Device buffers for the `_dev` entry points. */
+wm_status wm_dev_alloc(wm_ctx *ctx, size_t bytes, void **out);
+wm_status wm_dev_free(wm_ctx *ctx, void *ptr);
+wm_status wm_memcpy_h2d(wm_ctx *ctx, void *dst, const void *src, size_t bytes);
+wm_status wm_memcpy_d2h(wm_ctx *ctx, void *dst, const void *src, size_t bytes);
+
+/* ---- tensors (TensorView, src/gguf/tensor.rs:21-54) ------------------ */
+
+/* Upload an I2_S BitLinear weight: `packed` is TensorView::data (out_dim rows
+ * of in_dim/4 bytes, src/gguf/tensor.rs:45), `scale_block` is
+ * TensorView::scale_data (the 32-byte trailing block whose first 4 bytes are
+ * the LE f32 scale, src/gguf/tensor.rs:278-309).  Shape is GGUF order
+ * [in_dim, out_dim].  Rejects in_dim not a positive multiple of 128 and
+ * packed_len < in_dim/4*out_dim (src/model/bitlinear_sse2.rs:129-177), a
+ * missing/short scale block, and a non-finite scale.  Host bytes are only
+ * read during the call; the library owns the device copy. */
+wm_status wm_tensor_upload_i2s(wm_ctx *ctx, const uint8_t *packed, size_t packed_len,
+                               const uint8_t *scale_block, size_t scale_len, uint64_t in_dim,
+                               uint64_t out_dim, wm_tensor **out);
+/* Upload a Q6_K matrix of n_rows rows of row_len values (GGUF shape
+ * [row_len, n_rows]); row_len must be a positive multiple of 256 and
+ * len == n_rows * row_len/256 * 210 (src/gguf/tensor.rs:104-105, 206-231). */
+wm_status wm_tensor_upload_q6k(wm_ctx *ctx, const uint8_t *blocks, size_t len, uint64_t row_len,
+                               uint64_t n_rows, wm_tensor **out);
+void wm_tensor_destroy(wm_tensor *t);
+/* shape[0] = in_dim / row_len, shape[1] = out_dim / n_rows; type = wm_tensor_type */
+wm_status wm_tensor_info(const wm_tensor *t, uint64_t shape[2], int *type, float *scale);
+
+/* ---- BitLinear I2_S (src/model/bitlinear.rs, bitlinear_sse2.rs) ------ */
+
+/* output = w_scale * in_scale * (ternary(W) . q(input)), q = per-vector
+ * absmax int8 (src/model/bitlinear_sse2.rs:285-304), i32 accumulation.
+ * Replaces bitlinear_i2s_matvec_f32 (src/model/bitlinear.rs:67) /
+ * linear_matvec_f32 for I2_S (src/model/linear.rs:17). */
+wm_status wm_bitlinear_i2s_matvec_f32(wm_ctx *ctx, const wm_tensor *w, const float *input,
+                                      size_t input_len, float *output, size_t output_len);
+/* Same, with taps: the quantised activation (in_dim i8), its scale, and the
+ * per-row i32 dot before the f32 epilogue (any may be NULL). */
+wm_status wm_bitlinear_i2s_matvec_f32_debug(wm_ctx *ctx, const wm_tensor *w, const float *input,
+                                            size_t input_len, float *output, size_t output_len,
+                                            int8_t *act, float *act_scale, int32_t *acc);
+/* Device-pointer form: d_input[in_dim] f32 -> d_output[out_dim] f32. */
+wm_status wm_bitlinear_i2s_matvec_f32_dev(wm_ctx *ctx, const wm_tensor *w, const float *d_input,
+                                          float *d_output);
+/* Batched device form over `n_copies` weight tensors of one shape sharing one
+ * input, one launch (used to measure HBM bandwidth on matrices far smaller
+ * than the 256 MB Infinity Cache).  d_outputs is n_copies x out_dim. */
+wm_status wm_bitlinear_i2s_matvec_f32_multi_dev(wm_ctx *ctx, const wm_tensor *const *ws,
+                                                uint32_t n_copies, const float *d_input,
+                                                float *d_outputs);
+
+/* ---- Q6_K / lm-head (src/model/q6_k.rs, lm_head.rs) ------------------ */
+
+/* Dequantise one row (src/model/q6_k.rs:59-69); embedding gather for a
+ * Q6_K token_embd (src/model/primitives.rs:120-210). */
+wm_status wm_q6k_dequantize_row(wm_ctx *ctx, const wm_tensor *t, uint64_t row, float *out,
+                                size_t out_len);
+/* logits[v] = q6_k::dot_row(row v, hidden) for every row, in the SSE2
+ * accumulation order (src/model/lm_head.rs:29-108, q6_k_sse2.rs:46-116). */
+wm_status wm_compute_logits(wm_ctx *ctx, const wm_tensor *token_embd, const float *hidden,
+                            size_t hidden_len, float *logits, size_t vocab);
+/* compute_logits + argmax (src/model/lm_head.rs:161-174: first index of the
+ * maximum) in one pass; `logits` may be NULL when only the id is wanted. */
+wm_status wm_logits_argmax(wm_ctx *ctx, const wm_tensor *token_embd, const float *hidden,
+                           size_t hidden_len, float *logits, uint32_t *argmax);
+/* Device form: d_logits may be NULL; d_argmax is one uint32 in device memory. */
+wm_status wm_logits_argmax_dev(wm_ctx *ctx, const wm_tensor *token_embd, const float *d_hidden,
+                               float *d_logits, uint32_t *d_argmax);
+/* argmax over a host slice (src/model/lm_head.rs:161-174); WM_E_ARG when
+ * n == 0 (the reference's None). */
+wm_status wm_argmax(const float *logits, size_t n, uint32_t *out);
+
+/* ---- model + KV cache (src/model/{graph,kv_cache,cached_forward,generate}.rs) */
+
+/* ModelConfig fields the BitNet forward reads (src/model/config.rs:21-44). */
+typedef struct wm_model_config {
+    uint32_t n_layers;       /* block_count */
+    uint32_t n_embd;         /* embedding_length */
+    uint32_t n_ff;           /* feed_forward_length */
+    uint32_t n_heads;        /* head_count */
+    uint32_t n_kv_heads;     /* head_count_kv */
+    uint32_t head_dim;       /* embedding_length / head_count */
+    uint32_t n_rot;          /* rope_dimension_count */
+    uint32_t vocab_size;
+    uint32_t context_length; /* upper bound for KV caches */
+    float rms_eps;           /* layer_norm_rms_epsilon */
+    float rope_freq_base;    /* rope_freq_base (NEOX RoPE, src/model/primitives.rs:326-341) */
+} wm_model_config;
+
+/* ModelGraph::from_gguf (src/model/graph.rs:79-237): a device-resident
+ * model.  Tensors passed to wm_model_set_* are copied into the model's own
+ * fused device layout; the caller may destroy them afterwards. */
+wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **out);
+void wm_model_destroy(wm_model *m);
+/* LayerWeights (src/model/graph.rs:23-53): seven I2_S BitLinears and four
+ * f32 norm vectors (host pointers, n_embd or n_ff values). */
+wm_status wm_model_set_layer(wm_model *m, uint32_t layer, const wm_tensor *attn_q,
+                             const wm_tensor *attn_k, const wm_tensor *attn_v,
+                             const wm_tensor *attn_output, const wm_tensor *ffn_gate,
+                             const wm_tensor *ffn_up, const wm_tensor *ffn_down,
+                             const float *attn_norm, const float *attn_sub_norm,
+                             const float *ffn_norm, const float *ffn_sub_norm);
+/* Tied Q6_K token_embd / lm_head (src/model/graph.rs:134-163) and output_norm. */
+wm_status wm_model_set_output(wm_model *m, const wm_tensor *token_embd, const float *output_norm);
+
+/* KVCache::try_new (src/model/kv_cache.rs:67-131): i8 codes + one f32 scale
+ * per token per layer for K and V, on the device. */
+wm_status wm_kv_cache_create(wm_model *m, uint32_t max_seq_len, wm_kv_cache **out);
+void wm_kv_cache_destroy(wm_kv_cache *kv);
+uint32_t wm_kv_cache_position(const wm_kv_cache *kv);            /* :121-128 */
+wm_status wm_kv_cache_rollback(wm_kv_cache *kv, uint32_t position); /* :141-149 */
+/* KVCache::append (src/model/kv_cache.rs:154-185) for every layer at the next
+ * position: k and v are host f32, n_layers x kv_dim, layer-major. */
+wm_status wm_kv_cache_append_position(wm_kv_cache *kv, const float *k, const float *v);
+/* Same for n_pos positions at once: k and v are n_pos x n_layers x kv_dim. */
+wm_status wm_kv_cache_append_positions(wm_kv_cache *kv, const float *k, const float *v,
+                                       uint32_t n_pos);
+/* Raw i8 codes and scales of one layer's first n_pos positions (any output
+ * may be NULL). */
+wm_status wm_kv_cache_read_raw(wm_kv_cache *kv, uint32_t layer, int8_t *k, float *k_scales,
+                               int8_t *v, float *v_scales, uint32_t n_pos);
+
+/* forward_with_cache_into (src/model/cached_forward.rs:164-261): embed
+ * `token`, run every layer at `position` (== wm_kv_cache_position), apply
+ * output_norm.  hidden_out (n_embd, host, nullable) receives the final
+ * hidden; layer_trace (n_layers x n_embd, host, nullable) the hidden after
+ * each layer.  On a non-finite hidden the cache is rolled back and
+ * WM_E_NONFINITE returned with outputs untouched. */
+wm_status wm_forward_with_cache(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t position,
+                                float *hidden_out, float *layer_trace);
+/* One greedy step: forward_with_cache + compute_logits + argmax
+ * (src/model/generate.rs:165-187).  logits_out (vocab) and hidden_out may be
+ * NULL. */
+wm_status wm_decode_step(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t position,
+                         float *hidden_out, float *logits_out, uint32_t *next_token);
+/* greedy_generate_with_cache (src/model/generate.rs:111-189) continuing an
+ * existing cache: prefill `prompt` in order, then up to max_new greedy
+ * tokens, stopping at `eos` (< 0: none).  Writes *n_out ids to out_ids.
+ * The whole loop runs on the device; tokens never visit the host. */
+wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *prompt,
+                             uint32_t n_prompt, uint32_t max_new, int64_t eos, uint32_t *out_ids,
+                             uint32_t *n_out);
+
+/* ---- synthetic BitNet-shaped inputs (src/synth.rs) ------------------- */
+
+/* Counter-based SplitMix64 streams, identical on every host: value i of
+ * stream (seed, tag) is the (i+1)-th SplitMix64 output from state
+ * wm_synth_stream_seed(seed, tag). */
+uint64_t wm_synth_stream_seed(uint64_t seed, uint64_t tag);
+/* Ternary I2_S codes, each of {-1,0,+1} with probability 1/3, packed
+ * c0<<6 | c1<<4 | c2<<2 | c3 (src/synth.rs:239-265). */
+void wm_synth_i2s(uint64_t seed, uint64_t tag, uint8_t *packed, size_t n_bytes);
+/* f32 ~ N(0, sigma) (Box-Muller in double) and ~ U(lo, hi). */
+void wm_synth_normal(uint64_t seed, uint64_t tag, float *out, size_t n, double sigma);
+void wm_synth_uniform(uint64_t seed, uint64_t tag, float *out, size_t n, double lo, double hi);
+/* Q6_K rows: ql/qh uniform bytes, sub-scales uniform in [-32, 31],
+ * d = f16(|N(0, d_sigma)|). */
+void wm_synth_q6k(uint64_t seed, uint64_t tag, uint8_t *blocks, size_t n_blocks, double d_sigma);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WILLAMETTE_HIP_H */

@@ -1,0 +1,233 @@
+"""Seeded BitNet b1.58 models with random-init weights (the role of the
+reference's src/synth.rs, at BitNet-b1.58-2B shape).
+
+Every tensor is drawn from its own counter-based SplitMix64 stream
+(wm_synth_* in libwillamette_hip.so), keyed by (master seed, tag), so the
+same weights can be produced on any host and fed identically to the device
+model and to the oracle.
+
+Distributions (per workload definition):
+  I2_S weights   each of {-1, 0, +1} with probability 1/3, I2_S byte layout
+  I2_S scales    U(0.5, 2) per tensor
+  norm weights   U(0.9, 1.1)
+  token_embd     Q6_K: ql/qh uniform bytes, sub-scales uniform in [-32, 31],
+                 d = f16(|N(0, 1e-3)|)
+  KV prefill     N(0, 1) per (position, layer) K and V vector
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+import willamette_hip as wh
+
+
+def master_seed(config_index: int) -> int:
+    """Seed of workload k: 0x5749_4C4C_0000_000k ("WILL" + k)."""
+    return 0x5749_4C4C_0000_0000 | config_index
+
+
+@dataclass(frozen=True)
+class BitNetConfig:
+    n_layers: int = 30
+    n_embd: int = 2560
+    n_ff: int = 6912
+    n_heads: int = 20
+    n_kv_heads: int = 5
+    head_dim: int = 128
+    vocab: int = 128256
+    context_length: int = 4096
+    rms_eps: float = 1e-5
+    rope_base: float = 500000.0
+
+    @property
+    def kv_dim(self) -> int:
+        return self.n_kv_heads * self.head_dim
+
+    def c_config(self) -> wh.ModelConfig:
+        return wh.ModelConfig(self.n_layers, self.n_embd, self.n_ff, self.n_heads, self.n_kv_heads,
+                              self.head_dim, self.head_dim, self.vocab, self.context_length,
+                              self.rms_eps, self.rope_base)
+
+    def weight_bytes(self) -> dict:
+        """Algorithmic bytes of the weights one decode token streams."""
+        E, F, KV = self.n_embd, self.n_ff, self.kv_dim
+        i2s = self.n_layers * (E * E + 2 * E * KV + E * E + 3 * E * F) // 4
+        norms = self.n_layers * (3 * E + F) * 4 + E * 4
+        lm = self.vocab * (E // 256) * 210
+        return {"i2s": i2s, "norms": norms, "lm_head": lm}
+
+
+BITNET_2B = BitNetConfig()
+
+ROLES = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+NORMS = ("attn_norm", "attn_sub_norm", "ffn_norm", "ffn_sub_norm")
+
+
+def role_shape(cfg: BitNetConfig, role: str):
+    """(in_dim, out_dim) in GGUF order (docs/BITLINEAR_I2S_MATVEC.md:26-34)."""
+    E, F, KV = cfg.n_embd, cfg.n_ff, cfg.kv_dim
+    return {"attn_q": (E, E), "attn_k": (E, KV), "attn_v": (E, KV), "attn_output": (E, E),
+            "ffn_gate": (E, F), "ffn_up": (E, F), "ffn_down": (F, E)}[role]
+
+
+def _tag(layer: int, kind: int, idx: int) -> int:
+    return (layer << 16) | (kind << 8) | idx
+
+
+@dataclass
+class HostLayer:
+    packed: dict = field(default_factory=dict)  # role -> uint8[in/4*out]
+    scales: dict = field(default_factory=dict)  # role -> float
+    norms: dict = field(default_factory=dict)   # name -> float32[n]
+
+
+@dataclass
+class HostModel:
+    cfg: BitNetConfig
+    seed: int
+    layers: list
+    token_embd: np.ndarray  # Q6_K bytes, vocab x (n_embd/256*210)
+    output_norm: np.ndarray
+
+
+def make_host_model(cfg: BitNetConfig, seed: int) -> HostModel:
+    layers = []
+    for l in range(cfg.n_layers):
+        hl = HostLayer()
+        for i, role in enumerate(ROLES):
+            ind, outd = role_shape(cfg, role)
+            hl.packed[role] = wh.synth_i2s(seed, _tag(l, 1, i), ind, outd)
+            hl.scales[role] = float(wh.synth_uniform(seed, _tag(l, 2, i), 1, 0.5, 2.0)[0])
+        for i, name in enumerate(NORMS):
+            n = cfg.n_ff if name == "ffn_sub_norm" else cfg.n_embd
+            hl.norms[name] = wh.synth_uniform(seed, _tag(l, 3, i), n, 0.9, 1.1)
+        layers.append(hl)
+    embd = wh.synth_q6k(seed, _tag(0xFFFF, 4, 0), cfg.vocab, cfg.n_embd, 1e-3)
+    out_norm = wh.synth_uniform(seed, _tag(0xFFFF, 5, 0), cfg.n_embd, 0.9, 1.1)
+    return HostModel(cfg, seed, layers, embd, out_norm)
+
+
+def kv_prefill(cfg: BitNetConfig, seed: int, n_pos: int):
+    """N(0,1) K and V for n_pos positions, shaped [n_pos][n_layers][kv_dim]."""
+    n = n_pos * cfg.n_layers * cfg.kv_dim
+    k = wh.synth_normal(seed, _tag(0xFFFE, 6, 0), n).reshape(n_pos, cfg.n_layers, cfg.kv_dim)
+    v = wh.synth_normal(seed, _tag(0xFFFE, 6, 1), n).reshape(n_pos, cfg.n_layers, cfg.kv_dim)
+    return k, v
+
+
+def load_device_model(ctx: wh.Context, hm: HostModel) -> "DeviceModel":
+    return DeviceModel(ctx, hm)
+
+
+class DeviceModel:
+    """wm_model built from a HostModel (ModelGraph::from_gguf role)."""
+
+    def __init__(self, ctx: wh.Context, hm: HostModel):
+        self.ctx, self.cfg = ctx, hm.cfg
+        cc = hm.cfg.c_config()
+        h = wh._vp()
+        ctx.check(wh.lib.wm_model_create(ctx.h, wh.C.byref(cc), wh.C.byref(h)))
+        self.h = h
+        for l, hl in enumerate(hm.layers):
+            ts = []
+            for role in ROLES:
+                ind, outd = role_shape(hm.cfg, role)
+                ts.append(ctx.upload_i2s(hl.packed[role], hl.scales[role], ind, outd))
+            nrm = [np.ascontiguousarray(hl.norms[n], dtype=np.float32) for n in NORMS]
+            ctx.check(wh.lib.wm_model_set_layer(self.h, l, *[t.h for t in ts],
+                                                *[wh._ptr(a, wh.C.c_float) for a in nrm]))
+            for t in ts:
+                t.close()
+        emb = ctx.upload_q6k(hm.token_embd, hm.cfg.n_embd, hm.cfg.vocab)
+        on = np.ascontiguousarray(hm.output_norm, dtype=np.float32)
+        ctx.check(wh.lib.wm_model_set_output(self.h, emb.h, wh._ptr(on, wh.C.c_float)))
+        emb.close()
+
+    def close(self):
+        if self.h:
+            wh.lib.wm_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def kv_cache(self, max_seq: int) -> "DeviceKV":
+        return DeviceKV(self, max_seq)
+
+
+class DeviceKV:
+    def __init__(self, model: DeviceModel, max_seq: int):
+        self.model, self.ctx = model, model.ctx
+        h = wh._vp()
+        self.ctx.check(wh.lib.wm_kv_cache_create(model.h, max_seq, wh.C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            wh.lib.wm_kv_cache_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def position(self) -> int:
+        return int(wh.lib.wm_kv_cache_position(self.h))
+
+    def rollback(self, pos: int):
+        self.ctx.check(wh.lib.wm_kv_cache_rollback(self.h, pos))
+
+    def append_positions(self, k: np.ndarray, v: np.ndarray):
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        n_pos = k.shape[0]
+        self.ctx.check(wh.lib.wm_kv_cache_append_positions(self.h, wh._ptr(k, wh.C.c_float),
+                                                           wh._ptr(v, wh.C.c_float), n_pos))
+
+    def read_raw(self, layer: int, n_pos: int):
+        kvd = self.model.cfg.kv_dim
+        k = np.empty(n_pos * kvd, np.int8)
+        v = np.empty(n_pos * kvd, np.int8)
+        ks = np.empty(n_pos, np.float32)
+        vs = np.empty(n_pos, np.float32)
+        self.ctx.check(wh.lib.wm_kv_cache_read_raw(self.h, layer, wh._ptr(k, wh.C.c_int8),
+                                                   wh._ptr(ks, wh.C.c_float), wh._ptr(v, wh.C.c_int8),
+                                                   wh._ptr(vs, wh.C.c_float), n_pos))
+        return k.reshape(n_pos, kvd), ks, v.reshape(n_pos, kvd), vs
+
+    def forward(self, token: int, pos: int, trace: bool = False):
+        cfg = self.model.cfg
+        hidden = np.empty(cfg.n_embd, np.float32)
+        tr = np.empty((cfg.n_layers, cfg.n_embd), np.float32) if trace else None
+        self.ctx.check(wh.lib.wm_forward_with_cache(self.model.h, self.h, token, pos,
+                                                    wh._ptr(hidden, wh.C.c_float),
+                                                    wh._ptr(tr, wh.C.c_float) if trace else None))
+        return (hidden, tr) if trace else hidden
+
+    def decode_step(self, token: int, pos: int, want_logits: bool = True):
+        cfg = self.model.cfg
+        hidden = np.empty(cfg.n_embd, np.float32)
+        logits = np.empty(cfg.vocab, np.float32) if want_logits else None
+        nxt = wh.C.c_uint32()
+        self.ctx.check(wh.lib.wm_decode_step(self.model.h, self.h, token, pos,
+                                             wh._ptr(hidden, wh.C.c_float),
+                                             wh._ptr(logits, wh.C.c_float) if want_logits else None,
+                                             wh.C.byref(nxt)))
+        return hidden, logits, int(nxt.value)
+
+    def greedy(self, prompt, max_new: int, eos: int = -1):
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.empty(max(max_new, 1), np.uint32)
+        n = wh.C.c_uint32()
+        self.ctx.check(wh.lib.wm_greedy_generate(self.model.h, self.h, wh._ptr(prompt, wh.C.c_uint32),
+                                                 prompt.size, max_new, eos,
+                                                 wh._ptr(out, wh.C.c_uint32), wh.C.byref(n)))
+        return out[: n.value].tolist()

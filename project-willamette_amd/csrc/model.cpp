@@ -1,0 +1,614 @@
+// Device-resident BitNet b1.58 model, KV cache and decode step.
+//
+// Reference: ModelGraph::from_gguf (src/model/graph.rs:79-237), KVCache
+// (src/model/kv_cache.rs:49-259), forward_with_cache_into
+// (src/model/cached_forward.rs:164-521), greedy_generate_with_cache
+// (src/model/generate.rs:111-189).
+//
+// One decode step is a fixed sequence of kernels on the context's stream:
+//   embed (Q6_K row) ->
+//   per layer: [residual +] attn_norm+quant -> QKV partial dots -> QKV epilogue
+//              (RoPE, KV append) -> scores -> softmax+V -> attn_sub_norm+quant
+//              -> O partial dots -> residual + ffn_norm+quant -> gate/up partial
+//              dots -> relu^2*up -> ffn_sub_norm+quant -> down partial dots
+//   -> residual + output_norm -> lm-head logits + argmax.
+// The residual of each BitLinear is folded into the next norm kernel.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "wm_internal.h"
+
+// launchers from k_layer.hip
+void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, uint32_t rows_total,
+                             uint32_t row0, float w_scale, const wm_act_meta *meta_in,
+                             const float *w, uint32_t n, float eps, uint8_t *act,
+                             wm_act_meta *meta_out, float *y_out, uint32_t *err_flag,
+                             uint32_t layer_tag, hipStream_t s);
+void wm_launch_qkv_rope_kv(const int32_t *partial, uint32_t split, uint32_t rows_total,
+                           uint32_t q_row0, uint32_t k_row0, uint32_t v_row0, uint32_t n_q,
+                           uint32_t n_kv, float q_scale, float k_scale, float v_scale,
+                           const wm_act_meta *meta, const float *rope_cos, const float *rope_sin,
+                           uint32_t head_dim, uint32_t n_rot, uint32_t pos, float *q_out,
+                           int8_t *k_cache, int8_t *v_cache, float *k_scale_out,
+                           float *v_scale_out, hipStream_t s);
+void wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_scales,
+                         const int8_t *v_cache, const float *v_scales, float *scores,
+                         uint32_t score_stride, float *out, uint32_t n_heads, uint32_t n_kv_heads,
+                         uint32_t head_dim, uint32_t n_past, float scale, hipStream_t s);
+void wm_launch_gateup_relu2(const int32_t *partial, uint32_t split, uint32_t rows_total,
+                            uint32_t gate_row0, uint32_t up_row0, uint32_t n_ff, float gate_scale,
+                            float up_scale, const wm_act_meta *meta, float *h, hipStream_t s);
+void wm_launch_kv_append(const float *k, const float *v, uint32_t kv_dim, uint32_t n_layers,
+                         uint32_t pos0, uint32_t n_pos, uint32_t max_seq, int8_t *k_cache,
+                         float *k_scales, int8_t *v_cache, float *v_scales, hipStream_t s);
+
+namespace {
+
+struct dev_lin {
+    uint8_t *w = nullptr;  // library I2_S layout (owned copy)
+    uint32_t n_groups = 0;
+    float scale = 1.0f;
+};
+
+struct dev_layer {
+    dev_lin q, k, v, o, gate, up, down;
+    float *attn_norm = nullptr, *attn_sub_norm = nullptr, *ffn_norm = nullptr,
+          *ffn_sub_norm = nullptr;
+    bool set = false;
+};
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+}  // namespace
+
+struct wm_model {
+    wm_ctx *ctx = nullptr;
+    wm_model_config cfg{};
+    uint32_t kv_dim = 0;
+    std::vector<dev_layer> layers;
+    // tied embedding / lm-head (library Q6_K layout) and output norm
+    uint8_t *embd = nullptr;
+    uint32_t embd_blocks = 0, embd_rowgroups = 0;
+    float *output_norm = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    // workspace
+    uint8_t *ws = nullptr;
+    float *hidden = nullptr, *q = nullptr, *attn_out = nullptr, *h_ff = nullptr, *final_hidden = nullptr;
+    float *logits = nullptr, *scores = nullptr;
+    uint8_t *act = nullptr;
+    wm_act_meta *meta = nullptr;  // [4]: attn, sub, ffn, ffn_sub
+    int32_t *partial = nullptr;
+    uint32_t *dscalars = nullptr;  // [0] token, [1] next token, [2] error flag
+    void *lm_work = nullptr;
+    // split choices
+    uint32_t split_qkv = 1, split_o = 1, split_gu = 1, split_down = 1;
+};
+
+struct wm_kv_cache {
+    wm_model *m = nullptr;
+    uint32_t max_seq = 0, pos = 0;
+    int8_t *k = nullptr, *v = nullptr;   // [layer][max_seq][kv_dim]
+    float *ks = nullptr, *vs = nullptr;  // [layer][max_seq]
+};
+
+namespace {
+
+wm_status copy_lin(wm_model *m, const wm_tensor *t, uint64_t in_dim, uint64_t out_dim, dev_lin *out,
+                   const char *name) {
+    wm_ctx *ctx = m->ctx;
+    if (!t) return wm_set_error(ctx, WM_E_ARG, "%s: missing tensor", name);
+    if (t->type != WM_TYPE_I2S)
+        return wm_set_error(ctx, WM_E_UNSUPPORTED_TYPE, "%s: tensor type %d is not I2_S", name, t->type);
+    if (t->in_dim != in_dim || t->out_dim != out_dim)
+        return wm_set_error(ctx, WM_E_SHAPE, "%s: shape [%llu, %llu] != [%llu, %llu]", name,
+                            (unsigned long long)t->in_dim, (unsigned long long)t->out_dim,
+                            (unsigned long long)in_dim, (unsigned long long)out_dim);
+    if (out->w) WM_HIP(ctx, hipFree(out->w));
+    out->w = nullptr;
+    WM_HIP(ctx, hipMalloc(&out->w, t->bytes));
+    WM_HIP(ctx, hipMemcpyAsync(out->w, t->d, t->bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    out->n_groups = t->n_groups;
+    out->scale = t->scale;
+    return WM_OK;
+}
+
+wm_status copy_norm(wm_model *m, const float *src, uint32_t n, float **dst, const char *name) {
+    wm_ctx *ctx = m->ctx;
+    if (!src) return wm_set_error(ctx, WM_E_ARG, "%s: missing norm weights", name);
+    if (!*dst) WM_HIP(ctx, hipMalloc((void **)dst, (size_t)n * 4));
+    WM_HIP(ctx, hipMemcpyAsync(*dst, src, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+    return WM_OK;
+}
+
+void free_lin(dev_lin &l) {
+    if (l.w) hipFree(l.w);
+    l.w = nullptr;
+}
+
+bool model_ready(const wm_model *m) {
+    if (!m->embd || !m->output_norm) return false;
+    for (auto &l : m->layers)
+        if (!l.set) return false;
+    return true;
+}
+
+// Enqueue the layers + output norm for one token at `pos`; the token id is
+// read from m->dscalars[0] on the device.
+void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_trace_dev) {
+    const wm_model_config &c = m->cfg;
+    hipStream_t s = m->ctx->stream;
+    const uint32_t E = c.n_embd, F = c.n_ff, KV = m->kv_dim;
+    const uint32_t n_chunks_e = E / I2S_CHUNK_COLS, n_chunks_f = F / I2S_CHUNK_COLS;
+    wm_launch_q6k_dequant_row_dev(m->embd, m->embd_blocks, m->dscalars, m->hidden, s);
+    const float scale = 1.0f / sqrtf((float)c.head_dim);  // primitives.rs:354
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        const dev_layer &L = m->layers[l];
+        // residual of the previous layer's ffn_down, folded into attn_norm
+        if (l == 0) {
+            wm_launch_rmsnorm_quant(m->hidden, nullptr, 0, 0, 0, 0.0f, nullptr, L.attn_norm, E,
+                                    c.rms_eps, m->act, &m->meta[0], nullptr, nullptr, 0, s);
+        } else {
+            const dev_layer &P = m->layers[l - 1];
+            wm_launch_rmsnorm_quant(m->hidden, m->partial, m->split_down, P.down.n_groups * 64, 0,
+                                    P.down.scale, &m->meta[3], L.attn_norm, E, c.rms_eps, m->act,
+                                    &m->meta[0], nullptr, m->dscalars + 2, l, s);
+            if (layer_trace_dev)
+                hipMemcpyAsync(layer_trace_dev + (size_t)(l - 1) * E, m->hidden, (size_t)E * 4,
+                               hipMemcpyDeviceToDevice, s);
+        }
+        // Q, K, V: one launch over three tensors sharing the quantised input
+        wm_i2s_desc qkv[3] = {{L.q.w, L.q.n_groups}, {L.k.w, L.k.n_groups}, {L.v.w, L.v.n_groups}};
+        const uint32_t rows_qkv = (L.q.n_groups + L.k.n_groups + L.v.n_groups) * 64;
+        wm_launch_i2s_partial(qkv, 3, n_chunks_e, m->act, m->partial, m->split_qkv, rows_qkv, s);
+        const size_t kv_off = ((size_t)l * kv->max_seq + pos);
+        wm_launch_qkv_rope_kv(m->partial, m->split_qkv, rows_qkv, 0, L.q.n_groups * 64,
+                              (L.q.n_groups + L.k.n_groups) * 64, E, KV, L.q.scale, L.k.scale,
+                              L.v.scale, &m->meta[0], m->rope_cos, m->rope_sin, c.head_dim, c.n_rot,
+                              pos, m->q, kv->k + kv_off * KV, kv->v + kv_off * KV, kv->ks + kv_off,
+                              kv->vs + kv_off, s);
+        const size_t lay = (size_t)l * kv->max_seq;
+        wm_launch_attention(m->q, kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV, kv->vs + lay,
+                            m->scores, c.context_length, m->attn_out, c.n_heads, c.n_kv_heads,
+                            c.head_dim, pos + 1, scale, s);
+        wm_launch_rmsnorm_quant(m->attn_out, nullptr, 0, 0, 0, 0.0f, nullptr, L.attn_sub_norm, E,
+                                c.rms_eps, m->act, &m->meta[1], nullptr, nullptr, 0, s);
+        wm_i2s_desc od = {L.o.w, L.o.n_groups};
+        wm_launch_i2s_partial(&od, 1, n_chunks_e, m->act, m->partial, m->split_o, L.o.n_groups * 64, s);
+        // hidden += wo_out, then ffn_norm
+        wm_launch_rmsnorm_quant(m->hidden, m->partial, m->split_o, L.o.n_groups * 64, 0, L.o.scale,
+                                &m->meta[1], L.ffn_norm, E, c.rms_eps, m->act, &m->meta[2], nullptr,
+                                nullptr, 0, s);
+        wm_i2s_desc gu[2] = {{L.gate.w, L.gate.n_groups}, {L.up.w, L.up.n_groups}};
+        const uint32_t rows_gu = (L.gate.n_groups + L.up.n_groups) * 64;
+        wm_launch_i2s_partial(gu, 2, n_chunks_e, m->act, m->partial, m->split_gu, rows_gu, s);
+        wm_launch_gateup_relu2(m->partial, m->split_gu, rows_gu, 0, L.gate.n_groups * 64, F,
+                               L.gate.scale, L.up.scale, &m->meta[2], m->h_ff, s);
+        wm_launch_rmsnorm_quant(m->h_ff, nullptr, 0, 0, 0, 0.0f, nullptr, L.ffn_sub_norm, F,
+                                c.rms_eps, m->act, &m->meta[3], nullptr, nullptr, 0, s);
+        wm_i2s_desc dd = {L.down.w, L.down.n_groups};
+        wm_launch_i2s_partial(&dd, 1, n_chunks_f, m->act, m->partial, m->split_down,
+                              L.down.n_groups * 64, s);
+    }
+    // last residual + output_norm (f32 out, no quantisation)
+    const dev_layer &P = m->layers[c.n_layers - 1];
+    wm_launch_rmsnorm_quant(m->hidden, m->partial, m->split_down, P.down.n_groups * 64, 0,
+                            P.down.scale, &m->meta[3], m->output_norm, E, c.rms_eps, nullptr,
+                            nullptr, m->final_hidden, m->dscalars + 2, c.n_layers, s);
+    if (layer_trace_dev)
+        hipMemcpyAsync(layer_trace_dev + (size_t)(c.n_layers - 1) * E, m->hidden, (size_t)E * 4,
+                       hipMemcpyDeviceToDevice, s);
+}
+
+wm_status check_step(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t pos) {
+    wm_ctx *ctx = m->ctx;
+    if (!model_ready(m)) return wm_set_error(ctx, WM_E_STATE, "model: weights not fully set");
+    if (kv->m != m) return wm_set_error(ctx, WM_E_ARG, "kv cache belongs to another model");
+    if (pos != kv->pos)
+        return wm_set_error(ctx, WM_E_STATE,
+                            "forward_with_cache: cache.position()=%u != position=%u; tokens must be processed in order",
+                            kv->pos, pos);
+    if (pos >= kv->max_seq)
+        return wm_set_error(ctx, WM_E_SHAPE, "KVCache::append: already at max_seq_len %u", kv->max_seq);
+    if (token >= m->cfg.vocab_size)
+        return wm_set_error(ctx, WM_E_SHAPE, "forward_with_cache: token_id %u out of vocab range %u",
+                            token, m->cfg.vocab_size);
+    return WM_OK;
+}
+
+// After the step: read the error flag; on a non-finite hidden the cache is
+// rolled back (cached_forward.rs:256-259) and the flag cleared.
+wm_status finish_step(wm_model *m, wm_kv_cache *kv, uint32_t pos, bool *failed) {
+    wm_ctx *ctx = m->ctx;
+    uint32_t flag = 0;
+    WM_HIP(ctx, hipMemcpyAsync(&flag, m->dscalars + 2, 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    *failed = flag != 0;
+    if (flag) {
+        uint32_t zero = 0;
+        WM_HIP(ctx, hipMemcpyAsync(m->dscalars + 2, &zero, 4, hipMemcpyHostToDevice, ctx->stream));
+        WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        kv->pos = pos;
+        return wm_set_error(ctx, WM_E_NONFINITE, "forward_with_cache: non-finite hidden after layer %u",
+                            flag - 1);
+    }
+    kv->pos = pos + 1;
+    return WM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **out) {
+    if (!ctx || !cfg || !out) return WM_E_ARG;
+    *out = nullptr;
+    const wm_model_config &c = *cfg;
+    if (!c.n_layers || !c.n_embd || !c.n_ff || !c.n_heads || !c.n_kv_heads || !c.head_dim ||
+        !c.vocab_size || !c.context_length)
+        return wm_set_error(ctx, WM_E_SHAPE, "model config: zero dimension");
+    if (c.n_heads % c.n_kv_heads)
+        return wm_set_error(ctx, WM_E_SHAPE, "gqa_group_size: n_heads (%u) not divisible by n_kv_heads (%u)",
+                            c.n_heads, c.n_kv_heads);
+    if (c.n_heads * c.head_dim != c.n_embd || c.head_dim % 64 || c.head_dim > 1024)
+        return wm_set_error(ctx, WM_E_SHAPE, "model config: head_dim %u unsupported", c.head_dim);
+    if (c.n_rot == 0 || c.n_rot % 2 || c.n_rot > c.head_dim)
+        return wm_set_error(ctx, WM_E_SHAPE, "apply_rope_f32: n_rot=%u must be even and <= head_dim",
+                            c.n_rot);
+    if (c.n_embd % QK_I2S || c.n_ff % QK_I2S || c.n_embd % Q6K_VALUES)
+        return wm_set_error(ctx, WM_E_SHAPE, "model config: n_embd/n_ff must be multiples of 256/128");
+    if (c.n_ff > 16384 || c.n_embd > 16384 || c.context_length > 8192)
+        return wm_set_error(ctx, WM_E_SHAPE, "model config: dimensions beyond the supported range");
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    wm_model *m = new wm_model();
+    m->ctx = ctx;
+    m->cfg = c;
+    m->kv_dim = c.n_kv_heads * c.head_dim;
+    m->layers.resize(c.n_layers);
+    // RoPE angle tables, computed with the host libm exactly as
+    // apply_rope_f32 computes them (src/model/primitives.rs:313-318).
+    const uint32_t half = c.n_rot / 2;
+    std::vector<float> cs((size_t)c.context_length * half), sn(cs.size());
+    for (uint32_t p = 0; p < c.context_length; p++) {
+        const float pos = (float)p;
+        for (uint32_t j = 0; j < half; j++) {
+            float exponent = -2.0f * (float)j / (float)c.n_rot;
+            float theta = pos * powf(c.rope_freq_base, exponent);
+            sn[(size_t)p * half + j] = sinf(theta);
+            cs[(size_t)p * half + j] = cosf(theta);
+        }
+    }
+    const uint32_t E = c.n_embd, F = c.n_ff;
+    const uint32_t eg = (E + 63) / 64, fg = (F + 63) / 64, kvg = (m->kv_dim + 63) / 64;
+    m->split_qkv = wm_i2s_pick_split(eg + 2 * kvg, E / 64);
+    m->split_o = wm_i2s_pick_split(eg, E / 64);
+    m->split_gu = wm_i2s_pick_split(2 * fg, E / 64);
+    m->split_down = wm_i2s_pick_split(eg, F / 64);
+    size_t part = 0;
+    part = std::max(part, (size_t)m->split_qkv * (eg + 2 * kvg) * 64);
+    part = std::max(part, (size_t)m->split_o * eg * 64);
+    part = std::max(part, (size_t)m->split_gu * 2 * fg * 64);
+    part = std::max(part, (size_t)m->split_down * eg * 64);
+    const size_t sizes[] = {
+        align256((size_t)E * 4),                                  // hidden
+        align256((size_t)E * 4),                                  // q
+        align256((size_t)E * 4),                                  // attn_out
+        align256((size_t)F * 4),                                  // h_ff
+        align256((size_t)E * 4),                                  // final_hidden
+        align256((size_t)c.vocab_size * 4),                       // logits
+        align256((size_t)c.n_heads * c.context_length * 4),       // scores
+        align256((size_t)std::max(E, F)),                         // act
+        256,                                                      // meta[4]
+        align256(part * 4),                                       // partial
+        256,                                                      // device scalars
+        align256(wm_q6k_logits_work_bytes()),                     // lm-head work
+        align256(cs.size() * 4), align256(cs.size() * 4),         // rope tables
+    };
+    size_t total = 0;
+    for (size_t sz : sizes) total += sz;
+    hipError_t e = hipMalloc((void **)&m->ws, total);
+    if (e != hipSuccess) {
+        delete m;
+        return wm_hip_error(ctx, e, "wm_model_create workspace");
+    }
+    uint8_t *p = m->ws;
+    void **slots[] = {(void **)&m->hidden, (void **)&m->q, (void **)&m->attn_out, (void **)&m->h_ff,
+                      (void **)&m->final_hidden, (void **)&m->logits, (void **)&m->scores,
+                      (void **)&m->act, (void **)&m->meta, (void **)&m->partial,
+                      (void **)&m->dscalars, (void **)&m->lm_work, (void **)&m->rope_cos,
+                      (void **)&m->rope_sin};
+    for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); i++) {
+        *slots[i] = p;
+        p += sizes[i];
+    }
+    e = hipMemsetAsync(m->ws, 0, total, ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        hipFree(m->ws);
+        delete m;
+        return wm_hip_error(ctx, e, "wm_model_create");
+    }
+    *out = m;
+    return WM_OK;
+}
+
+void wm_model_destroy(wm_model *m) {
+    if (!m) return;
+    hipSetDevice(m->ctx->device);
+    hipStreamSynchronize(m->ctx->stream);
+    for (auto &l : m->layers) {
+        free_lin(l.q); free_lin(l.k); free_lin(l.v); free_lin(l.o);
+        free_lin(l.gate); free_lin(l.up); free_lin(l.down);
+        float *n[] = {l.attn_norm, l.attn_sub_norm, l.ffn_norm, l.ffn_sub_norm};
+        for (float *x : n)
+            if (x) hipFree(x);
+    }
+    if (m->embd) hipFree(m->embd);
+    if (m->output_norm) hipFree(m->output_norm);
+    if (m->ws) hipFree(m->ws);
+    delete m;
+}
+
+wm_status wm_model_set_layer(wm_model *m, uint32_t layer, const wm_tensor *attn_q,
+                             const wm_tensor *attn_k, const wm_tensor *attn_v,
+                             const wm_tensor *attn_output, const wm_tensor *ffn_gate,
+                             const wm_tensor *ffn_up, const wm_tensor *ffn_down,
+                             const float *attn_norm, const float *attn_sub_norm,
+                             const float *ffn_norm, const float *ffn_sub_norm) {
+    if (!m) return WM_E_ARG;
+    wm_ctx *ctx = m->ctx;
+    if (layer >= m->cfg.n_layers)
+        return wm_set_error(ctx, WM_E_ARG, "layer %u >= n_layers %u", layer, m->cfg.n_layers);
+    const uint64_t E = m->cfg.n_embd, F = m->cfg.n_ff, KV = m->kv_dim;
+    // shapes of src/model/graph.rs role table (docs/BITLINEAR_I2S_MATVEC.md:26-34)
+    const wm_tensor *ts[7] = {attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up, ffn_down};
+    const uint64_t ins[7] = {E, E, E, E, E, E, F}, outs[7] = {E, KV, KV, E, F, F, E};
+    const char *names[7] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
+    for (int i = 0; i < 7; i++) {
+        if (!ts[i]) return wm_set_error(ctx, WM_E_ARG, "%s: missing tensor", names[i]);
+        if (ts[i]->ctx != ctx) return wm_set_error(ctx, WM_E_ARG, "%s: tensor of another context", names[i]);
+        if (ts[i]->type != WM_TYPE_I2S)
+            return wm_set_error(ctx, WM_E_UNSUPPORTED_TYPE, "%s: tensor type %d is not I2_S", names[i],
+                                ts[i]->type);
+        if (ts[i]->in_dim != ins[i] || ts[i]->out_dim != outs[i])
+            return wm_set_error(ctx, WM_E_SHAPE, "%s: shape [%llu, %llu] != [%llu, %llu]", names[i],
+                                (unsigned long long)ts[i]->in_dim, (unsigned long long)ts[i]->out_dim,
+                                (unsigned long long)ins[i], (unsigned long long)outs[i]);
+    }
+    if (!attn_norm || !attn_sub_norm || !ffn_norm || !ffn_sub_norm)
+        return wm_set_error(ctx, WM_E_ARG, "layer %u: missing norm weights", layer);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    dev_layer &L = m->layers[layer];
+    dev_lin *dst[7] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
+    wm_status st;
+    for (int i = 0; i < 7; i++)
+        if ((st = copy_lin(m, ts[i], ins[i], outs[i], dst[i], names[i]))) return st;
+    if ((st = copy_norm(m, attn_norm, (uint32_t)E, &L.attn_norm, "attn_norm"))) return st;
+    if ((st = copy_norm(m, attn_sub_norm, (uint32_t)E, &L.attn_sub_norm, "attn_sub_norm"))) return st;
+    if ((st = copy_norm(m, ffn_norm, (uint32_t)E, &L.ffn_norm, "ffn_norm"))) return st;
+    if ((st = copy_norm(m, ffn_sub_norm, (uint32_t)F, &L.ffn_sub_norm, "ffn_sub_norm"))) return st;
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    L.set = true;
+    return WM_OK;
+}
+
+wm_status wm_model_set_output(wm_model *m, const wm_tensor *token_embd, const float *output_norm) {
+    if (!m) return WM_E_ARG;
+    wm_ctx *ctx = m->ctx;
+    if (!token_embd || !output_norm) return wm_set_error(ctx, WM_E_ARG, "set_output: missing argument");
+    if (token_embd->type != WM_TYPE_Q6K)
+        return wm_set_error(ctx, WM_E_UNSUPPORTED_TYPE, "token_embd: tensor type %d is not Q6_K",
+                            token_embd->type);
+    if (token_embd->in_dim != m->cfg.n_embd || token_embd->out_dim != m->cfg.vocab_size)
+        return wm_set_error(ctx, WM_E_SHAPE, "compute_logits: token_embd shape [%llu, %llu] != [%u, %u]",
+                            (unsigned long long)token_embd->in_dim, (unsigned long long)token_embd->out_dim,
+                            m->cfg.n_embd, m->cfg.vocab_size);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    if (m->embd) WM_HIP(ctx, hipFree(m->embd));
+    m->embd = nullptr;
+    WM_HIP(ctx, hipMalloc((void **)&m->embd, token_embd->bytes));
+    WM_HIP(ctx, hipMemcpyAsync(m->embd, token_embd->d, token_embd->bytes, hipMemcpyDeviceToDevice,
+                               ctx->stream));
+    m->embd_blocks = token_embd->n_blocks;
+    m->embd_rowgroups = token_embd->n_rowgroups;
+    wm_status st = copy_norm(m, output_norm, m->cfg.n_embd, &m->output_norm, "output_norm");
+    if (st) return st;
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return WM_OK;
+}
+
+wm_status wm_kv_cache_create(wm_model *m, uint32_t max_seq_len, wm_kv_cache **out) {
+    if (!m || !out) return WM_E_ARG;
+    *out = nullptr;
+    wm_ctx *ctx = m->ctx;
+    if (max_seq_len == 0 || max_seq_len > m->cfg.context_length)
+        return wm_set_error(ctx, WM_E_SHAPE, "KVCache::new: max_seq_len %u outside (0, context_length=%u]",
+                            max_seq_len, m->cfg.context_length);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    wm_kv_cache *kv = new wm_kv_cache();
+    kv->m = m;
+    kv->max_seq = max_seq_len;
+    const size_t nq = (size_t)m->cfg.n_layers * max_seq_len * m->kv_dim;
+    const size_t ns = (size_t)m->cfg.n_layers * max_seq_len;
+    hipError_t e = hipMalloc((void **)&kv->k, nq);
+    if (e == hipSuccess) e = hipMalloc((void **)&kv->v, nq);
+    if (e == hipSuccess) e = hipMalloc((void **)&kv->ks, ns * 4);
+    if (e == hipSuccess) e = hipMalloc((void **)&kv->vs, ns * 4);
+    if (e != hipSuccess) {
+        wm_kv_cache_destroy(kv);
+        return wm_hip_error(ctx, e, "KVCache::new");
+    }
+    *out = kv;
+    return WM_OK;
+}
+
+void wm_kv_cache_destroy(wm_kv_cache *kv) {
+    if (!kv) return;
+    hipSetDevice(kv->m->ctx->device);
+    hipStreamSynchronize(kv->m->ctx->stream);
+    if (kv->k) hipFree(kv->k);
+    if (kv->v) hipFree(kv->v);
+    if (kv->ks) hipFree(kv->ks);
+    if (kv->vs) hipFree(kv->vs);
+    delete kv;
+}
+
+uint32_t wm_kv_cache_position(const wm_kv_cache *kv) { return kv ? kv->pos : 0; }
+
+wm_status wm_kv_cache_rollback(wm_kv_cache *kv, uint32_t position) {
+    if (!kv) return WM_E_ARG;
+    if (position < kv->pos) kv->pos = position;  // truncate (kv_cache.rs:141-149)
+    return WM_OK;
+}
+
+wm_status wm_kv_cache_append_positions(wm_kv_cache *kv, const float *k, const float *v,
+                                       uint32_t n_pos) {
+    if (!kv || !k || !v) return WM_E_ARG;
+    wm_model *m = kv->m;
+    wm_ctx *ctx = m->ctx;
+    if (n_pos == 0) return WM_OK;
+    if ((uint64_t)kv->pos + n_pos > kv->max_seq)
+        return wm_set_error(ctx, WM_E_SHAPE, "KVCache::append: already at max_seq_len %u", kv->max_seq);
+    const size_t n = (size_t)n_pos * m->cfg.n_layers * m->kv_dim;
+    void *scratch;
+    wm_status st = wm_ctx_scratch(ctx, 2 * n * 4, &scratch);
+    if (st) return st;
+    float *dk = (float *)scratch, *dv = dk + n;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    WM_HIP(ctx, hipMemcpyAsync(dk, k, n * 4, hipMemcpyHostToDevice, ctx->stream));
+    WM_HIP(ctx, hipMemcpyAsync(dv, v, n * 4, hipMemcpyHostToDevice, ctx->stream));
+    wm_launch_kv_append(dk, dv, m->kv_dim, m->cfg.n_layers, kv->pos, n_pos, kv->max_seq, kv->k, kv->ks,
+                        kv->v, kv->vs, ctx->stream);
+    WM_HIP(ctx, hipGetLastError());
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    kv->pos += n_pos;
+    return WM_OK;
+}
+
+wm_status wm_kv_cache_append_position(wm_kv_cache *kv, const float *k, const float *v) {
+    return wm_kv_cache_append_positions(kv, k, v, 1);
+}
+
+wm_status wm_kv_cache_read_raw(wm_kv_cache *kv, uint32_t layer, int8_t *k, float *k_scales,
+                               int8_t *v, float *v_scales, uint32_t n_pos) {
+    if (!kv) return WM_E_ARG;
+    wm_ctx *ctx = kv->m->ctx;
+    if (layer >= kv->m->cfg.n_layers || n_pos > kv->max_seq)
+        return wm_set_error(ctx, WM_E_ARG, "read_raw: layer/position out of range");
+    const size_t KV = kv->m->kv_dim, lay = (size_t)layer * kv->max_seq;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    if (k) WM_HIP(ctx, hipMemcpyAsync(k, kv->k + lay * KV, n_pos * KV, hipMemcpyDeviceToHost, ctx->stream));
+    if (v) WM_HIP(ctx, hipMemcpyAsync(v, kv->v + lay * KV, n_pos * KV, hipMemcpyDeviceToHost, ctx->stream));
+    if (k_scales)
+        WM_HIP(ctx, hipMemcpyAsync(k_scales, kv->ks + lay, n_pos * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (v_scales)
+        WM_HIP(ctx, hipMemcpyAsync(v_scales, kv->vs + lay, n_pos * 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return WM_OK;
+}
+
+wm_status wm_forward_with_cache(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t position,
+                                float *hidden_out, float *layer_trace) {
+    if (!m || !kv) return WM_E_ARG;
+    wm_ctx *ctx = m->ctx;
+    wm_status st = check_step(m, kv, token, position);
+    if (st) return st;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    float *trace_dev = nullptr;
+    const size_t E = m->cfg.n_embd;
+    if (layer_trace) {
+        void *scratch;
+        if ((st = wm_ctx_scratch(ctx, (size_t)m->cfg.n_layers * E * 4, &scratch))) return st;
+        trace_dev = (float *)scratch;
+    }
+    WM_HIP(ctx, hipMemcpyAsync(m->dscalars, &token, 4, hipMemcpyHostToDevice, ctx->stream));
+    enqueue_forward(m, kv, position, trace_dev);
+    WM_HIP(ctx, hipGetLastError());
+    bool failed = false;
+    if ((st = finish_step(m, kv, position, &failed))) return st;
+    if (hidden_out)
+        WM_HIP(ctx, hipMemcpyAsync(hidden_out, m->final_hidden, E * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (layer_trace)
+        WM_HIP(ctx, hipMemcpyAsync(layer_trace, trace_dev, (size_t)m->cfg.n_layers * E * 4,
+                                   hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return WM_OK;
+}
+
+wm_status wm_decode_step(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t position,
+                         float *hidden_out, float *logits_out, uint32_t *next_token) {
+    if (!m || !kv) return WM_E_ARG;
+    wm_ctx *ctx = m->ctx;
+    wm_status st = check_step(m, kv, token, position);
+    if (st) return st;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    WM_HIP(ctx, hipMemcpyAsync(m->dscalars, &token, 4, hipMemcpyHostToDevice, ctx->stream));
+    enqueue_forward(m, kv, position, nullptr);
+    wm_launch_q6k_logits_argmax(m->embd, m->embd_blocks, m->cfg.vocab_size, m->embd_rowgroups,
+                                m->final_hidden, m->logits, m->dscalars + 1, m->lm_work, ctx->stream);
+    WM_HIP(ctx, hipGetLastError());
+    bool failed = false;
+    if ((st = finish_step(m, kv, position, &failed))) return st;
+    const size_t E = m->cfg.n_embd;
+    if (hidden_out)
+        WM_HIP(ctx, hipMemcpyAsync(hidden_out, m->final_hidden, E * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (logits_out)
+        WM_HIP(ctx, hipMemcpyAsync(logits_out, m->logits, (size_t)m->cfg.vocab_size * 4,
+                                   hipMemcpyDeviceToHost, ctx->stream));
+    uint32_t next = 0;
+    WM_HIP(ctx, hipMemcpyAsync(&next, m->dscalars + 1, 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (next_token) *next_token = next;
+    return WM_OK;
+}
+
+wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *prompt,
+                             uint32_t n_prompt, uint32_t max_new, int64_t eos, uint32_t *out_ids,
+                             uint32_t *n_out) {
+    if (!m || !kv || !n_out || (max_new && !out_ids)) return WM_E_ARG;
+    wm_ctx *ctx = m->ctx;
+    *n_out = 0;
+    if (!prompt || n_prompt == 0)
+        return wm_set_error(ctx, WM_E_ARG, "greedy_generate_with_cache: prompt_ids must not be empty");
+    for (uint32_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= m->cfg.vocab_size)
+            return wm_set_error(ctx, WM_E_SHAPE,
+                                "greedy_generate_with_cache: prompt token %u (idx %u) out of vocab range %u",
+                                prompt[i], i, m->cfg.vocab_size);
+    if ((uint64_t)kv->pos + n_prompt + (max_new ? max_new - 1 : 0) > kv->max_seq)
+        return wm_set_error(ctx, WM_E_SHAPE, "greedy_generate_with_cache: budget exceeds max_seq_len %u",
+                            kv->max_seq);
+    const uint32_t start = kv->pos;
+    wm_status st;
+    for (uint32_t i = 0; i + 1 < n_prompt; i++)
+        if ((st = wm_forward_with_cache(m, kv, prompt[i], kv->pos, nullptr, nullptr))) {
+            kv->pos = start;
+            return st;
+        }
+    uint32_t next = 0;
+    if ((st = wm_decode_step(m, kv, prompt[n_prompt - 1], kv->pos, nullptr, nullptr, &next))) {
+        kv->pos = start;
+        return st;
+    }
+    uint32_t n = 0;
+    for (uint32_t step = 0; step < max_new; step++) {
+        if (eos >= 0 && (int64_t)next == eos) break;
+        out_ids[n++] = next;
+        if (step + 1 < max_new) {
+            uint32_t tok = next;
+            if ((st = wm_decode_step(m, kv, tok, kv->pos, nullptr, nullptr, &next))) {
+                kv->pos = start;
+                return st;
+            }
+        }
+    }
+    *n_out = n;
+    return WM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,502 @@
+// C ABI: context, device buffers, tensors, BitLinear and Q6_K entry points.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "wm_internal.h"
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+wm_status wm_set_error(wm_ctx *ctx, wm_status st, const char *fmt, ...) {
+    if (ctx) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof(buf), fmt, ap);
+        va_end(ap);
+        ctx->last_error = buf;
+    }
+    return st;
+}
+
+wm_status wm_hip_error(wm_ctx *ctx, hipError_t e, const char *what) {
+    if (e == hipErrorOutOfMemory)
+        return wm_set_error(ctx, WM_E_OOM, "%s: %s", what, hipGetErrorString(e));
+    return wm_set_error(ctx, WM_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+wm_status wm_ctx_scratch(wm_ctx *ctx, size_t bytes, void **out) {
+    if (ctx->scratch_bytes < bytes) {
+        if (ctx->scratch) WM_HIP(ctx, hipFree(ctx->scratch));
+        ctx->scratch = nullptr;
+        ctx->scratch_bytes = 0;
+        size_t cap = bytes < (1u << 20) ? (1u << 20) : bytes;
+        WM_HIP(ctx, hipMalloc(&ctx->scratch, cap));
+        ctx->scratch_bytes = cap;
+    }
+    *out = ctx->scratch;
+    return WM_OK;
+}
+
+wm_status wm_ctx_pinned(wm_ctx *ctx, size_t bytes, void **out) {
+    if (ctx->pinned_bytes < bytes) {
+        if (ctx->pinned) WM_HIP(ctx, hipHostFree(ctx->pinned));
+        ctx->pinned = nullptr;
+        ctx->pinned_bytes = 0;
+        size_t cap = bytes < (1u << 20) ? (1u << 20) : bytes;
+        WM_HIP(ctx, hipHostMalloc(&ctx->pinned, cap, hipHostMallocDefault));
+        ctx->pinned_bytes = cap;
+    }
+    *out = ctx->pinned;
+    return WM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------
+extern "C" {
+
+const char *wm_version(void) { return "willamette-hip 0.1 (gfx950)"; }
+
+wm_status wm_ctx_create(int device, wm_ctx **out) {
+    if (!out) return WM_E_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return WM_E_HIP;
+    if (device < 0 || device >= n) return WM_E_ARG;
+    if (hipSetDevice(device) != hipSuccess) return WM_E_HIP;
+    wm_ctx *c = new wm_ctx();
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return WM_E_HIP;
+    }
+    *out = c;
+    return WM_OK;
+}
+
+void wm_ctx_destroy(wm_ctx *ctx) {
+    if (!ctx) return;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    if (ctx->scratch) hipFree(ctx->scratch);
+    if (ctx->pinned) hipHostFree(ctx->pinned);
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+const char *wm_last_error(const wm_ctx *ctx) { return ctx ? ctx->last_error.c_str() : ""; }
+
+void *wm_ctx_stream(wm_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+wm_status wm_ctx_synchronize(wm_ctx *ctx) {
+    if (!ctx) return WM_E_ARG;
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return WM_OK;
+}
+
+wm_status wm_dev_alloc(wm_ctx *ctx, size_t bytes, void **out) {
+    if (!ctx || !out) return WM_E_ARG;
+    *out = nullptr;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    WM_HIP(ctx, hipMalloc(out, bytes ? bytes : 1));
+    return WM_OK;
+}
+
+wm_status wm_dev_free(wm_ctx *ctx, void *ptr) {
+    if (!ctx) return WM_E_ARG;
+    if (ptr) {
+        WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        WM_HIP(ctx, hipFree(ptr));
+    }
+    return WM_OK;
+}
+
+wm_status wm_memcpy_h2d(wm_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return WM_E_ARG;
+    WM_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return WM_OK;
+}
+
+wm_status wm_memcpy_d2h(wm_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return WM_E_ARG;
+    WM_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return WM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// tensors
+// ---------------------------------------------------------------------------
+
+wm_status wm_tensor_upload_i2s(wm_ctx *ctx, const uint8_t *packed, size_t packed_len,
+                               const uint8_t *scale_block, size_t scale_len, uint64_t in_dim,
+                               uint64_t out_dim, wm_tensor **out) {
+    if (!ctx || !out) return WM_E_ARG;
+    *out = nullptr;
+    // src/model/bitlinear_sse2.rs:129-177 and src/gguf/tensor.rs:278-309
+    if (in_dim == 0 || in_dim % QK_I2S)
+        return wm_set_error(ctx, WM_E_SHAPE,
+                            "bitlinear: in_dim %llu is not a positive multiple of %d",
+                            (unsigned long long)in_dim, QK_I2S);
+    if (out_dim == 0 || out_dim > (1ull << 30) || in_dim > (1ull << 24))
+        return wm_set_error(ctx, WM_E_SHAPE, "bitlinear: unsupported shape [%llu, %llu]",
+                            (unsigned long long)in_dim, (unsigned long long)out_dim);
+    uint64_t expected = in_dim / 4 * out_dim;
+    if (!packed || packed_len < expected)
+        return wm_set_error(ctx, WM_E_SHAPE, "bitlinear: data.len()=%zu < %llu (in_dim/4 x out_dim)",
+                            packed_len, (unsigned long long)expected);
+    if (!scale_block || scale_len < 4)
+        return wm_set_error(ctx, WM_E_SHAPE, "i2s_scale: scale_data missing or shorter than 4 bytes");
+    float scale;
+    std::memcpy(&scale, scale_block, 4);
+    if (!std::isfinite(scale))
+        return wm_set_error(ctx, WM_E_NONFINITE, "i2s_scale: non-finite scale (%g)", (double)scale);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    wm_tensor *t = new wm_tensor();
+    t->ctx = ctx;
+    t->type = WM_TYPE_I2S;
+    t->in_dim = in_dim;
+    t->out_dim = out_dim;
+    t->scale = scale;
+    t->n_groups = (uint32_t)((out_dim + I2S_GROUP_ROWS - 1) / I2S_GROUP_ROWS);
+    t->n_chunks = (uint32_t)(in_dim / I2S_CHUNK_COLS);
+    t->bytes = (size_t)t->n_groups * t->n_chunks * I2S_GROUP_ROWS * 16;
+    void *raw = nullptr;
+    hipError_t e = hipMalloc(&t->d, t->bytes);
+    if (e == hipSuccess) e = hipMalloc(&raw, expected);
+    if (e == hipSuccess) e = hipMemcpyAsync(raw, packed, expected, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) {
+        wm_launch_i2s_repack((const uint8_t *)raw, (uint8_t *)t->d, (uint32_t)in_dim,
+                             (uint32_t)out_dim, t->n_groups, ctx->stream);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (raw) hipFree(raw);
+    if (e != hipSuccess) {
+        if (t->d) hipFree(t->d);
+        delete t;
+        return wm_hip_error(ctx, e, "wm_tensor_upload_i2s");
+    }
+    *out = t;
+    return WM_OK;
+}
+
+wm_status wm_tensor_upload_q6k(wm_ctx *ctx, const uint8_t *blocks, size_t len, uint64_t row_len,
+                               uint64_t n_rows, wm_tensor **out) {
+    if (!ctx || !out) return WM_E_ARG;
+    *out = nullptr;
+    if (row_len == 0 || row_len % Q6K_VALUES || row_len > 65536)
+        return wm_set_error(ctx, WM_E_SHAPE, "Q6_K value count %llu is not a multiple of 256",
+                            (unsigned long long)row_len);
+    if (n_rows == 0 || n_rows > (1ull << 28))
+        return wm_set_error(ctx, WM_E_SHAPE, "Q6_K: unsupported row count %llu",
+                            (unsigned long long)n_rows);
+    uint64_t expected = n_rows * (row_len / Q6K_VALUES) * Q6K_BYTES;
+    if (!blocks || len != expected)
+        return wm_set_error(ctx, WM_E_SHAPE, "Q6_K tensor has %zu bytes, expected %llu", len,
+                            (unsigned long long)expected);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    wm_tensor *t = new wm_tensor();
+    t->ctx = ctx;
+    t->type = WM_TYPE_Q6K;
+    t->in_dim = row_len;
+    t->out_dim = n_rows;
+    t->n_blocks = (uint32_t)(row_len / Q6K_VALUES);
+    t->n_rowgroups = (uint32_t)((n_rows + Q6K_GROUP_ROWS - 1) / Q6K_GROUP_ROWS);
+    t->bytes = (size_t)t->n_rowgroups * t->n_blocks * Q6K_GROUP_BLOCK_BYTES;
+    void *raw = nullptr;
+    hipError_t e = hipMalloc(&t->d, t->bytes);
+    if (e == hipSuccess) e = hipMalloc(&raw, expected);
+    if (e == hipSuccess) e = hipMemcpyAsync(raw, blocks, expected, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) {
+        wm_launch_q6k_repack((const uint8_t *)raw, (uint8_t *)t->d, (uint32_t)n_rows, t->n_blocks,
+                             t->n_rowgroups, ctx->stream);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (raw) hipFree(raw);
+    if (e != hipSuccess) {
+        if (t->d) hipFree(t->d);
+        delete t;
+        return wm_hip_error(ctx, e, "wm_tensor_upload_q6k");
+    }
+    *out = t;
+    return WM_OK;
+}
+
+void wm_tensor_destroy(wm_tensor *t) {
+    if (!t) return;
+    if (t->d) {
+        hipSetDevice(t->ctx->device);
+        hipStreamSynchronize(t->ctx->stream);
+        hipFree(t->d);
+    }
+    delete t;
+}
+
+wm_status wm_tensor_info(const wm_tensor *t, uint64_t shape[2], int *type, float *scale) {
+    if (!t) return WM_E_ARG;
+    if (shape) {
+        shape[0] = t->in_dim;
+        shape[1] = t->out_dim;
+    }
+    if (type) *type = t->type;
+    if (scale) *scale = t->scale;
+    return WM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// BitLinear
+// ---------------------------------------------------------------------------
+
+static wm_status check_i2s(wm_ctx *ctx, const wm_tensor *w) {
+    if (!ctx || !w) return WM_E_ARG;
+    if (w->type != WM_TYPE_I2S)
+        return wm_set_error(ctx, WM_E_UNSUPPORTED_TYPE, "bitlinear: tensor type %d is not I2_S",
+                            w->type);
+    if (w->ctx != ctx) return wm_set_error(ctx, WM_E_ARG, "bitlinear: tensor of another context");
+    return WM_OK;
+}
+
+// Device workspace for one matvec: act (in_dim bytes, 16-aligned), meta,
+// partials (split x rows).
+struct mv_ws {
+    uint8_t *act;
+    wm_act_meta *meta;
+    int32_t *partial;
+    float *x, *y;
+    int32_t *dot;
+};
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static void run_matvec(wm_ctx *ctx, const wm_tensor *w, const float *d_x, float *d_y,
+                       int32_t *d_dot, uint8_t *act, wm_act_meta *meta, int32_t *partial) {
+    uint32_t split = wm_i2s_pick_split(w->n_groups, w->n_chunks);
+    uint32_t rows_total = w->n_groups * I2S_GROUP_ROWS;
+    wm_launch_quantize_act(d_x, (uint32_t)w->in_dim, act, meta, ctx->stream);
+    wm_i2s_desc desc{(const uint8_t *)w->d, w->n_groups};
+    wm_launch_i2s_partial(&desc, 1, w->n_chunks, act, partial, split, rows_total, ctx->stream);
+    wm_launch_i2s_finalize(partial, split, rows_total, 0, (uint32_t)w->out_dim, w->scale, meta, d_y,
+                           d_dot, ctx->stream);
+}
+
+static size_t matvec_ws_bytes(const wm_tensor *w) {
+    uint32_t split = wm_i2s_pick_split(w->n_groups, w->n_chunks);
+    return align256(w->in_dim) + 256 + align256((size_t)split * w->n_groups * I2S_GROUP_ROWS * 4);
+}
+
+wm_status wm_bitlinear_i2s_matvec_f32_debug(wm_ctx *ctx, const wm_tensor *w, const float *input,
+                                            size_t input_len, float *output, size_t output_len,
+                                            int8_t *act_out, float *act_scale, int32_t *acc_out) {
+    wm_status st = check_i2s(ctx, w);
+    if (st) return st;
+    if (!input || !output) return wm_set_error(ctx, WM_E_ARG, "bitlinear: null input/output");
+    if (input_len != w->in_dim)
+        return wm_set_error(ctx, WM_E_SHAPE, "bitlinear: input.len()=%zu != in_dim=%llu", input_len,
+                            (unsigned long long)w->in_dim);
+    if (output_len != w->out_dim)
+        return wm_set_error(ctx, WM_E_SHAPE, "bitlinear: output.len()=%zu != out_dim=%llu",
+                            output_len, (unsigned long long)w->out_dim);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    const size_t in_b = align256(w->in_dim * 4), out_b = align256(w->out_dim * 4);
+    const size_t ws_b = matvec_ws_bytes(w);
+    void *scratch;
+    if ((st = wm_ctx_scratch(ctx, in_b + 2 * out_b + ws_b, &scratch))) return st;
+    uint8_t *base = (uint8_t *)scratch;
+    float *d_x = (float *)base;
+    float *d_y = (float *)(base + in_b);
+    int32_t *d_dot = (int32_t *)(base + in_b + out_b);
+    uint8_t *act = base + in_b + 2 * out_b;
+    wm_act_meta *meta = (wm_act_meta *)(act + align256(w->in_dim));
+    int32_t *partial = (int32_t *)((uint8_t *)meta + 256);
+    WM_HIP(ctx, hipMemcpyAsync(d_x, input, w->in_dim * 4, hipMemcpyHostToDevice, ctx->stream));
+    run_matvec(ctx, w, d_x, d_y, d_dot, act, meta, partial);
+    WM_HIP(ctx, hipGetLastError());
+    WM_HIP(ctx, hipMemcpyAsync(output, d_y, w->out_dim * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (acc_out)
+        WM_HIP(ctx, hipMemcpyAsync(acc_out, d_dot, w->out_dim * 4, hipMemcpyDeviceToHost, ctx->stream));
+    std::vector<uint8_t> act_perm;
+    wm_act_meta meta_h{};
+    if (act_out) {
+        act_perm.resize(w->in_dim);
+        WM_HIP(ctx, hipMemcpyAsync(act_perm.data(), act, w->in_dim, hipMemcpyDeviceToHost, ctx->stream));
+    }
+    if (act_scale)
+        WM_HIP(ctx, hipMemcpyAsync(&meta_h, meta, sizeof(meta_h), hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (act_out)
+        for (uint32_t i = 0; i < w->in_dim; i++) act_out[i] = (int8_t)act_perm[wm_act_perm(i)];
+    if (act_scale) *act_scale = meta_h.scale;
+    return WM_OK;
+}
+
+wm_status wm_bitlinear_i2s_matvec_f32(wm_ctx *ctx, const wm_tensor *w, const float *input,
+                                      size_t input_len, float *output, size_t output_len) {
+    return wm_bitlinear_i2s_matvec_f32_debug(ctx, w, input, input_len, output, output_len, nullptr,
+                                             nullptr, nullptr);
+}
+
+wm_status wm_bitlinear_i2s_matvec_f32_dev(wm_ctx *ctx, const wm_tensor *w, const float *d_input,
+                                          float *d_output) {
+    return wm_bitlinear_i2s_matvec_f32_multi_dev(ctx, &w, 1, d_input, d_output);
+}
+
+wm_status wm_bitlinear_i2s_matvec_f32_multi_dev(wm_ctx *ctx, const wm_tensor *const *ws,
+                                                uint32_t n_copies, const float *d_input,
+                                                float *d_outputs) {
+    if (!ctx || !ws || !n_copies || !d_input || !d_outputs) return WM_E_ARG;
+    wm_status st;
+    for (uint32_t i = 0; i < n_copies; i++) {
+        if ((st = check_i2s(ctx, ws[i]))) return st;
+        if (ws[i]->in_dim != ws[0]->in_dim || ws[i]->out_dim != ws[0]->out_dim)
+            return wm_set_error(ctx, WM_E_SHAPE, "bitlinear multi: tensors differ in shape");
+    }
+    const wm_tensor *w0 = ws[0];
+    const uint32_t per = w0->n_groups;
+    const uint32_t max_n = n_copies < WM_I2S_MAX_MULTI ? n_copies : WM_I2S_MAX_MULTI;
+    const uint32_t split = wm_i2s_pick_split(per * max_n, w0->n_chunks);
+    const size_t rows_max = (size_t)per * max_n * I2S_GROUP_ROWS;
+    const size_t need = align256(w0->in_dim) + 256 + align256(max_n * 4) +
+                        align256((size_t)split * rows_max * 4);
+    void *scratch;
+    if ((st = wm_ctx_scratch(ctx, need, &scratch))) return st;
+    uint8_t *act = (uint8_t *)scratch;
+    wm_act_meta *meta = (wm_act_meta *)(act + align256(w0->in_dim));
+    float *scales = (float *)((uint8_t *)meta + 256);
+    int32_t *partial = (int32_t *)((uint8_t *)scales + align256(max_n * 4));
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    wm_launch_quantize_act(d_input, (uint32_t)w0->in_dim, act, meta, ctx->stream);
+    for (uint32_t base = 0; base < n_copies; base += WM_I2S_MAX_MULTI) {
+        const uint32_t n = n_copies - base < WM_I2S_MAX_MULTI ? n_copies - base : WM_I2S_MAX_MULTI;
+        wm_i2s_desc desc[WM_I2S_MAX_MULTI];
+        float hs[WM_I2S_MAX_MULTI];
+        for (uint32_t i = 0; i < n; i++) {
+            desc[i] = {(const uint8_t *)ws[base + i]->d, per};
+            hs[i] = ws[base + i]->scale;
+        }
+        // the scales ride on the stream so a later chunk cannot overwrite them early
+        WM_HIP(ctx, hipMemcpyAsync(scales, hs, n * 4, hipMemcpyHostToDevice, ctx->stream));
+        const uint32_t rows_total = per * n * I2S_GROUP_ROWS;
+        const uint32_t sp = n == max_n ? split : wm_i2s_pick_split(per * n, w0->n_chunks);
+        wm_launch_i2s_partial(desc, (int)n, w0->n_chunks, act, partial, sp, rows_total, ctx->stream);
+        wm_launch_i2s_finalize_multi(partial, sp, rows_total, per * I2S_GROUP_ROWS,
+                                     (uint32_t)w0->out_dim, n, scales, meta,
+                                     d_outputs + (size_t)base * w0->out_dim, ctx->stream);
+    }
+    WM_HIP(ctx, hipGetLastError());
+    return WM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K
+// ---------------------------------------------------------------------------
+
+static wm_status check_q6k(wm_ctx *ctx, const wm_tensor *t) {
+    if (!ctx || !t) return WM_E_ARG;
+    if (t->type != WM_TYPE_Q6K)
+        return wm_set_error(ctx, WM_E_UNSUPPORTED_TYPE, "Q6_K: tensor type %d is not Q6_K", t->type);
+    if (t->ctx != ctx) return wm_set_error(ctx, WM_E_ARG, "Q6_K: tensor of another context");
+    return WM_OK;
+}
+
+wm_status wm_q6k_dequantize_row(wm_ctx *ctx, const wm_tensor *t, uint64_t row, float *out,
+                                size_t out_len) {
+    wm_status st = check_q6k(ctx, t);
+    if (st) return st;
+    if (!out) return WM_E_ARG;
+    if (out_len != t->in_dim)
+        return wm_set_error(ctx, WM_E_SHAPE, "embedding_gather: out.len()=%zu != n_embd=%llu",
+                            out_len, (unsigned long long)t->in_dim);
+    if (row >= t->out_dim)
+        return wm_set_error(ctx, WM_E_SHAPE, "embedding_gather: token_id %llu out of range (vocab_size=%llu)",
+                            (unsigned long long)row, (unsigned long long)t->out_dim);
+    void *scratch;
+    if ((st = wm_ctx_scratch(ctx, t->in_dim * 4, &scratch))) return st;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    wm_launch_q6k_dequant_row((const uint8_t *)t->d, t->n_blocks, (uint32_t)row, (float *)scratch,
+                              ctx->stream);
+    WM_HIP(ctx, hipGetLastError());
+    WM_HIP(ctx, hipMemcpyAsync(out, scratch, t->in_dim * 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return WM_OK;
+}
+
+wm_status wm_logits_argmax_dev(wm_ctx *ctx, const wm_tensor *t, const float *d_hidden,
+                               float *d_logits, uint32_t *d_argmax) {
+    wm_status st = check_q6k(ctx, t);
+    if (st) return st;
+    if (!d_hidden || (!d_logits && !d_argmax)) return WM_E_ARG;
+    const size_t lb = align256(t->out_dim * 4);
+    void *scratch;
+    if ((st = wm_ctx_scratch(ctx, lb + wm_q6k_logits_work_bytes(), &scratch))) return st;
+    float *logits = d_logits ? d_logits : (float *)scratch;
+    void *work = (uint8_t *)scratch + lb;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    wm_launch_q6k_logits_argmax((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
+                                t->n_rowgroups, d_hidden, logits, d_argmax, work, ctx->stream);
+    WM_HIP(ctx, hipGetLastError());
+    return WM_OK;
+}
+
+wm_status wm_logits_argmax(wm_ctx *ctx, const wm_tensor *t, const float *hidden,
+                           size_t hidden_len, float *logits, uint32_t *argmax) {
+    wm_status st = check_q6k(ctx, t);
+    if (st) return st;
+    if (!hidden || (!logits && !argmax)) return WM_E_ARG;
+    if (hidden_len != t->in_dim)
+        return wm_set_error(ctx, WM_E_SHAPE, "compute_logits: final_hidden.len()=%zu != embedding_length=%llu",
+                            hidden_len, (unsigned long long)t->in_dim);
+    const size_t hb = align256(t->in_dim * 4), lb = align256(t->out_dim * 4);
+    const size_t need = hb + lb + 256 + lb + wm_q6k_logits_work_bytes();
+    void *scratch;
+    if ((st = wm_ctx_scratch(ctx, need, &scratch))) return st;
+    uint8_t *base = (uint8_t *)scratch;
+    float *d_h = (float *)base;
+    float *d_l = (float *)(base + hb);
+    uint32_t *d_a = (uint32_t *)(base + hb + lb);
+    void *work = base + hb + lb + 256;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    WM_HIP(ctx, hipMemcpyAsync(d_h, hidden, t->in_dim * 4, hipMemcpyHostToDevice, ctx->stream));
+    wm_launch_q6k_logits_argmax((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
+                                t->n_rowgroups, d_h, d_l, d_a, work, ctx->stream);
+    WM_HIP(ctx, hipGetLastError());
+    if (logits)
+        WM_HIP(ctx, hipMemcpyAsync(logits, d_l, t->out_dim * 4, hipMemcpyDeviceToHost, ctx->stream));
+    uint32_t a = 0;
+    WM_HIP(ctx, hipMemcpyAsync(&a, d_a, 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (argmax) *argmax = a;
+    return WM_OK;
+}
+
+wm_status wm_compute_logits(wm_ctx *ctx, const wm_tensor *t, const float *hidden,
+                            size_t hidden_len, float *logits, size_t vocab) {
+    wm_status st = check_q6k(ctx, t);
+    if (st) return st;
+    if (!logits) return WM_E_ARG;
+    if (vocab != t->out_dim)
+        return wm_set_error(ctx, WM_E_SHAPE, "compute_logits: vocab %zu != %llu", vocab,
+                            (unsigned long long)t->out_dim);
+    return wm_logits_argmax(ctx, t, hidden, hidden_len, logits, nullptr);
+}
+
+wm_status wm_argmax(const float *logits, size_t n, uint32_t *out) {
+    if (!logits || !out || n == 0) return WM_E_ARG;
+    size_t best = 0;
+    float bv = logits[0];
+    for (size_t i = 1; i < n; i++)
+        if (logits[i] > bv) {
+            bv = logits[i];
+            best = i;
+        }
+    *out = (uint32_t)best;
+    return WM_OK;
+}
+
+}  // extern "C"

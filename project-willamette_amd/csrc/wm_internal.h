@@ -1,0 +1,189 @@
+// Internal definitions shared by the HIP translation units of
+// libwillamette_hip.so.  gfx950 (CDNA4) only.
+//
+// Every f32 expression on the decode path is evaluated as the reference's
+// Rust code evaluates it: one IEEE round-to-nearest-even rounding per `+`,
+// `*`, `/`, `sqrt`, never contracted (the library is built with
+// -ffp-contract=off; fused multiply-adds appear only where written as
+// __builtin_fma* and are exact there), IEEE denormals, and reductions in the
+// reference's sequential order wherever the reference's order fixes the
+// rounding.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "willamette_hip.h"
+#define WM_HD __host__ __device__
+#include "wm_expf.h"
+
+// ---------------------------------------------------------------------------
+// host-side plumbing
+// ---------------------------------------------------------------------------
+
+struct wm_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string last_error;
+    // Scratch used by the host-pointer entry points (grown on demand).
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+    void *pinned = nullptr;  // pinned host staging
+    size_t pinned_bytes = 0;
+};
+
+struct wm_tensor {
+    wm_ctx *ctx = nullptr;
+    int type = 0;
+    uint64_t in_dim = 0;   // I2_S: columns; Q6_K: row_len
+    uint64_t out_dim = 0;  // I2_S: rows;    Q6_K: n_rows
+    float scale = 1.0f;    // I2_S per-tensor scale
+    void *d = nullptr;     // device data in the library's layout
+    size_t bytes = 0;
+    // I2_S layout: 64-row groups x (in_dim/64) 16-byte chunks x 64 rows.
+    uint32_t n_groups = 0, n_chunks = 0;
+    // Q6_K layout: 4-row groups x blocks, 840 bytes per (group, block).
+    uint32_t n_rowgroups = 0, n_blocks = 0;
+};
+
+wm_status wm_set_error(wm_ctx *ctx, wm_status st, const char *fmt, ...);
+wm_status wm_hip_error(wm_ctx *ctx, hipError_t e, const char *what);
+#define WM_HIP(ctx, expr)                                          \
+    do {                                                           \
+        hipError_t e_ = (expr);                                    \
+        if (e_ != hipSuccess) return wm_hip_error((ctx), e_, #expr); \
+    } while (0)
+
+// Grows ctx->scratch to at least `bytes` and returns it.
+wm_status wm_ctx_scratch(wm_ctx *ctx, size_t bytes, void **out);
+wm_status wm_ctx_pinned(wm_ctx *ctx, size_t bytes, void **out);
+
+// ---------------------------------------------------------------------------
+// constants of the I2_S / Q6_K formats (src/gguf/tensor.rs:86-105)
+// ---------------------------------------------------------------------------
+constexpr int QK_I2S = 128;        // values per packed block
+constexpr int I2S_BLOCK_BYTES = 32;
+constexpr int I2S_GROUP_ROWS = 64;  // rows per group of the device layout
+constexpr int I2S_CHUNK_COLS = 64;  // columns covered by one 16-byte chunk
+#define WM_I2S_MAX_MULTI 64
+constexpr int Q6K_VALUES = 256;
+constexpr int Q6K_BYTES = 210;
+constexpr int Q6K_GROUP_ROWS = 4;         // rows per wave in the device layout
+constexpr int Q6K_GROUP_BLOCK_BYTES = 840;  // 4 rows x 210 bytes
+constexpr int Q6K_SC_OFFSET = 768;          // per (group, block): q6 768 B, sc 64 B, d 8 B
+constexpr int Q6K_D_OFFSET = 832;
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+
+// Rust `(v).round().clamp(-127.0, 127.0) as i8`: round half away from zero,
+// a clamp that lets NaN through, and a saturating cast that maps NaN to 0
+// (src/model/bitlinear_sse2.rs:300, src/model/kv_cache.rs:255).
+__device__ __forceinline__ int wm_round_clamp_i8(float v) {
+    float r = roundf(v);
+    r = r < -127.0f ? -127.0f : r;
+    r = r > 127.0f ? 127.0f : r;
+    return (r != r) ? 0 : (int)r;
+}
+
+// Exact IEEE binary16 -> binary32 in integer arithmetic
+// (src/model/primitives.rs:61-88); no dependence on the FP unit's
+// denormal mode.
+__device__ __forceinline__ float wm_f16_bits_to_f32(uint32_t bits) {
+    uint32_t sign = (bits >> 15) & 1u, exp = (bits >> 10) & 0x1Fu, man = bits & 0x3FFu;
+    uint32_t out;
+    if (exp == 0) {
+        if (man == 0) {
+            out = sign << 31;
+        } else {
+            // normalise the subnormal: value = man * 2^-24
+            int sh = __clz(man) - 21;  // leading zeros within 10 bits, +1 to hide the MSB
+            man = (man << sh) & 0x3FFu;
+            out = (sign << 31) | ((uint32_t)(127 - 15 + 1 - sh) << 23) | (man << 13);
+        }
+    } else if (exp == 0x1F) {
+        out = (sign << 31) | (0xFFu << 23) | (man << 13);
+    } else {
+        out = (sign << 31) | ((exp + (127 - 15)) << 23) | (man << 13);
+    }
+    return __uint_as_float(out);
+}
+
+// glibc-identical expf (host/device, see wm_expf.h)
+__device__ __forceinline__ float wm_expf(float x) { return wm::expf_glibc(x); }
+
+// Wave-level helpers (wave64).
+__device__ __forceinline__ int wm_wave_sum_i32(int v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+// max that never lets a NaN win (`if a > m { m = a }`)
+__device__ __forceinline__ float wm_max_nonan(float m, float a) { return a > m ? a : m; }
+__device__ __forceinline__ float wm_wave_max_nonan(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = wm_max_nonan(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Position of activation element i (0 <= i < in_dim) in the chunk-permuted
+// layout the I2_S matvec reads: chunk c = 16-byte weight chunk index along
+// the row, 64 bytes per chunk ordered [quarter k][gp].
+__host__ __device__ __forceinline__ uint32_t wm_act_perm(uint32_t i) {
+    uint32_t bk = i >> 7, rem = i & 127u, k = rem >> 5, rem32 = rem & 31u;
+    uint32_t half = rem32 >> 4, gp = rem32 & 15u;
+    return (bk * 2 + half) * 64 + k * 16 + gp;
+}
+
+// ---------------------------------------------------------------------------
+// kernel launchers (defined in the .hip files)
+// ---------------------------------------------------------------------------
+
+// Activation record written by every quantising kernel and read by the
+// matvec epilogues: the per-vector absmax scale and the sum of the int8
+// activations (the matvec computes sum(code * a) with code in {0,1,2} and
+// subtracts sum(a) to obtain sum(ternary * a)).
+struct wm_act_meta {
+    float scale;
+    int32_t asum;
+};
+
+// I2_S repack: raw TensorView bytes (device) -> library layout (device).
+void wm_launch_i2s_repack(const uint8_t *raw, uint8_t *out, uint32_t in_dim, uint32_t out_dim,
+                          uint32_t n_groups, hipStream_t s);
+// Quantise f32 x[n] -> permuted int8 act + meta (one workgroup).
+void wm_launch_quantize_act(const float *x, uint32_t n, uint8_t *act, wm_act_meta *meta,
+                            hipStream_t s);
+// Partial dots over K splits (one launch covers up to WM_I2S_MAX_MULTI
+// tensors sharing one input): partial[split][row], rows = n_groups*64.
+struct wm_i2s_desc {
+    const uint8_t *w;  // library layout
+    uint32_t n_groups;
+};
+void wm_launch_i2s_partial(const wm_i2s_desc *descs, int n_desc, uint32_t n_chunks,
+                           const uint8_t *act, int32_t *partial, uint32_t split,
+                           uint32_t rows_total, hipStream_t s);
+// y[j] = (w_scale * act_scale) * (sum_s partial[s][j] - asum), j < out_dim.
+void wm_launch_i2s_finalize(const int32_t *partial, uint32_t split, uint32_t rows_total,
+                            uint32_t row0, uint32_t out_dim, float w_scale,
+                            const wm_act_meta *meta, float *y, int32_t *dot_out, hipStream_t s);
+uint32_t wm_i2s_pick_split(uint32_t n_groups, uint32_t n_chunks);
+void wm_launch_i2s_finalize_multi(const int32_t *partial, uint32_t split, uint32_t rows_total,
+                                  uint32_t rows_per_copy, uint32_t out_dim, uint32_t n_copies,
+                                  const float *w_scales, const wm_act_meta *meta, float *y,
+                                  hipStream_t s);
+
+// Q6_K
+void wm_launch_q6k_repack(const uint8_t *raw, uint8_t *out, uint32_t n_rows, uint32_t n_blocks,
+                          uint32_t n_rowgroups, hipStream_t s);
+void wm_launch_q6k_dequant_row(const uint8_t *w, uint32_t n_blocks, uint32_t row, float *out,
+                               hipStream_t s);
+void wm_launch_q6k_dequant_row_dev(const uint8_t *w, uint32_t n_blocks, const uint32_t *d_row,
+                                   float *out, hipStream_t s);
+// logits (exact SSE2 order) + per-block argmax candidates + final argmax.
+void wm_launch_q6k_logits_argmax(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
+                                 uint32_t n_rowgroups, const float *hidden, float *logits,
+                                 uint32_t *argmax_out, void *work, hipStream_t s);
+size_t wm_q6k_logits_work_bytes();

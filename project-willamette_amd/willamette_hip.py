@@ -1,0 +1,343 @@
+"""ctypes binding of libwillamette_hip.so (the C ABI in include/willamette_hip.h).
+
+Python-side mirror of project-willamette's Rust API for the BitNet decode
+path, for tests and benchmarks:
+
+    bitlinear_i2s_matvec_f32(weight, input) -> output   src/model/bitlinear.rs:67
+    compute_logits(hidden, token_embd) -> logits        src/model/lm_head.rs:29
+    argmax(logits) -> id | None                         src/model/lm_head.rs:161
+    Model / KVCache / forward_with_cache / greedy_generate
+                                  src/model/{graph,kv_cache,cached_forward,generate}.rs
+
+Errors raise WillametteError carrying the C status, mirroring the Rust
+`Result<_, WillametteError>` (src/error.rs:9-57).  There is no CPU
+fallback: if the shared library is missing this module fails to import.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("WILLAMETTE_HIP_LIB", _PKG / "libwillamette_hip.so"))
+
+if not LIB_PATH.exists():
+    raise ImportError(
+        f"{LIB_PATH} is missing: build it with `python project-willamette_amd/build.py` "
+        "(or __graft_entry__.build()); there is no CPU fallback"
+    )
+
+lib = C.CDLL(str(LIB_PATH))
+
+WM_OK = 0
+STATUS = {
+    1: "UnsupportedTensorType",
+    2: "Shape",
+    3: "NonFinite",
+    4: "OutOfMemory",
+    5: "Hip",
+    6: "Arg",
+    7: "State",
+}
+TYPE_I2S = 36
+TYPE_Q6K = 14
+
+
+class WillametteError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[{STATUS.get(status, status)}] {message}")
+        self.status = status
+        self.kind = STATUS.get(status, str(status))
+
+
+_u8p = C.POINTER(C.c_uint8)
+_i8p = C.POINTER(C.c_int8)
+_f32p = C.POINTER(C.c_float)
+_i32p = C.POINTER(C.c_int32)
+_u32p = C.POINTER(C.c_uint32)
+_vp = C.c_void_p
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [
+        ("n_layers", C.c_uint32),
+        ("n_embd", C.c_uint32),
+        ("n_ff", C.c_uint32),
+        ("n_heads", C.c_uint32),
+        ("n_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32),
+        ("n_rot", C.c_uint32),
+        ("vocab_size", C.c_uint32),
+        ("context_length", C.c_uint32),
+        ("rms_eps", C.c_float),
+        ("rope_freq_base", C.c_float),
+    ]
+
+
+def _sig(name, restype, *argtypes):
+    f = getattr(lib, name)
+    f.restype = restype
+    f.argtypes = list(argtypes)
+    return f
+
+
+# Every symbol the header declares.
+EXPORTS = {
+    "wm_ctx_create": (C.c_int, C.c_int, C.POINTER(_vp)),
+    "wm_ctx_destroy": (None, _vp),
+    "wm_last_error": (C.c_char_p, _vp),
+    "wm_ctx_stream": (_vp, _vp),
+    "wm_ctx_synchronize": (C.c_int, _vp),
+    "wm_version": (C.c_char_p,),
+    "wm_dev_alloc": (C.c_int, _vp, C.c_size_t, C.POINTER(_vp)),
+    "wm_dev_free": (C.c_int, _vp, _vp),
+    "wm_memcpy_h2d": (C.c_int, _vp, _vp, _vp, C.c_size_t),
+    "wm_memcpy_d2h": (C.c_int, _vp, _vp, _vp, C.c_size_t),
+    "wm_tensor_upload_i2s": (C.c_int, _vp, _u8p, C.c_size_t, _u8p, C.c_size_t, C.c_uint64,
+                             C.c_uint64, C.POINTER(_vp)),
+    "wm_tensor_upload_q6k": (C.c_int, _vp, _u8p, C.c_size_t, C.c_uint64, C.c_uint64,
+                             C.POINTER(_vp)),
+    "wm_tensor_destroy": (None, _vp),
+    "wm_tensor_info": (C.c_int, _vp, C.POINTER(C.c_uint64), C.POINTER(C.c_int), _f32p),
+    "wm_bitlinear_i2s_matvec_f32": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p, C.c_size_t),
+    "wm_bitlinear_i2s_matvec_f32_debug": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p,
+                                          C.c_size_t, _i8p, _f32p, _i32p),
+    "wm_bitlinear_i2s_matvec_f32_dev": (C.c_int, _vp, _vp, _vp, _vp),
+    "wm_bitlinear_i2s_matvec_f32_multi_dev": (C.c_int, _vp, C.POINTER(_vp), C.c_uint32, _vp, _vp),
+    "wm_q6k_dequantize_row": (C.c_int, _vp, _vp, C.c_uint64, _f32p, C.c_size_t),
+    "wm_compute_logits": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p, C.c_size_t),
+    "wm_logits_argmax": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p, _u32p),
+    "wm_logits_argmax_dev": (C.c_int, _vp, _vp, _vp, _vp, _vp),
+    "wm_argmax": (C.c_int, _f32p, C.c_size_t, _u32p),
+    "wm_model_create": (C.c_int, _vp, C.POINTER(ModelConfig), C.POINTER(_vp)),
+    "wm_model_destroy": (None, _vp),
+    "wm_model_set_layer": (C.c_int, _vp, C.c_uint32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32p,
+                           _f32p, _f32p, _f32p),
+    "wm_model_set_output": (C.c_int, _vp, _vp, _f32p),
+    "wm_kv_cache_create": (C.c_int, _vp, C.c_uint32, C.POINTER(_vp)),
+    "wm_kv_cache_destroy": (None, _vp),
+    "wm_kv_cache_position": (C.c_uint32, _vp),
+    "wm_kv_cache_rollback": (C.c_int, _vp, C.c_uint32),
+    "wm_kv_cache_append_position": (C.c_int, _vp, _f32p, _f32p),
+    "wm_kv_cache_append_positions": (C.c_int, _vp, _f32p, _f32p, C.c_uint32),
+    "wm_kv_cache_read_raw": (C.c_int, _vp, C.c_uint32, _i8p, _f32p, _i8p, _f32p, C.c_uint32),
+    "wm_forward_with_cache": (C.c_int, _vp, _vp, C.c_uint32, C.c_uint32, _f32p, _f32p),
+    "wm_decode_step": (C.c_int, _vp, _vp, C.c_uint32, C.c_uint32, _f32p, _f32p, _u32p),
+    "wm_greedy_generate": (C.c_int, _vp, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_int64, _u32p,
+                           _u32p),
+    "wm_synth_stream_seed": (C.c_uint64, C.c_uint64, C.c_uint64),
+    "wm_synth_i2s": (None, C.c_uint64, C.c_uint64, _u8p, C.c_size_t),
+    "wm_synth_normal": (None, C.c_uint64, C.c_uint64, _f32p, C.c_size_t, C.c_double),
+    "wm_synth_uniform": (None, C.c_uint64, C.c_uint64, _f32p, C.c_size_t, C.c_double, C.c_double),
+    "wm_synth_q6k": (None, C.c_uint64, C.c_uint64, _u8p, C.c_size_t, C.c_double),
+}
+
+for _name, (_res, *_args) in EXPORTS.items():
+    _sig(_name, _res, *_args)
+
+
+def _ptr(a: np.ndarray, ct):
+    return a.ctypes.data_as(C.POINTER(ct))
+
+
+# ---------------------------------------------------------------------------
+# synthetic inputs (src/synth.rs role; host only, no GPU needed)
+# ---------------------------------------------------------------------------
+
+def synth_i2s(seed: int, tag: int, in_dim: int, out_dim: int) -> np.ndarray:
+    out = np.empty(in_dim // 4 * out_dim, dtype=np.uint8)
+    lib.wm_synth_i2s(seed, tag, _ptr(out, C.c_uint8), out.size)
+    return out
+
+
+def synth_normal(seed: int, tag: int, n: int, sigma: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib.wm_synth_normal(seed, tag, _ptr(out, C.c_float), n, sigma)
+    return out
+
+
+def synth_uniform(seed: int, tag: int, n: int, lo: float, hi: float) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib.wm_synth_uniform(seed, tag, _ptr(out, C.c_float), n, lo, hi)
+    return out
+
+
+def synth_q6k(seed: int, tag: int, n_rows: int, row_len: int, d_sigma: float = 1e-3) -> np.ndarray:
+    n_blocks = n_rows * (row_len // 256)
+    out = np.empty(n_blocks * 210, dtype=np.uint8)
+    lib.wm_synth_q6k(seed, tag, _ptr(out, C.c_uint8), n_blocks, d_sigma)
+    return out
+
+
+def scale_block(scale: float) -> np.ndarray:
+    """The 32-byte I2_S trailing block: LE f32 scale + 28 zero bytes."""
+    b = np.zeros(32, dtype=np.uint8)
+    b[:4] = np.frombuffer(np.float32(scale).tobytes(), dtype=np.uint8)
+    return b
+
+
+def argmax(logits: np.ndarray):
+    """src/model/lm_head.rs:161-174 (None for an empty slice)."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    out = C.c_uint32()
+    st = lib.wm_argmax(_ptr(logits, C.c_float), logits.size, C.byref(out))
+    return None if st else int(out.value)
+
+
+# ---------------------------------------------------------------------------
+# context / tensors
+# ---------------------------------------------------------------------------
+
+class Context:
+    def __init__(self, device: int = 0):
+        h = _vp()
+        st = lib.wm_ctx_create(device, C.byref(h))
+        if st:
+            raise WillametteError(st, f"wm_ctx_create(device={device}) failed")
+        self.h = h
+
+    def check(self, st: int):
+        if st:
+            raise WillametteError(st, lib.wm_last_error(self.h).decode())
+
+    def close(self):
+        if self.h:
+            lib.wm_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synchronize(self):
+        self.check(lib.wm_ctx_synchronize(self.h))
+
+    @property
+    def stream(self) -> int:
+        return lib.wm_ctx_stream(self.h) or 0
+
+    # device buffers
+    def alloc(self, nbytes: int) -> "DeviceBuffer":
+        return DeviceBuffer(self, nbytes)
+
+    def to_device(self, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = DeviceBuffer(self, a.nbytes)
+        self.check(lib.wm_memcpy_h2d(self.h, b.ptr, a.ctypes.data, a.nbytes))
+        return b
+
+    # tensors
+    def upload_i2s(self, packed: np.ndarray, scale, in_dim: int, out_dim: int) -> "Tensor":
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        sb = scale if isinstance(scale, np.ndarray) else scale_block(float(scale))
+        sb = np.ascontiguousarray(sb, dtype=np.uint8)
+        h = _vp()
+        self.check(lib.wm_tensor_upload_i2s(self.h, _ptr(packed, C.c_uint8), packed.size,
+                                            _ptr(sb, C.c_uint8), sb.size, in_dim, out_dim,
+                                            C.byref(h)))
+        return Tensor(self, h)
+
+    def upload_q6k(self, blocks: np.ndarray, row_len: int, n_rows: int) -> "Tensor":
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        h = _vp()
+        self.check(lib.wm_tensor_upload_q6k(self.h, _ptr(blocks, C.c_uint8), blocks.size, row_len,
+                                            n_rows, C.byref(h)))
+        return Tensor(self, h)
+
+
+class DeviceBuffer:
+    def __init__(self, ctx: Context, nbytes: int):
+        self.ctx = ctx
+        p = _vp()
+        ctx.check(lib.wm_dev_alloc(ctx.h, nbytes, C.byref(p)))
+        self.ptr = p.value
+        self.nbytes = nbytes
+
+    def to_host(self, dtype, count=None) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        count = self.nbytes // dtype.itemsize if count is None else count
+        out = np.empty(count, dtype=dtype)
+        self.ctx.check(lib.wm_memcpy_d2h(self.ctx.h, out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr and self.ctx.h:
+            lib.wm_dev_free(self.ctx.h, self.ptr)
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Tensor:
+    def __init__(self, ctx: Context, h):
+        self.ctx, self.h = ctx, h
+        shape = (C.c_uint64 * 2)()
+        t = C.c_int()
+        s = C.c_float()
+        ctx.check(lib.wm_tensor_info(h, shape, C.byref(t), C.byref(s)))
+        self.shape = (int(shape[0]), int(shape[1]))
+        self.type = t.value
+        self.scale = s.value
+
+    def close(self):
+        if self.h:
+            lib.wm_tensor_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------------------
+# kernels (host-slice API, mirrors the Rust signatures)
+# ---------------------------------------------------------------------------
+
+def bitlinear_i2s_matvec_f32(ctx: Context, w: Tensor, x: np.ndarray, debug: bool = False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(w.shape[1], dtype=np.float32)
+    if not debug:
+        ctx.check(lib.wm_bitlinear_i2s_matvec_f32(ctx.h, w.h, _ptr(x, C.c_float), x.size,
+                                                  _ptr(y, C.c_float), y.size))
+        return y
+    act = np.empty(w.shape[0], dtype=np.int8)
+    acc = np.empty(w.shape[1], dtype=np.int32)
+    sc = C.c_float()
+    ctx.check(lib.wm_bitlinear_i2s_matvec_f32_debug(ctx.h, w.h, _ptr(x, C.c_float), x.size,
+                                                    _ptr(y, C.c_float), y.size, _ptr(act, C.c_int8),
+                                                    C.byref(sc), _ptr(acc, C.c_int32)))
+    return y, act, float(np.float32(sc.value)), acc
+
+
+def q6k_dequantize_row(ctx: Context, t: Tensor, row: int) -> np.ndarray:
+    out = np.empty(t.shape[0], dtype=np.float32)
+    ctx.check(lib.wm_q6k_dequantize_row(ctx.h, t.h, row, _ptr(out, C.c_float), out.size))
+    return out
+
+
+def compute_logits(ctx: Context, t: Tensor, hidden: np.ndarray) -> np.ndarray:
+    hidden = np.ascontiguousarray(hidden, dtype=np.float32)
+    out = np.empty(t.shape[1], dtype=np.float32)
+    ctx.check(lib.wm_compute_logits(ctx.h, t.h, _ptr(hidden, C.c_float), hidden.size,
+                                    _ptr(out, C.c_float), out.size))
+    return out
+
+
+def logits_argmax(ctx: Context, t: Tensor, hidden: np.ndarray, want_logits: bool = True):
+    hidden = np.ascontiguousarray(hidden, dtype=np.float32)
+    out = np.empty(t.shape[1], dtype=np.float32) if want_logits else None
+    a = C.c_uint32()
+    ctx.check(lib.wm_logits_argmax(ctx.h, t.h, _ptr(hidden, C.c_float), hidden.size,
+                                   _ptr(out, C.c_float) if out is not None else None, C.byref(a)))
+    return out, int(a.value)

@@ -1,0 +1,177 @@
+"""GPU parity: the full decode step (embedding, 30-layer forward with KV
+cache, output norm, lm-head, argmax) vs the oracle.
+
+Bar: hidden states after every layer, final hidden, logits and KV cache
+codes bit-identical to the oracle on the same seeded inputs, so greedy ids
+are identical; the BitNet-2B-shaped 64-step greedy decode is checked against
+committed oracle fixtures (tests/golden/bitnet2b_decode64.json).
+"""
+import hashlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import bitnet_synth as bs
+import willamette_hip as wh
+from oracle.oracle_model import OracleModel
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+SMALL = bs.BitNetConfig(n_layers=2, n_embd=256, n_ff=512, n_heads=2, n_kv_heads=1, head_dim=128,
+                        vocab=1000, context_length=64)
+GQA4 = bs.BitNetConfig(n_layers=3, n_embd=256, n_ff=384, n_heads=4, n_kv_heads=1, head_dim=64,
+                       vocab=777, context_length=96)
+
+
+def bits_equal(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.fixture(scope="module", params=[SMALL, GQA4], ids=["small", "gqa4"])
+def pair(request, ctx):
+    cfg = request.param
+    hm = bs.make_host_model(cfg, seed=1234 + cfg.n_layers)
+    dev = bs.load_device_model(ctx, hm)
+    orm = OracleModel(hm)
+    yield cfg, hm, dev, orm
+    dev.close()
+    orm.close()
+
+
+def test_forward_positions_bit_exact(pair):
+    cfg, hm, dev, orm = pair
+    dkv, okv = dev.kv_cache(cfg.context_length), orm.kv(cfg.context_length)
+    tokens = [3, 17, 999 % cfg.vocab, 0, 42, 42, 7, 500 % cfg.vocab, 1, 2, 3, 4]
+    for pos, tok in enumerate(tokens):
+        h, tr = dkv.forward(tok, pos, trace=True)
+        rh, rtr = okv.forward(tok, pos, trace=True)
+        for l in range(cfg.n_layers):
+            assert bits_equal(tr[l], rtr[l]), f"pos {pos}: hidden after layer {l} differs"
+        assert bits_equal(h, rh), f"pos {pos}: final hidden differs"
+    assert dkv.position == okv.position == len(tokens)
+    for l in range(cfg.n_layers):
+        dk, dks, dv, dvs = dkv.read_raw(l, len(tokens))
+        ok, oks, ov, ovs = okv.read_raw(l, len(tokens))
+        assert np.array_equal(dk, ok) and np.array_equal(dv, ov)
+        assert bits_equal(dks, oks) and bits_equal(dvs, ovs)
+
+
+def test_prefill_then_greedy_bit_exact(pair):
+    cfg, hm, dev, orm = pair
+    n_pre = cfg.context_length // 2
+    k, v = bs.kv_prefill(cfg, seed=99, n_pos=n_pre)
+    dkv, okv = dev.kv_cache(cfg.context_length), orm.kv(cfg.context_length)
+    dkv.append_positions(k, v)
+    okv.append_positions(k, v)
+    for l in range(cfg.n_layers):
+        dk, dks, _, dvs = dkv.read_raw(l, n_pre)
+        ok, oks, _, ovs = okv.read_raw(l, n_pre)
+        assert np.array_equal(dk, ok) and bits_equal(dks, oks) and bits_equal(dvs, ovs)
+    # step by step: logits and next token
+    tok, pos = 5, n_pre
+    for step in range(6):
+        h, logits, nxt = dkv.decode_step(tok, pos)
+        rh = okv.forward(tok, pos)
+        rlogits, rnxt = okv.logits_argmax(rh)
+        assert bits_equal(h, rh) and bits_equal(logits, rlogits), f"step {step}"
+        assert nxt == rnxt
+        tok, pos = nxt, pos + 1
+    # greedy loop on both from here
+    ids = dkv.greedy([tok], max_new=cfg.context_length - pos - 2)
+    rids = okv.greedy([tok], max_new=cfg.context_length - pos - 2)
+    assert ids == rids and len(ids) > 0
+
+
+def test_greedy_eos_stops(pair):
+    cfg, hm, dev, orm = pair
+    dkv, okv = dev.kv_cache(cfg.context_length), orm.kv(cfg.context_length)
+    ids = dkv.greedy([1, 2, 3], max_new=8)
+    eos = ids[3]
+    dkv2 = dev.kv_cache(cfg.context_length)
+    ids2 = dkv2.greedy([1, 2, 3], max_new=8, eos=eos)
+    assert ids2 == ids[: ids.index(eos)]
+    assert ids == okv.greedy([1, 2, 3], max_new=8)
+
+
+def test_position_protocol_and_nonfinite_rollback(ctx):
+    cfg = SMALL
+    hm = bs.make_host_model(cfg, seed=5)
+    dev = bs.load_device_model(ctx, hm)
+    dkv = dev.kv_cache(cfg.context_length)
+    dkv.forward(1, 0)
+    with pytest.raises(wh.WillametteError) as e:
+        dkv.forward(1, 5)  # tokens must be processed in order
+    assert e.value.kind == "State"
+    with pytest.raises(wh.WillametteError) as e:
+        dkv.forward(cfg.vocab, 1)  # token out of vocab
+    assert e.value.kind == "Shape"
+    assert dkv.position == 1
+    # an infinite norm weight makes layer 0's output non-finite -> error + rollback
+    hm.layers[0].norms["ffn_norm"][:] = np.inf
+    bad = bs.load_device_model(ctx, hm)
+    bkv = bad.kv_cache(cfg.context_length)
+    with pytest.raises(wh.WillametteError) as e:
+        bkv.forward(1, 0)
+    assert e.value.kind == "NonFinite" and bkv.position == 0
+    orm = OracleModel(hm)
+    okv = orm.kv(cfg.context_length)
+    with pytest.raises(RuntimeError):
+        okv.forward(1, 0)
+    assert okv.position == 0
+
+
+def test_zero_weight_model_closed_form(ctx):
+    """tests/synthetic_model.rs analogue: all-zero ternary weights, unit norms,
+    an all-ones embedding -> every BitLinear outputs 0, the hidden stays the
+    embedding, output = 1/sqrt(1 + eps), all logits tie -> token 0."""
+    cfg = SMALL
+    hm = bs.make_host_model(cfg, seed=6)
+    for hl in hm.layers:
+        for r in bs.ROLES:
+            hl.packed[r][:] = 0x55
+        for n in bs.NORMS:
+            hl.norms[n][:] = 1.0
+    ones = np.concatenate([np.full(128, 0x11, np.uint8), np.full(64, 0xAA, np.uint8),
+                           np.full(16, 1, np.uint8), np.array([0x00, 0x3C], np.uint8)])
+    hm.token_embd = np.tile(ones, cfg.vocab * (cfg.n_embd // 256))
+    hm.output_norm[:] = 1.0
+    dev = bs.load_device_model(ctx, hm)
+    dkv = dev.kv_cache(cfg.context_length)
+    h, logits, nxt = dkv.decode_step(3, 0)
+    expect = np.float32(1.0) * (np.float32(1.0) / np.sqrt(np.float32(1.0) + np.float32(1e-5)))
+    assert np.all(h == expect)
+    assert np.all(logits == logits[0]) and nxt == 0
+
+
+def _sha(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a, np.float32).tobytes()).hexdigest()
+
+
+def test_bitnet2b_decode64_matches_oracle_fixture(ctx):
+    """Full BitNet-2B shape: 30 layers, 2560/6912, 20/5 heads, vocab 128256,
+    KV pre-filled to 1024 positions with N(0,1), start token 15339, 64
+    greedy steps.  Ids and every step's logits (sha256) must match the
+    oracle's run recorded in tests/golden/bitnet2b_decode64.json."""
+    gold = json.loads((GOLDEN / "bitnet2b_decode64.json").read_text())
+    cfg = bs.BITNET_2B
+    seed = bs.master_seed(4)
+    hm = bs.make_host_model(cfg, seed)
+    dev = bs.load_device_model(ctx, hm)
+    k, v = bs.kv_prefill(cfg, seed, gold["prefill"])
+    dkv = dev.kv_cache(cfg.context_length)
+    dkv.append_positions(k, v)
+    del k, v
+    tok, pos = gold["start_token"], gold["prefill"]
+    ids, shas = [], []
+    for step in range(gold["steps"]):
+        _, logits, nxt = dkv.decode_step(tok, pos)
+        shas.append(_sha(logits))
+        ids.append(nxt)
+        tok, pos = nxt, pos + 1
+    assert ids == gold["ids"]
+    assert shas == gold["logits_sha256"]
