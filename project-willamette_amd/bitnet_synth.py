@@ -124,12 +124,15 @@ def load_device_model(ctx: wh.Context, hm: HostModel) -> "DeviceModel":
 class DeviceModel:
     """wm_model built from a HostModel (ModelGraph::from_gguf role)."""
 
+    _close_rank = 1
+
     def __init__(self, ctx: wh.Context, hm: HostModel):
         self.ctx, self.cfg = ctx, hm.cfg
         cc = hm.cfg.c_config()
         h = wh._vp()
         ctx.check(wh.lib.wm_model_create(ctx.h, wh.C.byref(cc), wh.C.byref(h)))
         self.h = h
+        ctx.adopt(self)
         for l, hl in enumerate(hm.layers):
             ts = []
             for role in ROLES:
@@ -161,11 +164,14 @@ class DeviceModel:
 
 
 class DeviceKV:
+    _close_rank = 0
+
     def __init__(self, model: DeviceModel, max_seq: int):
         self.model, self.ctx = model, model.ctx
         h = wh._vp()
         self.ctx.check(wh.lib.wm_kv_cache_create(model.h, max_seq, wh.C.byref(h)))
         self.h = h
+        self.ctx.adopt(self)
 
     def close(self):
         if self.h:

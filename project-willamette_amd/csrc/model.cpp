@@ -65,6 +65,7 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct wm_model {
     wm_ctx *ctx = nullptr;
+    int device = 0;
     wm_model_config cfg{};
     uint32_t kv_dim = 0;
     std::vector<dev_layer> layers;
@@ -88,6 +89,7 @@ struct wm_model {
 
 struct wm_kv_cache {
     wm_model *m = nullptr;
+    int device = 0;
     uint32_t max_seq = 0, pos = 0;
     int8_t *k = nullptr, *v = nullptr;   // [layer][max_seq][kv_dim]
     float *ks = nullptr, *vs = nullptr;  // [layer][max_seq]
@@ -258,11 +260,13 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
                             c.n_rot);
     if (c.n_embd % QK_I2S || c.n_ff % QK_I2S || c.n_embd % Q6K_VALUES)
         return wm_set_error(ctx, WM_E_SHAPE, "model config: n_embd/n_ff must be multiples of 256/128");
-    if (c.n_ff > 16384 || c.n_embd > 16384 || c.context_length > 8192)
+    // attention keeps a context's softmax weights in LDS (16 KB at 4096)
+    if (c.n_ff > 16384 || c.n_embd > 16384 || c.context_length > 4096)
         return wm_set_error(ctx, WM_E_SHAPE, "model config: dimensions beyond the supported range");
     WM_HIP(ctx, hipSetDevice(ctx->device));
     wm_model *m = new wm_model();
     m->ctx = ctx;
+    m->device = ctx->device;
     m->cfg = c;
     m->kv_dim = c.n_kv_heads * c.head_dim;
     m->layers.resize(c.n_layers);
@@ -339,8 +343,7 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
 
 void wm_model_destroy(wm_model *m) {
     if (!m) return;
-    hipSetDevice(m->ctx->device);
-    hipStreamSynchronize(m->ctx->stream);
+    hipSetDevice(m->device);
     for (auto &l : m->layers) {
         free_lin(l.q); free_lin(l.k); free_lin(l.v); free_lin(l.o);
         free_lin(l.gate); free_lin(l.up); free_lin(l.down);
@@ -432,6 +435,7 @@ wm_status wm_kv_cache_create(wm_model *m, uint32_t max_seq_len, wm_kv_cache **ou
     WM_HIP(ctx, hipSetDevice(ctx->device));
     wm_kv_cache *kv = new wm_kv_cache();
     kv->m = m;
+    kv->device = ctx->device;
     kv->max_seq = max_seq_len;
     const size_t nq = (size_t)m->cfg.n_layers * max_seq_len * m->kv_dim;
     const size_t ns = (size_t)m->cfg.n_layers * max_seq_len;
@@ -449,8 +453,7 @@ wm_status wm_kv_cache_create(wm_model *m, uint32_t max_seq_len, wm_kv_cache **ou
 
 void wm_kv_cache_destroy(wm_kv_cache *kv) {
     if (!kv) return;
-    hipSetDevice(kv->m->ctx->device);
-    hipStreamSynchronize(kv->m->ctx->stream);
+    hipSetDevice(kv->device);
     if (kv->k) hipFree(kv->k);
     if (kv->v) hipFree(kv->v);
     if (kv->ks) hipFree(kv->ks);

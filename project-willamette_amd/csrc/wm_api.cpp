@@ -159,6 +159,7 @@ wm_status wm_tensor_upload_i2s(wm_ctx *ctx, const uint8_t *packed, size_t packed
     WM_HIP(ctx, hipSetDevice(ctx->device));
     wm_tensor *t = new wm_tensor();
     t->ctx = ctx;
+    t->device = ctx->device;
     t->type = WM_TYPE_I2S;
     t->in_dim = in_dim;
     t->out_dim = out_dim;
@@ -203,6 +204,7 @@ wm_status wm_tensor_upload_q6k(wm_ctx *ctx, const uint8_t *blocks, size_t len, u
     WM_HIP(ctx, hipSetDevice(ctx->device));
     wm_tensor *t = new wm_tensor();
     t->ctx = ctx;
+    t->device = ctx->device;
     t->type = WM_TYPE_Q6K;
     t->in_dim = row_len;
     t->out_dim = n_rows;
@@ -232,8 +234,7 @@ wm_status wm_tensor_upload_q6k(wm_ctx *ctx, const uint8_t *blocks, size_t len, u
 void wm_tensor_destroy(wm_tensor *t) {
     if (!t) return;
     if (t->d) {
-        hipSetDevice(t->ctx->device);
-        hipStreamSynchronize(t->ctx->stream);
+        hipSetDevice(t->device);
         hipFree(t->d);
     }
     delete t;

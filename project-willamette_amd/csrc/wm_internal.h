@@ -35,8 +35,12 @@ struct wm_ctx {
     size_t pinned_bytes = 0;
 };
 
+// Objects created on a context keep their own device id: destroying them
+// never touches the context (which may already be gone); hipFree
+// synchronises the device itself.
 struct wm_tensor {
     wm_ctx *ctx = nullptr;
+    int device = 0;
     int type = 0;
     uint64_t in_dim = 0;   // I2_S: columns; Q6_K: row_len
     uint64_t out_dim = 0;  // I2_S: rows;    Q6_K: n_rows

@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 from pathlib import Path
 
 import numpy as np
@@ -198,13 +199,21 @@ class Context:
         if st:
             raise WillametteError(st, f"wm_ctx_create(device={device}) failed")
         self.h = h
+        self._children = weakref.WeakSet()  # tensors, buffers, models, caches
+
+    def adopt(self, child):
+        self._children.add(child)
+        return child
 
     def check(self, st: int):
         if st:
             raise WillametteError(st, lib.wm_last_error(self.h).decode())
 
     def close(self):
+        """Destroys every live object made on this context, then the context."""
         if self.h:
+            for c in sorted(list(self._children), key=lambda c: getattr(c, "_close_rank", 0)):
+                c.close()
             lib.wm_ctx_destroy(self.h)
             self.h = None
 
@@ -251,12 +260,15 @@ class Context:
 
 
 class DeviceBuffer:
+    _close_rank = 2
+
     def __init__(self, ctx: Context, nbytes: int):
         self.ctx = ctx
         p = _vp()
         ctx.check(lib.wm_dev_alloc(ctx.h, nbytes, C.byref(p)))
         self.ptr = p.value
         self.nbytes = nbytes
+        ctx.adopt(self)
 
     def to_host(self, dtype, count=None) -> np.ndarray:
         dtype = np.dtype(dtype)
@@ -270,6 +282,8 @@ class DeviceBuffer:
             lib.wm_dev_free(self.ctx.h, self.ptr)
         self.ptr = None
 
+    close = free
+
     def __del__(self):
         try:
             self.free()
@@ -278,8 +292,11 @@ class DeviceBuffer:
 
 
 class Tensor:
+    _close_rank = 2
+
     def __init__(self, ctx: Context, h):
         self.ctx, self.h = ctx, h
+        ctx.adopt(self)
         shape = (C.c_uint64 * 2)()
         t = C.c_int()
         s = C.c_float()

@@ -111,8 +111,13 @@ def test_position_protocol_and_nonfinite_rollback(ctx):
         dkv.forward(cfg.vocab, 1)  # token out of vocab
     assert e.value.kind == "Shape"
     assert dkv.position == 1
-    # an infinite norm weight makes layer 0's output non-finite -> error + rollback
-    hm.layers[0].norms["ffn_norm"][:] = np.inf
+    # An infinite ffn_sub_norm weight: the down projection's int8 quantiser
+    # sees absmax = inf, every code becomes 0 and its scale inf, so the
+    # projection yields inf * 0 = NaN and layer 0's hidden is non-finite
+    # -> error + rollback (src/model/cached_forward.rs:256-259, :511-521).
+    # (An infinite ffn_norm would not do: the NaN gate is zeroed by ReLU and
+    # the sub-norm's quantiser drops NaN, so the hidden stays finite.)
+    hm.layers[0].norms["ffn_sub_norm"][:] = np.inf
     bad = bs.load_device_model(ctx, hm)
     bkv = bad.kv_cache(cfg.context_length)
     with pytest.raises(wh.WillametteError) as e:
