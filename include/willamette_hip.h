@@ -210,6 +210,14 @@ wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *promp
                              uint32_t n_prompt, uint32_t max_new, int64_t eos, uint32_t *out_ids,
                              uint32_t *n_out);
 
+/* ---- test hook ------------------------------------------------------- */
+
+/* No counterpart in the reference: runs the device's exact evaluation of
+ * the left-to-right f32 sum s = ((0 + a[0]) + a[1]) + ... of n non-negative
+ * terms (host array), the routine behind every RMSNorm sum of squares and
+ * softmax denominator, so tests can check it on adversarial inputs. */
+wm_status wm_debug_seq_sum(wm_ctx *ctx, const float *values, size_t n, float *sum);
+
 /* ---- synthetic BitNet-shaped inputs (src/synth.rs) ------------------- */
 
 /* Counter-based SplitMix64 streams, identical on every host: value i of

@@ -55,12 +55,23 @@ float or_f16_to_f32(uint16_t bits) {
 }
 
 /* src/model/bitlinear.rs:43-50: 00 -> -1, 01 -> 0, 10 -> +1, 11 -> 0 */
-int8_t or_ternary_from_code(uint8_t code) {
+static inline int8_t ternary(uint8_t code) {
     switch (code & 3u) {
     case 0: return -1;
     case 2: return 1;
     default: return 0;
     }
+}
+
+int8_t or_ternary_from_code(uint8_t code) { return ternary(code); }
+
+/* unpack_block (src/model/bitlinear_sse2.rs:183-193) through a 256-entry
+ * table of the four ternary values a byte holds. */
+static int8_t g_unpack_lut[256][4];
+static pthread_once_t g_lut_once = PTHREAD_ONCE_INIT;
+static void init_lut(void) {
+    for (int b = 0; b < 256; b++)
+        for (int q = 0; q < 4; q++) g_unpack_lut[b][q] = ternary((uint8_t)(b >> (6 - 2 * q)));
 }
 
 float or_expf(float x) { return expf(x); }
@@ -124,10 +135,10 @@ int or_i2s_unpack_row(const uint8_t *packed, size_t in_dim, size_t out_dim, size
         for (size_t gp = 0; gp < I2S_BLOCK_BYTES; gp++) {
             uint8_t b = r[bk * I2S_BLOCK_BYTES + gp];
             int8_t *o = out + bk * QK_I2S + gp;
-            o[0] = or_ternary_from_code(b >> 6);
-            o[32] = or_ternary_from_code(b >> 4);
-            o[64] = or_ternary_from_code(b >> 2);
-            o[96] = or_ternary_from_code(b);
+            o[0] = ternary(b >> 6);
+            o[32] = ternary(b >> 4);
+            o[64] = ternary(b >> 2);
+            o[96] = ternary(b);
         }
     }
     return 0;
@@ -170,16 +181,17 @@ int or_bitlinear_i2s_matvec_f32_sse2_i8(const uint8_t *packed, size_t packed_len
     float combined = w_scale * input_scale;
     size_t bpr = in_dim / 4;
     int8_t unpacked[QK_I2S];
+    pthread_once(&g_lut_once, init_lut);
     for (size_t j = 0; j < out_dim; j++) {
         int32_t dot = 0;
         for (size_t bk = 0; bk < in_dim / QK_I2S; bk++) {
             const uint8_t *blk = packed + j * bpr + bk * I2S_BLOCK_BYTES;
             for (int gp = 0; gp < I2S_BLOCK_BYTES; gp++) {
-                uint8_t b = blk[gp];
-                unpacked[gp] = or_ternary_from_code(b >> 6);
-                unpacked[gp + 32] = or_ternary_from_code(b >> 4);
-                unpacked[gp + 64] = or_ternary_from_code(b >> 2);
-                unpacked[gp + 96] = or_ternary_from_code(b);
+                const int8_t *t = g_unpack_lut[blk[gp]];
+                unpacked[gp] = t[0];
+                unpacked[gp + 32] = t[1];
+                unpacked[gp + 64] = t[2];
+                unpacked[gp + 96] = t[3];
             }
             dot += dot_block_sse2(unpacked, act + bk * QK_I2S);
         }

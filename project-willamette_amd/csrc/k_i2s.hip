@@ -162,7 +162,11 @@ __global__ void k_i2s_finalize(const int32_t *__restrict__ partial, uint32_t spl
     uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= out_dim) return;
     int dot = -meta->asum;
-    for (uint32_t s = 0; s < split; s++) dot += partial[(uint64_t)s * rows_total + row0 + j];
+#pragma unroll
+    for (uint32_t s = 0; s < 16; s++) {  // split <= 16 (wm_i2s_pick_split); loads unconditional
+        const int v = partial[(uint64_t)min(s, split - 1) * rows_total + row0 + j];
+        dot += s < split ? v : 0;
+    }
     const float combined = w_scale * meta->scale;
     if (y) y[j] = combined * (float)dot;
     if (dot_out) dot_out[j] = dot;
@@ -212,6 +216,7 @@ uint32_t wm_i2s_pick_split(uint32_t n_groups, uint32_t n_chunks) {
     uint32_t split = (512 + n_groups - 1) / n_groups;
     uint32_t max_split = n_chunks / 4 ? n_chunks / 4 : 1;
     if (split > max_split) split = max_split;
+    if (split > 16) split = 16;  // consumers sum at most 16 partials per row
     if (split < 1) split = 1;
     return split;
 }

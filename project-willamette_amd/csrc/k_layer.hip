@@ -16,51 +16,11 @@
 // products, exp, the quantisation) runs across all lanes; only the adds of
 // the chain are serial.  Maxima and integer sums are order-free.
 #include "wm_internal.h"
+#include "wm_seqsum.h"
 
 namespace {
 
 constexpr int kNormThreads = 1024;
-
-// Sequential f32 sum of x[i]*x[i], i = 0..n-1, one accumulator, as
-// `for &xi in x { sum_sq += xi * xi }`.  Executed by every lane of the
-// calling wave on the same LDS data (broadcast reads), so the value is
-// uniform; the multiplies do not depend on the accumulator and issue ahead.
-__device__ __forceinline__ float seq_sum_squares(const float *__restrict__ xs, uint32_t n) {
-    float s = 0.0f;
-    uint32_t i = 0;
-    for (; i + 8 <= n; i += 8) {
-        float4 a = *reinterpret_cast<const float4 *>(xs + i);
-        float4 b = *reinterpret_cast<const float4 *>(xs + i + 4);
-        float p0 = a.x * a.x, p1 = a.y * a.y, p2 = a.z * a.z, p3 = a.w * a.w;
-        float p4 = b.x * b.x, p5 = b.y * b.y, p6 = b.z * b.z, p7 = b.w * b.w;
-        s = s + p0; s = s + p1; s = s + p2; s = s + p3;
-        s = s + p4; s = s + p5; s = s + p6; s = s + p7;
-    }
-    for (; i < n; i++) s = s + xs[i] * xs[i];
-    return s;
-}
-
-__device__ __forceinline__ float block_max_nonan(float v, float *red) {
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    v = wm_wave_max_nonan(v);
-    __syncthreads();
-    if (lane == 0) red[wid] = v;
-    __syncthreads();
-    float m = red[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); w++) m = wm_max_nonan(m, red[w]);
-    return m;
-}
-
-__device__ __forceinline__ int block_sum_i32(int v, int *red) {
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    v = wm_wave_sum_i32(v);
-    __syncthreads();
-    if (lane == 0) red[wid] = v;
-    __syncthreads();
-    int t = 0;
-    for (int w = 0; w < (int)(blockDim.x >> 6); w++) t += red[w];
-    return t;
-}
 
 // Residual source for k_rmsnorm_quant: y_j = (w_scale*act_scale)*(Σ_s partial[s][row0+j] - asum)
 struct residual_src {
@@ -74,65 +34,101 @@ struct residual_src {
 // then y = (x * rsqrt) * w with rsqrt = 1/sqrt(Σx²/n + eps), then either
 // y -> y_out (f32) or y -> per-vector absmax int8 (permuted layout) + meta.
 // err_flag: set to layer_tag if x (after the residual) is not all finite.
+constexpr int kMaxSplit = 16;  // K splits a residual source may carry
+
+template <int PER>  // values per thread: n <= PER * 1024
 __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
     float *__restrict__ x, residual_src res, const float *__restrict__ w, uint32_t n, float eps,
     uint8_t *__restrict__ act, wm_act_meta *__restrict__ meta_out, float *__restrict__ y_out,
     uint32_t *__restrict__ err_flag, uint32_t layer_tag) {
-    extern __shared__ float xs[];
+    extern __shared__ float sq[];  // x[j]*x[j]
     __shared__ float red_f[16];
     __shared__ int red_i[16];
-    __shared__ float s_rsqrt;
+    __shared__ float s_sum;
     const uint32_t tid = threadIdx.x;
+    float xv[PER], wv[PER];
     int nonfinite = 0;
-    if (res.partial) {
+    const bool has_res = res.partial != nullptr;
+    // Every load below is unconditional (indices clamped to n - 1) so that
+    // they are all in flight together; out-of-range values are masked after.
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const uint32_t j = min(tid + (uint32_t)i * kNormThreads, n - 1);
+        xv[i] = x[j];
+        wv[i] = w[j];
+    }
+    if (has_res) {
+        // hidden += wo_out / down (cached_forward.rs:405-408, :496-500)
         const float combined = res.w_scale * res.meta->scale;
         const int asum = res.meta->asum;
-        for (uint32_t j = tid; j < n; j += blockDim.x) {
-            int dot = -asum;
-            for (uint32_t s = 0; s < res.split; s++)
-                dot += res.partial[(uint64_t)s * res.rows_total + res.row0 + j];
-            float v = x[j] + combined * (float)dot;
-            x[j] = v;
-            xs[j] = v;
-            nonfinite |= !isfinite(v);
+        int dot[PER];
+#pragma unroll
+        for (int i = 0; i < PER; i++) dot[i] = -asum;
+#pragma unroll
+        for (int s = 0; s < kMaxSplit; s++) {
+            const uint32_t sc = min((uint32_t)s, res.split - 1);
+#pragma unroll
+            for (int i = 0; i < PER; i++) {
+                const uint32_t j = min(tid + (uint32_t)i * kNormThreads, n - 1);
+                const int v = res.partial[(uint64_t)sc * res.rows_total + res.row0 + j];
+                dot[i] += (uint32_t)s < res.split ? v : 0;
+            }
         }
-    } else {
-        for (uint32_t j = tid; j < n; j += blockDim.x) xs[j] = x[j];
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const uint32_t j = tid + (uint32_t)i * kNormThreads;
+            const float v = xv[i] + combined * (float)dot[i];
+            xv[i] = v;
+            if (j < n) {
+                x[j] = v;
+                nonfinite |= !isfinite(v);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const uint32_t j = tid + (uint32_t)i * kNormThreads;
+        if (j < n) sq[j] = xv[i] * xv[i];
+        else xv[i] = 0.0f;
     }
     if (err_flag) {
-        int any = block_sum_i32(nonfinite, red_i);
+        int any = wm_block_sum_i32(nonfinite, red_i);
         if (any && tid == 0 && *err_flag == 0) *err_flag = layer_tag;
     }
     __syncthreads();
+    // sum_sq over x in order (primitives.rs:243-246), by one wave
     if (tid < 64) {
-        float sum_sq = seq_sum_squares(xs, n);
-        if (tid == 0) {
-            float mean = sum_sq / (float)n;
-            s_rsqrt = 1.0f / sqrtf(mean + eps);
-        }
+        const float s = wm::seq_sum_nonneg(sq, n);
+        if (tid == 0) s_sum = s;
     }
     __syncthreads();
-    const float rs = s_rsqrt;
-    if (y_out) {
-        for (uint32_t j = tid; j < n; j += blockDim.x) y_out[j] = xs[j] * rs * w[j];
-        return;
-    }
-    // per-vector absmax int8 (src/model/bitlinear_sse2.rs:285-304)
+    const float mean = s_sum / (float)n;
+    const float rs = 1.0f / sqrtf(mean + eps);
     float m = 0.0f;
-    for (uint32_t j = tid; j < n; j += blockDim.x) m = wm_max_nonan(m, fabsf(xs[j] * rs * w[j]));
-    const float max_abs = block_max_nonan(m, red_f);
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const uint32_t j = tid + (uint32_t)i * kNormThreads;
+        xv[i] = xv[i] * rs * wv[i];  // out[i] = x[i] * rsqrt * weight[i]
+        if (j < n) {
+            if (y_out) y_out[j] = xv[i];
+            m = wm_max_nonan(m, fabsf(xv[i]));
+        }
+    }
+    if (y_out) return;
+    // per-vector absmax int8 (src/model/bitlinear_sse2.rs:285-304)
+    const float max_abs = wm_block_max_nonan(m, red_f);
     int sum = 0;
-    if (max_abs == 0.0f) {
-        for (uint32_t j = tid; j < n; j += blockDim.x) act[wm_act_perm(j)] = 0;
-    } else {
-        const float inv = 127.0f / max_abs;
-        for (uint32_t j = tid; j < n; j += blockDim.x) {
-            int q = wm_round_clamp_i8((xs[j] * rs * w[j]) * inv);
+    const float inv = 127.0f / max_abs;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const uint32_t j = tid + (uint32_t)i * kNormThreads;
+        if (j < n) {
+            const int q = max_abs == 0.0f ? 0 : wm_round_clamp_i8(xv[i] * inv);
             act[wm_act_perm(j)] = (uint8_t)(int8_t)q;
             sum += q;
         }
     }
-    sum = block_sum_i32(sum, red_i);
+    sum = wm_block_sum_i32(sum, red_i);
     if (tid == 0) {
         meta_out->scale = max_abs == 0.0f ? 1.0f : max_abs / 127.0f;
         meta_out->asum = sum;
@@ -145,7 +141,7 @@ __device__ void kv_quantise_store(const float *__restrict__ v, uint32_t n, int8_
                                   float *__restrict__ scale_out, float *red) {
     float m = 0.0f;
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) m = wm_max_nonan(m, fabsf(v[i]));
-    const float absmax = block_max_nonan(m, red);
+    const float absmax = wm_block_max_nonan(m, red);
     if (absmax == 0.0f || !isfinite(absmax)) {
         for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) q[i] = 0;
         if (threadIdx.x == 0) *scale_out = 0.0f;
@@ -180,15 +176,34 @@ __global__ __launch_bounds__(1024) void k_qkv_rope_kv(qkv_args a) {
     const float in_scale = a.meta->scale;
     const int asum = a.meta->asum;
     const uint32_t total = a.n_q + 2 * a.n_kv;
-    for (uint32_t i = threadIdx.x; i < total; i += blockDim.x) {
-        uint32_t row;
-        float ws;
-        if (i < a.n_q) { row = a.q_row0 + i; ws = a.q_scale; }
-        else if (i < a.n_q + a.n_kv) { row = a.k_row0 + (i - a.n_q); ws = a.k_scale; }
-        else { row = a.v_row0 + (i - a.n_q - a.n_kv); ws = a.v_scale; }
-        int dot = -asum;
-        for (uint32_t s = 0; s < a.split; s++) dot += a.partial[(uint64_t)s * a.rows_total + row];
-        sm[i] = (ws * in_scale) * (float)dot;
+    constexpr int PER = 4;
+    for (uint32_t base = 0; base < total; base += PER * 1024) {
+        uint32_t row[PER];
+        float ws[PER];
+        int dot[PER];
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const uint32_t i = min(base + threadIdx.x + (uint32_t)k * 1024, total - 1);
+            if (i < a.n_q) { row[k] = a.q_row0 + i; ws[k] = a.q_scale; }
+            else if (i < a.n_q + a.n_kv) { row[k] = a.k_row0 + (i - a.n_q); ws[k] = a.k_scale; }
+            else { row[k] = a.v_row0 + (i - a.n_q - a.n_kv); ws[k] = a.v_scale; }
+            dot[k] = -asum;
+        }
+        // all partial loads unconditional, so they are in flight together
+#pragma unroll
+        for (int s = 0; s < kMaxSplit; s++) {
+            const uint32_t sc = min((uint32_t)s, a.split - 1);
+#pragma unroll
+            for (int k = 0; k < PER; k++) {
+                const int v = a.partial[(uint64_t)sc * a.rows_total + row[k]];
+                dot[k] += (uint32_t)s < a.split ? v : 0;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const uint32_t i = base + threadIdx.x + (uint32_t)k * 1024;
+            if (i < total) sm[i] = (ws[k] * in_scale) * (float)dot[k];
+        }
     }
     __syncthreads();
     // RoPE pairs (j, j + n_rot/2) in every head of Q and K
@@ -212,109 +227,6 @@ __global__ __launch_bounds__(1024) void k_qkv_rope_kv(qkv_args a) {
     kv_quantise_store(vs, a.n_kv, a.v_cache, a.v_scale_out, red);
 }
 
-struct attn_args {
-    const float *q;          // [n_heads][head_dim]
-    const int8_t *k_cache;   // this layer: [max_seq][kv_dim]
-    const float *k_scales;   // [max_seq]
-    const int8_t *v_cache;
-    const float *v_scales;
-    float *scores;           // [n_heads][score_stride]
-    float *out;              // [n_heads][head_dim]
-    uint32_t n_past, kv_dim, head_dim, group, score_stride;
-    float scale;
-};
-
-// scores[h][p] = (Σ_i q_h[i] * k_p[i]) * scale, the sum sequential over i
-// (cached_forward.rs:425-431); k_p[i] = (q8 as f32) * k_scale[p]
-// (kv_cache.rs:213-215).  One lane per position.
-__global__ __launch_bounds__(64) void k_attn_scores(attn_args a) {
-    const uint32_t h = blockIdx.x, p = blockIdx.y * 64 + threadIdx.x;
-    if (p >= a.n_past) return;
-    const uint32_t kvh = h / a.group;
-    const float *qh = a.q + (uint64_t)h * a.head_dim;
-    const int8_t *kp = a.k_cache + (uint64_t)p * a.kv_dim + kvh * a.head_dim;
-    const float ksc = a.k_scales[p];
-    float s = 0.0f;
-    for (uint32_t i = 0; i < a.head_dim; i += 16) {
-        int4 raw = *reinterpret_cast<const int4 *>(kp + i);
-        const int8_t *b = reinterpret_cast<const int8_t *>(&raw);
-#pragma unroll
-        for (int t = 0; t < 16; t++) {
-            float kd = (float)b[t] * ksc;
-            s = s + qh[i + t] * kd;
-        }
-    }
-    a.scores[(uint64_t)h * a.score_stride + p] = s * a.scale;
-}
-
-constexpr int kAttnThreads = 256;
-constexpr int kAttnTile = 128;  // positions per product tile
-constexpr int kAttnDims = 64;   // head dims per workgroup
-
-// softmax over scores[h][0..n_past) (attention.rs:45-73) then
-// out[h][d] = Σ_p w_p * v_p[d], sequential over p (cached_forward.rs:440-447),
-// for the 64 dimensions d0..d0+63 of head h.  Grid (n_heads, head_dim/64).
-__global__ __launch_bounds__(kAttnThreads) void k_attn_softmax_v(attn_args a) {
-    extern __shared__ float sm[];
-    float *wts = sm;                         // [n_past]
-    float *prod = sm + ((a.n_past + 3) & ~3u);  // [kAttnTile][kAttnDims]
-    __shared__ float red[16];
-    __shared__ float s_inv;
-    __shared__ int s_mode;
-    const uint32_t h = blockIdx.x, d0 = blockIdx.y * kAttnDims, tid = threadIdx.x;
-    const uint32_t n = a.n_past;
-    const float *sc = a.scores + (uint64_t)h * a.score_stride;
-    float m = -INFINITY;
-    for (uint32_t p = tid; p < n; p += blockDim.x) {
-        float v = sc[p];
-        wts[p] = v;
-        m = wm_max_nonan(m, v);
-    }
-    const float mx = block_max_nonan(m, red);
-    float *out = a.out + (uint64_t)h * a.head_dim + d0;
-    if (!isfinite(mx)) {  // every weight becomes 0 -> output stays 0
-        for (uint32_t d = tid; d < kAttnDims; d += blockDim.x) out[d] = 0.0f;
-        return;
-    }
-    for (uint32_t p = tid; p < n; p += blockDim.x) wts[p] = wm_expf(wts[p] - mx);
-    __syncthreads();
-    if (tid < 64) {
-        float sum = 0.0f;
-        uint32_t p = 0;
-        for (; p + 4 <= n; p += 4) {
-            float4 e = *reinterpret_cast<const float4 *>(wts + p);
-            sum = sum + e.x; sum = sum + e.y; sum = sum + e.z; sum = sum + e.w;
-        }
-        for (; p < n; p++) sum = sum + wts[p];
-        if (tid == 0) {
-            s_mode = sum > 0.0f;
-            s_inv = 1.0f / sum;
-        }
-    }
-    __syncthreads();
-    if (s_mode) {
-        const float inv = s_inv;
-        for (uint32_t p = tid; p < n; p += blockDim.x) wts[p] = wts[p] * inv;
-    }
-    __syncthreads();
-    const uint32_t kvh = h / a.group;
-    const int8_t *vbase = a.v_cache + kvh * a.head_dim + d0;
-    float acc = 0.0f;  // lane d of wave 0
-    for (uint32_t t0 = 0; t0 < n; t0 += kAttnTile) {
-        const uint32_t tn = n - t0 < (uint32_t)kAttnTile ? n - t0 : (uint32_t)kAttnTile;
-        for (uint32_t idx = tid; idx < tn * kAttnDims; idx += blockDim.x) {
-            uint32_t pl = idx / kAttnDims, d = idx % kAttnDims, p = t0 + pl;
-            float vd = (float)vbase[(uint64_t)p * a.kv_dim + d] * a.v_scales[p];
-            prod[pl * kAttnDims + d] = wts[p] * vd;
-        }
-        __syncthreads();
-        if (tid < kAttnDims)
-            for (uint32_t pl = 0; pl < tn; pl++) acc = acc + prod[pl * kAttnDims + tid];
-        __syncthreads();
-    }
-    if (tid < kAttnDims) out[tid] = acc;
-}
-
 // relu(g)^2 * u over the gate/up BitLinear outputs (ffn.rs:37-65).
 __global__ void k_gateup_relu2(const int32_t *__restrict__ partial, uint32_t split,
                                uint32_t rows_total, uint32_t gate_row0, uint32_t up_row0,
@@ -324,9 +236,13 @@ __global__ void k_gateup_relu2(const int32_t *__restrict__ partial, uint32_t spl
     if (j >= n_ff) return;
     const int asum = meta->asum;
     int dg = -asum, du = -asum;
-    for (uint32_t s = 0; s < split; s++) {
-        dg += partial[(uint64_t)s * rows_total + gate_row0 + j];
-        du += partial[(uint64_t)s * rows_total + up_row0 + j];
+#pragma unroll
+    for (int s = 0; s < kMaxSplit; s++) {
+        const uint32_t sc = min((uint32_t)s, split - 1);
+        const int g = partial[(uint64_t)sc * rows_total + gate_row0 + j];
+        const int u = partial[(uint64_t)sc * rows_total + up_row0 + j];
+        dg += (uint32_t)s < split ? g : 0;
+        du += (uint32_t)s < split ? u : 0;
     }
     const float g = (gate_scale * meta->scale) * (float)dg;
     const float u = (up_scale * meta->scale) * (float)du;
@@ -351,11 +267,21 @@ __global__ __launch_bounds__(256) void k_kv_append(const float *__restrict__ k,
     kv_quantise_store(v + src, kv_dim, v_cache + dst * kv_dim, v_scales + dst, red);
 }
 
+__global__ __launch_bounds__(64) void k_debug_seq_sum(const float *__restrict__ a, uint32_t n,
+                                                      float *__restrict__ out) {
+    const float s = wm::seq_sum_nonneg(a, n);
+    if (threadIdx.x == 0) *out = s;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
+
+void wm_launch_debug_seq_sum(const float *a, uint32_t n, float *out, hipStream_t s) {
+    hipLaunchKernelGGL(k_debug_seq_sum, dim3(1), dim3(64), 0, s, a, n, out);
+}
 
 void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, uint32_t rows_total,
                              uint32_t row0, float w_scale, const wm_act_meta *meta_in,
@@ -364,8 +290,20 @@ void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, u
                              uint32_t layer_tag, hipStream_t s) {
     residual_src res{partial, split, rows_total, row0, w_scale, meta_in};
     size_t lds = ((size_t)n + 8) * sizeof(float);
-    hipLaunchKernelGGL(k_rmsnorm_quant, dim3(1), dim3(kNormThreads), lds, s, x, res, w, n, eps, act,
-                       meta_out, y_out, err_flag, layer_tag);
+    const int per = (int)((n + kNormThreads - 1) / kNormThreads);
+#define WM_NORM_CASE(P)                                                                            \
+    case P:                                                                                        \
+        hipLaunchKernelGGL(k_rmsnorm_quant<P>, dim3(1), dim3(kNormThreads), lds, s, x, res, w, n,  \
+                           eps, act, meta_out, y_out, err_flag, layer_tag);                        \
+        break;
+    switch (per) {
+        WM_NORM_CASE(1) WM_NORM_CASE(2) WM_NORM_CASE(3) WM_NORM_CASE(4)
+        WM_NORM_CASE(5) WM_NORM_CASE(6) WM_NORM_CASE(7) WM_NORM_CASE(8)
+        WM_NORM_CASE(9) WM_NORM_CASE(10) WM_NORM_CASE(11) WM_NORM_CASE(12)
+        WM_NORM_CASE(13) WM_NORM_CASE(14) WM_NORM_CASE(15) WM_NORM_CASE(16)
+        default: break;
+    }
+#undef WM_NORM_CASE
 }
 
 void wm_launch_qkv_rope_kv(const int32_t *partial, uint32_t split, uint32_t rows_total,
@@ -380,18 +318,6 @@ void wm_launch_qkv_rope_kv(const int32_t *partial, uint32_t split, uint32_t rows
                k_scale_out, v_scale_out};
     size_t lds = (size_t)(n_q + 2 * n_kv) * sizeof(float);
     hipLaunchKernelGGL(k_qkv_rope_kv, dim3(1), dim3(1024), lds, s, a);
-}
-
-void wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_scales,
-                         const int8_t *v_cache, const float *v_scales, float *scores,
-                         uint32_t score_stride, float *out, uint32_t n_heads, uint32_t n_kv_heads,
-                         uint32_t head_dim, uint32_t n_past, float scale, hipStream_t s) {
-    attn_args a{q, k_cache, k_scales, v_cache, v_scales, scores, out, n_past,
-                n_kv_heads * head_dim, head_dim, n_heads / n_kv_heads, score_stride, scale};
-    hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, (n_past + 63) / 64), dim3(64), 0, s, a);
-    size_t lds = (((size_t)n_past + 3) & ~(size_t)3) * 4 + (size_t)kAttnTile * kAttnDims * 4;
-    hipLaunchKernelGGL(k_attn_softmax_v, dim3(n_heads, head_dim / kAttnDims), dim3(kAttnThreads), lds,
-                       s, a);
 }
 
 void wm_launch_gateup_relu2(const int32_t *partial, uint32_t split, uint32_t rows_total,

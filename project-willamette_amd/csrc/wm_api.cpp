@@ -487,6 +487,21 @@ wm_status wm_compute_logits(wm_ctx *ctx, const wm_tensor *t, const float *hidden
     return wm_logits_argmax(ctx, t, hidden, hidden_len, logits, nullptr);
 }
 
+wm_status wm_debug_seq_sum(wm_ctx *ctx, const float *values, size_t n, float *sum) {
+    if (!ctx || !sum || (n && !values) || n > (1u << 26)) return WM_E_ARG;
+    void *scratch;
+    wm_status st = wm_ctx_scratch(ctx, n * 4 + 256, &scratch);
+    if (st) return st;
+    float *d_in = (float *)scratch, *d_out = (float *)((uint8_t *)scratch + ((n * 4 + 255) & ~(size_t)255));
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    if (n) WM_HIP(ctx, hipMemcpyAsync(d_in, values, n * 4, hipMemcpyHostToDevice, ctx->stream));
+    wm_launch_debug_seq_sum(d_in, (uint32_t)n, d_out, ctx->stream);
+    WM_HIP(ctx, hipGetLastError());
+    WM_HIP(ctx, hipMemcpyAsync(sum, d_out, 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return WM_OK;
+}
+
 wm_status wm_argmax(const float *logits, size_t n, uint32_t *out) {
     if (!logits || !out || n == 0) return WM_E_ARG;
     size_t best = 0;

@@ -33,7 +33,9 @@ constexpr uint64_t kExp2Tab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-WM_HD inline float expf_glibc(float x) {
+// `tab` is kExp2Tab or a copy of it (device code passes an LDS copy so the
+// per-lane table lookup does not wait on global memory).
+WM_HD inline float expf_glibc(float x, const uint64_t *tab = kExp2Tab) {
     const double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
     const double kShift = 0x1.8p+52;
     const double kC0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);
@@ -59,7 +61,7 @@ WM_HD inline float expf_glibc(float x) {
     std::memcpy(&ki, &kd, 8);
     kd -= kShift;
     const double r = __builtin_fma(kInvLn2N, xd, -kd);
-    const uint64_t t = kExp2Tab[ki & 31u] + (ki << 47);
+    const uint64_t t = tab[ki & 31u] + (ki << 47);
     double s;
     std::memcpy(&s, &t, 8);
     const double z = __builtin_fma(kC0, r, kC1);

@@ -132,6 +132,29 @@ __device__ __forceinline__ float wm_wave_max_nonan(float v) {
     return v;
 }
 
+// Block-wide reductions (red: >= blockDim/64 slots of LDS).  Both are
+// order-free: a NaN-ignoring max and an integer sum.
+__device__ __forceinline__ float wm_block_max_nonan(float v, float *red) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    v = wm_wave_max_nonan(v);
+    __syncthreads();
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float m = red[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) m = wm_max_nonan(m, red[w]);
+    return m;
+}
+__device__ __forceinline__ int wm_block_sum_i32(int v, int *red) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    v = wm_wave_sum_i32(v);
+    __syncthreads();
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    int t = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); w++) t += red[w];
+    return t;
+}
+
 // Position of activation element i (0 <= i < in_dim) in the chunk-permuted
 // layout the I2_S matvec reads: chunk c = 16-byte weight chunk index along
 // the row, 64 bytes per chunk ordered [quarter k][gp].
@@ -191,3 +214,4 @@ void wm_launch_q6k_logits_argmax(const uint8_t *w, uint32_t n_blocks, uint32_t n
                                  uint32_t n_rowgroups, const float *hidden, float *logits,
                                  uint32_t *argmax_out, void *work, hipStream_t s);
 size_t wm_q6k_logits_work_bytes();
+void wm_launch_debug_seq_sum(const float *a, uint32_t n, float *out, hipStream_t s);

@@ -129,6 +129,7 @@ EXPORTS = {
     "wm_decode_step": (C.c_int, _vp, _vp, C.c_uint32, C.c_uint32, _f32p, _f32p, _u32p),
     "wm_greedy_generate": (C.c_int, _vp, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_int64, _u32p,
                            _u32p),
+    "wm_debug_seq_sum": (C.c_int, _vp, _f32p, C.c_size_t, _f32p),
     "wm_synth_stream_seed": (C.c_uint64, C.c_uint64, C.c_uint64),
     "wm_synth_i2s": (None, C.c_uint64, C.c_uint64, _u8p, C.c_size_t),
     "wm_synth_normal": (None, C.c_uint64, C.c_uint64, _f32p, C.c_size_t, C.c_double),
@@ -335,6 +336,14 @@ def bitlinear_i2s_matvec_f32(ctx: Context, w: Tensor, x: np.ndarray, debug: bool
                                                     _ptr(y, C.c_float), y.size, _ptr(act, C.c_int8),
                                                     C.byref(sc), _ptr(acc, C.c_int32)))
     return y, act, float(np.float32(sc.value)), acc
+
+
+def debug_seq_sum(ctx: Context, values: np.ndarray) -> np.float32:
+    """The device's exact left-to-right f32 sum (test hook)."""
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    out = C.c_float()
+    ctx.check(lib.wm_debug_seq_sum(ctx.h, _ptr(values, C.c_float), values.size, C.byref(out)))
+    return np.float32(out.value)
 
 
 def q6k_dequantize_row(ctx: Context, t: Tensor, row: int) -> np.ndarray:
