@@ -75,19 +75,22 @@ def decode_tokens(dkv, n: int, tok: int, pos: int):
 
 
 def lm_head_kernel(ctx, wh, hm, cfg, reps: int):
-    """Average duration of one Q6_K logits launch (no argmax kernel)."""
-    t = ctx.upload_q6k(hm.token_embd, cfg.n_embd, cfg.vocab)
+    """Average duration of one Q6_K logits launch (no argmax kernel),
+    alternating between two device copies of the 269 MB tensor so that the
+    256 MB Infinity Cache cannot serve a launch from the previous one."""
+    ts = [ctx.upload_q6k(hm.token_embd, cfg.n_embd, cfg.vocab) for _ in range(2)]
     h = ctx.to_device(wh.synth_normal(0x5749_4C4C_0000_0002, 2, cfg.n_embd))
     logits = ctx.alloc(cfg.vocab * 4)
-    for _ in range(3):
-        ctx.check(wh.lib.wm_logits_argmax_dev(ctx.h, t.h, h.ptr, logits.ptr, None))
+    for i in range(4):
+        ctx.check(wh.lib.wm_logits_argmax_dev(ctx.h, ts[i & 1].h, h.ptr, logits.ptr, None))
     timer = HipTimer(ctx.stream)
     timer.start()
-    for _ in range(reps):
-        ctx.check(wh.lib.wm_logits_argmax_dev(ctx.h, t.h, h.ptr, logits.ptr, None))
+    for i in range(reps):
+        ctx.check(wh.lib.wm_logits_argmax_dev(ctx.h, ts[i & 1].h, h.ptr, logits.ptr, None))
     ms = timer.stop_ms() / reps
     bytes_per = cfg.vocab * (cfg.n_embd // 256) * 210 + cfg.n_embd * 4 + cfg.vocab * 4
-    t.close()
+    for t in ts:
+        t.close()
     return ms, bytes_per
 
 
@@ -134,6 +137,76 @@ def cpu_baseline(hm, cfg, n_tokens: int, threads: int):
     return n_tokens / dt, dt
 
 
+COPY_BYTES = 1 << 30  # calibration copy for the HBM byte counters
+
+
+def probe(kind: str, reps: int):
+    """Short fixed run for hardware-counter passes (rocprofv3 --pmc): `reps`
+    launches of one kernel at its benchmark shape, then `reps` device-to-device
+    copies of COPY_BYTES, whose FETCH_SIZE / WRITE_SIZE readings convert the
+    counters into bytes."""
+    import willamette_hip as wh
+    import bitnet_synth as bs
+    cfg = bs.BITNET_2B
+    ctx = wh.Context(0)
+    held = []
+    if kind == "lm_head":
+        blocks = wh.synth_q6k(0x5749_4C4C_0000_0002, 1, cfg.vocab, cfg.n_embd, 1e-3)
+        ts = [ctx.upload_q6k(blocks, cfg.n_embd, cfg.vocab) for _ in range(2)]
+        del blocks
+        h = ctx.to_device(wh.synth_normal(0x5749_4C4C_0000_0002, 2, cfg.n_embd))
+        logits = ctx.alloc(cfg.vocab * 4)
+        held += ts + [h, logits]
+        turn = [0]
+
+        def launch():
+            t = ts[turn[0] & 1]
+            turn[0] += 1
+            ctx.check(wh.lib.wm_logits_argmax_dev(ctx.h, t.h, h.ptr, logits.ptr, None))
+    elif kind == "i2s":
+        copies = 320
+        seed = 0x5749_4C4C_0000_0001
+        packed = wh.synth_i2s(seed, 1, 2560, 2560)
+        ws = [ctx.upload_i2s(packed, 1.25, 2560, 2560) for _ in range(copies)]
+        x = ctx.to_device(wh.synth_normal(seed, 3, 2560))
+        y = ctx.alloc(copies * 2560 * 4)
+        arr = (wh._vp * copies)(*[w.h.value for w in ws])
+        held += ws + [x, y]
+        launch = lambda: ctx.check(wh.lib.wm_bitlinear_i2s_matvec_f32_multi_dev(
+            ctx.h, arr, copies, x.ptr, y.ptr))
+    else:
+        sys.exit(f"unknown probe {kind!r}")
+    for _ in range(reps):
+        launch()
+    ctx.synchronize()
+    log(f"probe {kind}: {reps} launches done")
+    src, dst = ctx.alloc(COPY_BYTES), ctx.alloc(COPY_BYTES)
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    for _ in range(reps):
+        assert hip.hipMemcpyAsync(C.c_void_p(dst.ptr), C.c_void_p(src.ptr), COPY_BYTES, 3,
+                                  C.c_void_p(ctx.stream)) == 0
+    ctx.synchronize()
+    log(f"probe copy: {reps} x {COPY_BYTES} bytes done")
+    for obj in held + [src, dst]:
+        (obj.close if hasattr(obj, "close") else obj.free)()
+    ctx.close()
+
+
+def traffic_record(kernel_file: str):
+    """HBM bytes per launch from the committed counter summary, used only
+    while the kernel source it was measured on is unchanged."""
+    import hashlib
+    rec_path = ROOT / "profiles" / "traffic.json"
+    src = ROOT / "project-willamette_amd" / "csrc" / kernel_file
+    if not rec_path.exists() or not src.exists():
+        return None
+    rec = json.loads(rec_path.read_text()).get(kernel_file)
+    if not rec or rec.get("source_sha256") != hashlib.sha256(src.read_bytes()).hexdigest():
+        return None
+    return rec["bytes_per_launch"]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -141,7 +214,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--probe", choices=["lm_head", "i2s"],
+                    help="only run one kernel (and a calibration copy) for counter passes")
+    ap.add_argument("--probe-reps", type=int, default=5)
     args = ap.parse_args()
+    if args.probe:
+        probe(args.probe, args.probe_reps)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(the decode path runs on a single MI355X)", file=sys.stderr)
@@ -219,7 +298,8 @@ def main():
                    "kv_heads": cfg.n_kv_heads, "vocab": cfg.vocab, "kv_prefill": PREFILL,
                    "decode_tokens": args.steps, "start_token": START_TOKEN, "exact": True},
         "roofline": {"bound": "hbm", "achieved": round(lm_gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(lm_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(lm_gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic_record("k_q6k.hip"),
                      "kernel": "k_q6k_logits (Q6_K lm-head 128256x2560)",
                      "us_per_launch": round(lm_ms * 1000, 2)},
         "cpu_baseline": cpu,

@@ -205,7 +205,8 @@ wm_status wm_decode_step(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t 
 /* greedy_generate_with_cache (src/model/generate.rs:111-189) continuing an
  * existing cache: prefill `prompt` in order, then up to max_new greedy
  * tokens, stopping at `eos` (< 0: none).  Writes *n_out ids to out_ids.
- * The whole loop runs on the device; tokens never visit the host. */
+ * Activations and the cache stay on the device; each step returns only its
+ * 4-byte token id to the host, which feeds it to the next step. */
 wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *prompt,
                              uint32_t n_prompt, uint32_t max_new, int64_t eos, uint32_t *out_ids,
                              uint32_t *n_out);

@@ -73,11 +73,11 @@ constexpr int kPStride = 68;    // floats per dim row of a product tile
 // waves 1-2 write tiles of products w_p * v_p[d] while wave 0 adds the
 // previous tile, one chain per dimension.
 __global__ __launch_bounds__(kThreads) void k_attn_softmax_v(attn_args a) {
-    extern __shared__ float sm[];
+    extern __shared__ __align__(16) float sm[];
     const uint32_t n = a.n_past;
     const uint32_t npad = (n + 3) & ~3u;
-    float *wts = sm;                                        // [npad]
-    float *vsc = wts + npad;                                // [npad]
+    float *wts = sm;                                        // [seq_sum_padded(n)]
+    float *vsc = wts + wm::seq_sum_padded(n);               // [npad]
     int4 *vq = reinterpret_cast<int4 *>(vsc + npad);        // [npad] x 16 int8
     float *prod = reinterpret_cast<float *>(vq + npad);     // [2][kDims][kPStride]
     __shared__ float red[16];
@@ -160,10 +160,16 @@ __global__ __launch_bounds__(kThreads) void k_attn_softmax_v(attn_args a) {
                 float *dst = prod + (t & 1) * (kDims * kPStride) + dh * kPStride + pl;
                 if (p < n) {
                     const int4 v4 = vq[p];
-                    const int8_t *b = reinterpret_cast<const int8_t *>(&v4) + dh;
+                    // this thread's 8 bytes, selected by register (no byte-indexed stack copy)
+                    const uint32_t lo = dh ? (uint32_t)v4.z : (uint32_t)v4.x;
+                    const uint32_t hi = dh ? (uint32_t)v4.w : (uint32_t)v4.y;
                     const float w = wts[p], s = vsc[p];
 #pragma unroll
-                    for (int i = 0; i < 8; i++) dst[i * kPStride] = w * ((float)b[i] * s);  // w * v_h[d]
+                    for (int i = 0; i < 8; i++) {
+                        const uint32_t word = i < 4 ? lo : hi;
+                        const float vd = (float)(int8_t)(word >> (8 * (i & 3))) * s;  // read_into: q * scale
+                        dst[i * kPStride] = w * vd;                                    // w * v_h[d]
+                    }
                 }
             }
         } else if (tid < kDims && t > 0) {
@@ -197,6 +203,7 @@ void wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
                 n_kv_heads * head_dim, head_dim, n_heads / n_kv_heads, score_stride, scale};
     hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, (n_past + 63) / 64), dim3(64), 0, s, a);
     const size_t npad = ((size_t)n_past + 3) & ~(size_t)3;
-    const size_t lds = npad * (4 + 4 + 16) + (size_t)2 * kDims * kPStride * 4;
+    const size_t lds = (size_t)wm::seq_sum_padded(n_past) * 4 + npad * (4 + 16) +
+                       (size_t)2 * kDims * kPStride * 4;
     hipLaunchKernelGGL(k_attn_softmax_v, dim3(n_heads, head_dim / kDims), dim3(kThreads), lds, s, a);
 }

@@ -41,7 +41,7 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
     float *__restrict__ x, residual_src res, const float *__restrict__ w, uint32_t n, float eps,
     uint8_t *__restrict__ act, wm_act_meta *__restrict__ meta_out, float *__restrict__ y_out,
     uint32_t *__restrict__ err_flag, uint32_t layer_tag) {
-    extern __shared__ float sq[];  // x[j]*x[j]
+    extern __shared__ __align__(16) float sq[];  // x[j]*x[j], wm::seq_sum_padded(n) entries
     __shared__ float red_f[16];
     __shared__ int red_i[16];
     __shared__ float s_sum;
@@ -267,10 +267,23 @@ __global__ __launch_bounds__(256) void k_kv_append(const float *__restrict__ k,
     kv_quantise_store(v + src, kv_dim, v_cache + dst * kv_dim, v_scales + dst, red);
 }
 
-__global__ __launch_bounds__(64) void k_debug_seq_sum(const float *__restrict__ a, uint32_t n,
-                                                      float *__restrict__ out) {
-    const float s = wm::seq_sum_nonneg(a, n);
-    if (threadIdx.x == 0) *out = s;
+// Test hook: the terms are staged into LDS (as every caller holds them)
+// when they fit, else read from global memory; either way the array is
+// padded to wm::seq_sum_padded(n) entries.
+constexpr uint32_t kDebugSeqLds = 32768;
+__global__ __launch_bounds__(1024) void k_debug_seq_sum(const float *__restrict__ a, uint32_t n,
+                                                        float *__restrict__ out) {
+    extern __shared__ __align__(16) float terms[];
+    const float *src = a;
+    if (n <= kDebugSeqLds) {
+        for (uint32_t i = threadIdx.x; i < wm::seq_sum_padded(n); i += blockDim.x) terms[i] = a[i];
+        __syncthreads();
+        src = terms;
+    }
+    if (threadIdx.x < 64) {
+        const float s = wm::seq_sum_nonneg(src, n);
+        if (threadIdx.x == 0) *out = s;
+    }
 }
 
 }  // namespace
@@ -280,7 +293,8 @@ __global__ __launch_bounds__(64) void k_debug_seq_sum(const float *__restrict__ 
 // ---------------------------------------------------------------------------
 
 void wm_launch_debug_seq_sum(const float *a, uint32_t n, float *out, hipStream_t s) {
-    hipLaunchKernelGGL(k_debug_seq_sum, dim3(1), dim3(64), 0, s, a, n, out);
+    const size_t lds = n <= kDebugSeqLds ? (size_t)wm::seq_sum_padded(n) * sizeof(float) : 0;
+    hipLaunchKernelGGL(k_debug_seq_sum, dim3(1), dim3(1024), lds, s, a, n, out);
 }
 
 void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, uint32_t rows_total,
@@ -289,7 +303,7 @@ void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, u
                              wm_act_meta *meta_out, float *y_out, uint32_t *err_flag,
                              uint32_t layer_tag, hipStream_t s) {
     residual_src res{partial, split, rows_total, row0, w_scale, meta_in};
-    size_t lds = ((size_t)n + 8) * sizeof(float);
+    size_t lds = (size_t)wm::seq_sum_padded(n) * sizeof(float);
     const int per = (int)((n + kNormThreads - 1) / kNormThreads);
 #define WM_NORM_CASE(P)                                                                            \
     case P:                                                                                        \

@@ -489,10 +489,12 @@ wm_status wm_compute_logits(wm_ctx *ctx, const wm_tensor *t, const float *hidden
 
 wm_status wm_debug_seq_sum(wm_ctx *ctx, const float *values, size_t n, float *sum) {
     if (!ctx || !sum || (n && !values) || n > (1u << 26)) return WM_E_ARG;
+    // terms padded to whole 512-term steps (read, never used)
+    const size_t padded = (n + 511) / 512 * 512;
     void *scratch;
-    wm_status st = wm_ctx_scratch(ctx, n * 4 + 256, &scratch);
+    wm_status st = wm_ctx_scratch(ctx, padded * 4 + 256, &scratch);
     if (st) return st;
-    float *d_in = (float *)scratch, *d_out = (float *)((uint8_t *)scratch + ((n * 4 + 255) & ~(size_t)255));
+    float *d_in = (float *)scratch, *d_out = (float *)((uint8_t *)scratch + padded * 4);
     WM_HIP(ctx, hipSetDevice(ctx->device));
     if (n) WM_HIP(ctx, hipMemcpyAsync(d_in, values, n * 4, hipMemcpyHostToDevice, ctx->stream));
     wm_launch_debug_seq_sum(d_in, (uint32_t)n, d_out, ctx->stream);

@@ -8,7 +8,7 @@
 // a different token, so the device must produce exactly this value.  Doing
 // the adds one by one costs ~30 cycles per term (each step waits on the
 // previous one); this routine produces the same bits with one wave working
-// on 256 terms at a time:
+// on 512 terms at a time:
 //
 //   While s stays inside one binade [2^E, 2^(E+1)) with ulp u = 2^(E-23),
 //   s = N*u for an integer N in [2^23, 2^24), and
@@ -27,7 +27,8 @@
 // (increment 0, never a tie), which the code also concludes.
 //
 // Called by all 64 lanes of one wave with the terms in LDS (or any memory
-// readable by every lane); returns the sum in every lane.
+// readable by every lane); returns the sum in every lane.  Non-negative
+// terms make every step an increase, so only upward crossings occur.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -51,69 +52,109 @@ __device__ __forceinline__ int wave_incl_scan_i32(int x) {
     return x;
 }
 
+// Terms handled per wave step (8 per lane).  Callers allocate the term
+// array 16-byte aligned and readable up to seq_sum_padded(n) entries; the
+// entries past n are read but ignored.
+constexpr uint32_t kSeqBatch = 512;
+constexpr int kSeqLead = 128;  // leading terms added one by one
+__host__ __device__ constexpr uint32_t seq_sum_padded(uint32_t n) {
+    return (n + kSeqBatch - 1) / kSeqBatch * kSeqBatch;
+}
+
 // Sequential f32 sum of n non-negative terms a[0..n) (as s += a[i]).
 // Negative terms are not allowed (the caller's terms are squares or exp()).
+//
+// Per step the wave holds 512 terms in registers.  The run test works from
+// s's own bits: a normal s is N * 2^(E-23) with N its 24-bit significand and
+// a term's increment is RN_int(ldexp(a, 23 - E)).  The same test covers the
+// other values of s through the shift alone: while s is +0 or subnormal the
+// shift is +255, so every non-zero term overflows the run limit and is added
+// on its own (zero terms leave s unchanged); while s is +inf it is -255, so
+// finite terms add nothing and only NaN or inf terms are added on their own.
+// A NaN s absorbs everything.  Terms already added are zeroed in the
+// registers and the same registers are rescanned with the new s, so no term
+// is loaded twice.  The first kSeqLead terms, which move s through many
+// binades and (while s is small) hold most of the halfway cases, are added
+// one at a time straight from the registers.
 __device__ inline float seq_sum_nonneg(const float *a, uint32_t n) {
     const uint32_t lane = threadIdx.x & 63;
     float s = 0.0f;
-    uint32_t k = 0;
-    // Leading terms one at a time: the first terms move s across many
-    // binades, which would end every parallel run after one term.
-    const uint32_t lead = n < 32 ? n : 32;
-    for (; k < lead; k++) s = s + a[k];
-    while (k < n) {
-        if (!(s >= 0x1p-60f && s <= 0x1p+100f)) {  // zero, tiny, huge, inf or NaN
-            for (; k < n; k++) s = s + a[k];
-            break;
-        }
-        const int E = (int)((__float_as_uint(s) >> 23) & 0xffu) - 127;
-        const int sh = 23 - E;
-        const int N = (int)ldexpf(s, sh);  // s / ulp, in [2^23, 2^24)
-        const uint32_t base = k + 4 * lane;
-        float v[4];
-        // unconditional loads from clamped indices, so all four are in flight at once
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t i = base + j < n ? base + j : n - 1;
-            v[j] = a[i];
+    if (n == 0) return s;
+    float4 nx0 = *reinterpret_cast<const float4 *>(a + 8 * lane);
+    float4 nx1 = *reinterpret_cast<const float4 *>(a + 8 * lane + 4);
+    for (uint32_t k = 0; k < n; k += kSeqBatch) {
+        const uint32_t base = k + 8 * lane;
+        float v[8] = {nx0.x, nx0.y, nx0.z, nx0.w, nx1.x, nx1.y, nx1.z, nx1.w};
+        if (k + kSeqBatch < n) {  // next step's terms, in flight during this one
+            nx0 = *reinterpret_cast<const float4 *>(a + base + kSeqBatch);
+            nx1 = *reinterpret_cast<const float4 *>(a + base + kSeqBatch + 4);
         }
 #pragma unroll
-        for (int j = 0; j < 4; j++) v[j] = (base + j < n) ? v[j] : 0.0f;
-        int rho[4];
-        bool bad[4];
+        for (int j = 0; j < 8; j++) v[j] = base + j < n ? v[j] : 0.0f;
+        if (k == 0) {
+            // terms 0..127 sit in lanes 0-15; adding the zeros past n changes nothing
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float r = ldexpf(v[j], sh);  // a / ulp
-            const bool ok = r < 0x1p22f;     // false for NaN, inf, huge
-            const float f = floorf(r);
-            const float fr = r - f;
-            bad[j] = !ok || fr == 0.5f;
-            rho[j] = bad[j] ? 0 : (int)f + (fr > 0.5f ? 1 : 0);
-        }
-        const int p0 = rho[0], p1 = p0 + rho[1], p2 = p1 + rho[2], p3 = p2 + rho[3];
-        const int incl = wave_incl_scan_i32(p3);
-        const int excl = incl - p3;
-        const int limit = (1 << 24) - 1 - N;  // run continues while prefix < limit
-        const int pj[4] = {p0, p1, p2, p3};
-        int first = 4;
+            for (int L = 0; L < kSeqLead / 8; L++)
 #pragma unroll
-        for (int j = 3; j >= 0; j--)
-            if (bad[j] || excl + pj[j] >= limit) first = j;
-        const uint64_t mask = __ballot(first < 4);
-        if (mask == 0) {
-            const int total = __builtin_amdgcn_readlane(incl, 63);
-            s = ldexpf((float)(N + total), -sh);
-            k = (k + 256 < n) ? k + 256 : n;
-            continue;
+                for (int j = 0; j < 8; j++)
+                    s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), L));
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = lane < kSeqLead / 8 ? 0.0f : v[j];
         }
-        const int fl = __ffsll((unsigned long long)mask) - 1;
-        const int before = excl + (first == 0 ? 0 : (first == 1 ? p0 : (first == 2 ? p1 : p2)));
-        const int jl = __builtin_amdgcn_readlane(first, fl);
-        const int pre = __builtin_amdgcn_readlane(before, fl);
-        const uint32_t idx = k + 4 * (uint32_t)fl + (uint32_t)jl;
-        s = ldexpf((float)(N + pre), -sh);  // the run before the offending term
-        s = s + a[idx];                     // that term, by an ordinary add
-        k = idx + 1;
+        // Each restart zeroes at least one non-zero term, so a step ends after
+        // at most 513 passes; the bound is explicit all the same.
+        for (uint32_t pass = 0; pass <= kSeqBatch; pass++) {
+            if (s != s) return s;
+            const uint32_t bits = __float_as_uint(s);  // s >= +0
+            const uint32_t ef = bits >> 23;
+            const bool normal = ef - 1u < 254u;
+            const int sh = normal ? 150 - (int)ef : (ef == 0 ? 255 : -255);
+            const int N = normal ? (int)((bits & 0x7fffffu) | 0x800000u) : 0;
+            int p[8], rho[8];
+            bool bad[8];
+            int run = 0;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float r = ldexpf(v[j], sh);    // a / ulp(s); exact unless < 2^-126
+                const bool fin = r < 0x1p22f;         // false for NaN, inf, huge
+                const float rr = fin ? r : 0.0f;
+                bad[j] = !fin || rr - floorf(rr) == 0.5f;  // halfway: parity decides
+                rho[j] = (int)rintf(rr);
+                run += rho[j];
+                p[j] = run;
+            }
+            const int incl = wave_incl_scan_i32(run);
+            const int excl = incl - run;
+            const int limit = (1 << 24) - 1 - N;  // N + prefix must stay below 2^24 - 1
+            int first = 8, before = 0;
+#pragma unroll
+            for (int j = 7; j >= 0; j--) {
+                // A term with increment 0 leaves N + prefix where it was, so it
+                // never crosses; hence offenders are never zero terms (a zero
+                // term is neither bad nor crossing), and every restart below
+                // consumes a non-zero term.
+                const bool off = bad[j] || (rho[j] > 0 && excl + p[j] >= limit);
+                first = off ? j : first;
+                before = off ? excl + (j ? p[j - 1] : 0) : before;
+            }
+            const uint64_t mask = __ballot(first < 8);
+            if (mask == 0) {
+                if (normal) s = ldexpf((float)(N + __builtin_amdgcn_readlane(incl, 63)), -sh);
+                break;
+            }
+            const int fl = __ffsll((unsigned long long)mask) - 1;
+            const int jl = __builtin_amdgcn_readlane(first, fl);
+            const int pre = __builtin_amdgcn_readlane(before, fl);
+            float vo = v[0];
+#pragma unroll
+            for (int j = 1; j < 8; j++) vo = j == jl ? v[j] : vo;
+            vo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vo), fl));
+            if (normal) s = ldexpf((float)(N + pre), -sh);  // the run before the offender
+            s = s + vo;                                      // the offender, by an ordinary add
+            const uint32_t done = 8 * (uint32_t)fl + (uint32_t)jl;  // last term now in s
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = 8 * lane + j <= done ? 0.0f : v[j];
+        }
     }
     return s;
 }

@@ -58,6 +58,10 @@ def cases():
     inf = rng.standard_normal(700).astype(np.float32) ** 2
     inf[10] = np.inf
     out.append(("inf", inf))
+    # s reaches a significand of all ones (N = 2^24 - 1) after the leading
+    # terms; zero-increment terms there must not end the run
+    out.append(("allones_significand", np.concatenate(
+        [[16777215.0], np.zeros(127), [0.25, 0, 0, 1.0, 0.5, 3.0], np.full(600, 0.25)]).astype(np.float32)))
     # long random runs with many ties: values on a coarse grid
     g = (rng.integers(0, 64, 20000) * 0.25).astype(np.float32)
     out.append(("grid", np.concatenate([[2.0 ** 22], g]).astype(np.float32)))

@@ -1,0 +1,142 @@
+"""CPU model of the wave-parallel exact sum in
+project-willamette_amd/csrc/wm_seqsum.h (64 lanes x 8 terms per step, the
+128-term sequential lead, the run test on s's significand, restarts that zero
+consumed terms), evaluated in numpy float32 and compared bit for bit with the
+left-to-right float32 accumulation.  It checks the algorithm itself (exactness
+and the bound on passes per step) without a GPU; the GPU tests check the
+device code against the same sequential sums."""
+import numpy as np
+import pytest
+
+f32 = np.float32
+LANES, PER = 64, 8
+STEP = LANES * PER
+LEAD = 128
+
+
+class PassCapReached(RuntimeError):
+    pass
+
+
+def model_sum(a):
+    """Returns (sum, largest pass index used in any step)."""
+    a = np.asarray(a, np.float32)
+    n = a.size
+    s = f32(0.0)
+    max_pass = 0
+    if n == 0:
+        return s, 0
+    buf = np.zeros(-(-n // STEP) * STEP, np.float32)
+    buf[:n] = a
+    pos = np.arange(STEP).reshape(LANES, PER)
+    for k in range(0, n, STEP):
+        v = buf[k:k + STEP].reshape(LANES, PER).copy()
+        v[k + pos >= n] = 0
+        if k == 0:
+            with np.errstate(all="ignore"):
+                for t in range(LEAD):
+                    s = f32(s + v[t // PER, t % PER])
+            v[:LEAD // PER, :] = 0
+        for ps in range(STEP + 1):
+            max_pass = max(max_pass, ps)
+            if np.isnan(s):
+                return s, max_pass
+            bits = int(np.array(s, np.float32).view(np.uint32))
+            ef = bits >> 23
+            normal = 1 <= ef <= 254
+            sh = 150 - ef if normal else (255 if ef == 0 else -255)
+            N = ((bits & 0x7FFFFF) | 0x800000) if normal else 0
+            with np.errstate(all="ignore"):
+                r = np.ldexp(v, sh).astype(np.float32)
+            fin = r < f32(2.0 ** 22)
+            rr = np.where(fin, r, f32(0)).astype(np.float32)
+            bad = (~fin) | ((rr - np.floor(rr)) == f32(0.5))
+            rho = np.rint(rr).astype(np.int64)
+            p = np.cumsum(rho, axis=1)
+            incl = np.cumsum(p[:, -1])
+            excl = incl - p[:, -1]
+            limit = (1 << 24) - 1 - N
+            off = bad | ((rho > 0) & (excl[:, None] + p >= limit))
+            if not off.any():
+                if normal:
+                    s = f32(np.ldexp(f32(N + int(incl[-1])), -sh))
+                break
+            fl, jl = divmod(int(np.argmax(off.reshape(-1))), PER)
+            pre = int(excl[fl]) + (int(p[fl, jl - 1]) if jl else 0)
+            if normal:
+                s = f32(np.ldexp(f32(N + pre), -sh))
+            with np.errstate(all="ignore"):
+                s = f32(s + v[fl, jl])
+            v[pos <= PER * fl + jl] = 0
+        else:
+            raise PassCapReached()
+    return s, max_pass
+
+
+def sequential(a):
+    a = np.asarray(a, np.float32)
+    if a.size == 0:
+        return f32(0.0)
+    with np.errstate(all="ignore"):
+        return np.add.accumulate(a, dtype=np.float32)[-1]
+
+
+def same(x, y):
+    x, y = np.float32(x), np.float32(y)
+    return (np.isnan(x) and np.isnan(y)) or x.view(np.uint32) == y.view(np.uint32)
+
+
+def inputs():
+    rng = np.random.default_rng(7)
+    out = [
+        ("empty", np.zeros(0, np.float32)),
+        ("sq2560", rng.standard_normal(2560).astype(np.float32) ** 2),
+        ("sq6912", rng.standard_normal(6912).astype(np.float32) ** 2),
+        ("zeros", np.zeros(3000, np.float32)),
+        ("subnormal", np.full(2000, 1e-40, np.float32)),
+        ("ties_ulp2", np.concatenate([[2.0 ** 24], rng.integers(0, 4, 3000)]).astype(np.float32)),
+        ("allones_significand", np.concatenate(
+            [[16777215.0], np.zeros(LEAD - 1), [0.25, 0, 0, 1.0, 0.5, 3.0], np.ones(1000)]).astype(np.float32)),
+        ("overflow", np.full(300, 3e37, np.float32)),
+    ]
+    x = (rng.standard_normal(1100) * 8).astype(np.float32)
+    out.append(("softmax_wide", np.exp(x - x.max()).astype(np.float32)))
+    nan = rng.standard_normal(700).astype(np.float32) ** 2
+    nan[400] = np.nan
+    out.append(("nan", nan))
+    return out
+
+
+@pytest.mark.parametrize("name,a", inputs(), ids=[c[0] for c in inputs()])
+def test_model_matches_sequential(name, a):
+    got, max_pass = model_sum(a)
+    assert same(got, sequential(a)), name
+    assert max_pass <= STEP
+
+
+def test_model_fuzz():
+    rng = np.random.default_rng(11)
+    for i in range(400):
+        n = int(rng.integers(1, 2000))
+        sc = float(2.0 ** rng.integers(-20, 20))
+        kind = i % 4
+        if kind == 0:
+            a = (rng.standard_normal(n) * sc).astype(np.float32) ** 2
+        elif kind == 1:
+            a = (rng.integers(0, 8, n) * sc).astype(np.float32)
+        elif kind == 2:
+            x = (rng.standard_normal(n) * 8).astype(np.float32)
+            a = np.exp(x - x.max()).astype(np.float32)
+        else:
+            a = np.full(n, f32(2.0 ** rng.integers(-3, 3)), np.float32)
+            a[0] = f32(2 ** 24 - 1) * f32(2.0 ** rng.integers(-30, 0))
+        got, _ = model_sum(a)
+        assert same(got, sequential(a)), f"case {i} kind {kind} n {n}"
+
+
+def test_zero_increment_terms_never_end_a_run():
+    # Without the increment guard, a consumed (zeroed) term satisfies the
+    # crossing test when N = 2^24 - 1 and the pass repeats without progress.
+    a = np.concatenate([[16777215.0], np.zeros(LEAD - 1), [0.25, 0, 0, 1.0]]).astype(np.float32)
+    got, max_pass = model_sum(a)
+    assert same(got, sequential(a)) and max_pass < 8
