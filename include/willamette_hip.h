@@ -118,6 +118,19 @@ wm_status wm_bitlinear_i2s_matvec_f32_multi_dev(wm_ctx *ctx, const wm_tensor *co
                                                 uint32_t n_copies, const float *d_input,
                                                 float *d_outputs);
 
+/* Batched BitLinear: m activation rows x [m][in_dim] (device), each row
+ * quantised on its own (per-token absmax int8, src/model/bitlinear_sse2.rs:285-304),
+ * y[m][out_dim] (device).  Row r of y is bit-identical to
+ * wm_bitlinear_i2s_matvec_f32 on row r of x: the ternary x int8 products
+ * are exact i32 sums, here from int8 MFMA.  Used by the ragged batch
+ * (multi_token_forward's per-token linear_matvec_f32 calls,
+ * src/model/multi_forward.rs:107-110, :176, :202-203, :226). */
+wm_status wm_bitlinear_i2s_matmul_f32_dev(wm_ctx *ctx, const wm_tensor *w, const float *d_x,
+                                          uint32_t m, float *d_y);
+/* Host-slice form: x_len == m * in_dim, y_len == m * out_dim. */
+wm_status wm_bitlinear_i2s_matmul_f32(wm_ctx *ctx, const wm_tensor *w, const float *x,
+                                      size_t x_len, uint32_t m, float *y, size_t y_len);
+
 /* ---- Q6_K / lm-head (src/model/q6_k.rs, lm_head.rs) ------------------ */
 
 /* Dequantise one row (src/model/q6_k.rs:59-69); embedding gather for a
@@ -210,6 +223,25 @@ wm_status wm_decode_step(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t 
 wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *prompt,
                              uint32_t n_prompt, uint32_t max_new, int64_t eos, uint32_t *out_ids,
                              uint32_t *n_out);
+
+/* Ragged multi-sequence step (continuous batching).  Sequence i appends
+ * n_new[i] tokens (tokens[] holds them sequence after sequence) to its own
+ * cache caches[i], starting at wm_kv_cache_position(caches[i]); each token
+ * attends to its sequence's cache up to and including itself.  The result
+ * is bit-identical to running wm_forward_with_cache on every token in order,
+ * sequence by sequence: multi_token_forward (src/model/multi_forward.rs:49-243)
+ * with a pre-filled cache, new K/V going through the int8 KV quantiser as in
+ * the sequential prefill of src/model/generate.rs:151-160.
+ *   last_hidden (n_seqs x n_embd, host, nullable): each sequence's last
+ *     token after output_norm;
+ *   next_tokens (n_seqs, host, nullable): argmax of that token's logits.
+ * The caches must be distinct and belong to `m`; head_dim must be 64 or 128
+ * and n_heads / n_kv_heads one of 1, 2, 4, 8.  A non-finite hidden in any
+ * token leaves every cache at its starting position and returns
+ * WM_E_NONFINITE. */
+wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_seqs,
+                           const uint32_t *n_new, const uint32_t *tokens, float *last_hidden,
+                           uint32_t *next_tokens);
 
 /* ---- test hook ------------------------------------------------------- */
 

@@ -162,6 +162,21 @@ class DeviceModel:
     def kv_cache(self, max_seq: int) -> "DeviceKV":
         return DeviceKV(self, max_seq)
 
+    def batch_forward(self, kvs, seqs, want_hidden: bool = True, want_next: bool = True):
+        """Ragged step: seqs[i] (token ids) appended to kvs[i] in one batch.
+        Returns (last hidden per sequence, next token per sequence)."""
+        n = len(kvs)
+        arr = (wh._vp * n)(*[kv.h.value for kv in kvs])
+        n_new = np.array([len(t) for t in seqs], np.uint32)
+        toks = np.ascontiguousarray(np.concatenate([np.asarray(t, np.uint32) for t in seqs]))
+        hidden = np.empty((n, self.cfg.n_embd), np.float32) if want_hidden else None
+        nxt = np.empty(n, np.uint32) if want_next else None
+        self.ctx.check(wh.lib.wm_batch_forward(
+            self.h, arr, n, wh._ptr(n_new, wh.C.c_uint32), wh._ptr(toks, wh.C.c_uint32),
+            wh._ptr(hidden, wh.C.c_float) if want_hidden else None,
+            wh._ptr(nxt, wh.C.c_uint32) if want_next else None))
+        return hidden, (nxt.tolist() if want_next else None)
+
 
 class DeviceKV:
     _close_rank = 0

@@ -135,23 +135,6 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
     }
 }
 
-// KV quantisation of one token vector in LDS (src/model/kv_cache.rs:245-259):
-// absmax (NaN never raises it), zero/non-finite absmax -> zeros + scale 0.
-__device__ void kv_quantise_store(const float *__restrict__ v, uint32_t n, int8_t *__restrict__ q,
-                                  float *__restrict__ scale_out, float *red) {
-    float m = 0.0f;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) m = wm_max_nonan(m, fabsf(v[i]));
-    const float absmax = wm_block_max_nonan(m, red);
-    if (absmax == 0.0f || !isfinite(absmax)) {
-        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) q[i] = 0;
-        if (threadIdx.x == 0) *scale_out = 0.0f;
-        return;
-    }
-    const float inv = 127.0f / absmax;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) q[i] = (int8_t)wm_round_clamp_i8(v[i] * inv);
-    if (threadIdx.x == 0) *scale_out = absmax / 127.0f;
-}
-
 struct qkv_args {
     const int32_t *partial;
     uint32_t split, rows_total;
@@ -222,9 +205,9 @@ __global__ __launch_bounds__(1024) void k_qkv_rope_kv(qkv_args a) {
     }
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < a.n_q; i += blockDim.x) a.q_out[i] = qs[i];
-    kv_quantise_store(ks, a.n_kv, a.k_cache, a.k_scale_out, red);
+    wm_kv_quantise_store(ks, a.n_kv, a.k_cache, a.k_scale_out, red);
     __syncthreads();
-    kv_quantise_store(vs, a.n_kv, a.v_cache, a.v_scale_out, red);
+    wm_kv_quantise_store(vs, a.n_kv, a.v_cache, a.v_scale_out, red);
 }
 
 // relu(g)^2 * u over the gate/up BitLinear outputs (ffn.rs:37-65).
@@ -262,9 +245,9 @@ __global__ __launch_bounds__(256) void k_kv_append(const float *__restrict__ k,
     const uint32_t l = blockIdx.x, p = blockIdx.y;
     const uint64_t src = ((uint64_t)p * n_layers + l) * kv_dim;
     const uint64_t dst = ((uint64_t)l * max_seq + pos0 + p);
-    kv_quantise_store(k + src, kv_dim, k_cache + dst * kv_dim, k_scales + dst, red);
+    wm_kv_quantise_store(k + src, kv_dim, k_cache + dst * kv_dim, k_scales + dst, red);
     __syncthreads();
-    kv_quantise_store(v + src, kv_dim, v_cache + dst * kv_dim, v_scales + dst, red);
+    wm_kv_quantise_store(v + src, kv_dim, v_cache + dst * kv_dim, v_scales + dst, red);
 }
 
 // Test hook: the terms are staged into LDS (as every caller holds them)

@@ -92,10 +92,13 @@ __device__ __forceinline__ uint32_t q6_step(uint32_t w0, uint32_t w1, uint32_t w
 }
 
 // Dequantise row values: thread t of 256 handles value t of each block.
+// Grid (n_blocks, n_rows): row blockIdx.y comes from d_row[blockIdx.y] when
+// d_row is given and goes to out + blockIdx.y * ld.
 __global__ void k_q6k_dequant_row(const uint8_t *__restrict__ w, uint32_t n_blocks,
                                   uint32_t row, const uint32_t *__restrict__ d_row,
-                                  float *__restrict__ out) {
-    if (d_row) row = *d_row;
+                                  float *__restrict__ out, uint32_t ld) {
+    if (d_row) row = d_row[blockIdx.y];
+    out += (uint64_t)blockIdx.y * ld;
     const uint32_t G = row / Q6K_GROUP_ROWS, r = row % Q6K_GROUP_ROWS;
     const uint32_t b = blockIdx.x, t = threadIdx.x;
     const uint8_t *base = w + ((uint64_t)G * n_blocks + b) * Q6K_GROUP_BLOCK_BYTES;
@@ -248,13 +251,19 @@ void wm_launch_q6k_repack(const uint8_t *raw, uint8_t *out, uint32_t n_rows, uin
 void wm_launch_q6k_dequant_row(const uint8_t *w, uint32_t n_blocks, uint32_t row, float *out,
                                hipStream_t s) {
     hipLaunchKernelGGL(k_q6k_dequant_row, dim3(n_blocks), dim3(256), 0, s, w, n_blocks, row,
-                       (const uint32_t *)nullptr, out);
+                       (const uint32_t *)nullptr, out, 0u);
 }
 
 void wm_launch_q6k_dequant_row_dev(const uint8_t *w, uint32_t n_blocks, const uint32_t *d_row,
                                    float *out, hipStream_t s) {
     hipLaunchKernelGGL(k_q6k_dequant_row, dim3(n_blocks), dim3(256), 0, s, w, n_blocks, 0u, d_row,
-                       out);
+                       out, 0u);
+}
+
+void wm_launch_q6k_dequant_rows_dev(const uint8_t *w, uint32_t n_blocks, const uint32_t *d_rows,
+                                    uint32_t n_rows, float *out, uint32_t ld, hipStream_t s) {
+    hipLaunchKernelGGL(k_q6k_dequant_row, dim3(n_blocks, n_rows), dim3(256), 0, s, w, n_blocks, 0u,
+                       d_rows, out, ld);
 }
 
 size_t wm_q6k_logits_work_bytes() { return sizeof(argcand) * kMaxArgBlocks + 256; }

@@ -85,6 +85,15 @@ struct wm_model {
     void *lm_work = nullptr;
     // split choices
     uint32_t split_qkv = 1, split_o = 1, split_gu = 1, split_down = 1;
+    // ragged-batch workspace, grown on demand to b_cap tokens
+    uint8_t *bws = nullptr;
+    uint32_t b_cap = 0;
+    float *b_hidden = nullptr, *b_yqkv = nullptr, *b_q = nullptr, *b_attn = nullptr,
+          *b_yo = nullptr, *b_ygu = nullptr, *b_ydown = nullptr, *b_final = nullptr;
+    uint8_t *b_act = nullptr;
+    wm_act_meta *b_meta = nullptr;
+    wm_batch_tok *b_tok = nullptr;
+    uint32_t *b_ids = nullptr, *b_next = nullptr;
 };
 
 struct wm_kv_cache {
@@ -239,9 +248,181 @@ wm_status finish_step(wm_model *m, wm_kv_cache *kv, uint32_t pos, bool *failed) 
     return WM_OK;
 }
 
+constexpr uint32_t kBatchMaxTokens = 16384;
+
+// Grow the ragged-batch workspace to hold `M` tokens.
+wm_status ensure_batch_ws(wm_model *m, uint32_t M) {
+    if (M <= m->b_cap) return WM_OK;
+    wm_ctx *ctx = m->ctx;
+    const uint32_t cap = (M + WM_GEMM_TILE_TOKENS - 1) / WM_GEMM_TILE_TOKENS * WM_GEMM_TILE_TOKENS;
+    const size_t E = m->cfg.n_embd, F = m->cfg.n_ff, KV = m->kv_dim;
+    const size_t sizes[] = {
+        align256(cap * E * 4),             // hidden
+        align256(cap * (E + 2 * KV) * 4),  // q|k|v BitLinear outputs
+        align256(cap * E * 4),             // q after RoPE
+        align256(cap * E * 4),             // attention output
+        align256(cap * E * 4),             // wo output
+        align256(cap * 2 * F * 4),         // gate|up outputs
+        align256(cap * E * 4),             // down output
+        align256(cap * E * 4),             // output_norm
+        align256(cap * std::max(E, F)),    // int8 activations (GEMM layout)
+        align256(cap * sizeof(wm_act_meta)),
+        align256(cap * sizeof(wm_batch_tok)),
+        align256(cap * 4),                 // token ids
+        align256(cap * 4),                 // next tokens
+    };
+    size_t total = 0;
+    for (size_t sz : sizes) total += sz;
+    WM_HIP(ctx, hipSetDevice(m->device));
+    if (m->bws) {
+        WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        WM_HIP(ctx, hipFree(m->bws));
+        m->bws = nullptr;
+        m->b_cap = 0;
+    }
+    WM_HIP(ctx, hipMalloc((void **)&m->bws, total));
+    uint8_t *p = m->bws;
+    void **slots[] = {(void **)&m->b_hidden, (void **)&m->b_yqkv, (void **)&m->b_q,
+                      (void **)&m->b_attn,   (void **)&m->b_yo,   (void **)&m->b_ygu,
+                      (void **)&m->b_ydown,  (void **)&m->b_final, (void **)&m->b_act,
+                      (void **)&m->b_meta,   (void **)&m->b_tok,  (void **)&m->b_ids,
+                      (void **)&m->b_next};
+    for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); i++) {
+        *slots[i] = p;
+        p += sizes[i];
+    }
+    m->b_cap = cap;
+    return WM_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_seqs,
+                           const uint32_t *n_new, const uint32_t *tokens, float *last_hidden,
+                           uint32_t *next_tokens) {
+    if (!m) return WM_E_ARG;
+    wm_ctx *ctx = m->ctx;
+    if (!caches || !n_new || !tokens || n_seqs == 0)
+        return wm_set_error(ctx, WM_E_ARG, "batch_forward: empty batch");
+    if (!model_ready(m)) return wm_set_error(ctx, WM_E_STATE, "model: weights not fully set");
+    const wm_model_config &c = m->cfg;
+    const uint32_t group = c.n_heads / c.n_kv_heads;
+    if (!wm_attn_rows_supported(c.head_dim, group))
+        return wm_set_error(ctx, WM_E_SHAPE, "batch_forward: head_dim %u with %u query heads per kv head is not supported",
+                            c.head_dim, group);
+    if (c.n_embd > 8192 || c.n_ff > 8192)  // one 1024-thread workgroup per row norm, <= 8 values per thread
+        return wm_set_error(ctx, WM_E_SHAPE, "batch_forward: n_embd/n_ff above 8192 are not supported");
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < n_seqs; i++) {
+        const wm_kv_cache *kv = caches[i];
+        if (!kv || kv->m != m) return wm_set_error(ctx, WM_E_ARG, "batch_forward: cache %u is not a cache of this model", i);
+        for (uint32_t j = 0; j < i; j++)
+            if (caches[j] == kv) return wm_set_error(ctx, WM_E_ARG, "batch_forward: cache %u appears twice", i);
+        if (n_new[i] == 0)
+            return wm_set_error(ctx, WM_E_ARG, "multi_token_forward: token_ids must not be empty (sequence %u)", i);
+        if ((uint64_t)kv->pos + n_new[i] > kv->max_seq)
+            return wm_set_error(ctx, WM_E_SHAPE, "KVCache::append: sequence %u would pass max_seq_len %u", i,
+                                kv->max_seq);
+        total += n_new[i];
+    }
+    if (total > kBatchMaxTokens)
+        return wm_set_error(ctx, WM_E_SHAPE, "batch_forward: %llu tokens exceed the batch limit %u",
+                            (unsigned long long)total, kBatchMaxTokens);
+    const uint32_t M = (uint32_t)total;
+    for (uint32_t t = 0; t < M; t++)
+        if (tokens[t] >= c.vocab_size)
+            return wm_set_error(ctx, WM_E_SHAPE, "forward_with_cache: token_id %u out of vocab range %u",
+                                tokens[t], c.vocab_size);
+    wm_status st = ensure_batch_ws(m, M);
+    if (st) return st;
+    std::vector<wm_batch_tok> tok(M);
+    std::vector<uint32_t> last(n_seqs);
+    uint32_t n_max = 1, t = 0;
+    for (uint32_t i = 0; i < n_seqs; i++) {
+        wm_kv_cache *kv = caches[i];
+        for (uint32_t j = 0; j < n_new[i]; j++, t++) {
+            tok[t] = wm_batch_tok{kv->k, kv->v, kv->ks, kv->vs, kv->max_seq, kv->pos + j};
+            n_max = std::max(n_max, kv->pos + j + 1);
+        }
+        last[i] = t - 1;
+    }
+    hipStream_t s = ctx->stream;
+    WM_HIP(ctx, hipSetDevice(m->device));
+    WM_HIP(ctx, hipMemcpyAsync(m->b_tok, tok.data(), M * sizeof(wm_batch_tok), hipMemcpyHostToDevice, s));
+    WM_HIP(ctx, hipMemcpyAsync(m->b_ids, tokens, M * 4, hipMemcpyHostToDevice, s));
+
+    const uint32_t E = c.n_embd, F = c.n_ff, KV = m->kv_dim, QKV = E + 2 * KV;
+    const uint32_t m_pad = (M + WM_GEMM_TILE_TOKENS - 1) / WM_GEMM_TILE_TOKENS * WM_GEMM_TILE_TOKENS;
+    const uint32_t nce = E / I2S_CHUNK_COLS, ncf = F / I2S_CHUNK_COLS;
+    const float scale = 1.0f / sqrtf((float)c.head_dim);  // primitives.rs:354
+    uint32_t *err = m->dscalars + 2;
+    wm_launch_q6k_dequant_rows_dev(m->embd, m->embd_blocks, m->b_ids, M, m->b_hidden, E, s);
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        const dev_layer &L = m->layers[l];
+        // [hidden += down of the previous layer], attn_norm, int8
+        wm_norm_rows nr{m->b_hidden, E, l ? m->b_ydown : nullptr, E, nullptr, 0, L.attn_norm, E,
+                        c.rms_eps, m->b_act, m_pad, m->b_meta, nullptr, 0, l ? err : nullptr, l};
+        wm_launch_rmsnorm_rows(nr, M, s);
+        const wm_gemm_desc qkv[3] = {{L.q.w, L.q.n_groups, E, 0, L.q.scale},
+                                     {L.k.w, L.k.n_groups, KV, E, L.k.scale},
+                                     {L.v.w, L.v.n_groups, KV, E + KV, L.v.scale}};
+        wm_launch_i2s_gemm(qkv, 3, nce, m->b_act, M, m_pad, m->b_meta, m->b_yqkv, QKV, s);
+        wm_launch_qkv_rows(m->b_yqkv, QKV, m->rope_cos, m->rope_sin, m->b_tok, M, l, E, KV,
+                           c.head_dim, c.n_rot, m->b_q, s);
+        wm_launch_attn_rows(m->b_q, m->b_tok, M, n_max, l, c.n_kv_heads, c.head_dim, group, scale,
+                            m->b_attn, s);
+        nr = wm_norm_rows{m->b_attn, E, nullptr, 0, nullptr, 0, L.attn_sub_norm, E, c.rms_eps,
+                          m->b_act, m_pad, m->b_meta, nullptr, 0, nullptr, 0};
+        wm_launch_rmsnorm_rows(nr, M, s);
+        const wm_gemm_desc od = {L.o.w, L.o.n_groups, E, 0, L.o.scale};
+        wm_launch_i2s_gemm(&od, 1, nce, m->b_act, M, m_pad, m->b_meta, m->b_yo, E, s);
+        // hidden += wo, ffn_norm, int8
+        nr = wm_norm_rows{m->b_hidden, E, m->b_yo, E, nullptr, 0, L.ffn_norm, E, c.rms_eps,
+                          m->b_act, m_pad, m->b_meta, nullptr, 0, nullptr, 0};
+        wm_launch_rmsnorm_rows(nr, M, s);
+        const wm_gemm_desc gu[2] = {{L.gate.w, L.gate.n_groups, F, 0, L.gate.scale},
+                                    {L.up.w, L.up.n_groups, F, F, L.up.scale}};
+        wm_launch_i2s_gemm(gu, 2, nce, m->b_act, M, m_pad, m->b_meta, m->b_ygu, 2 * F, s);
+        // relu^2(gate) * up, ffn_sub_norm, int8
+        nr = wm_norm_rows{nullptr, 0, nullptr, 0, m->b_ygu, 2 * F, L.ffn_sub_norm, F, c.rms_eps,
+                          m->b_act, m_pad, m->b_meta, nullptr, 0, nullptr, 0};
+        wm_launch_rmsnorm_rows(nr, M, s);
+        const wm_gemm_desc dd = {L.down.w, L.down.n_groups, E, 0, L.down.scale};
+        wm_launch_i2s_gemm(&dd, 1, ncf, m->b_act, M, m_pad, m->b_meta, m->b_ydown, E, s);
+    }
+    // hidden += down of the last layer, output_norm (f32)
+    wm_norm_rows fin{m->b_hidden, E, m->b_ydown, E, nullptr, 0, m->output_norm, E, c.rms_eps,
+                     nullptr, m_pad, nullptr, m->b_final, E, err, c.n_layers};
+    wm_launch_rmsnorm_rows(fin, M, s);
+    if (next_tokens)
+        for (uint32_t i = 0; i < n_seqs; i++)
+            wm_launch_q6k_logits_argmax(m->embd, m->embd_blocks, c.vocab_size, m->embd_rowgroups,
+                                        m->b_final + (size_t)last[i] * E, m->logits, m->b_next + i,
+                                        m->lm_work, s);
+    WM_HIP(ctx, hipGetLastError());
+    uint32_t flag = 0;
+    WM_HIP(ctx, hipMemcpyAsync(&flag, err, 4, hipMemcpyDeviceToHost, s));
+    WM_HIP(ctx, hipStreamSynchronize(s));
+    if (flag) {
+        uint32_t zero = 0;
+        WM_HIP(ctx, hipMemcpyAsync(err, &zero, 4, hipMemcpyHostToDevice, s));
+        WM_HIP(ctx, hipStreamSynchronize(s));
+        return wm_set_error(ctx, WM_E_NONFINITE,
+                            "multi_token_forward: non-finite hidden after layer %u; no cache advanced",
+                            flag - 1);
+    }
+    if (last_hidden)
+        for (uint32_t i = 0; i < n_seqs; i++)
+            WM_HIP(ctx, hipMemcpyAsync(last_hidden + (size_t)i * E, m->b_final + (size_t)last[i] * E,
+                                       (size_t)E * 4, hipMemcpyDeviceToHost, s));
+    if (next_tokens)
+        WM_HIP(ctx, hipMemcpyAsync(next_tokens, m->b_next, n_seqs * 4, hipMemcpyDeviceToHost, s));
+    WM_HIP(ctx, hipStreamSynchronize(s));
+    for (uint32_t i = 0; i < n_seqs; i++) caches[i]->pos += n_new[i];
+    return WM_OK;
+}
 
 wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **out) {
     if (!ctx || !cfg || !out) return WM_E_ARG;
@@ -354,6 +535,7 @@ void wm_model_destroy(wm_model *m) {
     if (m->embd) hipFree(m->embd);
     if (m->output_norm) hipFree(m->output_norm);
     if (m->ws) hipFree(m->ws);
+    if (m->bws) hipFree(m->bws);
     delete m;
 }
 

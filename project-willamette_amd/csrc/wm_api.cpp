@@ -394,6 +394,55 @@ wm_status wm_bitlinear_i2s_matvec_f32_multi_dev(wm_ctx *ctx, const wm_tensor *co
     return WM_OK;
 }
 
+wm_status wm_bitlinear_i2s_matmul_f32_dev(wm_ctx *ctx, const wm_tensor *w, const float *d_x,
+                                          uint32_t m, float *d_y) {
+    wm_status st = check_i2s(ctx, w);
+    if (st) return st;
+    if (!d_x || !d_y || m == 0) return wm_set_error(ctx, WM_E_ARG, "bitlinear matmul: empty batch");
+    const uint32_t m_pad = (m + WM_GEMM_TILE_TOKENS - 1) / WM_GEMM_TILE_TOKENS * WM_GEMM_TILE_TOKENS;
+    const size_t act_bytes = align256((size_t)w->in_dim * m_pad);
+    void *scratch;
+    if ((st = wm_ctx_scratch(ctx, act_bytes + align256((size_t)m * sizeof(wm_act_meta)), &scratch)))
+        return st;
+    uint8_t *act = (uint8_t *)scratch;
+    wm_act_meta *meta = (wm_act_meta *)(act + act_bytes);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    wm_launch_quantize_rows(d_x, (uint32_t)w->in_dim, (uint32_t)w->in_dim, m, m_pad, act, meta,
+                            ctx->stream);
+    wm_gemm_desc d{(const uint8_t *)w->d, w->n_groups, (uint32_t)w->out_dim, 0, w->scale};
+    wm_launch_i2s_gemm(&d, 1, w->n_chunks, act, m, m_pad, meta, d_y, (uint32_t)w->out_dim,
+                       ctx->stream);
+    WM_HIP(ctx, hipGetLastError());
+    return WM_OK;
+}
+
+wm_status wm_bitlinear_i2s_matmul_f32(wm_ctx *ctx, const wm_tensor *w, const float *x,
+                                      size_t x_len, uint32_t m, float *y, size_t y_len) {
+    wm_status st = check_i2s(ctx, w);
+    if (st) return st;
+    if (!x || !y || m == 0) return wm_set_error(ctx, WM_E_ARG, "bitlinear matmul: empty batch");
+    if (x_len != (size_t)m * w->in_dim)
+        return wm_set_error(ctx, WM_E_SHAPE, "bitlinear_i2s_matmul: input.len()=%zu != %u x in_dim=%llu",
+                            x_len, m, (unsigned long long)w->in_dim);
+    if (y_len != (size_t)m * w->out_dim)
+        return wm_set_error(ctx, WM_E_SHAPE, "bitlinear_i2s_matmul: output.len()=%zu != %u x out_dim=%llu",
+                            y_len, m, (unsigned long long)w->out_dim);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    void *dx = nullptr, *dy = nullptr;
+    WM_HIP(ctx, hipMalloc(&dx, x_len * 4));
+    hipError_t e = hipMalloc(&dy, y_len * 4);
+    if (e == hipSuccess) e = hipMemcpyAsync(dx, x, x_len * 4, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) {
+        st = wm_bitlinear_i2s_matmul_f32_dev(ctx, w, (const float *)dx, m, (float *)dy);
+        if (st == WM_OK) e = hipMemcpyAsync(y, dy, y_len * 4, hipMemcpyDeviceToHost, ctx->stream);
+        if (st == WM_OK && e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    }
+    hipFree(dx);
+    if (dy) hipFree(dy);
+    if (e != hipSuccess) return wm_hip_error(ctx, e, "bitlinear_i2s_matmul");
+    return st;
+}
+
 // ---------------------------------------------------------------------------
 // Q6_K
 // ---------------------------------------------------------------------------

@@ -155,6 +155,25 @@ __device__ __forceinline__ int wm_block_sum_i32(int v, int *red) {
     return t;
 }
 
+// KV quantisation of one token vector (src/model/kv_cache.rs:245-259), by
+// the whole workgroup: absmax (NaN never raises it); a zero or non-finite
+// absmax stores zeros with scale 0.
+__device__ inline void wm_kv_quantise_store(const float *__restrict__ v, uint32_t n,
+                                            int8_t *__restrict__ q, float *__restrict__ scale_out,
+                                            float *red) {
+    float m = 0.0f;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) m = wm_max_nonan(m, fabsf(v[i]));
+    const float absmax = wm_block_max_nonan(m, red);
+    if (absmax == 0.0f || !isfinite(absmax)) {
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) q[i] = 0;
+        if (threadIdx.x == 0) *scale_out = 0.0f;
+        return;
+    }
+    const float inv = 127.0f / absmax;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) q[i] = (int8_t)wm_round_clamp_i8(v[i] * inv);
+    if (threadIdx.x == 0) *scale_out = absmax / 127.0f;
+}
+
 // Position of activation element i (0 <= i < in_dim) in the chunk-permuted
 // layout the I2_S matvec reads: chunk c = 16-byte weight chunk index along
 // the row, 64 bytes per chunk ordered [quarter k][gp].
@@ -209,9 +228,74 @@ void wm_launch_q6k_dequant_row(const uint8_t *w, uint32_t n_blocks, uint32_t row
                                hipStream_t s);
 void wm_launch_q6k_dequant_row_dev(const uint8_t *w, uint32_t n_blocks, const uint32_t *d_row,
                                    float *out, hipStream_t s);
+// n_rows rows, row i = d_rows[i], written to out + i * ld
+void wm_launch_q6k_dequant_rows_dev(const uint8_t *w, uint32_t n_blocks, const uint32_t *d_rows,
+                                    uint32_t n_rows, float *out, uint32_t ld, hipStream_t s);
 // logits (exact SSE2 order) + per-block argmax candidates + final argmax.
 void wm_launch_q6k_logits_argmax(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                                  uint32_t n_rowgroups, const float *hidden, float *logits,
                                  uint32_t *argmax_out, void *work, hipStream_t s);
 size_t wm_q6k_logits_work_bytes();
+
+// ---------------------------------------------------------------------------
+// ragged multi-sequence batch
+// ---------------------------------------------------------------------------
+
+// Per-token record: the token's sequence cache and its position in it.
+struct wm_batch_tok {
+    int8_t *k, *v;   // codes [layer][max_seq][kv_dim]
+    float *ks, *vs;  // scales [layer][max_seq]
+    uint32_t max_seq, pos;
+};
+
+// Activation layout of the batched I2_S GEMM: per 64-column chunk c (the
+// columns one 16-byte weight chunk covers), all tokens' 64 bytes, each
+// ordered [dword j of the weight chunk][quarter q][byte g], so that the 16
+// bytes one MFMA lane needs for weight dword j are contiguous.
+__host__ __device__ __forceinline__ uint64_t wm_gemm_act_offset(uint32_t i, uint32_t t,
+                                                                uint32_t m_pad) {
+    const uint32_t bk = i >> 7, rem = i & 127u, q = rem >> 5, r32 = rem & 31u;
+    const uint32_t half = r32 >> 4, gp = r32 & 15u;
+    const uint32_t c = bk * 2 + half, j = gp >> 2, g = gp & 3u;
+    return ((uint64_t)c * m_pad + t) * 64 + j * 16 + q * 4 + g;
+}
+
+#define WM_GEMM_MAX_DESC 4
+#define WM_GEMM_TILE_TOKENS 64
+struct wm_gemm_desc {
+    const uint8_t *w;   // library I2_S layout
+    uint32_t n_groups;  // 64-row groups
+    uint32_t out_dim;   // rows written (the tail of the last group is padding)
+    uint32_t out_row0;  // first output column of this tensor in y
+    float scale;        // per-tensor weight scale
+};
+// y[t * ldy + out_row0 + r] = (scale * meta[t].scale) * (Σ_k code·act - meta[t].asum)
+void wm_launch_i2s_gemm(const wm_gemm_desc *d, int n_desc, uint32_t n_chunks, const uint8_t *act,
+                        uint32_t m, uint32_t m_pad, const wm_act_meta *meta, float *y,
+                        uint32_t ldy, hipStream_t s);
+// Per-row absmax int8 of x[t * ldx + 0..n) into the GEMM layout + meta[t].
+void wm_launch_quantize_rows(const float *x, uint32_t ldx, uint32_t n, uint32_t m, uint32_t m_pad,
+                             uint8_t *act, wm_act_meta *meta, hipStream_t s);
+// RMSNorm per row.  Source: x[t] (+ res[t], written back to x) or, with gu,
+// relu(gu[t][j])^2 * gu[t][n + j].  Output: act/meta (quantised) or y_out.
+struct wm_norm_rows {
+    float *x; uint32_t ldx;
+    const float *res; uint32_t ldr;
+    const float *gu; uint32_t ldgu;
+    const float *w; uint32_t n; float eps;
+    uint8_t *act; uint32_t m_pad; wm_act_meta *meta;
+    float *y_out; uint32_t ldo;
+    uint32_t *err_flag; uint32_t tag;
+};
+void wm_launch_rmsnorm_rows(const wm_norm_rows &a, uint32_t m, hipStream_t s);
+// RoPE + K/V append per token of a batch for one layer.
+void wm_launch_qkv_rows(const float *y, uint32_t ldy, const float *rope_cos, const float *rope_sin,
+                        const wm_batch_tok *tok, uint32_t m, uint32_t layer, uint32_t n_q,
+                        uint32_t n_kv, uint32_t head_dim, uint32_t n_rot, float *q_out,
+                        hipStream_t s);
+// Causal GQA attention of every token of a batch over its own sequence cache.
+bool wm_attn_rows_supported(uint32_t head_dim, uint32_t group);
+void wm_launch_attn_rows(const float *q, const wm_batch_tok *tok, uint32_t m, uint32_t n_max,
+                         uint32_t layer, uint32_t n_kv_heads, uint32_t head_dim, uint32_t group,
+                         float scale, float *out, hipStream_t s);
 void wm_launch_debug_seq_sum(const float *a, uint32_t n, float *out, hipStream_t s);

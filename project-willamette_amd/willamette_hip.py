@@ -108,6 +108,9 @@ EXPORTS = {
                                           C.c_size_t, _i8p, _f32p, _i32p),
     "wm_bitlinear_i2s_matvec_f32_dev": (C.c_int, _vp, _vp, _vp, _vp),
     "wm_bitlinear_i2s_matvec_f32_multi_dev": (C.c_int, _vp, C.POINTER(_vp), C.c_uint32, _vp, _vp),
+    "wm_bitlinear_i2s_matmul_f32_dev": (C.c_int, _vp, _vp, _vp, C.c_uint32, _vp),
+    "wm_bitlinear_i2s_matmul_f32": (C.c_int, _vp, _vp, _f32p, C.c_size_t, C.c_uint32, _f32p,
+                                    C.c_size_t),
     "wm_q6k_dequantize_row": (C.c_int, _vp, _vp, C.c_uint64, _f32p, C.c_size_t),
     "wm_compute_logits": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p, C.c_size_t),
     "wm_logits_argmax": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p, _u32p),
@@ -129,6 +132,7 @@ EXPORTS = {
     "wm_decode_step": (C.c_int, _vp, _vp, C.c_uint32, C.c_uint32, _f32p, _f32p, _u32p),
     "wm_greedy_generate": (C.c_int, _vp, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_int64, _u32p,
                            _u32p),
+    "wm_batch_forward": (C.c_int, _vp, C.POINTER(_vp), C.c_uint32, _u32p, _u32p, _f32p, _u32p),
     "wm_debug_seq_sum": (C.c_int, _vp, _f32p, C.c_size_t, _f32p),
     "wm_synth_stream_seed": (C.c_uint64, C.c_uint64, C.c_uint64),
     "wm_synth_i2s": (None, C.c_uint64, C.c_uint64, _u8p, C.c_size_t),
@@ -336,6 +340,17 @@ def bitlinear_i2s_matvec_f32(ctx: Context, w: Tensor, x: np.ndarray, debug: bool
                                                     _ptr(y, C.c_float), y.size, _ptr(act, C.c_int8),
                                                     C.byref(sc), _ptr(acc, C.c_int32)))
     return y, act, float(np.float32(sc.value)), acc
+
+
+def bitlinear_i2s_matmul_f32(ctx: Context, w: Tensor, x: np.ndarray) -> np.ndarray:
+    """Rows of x (m x in_dim) through the batched BitLinear: row r equals
+    bitlinear_i2s_matvec_f32 on x[r]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = x.shape[0]
+    y = np.empty((m, w.shape[1]), dtype=np.float32)
+    ctx.check(lib.wm_bitlinear_i2s_matmul_f32(ctx.h, w.h, _ptr(x, C.c_float), x.size, m,
+                                              _ptr(y, C.c_float), y.size))
+    return y
 
 
 def debug_seq_sum(ctx: Context, values: np.ndarray) -> np.float32:
