@@ -115,6 +115,76 @@ def i2s_stream(ctx, wh, copies: int, reps: int):
     return ms, per_matvec * copies
 
 
+INT8_MFMA_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
+
+
+def ragged_batch(ctx, wh, bs, dev, cfg, steps: int):
+    """Continuous-batching step: 16 sequences with contexts ~U[128, 4064]
+    (pre-filled with N(0,1) K/V through the int8 KV quantiser) append
+    ~U[1, 32] new tokens each in one wm_batch_forward call.  Also times the
+    batched BitLinear (per-row int8 quantiser + int8 MFMA GEMM) at the
+    three BitNet-2B GEMM shapes with M = the batch's token count."""
+    rng = np.random.default_rng(bs.master_seed(5))
+    n_seq = 16
+    ctxs = [int(c) for c in rng.integers(128, 4064 + 1, n_seq)]
+    news = [int(n) for n in rng.integers(1, 32 + 1, n_seq)]
+    seqs = [[int(t) for t in rng.integers(0, cfg.vocab, n)] for n in news]
+    kvs = []
+    for i, c in enumerate(ctxs):
+        kv = dev.kv_cache(cfg.context_length)
+        k, v = bs.kv_prefill(cfg, bs.master_seed(5) + 1 + i, c)
+        kv.append_positions(k, v)
+        del k, v
+        kvs.append(kv)
+    m_tok = sum(news)
+    log(f"ragged batch: {n_seq} sequences, contexts {min(ctxs)}..{max(ctxs)}, {m_tok} new tokens")
+
+    def step():
+        out = dev.batch_forward(kvs, seqs, want_hidden=False, want_next=True)
+        for kv, c in zip(kvs, ctxs):
+            kv.rollback(c)
+        return out
+
+    step()
+    timer = HipTimer(ctx.stream)
+    t0 = time.perf_counter()
+    timer.start()
+    for _ in range(steps):
+        _, nxt = step()
+    ev_ms = timer.stop_ms() / steps
+    wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
+    for kv in kvs:
+        kv.close()
+    # batched BitLinear alone, M = m_tok rows
+    gemm = {}
+    seed = bs.master_seed(5)
+    for name, in_dim, out_dim in (("2560x2560", 2560, 2560), ("6912x2560", 2560, 6912),
+                                  ("2560x6912", 6912, 2560)):
+        w = ctx.upload_i2s(wh.synth_i2s(seed, 9, in_dim, out_dim), 1.25, in_dim, out_dim)
+        x = ctx.to_device(wh.synth_normal(seed, 10, m_tok * in_dim))
+        y = ctx.alloc(m_tok * out_dim * 4)
+        run = lambda: ctx.check(wh.lib.wm_bitlinear_i2s_matmul_f32_dev(ctx.h, w.h, x.ptr, m_tok, y.ptr))
+        for _ in range(3):
+            run()
+        reps = 50
+        timer.start()
+        for _ in range(reps):
+            run()
+        us = timer.stop_ms() * 1000.0 / reps
+        tops = 2.0 * m_tok * in_dim * out_dim / (us * 1e-6) / 1e12
+        gemm[name] = {"us": round(us, 2), "tops": round(tops, 2),
+                      "frac_int8_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4)}
+        w.close()
+        x.free()
+        y.free()
+    return {"sequences": n_seq, "new_tokens": m_tok, "context_min": min(ctxs),
+            "context_max": max(ctxs), "ms_per_step": round(wall_ms, 3),
+            "gpu_event_ms_per_step": round(ev_ms, 3),
+            "tokens_per_s": round(m_tok / (wall_ms / 1000.0), 1),
+            "next_token_checksum": int(np.bitwise_xor.reduce(np.array(nxt, np.uint64))),
+            "bitlinear_gemm_incl_row_quantiser": gemm}
+
+
 def cpu_baseline(hm, cfg, n_tokens: int, threads: int):
     """The oracle (C restatement of the reference's x86 SSE2 path) on this
     host: BitLinear single-threaded, lm-head rows over `threads` threads
@@ -214,6 +284,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-batch", action="store_true", help="skip the ragged-batch measurement")
+    ap.add_argument("--batch-steps", type=int, default=5)
     ap.add_argument("--probe", choices=["lm_head", "i2s"],
                     help="only run one kernel (and a calibration copy) for counter passes")
     ap.add_argument("--probe-reps", type=int, default=5)
@@ -265,6 +337,11 @@ def main():
     mv_gbps = mv_bytes / (mv_ms / 1000.0) / 1e9
     log(f"i2_s 2560x2560 x{copies}: {mv_ms * 1000 / copies:.2f} us/matvec, {mv_gbps:.0f} GB/s")
 
+    batch = None
+    if not args.no_batch:
+        batch = ragged_batch(ctx, wh, bs, dev, cfg, args.batch_steps)
+        log(f"ragged batch: {batch['tokens_per_s']} tok/s, {batch['ms_per_step']} ms/step")
+
     wb = cfg.weight_bytes()
     kv_read = sum(cfg.n_layers * (p + 1) * cfg.kv_dim * 2 * 1 + cfg.n_layers * (p + 1) * 8
                   for p in range(PREFILL, PREFILL + args.steps)) / args.steps
@@ -309,6 +386,7 @@ def main():
                                       "us_per_matvec": round(mv_ms * 1000 / copies, 3),
                                       "copies": copies},
         },
+        "ragged_batch": batch,
         "decode_effective_gbps": round(decode_gbps, 1),
         "gpu_event_ms_per_token": round(gpu_ms / args.steps, 4),
         "token_checksum": int(np.bitwise_xor.reduce(np.array(ids, np.uint64))),

@@ -309,154 +309,153 @@ __global__ __launch_bounds__(256) void k_qkv_rows(qkv_rows_args a) {
 }
 
 // ---------------------------------------------------------------------------
-// causal GQA attention per (kv head, token) over the token's own sequence
-// (cached_forward.rs:417-449, attention.rs:45-73)
+// causal GQA attention of every token over its own sequence
+// (cached_forward.rs:417-449, attention.rs:45-73), in two kernels
 // ---------------------------------------------------------------------------
 //
-// The G query heads of one KV head share a workgroup, so each K and V row
-// is read once for all of them.  Per head:
-//   scores: one thread per position, the 128-term dot in order (k = q8·s);
-//   softmax: max, exp (glibc expf), exact sequential Σ, * (1/Σ);
-//   output: 32 threads per head, each owning HD/32 dims, Σ_p w_p·v_p[d] in
-//   position order.
+// Scores: one thread per (position, KV head) computes the G query heads'
+// 128-term dots from one K row, each in order with k = q8 * scale, then
+// * (1/sqrt(head_dim)), into scores[t][h][p].
+// Softmax + V: one workgroup per (token, head): max, exp (glibc expf), exact
+// sequential sum, * (1/sum), then one thread per output dimension runs
+// Σ_p w_p * v_p[d] in position order.
 struct attn_rows_args {
     const float *q;  // [t][n_heads * head_dim]
     const wm_batch_tok *tok;
+    float *scores;   // [t][n_heads][score_stride]
     float *out;      // [t][n_heads * head_dim]
-    uint32_t layer, kv_dim, n_max;
+    uint32_t layer, kv_dim, n_heads, score_stride, n_max;
     float scale;
 };
 
-constexpr int kAttnThreads = 128;
+constexpr int kScoreThreads = 256;
 
 template <int HD, int G>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_rows(attn_rows_args a) {
-    constexpr int DPT = HD / 32;  // dims per thread in the output phase
-    extern __shared__ __align__(16) float sm[];
-    __shared__ uint64_t exp_tab[32];
-    __shared__ float red[2];
-    __shared__ float s_max[G], s_inv[G];
-    __shared__ int s_mode[G];
-    const uint32_t kvh = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+__global__ __launch_bounds__(kScoreThreads) void k_attn_scores_rows(attn_rows_args a) {
+    __shared__ float qs[G * HD];
+    const uint32_t kvh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
     const wm_batch_tok tk = a.tok[t];
     const uint32_t n = tk.pos + 1;
-    const uint32_t npad = wm::seq_sum_padded(a.n_max);
-    float *qs = sm;           // [G][HD]
-    float *w = qs + G * HD;   // [G][npad]
+    const uint32_t p0 = blockIdx.x * kScoreThreads;
+    if (p0 >= n) return;  // the whole block lies past this token's context
+    const float *qsrc = a.q + (uint64_t)t * a.n_heads * HD + (uint64_t)kvh * G * HD;
+    for (uint32_t i = tid; i < (uint32_t)(G * HD); i += kScoreThreads) qs[i] = qsrc[i];
+    __syncthreads();
+    const uint32_t p = p0 + tid;
+    if (p >= n) return;
     const uint64_t lay = (uint64_t)a.layer * tk.max_seq;
-    const int8_t *kc = tk.k + lay * a.kv_dim + kvh * HD;
-    const int8_t *vc = tk.v + lay * a.kv_dim + kvh * HD;
-    const float *ksc = tk.ks + lay, *vsc = tk.vs + lay;
-    const float *qsrc = a.q + (uint64_t)t * (a.kv_dim / HD) * G * HD + (uint64_t)kvh * G * HD;
-    for (uint32_t i = tid; i < (uint32_t)(G * HD); i += kAttnThreads) qs[i] = qsrc[i];
+    const int8_t *kp = tk.k + (lay + p) * a.kv_dim + kvh * HD;
+    int4 raw[HD / 16];
+#pragma unroll
+    for (int b = 0; b < HD / 16; b++) raw[b] = *reinterpret_cast<const int4 *>(kp + b * 16);
+    const float kscale = tk.ks[lay + p];
+    float s[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) s[h] = 0.0f;
+#pragma unroll
+    for (int b = 0; b < HD / 16; b++) {
+        const uint32_t wd[4] = {(uint32_t)raw[b].x, (uint32_t)raw[b].y, (uint32_t)raw[b].z,
+                                (uint32_t)raw[b].w};
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const float kd = (float)(int8_t)(wd[e >> 2] >> (8 * (e & 3))) * kscale;  // read_into
+#pragma unroll
+            for (int h = 0; h < G; h++) s[h] = s[h] + qs[h * HD + b * 16 + e] * kd;
+        }
+    }
+    float *dst = a.scores + ((uint64_t)t * a.n_heads + kvh * G) * a.score_stride + p;
+#pragma unroll
+    for (int h = 0; h < G; h++) dst[(uint64_t)h * a.score_stride] = s[h] * a.scale;
+}
+
+constexpr int kVTile = 64;  // V rows per LDS tile
+
+template <int HD>
+__global__ __launch_bounds__(HD) void k_attn_softmax_v_rows(attn_rows_args a) {
+    // LDS: weights [seq_sum_padded(n_max)] | V tile [kVTile][HD] bytes | V scales [kVTile]
+    extern __shared__ __align__(16) float wts[];
+    __shared__ uint64_t exp_tab[32];
+    __shared__ float red[2];
+    __shared__ float s_inv;
+    __shared__ int s_mode;
+    const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const uint32_t group = a.n_heads / (a.kv_dim / HD), kvh = h / group;
+    const wm_batch_tok tk = a.tok[t];
+    const uint32_t n = tk.pos + 1;
+    int8_t *vt = reinterpret_cast<int8_t *>(wts + wm::seq_sum_padded(a.n_max));
+    float *st = reinterpret_cast<float *>(vt + kVTile * HD);
+    const float *sc = a.scores + ((uint64_t)t * a.n_heads + h) * a.score_stride;
     if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
+    float m = -INFINITY;
+    for (uint32_t p = tid; p < n; p += HD) {
+        const float v = sc[p];
+        wts[p] = v;
+        m = wm_max_nonan(m, v);
+    }
+    m = wm_wave_max_nonan(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
-    // 1. scores
-    float lmax[G];
-#pragma unroll
-    for (int h = 0; h < G; h++) lmax[h] = -INFINITY;
-    for (uint32_t p = tid; p < n; p += kAttnThreads) {
-        int4 raw[HD / 16];
-#pragma unroll
-        for (int b = 0; b < HD / 16; b++)
-            raw[b] = *reinterpret_cast<const int4 *>(kc + (uint64_t)p * a.kv_dim + b * 16);
-        const float kscale = ksc[p];
-        float s[G];
-#pragma unroll
-        for (int h = 0; h < G; h++) s[h] = 0.0f;
-#pragma unroll
-        for (int b = 0; b < HD / 16; b++) {
-            const uint32_t wd[4] = {(uint32_t)raw[b].x, (uint32_t)raw[b].y, (uint32_t)raw[b].z,
-                                    (uint32_t)raw[b].w};
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const float kd = (float)(int8_t)(wd[e >> 2] >> (8 * (e & 3))) * kscale;
-#pragma unroll
-                for (int h = 0; h < G; h++) s[h] = s[h] + qs[h * HD + b * 16 + e] * kd;
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            const float v = s[h] * a.scale;
-            w[h * npad + p] = v;
-            lmax[h] = wm_max_nonan(lmax[h], v);
+    const float mx = HD > 64 ? wm_max_nonan(red[0], red[1]) : red[0];
+    float *out = a.out + (uint64_t)t * a.n_heads * HD + (uint64_t)h * HD;
+    if (!isfinite(mx)) {  // every weight is 0 or NaN: the output stays 0
+        out[tid] = 0.0f;
+        return;
+    }
+    for (uint32_t p = tid; p < n; p += HD) wts[p] = wm::expf_glibc(wts[p] - mx, exp_tab);
+    __syncthreads();
+    if (tid < 64) {
+        const float sum = wm::seq_sum_nonneg(wts, n);
+        if (tid == 0) {
+            s_mode = sum > 0.0f;
+            s_inv = 1.0f / sum;
         }
     }
-    // 2. softmax per head
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        float mh = wm_wave_max_nonan(lmax[h]);
+    __syncthreads();
+    if (s_mode) {
+        const float inv = s_inv;
+        for (uint32_t p = tid; p < n; p += HD) wts[p] = wts[p] * inv;
+    }
+    // V rows of this KV head go through LDS a tile at a time: every thread
+    // loads 16-byte pieces (all in flight together, the next tile's while the
+    // current one is consumed), then thread d runs its chain from LDS.
+    const uint64_t lay = (uint64_t)a.layer * tk.max_seq;
+    const int8_t *vg = tk.v + lay * a.kv_dim + kvh * HD;
+    const float *vsg = tk.vs + lay;
+    // Tile rows p0 .. p0+63, indices clamped to n-1 so every load is in range
+    // and unconditional: thread tid takes 16-byte pieces tid, tid+HD, tid+2HD,
+    // tid+3HD (piece = row * HD/16 + column) and threads < 64 one scale each.
+    constexpr uint32_t kPR = HD / 16;  // pieces per row
+    const uint32_t r0 = tid / kPR, c0 = (tid % kPR) * 16, rstep = HD / kPR;
+    int4 pre0, pre1, pre2, pre3;
+    float spre = 0.0f;
+#define WM_FETCH_V(P0)                                                                       \
+    do {                                                                                     \
+        const uint32_t q0 = (P0) + r0;                                                       \
+        pre0 = *reinterpret_cast<const int4 *>(vg + (uint64_t)min(q0, n - 1) * a.kv_dim + c0); \
+        pre1 = *reinterpret_cast<const int4 *>(vg + (uint64_t)min(q0 + rstep, n - 1) * a.kv_dim + c0); \
+        pre2 = *reinterpret_cast<const int4 *>(vg + (uint64_t)min(q0 + 2 * rstep, n - 1) * a.kv_dim + c0); \
+        pre3 = *reinterpret_cast<const int4 *>(vg + (uint64_t)min(q0 + 3 * rstep, n - 1) * a.kv_dim + c0); \
+        if (tid < (uint32_t)kVTile) spre = vsg[min((P0) + tid, n - 1)];                       \
+    } while (0)
+    WM_FETCH_V(0u);
+    float acc = 0.0f;
+    for (uint32_t p0 = 0; p0 < n; p0 += kVTile) {
+        __syncthreads();  // previous tile consumed (and, first time, the weights written)
+        int4 *vt4 = reinterpret_cast<int4 *>(vt);
+        vt4[tid] = pre0;
+        vt4[tid + HD] = pre1;
+        vt4[tid + 2 * HD] = pre2;
+        vt4[tid + 3 * HD] = pre3;
+        if (tid < (uint32_t)kVTile) st[tid] = spre;
         __syncthreads();
-        if ((tid & 63) == 0) red[tid >> 6] = mh;
-        __syncthreads();
-        if (tid == 0) s_max[h] = wm_max_nonan(red[0], red[1]);
+        WM_FETCH_V(p0 + kVTile);  // next tile; past the end the clamped rows re-read row n-1
+        const uint32_t tn = n - p0 < (uint32_t)kVTile ? n - p0 : (uint32_t)kVTile;
+        const float *wp = wts + p0;
+        for (uint32_t q = 0; q < tn; q++)
+            acc = acc + wp[q] * ((float)vt[q * HD + tid] * st[q]);  // w * (q8 * scale)
     }
-    __syncthreads();
-    for (uint32_t i = tid; i < (uint32_t)G * n; i += kAttnThreads) {
-        const uint32_t h = i / n, p = i - h * n;
-        const float mx = s_max[h];
-        if (isfinite(mx)) w[h * npad + p] = wm::expf_glibc(w[h * npad + p] - mx, exp_tab);
-    }
-    __syncthreads();
-    for (int h = (int)(tid >> 6); h < G; h += 2) {
-        if (!isfinite(s_max[h])) continue;
-        const float sum = wm::seq_sum_nonneg(w + h * npad, n);
-        if ((tid & 63) == 0) {
-            s_mode[h] = sum > 0.0f;
-            s_inv[h] = 1.0f / sum;
-        }
-    }
-    __syncthreads();
-    for (uint32_t i = tid; i < (uint32_t)G * n; i += kAttnThreads) {
-        const uint32_t h = i / n, p = i - h * n;
-        if (isfinite(s_max[h]) && s_mode[h]) w[h * npad + p] = w[h * npad + p] * s_inv[h];
-    }
-    __syncthreads();
-    // 3. out_h[d] = Σ_p w_p * v_p[d]
-    float *out = a.out + (uint64_t)t * (a.kv_dim / HD) * G * HD + (uint64_t)kvh * G * HD;
-    for (int h = (int)(tid >> 5); h < G; h += kAttnThreads / 32) {
-        const uint32_t d0 = (tid & 31) * DPT;
-        float acc[DPT];
-#pragma unroll
-        for (int e = 0; e < DPT; e++) acc[e] = 0.0f;
-        if (isfinite(s_max[h])) {
-            const float *wh = w + h * npad;
-            uint32_t p = 0;
-            for (; p + 8 <= n; p += 8) {
-                uint32_t vr[8];
-                float vs8[8];
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const int8_t *src = vc + (uint64_t)(p + u) * a.kv_dim + d0;
-                    vr[u] = DPT == 4 ? *reinterpret_cast<const uint32_t *>(src)
-                                     : (uint32_t)*reinterpret_cast<const uint16_t *>(src);
-                    vs8[u] = vsc[p + u];
-                }
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const float wp = wh[p + u];
-#pragma unroll
-                    for (int e = 0; e < DPT; e++) {
-                        const float vd = (float)(int8_t)(vr[u] >> (8 * e)) * vs8[u];  // read_into
-                        acc[e] = acc[e] + wp * vd;
-                    }
-                }
-            }
-            for (; p < n; p++) {
-                const int8_t *src = vc + (uint64_t)p * a.kv_dim + d0;
-                const uint32_t vv = DPT == 4 ? *reinterpret_cast<const uint32_t *>(src)
-                                             : (uint32_t)*reinterpret_cast<const uint16_t *>(src);
-                const float s = vsc[p], wp = wh[p];
-#pragma unroll
-                for (int e = 0; e < DPT; e++) {
-                    const float vd = (float)(int8_t)(vv >> (8 * e)) * s;
-                    acc[e] = acc[e] + wp * vd;
-                }
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < DPT; e++) out[h * HD + d0 + e] = acc[e];
-    }
+    out[tid] = acc;
+#undef WM_FETCH_V
 }
 
 }  // namespace
@@ -524,18 +523,27 @@ bool wm_attn_rows_supported(uint32_t head_dim, uint32_t group) {
            (group == 1 || group == 2 || group == 4 || group == 8);
 }
 
+size_t wm_attn_rows_scores_bytes(uint32_t m, uint32_t n_heads, uint32_t n_max) {
+    return (size_t)m * n_heads * ((n_max + 3u) & ~3u) * sizeof(float);
+}
+
 void wm_launch_attn_rows(const float *q, const wm_batch_tok *tok, uint32_t m, uint32_t n_max,
                          uint32_t layer, uint32_t n_kv_heads, uint32_t head_dim, uint32_t group,
-                         float scale, float *out, hipStream_t s) {
-    attn_rows_args a{q, tok, out, layer, n_kv_heads * head_dim, n_max, scale};
-    const size_t lds = (size_t)group * (head_dim + wm::seq_sum_padded(n_max)) * sizeof(float);
-    const dim3 grid(n_kv_heads, m), block(kAttnThreads);
-#define WM_ATTN_CASE(HD, G)                                                                    \
-    if (head_dim == HD && group == G) {                                                        \
-        hipLaunchKernelGGL((k_attn_rows<HD, G>), grid, block, lds, s, a);                      \
-        return;                                                                                \
-    }
-    WM_ATTN_CASE(128, 1) WM_ATTN_CASE(128, 2) WM_ATTN_CASE(128, 4) WM_ATTN_CASE(128, 8)
-    WM_ATTN_CASE(64, 1) WM_ATTN_CASE(64, 2) WM_ATTN_CASE(64, 4) WM_ATTN_CASE(64, 8)
-#undef WM_ATTN_CASE
+                         float scale, float *scores, float *out, hipStream_t s) {
+    const uint32_t n_heads = n_kv_heads * group;
+    attn_rows_args a{q, tok, scores, out, layer, n_kv_heads * head_dim, n_heads,
+                     (n_max + 3u) & ~3u, n_max, scale};
+    const dim3 sgrid((n_max + kScoreThreads - 1) / kScoreThreads, n_kv_heads, m);
+#define WM_SCORES_CASE(HD, G)                                                                  \
+    if (head_dim == HD && group == G)                                                          \
+        hipLaunchKernelGGL((k_attn_scores_rows<HD, G>), sgrid, dim3(kScoreThreads), 0, s, a);
+    WM_SCORES_CASE(128, 1) WM_SCORES_CASE(128, 2) WM_SCORES_CASE(128, 4) WM_SCORES_CASE(128, 8)
+    WM_SCORES_CASE(64, 1) WM_SCORES_CASE(64, 2) WM_SCORES_CASE(64, 4) WM_SCORES_CASE(64, 8)
+#undef WM_SCORES_CASE
+    const size_t lds = (size_t)wm::seq_sum_padded(n_max) * sizeof(float) +
+                       (size_t)kVTile * head_dim + kVTile * sizeof(float);
+    if (head_dim == 128)
+        hipLaunchKernelGGL(k_attn_softmax_v_rows<128>, dim3(n_heads, m), dim3(128), lds, s, a);
+    else
+        hipLaunchKernelGGL(k_attn_softmax_v_rows<64>, dim3(n_heads, m), dim3(64), lds, s, a);
 }

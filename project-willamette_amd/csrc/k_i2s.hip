@@ -103,6 +103,7 @@ struct i2s_multi {
     const uint8_t *w[WM_I2S_MAX_MULTI];
     uint32_t group_end[WM_I2S_MAX_MULTI];  // cumulative group counts
     int n;
+    uint32_t uniform_groups;  // every tensor has this many groups (0: they differ)
 };
 
 __device__ __forceinline__ void dot_chunk(const uint4 wv, const int *__restrict__ a,
@@ -118,41 +119,84 @@ __device__ __forceinline__ void dot_chunk(const uint4 wv, const int *__restrict_
     }
 }
 
-// grid: x = global group index over all tensors, y = K split.  One wave.
+// grid: x = (global group index over all tensors) / RG, y = K split.  One
+// wave, owning RG consecutive 64-row groups of one tensor: lane r computes
+// row r of each.  The wave's slice of the activation vector is staged in LDS
+// once; every activation read (a uniform broadcast) then serves RG weight
+// chunks.  Weights stream in rounds of 4 x RG 1 KiB loads, the next round in
+// flight while the current one is reduced; chunk indices past the slice are
+// clamped to its last chunk, so every load is in range and unconditional.
+template <int RG>
 __global__ __launch_bounds__(64) void k_i2s_partial(i2s_multi m, uint32_t n_chunks,
                                                     const int *__restrict__ act,
                                                     int32_t *__restrict__ partial,
                                                     uint32_t rows_total) {
-    const uint32_t gg = blockIdx.x;
+    extern __shared__ __align__(16) int act_s[];  // chunks c0..c1-1, 16 ints each
+    const uint32_t gg = blockIdx.x * RG;  // first global group of this wave
     int t = 0;
-    if (m.n > 1) {  // binary search over the cumulative group counts (uniform)
+    uint32_t g = gg;
+    if (m.uniform_groups) {
+        t = (int)(gg / m.uniform_groups);
+        g = gg - (uint32_t)t * m.uniform_groups;
+    } else if (m.n > 1) {  // binary search over the cumulative group counts (uniform)
         int lo = 0, hi = m.n - 1;
         while (lo < hi) {
             int mid = (lo + hi) >> 1;
             if (gg < m.group_end[mid]) hi = mid; else lo = mid + 1;
         }
         t = lo;
+        g = gg - (t ? m.group_end[t - 1] : 0);
     }
-    const uint32_t g = gg - (t ? m.group_end[t - 1] : 0);
     const uint4 *__restrict__ W = reinterpret_cast<const uint4 *>(m.w[t]);
     const uint32_t split = gridDim.y, s = blockIdx.y;
     const uint32_t c0 = (uint32_t)(((uint64_t)n_chunks * s) / split);
     const uint32_t c1 = (uint32_t)(((uint64_t)n_chunks * (s + 1)) / split);
-    const uint32_t r = threadIdx.x;
-    const uint4 *wp = W + ((uint64_t)g * n_chunks) * I2S_GROUP_ROWS + r;
-    int acc16 = 0, acc4 = 0, acc1 = 0;
-    uint32_t c = c0;
-    for (; c + 4 <= c1; c += 4) {
-        uint4 w0 = wp[(c + 0) * I2S_GROUP_ROWS], w1 = wp[(c + 1) * I2S_GROUP_ROWS];
-        uint4 w2 = wp[(c + 2) * I2S_GROUP_ROWS], w3 = wp[(c + 3) * I2S_GROUP_ROWS];
-        dot_chunk(w0, act + (c + 0) * 16, acc16, acc4, acc1);
-        dot_chunk(w1, act + (c + 1) * 16, acc16, acc4, acc1);
-        dot_chunk(w2, act + (c + 2) * 16, acc16, acc4, acc1);
-        dot_chunk(w3, act + (c + 3) * 16, acc16, acc4, acc1);
+    const uint32_t r = threadIdx.x, nc = c1 - c0;
+    const uint64_t gstride = (uint64_t)n_chunks * I2S_GROUP_ROWS;  // uint4 per group
+    const uint4 *wp = W + ((uint64_t)g * n_chunks + c0) * I2S_GROUP_ROWS + r;
+    uint4 cur[4][RG];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int q = 0; q < RG; q++)
+            cur[u][q] = wm_load_stream(wp + q * gstride + min((uint32_t)u, nc - 1) * I2S_GROUP_ROWS);
+    const int4 *ag = reinterpret_cast<const int4 *>(act) + (uint64_t)c0 * 4;
+    for (uint32_t i = r; i < nc * 4; i += 64) reinterpret_cast<int4 *>(act_s)[i] = ag[i];
+    __syncthreads();
+    int acc16[RG], acc4[RG], acc1[RG];
+#pragma unroll
+    for (int q = 0; q < RG; q++) acc16[q] = acc4[q] = acc1[q] = 0;
+    uint32_t c = 0;
+    for (; c + 4 <= nc; c += 4) {
+        uint4 nxt[4][RG];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int q = 0; q < RG; q++)
+                nxt[u][q] = wm_load_stream(wp + q * gstride +
+                                           min(c + 4 + (uint32_t)u, nc - 1) * I2S_GROUP_ROWS);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int *a = act_s + (c + u) * 16;
+#pragma unroll
+            for (int q = 0; q < RG; q++) dot_chunk(cur[u][q], a, acc16[q], acc4[q], acc1[q]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int q = 0; q < RG; q++) cur[u][q] = nxt[u][q];
     }
-    for (; c < c1; c++) dot_chunk(wp[c * I2S_GROUP_ROWS], act + c * 16, acc16, acc4, acc1);
-    partial[(uint64_t)s * rows_total + (uint64_t)gg * I2S_GROUP_ROWS + r] =
-        (acc16 >> 4) + (acc4 >> 2) + acc1;
+    // the last nc % 4 chunks are cur[0 .. nc%4-1] (loaded by the final round)
+#pragma unroll
+    for (int u = 0; u < 3; u++)
+        if (c + u < nc)
+#pragma unroll
+            for (int q = 0; q < RG; q++)
+                dot_chunk(cur[u][q], act_s + (c + u) * 16, acc16[q], acc4[q], acc1[q]);
+#pragma unroll
+    for (int q = 0; q < RG; q++)
+        partial[(uint64_t)s * rows_total + (uint64_t)(gg + q) * I2S_GROUP_ROWS + r] =
+            (acc16[q] >> 4) + (acc4[q] >> 2) + acc1[q];
 }
 
 __global__ void k_i2s_finalize(const int32_t *__restrict__ partial, uint32_t split,
@@ -212,8 +256,10 @@ void wm_launch_quantize_act(const float *x, uint32_t n, uint8_t *act, wm_act_met
 }
 
 uint32_t wm_i2s_pick_split(uint32_t n_groups, uint32_t n_chunks) {
-    // Aim for ~2 waves per CU over 256 CUs with at least 4 chunks per wave.
-    uint32_t split = (512 + n_groups - 1) / n_groups;
+    // Each wave streams its chunks four loads at a time, one memory latency
+    // per round; aim for ~32 waves per CU over 256 CUs so that few rounds
+    // remain per wave, with at least 4 chunks (one round) per wave.
+    uint32_t split = (4096 + n_groups - 1) / n_groups;
     uint32_t max_split = n_chunks / 4 ? n_chunks / 4 : 1;
     if (split > max_split) split = max_split;
     if (split > 16) split = 16;  // consumers sum at most 16 partials per row
@@ -227,12 +273,16 @@ void wm_launch_i2s_partial(const wm_i2s_desc *descs, int n_desc, uint32_t n_chun
     i2s_multi m{};
     uint32_t acc = 0;
     m.n = n_desc;
+    m.uniform_groups = descs[0].n_groups;
     for (int i = 0; i < n_desc; i++) {
         m.w[i] = descs[i].w;
         acc += descs[i].n_groups;
         m.group_end[i] = acc;
+        if (descs[i].n_groups != descs[0].n_groups) m.uniform_groups = 0;
     }
-    hipLaunchKernelGGL(k_i2s_partial, dim3(acc, split), dim3(64), 0, s, m, n_chunks,
+    const size_t lds = (size_t)((n_chunks + split - 1) / split) * 64;  // activation slice
+    // One group per wave: measured faster than two (fewer waves hide less latency).
+    hipLaunchKernelGGL(k_i2s_partial<1>, dim3(acc, split), dim3(64), lds, s, m, n_chunks,
                        reinterpret_cast<const int *>(act), partial, rows_total);
 }
 

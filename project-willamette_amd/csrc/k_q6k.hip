@@ -147,8 +147,10 @@ __global__ __launch_bounds__(kLogitsBlock) void k_q6k_logits(
         for (uint32_t b = 0; b < n_blocks; b++) {
             const uint8_t *base = gbase + (uint64_t)b * Q6K_GROUP_BLOCK_BYTES;
             const uint32_t *q6 = reinterpret_cast<const uint32_t *>(base) + lane * 3;
-            const uint32_t w0 = q6[0], w1 = q6[1], w2 = q6[2];
-            const uint32_t scw = reinterpret_cast<const uint32_t *>(base + Q6K_SC_OFFSET)[r * 4 + k];
+            const uint32_t w0 = wm_load_stream_u32(q6), w1 = wm_load_stream_u32(q6 + 1),
+                           w2 = wm_load_stream_u32(q6 + 2);
+            const uint32_t scw =
+                wm_load_stream_u32(reinterpret_cast<const uint32_t *>(base + Q6K_SC_OFFSET) + r * 4 + k);
             const float d =
                 wm_f16_bits_to_f32(reinterpret_cast<const uint16_t *>(base + Q6K_D_OFFSET)[r]);
             const float *xb = xl + b * 16;

@@ -94,6 +94,8 @@ struct wm_model {
     wm_act_meta *b_meta = nullptr;
     wm_batch_tok *b_tok = nullptr;
     uint32_t *b_ids = nullptr, *b_next = nullptr;
+    float *b_scores = nullptr;  // attention scores [t][head][context], grown on demand
+    size_t b_scores_bytes = 0;
 };
 
 struct wm_kv_cache {
@@ -350,6 +352,15 @@ wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_s
     }
     hipStream_t s = ctx->stream;
     WM_HIP(ctx, hipSetDevice(m->device));
+    const size_t sc_bytes = wm_attn_rows_scores_bytes(M, c.n_heads, n_max);
+    if (sc_bytes > m->b_scores_bytes) {
+        WM_HIP(ctx, hipStreamSynchronize(s));
+        if (m->b_scores) WM_HIP(ctx, hipFree(m->b_scores));
+        m->b_scores = nullptr;
+        m->b_scores_bytes = 0;
+        WM_HIP(ctx, hipMalloc((void **)&m->b_scores, sc_bytes));
+        m->b_scores_bytes = sc_bytes;
+    }
     WM_HIP(ctx, hipMemcpyAsync(m->b_tok, tok.data(), M * sizeof(wm_batch_tok), hipMemcpyHostToDevice, s));
     WM_HIP(ctx, hipMemcpyAsync(m->b_ids, tokens, M * 4, hipMemcpyHostToDevice, s));
 
@@ -372,7 +383,7 @@ wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_s
         wm_launch_qkv_rows(m->b_yqkv, QKV, m->rope_cos, m->rope_sin, m->b_tok, M, l, E, KV,
                            c.head_dim, c.n_rot, m->b_q, s);
         wm_launch_attn_rows(m->b_q, m->b_tok, M, n_max, l, c.n_kv_heads, c.head_dim, group, scale,
-                            m->b_attn, s);
+                            m->b_scores, m->b_attn, s);
         nr = wm_norm_rows{m->b_attn, E, nullptr, 0, nullptr, 0, L.attn_sub_norm, E, c.rms_eps,
                           m->b_act, m_pad, m->b_meta, nullptr, 0, nullptr, 0};
         wm_launch_rmsnorm_rows(nr, M, s);
@@ -536,6 +547,7 @@ void wm_model_destroy(wm_model *m) {
     if (m->output_norm) hipFree(m->output_norm);
     if (m->ws) hipFree(m->ws);
     if (m->bws) hipFree(m->bws);
+    if (m->b_scores) hipFree(m->b_scores);
     delete m;
 }
 

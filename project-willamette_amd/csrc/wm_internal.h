@@ -120,6 +120,17 @@ __device__ __forceinline__ float wm_f16_bits_to_f32(uint32_t bits) {
 // glibc-identical expf (host/device, see wm_expf.h)
 __device__ __forceinline__ float wm_expf(float x) { return wm::expf_glibc(x); }
 
+// Streaming (non-temporal) 16-byte load for data read exactly once, such as
+// matvec weights: it keeps them from displacing reused lines in the caches.
+typedef unsigned int wm_v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 wm_load_stream(const void *p) {
+    const wm_v4u v = __builtin_nontemporal_load(reinterpret_cast<const wm_v4u *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t wm_load_stream_u32(const void *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
+}
+
 // Wave-level helpers (wave64).
 __device__ __forceinline__ int wm_wave_sum_i32(int v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -295,7 +306,8 @@ void wm_launch_qkv_rows(const float *y, uint32_t ldy, const float *rope_cos, con
                         hipStream_t s);
 // Causal GQA attention of every token of a batch over its own sequence cache.
 bool wm_attn_rows_supported(uint32_t head_dim, uint32_t group);
+size_t wm_attn_rows_scores_bytes(uint32_t m, uint32_t n_heads, uint32_t n_max);
 void wm_launch_attn_rows(const float *q, const wm_batch_tok *tok, uint32_t m, uint32_t n_max,
                          uint32_t layer, uint32_t n_kv_heads, uint32_t head_dim, uint32_t group,
-                         float scale, float *out, hipStream_t s);
+                         float scale, float *scores, float *out, hipStream_t s);
 void wm_launch_debug_seq_sum(const float *a, uint32_t n, float *out, hipStream_t s);
