@@ -74,24 +74,38 @@ def decode_tokens(dkv, n: int, tok: int, pos: int):
     return ids
 
 
-def lm_head_kernel(ctx, wh, hm, cfg, reps: int):
-    """Average duration of one Q6_K logits launch (no argmax kernel),
-    alternating between two device copies of the 269 MB tensor so that the
-    256 MB Infinity Cache cannot serve a launch from the previous one."""
+def lm_head_kernels(ctx, wh, hm, cfg, reps: int):
+    """Average durations (ms) on the library's stream of the tied Q6_K
+    lm-head, alternating between two device copies of the 269 MB tensor so
+    that the 256 MB Infinity Cache cannot serve a launch from the previous one:
+      bounded - one launch of the id-only path's bounded pass (the kernel the
+                decode step spends its lm-head time in);
+      id_only - the whole id-only path (bounded pass, rescoring, final argmax);
+      exact   - the bit-exact logits kernel (used when logits are wanted)."""
     ts = [ctx.upload_q6k(hm.token_embd, cfg.n_embd, cfg.vocab) for _ in range(2)]
     h = ctx.to_device(wh.synth_normal(0x5749_4C4C_0000_0002, 2, cfg.n_embd))
-    logits = ctx.alloc(cfg.vocab * 4)
-    for i in range(4):
-        ctx.check(wh.lib.wm_logits_argmax_dev(ctx.h, ts[i & 1].h, h.ptr, logits.ptr, None))
+    logits, bound, amax = ctx.alloc(cfg.vocab * 4), ctx.alloc(cfg.vocab * 4), ctx.alloc(256)
+    runs = {
+        "bounded": lambda t: wh.lib.wm_debug_q6k_bounded_logits_dev(ctx.h, t.h, h.ptr, logits.ptr,
+                                                                    bound.ptr),
+        "id_only": lambda t: wh.lib.wm_logits_argmax_dev(ctx.h, t.h, h.ptr, None, amax.ptr),
+        "exact": lambda t: wh.lib.wm_logits_argmax_dev(ctx.h, t.h, h.ptr, logits.ptr, None),
+    }
     timer = HipTimer(ctx.stream)
-    timer.start()
-    for i in range(reps):
-        ctx.check(wh.lib.wm_logits_argmax_dev(ctx.h, ts[i & 1].h, h.ptr, logits.ptr, None))
-    ms = timer.stop_ms() / reps
+    out = {}
+    for name, run in runs.items():
+        for i in range(4):
+            ctx.check(run(ts[i & 1]))
+        timer.start()
+        for i in range(reps):
+            ctx.check(run(ts[i & 1]))
+        out[name] = timer.stop_ms() / reps
     bytes_per = cfg.vocab * (cfg.n_embd // 256) * 210 + cfg.n_embd * 4 + cfg.vocab * 4
+    for b in (h, logits, bound, amax):
+        b.free()
     for t in ts:
         t.close()
-    return ms, bytes_per
+    return out, bytes_per
 
 
 def i2s_stream(ctx, wh, copies: int, reps: int):
@@ -220,19 +234,23 @@ def probe(kind: str, reps: int):
     cfg = bs.BITNET_2B
     ctx = wh.Context(0)
     held = []
-    if kind == "lm_head":
+    if kind in ("lm_head", "lm_head_exact"):
         blocks = wh.synth_q6k(0x5749_4C4C_0000_0002, 1, cfg.vocab, cfg.n_embd, 1e-3)
         ts = [ctx.upload_q6k(blocks, cfg.n_embd, cfg.vocab) for _ in range(2)]
         del blocks
         h = ctx.to_device(wh.synth_normal(0x5749_4C4C_0000_0002, 2, cfg.n_embd))
-        logits = ctx.alloc(cfg.vocab * 4)
-        held += ts + [h, logits]
+        logits, bound = ctx.alloc(cfg.vocab * 4), ctx.alloc(cfg.vocab * 4)
+        held += ts + [h, logits, bound]
         turn = [0]
 
         def launch():
             t = ts[turn[0] & 1]
             turn[0] += 1
-            ctx.check(wh.lib.wm_logits_argmax_dev(ctx.h, t.h, h.ptr, logits.ptr, None))
+            if kind == "lm_head":  # the id-only path's bounded pass
+                ctx.check(wh.lib.wm_debug_q6k_bounded_logits_dev(ctx.h, t.h, h.ptr, logits.ptr,
+                                                                 bound.ptr))
+            else:
+                ctx.check(wh.lib.wm_logits_argmax_dev(ctx.h, t.h, h.ptr, logits.ptr, None))
     elif kind == "i2s":
         copies = 320
         seed = 0x5749_4C4C_0000_0001
@@ -263,16 +281,18 @@ def probe(kind: str, reps: int):
     ctx.close()
 
 
-def traffic_record(kernel_file: str):
-    """HBM bytes per launch from the committed counter summary, used only
-    while the kernel source it was measured on is unchanged."""
+def traffic_record(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary,
+    used only while the kernel source it was measured on is unchanged."""
     import hashlib
     rec_path = ROOT / "profiles" / "traffic.json"
-    src = ROOT / "project-willamette_amd" / "csrc" / kernel_file
-    if not rec_path.exists() or not src.exists():
+    if not rec_path.exists():
         return None
-    rec = json.loads(rec_path.read_text()).get(kernel_file)
-    if not rec or rec.get("source_sha256") != hashlib.sha256(src.read_bytes()).hexdigest():
+    rec = json.loads(rec_path.read_text()).get(kernel)
+    if not rec:
+        return None
+    src = ROOT / "project-willamette_amd" / "csrc" / rec["source"]
+    if not src.exists() or rec.get("source_sha256") != hashlib.sha256(src.read_bytes()).hexdigest():
         return None
     return rec["bytes_per_launch"]
 
@@ -286,7 +306,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batch", action="store_true", help="skip the ragged-batch measurement")
     ap.add_argument("--batch-steps", type=int, default=5)
-    ap.add_argument("--probe", choices=["lm_head", "i2s"],
+    ap.add_argument("--probe", choices=["lm_head", "lm_head_exact", "i2s"],
                     help="only run one kernel (and a calibration copy) for counter passes")
     ap.add_argument("--probe-reps", type=int, default=5)
     args = ap.parse_args()
@@ -329,9 +349,11 @@ def main():
     tok_s = args.steps / (wall_ms / 1000.0)
     log(f"decode: {tok_s:.1f} tok/s ({ms_tok:.3f} ms/token wall, {gpu_ms / args.steps:.3f} ms/token events)")
 
-    lm_ms, lm_bytes = lm_head_kernel(ctx, wh, hm, cfg, reps=50)
+    lm, lm_bytes = lm_head_kernels(ctx, wh, hm, cfg, reps=50)
+    lm_ms = lm["bounded"]
     lm_gbps = lm_bytes / (lm_ms / 1000.0) / 1e9
-    log(f"lm-head kernel: {lm_ms * 1000:.1f} us, {lm_gbps:.0f} GB/s")
+    gbps = {k: lm_bytes / (v / 1000.0) / 1e9 for k, v in lm.items()}
+    log("lm-head: " + ", ".join(f"{k} {v * 1000:.1f} us ({gbps[k]:.0f} GB/s)" for k, v in lm.items()))
     copies = 320  # 320 x 1.64 MB = 524 MB > 256 MB Infinity Cache
     mv_ms, mv_bytes = i2s_stream(ctx, wh, copies, reps=10)
     mv_gbps = mv_bytes / (mv_ms / 1000.0) / 1e9
@@ -376,12 +398,14 @@ def main():
                    "decode_tokens": args.steps, "start_token": START_TOKEN, "exact": True},
         "roofline": {"bound": "hbm", "achieved": round(lm_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(lm_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic_record("k_q6k.hip"),
-                     "kernel": "k_q6k_logits (Q6_K lm-head 128256x2560)",
+                     "traffic": traffic_record("k_q6k_bounded"),
+                     "kernel": "k_q6k_bounded (Q6_K lm-head 128256x2560, id-only pass)",
                      "us_per_launch": round(lm_ms * 1000, 2)},
         "cpu_baseline": cpu,
         "matvec": {
-            "q6k_lm_head_128256x2560": {"gbps": round(lm_gbps, 1), "frac": round(lm_gbps / HBM_PEAK_GBPS, 4)},
+            "q6k_lm_head_128256x2560": {
+                k: {"us": round(v * 1000, 2), "gbps": round(gbps[k], 1),
+                    "frac": round(gbps[k] / HBM_PEAK_GBPS, 4)} for k, v in lm.items()},
             "i2s_2560x2560_rotated": {"gbps": round(mv_gbps, 1), "frac": round(mv_gbps / HBM_PEAK_GBPS, 4),
                                       "us_per_matvec": round(mv_ms * 1000 / copies, 3),
                                       "copies": copies},

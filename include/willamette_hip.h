@@ -142,10 +142,16 @@ wm_status wm_q6k_dequantize_row(wm_ctx *ctx, const wm_tensor *t, uint64_t row, f
 wm_status wm_compute_logits(wm_ctx *ctx, const wm_tensor *token_embd, const float *hidden,
                             size_t hidden_len, float *logits, size_t vocab);
 /* compute_logits + argmax (src/model/lm_head.rs:161-174: first index of the
- * maximum) in one pass; `logits` may be NULL when only the id is wanted. */
+ * maximum).  With `logits` non-NULL every logit is the reference's, bit for
+ * bit.  With `logits` NULL only the id is computed: a bandwidth-bound
+ * fixed-point pass bounds every row's distance from the reference's value,
+ * and only rows whose bound reaches the best row are recomputed in the
+ * reference's order, so the id is still exactly the reference's argmax.
+ * Rows above 8192 values or beyond 4194304 rows: WM_E_SHAPE. */
 wm_status wm_logits_argmax(wm_ctx *ctx, const wm_tensor *token_embd, const float *hidden,
                            size_t hidden_len, float *logits, uint32_t *argmax);
-/* Device form: d_logits may be NULL; d_argmax is one uint32 in device memory. */
+/* Device form: d_logits may be NULL (then the id-only path above runs);
+ * d_argmax is one uint32 in device memory. */
 wm_status wm_logits_argmax_dev(wm_ctx *ctx, const wm_tensor *token_embd, const float *d_hidden,
                                float *d_logits, uint32_t *d_argmax);
 /* argmax over a host slice (src/model/lm_head.rs:161-174); WM_E_ARG when
@@ -250,6 +256,18 @@ wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_s
  * terms (host array), the routine behind every RMSNorm sum of squares and
  * softmax denominator, so tests can check it on adversarial inputs. */
 wm_status wm_debug_seq_sum(wm_ctx *ctx, const float *values, size_t n, float *sum);
+
+/* No counterpart in the reference: the id-only lm-head's bounded pass alone.
+ * approx[v] is row v's fixed-point dot and bound[v] a bound on its distance
+ * from the reference's f32 logit (the property the argmax proof rests on),
+ * so tests can check |approx - logit| <= bound on every row. */
+wm_status wm_debug_q6k_bounded_logits(wm_ctx *ctx, const wm_tensor *token_embd,
+                                      const float *hidden, size_t hidden_len, float *approx,
+                                      float *bound);
+/* Device-pointer form, asynchronous: one launch of the bounded pass (the
+ * kernel the id-only lm-head spends its time in), for timing it alone. */
+wm_status wm_debug_q6k_bounded_logits_dev(wm_ctx *ctx, const wm_tensor *token_embd,
+                                          const float *d_hidden, float *d_approx, float *d_bound);
 
 /* ---- synthetic BitNet-shaped inputs (src/synth.rs) ------------------- */
 

@@ -13,20 +13,43 @@
 // index within a half-block is 32k + 16*band + 4*chunk + l, in (block, half,
 // band, chunk) order, and the 16 partials are combined as
 //   v_l = (p0l + p1l) + (p2l + p3l);  dot = (v0 + v3) + (v1 + v2).
-// The lm-head kernel gives each of those 16 partial sums to its own lane, so
-// a wave computes 4 rows with exactly the reference's roundings.
+// The exact kernel gives each of those 16 partial sums to its own lane, so a
+// wave computes 4 rows with exactly the reference's roundings.
 //
 // Device layout (k_q6k_repack): rows in groups of 4; per (group, block) 840
-// bytes: for lane L' = 16*row + 4k + l the 16 six-bit quants it consumes in
-// this block, packed into 3 dwords (step s at bits 6s..6s+5); then per row
-// the 16 sub-scales as 4 dwords (dword k, byte 2h+band = sc[8h + band + 2k]);
-// then the 4 f16 d values.  Same byte count as the GGUF tensor.
+// bytes, the same byte count as the GGUF blocks:
+//   bytes 0..767   lane L' = 16*row + 4k + l holds, in 3 dwords, the 16
+//                  six-bit quants it consumes in this block, step s = 4*hn + c
+//                  (hn = 2*half + band, c = chunk):
+//                    dword 0: low nibbles of s = 0..7  at bits 8c + 4(hn & 1)
+//                    dword 1: low nibbles of s = 8..15 at bits 8c + 4(hn & 1)
+//                    dword 2: high bit pairs, byte c bits 2hn..2hn+1
+//                  so that four AND/OR operations per dword rebuild the
+//                  quants as bytes: byte c of U[hn] = q(4*hn + c);
+//   bytes 768..831 per row the 16 sub-scales as 4 dwords (dword k, byte hn =
+//                  sc[8h + band + 2k]);
+//   bytes 832..839 the 4 f16 d values.
+//
+// Two lm-head paths:
+//  * exact (k_q6k_logits): every logit bit-identical to the reference, one
+//    lane per SSE2 partial sum.  Used whenever the caller wants the logits.
+//  * argmax-only (k_q6k_bounded -> k_q6k_select): a
+//    bandwidth-bound pass computes every row's dot from
+//    the int8 quants with v_dot4_i32_i8 against a 16-bit fixed-point copy of
+//    the hidden vector, together with a rigorous bound on its distance from
+//    the reference's f32 result.  Only rows whose upper bound reaches the
+//    largest lower bound are recomputed in the exact order; every other row
+//    is provably below the maximum, so the argmax is the reference's.
+#include <hip/hip_fp16.h>
+
 #include "wm_internal.h"
 
 namespace {
 
 constexpr int kLogitsBlock = 256;  // 4 waves
 constexpr int kMaxArgBlocks = 2048;
+constexpr int kBoundedBlock = 256;
+constexpr uint32_t kBoundedMaxBlocks = 2048;
 
 __host__ __device__ __forceinline__ int q6_of(const uint8_t *blk, int h, int k, int l) {
     const uint8_t *ql = blk + h * 64, *qh = blk + 128 + h * 32;
@@ -62,13 +85,12 @@ __global__ void k_q6k_repack(const uint8_t *__restrict__ raw, uint8_t *__restric
             for (int l = 0; l < 4; l++) {
                 uint32_t w[3] = {0, 0, 0};
                 for (int s = 0; s < 16; s++) {
-                    int hn = s >> 2, c = s & 3, h = hn >> 1, n = hn & 1;
-                    uint32_t v = (uint32_t)q6_of(blk, h, k, n * 16 + c * 4 + l);
-                    int bit = 6 * s;
-                    w[bit >> 5] |= v << (bit & 31);
-                    if ((bit & 31) > 26) w[(bit >> 5) + 1] |= v >> (32 - (bit & 31));
+                    const int hn = s >> 2, c = s & 3, h = hn >> 1, n = hn & 1;
+                    const uint32_t v = (uint32_t)q6_of(blk, h, k, n * 16 + c * 4 + l);
+                    w[s >> 3] |= (v & 15u) << (8 * c + 4 * (hn & 1));
+                    w[2] |= (v >> 4) << (8 * c + 2 * hn);
                 }
-                int L = r * 16 + k * 4 + l;
+                const int L = r * 16 + k * 4 + l;
                 q6[L * 3 + 0] = w[0]; q6[L * 3 + 1] = w[1]; q6[L * 3 + 2] = w[2];
             }
             uint32_t sc = 0;
@@ -82,13 +104,13 @@ __global__ void k_q6k_repack(const uint8_t *__restrict__ raw, uint8_t *__restric
     }
 }
 
-__device__ __forceinline__ uint32_t q6_step(uint32_t w0, uint32_t w1, uint32_t w2, int s) {
-    int bit = 6 * s;
-    uint32_t lo = bit < 32 ? w0 : (bit < 64 ? w1 : w2);
-    uint32_t hi = bit < 32 ? w1 : w2;
-    int sh = bit & 31;
-    uint32_t v = sh ? ((lo >> sh) | (hi << (32 - sh))) : lo;
-    return v & 63u;
+// The 16 quants of one lane as 4 dwords of bytes: byte c of U[hn] = q(4hn + c).
+__device__ __forceinline__ void q6_unpack(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t U[4]) {
+    const uint32_t m = 0x0F0F0F0Fu, mh = 0x30303030u;
+    U[0] = (w0 & m) | ((w2 << 4) & mh);
+    U[1] = ((w0 >> 4) & m) | ((w2 << 2) & mh);
+    U[2] = (w1 & m) | (w2 & mh);
+    U[3] = ((w1 >> 4) & m) | ((w2 >> 2) & mh);
 }
 
 // Dequantise row values: thread t of 256 handles value t of each block.
@@ -103,11 +125,13 @@ __global__ void k_q6k_dequant_row(const uint8_t *__restrict__ w, uint32_t n_bloc
     const uint32_t b = blockIdx.x, t = threadIdx.x;
     const uint8_t *base = w + ((uint64_t)G * n_blocks + b) * Q6K_GROUP_BLOCK_BYTES;
     const int h = t >> 7, k = (t >> 5) & 3, n = (t >> 4) & 1, c = (t >> 2) & 3, l = t & 3;
-    const int L = r * 16 + k * 4 + l, s = (h * 2 + n) * 4 + c;
+    const int L = r * 16 + k * 4 + l, hn = h * 2 + n;
     const uint32_t *q6 = reinterpret_cast<const uint32_t *>(base) + L * 3;
-    const uint32_t q = q6_step(q6[0], q6[1], q6[2], s);
+    const uint32_t lo = (q6[hn >> 1] >> (8 * c + 4 * (hn & 1))) & 15u;
+    const uint32_t hi = (q6[2] >> (8 * c + 2 * hn)) & 3u;
+    const uint32_t q = lo | (hi << 4);
     const uint32_t scw = reinterpret_cast<const uint32_t *>(base + Q6K_SC_OFFSET)[r * 4 + k];
-    const int sc = (int)(int8_t)(scw >> (8 * (h * 2 + n)));
+    const int sc = (int)(int8_t)(scw >> (8 * hn));
     const float d = wm_f16_bits_to_f32(reinterpret_cast<const uint16_t *>(base + Q6K_D_OFFSET)[r]);
     out[b * Q6K_VALUES + t] = d * (float)sc * (float)((int)q - 32);
 }
@@ -122,68 +146,141 @@ __device__ __forceinline__ bool cand_better(float v, uint32_t i, float bv, uint3
     return v > bv || (v == bv && i < bi);
 }
 
-__global__ __launch_bounds__(kLogitsBlock) void k_q6k_logits(
-    const uint8_t *__restrict__ w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
-    const float *__restrict__ hidden, float *__restrict__ logits, argcand *__restrict__ cands) {
-    extern __shared__ float xs[];  // [16][n_blocks*16 + 4]
-    const uint32_t stride = n_blocks * 16 + 4;
-    // permute the hidden vector into lane order: lane L = 4k + l, step s of block b
+// ---------------------------------------------------------------------------
+// exact row dot (reference order)
+// ---------------------------------------------------------------------------
+
+// The hidden vector permuted into lane order: xs[L * stride + b*16 + s]
+// holds the value lane L = 4k + l multiplies at step s of block b.
+__host__ __device__ __forceinline__ uint32_t xs_stride(uint32_t n_blocks) { return n_blocks * 16 + 4; }
+
+__device__ void build_xs(const float *__restrict__ hidden, uint32_t n_blocks, float *xs) {
+    const uint32_t stride = xs_stride(n_blocks);
     for (uint32_t idx = threadIdx.x; idx < 16u * n_blocks * 16u; idx += blockDim.x) {
         uint32_t L = idx / (n_blocks * 16), rem = idx % (n_blocks * 16);
         uint32_t b = rem / 16, s = rem % 16;
         uint32_t k = L >> 2, l = L & 3, hn = s >> 2, c = s & 3, h = hn >> 1, n = hn & 1;
         xs[L * stride + b * 16 + s] = hidden[b * 256 + h * 128 + k * 32 + n * 16 + c * 4 + l];
     }
-    __syncthreads();
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t r = lane >> 4, L = lane & 15, k = L >> 2;
-    const float *xl = xs + L * stride;
-    float best_v = -INFINITY;
-    uint32_t best_i = 0xFFFFFFFFu;
-    const uint32_t waves_total = gridDim.x * (blockDim.x >> 6);
-    for (uint32_t G = blockIdx.x * (blockDim.x >> 6) + wave; G < n_rowgroups; G += waves_total) {
-        const uint8_t *gbase = w + (uint64_t)G * n_blocks * Q6K_GROUP_BLOCK_BYTES;
-        float acc = 0.0f;
-        for (uint32_t b = 0; b < n_blocks; b++) {
-            const uint8_t *base = gbase + (uint64_t)b * Q6K_GROUP_BLOCK_BYTES;
-            const uint32_t *q6 = reinterpret_cast<const uint32_t *>(base) + lane * 3;
-            const uint32_t w0 = wm_load_stream_u32(q6), w1 = wm_load_stream_u32(q6 + 1),
-                           w2 = wm_load_stream_u32(q6 + 2);
-            const uint32_t scw =
-                wm_load_stream_u32(reinterpret_cast<const uint32_t *>(base + Q6K_SC_OFFSET) + r * 4 + k);
-            const float d =
-                wm_f16_bits_to_f32(reinterpret_cast<const uint16_t *>(base + Q6K_D_OFFSET)[r]);
-            const float *xb = xl + b * 16;
-            if (__builtin_expect(isfinite(d), 1)) {
+}
+
+// One lane's data for CH consecutive blocks of a 4-row group.
+template <int CH>
+struct q6_lane_blocks {
+    uint32_t w0[CH], w1[CH], w2[CH], scw[CH], db[CH];
+};
+
+// Loads through a buffer descriptor of a wave-uniform group base (streaming
+// kernels): lane offsets are per-lane constants, block offsets uniform.
+template <int CH>
+__device__ __forceinline__ void q6_load_uniform(q6_lane_blocks<CH> &v, __amdgpu_buffer_rsrc_t rs,
+                                                uint32_t b0, uint32_t off_q, uint32_t off_sc,
+                                                uint32_t off_d) {
 #pragma unroll
-                for (int hn = 0; hn < 4; hn++) {
-                    const float S = d * (float)(int)(int8_t)(scw >> (8 * hn));
-                    const float nS32 = -32.0f * S;
+    for (int j = 0; j < CH; j++) {
+        const uint32_t so = (b0 + j) * Q6K_GROUP_BLOCK_BYTES;
+        const wm_v3u q = __builtin_amdgcn_raw_buffer_load_b96(rs, off_q, so, WM_LOAD_NT);
+        v.w0[j] = q.x;
+        v.w1[j] = q.y;
+        v.w2[j] = q.z;
+        v.scw[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, off_sc, so, WM_LOAD_NT);
+        v.db[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, off_d, so, 0);
+    }
+}
+
+// Loads from a per-lane group base (rows gathered from different groups).
+template <int CH>
+__device__ __forceinline__ void q6_load_lane(q6_lane_blocks<CH> &v, const uint8_t *gbase,
+                                             uint32_t b0, uint32_t off_q, uint32_t off_sc,
+                                             uint32_t off_d) {
 #pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        const int s = hn * 4 + c;
-                        // (q6 - 32) * S is exact in f32, so the fused form equals the
-                        // reference's rounded product q * (d*sc).
-                        const float qS = __builtin_fmaf((float)q6_step(w0, w1, w2, s), S, nS32);
-                        acc = acc + qS * xb[s];
-                    }
+    for (int j = 0; j < CH; j++) {
+        const uint8_t *base = gbase + (b0 + j) * Q6K_GROUP_BLOCK_BYTES;
+        const uint32_t *q6 = reinterpret_cast<const uint32_t *>(base + off_q);
+        v.w0[j] = q6[0];
+        v.w1[j] = q6[1];
+        v.w2[j] = q6[2];
+        v.scw[j] = *reinterpret_cast<const uint32_t *>(base + off_sc);
+        v.db[j] = *reinterpret_cast<const uint16_t *>(base + off_d);
+    }
+}
+
+// Accumulate blocks b0..b0+CH-1 into this lane's partial in the SSE2 order
+// (xl = xs + L*stride).
+template <int CH>
+__device__ __forceinline__ void q6_exact_accum(const q6_lane_blocks<CH> &v, uint32_t b0,
+                                               const float *xl, float &acc) {
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+        uint32_t U[4];
+        q6_unpack(v.w0[j], v.w1[j], v.w2[j], U);
+        const float d = wm_f16_bits_to_f32(v.db[j]);
+        const float *xb = xl + (b0 + j) * 16;
+        if (__builtin_expect(isfinite(d), 1)) {
+#pragma unroll
+            for (int hn = 0; hn < 4; hn++) {
+                const float S = d * (float)(int)(int8_t)(v.scw[j] >> (8 * hn));
+                const float nS32 = -32.0f * S;
+                const float4 x4 = *reinterpret_cast<const float4 *>(xb + hn * 4);
+                const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    // (q - 32) * S is exact in f32, so the fused form equals the
+                    // reference's rounded product q * (d*sc).
+                    const float qf = (float)((U[hn] >> (8 * c)) & 0xFFu);
+                    const float qS = __builtin_fmaf(qf, S, nS32);
+                    acc = acc + qS * xv[c];
                 }
-            } else {
-                for (int hn = 0; hn < 4; hn++) {
-                    const float S = d * (float)(int)(int8_t)(scw >> (8 * hn));
-                    for (int c = 0; c < 4; c++) {
-                        const int s = hn * 4 + c;
-                        const float qS = (float)((int)q6_step(w0, w1, w2, s) - 32) * S;
-                        acc = acc + qS * xb[s];
-                    }
+            }
+        } else {
+            for (int hn = 0; hn < 4; hn++) {
+                const float S = d * (float)(int)(int8_t)(v.scw[j] >> (8 * hn));
+                for (int c = 0; c < 4; c++) {
+                    const int q = (int)((U[hn] >> (8 * c)) & 0xFFu);
+                    const float qS = (float)(q - 32) * S;
+                    acc = acc + qS * xb[hn * 4 + c];
                 }
             }
         }
-        // v_l = (p0l + p1l) + (p2l + p3l); dot = (v0 + v3) + (v1 + v2)
-        float t = acc + __shfl_xor(acc, 4, 64);
-        float v = t + __shfl_xor(t, 8, 64);
-        float u = v + __shfl_xor(v, 3, 64);
-        float dot = u + __shfl_xor(u, 1, 64);
+    }
+}
+
+// Combine the 16 partials of a lane group: v_l = (p0l + p1l) + (p2l + p3l);
+// dot = (v0 + v3) + (v1 + v2).  The dot ends up in all 16 lanes.
+__device__ __forceinline__ float q6_combine(float acc) {
+    float t = acc + __shfl_xor(acc, 4, 64);
+    float v = t + __shfl_xor(t, 8, 64);
+    float u = v + __shfl_xor(v, 3, 64);
+    return u + __shfl_xor(u, 1, 64);
+}
+
+template <int CH>
+__global__ __launch_bounds__(kLogitsBlock) void k_q6k_logits(
+    const uint8_t *__restrict__ w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
+    const float *__restrict__ hidden, float *__restrict__ logits, argcand *__restrict__ cands) {
+    extern __shared__ float xs[];  // [16][n_blocks*16 + 4]
+    build_xs(hidden, n_blocks, xs);
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t r = lane >> 4, L = lane & 15;
+    const float *xl = xs + L * xs_stride(n_blocks);
+    const uint32_t off_q = lane * 12, off_sc = Q6K_SC_OFFSET + (r * 4 + (L >> 2)) * 4,
+                   off_d = Q6K_D_OFFSET + r * 2;
+    const uint32_t group_bytes = n_blocks * Q6K_GROUP_BLOCK_BYTES;
+    float best_v = -INFINITY;
+    uint32_t best_i = 0xFFFFFFFFu;
+    constexpr uint32_t kWaves = kLogitsBlock / 64;
+    const uint32_t waves_total = gridDim.x * kWaves;
+    for (uint32_t G = blockIdx.x * kWaves + wave; G < n_rowgroups; G += waves_total) {
+        const __amdgpu_buffer_rsrc_t rs = wm_rsrc(w + (uint64_t)G * group_bytes, group_bytes);
+        float acc = 0.0f;
+        for (uint32_t b0 = 0; b0 < n_blocks; b0 += CH) {
+            q6_lane_blocks<CH> v;
+            q6_load_uniform<CH>(v, rs, b0, off_q, off_sc, off_d);
+            q6_exact_accum<CH>(v, b0, xl, acc);
+        }
+        const float dot = q6_combine(acc);
         const uint32_t row = G * Q6K_GROUP_ROWS + r;
         if (L == 0 && row < n_rows) {
             if (logits) logits[row] = dot;
@@ -239,6 +336,400 @@ __global__ void k_argmax_final(const argcand *__restrict__ cands, uint32_t n_can
     }
 }
 
+// ---------------------------------------------------------------------------
+// argmax-only path
+// ---------------------------------------------------------------------------
+
+// The hidden vector as 16-bit fixed point, x_i ~ 2^e * X_i with
+// X_i = rint(x_i * 2^-e), |X_i| <= 32639, split X = 256*xh + xl into two int8
+// (xh = (X + 128) >> 8, xl = X - 256*xh in [-128, 127]).  Entry (b, p) holds,
+// for lane position p = 4k + l of block b and group hn, the four values that
+// meet byte c of that lane's U[hn]: xh and xl packed as int8x4 and
+// c[hn] = -32 * sum_c X (which folds the quants' offset of 32 into the dot).
+struct q6k_xq {
+    int xh[4], xl[4], c[4];
+};
+struct q6k_xhdr {
+    int e;          // scale exponent
+    uint32_t ok;    // 0: the hidden vector holds a NaN or an infinity
+    float bound_k;  // row bound = bound_k * sigma_r, sigma_r = sum_j |d * sc_j|
+    float mag_k;    // row magnitude bound factor (overflow guard)
+};
+
+// sigma_r = sum over the row's blocks b and sub-blocks j of |d_b * sc_bj|,
+// from the raw GGUF blocks, in double and rounded up to f32 (non-finite d
+// gives a non-finite sigma, which makes the row a rescoring candidate).
+__global__ void k_q6k_row_sigma(const uint8_t *__restrict__ raw, uint32_t n_rows,
+                                uint32_t n_blocks, float *__restrict__ sigma) {
+    const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= n_rows) return;
+    double s = 0.0;
+    for (uint32_t b = 0; b < n_blocks; b++) {
+        const uint8_t *blk = raw + ((uint64_t)row * n_blocks + b) * Q6K_BYTES;
+        int asc = 0;
+        for (int j = 0; j < 16; j++) asc += abs((int)(int8_t)blk[192 + j]);
+        const double d = (double)wm_f16_bits_to_f32(blk[208] | (blk[209] << 8));
+        s += fabs(d) * asc;
+    }
+    sigma[row] = (float)(s * (1.0 + 0x1p-20));
+}
+
+// Build the fixed-point copy of hidden[n_blocks*256] in LDS (xq[n_blocks*16])
+// and the bound factors, by the whole workgroup.  Every workgroup of the
+// bounded pass does this for itself (the 10 KB vector stays in L2), so the
+// pass needs no preparatory launch.
+__device__ q6k_xhdr xprep_block(const float *__restrict__ hidden, uint32_t n_blocks, q6k_xq *xq,
+                                float *red, int *redi) {
+    const uint32_t n = n_blocks * 256, tid = threadIdx.x;
+    float m = 0.0f;
+    int bad = 0;
+    for (uint32_t i = tid; i < n; i += blockDim.x) {
+        const float v = hidden[i];
+        bad |= !isfinite(v);
+        m = fmaxf(m, fabsf(v));
+    }
+    const float maxabs = wm_block_max_nonan(m, red);
+    bad = wm_block_sum_i32(bad, redi);
+    // smallest e with maxabs * 2^-e <= 32639, kept >= -140 so 2^e stays representable
+    int e = 0;
+    if (maxabs > 0.0f && !bad) {
+        int E;
+        frexpf(maxabs, &E);  // maxabs < 2^E
+        e = E - 15;
+        if (ldexpf(maxabs, -e) > 32639.0f) e++;
+        if (e < -140) e = -140;
+    }
+    for (uint32_t idx = tid; idx < n_blocks * 64; idx += blockDim.x) {
+        const uint32_t b = idx >> 6, p = (idx >> 2) & 15, hn = idx & 3;
+        const uint32_t k = p >> 2, l = p & 3, h = hn >> 1, band = hn & 1;
+        const float *src = hidden + b * 256 + h * 128 + k * 32 + band * 16 + l;
+        uint32_t ph = 0, pl = 0;
+        int sum = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int v = bad ? 0 : (int)rintf(ldexpf(src[c * 4], -e));
+            const int xh = (v + 128) >> 8, xl = v - 256 * xh;
+            ph |= (uint32_t)(xh & 0xFF) << (8 * c);
+            pl |= (uint32_t)(xl & 0xFF) << (8 * c);
+            sum += v;
+        }
+        q6k_xq &o = xq[b * 16 + p];
+        o.xh[hn] = (int)ph;
+        o.xl[hn] = (int)pl;
+        o.c[hn] = -32 * sum;
+    }
+    // Distance between the bounded pass and the reference's f32 dot, per
+    // unit of sigma_r = sum_j |S_j| (S_j = d * sc_j, 16 values per sub-block,
+    // |q - 32| <= 32, so a row's sum_i |(q-32) * S * y_i| <= 512 * max|y| * sigma_r):
+    //  - fixed point: |x - 2^e X| <= 2^(e-1): 2^(e+8) * sigma_r;
+    //  - this pass's f32 work (i32 -> f32, n_blocks fmas, 4 tree adds), on
+    //    terms |d * T| with |2^e X| <= maxabs + 2^(e-1):
+    //    gamma_(nb+5) * 512 * (maxabs + 2^(e-1)) * sigma_r;
+    //  - the reference's f32 work (one product rounding, 16*nb - 1
+    //    sequential adds, 4 combine adds): gamma_(16nb+5) * 512 * maxabs * sigma_r.
+    const double u = 0x1p-24;
+    const double gA = (n_blocks + 6) * u * 1.01, gB = (16.0 * n_blocks + 6) * u * 1.01;
+    const double half_ulp = ldexp(1.0, e - 1);
+    const double k = ldexp(1.0, e + 8) + 512.0 * (gA * ((double)maxabs + half_ulp) + gB * (double)maxabs);
+    q6k_xhdr hd;
+    hd.e = e;
+    hd.ok = bad ? 0u : 1u;
+    hd.bound_k = (float)(k * (1.0 + 0x1p-16));
+    hd.mag_k = (float)(512.0 * ((double)maxabs + half_ulp) * (1.0 + 0x1p-16));
+    return hd;
+}
+
+// d = a * b + c on the low 24 bits of a and b (sign-extended), low 32 bits of
+// the result: one full-rate v_mad_i32_i24.  (For this use the compiler emits a
+// quarter-rate 32-bit multiply.)  The operands must come from ordinary VALU
+// instructions: the instruction is opaque to the compiler's hazard tracking,
+// so it must not read a register a DOT instruction has just written.
+__device__ __forceinline__ int mad_i24(int a, int b, int c) {
+    int d;
+    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+
+// Bounded pass.  Workgroup w takes the 4-row groups [g0, g1) (contiguous, so
+// its rows form one range), its waves taking them in turn.  Lane (r, p =
+// 4k + l) of a wave handles the same 16 quants per block as in the exact
+// kernel; per group hn it takes two int8 dots of the bytes U[hn] with xh and
+// xl, I = 256*dh + dl (exact, |I| < 2^23), and T = sum_hn sc_hn * I (exact,
+// |T| < 2^31); then acc += d * T in f32.  Per row: logit ~ 2^e * sum of the
+// 16 lanes' acc, bound = bound_k * sigma_r, widened so that rounding a +-
+// bound in f32 cannot cross the true interval.  The workgroup's largest
+// lower and upper bounds go to wg_lb / wg_ub.
+template <int CH>
+__global__ __launch_bounds__(kBoundedBlock) void k_q6k_bounded(
+    const uint8_t *__restrict__ w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
+    const float *__restrict__ sigma, const float *__restrict__ hidden, float *__restrict__ approx,
+    float *__restrict__ bound, float *__restrict__ wg_lb, float *__restrict__ wg_ub) {
+    extern __shared__ __align__(16) q6k_xq xq[];  // [n_blocks][16]
+    __shared__ float red[kBoundedBlock / 64], red2[kBoundedBlock / 64];
+    __shared__ int redi[kBoundedBlock / 64];
+    const q6k_xhdr hdr = xprep_block(hidden, n_blocks, xq, red, redi);
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t r = lane >> 4, p = lane & 15, k = p >> 2;
+    const uint32_t off_q = lane * 12, off_sc = Q6K_SC_OFFSET + (r * 4 + k) * 4,
+                   off_d = Q6K_D_OFFSET + r * 2;
+    const uint32_t group_bytes = n_blocks * Q6K_GROUP_BLOCK_BYTES;
+    const uint32_t g0 = (uint32_t)((uint64_t)blockIdx.x * n_rowgroups / gridDim.x);
+    const uint32_t g1 = (uint32_t)((uint64_t)(blockIdx.x + 1) * n_rowgroups / gridDim.x);
+    float lb_max = -INFINITY, ub_max = -INFINITY;
+    constexpr uint32_t kWaves = kBoundedBlock / 64;
+    for (uint32_t G = g0 + wave; G < g1; G += kWaves) {
+        const __amdgpu_buffer_rsrc_t rs = wm_rsrc(w + (uint64_t)G * group_bytes, group_bytes);
+        float acc = 0.0f;
+        for (uint32_t b0 = 0; b0 < n_blocks; b0 += CH) {
+            q6_lane_blocks<CH> v;
+            q6_load_uniform<CH>(v, rs, b0, off_q, off_sc, off_d);
+#pragma unroll
+            for (int j = 0; j < CH; j++) {
+                uint32_t U[4];
+                q6_unpack(v.w0[j], v.w1[j], v.w2[j], U);
+                const q6k_xq &xv = xq[(b0 + j) * 16 + p];
+                int T = 0;
+#pragma unroll
+                for (int hn = 0; hn < 4; hn++) {
+                    const int sc = (int)(int8_t)(v.scw[j] >> (8 * hn));
+                    const int dh = __builtin_amdgcn_sdot4((int)U[hn], xv.xh[hn], 0, false);
+                    const int dl = __builtin_amdgcn_sdot4((int)U[hn], xv.xl[hn], xv.c[hn], false);
+                    const int I = (int)(((uint32_t)dh << 8) + (uint32_t)dl);  // a VALU result
+                    T = mad_i24(sc, I, T);
+                }
+                const float d = __half2float(__ushort_as_half((unsigned short)v.db[j]));
+                acc = __builtin_fmaf(d, (float)T, acc);
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) acc = acc + __shfl_xor(acc, o, 64);
+        const uint32_t row = G * Q6K_GROUP_ROWS + r;
+        if (p == 0 && row < n_rows) {
+            float a, eb;
+            const float sg = sigma[row];
+            if (hdr.ok) {
+                a = ldexpf(acc, hdr.e);
+                eb = hdr.bound_k * sg;
+                eb = eb + eb * 0x1p-20f + fabsf(a) * 0x1p-22f + 1e-35f;
+                // terms this large could overflow in the reference's partial sums
+                if (!(hdr.mag_k * sg < 1e37f)) eb = INFINITY;
+            } else {
+                a = NAN;
+                eb = INFINITY;
+            }
+            approx[row] = a;
+            bound[row] = eb;
+            const float lb = a - eb, ub = a + eb;
+            if (lb > lb_max) lb_max = lb;                     // NaN never raises it
+            if (!(ub <= ub_max)) ub_max = ub == ub ? ub : INFINITY;  // NaN counts as +inf
+        }
+    }
+    lb_max = wm_wave_max_nonan(lb_max);
+    ub_max = wm_wave_max_nonan(ub_max);
+    if (lane == 0) {
+        red[wave] = lb_max;
+        red2[wave] = ub_max;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float m = red[0], mu = red2[0];
+        for (int i = 1; i < (int)kWaves; i++) {
+            m = wm_max_nonan(m, red[i]);
+            mu = wm_max_nonan(mu, red2[i]);
+        }
+        wg_lb[blockIdx.x] = m;
+        wg_ub[blockIdx.x] = mu;
+    }
+}
+
+// Selection, exact rescoring and the final argmax, in one workgroup.
+// A row can hold the maximum only if its upper bound reaches the largest
+// lower bound LB; every other row's reference logit is below LB, which is
+// at most the reference logit of the row attaining it.  So: workgroups of
+// the bounded pass whose largest upper bound reaches LB (and workgroup 0,
+// for row 0, whose exact value the NaN rule reads) have their rows scanned;
+// the rows that qualify are recomputed in the exact order (4 per wave pass)
+// and their logits overwritten with the exact values; the first index of the
+// maximum among them is the reference's argmax.
+constexpr int kSelectBlock = 1024;
+constexpr uint32_t kSelectCap = 2048;  // candidate rows held at once
+
+template <int CH>
+__global__ __launch_bounds__(kSelectBlock) void k_q6k_select(
+    const uint8_t *__restrict__ w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
+    const float *__restrict__ hidden, float *__restrict__ logits, const float *__restrict__ bound,
+    const float *__restrict__ wg_lb, const float *__restrict__ wg_ub, uint32_t n_wg,
+    uint32_t *__restrict__ argmax_out) {
+    extern __shared__ float xs[];  // [16][n_blocks*16 + 4]
+    __shared__ uint32_t wg_list[kBoundedMaxBlocks];
+    __shared__ uint32_t cand[kSelectCap];
+    __shared__ uint32_t n_wg_list, n_cand;
+    __shared__ float red[kSelectBlock / 64];
+    __shared__ argcand s_c[kSelectBlock / 64];
+    __shared__ float s_f0;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the hidden vector in lane order (xs[L*stride + b*16 + s] = x at
+    // b*256 + h*128 + k*32 + band*16 + c*4 + l, L = 4k + l, s = 4*(2h+band) + c)
+    const uint32_t stride = xs_stride(n_blocks);
+    for (uint32_t j = tid; j < n_blocks * 256; j += blockDim.x) {
+        const uint32_t b = j >> 8, h = (j >> 7) & 1, k = (j >> 5) & 3, band = (j >> 4) & 1,
+                       c = (j >> 2) & 3, l = j & 3;
+        xs[(4 * k + l) * stride + b * 16 + (2 * h + band) * 4 + c] = hidden[j];
+    }
+    float m = -INFINITY;
+    for (uint32_t i = tid; i < n_wg; i += blockDim.x) m = wm_max_nonan(m, wg_lb[i]);
+    if (tid == 0) {
+        n_wg_list = 0;
+        n_cand = 0;
+    }
+    const float lb_max = wm_block_max_nonan(m, red);  // (also orders the writes above)
+    for (uint32_t i = tid; i < n_wg; i += blockDim.x)
+        if (i == 0 || !(wg_ub[i] < lb_max)) wg_list[atomicAdd(&n_wg_list, 1u)] = i;
+    __syncthreads();
+    const uint32_t n_list = n_wg_list;
+    const uint32_t slot = lane >> 4, L = lane & 15;
+    const float *xl = xs + L * stride;
+    float best_v = -INFINITY;
+    uint32_t best_i = 0xFFFFFFFFu;
+    for (uint32_t li = 0; li < n_list; li++) {
+        const uint32_t wgi = wg_list[li];
+        const uint32_t r0 = (uint32_t)((uint64_t)wgi * n_rowgroups / n_wg) * Q6K_GROUP_ROWS;
+        const uint32_t r1 = min((uint32_t)((uint64_t)(wgi + 1) * n_rowgroups / n_wg) * Q6K_GROUP_ROWS, n_rows);
+        for (uint32_t base = r0; base < r1; base += blockDim.x) {
+            const uint32_t row = base + tid;
+            if (row < r1 && (row == 0 || !(logits[row] + bound[row] < lb_max)))
+                cand[atomicAdd(&n_cand, 1u)] = row;
+            __syncthreads();
+            const uint32_t nc = n_cand;
+            // rescore once the list could overflow on the next pass, and at the end
+            const bool last = li + 1 == n_list && base + blockDim.x >= r1;
+            if (nc + blockDim.x > kSelectCap || (last && nc)) {
+                for (uint32_t c0 = wave * 4; c0 < nc; c0 += 4 * (kSelectBlock / 64)) {
+                    const uint32_t ci = min(c0 + slot, nc - 1);
+                    const uint32_t crow = cand[ci];
+                    const uint8_t *gbase =
+                        w + (uint64_t)(crow / Q6K_GROUP_ROWS) * n_blocks * Q6K_GROUP_BLOCK_BYTES;
+                    const uint32_t rr = crow % Q6K_GROUP_ROWS;
+                    const uint32_t off_q = (16 * rr + L) * 12,
+                                   off_sc = Q6K_SC_OFFSET + (rr * 4 + (L >> 2)) * 4,
+                                   off_d = Q6K_D_OFFSET + rr * 2;
+                    float acc = 0.0f;
+                    for (uint32_t b0 = 0; b0 < n_blocks; b0 += CH) {
+                        q6_lane_blocks<CH> v;
+                        q6_load_lane<CH>(v, gbase, b0, off_q, off_sc, off_d);
+                        q6_exact_accum<CH>(v, b0, xl, acc);
+                    }
+                    const float dot = q6_combine(acc);
+                    if (L == 0 && c0 + slot < nc) {
+                        logits[crow] = dot;
+                        if (crow == 0) s_f0 = dot;
+                        if (cand_better(dot, crow, best_v, best_i)) {
+                            best_v = dot;
+                            best_i = crow;
+                        }
+                    }
+                }
+                __syncthreads();
+                if (tid == 0) n_cand = 0;
+            }
+            __syncthreads();
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        float ov = __shfl_xor(best_v, o, 64);
+        uint32_t oi = __shfl_xor(best_i, o, 64);
+        if (cand_better(ov, oi, best_v, best_i)) {
+            best_v = ov;
+            best_i = oi;
+        }
+    }
+    if (lane == 0) s_c[wave] = argcand{best_v, best_i};
+    __syncthreads();
+    if (tid == 0) {
+        argcand bc = s_c[0];
+        for (int i = 1; i < kSelectBlock / 64; i++)
+            if (cand_better(s_c[i].v, s_c[i].i, bc.v, bc.i)) bc = s_c[i];
+        // a NaN logit at index 0 wins (the reference's scan starts from
+        // logits[0] and NaN compares false); all -inf/NaN keeps index 0
+        *argmax_out = (s_f0 != s_f0 || bc.i == 0xFFFFFFFFu) ? 0u : bc.i;
+    }
+}
+
+int pick_ch(uint32_t n_blocks) {
+    for (int ch : {10, 8, 5, 4, 2})
+        if (n_blocks % ch == 0) return ch;
+    return 1;
+}
+
+// Work buffer layout (all offsets 256-aligned).
+struct work_layout {
+    size_t cands, bound, wg_lb, wg_ub, total;
+};
+size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+work_layout layout_of(uint32_t n_rows) {
+    work_layout l;
+    size_t o = 0;
+    l.cands = o; o += al256(sizeof(argcand) * kMaxArgBlocks);
+    l.bound = o; o += al256((size_t)n_rows * 4);
+    l.wg_lb = o; o += al256(4 * kBoundedMaxBlocks);
+    l.wg_ub = o; o += al256(4 * kBoundedMaxBlocks);
+    l.total = o;
+    return l;
+}
+
+// Workgroups of the bounded pass: as many as fit on the device at once (one
+// round, each with a contiguous range of row groups), at most one per 4 groups.
+template <int CH>
+uint32_t bounded_blocks_for(uint32_t n_rowgroups, size_t lds) {
+    static int cached[16] = {0};
+    int dev = 0;
+    hipGetDevice(&dev);
+    int per = dev < 16 ? cached[dev] : 0;
+    if (per == 0) {
+        int occ = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_q6k_bounded<CH>, kBoundedBlock, lds) != hipSuccess || occ < 1)
+            occ = 1;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            cus = 256;
+        per = occ * cus;
+        if (dev < 16) cached[dev] = per;
+    }
+    uint32_t blocks = (n_rowgroups + 3) / 4;
+    if (blocks > (uint32_t)per) blocks = (uint32_t)per;
+    if (blocks > kBoundedMaxBlocks) blocks = kBoundedMaxBlocks;
+    return blocks ? blocks : 1;
+}
+
+template <int CH>
+uint32_t launch_bounded_ch(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
+                           uint32_t n_rowgroups, const float *hidden, float *approx, float *bound,
+                           float *wg_lb, float *wg_ub, hipStream_t s) {
+    const size_t lds = sizeof(q6k_xq) * 16 * n_blocks;
+    const uint32_t blocks = bounded_blocks_for<CH>(n_rowgroups, lds);
+    const float *sigma = reinterpret_cast<const float *>(w + wm_q6k_sigma_offset(n_rowgroups, n_blocks));
+    hipLaunchKernelGGL(k_q6k_bounded<CH>, dim3(blocks), dim3(kBoundedBlock), lds, s, w, n_blocks,
+                       n_rows, n_rowgroups, sigma, hidden, approx, bound, wg_lb, wg_ub);
+    return blocks;
+}
+
+template <int CH>
+void launch_argmax_fast_ch(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
+                           uint32_t n_rowgroups, const float *hidden, float *logits,
+                           uint32_t *argmax_out, void *work, hipStream_t s) {
+    const work_layout lay = layout_of(n_rows);
+    uint8_t *wb = (uint8_t *)work;
+    float *bound = reinterpret_cast<float *>(wb + lay.bound);
+    float *wg_lb = reinterpret_cast<float *>(wb + lay.wg_lb);
+    float *wg_ub = reinterpret_cast<float *>(wb + lay.wg_ub);
+    const uint32_t n_wg = launch_bounded_ch<CH>(w, n_blocks, n_rows, n_rowgroups, hidden, logits,
+                                                bound, wg_lb, wg_ub, s);
+    const size_t lds = sizeof(float) * 16 * xs_stride(n_blocks);
+    hipLaunchKernelGGL(k_q6k_select<CH>, dim3(1), dim3(kSelectBlock), lds, s, w, n_blocks, n_rows,
+                       n_rowgroups, hidden, logits, bound, wg_lb, wg_ub, n_wg, argmax_out);
+}
+
 }  // namespace
 
 void wm_launch_q6k_repack(const uint8_t *raw, uint8_t *out, uint32_t n_rows, uint32_t n_blocks,
@@ -248,6 +739,9 @@ void wm_launch_q6k_repack(const uint8_t *raw, uint8_t *out, uint32_t n_rows, uin
     if (blocks > 65535u * 4) blocks = 65535u * 4;
     hipLaunchKernelGGL(k_q6k_repack, dim3(blocks), dim3(256), 0, s, raw, out, n_rows, n_blocks,
                        n_rowgroups);
+    float *sigma = reinterpret_cast<float *>(out + wm_q6k_sigma_offset(n_rowgroups, n_blocks));
+    hipLaunchKernelGGL(k_q6k_row_sigma, dim3((n_rows + 255) / 256), dim3(256), 0, s, raw, n_rows,
+                       n_blocks, sigma);
 }
 
 void wm_launch_q6k_dequant_row(const uint8_t *w, uint32_t n_blocks, uint32_t row, float *out,
@@ -268,25 +762,68 @@ void wm_launch_q6k_dequant_rows_dev(const uint8_t *w, uint32_t n_blocks, const u
                        d_rows, out, ld);
 }
 
-size_t wm_q6k_logits_work_bytes() { return sizeof(argcand) * kMaxArgBlocks + 256; }
+size_t wm_q6k_logits_work_bytes(uint32_t n_rows, uint32_t n_blocks) {
+    (void)n_blocks;
+    return layout_of(n_rows).total;
+}
 
-// `work` holds the per-block candidates.  When logits == nullptr the first
-// logit is still needed for the NaN rule: the caller always passes a logits
-// buffer (the library keeps one per context/model).
+// Exact logits (bit-identical to the reference) + optional argmax.  The
+// logits buffer is required: the final argmax step reads logits[0] for the
+// NaN rule.
 void wm_launch_q6k_logits_argmax(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                                  uint32_t n_rowgroups, const float *hidden, float *logits,
                                  uint32_t *argmax_out, void *work, hipStream_t s) {
-    uint32_t waves = 256 * 8;  // 8 waves per CU
     uint32_t blocks = (n_rowgroups + 3) / 4;
-    uint32_t max_blocks = waves / 4;
+    const uint32_t max_blocks = 256 * 6;  // 24 waves per CU
     if (blocks > max_blocks) blocks = max_blocks;
-    if (blocks > (uint32_t)kMaxArgBlocks) blocks = kMaxArgBlocks;
     if (blocks == 0) blocks = 1;
-    size_t lds = sizeof(float) * 16 * (n_blocks * 16 + 4);
-    argcand *cands = reinterpret_cast<argcand *>(work);
-    hipLaunchKernelGGL(k_q6k_logits, dim3(blocks), dim3(kLogitsBlock), lds, s, w, n_blocks,
-                       n_rows, n_rowgroups, hidden, logits, cands);
+    const size_t lds = sizeof(float) * 16 * (n_blocks * 16 + 4);
+    argcand *cands = reinterpret_cast<argcand *>((uint8_t *)work + layout_of(n_rows).cands);
+#define WM_LOGITS_CASE(C)                                                                           \
+    case C:                                                                                         \
+        hipLaunchKernelGGL(k_q6k_logits<C>, dim3(blocks), dim3(kLogitsBlock), lds, s, w, n_blocks, \
+                           n_rows, n_rowgroups, hidden, logits, cands);                             \
+        break;
+    switch (pick_ch(n_blocks)) {
+        WM_LOGITS_CASE(10) WM_LOGITS_CASE(8) WM_LOGITS_CASE(5) WM_LOGITS_CASE(4)
+        WM_LOGITS_CASE(2) default: WM_LOGITS_CASE(1)
+    }
+#undef WM_LOGITS_CASE
     if (argmax_out)
         hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(64), 0, s, cands, blocks, logits,
                            argmax_out);
+}
+
+// Argmax only: the bounded pass, then selection + exact rescoring + argmax
+// in one workgroup.  `logits` (n_rows floats) receives the bounded pass's
+// values, exact on the rows that were rescored (always including row 0).
+void wm_launch_q6k_argmax_fast(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
+                               uint32_t n_rowgroups, const float *hidden, float *logits,
+                               uint32_t *argmax_out, void *work, hipStream_t s) {
+    switch (pick_ch(n_blocks)) {
+        case 10: launch_argmax_fast_ch<10>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out, work, s); break;
+        case 8: launch_argmax_fast_ch<8>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out, work, s); break;
+        case 5: launch_argmax_fast_ch<5>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out, work, s); break;
+        case 4: launch_argmax_fast_ch<4>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out, work, s); break;
+        case 2: launch_argmax_fast_ch<2>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out, work, s); break;
+        default: launch_argmax_fast_ch<1>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out, work, s); break;
+    }
+}
+
+// Test hook / measurement: the bounded pass alone (approximate logits and
+// their bounds).
+void wm_launch_q6k_bounded_only(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
+                                uint32_t n_rowgroups, const float *hidden, float *approx,
+                                float *bound_out, void *work, hipStream_t s) {
+    const work_layout lay = layout_of(n_rows);
+    float *wg_lb = reinterpret_cast<float *>((uint8_t *)work + lay.wg_lb);
+    float *wg_ub = reinterpret_cast<float *>((uint8_t *)work + lay.wg_ub);
+    switch (pick_ch(n_blocks)) {
+        case 10: launch_bounded_ch<10>(w, n_blocks, n_rows, n_rowgroups, hidden, approx, bound_out, wg_lb, wg_ub, s); break;
+        case 8: launch_bounded_ch<8>(w, n_blocks, n_rows, n_rowgroups, hidden, approx, bound_out, wg_lb, wg_ub, s); break;
+        case 5: launch_bounded_ch<5>(w, n_blocks, n_rows, n_rowgroups, hidden, approx, bound_out, wg_lb, wg_ub, s); break;
+        case 4: launch_bounded_ch<4>(w, n_blocks, n_rows, n_rowgroups, hidden, approx, bound_out, wg_lb, wg_ub, s); break;
+        case 2: launch_bounded_ch<2>(w, n_blocks, n_rows, n_rowgroups, hidden, approx, bound_out, wg_lb, wg_ub, s); break;
+        default: launch_bounded_ch<1>(w, n_blocks, n_rows, n_rowgroups, hidden, approx, bound_out, wg_lb, wg_ub, s); break;
+    }
 }

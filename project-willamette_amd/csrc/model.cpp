@@ -409,9 +409,9 @@ wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_s
     wm_launch_rmsnorm_rows(fin, M, s);
     if (next_tokens)
         for (uint32_t i = 0; i < n_seqs; i++)
-            wm_launch_q6k_logits_argmax(m->embd, m->embd_blocks, c.vocab_size, m->embd_rowgroups,
-                                        m->b_final + (size_t)last[i] * E, m->logits, m->b_next + i,
-                                        m->lm_work, s);
+            wm_launch_q6k_argmax_fast(m->embd, m->embd_blocks, c.vocab_size, m->embd_rowgroups,
+                                      m->b_final + (size_t)last[i] * E, m->logits, m->b_next + i,
+                                      m->lm_work, s);
     WM_HIP(ctx, hipGetLastError());
     uint32_t flag = 0;
     WM_HIP(ctx, hipMemcpyAsync(&flag, err, 4, hipMemcpyDeviceToHost, s));
@@ -453,7 +453,9 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
     if (c.n_embd % QK_I2S || c.n_ff % QK_I2S || c.n_embd % Q6K_VALUES)
         return wm_set_error(ctx, WM_E_SHAPE, "model config: n_embd/n_ff must be multiples of 256/128");
     // attention keeps a context's softmax weights in LDS (16 KB at 4096)
-    if (c.n_ff > 16384 || c.n_embd > 16384 || c.context_length > 4096)
+    // (the lm-head stages one hidden vector in LDS: n_embd <= 8192)
+    if (c.n_ff > 16384 || c.n_embd > WM_Q6K_LOGITS_MAX_BLOCKS * Q6K_VALUES ||
+        c.context_length > 4096 || c.vocab_size > WM_Q6K_LOGITS_MAX_ROWS)
         return wm_set_error(ctx, WM_E_SHAPE, "model config: dimensions beyond the supported range");
     WM_HIP(ctx, hipSetDevice(ctx->device));
     wm_model *m = new wm_model();
@@ -498,7 +500,7 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
         256,                                                      // meta[4]
         align256(part * 4),                                       // partial
         256,                                                      // device scalars
-        align256(wm_q6k_logits_work_bytes()),                     // lm-head work
+        align256(wm_q6k_logits_work_bytes(c.vocab_size, c.n_embd / Q6K_VALUES)),  // lm-head work
         align256(cs.size() * 4), align256(cs.size() * 4),         // rope tables
     };
     size_t total = 0;
@@ -746,8 +748,15 @@ wm_status wm_decode_step(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t 
     WM_HIP(ctx, hipSetDevice(ctx->device));
     WM_HIP(ctx, hipMemcpyAsync(m->dscalars, &token, 4, hipMemcpyHostToDevice, ctx->stream));
     enqueue_forward(m, kv, position, nullptr);
-    wm_launch_q6k_logits_argmax(m->embd, m->embd_blocks, m->cfg.vocab_size, m->embd_rowgroups,
-                                m->final_hidden, m->logits, m->dscalars + 1, m->lm_work, ctx->stream);
+    // logits wanted: all of them in the reference's order; else the id-only path
+    if (logits_out)
+        wm_launch_q6k_logits_argmax(m->embd, m->embd_blocks, m->cfg.vocab_size, m->embd_rowgroups,
+                                    m->final_hidden, m->logits, m->dscalars + 1, m->lm_work,
+                                    ctx->stream);
+    else
+        wm_launch_q6k_argmax_fast(m->embd, m->embd_blocks, m->cfg.vocab_size, m->embd_rowgroups,
+                                  m->final_hidden, m->logits, m->dscalars + 1, m->lm_work,
+                                  ctx->stream);
     WM_HIP(ctx, hipGetLastError());
     bool failed = false;
     if ((st = finish_step(m, kv, position, &failed))) return st;

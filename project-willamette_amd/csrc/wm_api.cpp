@@ -210,7 +210,7 @@ wm_status wm_tensor_upload_q6k(wm_ctx *ctx, const uint8_t *blocks, size_t len, u
     t->out_dim = n_rows;
     t->n_blocks = (uint32_t)(row_len / Q6K_VALUES);
     t->n_rowgroups = (uint32_t)((n_rows + Q6K_GROUP_ROWS - 1) / Q6K_GROUP_ROWS);
-    t->bytes = (size_t)t->n_rowgroups * t->n_blocks * Q6K_GROUP_BLOCK_BYTES;
+    t->bytes = wm_q6k_sigma_offset(t->n_rowgroups, t->n_blocks) + (size_t)n_rows * 4;
     void *raw = nullptr;
     hipError_t e = hipMalloc(&t->d, t->bytes);
     if (e == hipSuccess) e = hipMalloc(&raw, expected);
@@ -455,6 +455,18 @@ static wm_status check_q6k(wm_ctx *ctx, const wm_tensor *t) {
     return WM_OK;
 }
 
+// The lm-head kernels stage one row's worth of the hidden vector in LDS.
+static wm_status check_lm_head(wm_ctx *ctx, const wm_tensor *t) {
+    wm_status st = check_q6k(ctx, t);
+    if (st) return st;
+    if (t->n_blocks > WM_Q6K_LOGITS_MAX_BLOCKS || t->out_dim > WM_Q6K_LOGITS_MAX_ROWS)
+        return wm_set_error(ctx, WM_E_SHAPE,
+                            "compute_logits: lm-head [%llu, %llu] above the supported [%u, %u]",
+                            (unsigned long long)t->in_dim, (unsigned long long)t->out_dim,
+                            WM_Q6K_LOGITS_MAX_BLOCKS * Q6K_VALUES, WM_Q6K_LOGITS_MAX_ROWS);
+    return WM_OK;
+}
+
 wm_status wm_q6k_dequantize_row(wm_ctx *ctx, const wm_tensor *t, uint64_t row, float *out,
                                 size_t out_len) {
     wm_status st = check_q6k(ctx, t);
@@ -479,31 +491,36 @@ wm_status wm_q6k_dequantize_row(wm_ctx *ctx, const wm_tensor *t, uint64_t row, f
 
 wm_status wm_logits_argmax_dev(wm_ctx *ctx, const wm_tensor *t, const float *d_hidden,
                                float *d_logits, uint32_t *d_argmax) {
-    wm_status st = check_q6k(ctx, t);
+    wm_status st = check_lm_head(ctx, t);
     if (st) return st;
     if (!d_hidden || (!d_logits && !d_argmax)) return WM_E_ARG;
     const size_t lb = align256(t->out_dim * 4);
+    const size_t wb = wm_q6k_logits_work_bytes((uint32_t)t->out_dim, t->n_blocks);
     void *scratch;
-    if ((st = wm_ctx_scratch(ctx, lb + wm_q6k_logits_work_bytes(), &scratch))) return st;
-    float *logits = d_logits ? d_logits : (float *)scratch;
+    if ((st = wm_ctx_scratch(ctx, lb + wb, &scratch))) return st;
     void *work = (uint8_t *)scratch + lb;
     WM_HIP(ctx, hipSetDevice(ctx->device));
-    wm_launch_q6k_logits_argmax((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
-                                t->n_rowgroups, d_hidden, logits, d_argmax, work, ctx->stream);
+    if (d_logits)
+        wm_launch_q6k_logits_argmax((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
+                                    t->n_rowgroups, d_hidden, d_logits, d_argmax, work, ctx->stream);
+    else
+        wm_launch_q6k_argmax_fast((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
+                                  t->n_rowgroups, d_hidden, (float *)scratch, d_argmax, work,
+                                  ctx->stream);
     WM_HIP(ctx, hipGetLastError());
     return WM_OK;
 }
 
 wm_status wm_logits_argmax(wm_ctx *ctx, const wm_tensor *t, const float *hidden,
                            size_t hidden_len, float *logits, uint32_t *argmax) {
-    wm_status st = check_q6k(ctx, t);
+    wm_status st = check_lm_head(ctx, t);
     if (st) return st;
     if (!hidden || (!logits && !argmax)) return WM_E_ARG;
     if (hidden_len != t->in_dim)
         return wm_set_error(ctx, WM_E_SHAPE, "compute_logits: final_hidden.len()=%zu != embedding_length=%llu",
                             hidden_len, (unsigned long long)t->in_dim);
     const size_t hb = align256(t->in_dim * 4), lb = align256(t->out_dim * 4);
-    const size_t need = hb + lb + 256 + lb + wm_q6k_logits_work_bytes();
+    const size_t need = hb + lb + 256 + wm_q6k_logits_work_bytes((uint32_t)t->out_dim, t->n_blocks);
     void *scratch;
     if ((st = wm_ctx_scratch(ctx, need, &scratch))) return st;
     uint8_t *base = (uint8_t *)scratch;
@@ -513,8 +530,14 @@ wm_status wm_logits_argmax(wm_ctx *ctx, const wm_tensor *t, const float *hidden,
     void *work = base + hb + lb + 256;
     WM_HIP(ctx, hipSetDevice(ctx->device));
     WM_HIP(ctx, hipMemcpyAsync(d_h, hidden, t->in_dim * 4, hipMemcpyHostToDevice, ctx->stream));
-    wm_launch_q6k_logits_argmax((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
-                                t->n_rowgroups, d_h, d_l, d_a, work, ctx->stream);
+    // Logits wanted: every row in the reference's exact order.  Only the id
+    // wanted: the bounded pass plus exact rescoring of the rows that can win.
+    if (logits)
+        wm_launch_q6k_logits_argmax((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
+                                    t->n_rowgroups, d_h, d_l, d_a, work, ctx->stream);
+    else
+        wm_launch_q6k_argmax_fast((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
+                                  t->n_rowgroups, d_h, d_l, d_a, work, ctx->stream);
     WM_HIP(ctx, hipGetLastError());
     if (logits)
         WM_HIP(ctx, hipMemcpyAsync(logits, d_l, t->out_dim * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -522,6 +545,46 @@ wm_status wm_logits_argmax(wm_ctx *ctx, const wm_tensor *t, const float *hidden,
     WM_HIP(ctx, hipMemcpyAsync(&a, d_a, 4, hipMemcpyDeviceToHost, ctx->stream));
     WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     if (argmax) *argmax = a;
+    return WM_OK;
+}
+
+wm_status wm_debug_q6k_bounded_logits_dev(wm_ctx *ctx, const wm_tensor *t, const float *d_hidden,
+                                          float *d_approx, float *d_bound) {
+    wm_status st = check_lm_head(ctx, t);
+    if (st) return st;
+    if (!d_hidden || !d_approx || !d_bound) return WM_E_ARG;
+    void *work;
+    if ((st = wm_ctx_scratch(ctx, wm_q6k_logits_work_bytes((uint32_t)t->out_dim, t->n_blocks), &work)))
+        return st;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    wm_launch_q6k_bounded_only((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
+                               t->n_rowgroups, d_hidden, d_approx, d_bound, work, ctx->stream);
+    WM_HIP(ctx, hipGetLastError());
+    return WM_OK;
+}
+
+wm_status wm_debug_q6k_bounded_logits(wm_ctx *ctx, const wm_tensor *t, const float *hidden,
+                                      size_t hidden_len, float *approx, float *bound) {
+    wm_status st = check_lm_head(ctx, t);
+    if (st) return st;
+    if (!hidden || !approx || !bound) return WM_E_ARG;
+    if (hidden_len != t->in_dim)
+        return wm_set_error(ctx, WM_E_SHAPE, "compute_logits: final_hidden.len()=%zu != embedding_length=%llu",
+                            hidden_len, (unsigned long long)t->in_dim);
+    const size_t hb = align256(t->in_dim * 4), lb = align256(t->out_dim * 4);
+    const size_t need = hb + 2 * lb + wm_q6k_logits_work_bytes((uint32_t)t->out_dim, t->n_blocks);
+    void *scratch;
+    if ((st = wm_ctx_scratch(ctx, need, &scratch))) return st;
+    uint8_t *base = (uint8_t *)scratch;
+    float *d_h = (float *)base, *d_a = (float *)(base + hb), *d_b = (float *)(base + hb + lb);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    WM_HIP(ctx, hipMemcpyAsync(d_h, hidden, t->in_dim * 4, hipMemcpyHostToDevice, ctx->stream));
+    wm_launch_q6k_bounded_only((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
+                               t->n_rowgroups, d_h, d_a, d_b, base + hb + 2 * lb, ctx->stream);
+    WM_HIP(ctx, hipGetLastError());
+    WM_HIP(ctx, hipMemcpyAsync(approx, d_a, t->out_dim * 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipMemcpyAsync(bound, d_b, t->out_dim * 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return WM_OK;
 }
 

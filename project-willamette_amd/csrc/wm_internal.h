@@ -79,6 +79,12 @@ constexpr int Q6K_GROUP_ROWS = 4;         // rows per wave in the device layout
 constexpr int Q6K_GROUP_BLOCK_BYTES = 840;  // 4 rows x 210 bytes
 constexpr int Q6K_SC_OFFSET = 768;          // per (group, block): q6 768 B, sc 64 B, d 8 B
 constexpr int Q6K_D_OFFSET = 832;
+// After the 4-row-group layout, 256-aligned: one f32 per row holding
+// sum_j |d * sc_j| rounded up (x-independent part of the id-only lm-head's
+// error bound).  Part of the same allocation, so copies of the tensor carry it.
+__host__ __device__ inline size_t wm_q6k_sigma_offset(uint32_t n_rowgroups, uint32_t n_blocks) {
+    return ((size_t)n_rowgroups * n_blocks * Q6K_GROUP_BLOCK_BYTES + 255) & ~(size_t)255;
+}
 
 // ---------------------------------------------------------------------------
 // device helpers
@@ -130,6 +136,18 @@ __device__ __forceinline__ uint4 wm_load_stream(const void *p) {
 __device__ __forceinline__ uint32_t wm_load_stream_u32(const void *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
 }
+
+// Buffer resource for raw (unformatted) loads from `bytes` bytes at `base`;
+// base must be wave-uniform (the descriptor lives in SGPRs).  Loads take a
+// per-lane 32-bit offset plus a wave-uniform one, so streaming kernels spend
+// no vector instructions on addresses; a lane offset at or past `bytes`
+// reads zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t wm_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+constexpr int WM_LOAD_NT = 2;  // cache policy bits of a buffer load: non-temporal
+typedef unsigned int wm_v3u __attribute__((ext_vector_type(3)));
 
 // Wave-level helpers (wave64).
 __device__ __forceinline__ int wm_wave_sum_i32(int v) {
@@ -233,6 +251,7 @@ void wm_launch_i2s_finalize_multi(const int32_t *partial, uint32_t split, uint32
                                   hipStream_t s);
 
 // Q6_K
+// (also writes the per-row sigma array at out + wm_q6k_sigma_offset)
 void wm_launch_q6k_repack(const uint8_t *raw, uint8_t *out, uint32_t n_rows, uint32_t n_blocks,
                           uint32_t n_rowgroups, hipStream_t s);
 void wm_launch_q6k_dequant_row(const uint8_t *w, uint32_t n_blocks, uint32_t row, float *out,
@@ -242,11 +261,26 @@ void wm_launch_q6k_dequant_row_dev(const uint8_t *w, uint32_t n_blocks, const ui
 // n_rows rows, row i = d_rows[i], written to out + i * ld
 void wm_launch_q6k_dequant_rows_dev(const uint8_t *w, uint32_t n_blocks, const uint32_t *d_rows,
                                     uint32_t n_rows, float *out, uint32_t ld, hipStream_t s);
-// logits (exact SSE2 order) + per-block argmax candidates + final argmax.
+// Largest row length (in 256-value blocks) the lm-head kernels stage in LDS,
+// and the most rows they take.
+constexpr uint32_t WM_Q6K_LOGITS_MAX_BLOCKS = 32;
+constexpr uint32_t WM_Q6K_LOGITS_MAX_ROWS = 2048u * 2048u;
+// logits (exact SSE2 order, required) + per-block argmax candidates + final
+// argmax (argmax_out nullable).
 void wm_launch_q6k_logits_argmax(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                                  uint32_t n_rowgroups, const float *hidden, float *logits,
                                  uint32_t *argmax_out, void *work, hipStream_t s);
-size_t wm_q6k_logits_work_bytes();
+// argmax only: bounded fixed-point pass + exact rescoring of the rows that
+// can still be the maximum.  logits (n_rows) receives the bounded values,
+// exact on the rescored rows.
+void wm_launch_q6k_argmax_fast(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
+                               uint32_t n_rowgroups, const float *hidden, float *logits,
+                               uint32_t *argmax_out, void *work, hipStream_t s);
+// test hook: the bounded pass alone (values and their error bounds)
+void wm_launch_q6k_bounded_only(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
+                                uint32_t n_rowgroups, const float *hidden, float *approx,
+                                float *bound_out, void *work, hipStream_t s);
+size_t wm_q6k_logits_work_bytes(uint32_t n_rows, uint32_t n_blocks);
 
 // ---------------------------------------------------------------------------
 // ragged multi-sequence batch

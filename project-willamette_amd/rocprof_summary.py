@@ -11,8 +11,8 @@ WRITE_SIZE; both report KiB per dispatch) into HBM bytes per launch of one
 kernel.  Each counter is scaled by what it reads for the largest
 device-to-device copy in the same run (`copy-bytes` read and written), so the
 figure is in bytes the memory system actually moved.  With --record, the
-result is stored under the kernel source file's name together with the
-SHA-256 of that file, so that a later benchmark uses it only while the kernel
+result is stored under the kernel's name together with its source file and
+that file's SHA-256, so that a later benchmark uses it only while the kernel
 is unchanged.
 """
 from __future__ import annotations
@@ -75,7 +75,7 @@ def traffic(args) -> str:
         rec_path = Path(args.record)
         rec = json.loads(rec_path.read_text()) if rec_path.exists() else {}
         src = Path(args.source)
-        rec[src.name] = {"kernel": args.kernel, "bytes_per_launch": round(total),
+        rec[args.kernel] = {"source": src.name, "bytes_per_launch": round(total),
                          "fetch_bytes": round(fetch_b), "write_bytes": round(write_b),
                          "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
                          "source_sha256": hashlib.sha256(src.read_bytes()).hexdigest()}

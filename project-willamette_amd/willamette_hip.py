@@ -134,6 +134,8 @@ EXPORTS = {
                            _u32p),
     "wm_batch_forward": (C.c_int, _vp, C.POINTER(_vp), C.c_uint32, _u32p, _u32p, _f32p, _u32p),
     "wm_debug_seq_sum": (C.c_int, _vp, _f32p, C.c_size_t, _f32p),
+    "wm_debug_q6k_bounded_logits": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p, _f32p),
+    "wm_debug_q6k_bounded_logits_dev": (C.c_int, _vp, _vp, _vp, _vp, _vp),
     "wm_synth_stream_seed": (C.c_uint64, C.c_uint64, C.c_uint64),
     "wm_synth_i2s": (None, C.c_uint64, C.c_uint64, _u8p, C.c_size_t),
     "wm_synth_normal": (None, C.c_uint64, C.c_uint64, _f32p, C.c_size_t, C.c_double),
@@ -382,3 +384,14 @@ def logits_argmax(ctx: Context, t: Tensor, hidden: np.ndarray, want_logits: bool
     ctx.check(lib.wm_logits_argmax(ctx.h, t.h, _ptr(hidden, C.c_float), hidden.size,
                                    _ptr(out, C.c_float) if out is not None else None, C.byref(a)))
     return out, int(a.value)
+
+
+def q6k_bounded_logits(ctx: Context, t: Tensor, hidden: np.ndarray):
+    """The id-only lm-head's bounded pass (test hook): per row the
+    fixed-point dot and a bound on its distance from the reference's logit."""
+    hidden = np.ascontiguousarray(hidden, dtype=np.float32)
+    approx = np.empty(t.shape[1], dtype=np.float32)
+    bound = np.empty(t.shape[1], dtype=np.float32)
+    ctx.check(lib.wm_debug_q6k_bounded_logits(ctx.h, t.h, _ptr(hidden, C.c_float), hidden.size,
+                                              _ptr(approx, C.c_float), _ptr(bound, C.c_float)))
+    return approx, bound
