@@ -87,12 +87,15 @@ def lm_head_kernels(ctx, wh, hm, cfg, reps: int):
     logits, bound, amax = ctx.alloc(cfg.vocab * 4), ctx.alloc(cfg.vocab * 4), ctx.alloc(256)
     runs = {
         "bounded": lambda t: wh.lib.wm_debug_q6k_bounded_logits_dev(ctx.h, t.h, h.ptr, logits.ptr,
-                                                                    bound.ptr),
+                                                                    bound.ptr, 1),
         "id_only": lambda t: wh.lib.wm_logits_argmax_dev(ctx.h, t.h, h.ptr, None, amax.ptr),
         "exact": lambda t: wh.lib.wm_logits_argmax_dev(ctx.h, t.h, h.ptr, logits.ptr, None),
     }
     timer = HipTimer(ctx.stream)
     out = {}
+    # the fixed-point copy of h that the "bounded" runs reuse (the decode step's
+    # output_norm kernel makes it as a by-product)
+    ctx.check(wh.lib.wm_debug_q6k_bounded_logits_dev(ctx.h, ts[0].h, h.ptr, logits.ptr, bound.ptr, 0))
     for name, run in runs.items():
         for i in range(4):
             ctx.check(run(ts[i & 1]))
@@ -248,7 +251,7 @@ def probe(kind: str, reps: int):
             turn[0] += 1
             if kind == "lm_head":  # the id-only path's bounded pass
                 ctx.check(wh.lib.wm_debug_q6k_bounded_logits_dev(ctx.h, t.h, h.ptr, logits.ptr,
-                                                                 bound.ptr))
+                                                                 bound.ptr, turn[0] > 1))
             else:
                 ctx.check(wh.lib.wm_logits_argmax_dev(ctx.h, t.h, h.ptr, logits.ptr, None))
     elif kind == "i2s":

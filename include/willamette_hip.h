@@ -264,10 +264,13 @@ wm_status wm_debug_seq_sum(wm_ctx *ctx, const float *values, size_t n, float *su
 wm_status wm_debug_q6k_bounded_logits(wm_ctx *ctx, const wm_tensor *token_embd,
                                       const float *hidden, size_t hidden_len, float *approx,
                                       float *bound);
-/* Device-pointer form, asynchronous: one launch of the bounded pass (the
- * kernel the id-only lm-head spends its time in), for timing it alone. */
+/* Device-pointer form, asynchronous, for timing the bounded pass (the kernel
+ * the id-only lm-head spends its time in) alone: with reuse_prep != 0 the
+ * fixed-point copy of the hidden vector made by the previous call on this
+ * context (same tensor shape) is reused and only the pass itself runs. */
 wm_status wm_debug_q6k_bounded_logits_dev(wm_ctx *ctx, const wm_tensor *token_embd,
-                                          const float *d_hidden, float *d_approx, float *d_bound);
+                                          const float *d_hidden, float *d_approx, float *d_bound,
+                                          int reuse_prep);
 
 /* ---- synthetic BitNet-shaped inputs (src/synth.rs) ------------------- */
 

@@ -16,6 +16,7 @@
 // products, exp, the quantisation) runs across all lanes; only the adds of
 // the chain are serial.  Maxima and integer sums are order-free.
 #include "wm_internal.h"
+#include "wm_q6k_xprep.h"
 #include "wm_seqsum.h"
 
 namespace {
@@ -40,7 +41,7 @@ template <int PER>  // values per thread: n <= PER * 1024
 __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
     float *__restrict__ x, residual_src res, const float *__restrict__ w, uint32_t n, float eps,
     uint8_t *__restrict__ act, wm_act_meta *__restrict__ meta_out, float *__restrict__ y_out,
-    uint32_t *__restrict__ err_flag, uint32_t layer_tag) {
+    uint32_t *__restrict__ err_flag, uint32_t layer_tag, uint8_t *__restrict__ q6k_prep) {
     extern __shared__ __align__(16) float sq[];  // x[j]*x[j], wm::seq_sum_padded(n) entries
     __shared__ float red_f[16];
     __shared__ int red_i[16];
@@ -114,7 +115,16 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
             m = wm_max_nonan(m, fabsf(xv[i]));
         }
     }
-    if (y_out) return;
+    if (y_out) {
+        // output_norm: also the fixed-point copy the id-only lm-head reads
+        if (q6k_prep) {
+            __syncthreads();  // y_out complete
+            const q6k_xhdr h = q6k_xprep_block(y_out, n / Q6K_VALUES,
+                                               reinterpret_cast<q6k_xq *>(q6k_prep), red_f, red_i);
+            if (tid == 0) *reinterpret_cast<q6k_xhdr *>(q6k_prep + q6k_xq_bytes(n / Q6K_VALUES)) = h;
+        }
+        return;
+    }
     // per-vector absmax int8 (src/model/bitlinear_sse2.rs:285-304)
     const float max_abs = wm_block_max_nonan(m, red_f);
     int sum = 0;
@@ -284,14 +294,14 @@ void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, u
                              uint32_t row0, float w_scale, const wm_act_meta *meta_in,
                              const float *w, uint32_t n, float eps, uint8_t *act,
                              wm_act_meta *meta_out, float *y_out, uint32_t *err_flag,
-                             uint32_t layer_tag, hipStream_t s) {
+                             uint32_t layer_tag, void *q6k_prep, hipStream_t s) {
     residual_src res{partial, split, rows_total, row0, w_scale, meta_in};
     size_t lds = (size_t)wm::seq_sum_padded(n) * sizeof(float);
     const int per = (int)((n + kNormThreads - 1) / kNormThreads);
 #define WM_NORM_CASE(P)                                                                            \
     case P:                                                                                        \
         hipLaunchKernelGGL(k_rmsnorm_quant<P>, dim3(1), dim3(kNormThreads), lds, s, x, res, w, n,  \
-                           eps, act, meta_out, y_out, err_flag, layer_tag);                        \
+                           eps, act, meta_out, y_out, err_flag, layer_tag, (uint8_t *)q6k_prep);  \
         break;
     switch (per) {
         WM_NORM_CASE(1) WM_NORM_CASE(2) WM_NORM_CASE(3) WM_NORM_CASE(4)

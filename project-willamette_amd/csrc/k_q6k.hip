@@ -18,14 +18,13 @@
 //
 // Device layout (k_q6k_repack): rows in groups of 4; per (group, block) 840
 // bytes, the same byte count as the GGUF blocks:
-//   bytes 0..767   lane L' = 16*row + 4k + l holds, in 3 dwords, the 16
-//                  six-bit quants it consumes in this block, step s = 4*hn + c
-//                  (hn = 2*half + band, c = chunk):
-//                    dword 0: low nibbles of s = 0..7  at bits 8c + 4(hn & 1)
-//                    dword 1: low nibbles of s = 8..15 at bits 8c + 4(hn & 1)
-//                    dword 2: high bit pairs, byte c bits 2hn..2hn+1
-//                  so that four AND/OR operations per dword rebuild the
-//                  quants as bytes: byte c of U[hn] = q(4*hn + c);
+//   bytes 0..767   lane L' = 16*row + 4k + l holds, in 3 dwords A, B, C, the
+//                  16 six-bit quants it consumes in this block, q(hn, c) for
+//                  hn = 2*half + band, c = chunk: byte c of A / B / C holds
+//                  q(0, c) / q(1, c) / q(2, c) in bits 0-5, and bits 6-7 of
+//                  the three bytes hold q(3, c)'s bits 0-1 / 2-3 / 4-5; so
+//                  the quants come back as bytes (byte c of U[hn] = q(hn, c))
+//                  with three ANDs and six shift/AND-OR operations;
 //   bytes 768..831 per row the 16 sub-scales as 4 dwords (dword k, byte hn =
 //                  sc[8h + band + 2k]);
 //   bytes 832..839 the 4 f16 d values.
@@ -43,6 +42,7 @@
 #include <hip/hip_fp16.h>
 
 #include "wm_internal.h"
+#include "wm_q6k_xprep.h"
 
 namespace {
 
@@ -50,6 +50,7 @@ constexpr int kLogitsBlock = 256;  // 4 waves
 constexpr int kMaxArgBlocks = 2048;
 constexpr int kBoundedBlock = 256;
 constexpr uint32_t kBoundedMaxBlocks = 2048;
+constexpr bool kPipelined = true;
 
 __host__ __device__ __forceinline__ int q6_of(const uint8_t *blk, int h, int k, int l) {
     const uint8_t *ql = blk + h * 64, *qh = blk + 128 + h * 32;
@@ -84,11 +85,12 @@ __global__ void k_q6k_repack(const uint8_t *__restrict__ raw, uint8_t *__restric
         for (int k = 0; k < 4; k++) {
             for (int l = 0; l < 4; l++) {
                 uint32_t w[3] = {0, 0, 0};
-                for (int s = 0; s < 16; s++) {
-                    const int hn = s >> 2, c = s & 3, h = hn >> 1, n = hn & 1;
-                    const uint32_t v = (uint32_t)q6_of(blk, h, k, n * 16 + c * 4 + l);
-                    w[s >> 3] |= (v & 15u) << (8 * c + 4 * (hn & 1));
-                    w[2] |= (v >> 4) << (8 * c + 2 * hn);
+                for (int c = 0; c < 4; c++) {
+                    uint32_t q[4];
+                    for (int hn = 0; hn < 4; hn++)
+                        q[hn] = (uint32_t)q6_of(blk, hn >> 1, k, (hn & 1) * 16 + c * 4 + l);
+                    for (int t = 0; t < 3; t++)
+                        w[t] |= (q[t] | (((q[3] >> (2 * t)) & 3u) << 6)) << (8 * c);
                 }
                 const int L = r * 16 + k * 4 + l;
                 q6[L * 3 + 0] = w[0]; q6[L * 3 + 1] = w[1]; q6[L * 3 + 2] = w[2];
@@ -104,13 +106,19 @@ __global__ void k_q6k_repack(const uint8_t *__restrict__ raw, uint8_t *__restric
     }
 }
 
-// The 16 quants of one lane as 4 dwords of bytes: byte c of U[hn] = q(4hn + c).
-__device__ __forceinline__ void q6_unpack(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t U[4]) {
-    const uint32_t m = 0x0F0F0F0Fu, mh = 0x30303030u;
-    U[0] = (w0 & m) | ((w2 << 4) & mh);
-    U[1] = ((w0 >> 4) & m) | ((w2 << 2) & mh);
-    U[2] = (w1 & m) | (w2 & mh);
-    U[3] = ((w1 >> 4) & m) | ((w2 >> 2) & mh);
+// The 16 quants of one lane as 4 dwords of bytes: byte c of U[hn] = q(hn, c).
+__device__ __forceinline__ void q6_unpack(uint32_t a, uint32_t b, uint32_t c, uint32_t U[4]) {
+    const uint32_t m = 0x3F3F3F3Fu;
+    U[0] = a & m;
+    U[1] = b & m;
+    U[2] = c & m;
+    U[3] = ((a >> 6) & 0x03030303u) | ((b >> 4) & 0x0C0C0C0Cu) | ((c >> 2) & 0x30303030u);
+}
+// One quant q(hn, c) of a lane's three dwords.
+__device__ __forceinline__ uint32_t q6_get(const uint32_t *w, int hn, int c) {
+    if (hn < 3) return (w[hn] >> (8 * c)) & 63u;
+    const int s = 8 * c + 6;
+    return ((w[0] >> s) & 3u) | (((w[1] >> s) & 3u) << 2) | (((w[2] >> s) & 3u) << 4);
 }
 
 // Dequantise row values: thread t of 256 handles value t of each block.
@@ -127,9 +135,8 @@ __global__ void k_q6k_dequant_row(const uint8_t *__restrict__ w, uint32_t n_bloc
     const int h = t >> 7, k = (t >> 5) & 3, n = (t >> 4) & 1, c = (t >> 2) & 3, l = t & 3;
     const int L = r * 16 + k * 4 + l, hn = h * 2 + n;
     const uint32_t *q6 = reinterpret_cast<const uint32_t *>(base) + L * 3;
-    const uint32_t lo = (q6[hn >> 1] >> (8 * c + 4 * (hn & 1))) & 15u;
-    const uint32_t hi = (q6[2] >> (8 * c + 2 * hn)) & 3u;
-    const uint32_t q = lo | (hi << 4);
+    const uint32_t wl[3] = {q6[0], q6[1], q6[2]};
+    const uint32_t q = q6_get(wl, hn, c);
     const uint32_t scw = reinterpret_cast<const uint32_t *>(base + Q6K_SC_OFFSET)[r * 4 + k];
     const int sc = (int)(int8_t)(scw >> (8 * hn));
     const float d = wm_f16_bits_to_f32(reinterpret_cast<const uint16_t *>(base + Q6K_D_OFFSET)[r]);
@@ -340,22 +347,6 @@ __global__ void k_argmax_final(const argcand *__restrict__ cands, uint32_t n_can
 // argmax-only path
 // ---------------------------------------------------------------------------
 
-// The hidden vector as 16-bit fixed point, x_i ~ 2^e * X_i with
-// X_i = rint(x_i * 2^-e), |X_i| <= 32639, split X = 256*xh + xl into two int8
-// (xh = (X + 128) >> 8, xl = X - 256*xh in [-128, 127]).  Entry (b, p) holds,
-// for lane position p = 4k + l of block b and group hn, the four values that
-// meet byte c of that lane's U[hn]: xh and xl packed as int8x4 and
-// c[hn] = -32 * sum_c X (which folds the quants' offset of 32 into the dot).
-struct q6k_xq {
-    int xh[4], xl[4], c[4];
-};
-struct q6k_xhdr {
-    int e;          // scale exponent
-    uint32_t ok;    // 0: the hidden vector holds a NaN or an infinity
-    float bound_k;  // row bound = bound_k * sigma_r, sigma_r = sum_j |d * sc_j|
-    float mag_k;    // row magnitude bound factor (overflow guard)
-};
-
 // sigma_r = sum over the row's blocks b and sub-blocks j of |d_b * sc_bj|,
 // from the raw GGUF blocks, in double and rounded up to f32 (non-finite d
 // gives a non-finite sigma, which makes the row a rescoring candidate).
@@ -374,71 +365,6 @@ __global__ void k_q6k_row_sigma(const uint8_t *__restrict__ raw, uint32_t n_rows
     sigma[row] = (float)(s * (1.0 + 0x1p-20));
 }
 
-// Build the fixed-point copy of hidden[n_blocks*256] in LDS (xq[n_blocks*16])
-// and the bound factors, by the whole workgroup.  Every workgroup of the
-// bounded pass does this for itself (the 10 KB vector stays in L2), so the
-// pass needs no preparatory launch.
-__device__ q6k_xhdr xprep_block(const float *__restrict__ hidden, uint32_t n_blocks, q6k_xq *xq,
-                                float *red, int *redi) {
-    const uint32_t n = n_blocks * 256, tid = threadIdx.x;
-    float m = 0.0f;
-    int bad = 0;
-    for (uint32_t i = tid; i < n; i += blockDim.x) {
-        const float v = hidden[i];
-        bad |= !isfinite(v);
-        m = fmaxf(m, fabsf(v));
-    }
-    const float maxabs = wm_block_max_nonan(m, red);
-    bad = wm_block_sum_i32(bad, redi);
-    // smallest e with maxabs * 2^-e <= 32639, kept >= -140 so 2^e stays representable
-    int e = 0;
-    if (maxabs > 0.0f && !bad) {
-        int E;
-        frexpf(maxabs, &E);  // maxabs < 2^E
-        e = E - 15;
-        if (ldexpf(maxabs, -e) > 32639.0f) e++;
-        if (e < -140) e = -140;
-    }
-    for (uint32_t idx = tid; idx < n_blocks * 64; idx += blockDim.x) {
-        const uint32_t b = idx >> 6, p = (idx >> 2) & 15, hn = idx & 3;
-        const uint32_t k = p >> 2, l = p & 3, h = hn >> 1, band = hn & 1;
-        const float *src = hidden + b * 256 + h * 128 + k * 32 + band * 16 + l;
-        uint32_t ph = 0, pl = 0;
-        int sum = 0;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int v = bad ? 0 : (int)rintf(ldexpf(src[c * 4], -e));
-            const int xh = (v + 128) >> 8, xl = v - 256 * xh;
-            ph |= (uint32_t)(xh & 0xFF) << (8 * c);
-            pl |= (uint32_t)(xl & 0xFF) << (8 * c);
-            sum += v;
-        }
-        q6k_xq &o = xq[b * 16 + p];
-        o.xh[hn] = (int)ph;
-        o.xl[hn] = (int)pl;
-        o.c[hn] = -32 * sum;
-    }
-    // Distance between the bounded pass and the reference's f32 dot, per
-    // unit of sigma_r = sum_j |S_j| (S_j = d * sc_j, 16 values per sub-block,
-    // |q - 32| <= 32, so a row's sum_i |(q-32) * S * y_i| <= 512 * max|y| * sigma_r):
-    //  - fixed point: |x - 2^e X| <= 2^(e-1): 2^(e+8) * sigma_r;
-    //  - this pass's f32 work (i32 -> f32, n_blocks fmas, 4 tree adds), on
-    //    terms |d * T| with |2^e X| <= maxabs + 2^(e-1):
-    //    gamma_(nb+5) * 512 * (maxabs + 2^(e-1)) * sigma_r;
-    //  - the reference's f32 work (one product rounding, 16*nb - 1
-    //    sequential adds, 4 combine adds): gamma_(16nb+5) * 512 * maxabs * sigma_r.
-    const double u = 0x1p-24;
-    const double gA = (n_blocks + 6) * u * 1.01, gB = (16.0 * n_blocks + 6) * u * 1.01;
-    const double half_ulp = ldexp(1.0, e - 1);
-    const double k = ldexp(1.0, e + 8) + 512.0 * (gA * ((double)maxabs + half_ulp) + gB * (double)maxabs);
-    q6k_xhdr hd;
-    hd.e = e;
-    hd.ok = bad ? 0u : 1u;
-    hd.bound_k = (float)(k * (1.0 + 0x1p-16));
-    hd.mag_k = (float)(512.0 * ((double)maxabs + half_ulp) * (1.0 + 0x1p-16));
-    return hd;
-}
-
 // d = a * b + c on the low 24 bits of a and b (sign-extended), low 32 bits of
 // the result: one full-rate v_mad_i32_i24.  (For this use the compiler emits a
 // quarter-rate 32-bit multiply.)  The operands must come from ordinary VALU
@@ -450,24 +376,63 @@ __device__ __forceinline__ int mad_i24(int a, int b, int c) {
     return d;
 }
 
+// The prep area from a hidden vector in device memory (one workgroup).
+__global__ __launch_bounds__(256) void k_q6k_xprep(const float *__restrict__ hidden,
+                                                   uint32_t n_blocks, uint8_t *__restrict__ prep) {
+    __shared__ float red[4];
+    __shared__ int redi[4];
+    const q6k_xhdr h = q6k_xprep_block(hidden, n_blocks, reinterpret_cast<q6k_xq *>(prep), red, redi);
+    if (threadIdx.x == 0) *reinterpret_cast<q6k_xhdr *>(prep + q6k_xq_bytes(n_blocks)) = h;
+}
+
+// One lane's contribution to its row's bounded dot over blocks b0..b0+CH-1:
+// per group hn two int8 dots of the bytes U[hn] with xh and xl,
+// I = 256*dh + dl (exact, |I| < 2^23), T = sum_hn sc_hn * I (exact,
+// |T| < 2^31), acc += d * T in f32.
+template <int CH>
+__device__ __forceinline__ void q6_bounded_accum(const q6_lane_blocks<CH> &v, uint32_t b0,
+                                                 const q6k_xq *xq, uint32_t p, float &acc) {
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+        uint32_t U[4];
+        q6_unpack(v.w0[j], v.w1[j], v.w2[j], U);
+        const q6k_xq &xv = xq[(b0 + j) * 16 + p];
+        int T = 0;
+#pragma unroll
+        for (int hn = 0; hn < 4; hn++) {
+            const int sc = (int)(int8_t)(v.scw[j] >> (8 * hn));
+            // (clamp selects the three-operand encoding, which needs no zeroed
+            // accumulator register; |dh| <= 32256 never saturates)
+            const int dh = __builtin_amdgcn_sdot4((int)U[hn], xv.xh[hn], 0, true);
+            const int dl = __builtin_amdgcn_sdot4((int)U[hn], xv.xl[hn], xv.c[hn], false);
+            const int I = (int)(((uint32_t)dh << 8) + (uint32_t)dl);  // a VALU result
+            T = mad_i24(sc, I, T);
+        }
+        const float d = __half2float(__ushort_as_half((unsigned short)v.db[j]));
+        acc = __builtin_fmaf(d, (float)T, acc);
+    }
+}
+
 // Bounded pass.  Workgroup w takes the 4-row groups [g0, g1) (contiguous, so
 // its rows form one range), its waves taking them in turn.  Lane (r, p =
 // 4k + l) of a wave handles the same 16 quants per block as in the exact
-// kernel; per group hn it takes two int8 dots of the bytes U[hn] with xh and
-// xl, I = 256*dh + dl (exact, |I| < 2^23), and T = sum_hn sc_hn * I (exact,
-// |T| < 2^31); then acc += d * T in f32.  Per row: logit ~ 2^e * sum of the
-// 16 lanes' acc, bound = bound_k * sigma_r, widened so that rounding a +-
-// bound in f32 cannot cross the true interval.  The workgroup's largest
-// lower and upper bounds go to wg_lb / wg_ub.
-template <int CH>
+// kernel (q6_bounded_accum).  Per row: logit ~ 2^e * sum of the 16 lanes'
+// acc, bound = bound_k * sigma_r, widened so that rounding a +- bound in f32
+// cannot cross the true interval.  The workgroup's largest lower and upper
+// bounds go to wg_lb / wg_ub.  PIPE: loads go in batches of CH blocks, the
+// next batch (of this group or the wave's next one) in flight while the
+// current one is reduced, so every wave keeps memory busy between its
+// reductions (two register sets of CH blocks).
+template <int CH, bool PIPE>
 __global__ __launch_bounds__(kBoundedBlock) void k_q6k_bounded(
     const uint8_t *__restrict__ w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
-    const float *__restrict__ sigma, const float *__restrict__ hidden, float *__restrict__ approx,
+    const float *__restrict__ sigma, const uint8_t *__restrict__ prep, float *__restrict__ approx,
     float *__restrict__ bound, float *__restrict__ wg_lb, float *__restrict__ wg_ub) {
     extern __shared__ __align__(16) q6k_xq xq[];  // [n_blocks][16]
     __shared__ float red[kBoundedBlock / 64], red2[kBoundedBlock / 64];
-    __shared__ int redi[kBoundedBlock / 64];
-    const q6k_xhdr hdr = xprep_block(hidden, n_blocks, xq, red, redi);
+    for (uint32_t i = threadIdx.x; i < n_blocks * 16 * 3; i += blockDim.x)
+        reinterpret_cast<int4 *>(xq)[i] = reinterpret_cast<const int4 *>(prep)[i];
+    const q6k_xhdr hdr = *reinterpret_cast<const q6k_xhdr *>(prep + q6k_xq_bytes(n_blocks));
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -479,36 +444,11 @@ __global__ __launch_bounds__(kBoundedBlock) void k_q6k_bounded(
     const uint32_t g1 = (uint32_t)((uint64_t)(blockIdx.x + 1) * n_rowgroups / gridDim.x);
     float lb_max = -INFINITY, ub_max = -INFINITY;
     constexpr uint32_t kWaves = kBoundedBlock / 64;
-    for (uint32_t G = g0 + wave; G < g1; G += kWaves) {
-        const __amdgpu_buffer_rsrc_t rs = wm_rsrc(w + (uint64_t)G * group_bytes, group_bytes);
-        float acc = 0.0f;
-        for (uint32_t b0 = 0; b0 < n_blocks; b0 += CH) {
-            q6_lane_blocks<CH> v;
-            q6_load_uniform<CH>(v, rs, b0, off_q, off_sc, off_d);
-#pragma unroll
-            for (int j = 0; j < CH; j++) {
-                uint32_t U[4];
-                q6_unpack(v.w0[j], v.w1[j], v.w2[j], U);
-                const q6k_xq &xv = xq[(b0 + j) * 16 + p];
-                int T = 0;
-#pragma unroll
-                for (int hn = 0; hn < 4; hn++) {
-                    const int sc = (int)(int8_t)(v.scw[j] >> (8 * hn));
-                    const int dh = __builtin_amdgcn_sdot4((int)U[hn], xv.xh[hn], 0, false);
-                    const int dl = __builtin_amdgcn_sdot4((int)U[hn], xv.xl[hn], xv.c[hn], false);
-                    const int I = (int)(((uint32_t)dh << 8) + (uint32_t)dl);  // a VALU result
-                    T = mad_i24(sc, I, T);
-                }
-                const float d = __half2float(__ushort_as_half((unsigned short)v.db[j]));
-                acc = __builtin_fmaf(d, (float)T, acc);
-            }
-        }
+    auto epilogue = [&](uint32_t row, float acc, float sg) {
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) acc = acc + __shfl_xor(acc, o, 64);
-        const uint32_t row = G * Q6K_GROUP_ROWS + r;
         if (p == 0 && row < n_rows) {
             float a, eb;
-            const float sg = sigma[row];
             if (hdr.ok) {
                 a = ldexpf(acc, hdr.e);
                 eb = hdr.bound_k * sg;
@@ -522,8 +462,62 @@ __global__ __launch_bounds__(kBoundedBlock) void k_q6k_bounded(
             approx[row] = a;
             bound[row] = eb;
             const float lb = a - eb, ub = a + eb;
-            if (lb > lb_max) lb_max = lb;                     // NaN never raises it
+            if (lb > lb_max) lb_max = lb;                            // NaN never raises it
             if (!(ub <= ub_max)) ub_max = ub == ub ? ub : INFINITY;  // NaN counts as +inf
+        }
+    };
+    if (PIPE) {
+        // batches (group G, blocks bi*CH ..): the next batch's loads are in
+        // flight while this one is reduced; two register sets used in turn
+        // (the loop body covers two batches, so no set is ever copied)
+        const uint32_t nbat = n_blocks / CH;
+        uint32_t G = g0 + wave, bi = 0;
+        if (G < g1) {
+            q6_lane_blocks<CH> A, B;
+            q6_load_uniform<CH>(A, wm_rsrc(w + (uint64_t)G * group_bytes, group_bytes), 0, off_q,
+                                off_sc, off_d);
+            float sg = sigma[min(G * Q6K_GROUP_ROWS + r, n_rows - 1)];
+            float acc = 0.0f;
+            // one batch: prefetch the next one into `nxt`, reduce `cur`;
+            // returns false after the wave's last batch
+            auto step = [&](const q6_lane_blocks<CH> &cur, q6_lane_blocks<CH> &nxt) -> bool {
+                uint32_t Gn = G, bn = bi + 1;
+                if (bn == nbat) {
+                    bn = 0;
+                    Gn = G + kWaves;
+                }
+                const bool more = Gn < g1;
+                float sg_n = sg;
+                if (more) {
+                    q6_load_uniform<CH>(nxt, wm_rsrc(w + (uint64_t)Gn * group_bytes, group_bytes),
+                                        bn * CH, off_q, off_sc, off_d);
+                    if (bn == 0) sg_n = sigma[min(Gn * Q6K_GROUP_ROWS + r, n_rows - 1)];
+                }
+                q6_bounded_accum<CH>(cur, bi * CH, xq, p, acc);
+                if (bi + 1 == nbat) {
+                    epilogue(G * Q6K_GROUP_ROWS + r, acc, sg);
+                    acc = 0.0f;
+                }
+                G = Gn;
+                bi = bn;
+                sg = sg_n;
+                return more;
+            };
+            while (step(A, B) && step(B, A)) {
+            }
+        }
+    } else {
+        for (uint32_t G = g0 + wave; G < g1; G += kWaves) {
+            const __amdgpu_buffer_rsrc_t rs = wm_rsrc(w + (uint64_t)G * group_bytes, group_bytes);
+            const uint32_t row = G * Q6K_GROUP_ROWS + r;
+            const float sg = sigma[min(row, n_rows - 1)];
+            float acc = 0.0f;
+            for (uint32_t b0 = 0; b0 < n_blocks; b0 += CH) {
+                q6_lane_blocks<CH> v;
+                q6_load_uniform<CH>(v, rs, b0, off_q, off_sc, off_d);
+                q6_bounded_accum<CH>(v, b0, xq, p, acc);
+            }
+            epilogue(row, acc, sg);
         }
     }
     lb_max = wm_wave_max_nonan(lb_max);
@@ -665,31 +659,32 @@ int pick_ch(uint32_t n_blocks) {
 
 // Work buffer layout (all offsets 256-aligned).
 struct work_layout {
-    size_t cands, bound, wg_lb, wg_ub, total;
+    size_t cands, bound, wg_lb, wg_ub, prep, total;
 };
 size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
-work_layout layout_of(uint32_t n_rows) {
+work_layout layout_of(uint32_t n_rows, uint32_t n_blocks) {
     work_layout l;
     size_t o = 0;
     l.cands = o; o += al256(sizeof(argcand) * kMaxArgBlocks);
     l.bound = o; o += al256((size_t)n_rows * 4);
     l.wg_lb = o; o += al256(4 * kBoundedMaxBlocks);
     l.wg_ub = o; o += al256(4 * kBoundedMaxBlocks);
+    l.prep = o; o += q6k_prep_bytes(n_blocks);
     l.total = o;
     return l;
 }
 
 // Workgroups of the bounded pass: as many as fit on the device at once (one
 // round, each with a contiguous range of row groups), at most one per 4 groups.
-template <int CH>
+template <int CH, bool PIPE>
 uint32_t bounded_blocks_for(uint32_t n_rowgroups, size_t lds) {
-    static int cached[16] = {0};
+    static int cached[16] = {0};  // per device, per instantiation
     int dev = 0;
-    hipGetDevice(&dev);
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
     int per = dev < 16 ? cached[dev] : 0;
     if (per == 0) {
         int occ = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_q6k_bounded<CH>, kBoundedBlock, lds) != hipSuccess || occ < 1)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_q6k_bounded<CH, PIPE>, kBoundedBlock, lds) != hipSuccess || occ < 1)
             occ = 1;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
             cus = 256;
@@ -704,27 +699,35 @@ uint32_t bounded_blocks_for(uint32_t n_rowgroups, size_t lds) {
 
 template <int CH>
 uint32_t launch_bounded_ch(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
-                           uint32_t n_rowgroups, const float *hidden, float *approx, float *bound,
+                           uint32_t n_rowgroups, const uint8_t *prep, float *approx, float *bound,
                            float *wg_lb, float *wg_ub, hipStream_t s) {
     const size_t lds = sizeof(q6k_xq) * 16 * n_blocks;
-    const uint32_t blocks = bounded_blocks_for<CH>(n_rowgroups, lds);
     const float *sigma = reinterpret_cast<const float *>(w + wm_q6k_sigma_offset(n_rowgroups, n_blocks));
-    hipLaunchKernelGGL(k_q6k_bounded<CH>, dim3(blocks), dim3(kBoundedBlock), lds, s, w, n_blocks,
-                       n_rows, n_rowgroups, sigma, hidden, approx, bound, wg_lb, wg_ub);
+    if (kPipelined) {
+        const uint32_t blocks = bounded_blocks_for<CH, true>(n_rowgroups, lds);
+        hipLaunchKernelGGL((k_q6k_bounded<CH, true>), dim3(blocks), dim3(kBoundedBlock), lds, s, w,
+                           n_blocks, n_rows, n_rowgroups, sigma, prep, approx, bound, wg_lb, wg_ub);
+        return blocks;
+    }
+    const uint32_t blocks = bounded_blocks_for<CH, false>(n_rowgroups, lds);
+    hipLaunchKernelGGL((k_q6k_bounded<CH, false>), dim3(blocks), dim3(kBoundedBlock), lds, s, w,
+                       n_blocks, n_rows, n_rowgroups, sigma, prep, approx, bound, wg_lb, wg_ub);
     return blocks;
 }
 
 template <int CH>
 void launch_argmax_fast_ch(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                            uint32_t n_rowgroups, const float *hidden, float *logits,
-                           uint32_t *argmax_out, void *work, hipStream_t s) {
-    const work_layout lay = layout_of(n_rows);
+                           uint32_t *argmax_out, void *work, bool prepared, hipStream_t s) {
+    const work_layout lay = layout_of(n_rows, n_blocks);
     uint8_t *wb = (uint8_t *)work;
     float *bound = reinterpret_cast<float *>(wb + lay.bound);
     float *wg_lb = reinterpret_cast<float *>(wb + lay.wg_lb);
     float *wg_ub = reinterpret_cast<float *>(wb + lay.wg_ub);
-    const uint32_t n_wg = launch_bounded_ch<CH>(w, n_blocks, n_rows, n_rowgroups, hidden, logits,
-                                                bound, wg_lb, wg_ub, s);
+    if (!prepared)
+        hipLaunchKernelGGL(k_q6k_xprep, dim3(1), dim3(256), 0, s, hidden, n_blocks, wb + lay.prep);
+    const uint32_t n_wg = launch_bounded_ch<CH>(w, n_blocks, n_rows, n_rowgroups, wb + lay.prep,
+                                                logits, bound, wg_lb, wg_ub, s);
     const size_t lds = sizeof(float) * 16 * xs_stride(n_blocks);
     hipLaunchKernelGGL(k_q6k_select<CH>, dim3(1), dim3(kSelectBlock), lds, s, w, n_blocks, n_rows,
                        n_rowgroups, hidden, logits, bound, wg_lb, wg_ub, n_wg, argmax_out);
@@ -763,8 +766,11 @@ void wm_launch_q6k_dequant_rows_dev(const uint8_t *w, uint32_t n_blocks, const u
 }
 
 size_t wm_q6k_logits_work_bytes(uint32_t n_rows, uint32_t n_blocks) {
-    (void)n_blocks;
-    return layout_of(n_rows).total;
+    return layout_of(n_rows, n_blocks).total;
+}
+
+void *wm_q6k_prep_area(void *work, uint32_t n_rows, uint32_t n_blocks) {
+    return (uint8_t *)work + layout_of(n_rows, n_blocks).prep;
 }
 
 // Exact logits (bit-identical to the reference) + optional argmax.  The
@@ -778,7 +784,7 @@ void wm_launch_q6k_logits_argmax(const uint8_t *w, uint32_t n_blocks, uint32_t n
     if (blocks > max_blocks) blocks = max_blocks;
     if (blocks == 0) blocks = 1;
     const size_t lds = sizeof(float) * 16 * (n_blocks * 16 + 4);
-    argcand *cands = reinterpret_cast<argcand *>((uint8_t *)work + layout_of(n_rows).cands);
+    argcand *cands = reinterpret_cast<argcand *>((uint8_t *)work + layout_of(n_rows, n_blocks).cands);
 #define WM_LOGITS_CASE(C)                                                                           \
     case C:                                                                                         \
         hipLaunchKernelGGL(k_q6k_logits<C>, dim3(blocks), dim3(kLogitsBlock), lds, s, w, n_blocks, \
@@ -797,33 +803,46 @@ void wm_launch_q6k_logits_argmax(const uint8_t *w, uint32_t n_blocks, uint32_t n
 // Argmax only: the bounded pass, then selection + exact rescoring + argmax
 // in one workgroup.  `logits` (n_rows floats) receives the bounded pass's
 // values, exact on the rows that were rescored (always including row 0).
+// prepared: the work buffer's prep area already holds `hidden` in fixed
+// point (written by the kernel that produced it).
 void wm_launch_q6k_argmax_fast(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                                uint32_t n_rowgroups, const float *hidden, float *logits,
-                               uint32_t *argmax_out, void *work, hipStream_t s) {
+                               uint32_t *argmax_out, void *work, bool prepared, hipStream_t s) {
+#define WM_F_CASE(C)                                                                               \
+    case C:                                                                                        \
+        launch_argmax_fast_ch<C>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out,    \
+                                 work, prepared, s);                                               \
+        break;
     switch (pick_ch(n_blocks)) {
-        case 10: launch_argmax_fast_ch<10>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out, work, s); break;
-        case 8: launch_argmax_fast_ch<8>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out, work, s); break;
-        case 5: launch_argmax_fast_ch<5>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out, work, s); break;
-        case 4: launch_argmax_fast_ch<4>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out, work, s); break;
-        case 2: launch_argmax_fast_ch<2>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out, work, s); break;
-        default: launch_argmax_fast_ch<1>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out, work, s); break;
+        WM_F_CASE(10) WM_F_CASE(8) WM_F_CASE(5) WM_F_CASE(4) WM_F_CASE(2) default: WM_F_CASE(1)
     }
+#undef WM_F_CASE
 }
 
 // Test hook / measurement: the bounded pass alone (approximate logits and
-// their bounds).
+// their bounds), after the fixed-point prep of `hidden` unless `prepared`.
 void wm_launch_q6k_bounded_only(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                                 uint32_t n_rowgroups, const float *hidden, float *approx,
-                                float *bound_out, void *work, hipStream_t s) {
-    const work_layout lay = layout_of(n_rows);
-    float *wg_lb = reinterpret_cast<float *>((uint8_t *)work + lay.wg_lb);
-    float *wg_ub = reinterpret_cast<float *>((uint8_t *)work + lay.wg_ub);
+                                float *bound_out, void *work, bool prepared, hipStream_t s) {
+    const work_layout lay = layout_of(n_rows, n_blocks);
+    uint8_t *wb = (uint8_t *)work;
+    float *wg_lb = reinterpret_cast<float *>(wb + lay.wg_lb);
+    float *wg_ub = reinterpret_cast<float *>(wb + lay.wg_ub);
+    if (!prepared)
+        hipLaunchKernelGGL(k_q6k_xprep, dim3(1), dim3(256), 0, s, hidden, n_blocks, wb + lay.prep);
+#define WM_B_CASE(C)                                                                               \
+    case C:                                                                                        \
+        launch_bounded_ch<C>(w, n_blocks, n_rows, n_rowgroups, wb + lay.prep, approx, bound_out,  \
+                             wg_lb, wg_ub, s);                                                     \
+        break;
     switch (pick_ch(n_blocks)) {
-        case 10: launch_bounded_ch<10>(w, n_blocks, n_rows, n_rowgroups, hidden, approx, bound_out, wg_lb, wg_ub, s); break;
-        case 8: launch_bounded_ch<8>(w, n_blocks, n_rows, n_rowgroups, hidden, approx, bound_out, wg_lb, wg_ub, s); break;
-        case 5: launch_bounded_ch<5>(w, n_blocks, n_rows, n_rowgroups, hidden, approx, bound_out, wg_lb, wg_ub, s); break;
-        case 4: launch_bounded_ch<4>(w, n_blocks, n_rows, n_rowgroups, hidden, approx, bound_out, wg_lb, wg_ub, s); break;
-        case 2: launch_bounded_ch<2>(w, n_blocks, n_rows, n_rowgroups, hidden, approx, bound_out, wg_lb, wg_ub, s); break;
-        default: launch_bounded_ch<1>(w, n_blocks, n_rows, n_rowgroups, hidden, approx, bound_out, wg_lb, wg_ub, s); break;
+        WM_B_CASE(10) WM_B_CASE(8) WM_B_CASE(5) WM_B_CASE(4) WM_B_CASE(2) default: WM_B_CASE(1)
     }
+#undef WM_B_CASE
+}
+
+void wm_launch_q6k_xprep(const float *hidden, uint32_t n_blocks, void *work, uint32_t n_rows,
+                         hipStream_t s) {
+    hipLaunchKernelGGL(k_q6k_xprep, dim3(1), dim3(256), 0, s, hidden, n_blocks,
+                       (uint8_t *)work + layout_of(n_rows, n_blocks).prep);
 }

@@ -25,7 +25,7 @@ void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, u
                              uint32_t row0, float w_scale, const wm_act_meta *meta_in,
                              const float *w, uint32_t n, float eps, uint8_t *act,
                              wm_act_meta *meta_out, float *y_out, uint32_t *err_flag,
-                             uint32_t layer_tag, hipStream_t s);
+                             uint32_t layer_tag, void *q6k_prep, hipStream_t s);
 void wm_launch_qkv_rope_kv(const int32_t *partial, uint32_t split, uint32_t rows_total,
                            uint32_t q_row0, uint32_t k_row0, uint32_t v_row0, uint32_t n_q,
                            uint32_t n_kv, float q_scale, float k_scale, float v_scale,
@@ -161,12 +161,12 @@ void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
         // residual of the previous layer's ffn_down, folded into attn_norm
         if (l == 0) {
             wm_launch_rmsnorm_quant(m->hidden, nullptr, 0, 0, 0, 0.0f, nullptr, L.attn_norm, E,
-                                    c.rms_eps, m->act, &m->meta[0], nullptr, nullptr, 0, s);
+                                    c.rms_eps, m->act, &m->meta[0], nullptr, nullptr, 0, nullptr, s);
         } else {
             const dev_layer &P = m->layers[l - 1];
             wm_launch_rmsnorm_quant(m->hidden, m->partial, m->split_down, P.down.n_groups * 64, 0,
                                     P.down.scale, &m->meta[3], L.attn_norm, E, c.rms_eps, m->act,
-                                    &m->meta[0], nullptr, m->dscalars + 2, l, s);
+                                    &m->meta[0], nullptr, m->dscalars + 2, l, nullptr, s);
             if (layer_trace_dev)
                 hipMemcpyAsync(layer_trace_dev + (size_t)(l - 1) * E, m->hidden, (size_t)E * 4,
                                hipMemcpyDeviceToDevice, s);
@@ -186,20 +186,20 @@ void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
                             m->scores, c.context_length, m->attn_out, c.n_heads, c.n_kv_heads,
                             c.head_dim, pos + 1, scale, s);
         wm_launch_rmsnorm_quant(m->attn_out, nullptr, 0, 0, 0, 0.0f, nullptr, L.attn_sub_norm, E,
-                                c.rms_eps, m->act, &m->meta[1], nullptr, nullptr, 0, s);
+                                c.rms_eps, m->act, &m->meta[1], nullptr, nullptr, 0, nullptr, s);
         wm_i2s_desc od = {L.o.w, L.o.n_groups};
         wm_launch_i2s_partial(&od, 1, n_chunks_e, m->act, m->partial, m->split_o, L.o.n_groups * 64, s);
         // hidden += wo_out, then ffn_norm
         wm_launch_rmsnorm_quant(m->hidden, m->partial, m->split_o, L.o.n_groups * 64, 0, L.o.scale,
                                 &m->meta[1], L.ffn_norm, E, c.rms_eps, m->act, &m->meta[2], nullptr,
-                                nullptr, 0, s);
+                                nullptr, 0, nullptr, s);
         wm_i2s_desc gu[2] = {{L.gate.w, L.gate.n_groups}, {L.up.w, L.up.n_groups}};
         const uint32_t rows_gu = (L.gate.n_groups + L.up.n_groups) * 64;
         wm_launch_i2s_partial(gu, 2, n_chunks_e, m->act, m->partial, m->split_gu, rows_gu, s);
         wm_launch_gateup_relu2(m->partial, m->split_gu, rows_gu, 0, L.gate.n_groups * 64, F,
                                L.gate.scale, L.up.scale, &m->meta[2], m->h_ff, s);
         wm_launch_rmsnorm_quant(m->h_ff, nullptr, 0, 0, 0, 0.0f, nullptr, L.ffn_sub_norm, F,
-                                c.rms_eps, m->act, &m->meta[3], nullptr, nullptr, 0, s);
+                                c.rms_eps, m->act, &m->meta[3], nullptr, nullptr, 0, nullptr, s);
         wm_i2s_desc dd = {L.down.w, L.down.n_groups};
         wm_launch_i2s_partial(&dd, 1, n_chunks_f, m->act, m->partial, m->split_down,
                               L.down.n_groups * 64, s);
@@ -208,7 +208,8 @@ void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
     const dev_layer &P = m->layers[c.n_layers - 1];
     wm_launch_rmsnorm_quant(m->hidden, m->partial, m->split_down, P.down.n_groups * 64, 0,
                             P.down.scale, &m->meta[3], m->output_norm, E, c.rms_eps, nullptr,
-                            nullptr, m->final_hidden, m->dscalars + 2, c.n_layers, s);
+                            nullptr, m->final_hidden, m->dscalars + 2, c.n_layers,
+                            wm_q6k_prep_area(m->lm_work, c.vocab_size, m->embd_blocks), s);
     if (layer_trace_dev)
         hipMemcpyAsync(layer_trace_dev + (size_t)(c.n_layers - 1) * E, m->hidden, (size_t)E * 4,
                        hipMemcpyDeviceToDevice, s);
@@ -411,7 +412,7 @@ wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_s
         for (uint32_t i = 0; i < n_seqs; i++)
             wm_launch_q6k_argmax_fast(m->embd, m->embd_blocks, c.vocab_size, m->embd_rowgroups,
                                       m->b_final + (size_t)last[i] * E, m->logits, m->b_next + i,
-                                      m->lm_work, s);
+                                      m->lm_work, false, s);
     WM_HIP(ctx, hipGetLastError());
     uint32_t flag = 0;
     WM_HIP(ctx, hipMemcpyAsync(&flag, err, 4, hipMemcpyDeviceToHost, s));
@@ -756,7 +757,7 @@ wm_status wm_decode_step(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t 
     else
         wm_launch_q6k_argmax_fast(m->embd, m->embd_blocks, m->cfg.vocab_size, m->embd_rowgroups,
                                   m->final_hidden, m->logits, m->dscalars + 1, m->lm_work,
-                                  ctx->stream);
+                                  true, ctx->stream);  // output_norm wrote the prep area
     WM_HIP(ctx, hipGetLastError());
     bool failed = false;
     if ((st = finish_step(m, kv, position, &failed))) return st;

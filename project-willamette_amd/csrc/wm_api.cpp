@@ -506,7 +506,7 @@ wm_status wm_logits_argmax_dev(wm_ctx *ctx, const wm_tensor *t, const float *d_h
     else
         wm_launch_q6k_argmax_fast((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
                                   t->n_rowgroups, d_hidden, (float *)scratch, d_argmax, work,
-                                  ctx->stream);
+                                  false, ctx->stream);
     WM_HIP(ctx, hipGetLastError());
     return WM_OK;
 }
@@ -537,7 +537,7 @@ wm_status wm_logits_argmax(wm_ctx *ctx, const wm_tensor *t, const float *hidden,
                                     t->n_rowgroups, d_h, d_l, d_a, work, ctx->stream);
     else
         wm_launch_q6k_argmax_fast((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
-                                  t->n_rowgroups, d_h, d_l, d_a, work, ctx->stream);
+                                  t->n_rowgroups, d_h, d_l, d_a, work, false, ctx->stream);
     WM_HIP(ctx, hipGetLastError());
     if (logits)
         WM_HIP(ctx, hipMemcpyAsync(logits, d_l, t->out_dim * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -549,7 +549,7 @@ wm_status wm_logits_argmax(wm_ctx *ctx, const wm_tensor *t, const float *hidden,
 }
 
 wm_status wm_debug_q6k_bounded_logits_dev(wm_ctx *ctx, const wm_tensor *t, const float *d_hidden,
-                                          float *d_approx, float *d_bound) {
+                                          float *d_approx, float *d_bound, int reuse_prep) {
     wm_status st = check_lm_head(ctx, t);
     if (st) return st;
     if (!d_hidden || !d_approx || !d_bound) return WM_E_ARG;
@@ -558,7 +558,8 @@ wm_status wm_debug_q6k_bounded_logits_dev(wm_ctx *ctx, const wm_tensor *t, const
         return st;
     WM_HIP(ctx, hipSetDevice(ctx->device));
     wm_launch_q6k_bounded_only((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
-                               t->n_rowgroups, d_hidden, d_approx, d_bound, work, ctx->stream);
+                               t->n_rowgroups, d_hidden, d_approx, d_bound, work, reuse_prep != 0,
+                               ctx->stream);
     WM_HIP(ctx, hipGetLastError());
     return WM_OK;
 }
@@ -580,7 +581,7 @@ wm_status wm_debug_q6k_bounded_logits(wm_ctx *ctx, const wm_tensor *t, const flo
     WM_HIP(ctx, hipSetDevice(ctx->device));
     WM_HIP(ctx, hipMemcpyAsync(d_h, hidden, t->in_dim * 4, hipMemcpyHostToDevice, ctx->stream));
     wm_launch_q6k_bounded_only((const uint8_t *)t->d, t->n_blocks, (uint32_t)t->out_dim,
-                               t->n_rowgroups, d_h, d_a, d_b, base + hb + 2 * lb, ctx->stream);
+                               t->n_rowgroups, d_h, d_a, d_b, base + hb + 2 * lb, false, ctx->stream);
     WM_HIP(ctx, hipGetLastError());
     WM_HIP(ctx, hipMemcpyAsync(approx, d_a, t->out_dim * 4, hipMemcpyDeviceToHost, ctx->stream));
     WM_HIP(ctx, hipMemcpyAsync(bound, d_b, t->out_dim * 4, hipMemcpyDeviceToHost, ctx->stream));

@@ -273,14 +273,19 @@ void wm_launch_q6k_logits_argmax(const uint8_t *w, uint32_t n_blocks, uint32_t n
 // argmax only: bounded fixed-point pass + exact rescoring of the rows that
 // can still be the maximum.  logits (n_rows) receives the bounded values,
 // exact on the rescored rows.
+// prepared: the work buffer's prep area (wm_q6k_prep_area) already holds the
+// fixed-point copy of `hidden` (the output-norm kernel writes it).
 void wm_launch_q6k_argmax_fast(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                                uint32_t n_rowgroups, const float *hidden, float *logits,
-                               uint32_t *argmax_out, void *work, hipStream_t s);
+                               uint32_t *argmax_out, void *work, bool prepared, hipStream_t s);
 // test hook: the bounded pass alone (values and their error bounds)
 void wm_launch_q6k_bounded_only(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                                 uint32_t n_rowgroups, const float *hidden, float *approx,
-                                float *bound_out, void *work, hipStream_t s);
+                                float *bound_out, void *work, bool prepared, hipStream_t s);
+void wm_launch_q6k_xprep(const float *hidden, uint32_t n_blocks, void *work, uint32_t n_rows,
+                         hipStream_t s);
 size_t wm_q6k_logits_work_bytes(uint32_t n_rows, uint32_t n_blocks);
+void *wm_q6k_prep_area(void *work, uint32_t n_rows, uint32_t n_blocks);
 
 // ---------------------------------------------------------------------------
 // ragged multi-sequence batch

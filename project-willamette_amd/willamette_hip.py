@@ -135,7 +135,7 @@ EXPORTS = {
     "wm_batch_forward": (C.c_int, _vp, C.POINTER(_vp), C.c_uint32, _u32p, _u32p, _f32p, _u32p),
     "wm_debug_seq_sum": (C.c_int, _vp, _f32p, C.c_size_t, _f32p),
     "wm_debug_q6k_bounded_logits": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p, _f32p),
-    "wm_debug_q6k_bounded_logits_dev": (C.c_int, _vp, _vp, _vp, _vp, _vp),
+    "wm_debug_q6k_bounded_logits_dev": (C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int),
     "wm_synth_stream_seed": (C.c_uint64, C.c_uint64, C.c_uint64),
     "wm_synth_i2s": (None, C.c_uint64, C.c_uint64, _u8p, C.c_size_t),
     "wm_synth_normal": (None, C.c_uint64, C.c_uint64, _f32p, C.c_size_t, C.c_double),
