@@ -45,7 +45,7 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
     extern __shared__ __align__(16) float sq[];  // x[j]*x[j], wm::seq_sum_padded(n) entries
     __shared__ float red_f[16];
     __shared__ int red_i[16];
-    __shared__ float s_sum;
+    __shared__ wm::seq_block_scratch seq_scratch;
     const uint32_t tid = threadIdx.x;
     float xv[PER], wv[PER];
     int nonfinite = 0;
@@ -97,13 +97,9 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         if (any && tid == 0 && *err_flag == 0) *err_flag = layer_tag;
     }
     __syncthreads();
-    // sum_sq over x in order (primitives.rs:243-246), by one wave
-    if (tid < 64) {
-        const float s = wm::seq_sum_nonneg(sq, n);
-        if (tid == 0) s_sum = s;
-    }
-    __syncthreads();
-    const float mean = s_sum / (float)n;
+    // sum_sq over x in order (primitives.rs:243-246), exactly, by the workgroup
+    const float sum_sq = wm::seq_sum_block_nonneg<PER>(sq, n, &seq_scratch);
+    const float mean = sum_sq / (float)n;
     const float rs = 1.0f / sqrtf(mean + eps);
     float m = 0.0f;
 #pragma unroll
@@ -260,21 +256,21 @@ __global__ __launch_bounds__(256) void k_kv_append(const float *__restrict__ k,
     wm_kv_quantise_store(v + src, kv_dim, v_cache + dst * kv_dim, v_scales + dst, red);
 }
 
-// Test hook: the terms are staged into LDS (as every caller holds them)
-// when they fit, else read from global memory; either way the array is
-// padded to wm::seq_sum_padded(n) entries.
+// Test hook: terms that fit in LDS (as every caller holds them) are summed
+// by the workgroup algorithm, longer arrays by the one-wave algorithm straight
+// from global memory.
 constexpr uint32_t kDebugSeqLds = 32768;
 __global__ __launch_bounds__(1024) void k_debug_seq_sum(const float *__restrict__ a, uint32_t n,
                                                         float *__restrict__ out) {
     extern __shared__ __align__(16) float terms[];
-    const float *src = a;
+    __shared__ wm::seq_block_scratch scratch;
     if (n <= kDebugSeqLds) {
-        for (uint32_t i = threadIdx.x; i < wm::seq_sum_padded(n); i += blockDim.x) terms[i] = a[i];
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) terms[i] = a[i];
         __syncthreads();
-        src = terms;
-    }
-    if (threadIdx.x < 64) {
-        const float s = wm::seq_sum_nonneg(src, n);
+        const float s = wm::seq_sum_block_nonneg<kDebugSeqLds / 1024>(terms, n, &scratch);
+        if (threadIdx.x == 0) *out = s;
+    } else if (threadIdx.x < 64) {
+        const float s = wm::seq_sum_nonneg(a, n);
         if (threadIdx.x == 0) *out = s;
     }
 }
@@ -286,7 +282,7 @@ __global__ __launch_bounds__(1024) void k_debug_seq_sum(const float *__restrict_
 // ---------------------------------------------------------------------------
 
 void wm_launch_debug_seq_sum(const float *a, uint32_t n, float *out, hipStream_t s) {
-    const size_t lds = n <= kDebugSeqLds ? (size_t)wm::seq_sum_padded(n) * sizeof(float) : 0;
+    const size_t lds = n <= kDebugSeqLds ? (size_t)n * sizeof(float) : 0;
     hipLaunchKernelGGL(k_debug_seq_sum, dim3(1), dim3(1024), lds, s, a, n, out);
 }
 

@@ -1,10 +1,18 @@
-"""CPU model of the wave-parallel exact sum in
-project-willamette_amd/csrc/wm_seqsum.h (64 lanes x 8 terms per step, the
-128-term sequential lead, the run test on s's significand, restarts that zero
-consumed terms), evaluated in numpy float32 and compared bit for bit with the
-left-to-right float32 accumulation.  It checks the algorithm itself (exactness
-and the bound on passes per step) without a GPU; the GPU tests check the
-device code against the same sequential sums."""
+"""CPU models of the exact evaluations of a left-to-right f32 sum in
+project-willamette_amd/csrc/wm_seqsum.h, in numpy float32, compared bit for
+bit with the left-to-right float32 accumulation:
+
+* the one-wave algorithm (64 lanes x 8 terms per step, the 128-term
+  sequential lead, the run test on s's significand, restarts that zero
+  consumed terms);
+* the workgroup algorithm (binades predicted from a float64 prefix sum,
+  break terms, integer segment sums, a sequential walk over the breaks with a
+  check of every prediction and the one-wave algorithm on any segment whose
+  check fails).
+
+They check the algorithms themselves (exactness, the bound on passes per
+step) without a GPU; the GPU tests check the device code against the same
+sequential sums."""
 import numpy as np
 import pytest
 
@@ -71,6 +79,72 @@ def model_sum(a):
         else:
             raise PassCapReached()
     return s, max_pass
+
+
+BLOCK_RECORDS = 512  # break records the workgroup algorithm keeps (else: one-wave path)
+
+
+def _exp2floor(x):
+    """floor(log2 x) of a positive finite float64."""
+    return int(np.frexp(x)[1]) - 1
+
+
+def model_block_sum(a, stats=None):
+    """Model of wm::seq_sum_block_nonneg: returns the sum."""
+    a = np.asarray(a, np.float32)
+    n = a.size
+    if n == 0:
+        return f32(0.0)
+    with np.errstate(all="ignore"):
+        P = np.concatenate([[0.0], np.cumsum(a.astype(np.float64))])  # P[k]: sum before term k
+    recs = []  # (index, binade after, increment prefix before, value)
+    pi = 0
+    for k in range(n):
+        pb, pa, v = P[k], P[k + 1], a[k]
+        brk = k == 0 or not (pb > 0) or not np.isfinite(pb) or not np.isfinite(pa)
+        if not brk:
+            eb, ea = _exp2floor(pb), _exp2floor(pa)
+            brk = ea != eb
+        if not brk:
+            with np.errstate(all="ignore"):
+                r = np.float32(np.ldexp(v, 23 - eb))
+            brk = not (r < f32(2.0 ** 22)) or (r - np.floor(r)) == f32(0.5)
+        if brk:
+            ea = _exp2floor(pa) if (pa > 0 and np.isfinite(pa)) else -1000
+            recs.append((k, ea, pi, v))
+        else:
+            pi += int(np.rint(r))
+    if stats is not None:
+        stats["breaks"] = len(recs)
+        stats["fallback_segments"] = 0
+    if len(recs) > BLOCK_RECORDS:
+        return model_sum(a)[0]
+    s = f32(0.0)
+    prev_t, prev_pi, e_seg = -1, 0, None
+    for (t, ea, pit, v) in recs + [(n, None, pi, None)]:
+        cnt = t - prev_t - 1
+        if cnt > 0:
+            d = pit - prev_pi
+            bits = int(np.array(s, np.float32).view(np.uint32))
+            ef = bits >> 23
+            ok = 1 <= ef <= 254 and e_seg is not None and ef - 127 == e_seg
+            if ok:
+                N = (bits & 0x7FFFFF) | 0x800000
+                ok = N + d <= (1 << 24) - 2
+            if ok:
+                s = f32(np.ldexp(f32(N + d), e_seg - 23))
+            else:  # the segment by the one-wave algorithm, from s
+                if stats is not None:
+                    stats["fallback_segments"] += 1
+                with np.errstate(all="ignore"):
+                    for x in a[prev_t + 1:t]:
+                        s = f32(s + x)
+        if t < n:
+            with np.errstate(all="ignore"):
+                s = f32(s + v)
+            e_seg = ea
+        prev_t, prev_pi = t, pit
+    return s
 
 
 def sequential(a):
@@ -140,3 +214,47 @@ def test_zero_increment_terms_never_end_a_run():
     a = np.concatenate([[16777215.0], np.zeros(LEAD - 1), [0.25, 0, 0, 1.0]]).astype(np.float32)
     got, max_pass = model_sum(a)
     assert same(got, sequential(a)) and max_pass < 8
+
+
+@pytest.mark.parametrize("name,a", inputs(), ids=[c[0] for c in inputs()])
+def test_block_model_matches_sequential(name, a):
+    assert same(model_block_sum(a), sequential(a)), name
+
+
+def test_block_model_fuzz():
+    rng = np.random.default_rng(13)
+    fallbacks = 0
+    for i in range(600):
+        n = int(rng.integers(1, 7000))
+        sc = float(2.0 ** rng.integers(-20, 20))
+        kind = i % 5
+        if kind == 0:
+            a = (rng.standard_normal(n) * sc).astype(np.float32) ** 2
+        elif kind == 1:
+            a = (rng.integers(0, 8, n) * sc).astype(np.float32)
+        elif kind == 2:
+            x = (rng.standard_normal(n) * 8).astype(np.float32)
+            a = np.exp(x - x.max()).astype(np.float32)
+        elif kind == 3:
+            a = np.full(n, f32(2.0 ** rng.integers(-3, 3)), np.float32)
+            a[0] = f32(2 ** 24 - 1) * f32(2.0 ** rng.integers(-30, 0))
+        else:  # sums that sit on binade boundaries
+            a = np.full(n, f32(1.0), np.float32)
+            a[::3] = f32(2.0) ** -rng.integers(20, 26)
+        st = {}
+        got = model_block_sum(a, st)
+        if kind != 3:  # kind 3 makes every term a tie: the fallback is the point
+            fallbacks += st["fallback_segments"]
+        assert same(got, sequential(a)), f"case {i} kind {kind} n {n}"
+    # predictions rarely fail on the other inputs
+    assert fallbacks < 10
+
+
+def test_block_model_rms_inputs_take_the_fast_path():
+    rng = np.random.default_rng(3)
+    for n in (2560, 6912):
+        for _ in range(20):
+            a = rng.standard_normal(n).astype(np.float32) ** 2
+            st = {}
+            assert same(model_block_sum(a, st), sequential(a))
+            assert st["breaks"] < 64 and st["fallback_segments"] <= 2
