@@ -401,7 +401,7 @@ def main():
                    "decode_tokens": args.steps, "start_token": START_TOKEN, "exact": True},
         "roofline": {"bound": "hbm", "achieved": round(lm_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(lm_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic_record("k_q6k_bounded"),
+                     "traffic": traffic_record("k_q6k_bounded<10, true>"),
                      "kernel": "k_q6k_bounded (Q6_K lm-head 128256x2560, id-only pass)",
                      "us_per_launch": round(lm_ms * 1000, 2)},
         "cpu_baseline": cpu,
