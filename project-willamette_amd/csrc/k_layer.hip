@@ -35,26 +35,31 @@ struct residual_src {
 // then y = (x * rsqrt) * w with rsqrt = 1/sqrt(Σx²/n + eps), then either
 // y -> y_out (f32) or y -> per-vector absmax int8 (permuted layout) + meta.
 // err_flag: set to layer_tag if x (after the residual) is not all finite.
+// Element-wise work uses element j = tid + i * kNormThreads (coalesced
+// loads: the residual's K-split partials are the kernel's largest read, and
+// one CU's L1 bandwidth bounds it); the exact sum takes the squares back
+// from LDS with each thread owning consecutive terms.  Five barriers in all.
 constexpr int kMaxSplit = 16;  // K splits a residual source may carry
 
-template <int PER>  // values per thread: n <= PER * 1024
-__global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
+template <int PER, int NT>  // NT threads, values per thread: n <= PER * NT
+__global__ __launch_bounds__(NT) void k_rmsnorm_quant(
     float *__restrict__ x, residual_src res, const float *__restrict__ w, uint32_t n, float eps,
     uint8_t *__restrict__ act, wm_act_meta *__restrict__ meta_out, float *__restrict__ y_out,
     uint32_t *__restrict__ err_flag, uint32_t layer_tag, uint8_t *__restrict__ q6k_prep) {
-    extern __shared__ __align__(16) float sq[];  // x[j]*x[j], wm::seq_sum_padded(n) entries
-    __shared__ float red_f[16];
-    __shared__ int red_i[16];
+    constexpr int NW = NT / 64;
+    extern __shared__ __align__(16) float sq[];  // x[j]*x[j], n entries
+    __shared__ float red_f[NW];
+    __shared__ int red_i[NW], red_nf[NW];
     __shared__ wm::seq_block_scratch seq_scratch;
-    const uint32_t tid = threadIdx.x;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     float xv[PER], wv[PER];
     int nonfinite = 0;
     const bool has_res = res.partial != nullptr;
-    // Every load below is unconditional (indices clamped to n - 1) so that
-    // they are all in flight together; out-of-range values are masked after.
+    // Every load below is issued before any is used (indices clamped to
+    // n - 1); out-of-range values are masked after.
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-        const uint32_t j = min(tid + (uint32_t)i * kNormThreads, n - 1);
+        const uint32_t j = min(tid + (uint32_t)i * NT, n - 1);
         xv[i] = x[j];
         wv[i] = w[j];
     }
@@ -62,22 +67,23 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         // hidden += wo_out / down (cached_forward.rs:405-408, :496-500)
         const float combined = res.w_scale * res.meta->scale;
         const int asum = res.meta->asum;
+        const int32_t *p = res.partial + res.row0;
         int dot[PER];
 #pragma unroll
         for (int i = 0; i < PER; i++) dot[i] = -asum;
 #pragma unroll
         for (int s = 0; s < kMaxSplit; s++) {
-            const uint32_t sc = min((uint32_t)s, res.split - 1);
+            if ((uint32_t)s < res.split) {
 #pragma unroll
-            for (int i = 0; i < PER; i++) {
-                const uint32_t j = min(tid + (uint32_t)i * kNormThreads, n - 1);
-                const int v = res.partial[(uint64_t)sc * res.rows_total + res.row0 + j];
-                dot[i] += (uint32_t)s < res.split ? v : 0;
+                for (int i = 0; i < PER; i++) {
+                    const uint32_t j = min(tid + (uint32_t)i * NT, n - 1);
+                    dot[i] += p[(uint64_t)s * res.rows_total + j];
+                }
             }
         }
 #pragma unroll
         for (int i = 0; i < PER; i++) {
-            const uint32_t j = tid + (uint32_t)i * kNormThreads;
+            const uint32_t j = tid + (uint32_t)i * NT;
             const float v = xv[i] + combined * (float)dot[i];
             xv[i] = v;
             if (j < n) {
@@ -88,27 +94,37 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
     }
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-        const uint32_t j = tid + (uint32_t)i * kNormThreads;
+        const uint32_t j = tid + (uint32_t)i * NT;
         if (j < n) sq[j] = xv[i] * xv[i];
         else xv[i] = 0.0f;
     }
-    if (err_flag) {
-        int any = wm_block_sum_i32(nonfinite, red_i);
-        if (any && tid == 0 && *err_flag == 0) *err_flag = layer_tag;
-    }
+    if (err_flag && lane == 0) red_nf[wid] = __builtin_amdgcn_ballot_w64(nonfinite != 0) != 0;
     __syncthreads();
     // sum_sq over x in order (primitives.rs:243-246), exactly, by the workgroup
-    const float sum_sq = wm::seq_sum_block_nonneg<PER>(sq, n, &seq_scratch);
+    float v2[PER];
+    {
+        const uint32_t m = (n + NT - 1) / NT, k0 = tid * m;
+#pragma unroll
+        for (int i = 0; i < PER; i++)
+            v2[i] = ((uint32_t)i < m && k0 + (uint32_t)i < n) ? sq[k0 + i] : 0.0f;
+    }
+    const float sum_sq = wm::seq_sum_block_owned<PER, NT>(v2, n, sq, &seq_scratch);
+    if (err_flag && tid == 0) {
+        int any = 0;
+#pragma unroll
+        for (int i = 0; i < NW; i++) any |= red_nf[i];
+        if (any && *err_flag == 0) *err_flag = layer_tag;
+    }
     const float mean = sum_sq / (float)n;
     const float rs = 1.0f / sqrtf(mean + eps);
-    float m = 0.0f;
+    float mx = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-        const uint32_t j = tid + (uint32_t)i * kNormThreads;
+        const uint32_t j = tid + (uint32_t)i * NT;
         xv[i] = xv[i] * rs * wv[i];  // out[i] = x[i] * rsqrt * weight[i]
         if (j < n) {
             if (y_out) y_out[j] = xv[i];
-            m = wm_max_nonan(m, fabsf(xv[i]));
+            mx = wm_max_nonan(mx, fabsf(xv[i]));
         }
     }
     if (y_out) {
@@ -122,22 +138,32 @@ __global__ __launch_bounds__(kNormThreads) void k_rmsnorm_quant(
         return;
     }
     // per-vector absmax int8 (src/model/bitlinear_sse2.rs:285-304)
-    const float max_abs = wm_block_max_nonan(m, red_f);
+    mx = wm_wave_max_nonneg(mx);
+    if (lane == 0) red_f[wid] = mx;
+    __syncthreads();
+    float max_abs = red_f[0];
+#pragma unroll
+    for (int i = 1; i < NW; i++) max_abs = wm_max_nonan(max_abs, red_f[i]);
     int sum = 0;
     const float inv = 127.0f / max_abs;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-        const uint32_t j = tid + (uint32_t)i * kNormThreads;
+        const uint32_t j = tid + (uint32_t)i * NT;
         if (j < n) {
             const int q = max_abs == 0.0f ? 0 : wm_round_clamp_i8(xv[i] * inv);
             act[wm_act_perm(j)] = (uint8_t)(int8_t)q;
             sum += q;
         }
     }
-    sum = wm_block_sum_i32(sum, red_i);
+    sum = wm_wave_total_i32(sum);
+    if (lane == 0) red_i[wid] = sum;
+    __syncthreads();
     if (tid == 0) {
+        int t = 0;
+#pragma unroll
+        for (int i = 0; i < NW; i++) t += red_i[i];
         meta_out->scale = max_abs == 0.0f ? 1.0f : max_abs / 127.0f;
-        meta_out->asum = sum;
+        meta_out->asum = t;
     }
 }
 
@@ -264,10 +290,17 @@ __global__ __launch_bounds__(1024) void k_debug_seq_sum(const float *__restrict_
                                                         float *__restrict__ out) {
     extern __shared__ __align__(16) float terms[];
     __shared__ wm::seq_block_scratch scratch;
+    constexpr int M = kDebugSeqLds / 1024;
     if (n <= kDebugSeqLds) {
-        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) terms[i] = a[i];
-        __syncthreads();
-        const float s = wm::seq_sum_block_nonneg<kDebugSeqLds / 1024>(terms, n, &scratch);
+        const uint32_t m = (n + 1023) / 1024, k0 = threadIdx.x * m;
+        float v[M];
+#pragma unroll
+        for (int j = 0; j < M; j++) {
+            const uint32_t k = k0 + (uint32_t)j;
+            v[j] = ((uint32_t)j < m && k < n) ? a[k] : 0.0f;
+            if ((uint32_t)j < m && k < n) terms[k] = v[j];
+        }
+        const float s = wm::seq_sum_block_owned<M, 1024>(v, n, terms, &scratch);
         if (threadIdx.x == 0) *out = s;
     } else if (threadIdx.x < 64) {
         const float s = wm::seq_sum_nonneg(a, n);
@@ -296,7 +329,8 @@ void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, u
     const int per = (int)((n + kNormThreads - 1) / kNormThreads);
 #define WM_NORM_CASE(P)                                                                            \
     case P:                                                                                        \
-        hipLaunchKernelGGL(k_rmsnorm_quant<P>, dim3(1), dim3(kNormThreads), lds, s, x, res, w, n,  \
+        hipLaunchKernelGGL((k_rmsnorm_quant<P, kNormThreads>), dim3(1), dim3(kNormThreads), lds, s, \
+                           x, res, w, n,                                                           \
                            eps, act, meta_out, y_out, err_flag, layer_tag, (uint8_t *)q6k_prep);  \
         break;
     switch (per) {

@@ -149,6 +149,78 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t wm_rsrc(const void *base, uint
 constexpr int WM_LOAD_NT = 2;  // cache policy bits of a buffer load: non-temporal
 typedef unsigned int wm_v3u __attribute__((ext_vector_type(3)));
 
+// DPP lane moves of the wave64 GFX9 family: row_shr:n (lane i of a 16-lane
+// row reads lane i-n of the same row), row_bcast:15 (lane 15 of each row to
+// every lane of the next row), row_bcast:31 (lane 31 to rows 2 and 3).
+// Lanes with no source, and rows outside ROW_MASK, read 0.  The whole wave
+// must be active.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int wm_dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, true);
+}
+constexpr int WM_DPP_ROW_SHR1 = 0x111, WM_DPP_ROW_SHR2 = 0x112, WM_DPP_ROW_SHR4 = 0x114,
+              WM_DPP_ROW_SHR8 = 0x118, WM_DPP_ROW_BCAST15 = 0x142, WM_DPP_ROW_BCAST31 = 0x143;
+
+// Inclusive wave scans (Hillis-Steele inside rows, then the two row
+// broadcasts).  Integer scans are exact; the float64 scan is a tree of
+// depth 6 over its inputs.
+template <int CTRL, int RM>
+__device__ __forceinline__ long long wm_dpp_i64(long long x) {
+    const int lo = wm_dpp<CTRL, RM>((int)(unsigned long long)x);
+    const int hi = wm_dpp<CTRL, RM>((int)((unsigned long long)x >> 32));
+    return (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+__device__ __forceinline__ int wm_wave_scan_i32(int x) {
+    x += wm_dpp<WM_DPP_ROW_SHR1, 0xF>(x);
+    x += wm_dpp<WM_DPP_ROW_SHR2, 0xF>(x);
+    x += wm_dpp<WM_DPP_ROW_SHR4, 0xF>(x);
+    x += wm_dpp<WM_DPP_ROW_SHR8, 0xF>(x);
+    x += wm_dpp<WM_DPP_ROW_BCAST15, 0xA>(x);
+    x += wm_dpp<WM_DPP_ROW_BCAST31, 0xC>(x);
+    return x;
+}
+__device__ __forceinline__ long long wm_wave_scan_i64(long long x) {
+    x += wm_dpp_i64<WM_DPP_ROW_SHR1, 0xF>(x);
+    x += wm_dpp_i64<WM_DPP_ROW_SHR2, 0xF>(x);
+    x += wm_dpp_i64<WM_DPP_ROW_SHR4, 0xF>(x);
+    x += wm_dpp_i64<WM_DPP_ROW_SHR8, 0xF>(x);
+    x += wm_dpp_i64<WM_DPP_ROW_BCAST15, 0xA>(x);
+    x += wm_dpp_i64<WM_DPP_ROW_BCAST31, 0xC>(x);
+    return x;
+}
+__device__ __forceinline__ double wm_wave_scan_f64(double x) {
+#define WM_F64_STEP(C, R) x += __longlong_as_double(wm_dpp_i64<C, R>(__double_as_longlong(x)))
+    WM_F64_STEP(WM_DPP_ROW_SHR1, 0xF);
+    WM_F64_STEP(WM_DPP_ROW_SHR2, 0xF);
+    WM_F64_STEP(WM_DPP_ROW_SHR4, 0xF);
+    WM_F64_STEP(WM_DPP_ROW_SHR8, 0xF);
+    WM_F64_STEP(WM_DPP_ROW_BCAST15, 0xA);
+    WM_F64_STEP(WM_DPP_ROW_BCAST31, 0xC);
+#undef WM_F64_STEP
+    return x;
+}
+// Wave totals, returned wave-uniform (lane 63 of an inclusive scan).
+__device__ __forceinline__ int wm_wave_total_i32(int x) {
+    return __builtin_amdgcn_readlane(wm_wave_scan_i32(x), 63);
+}
+// Largest of non-negative values, NaN never winning (a NaN input counts as 0).
+__device__ __forceinline__ float wm_wave_max_nonneg(float v) {
+    v = v > 0.0f ? v : 0.0f;
+#define WM_MAX_STEP(C, R)                                                                          \
+    {                                                                                              \
+        const float o = __int_as_float(wm_dpp<C, R>(__float_as_int(v)));                           \
+        v = o > v ? o : v;                                                                         \
+    }
+    WM_MAX_STEP(WM_DPP_ROW_SHR1, 0xF);
+    WM_MAX_STEP(WM_DPP_ROW_SHR2, 0xF);
+    WM_MAX_STEP(WM_DPP_ROW_SHR4, 0xF);
+    WM_MAX_STEP(WM_DPP_ROW_SHR8, 0xF);
+    WM_MAX_STEP(WM_DPP_ROW_BCAST15, 0xA);
+    WM_MAX_STEP(WM_DPP_ROW_BCAST31, 0xC);
+#undef WM_MAX_STEP
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // Wave-level helpers (wave64).
 __device__ __forceinline__ int wm_wave_sum_i32(int v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -35,6 +35,8 @@
 
 #include <cstdint>
 
+#include "wm_internal.h"
+
 namespace wm {
 
 // Inclusive prefix sum over the 64 lanes of a wave (rows of 16 via DPP
@@ -162,94 +164,114 @@ __device__ inline float seq_sum_nonneg(const float *a, uint32_t n) {
 // The one-wave algorithm spends its time on passes: every binade crossing and
 // every halfway case restarts a 512-term scan.  Here the work that does not
 // depend on the running value is done once, by every thread in parallel, and
-// only a short sequential walk remains:
+// only a short sequential walk remains.  Thread t owns the m = ceil(n / NT)
+// consecutive terms k = t*m + j and holds them in registers.
 //
 //  1. A float64 prefix sum P_k (sum of the terms before k) predicts the binade
 //     E of the f32 running sum before term k.  (The f32 sum differs from P_k
 //     by accumulated rounding, far less than the distance to a power of two
 //     for almost every k; every prediction is checked in step 3.)
-//  2. Term k is a break if k = 0, if P_k is not positive, if the predicted
-//     binade changes at k, if a_k / ulp is halfway between integers (the
-//     rounding then depends on the running significand's parity) or if it is
-//     huge or not finite.  Every other term contributes the integer increment
-//     RN_int(a_k / ulp(E)).  A block-wide integer prefix scan gives every
-//     segment between two breaks its total increment D.
-//  3. One wave walks the breaks in order.  For a segment it checks that the
-//     running sum s (exact so far) is a normal number in the predicted binade
-//     with significand N and N + D <= 2^24 - 2; then, as in the one-wave
-//     algorithm, s + (the segment, added term by term) = (N + D) * ulp
-//     exactly.  A break term is added with an ordinary f32 add.  A segment
-//     whose check fails is summed by the one-wave algorithm from s instead,
-//     so every outcome is the left-to-right sum.
+//  2. Term k is a break if k = 0, if P_k or P_(k+1) is not positive and
+//     finite, if their binades differ, if P_k (k a thread's first term) or
+//     P_(k+1) (k its last) lies close to a power of two (below), if
+//     a_k / ulp(E) is halfway between integers (the rounding
+//     then depends on the running significand's parity) or if it is huge.
+//     Every other term contributes the integer increment RN_int(a_k / ulp(E)).
+//     A wave-wide integer scan places each wave's breaks in its own record
+//     list, with the increment total before each.
+//  3. One wave joins the lists and walks the breaks in order.  For a segment
+//     (the terms between two breaks) it checks that the running sum s, exact
+//     so far, is a normal number in the segment's binade with significand N,
+//     and that N + D <= 2^24 - 2 for the segment's increment total D; then
+//     adding the segment term by term gives exactly (N + D) * ulp, as in the
+//     one-wave algorithm.  A break term is added with an ordinary f32 add.  A
+//     segment whose check fails is summed by the one-wave algorithm from s
+//     instead, so every outcome is the left-to-right sum.
+//
+// Why the "close to a power of two" rule.  The increments of one segment
+// must all be taken with the same binade.  Inside a thread P_(k+1) of term k
+// is bitwise P before term k+1, but across a thread boundary the two values
+// come from different additions: the owner of k adds a_k to its own prefix,
+// the next thread builds its prefix from the wave scan.  Every such value is
+// a sum of non-negative doubles through at most 2*MAXM + 6 + NT/64 + 1 < 2^7
+// additions along any path (MAXM <= 32), so it lies within relative
+// 2^7 * 2^-53 = 2^-46 of the exact prefix, and two computations of one
+// prefix within 2^-45 of each other.  A P_(k+1) farther than 2^-36 from
+// every power of two therefore shares its binade with any other computation
+// of the same prefix; one within 2^-36 makes term k a break, and then the
+// next thread's P_(k+1) (within 2^-36 + 2^-45 < 2^-34) makes term k+1 a
+// break too, so the segment after them starts with a binade computed by the
+// thread that computes its increments.
 //
 // With the squares of an RMSNorm (2560 or 6912 terms) a sum has about 18
-// breaks and a failed prediction in well under 1% of sums.  More than
-// kSeqRecords breaks (adversarial inputs) send the whole sum to the one-wave
-// algorithm.
-constexpr int kSeqRecords = 512;
+// breaks and a failed check in well under 1% of sums.  More than
+// kSeqWaveRecords breaks in one wave (adversarial inputs) send the whole sum
+// to the one-wave algorithm.
+constexpr int kSeqWaveRecords = 32;
+constexpr int kSeqMaxWaves = 16;
 
 struct seq_block_scratch {
-    double dw[16];
-    long long iw[16];
-    int idx[kSeqRecords];
-    int eaf[kSeqRecords];
-    long long pi[kSeqRecords];
-    float val[kSeqRecords];
-    long long total;
+    double dw[kSeqMaxWaves];     // per wave: float64 total of its terms
+    long long wt[kSeqMaxWaves];  // per wave: (breaks << 48) + increment total
+    int idx[kSeqMaxWaves][kSeqWaveRecords];        // term index of the break
+    int eaf[kSeqMaxWaves][kSeqWaveRecords];        // predicted binade after it
+    long long pi[kSeqMaxWaves][kSeqWaveRecords];   // wave's increments before it
+    float val[kSeqMaxWaves][kSeqWaveRecords];      // the term
+    long long woff[kSeqMaxWaves];  // increments of the waves before each wave
+    short map[kSeqMaxWaves * kSeqWaveRecords];    // record r -> wave * R + slot
     float out;
 };
 
-__device__ __forceinline__ double wave_incl_scan_f64(double x) {
-    const int lane = (int)(threadIdx.x & 63);
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const double y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
-    return x;
-}
-__device__ __forceinline__ long long wave_incl_scan_i64(long long x) {
-    const int lane = (int)(threadIdx.x & 63);
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const long long y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
-    return x;
-}
 // floor(log2 x) of a positive, finite, normal double
 __device__ __forceinline__ int exp2floor_f64(double x) {
     return (int)((__double_as_longlong(x) >> 52) & 0x7FF) - 1023;
 }
+// x (positive, finite, normal) within relative 2^-T of a power of two
+__device__ __forceinline__ bool near_pow2_f64(double x, int T) {
+    const unsigned long long mant = (unsigned long long)__double_as_longlong(x) & ((1ull << 52) - 1);
+    return mant <= (1ull << (52 - T)) || (1ull << 52) - mant <= (1ull << (53 - T));
+}
 
-// Left-to-right f32 sum of n non-negative terms a[0..n) (LDS), by every
-// thread of the workgroup (blockDim.x a multiple of 64, at most 1024); the
-// sum comes back in every thread.  MAXM >= ceil(n / blockDim.x).
-template <int MAXM>
-__device__ float seq_sum_block_nonneg(const float *a, uint32_t n, seq_block_scratch *sc) {
-    const uint32_t tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wid = tid >> 6;
+// Left-to-right f32 sum of n non-negative terms, by every thread of a
+// workgroup of NT threads (a multiple of 64, at most 1024).  v[j] holds term
+// k = threadIdx.x * m + j for j < m = ceil(n / NT) <= MAXM and k < n, and 0
+// otherwise; `a` holds all n terms, readable by wave 0 after a barrier (the
+// caller writes it before the call).  The sum comes back in every thread.
+template <int MAXM, int NT>
+__device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const float *a,
+                                     seq_block_scratch *sc) {
+    static_assert(NT % 64 == 0 && NT <= 64 * kSeqMaxWaves, "workgroup size");
+    static_assert(MAXM >= 1 && MAXM <= 32, "terms per thread");
+    constexpr int NW = NT / 64;
+    constexpr int R = kSeqWaveRecords;
+    constexpr long long kLow48 = (1LL << 48) - 1;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wid = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
     if (n == 0) return 0.0f;
-    const uint32_t m = (n + nt - 1) / nt;
+    const uint32_t m = (n + NT - 1) / NT;
     const uint32_t k0 = tid * m;
-    float v[MAXM];
+    // 1. float64 prefix before this thread's first term
     double loc = 0.0;
 #pragma unroll
-    for (int j = 0; j < MAXM; j++) {
-        const uint32_t k = k0 + (uint32_t)j;
-        v[j] = ((uint32_t)j < m && k < n) ? a[k] : 0.0f;
-        loc += (double)v[j];
-    }
-    // 1. P before this thread's first term
-    const double inc = wave_incl_scan_f64(loc);
+    for (int j = 0; j < MAXM; j++) loc += (double)v[j];
+    const double inc = wm_wave_scan_f64(loc);
+    // exclusive prefix: the inclusive scan one lane down
+    double ex = __shfl_up(inc, 1, 64);
+    if (lane == 0) ex = 0.0;
     if (lane == 63) sc->dw[wid] = inc;
     __syncthreads();
-    double P = inc - loc;
-    for (uint32_t w = 0; w < wid; w++) P += sc->dw[w];
-    // 2. breaks and increments
+    double off = 0.0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) off += w < (int)wid ? sc->dw[w] : 0.0;
+    double P = off + ex;
+    // 2. breaks and increments.  Inside a thread P after term k is bitwise P
+    // before term k+1, so the closeness test is needed only where the prefix
+    // comes from another thread: before the first term and after the last.
     bool brk[MAXM];
     int incr[MAXM], eaf[MAXM];
     long long pi_loc = 0;
     int nb = 0;
+    const uint32_t last = min(m, n > k0 ? n - k0 : 0u) - 1;  // index of the last valid term
 #pragma unroll
     for (int j = 0; j < MAXM; j++) {
         const uint32_t k = k0 + (uint32_t)j;
@@ -260,6 +282,8 @@ __device__ float seq_sum_block_nonneg(const float *a, uint32_t n, seq_block_scra
         const int eb = pb_ok ? exp2floor_f64(pb) : 0;
         const int ea = pa_ok ? exp2floor_f64(pa) : -1000;
         bool b = k == 0 || !pb_ok || !pa_ok || ea != eb;
+        if (j == 0) b = b || near_pow2_f64(pb, 34);
+        b = b || ((uint32_t)j == last && near_pow2_f64(pa, 36));
         int d = 0;
         if (!b) {
             const float r = ldexpf(v[j], 23 - eb);  // a_k / ulp; exact unless < 2^-126
@@ -272,77 +296,136 @@ __device__ float seq_sum_block_nonneg(const float *a, uint32_t n, seq_block_scra
         nb += brk[j] ? 1 : 0;
         pi_loc += incr[j];
     }
-    // block-wide exclusive scan of (break count << 48) + increment sum
+    // wave-local exclusive scan of (break count << 48) + increment sum; a
+    // wave has at most 64 * MAXM * 2^22 < 2^48 of increments
     const long long packed = ((long long)nb << 48) + pi_loc;
-    const long long pinc = wave_incl_scan_i64(packed);
-    if (lane == 63) sc->iw[wid] = pinc;
-    __syncthreads();
-    long long pex = pinc - packed;
-    for (uint32_t w = 0; w < wid; w++) pex += sc->iw[w];
-    if (tid == nt - 1) sc->total = pex + packed;
+    const long long pinc = wm_wave_scan_i64(packed);
+    const long long pex = pinc - packed;
     int pos = (int)(pex >> 48);
-    long long pi = pex & ((1LL << 48) - 1);
+    long long pi = pex & kLow48;
 #pragma unroll
     for (int j = 0; j < MAXM; j++) {
         if (brk[j]) {
-            if (pos < kSeqRecords) {
-                sc->idx[pos] = (int)(k0 + (uint32_t)j);
-                sc->eaf[pos] = eaf[j];
-                sc->pi[pos] = pi;
-                sc->val[pos] = v[j];
+            if (pos < R) {
+                sc->idx[wid][pos] = (int)(k0 + (uint32_t)j);
+                sc->eaf[wid][pos] = eaf[j];
+                sc->pi[wid][pos] = pi;
+                sc->val[wid][pos] = v[j];
             }
             pos++;
         } else {
             pi += incr[j];
         }
     }
+    if (lane == 63) sc->wt[wid] = pinc;
     __syncthreads();
-    // 3. the walk over the breaks (one wave)
+    // 3. the walk over the breaks (wave 0)
     if (wid == 0) {
-        const long long tot = sc->total;
-        const int nbrk = (int)(tot >> 48);
-        const long long pi_tot = tot & ((1LL << 48) - 1);
+        const long long wt = (int)lane < NW ? sc->wt[lane] : 0;
+        const int wc = (int)(wt >> 48);
+        const long long wp = wt & kLow48;
         float s = 0.0f;
-        if (nbrk > kSeqRecords) {
+        if (__builtin_amdgcn_ballot_w64(wc > R) != 0) {
             s = seq_sum_nonneg_from(0.0f, a, n);
         } else {
-            int prev_t = -1, e_seg = -1000;
-            long long prev_pi = 0;
-            // records 0..nbrk-1 and a final one at index n closing the last segment
+            const int cinc = wm_wave_scan_i32(wc);
+            const long long winc = wm_wave_scan_i64(wp);
+            const int cex = cinc - wc;  // first record of wave `lane`
+            const int nbrk = __builtin_amdgcn_readlane(cinc, 63);
+            const long long pi_tot =
+                (long long)(((unsigned long long)(unsigned)__builtin_amdgcn_readlane(
+                                 (int)((unsigned long long)winc >> 32), 63)
+                             << 32) |
+                            (unsigned)__builtin_amdgcn_readlane((int)winc, 63));
+            // record index -> (wave, slot), and each wave's increment offset
+            if ((int)lane < NW) {
+                sc->woff[lane] = winc - wp;
+                for (int j = 0; j < wc; j++) sc->map[cex + j] = (short)(lane * R + j);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const int *idx = &sc->idx[0][0], *eafp = &sc->eaf[0][0];
+            const long long *pis = &sc->pi[0][0];
+            const float *vals = &sc->val[0][0];
             for (int base = 0; base <= nbrk; base += 64) {
+                // lane l prepares step r = base + l: the segment between
+                // records r-1 and r, then record r's term (r == nbrk: the
+                // end; r > nbrk: a step that changes nothing)
                 const int r = base + (int)lane;
-                int ri = (int)n, re = 0;
-                long long rp = pi_tot;
-                float rv = 0.0f;
+                int t1 = (int)n, cnt = 0;
+                long long p1 = pi_tot;
+                float v1 = 0.0f;
                 if (r < nbrk) {
-                    ri = sc->idx[r];
-                    re = sc->eaf[r];
-                    rp = sc->pi[r];
-                    rv = sc->val[r];
+                    const int f = sc->map[r];
+                    t1 = idx[f];
+                    p1 = sc->woff[f / R] + pis[f];
+                    v1 = vals[f];
                 }
+                int t0 = -1, e0 = -1000;
+                long long p0 = 0;
+                if (r >= 1 && r - 1 < nbrk) {
+                    const int f = sc->map[r - 1];
+                    t0 = idx[f];
+                    e0 = eafp[f];
+                    p0 = sc->woff[f / R] + pis[f];
+                }
+                if (r <= nbrk) cnt = t1 - t0 - 1;  // terms in the segment
+                const long long dl = p1 - p0;      // their increments
+                const int D = (dl >= 0 && dl <= (1LL << 24)) ? (int)dl : (1 << 30);
                 const int here = min(64, nbrk + 1 - base);
-                for (int i = 0; i < here; i++) {
-                    const int t = __builtin_amdgcn_readlane(ri, i);
-                    const int rpi_lo = __builtin_amdgcn_readlane((int)(rp & 0xFFFFFFFF), i);
-                    const int rpi_hi = __builtin_amdgcn_readlane((int)(rp >> 32), i);
-                    const long long tpi = ((long long)rpi_hi << 32) | (unsigned int)rpi_lo;
-                    const int cnt = t - prev_t - 1;
-                    if (cnt > 0) {
-                        const long long d = tpi - prev_pi;
-                        const uint32_t bits = __float_as_uint(s);
-                        const uint32_t ef = bits >> 23;  // s >= +0 or NaN
-                        const long long N = (long long)((bits & 0x7FFFFFu) | 0x800000u);
-                        const bool ok = ef - 1u < 254u && (int)ef - 127 == e_seg && d >= 0 &&
-                                        N + d <= (1LL << 24) - 2;
-                        if (ok) s = ldexpf((float)(N + d), e_seg - 23);
-                        else s = seq_sum_nonneg_from(s, a + prev_t + 1, (uint32_t)cnt);
+                // When step r's check holds (s normal in binade e, s >= 2^e,
+                // s + D*ulp <= (2^24 - 2) * ulp), its segment adds exactly
+                // A = D * 2^(e-23): s + A is (N + D) * ulp, representable, so
+                // the f32 add is exact.  The serial part is then two f32 adds
+                // per step, t = s + A; s = t + V (V: the break term, +0 past
+                // the last record); every lane checks its own step afterwards
+                // from the value s had on entry.
+                const bool seg = cnt > 0;
+                const bool e_ok = e0 >= -126 && e0 <= 127;
+                const float A = seg && e_ok ? ldexpf((float)D, e0 - 23) : 0.0f;
+                const float lo = seg ? (e_ok ? ldexpf(1.0f, e0) : __int_as_float(0x7F800000)) : 0.0f;
+                const float hi = seg ? (e_ok ? ldexpf(16777214.0f, e0 - 23) : -1.0f)
+                                     : __int_as_float(0x7F800000);
+                const float s0 = s;
+                // s as a per-lane value, so the compiler keeps the chain on
+                // the vector unit (all lanes hold the same number)
+                float sv;
+                asm volatile("v_mov_b32 %0, %1" : "=v"(sv) : "v"(s));
+                float s_in = 0.0f;
+                for (int g = 0; g < here; g += 8) {
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        const int i = g + u;
+                        const float Ai = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(A), i));
+                        const float Vi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v1), i));
+                        s_in = (int)lane == i ? sv : s_in;
+                        sv = (sv + Ai) + Vi;
                     }
-                    if (t < (int)n) {
-                        s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rv), i));
-                        e_seg = __builtin_amdgcn_readlane(re, i);
+                }
+                s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sv)));
+                // lanes past `here` hold no step; a NaN s fails every check
+                const bool ok = (int)lane >= here || !seg || (s_in >= lo && s_in + A <= hi);
+                const int bad = __builtin_amdgcn_ballot_w64(!ok) != 0;
+                if (__builtin_amdgcn_readfirstlane(bad) != 0) {
+                    s = s0;
+                    for (int i = 0; i < here; i++) {
+                        const int c = __builtin_amdgcn_readlane(cnt, i);
+                        if (c > 0) {
+                            const int Di = __builtin_amdgcn_readlane(D, i);
+                            const int e = __builtin_amdgcn_readlane(e0, i);
+                            const uint32_t bits = (uint32_t)__builtin_amdgcn_readfirstlane(__float_as_int(s));
+                            const uint32_t ef = bits >> 23;
+                            const int N = (int)((bits & 0x7FFFFFu) | 0x800000u);
+                            if (ef - 1u < 254u && (int)ef - 127 == e && N + Di <= (1 << 24) - 2) {
+                                s = ldexpf((float)(N + Di), e - 23);
+                            } else {  // the segment term by term
+                                const int tp = __builtin_amdgcn_readlane(t0, i);
+                                s = seq_sum_nonneg_from(s, a + tp + 1, (uint32_t)c);
+                            }
+                        }
+                        s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v1), i));
                     }
-                    prev_t = t;
-                    prev_pi = tpi;
                 }
             }
         }

@@ -65,6 +65,15 @@ def cases():
     # long random runs with many ties: values on a coarse grid
     g = (rng.integers(0, 64, 20000) * 0.25).astype(np.float32)
     out.append(("grid", np.concatenate([[2.0 ** 22], g]).astype(np.float32)))
+    # exact prefix 2^-52 below 4096 at a thread boundary while the f32 sum
+    # lags 3 ulps behind (absorbed terms), then 2^-11, a tie and zeros
+    head = [4096.0 - 3 * 2.0 ** -12] + [2.0 ** -14] * 11 + [2.0 ** -i for i in range(15, 41)]
+    out.append(("prefix_at_power_of_two",
+                np.array(head + [2.0 ** -11, 2.0 ** -12] + [0.0] * 1460, np.float32)))
+    # the same with the boundary prefixes on many powers of two (m = 4)
+    ones = np.ones(4000, np.float32)
+    ones[::7] = np.float32(2.0 ** -30)
+    out.append(("ones_on_powers", ones))
     return out
 
 

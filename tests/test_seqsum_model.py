@@ -81,7 +81,8 @@ def model_sum(a):
     return s, max_pass
 
 
-BLOCK_RECORDS = 512  # break records the workgroup algorithm keeps (else: one-wave path)
+WAVE_RECORDS = 32  # break records per wave the workgroup algorithm keeps (else: one-wave path)
+BLOCK_THREADS = 1024
 
 
 def _exp2floor(x):
@@ -89,45 +90,78 @@ def _exp2floor(x):
     return int(np.frexp(x)[1]) - 1
 
 
-def model_block_sum(a, stats=None):
-    """Model of wm::seq_sum_block_nonneg: returns the sum."""
+def _near_pow2(x, t):
+    """x (positive, finite) within relative 2^-t of a power of two, by its bits."""
+    mant = int(np.array(x, np.float64).view(np.uint64)) & ((1 << 52) - 1)
+    return mant <= (1 << (52 - t)) or (1 << 52) - mant <= (1 << (53 - t))
+
+
+def model_block_sum(a, stats=None, nt=BLOCK_THREADS, start_prefix=None, near_rule=True):
+    """Model of wm::seq_sum_block_owned: returns the sum.
+
+    Thread t owns terms t*m .. t*m+m-1 (m = ceil(n / nt)) and starts from a
+    float64 prefix of the terms before them; `start_prefix(t, exact_prefix)`
+    may return another value for it, standing for a different order of the
+    same additions on the device (within relative 2^-45 of the exact one)."""
     a = np.asarray(a, np.float32)
     n = a.size
     if n == 0:
         return f32(0.0)
+    m = -(-n // nt)
     with np.errstate(all="ignore"):
-        P = np.concatenate([[0.0], np.cumsum(a.astype(np.float64))])  # P[k]: sum before term k
-    recs = []  # (index, binade after, increment prefix before, value)
-    pi = 0
-    for k in range(n):
-        pb, pa, v = P[k], P[k + 1], a[k]
-        brk = k == 0 or not (pb > 0) or not np.isfinite(pb) or not np.isfinite(pa)
-        if not brk:
-            eb, ea = _exp2floor(pb), _exp2floor(pa)
-            brk = ea != eb
-        if not brk:
+        S = np.concatenate([[0.0], np.cumsum(a.astype(np.float64))])  # S[k]: sum before term k
+    waves = {}  # wave -> [(index, binade after, wave increments before, value)]
+    wave_pi = {}
+    for t in range(-(-n // m)):
+        k0 = t * m
+        w = t // 64
+        P = S[k0]
+        if start_prefix is not None and t > 0:
+            P = start_prefix(t, P)
+        recs = waves.setdefault(w, [])
+        for k in range(k0, min(k0 + m, n)):
+            v = a[k]
+            pb = P
             with np.errstate(all="ignore"):
-                r = np.float32(np.ldexp(v, 23 - eb))
-            brk = not (r < f32(2.0 ** 22)) or (r - np.floor(r)) == f32(0.5)
-        if brk:
-            ea = _exp2floor(pa) if (pa > 0 and np.isfinite(pa)) else -1000
-            recs.append((k, ea, pi, v))
-        else:
-            pi += int(np.rint(r))
+                pa = np.float64(P) + np.float64(v)
+            P = pa
+            pb_ok = 0 < pb < 1e300
+            pa_ok = 0 < pa < 1e300
+            brk = k == 0 or not pb_ok or not pa_ok
+            if not brk:
+                eb, ea = _exp2floor(pb), _exp2floor(pa)
+                brk = ea != eb
+                if near_rule:  # only where the prefix crosses a thread boundary
+                    brk = brk or (k == k0 and _near_pow2(pb, 34)) or \
+                        (k == min(k0 + m, n) - 1 and _near_pow2(pa, 36))
+            if not brk:
+                with np.errstate(all="ignore"):
+                    r = np.float32(np.ldexp(v, 23 - eb))
+                brk = not (r < f32(2.0 ** 22)) or (r - np.floor(r)) == f32(0.5)
+            if brk:
+                ea = _exp2floor(pa) if pa_ok else -1000
+                recs.append((k, ea, wave_pi.get(w, 0), v))
+            else:
+                wave_pi[w] = wave_pi.get(w, 0) + int(np.rint(r))
     if stats is not None:
-        stats["breaks"] = len(recs)
+        stats["breaks"] = sum(len(r) for r in waves.values())
         stats["fallback_segments"] = 0
-    if len(recs) > BLOCK_RECORDS:
+    if any(len(r) > WAVE_RECORDS for r in waves.values()):
         return model_sum(a)[0]
+    # join the wave lists: global increment prefix = increments of earlier waves + wave-local
+    recs, off = [], 0
+    for w in sorted(set(waves) | set(wave_pi)):
+        recs += [(k, ea, off + p, v) for (k, ea, p, v) in waves.get(w, [])]
+        off += wave_pi.get(w, 0)
     s = f32(0.0)
     prev_t, prev_pi, e_seg = -1, 0, None
-    for (t, ea, pit, v) in recs + [(n, None, pi, None)]:
+    for (t, ea, pit, v) in recs + [(n, None, off, None)]:
         cnt = t - prev_t - 1
         if cnt > 0:
             d = pit - prev_pi
             bits = int(np.array(s, np.float32).view(np.uint32))
             ef = bits >> 23
-            ok = 1 <= ef <= 254 and e_seg is not None and ef - 127 == e_seg
+            ok = 1 <= ef <= 254 and e_seg is not None and ef - 127 == e_seg and 0 <= d <= (1 << 24)
             if ok:
                 N = (bits & 0x7FFFFF) | 0x800000
                 ok = N + d <= (1 << 24) - 2
@@ -258,3 +292,52 @@ def test_block_model_rms_inputs_take_the_fast_path():
             st = {}
             assert same(model_block_sum(a, st), sequential(a))
             assert st["breaks"] < 64 and st["fallback_segments"] <= 2
+
+
+def _boundary_case():
+    """Terms whose exact prefix at a thread boundary (term 38, m = 2) is
+    4096 - 2^-40, while the f32 running sum lags at 4096 - 3*2^-12: the
+    terms 2^-14 ... 2^-40 round away in f32.  Then 2^-11 (2 ulps below 4096,
+    1 ulp above), the tie 2^-12, and zeros."""
+    head = [4096.0 - 3 * 2.0 ** -12] + [2.0 ** -14] * 11 + [2.0 ** -i for i in range(15, 41)]
+    tail = [2.0 ** -11, 2.0 ** -12] + [0.0] * 1460
+    return np.array(head + tail, np.float32)
+
+
+def _flip_across_pow2(t, P):
+    """Another order's value of a prefix: within relative 2^-45 of P, on the
+    other side of a power of two whenever P is that close to one."""
+    e = _exp2floor(P)
+    for j in (e, e + 1):
+        if abs(P - 2.0 ** j) <= 2.0 ** (j - 46):
+            return 2.0 ** j * (1 + 2.0 ** -47) if P < 2.0 ** j else 2.0 ** j * (1 - 2.0 ** -47)
+    return P
+
+
+def test_block_model_boundary_prefix_order():
+    """A thread's prefix computed in another order may land on the other
+    side of a power of two than the previous thread's running prefix.
+    The near-power-of-two breaks keep the sum exact; without them the
+    segment's increments are taken in two different binades."""
+    a = _boundary_case()
+    assert -(-a.size // BLOCK_THREADS) == 2
+    want = sequential(a)
+    assert same(model_block_sum(a, start_prefix=_flip_across_pow2), want)
+    assert not same(model_block_sum(a, start_prefix=_flip_across_pow2, near_rule=False), want)
+
+
+def test_block_model_boundary_fuzz():
+    """Random prefixes pushed across nearby powers of two at every thread start."""
+    rng = np.random.default_rng(17)
+    for i in range(200):
+        n = int(rng.integers(1025, 7000))
+        m = -(-n // BLOCK_THREADS)
+        a = rng.integers(1, 4, n).astype(np.float32)
+        # make some thread boundary sit just below or at a power of two
+        k = m * int(rng.integers(1, n // m))
+        pre = float(np.sum(a[:k], dtype=np.float64))
+        target = 2.0 ** (int(np.log2(pre)) + 1)
+        a[k - 1] = np.float32(a[k - 1] + (target - pre) - rng.choice([0.0, 2.0 ** -20]))
+        if not np.isfinite(a).all() or (a < 0).any():
+            continue
+        assert same(model_block_sum(a, start_prefix=_flip_across_pow2), sequential(a)), f"case {i}"
