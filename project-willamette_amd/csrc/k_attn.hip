@@ -11,7 +11,8 @@
 //   with k_p[i] = (q8 as f32) * k_scale[p] (same for v).
 //
 // Every chain above is evaluated in exactly that order (the softmax
-// denominator through wm::seq_sum_nonneg), so the output is bit-identical.
+// denominator through wm::seq_sum_block_owned), so the output is
+// bit-identical.
 #include "wm_internal.h"
 #include "wm_seqsum.h"
 
@@ -27,32 +28,79 @@ struct attn_args {
     float *out;              // [n_heads][head_dim]
     uint32_t n_past, kv_dim, head_dim, group, score_stride;
     float scale;
+    // This token's K (after RoPE) and V, [kv_dim] f32: position n_past - 1
+    // is not in the cache yet.  Each kernel quantises what it needs of them
+    // exactly as KVCache::append does; one workgroup of each writes the
+    // cache row (k_row / v_row, kv_dim bytes) and its scale.
+    const float *k_new, *v_new;
+    const uint32_t *kv_absmax;  // [2]: absmax of k_new, v_new (float bits), by the QKV matvec
+    int8_t *k_row, *v_row;
+    float *k_row_scale, *v_row_scale;
 };
 
-// scores[h][p] = (Σ_i q_h[i] * k_p[i]) * scale.  One lane per position.
+constexpr uint32_t kMaxHeadDim = 128;
+
+// KVCache::append's quantiser (src/model/kv_cache.rs:245-259) for one value,
+// given the vector's absmax (NaN never raises it): a zero or non-finite
+// absmax gives 0 with scale 0.
+__device__ __forceinline__ bool kv_zero(float absmax) { return absmax == 0.0f || !isfinite(absmax); }
+__device__ __forceinline__ int8_t kv_q(float v, float absmax) {
+    return kv_zero(absmax) ? (int8_t)0 : (int8_t)wm_round_clamp_i8(v * (127.0f / absmax));
+}
+__device__ __forceinline__ float kv_scale(float absmax) { return kv_zero(absmax) ? 0.0f : absmax / 127.0f; }
+
+// scores[h][p] = (Σ_i q_h[i] * k_p[i]) * scale.  One lane per cached
+// position, blocks of 64; grid (n_heads, ceil((n_past - 1) / 64) + 1).  The
+// last block of each head scores position n_past - 1, whose K row is this
+// token's k_new quantised here exactly as KVCache::append does (head 0's also
+// writes the row to the cache): the products q_i * k_i lane-parallel, then
+// their sum in order by one lane.  It runs beside the cached blocks instead of
+// after its own loads.
 __global__ __launch_bounds__(64) void k_attn_scores(attn_args a) {
-    const uint32_t h = blockIdx.x, p = blockIdx.y * 64 + threadIdx.x;
-    if (p >= a.n_past) return;
-    const uint32_t kvh = h / a.group;
+    const uint32_t h = blockIdx.x, lane = threadIdx.x;
+    const uint32_t kvh = h / a.group, pnew = a.n_past - 1;
     const float *qh = a.q + (uint64_t)h * a.head_dim;
+    if (blockIdx.y == gridDim.y - 1) {
+        __shared__ float prod[kMaxHeadDim];
+        const float kabs = __uint_as_float(a.kv_absmax[0]);
+        const float ksn = kv_scale(kabs);
+        for (uint32_t i = lane; i < a.head_dim; i += 64) {
+            const float kd = (float)kv_q(a.k_new[kvh * a.head_dim + i], kabs) * ksn;  // read_into
+            prod[i] = qh[i] * kd;
+        }
+        if (h == 0) {
+            for (uint32_t i = lane; i < a.kv_dim; i += 64) a.k_row[i] = kv_q(a.k_new[i], kabs);
+            if (lane == 0) *a.k_row_scale = ksn;
+        }
+        wm_sync_lds();
+        if (lane == 0) {
+            float s = 0.0f;
+            for (uint32_t i = 0; i < a.head_dim; i += 4) {
+                const float4 f = *reinterpret_cast<const float4 *>(prod + i);
+                s = s + f.x; s = s + f.y; s = s + f.z; s = s + f.w;
+            }
+            a.scores[(uint64_t)h * a.score_stride + pnew] = s * a.scale;
+        }
+        return;
+    }
+    const uint32_t p = blockIdx.y * 64 + lane;
+    if (p >= pnew) return;
+    const uint32_t nb = a.head_dim / 16;  // 4 or 8 sixteen-byte segments
     const int8_t *kp = a.k_cache + (uint64_t)p * a.kv_dim + kvh * a.head_dim;
     const float ksc = a.k_scales[p];
+    int4 raw[kMaxHeadDim / 16];
+#pragma unroll
+    for (int b = 0; b < (int)(kMaxHeadDim / 16); b++)  // all 16-byte loads in flight together
+        raw[b] = *reinterpret_cast<const int4 *>(kp + (b < (int)nb ? b : 0) * 16);
     float s = 0.0f;
-    for (uint32_t i0 = 0; i0 < a.head_dim; i0 += 128) {  // head_dim is a multiple of 64
-        const uint32_t nb = a.head_dim - i0 >= 128 ? 8 : 4;
-        int4 raw[8];
 #pragma unroll
-        for (int b = 0; b < 8; b++)  // all 16-byte loads in flight together
-            raw[b] = *reinterpret_cast<const int4 *>(kp + i0 + (b < (int)nb ? b : 0) * 16);
+    for (int b = 0; b < (int)(kMaxHeadDim / 16); b++) {
+        if (b < (int)nb) {
+            const int8_t *kb = reinterpret_cast<const int8_t *>(&raw[b]);
 #pragma unroll
-        for (int b = 0; b < 8; b++) {
-            if (b < (int)nb) {
-                const int8_t *kb = reinterpret_cast<const int8_t *>(&raw[b]);
-#pragma unroll
-                for (int t = 0; t < 16; t++) {
-                    const float kd = (float)kb[t] * ksc;  // read_into: q as f32 * scale
-                    s = s + qh[i0 + b * 16 + t] * kd;
-                }
+            for (int t = 0; t < 16; t++) {
+                const float kd = (float)kb[t] * ksc;  // read_into: q as f32 * scale
+                s = s + qh[b * 16 + t] * kd;
             }
         }
     }
@@ -72,6 +120,7 @@ constexpr int kPStride = 68;    // floats per dim row of a product tile
 // flight at once; the softmax denominator is the exact sequential sum; then
 // waves 1-2 write tiles of products w_p * v_p[d] while wave 0 adds the
 // previous tile, one chain per dimension.
+template <int MAXM>  // n_past <= MAXM * kThreads (the exact sum's terms per thread)
 __global__ __launch_bounds__(kThreads) void k_attn_softmax_v(attn_args a) {
     extern __shared__ __align__(16) float sm[];
     const uint32_t n = a.n_past;
@@ -81,14 +130,16 @@ __global__ __launch_bounds__(kThreads) void k_attn_softmax_v(attn_args a) {
     int4 *vq = reinterpret_cast<int4 *>(vsc + npad);        // [npad] x 16 int8
     float *prod = reinterpret_cast<float *>(vq + npad);     // [2][kDims][kPStride]
     __shared__ float red[16];
-    __shared__ float s_inv;
-    __shared__ int s_mode;
+    __shared__ wm::seq_block_scratch seq_scratch;
     const uint32_t h = blockIdx.x, d0 = blockIdx.y * kDims, tid = threadIdx.x;
     const uint32_t kvh = h / a.group;
     const int8_t *vseg = a.v_cache + kvh * a.head_dim + d0;
     const float *sc = a.scores + (uint64_t)h * a.score_stride;
     __shared__ uint64_t exp_tab[32];
     if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
+    // this token's V (position n_past - 1 is not in the cache yet)
+    const uint32_t pnew = n - 1;
+    const float vabs = __uint_as_float(a.kv_absmax[1]);
     // 1. the loads, 4 per thread per round with clamped indices so none is
     //    conditional and all 12 of a round are in flight together
     float m = -INFINITY;
@@ -115,6 +166,13 @@ __global__ __launch_bounds__(kThreads) void k_attn_softmax_v(attn_args a) {
     }
     // 2. softmax (attention.rs:45-73)
     const float mx = wm_block_max_nonan(m, red);
+    if (tid < kDims)  // the new position's slice, quantised as KVCache::append does
+        reinterpret_cast<int8_t *>(vq + pnew)[tid] = kv_q(a.v_new[kvh * a.head_dim + d0 + tid], vabs);
+    if (tid == 0) vsc[pnew] = kv_scale(vabs);
+    if (h == 0 && blockIdx.y == 0) {
+        for (uint32_t i = tid; i < a.kv_dim; i += kThreads) a.v_row[i] = kv_q(a.v_new[i], vabs);
+        if (tid == 0) *a.v_row_scale = kv_scale(vabs);
+    }
     float *out = a.out + (uint64_t)h * a.head_dim + d0;
     if (!isfinite(mx)) {  // every weight becomes 0 -> output stays 0
         if (tid < kDims) out[tid] = 0.0f;
@@ -128,27 +186,29 @@ __global__ __launch_bounds__(kThreads) void k_attn_softmax_v(attn_args a) {
             const uint32_t p = min(base + tid + (uint32_t)i * kThreads, n - 1);
             e[i] = wm::expf_glibc(wts[p] - mx, exp_tab);
         }
-        __syncthreads();  // every read of this round before any write
+        wm_sync_lds();  // every read of this round before any write
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t p = base + tid + (uint32_t)i * kThreads;
             if (p < n) wts[p] = e[i];
         }
     }
-    __syncthreads();
-    if (tid < 64) {
-        const float sum = wm::seq_sum_nonneg(wts, n);
-        if (tid == 0) {
-            s_mode = sum > 0.0f;
-            s_inv = 1.0f / sum;
-        }
+    wm_sync_lds();
+    // Σ exp left to right (attention.rs:63-66), exactly, by the workgroup;
+    // thread t takes the terms t*m .. t*m+m-1
+    float ev[MAXM];
+    {
+        const uint32_t m = (n + kThreads - 1) / kThreads, k0 = tid * m;
+#pragma unroll
+        for (int j = 0; j < MAXM; j++)
+            ev[j] = ((uint32_t)j < m && k0 + (uint32_t)j < n) ? wts[k0 + j] : 0.0f;
     }
-    __syncthreads();
-    if (s_mode) {
-        const float inv = s_inv;
+    const float sum = wm::seq_sum_block_owned<MAXM, kThreads>(ev, n, wts, &seq_scratch);
+    if (sum > 0.0f) {
+        const float inv = 1.0f / sum;
         for (uint32_t p = tid; p < n; p += kThreads) wts[p] = wts[p] * inv;
     }
-    __syncthreads();
+    wm_sync_lds();
     // 3. products of tile t (waves 1-2) while wave 0 adds tile t - 1
     const uint32_t n_tiles = (n + kTile - 1) / kTile;
     const uint32_t pt = tid - 64, pl = pt >> 1, dh = (pt & 1) * 8;
@@ -188,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void k_attn_softmax_v(attn_args a) {
                 for (uint32_t q = 0; q < tn; q++) acc = acc + src[q];
             }
         }
-        __syncthreads();
+        wm_sync_lds();
     }
     if (tid < kDims) out[tid] = acc;
 }
@@ -198,12 +258,24 @@ __global__ __launch_bounds__(kThreads) void k_attn_softmax_v(attn_args a) {
 void wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_scales,
                          const int8_t *v_cache, const float *v_scales, float *scores,
                          uint32_t score_stride, float *out, uint32_t n_heads, uint32_t n_kv_heads,
-                         uint32_t head_dim, uint32_t n_past, float scale, hipStream_t s) {
-    attn_args a{q, k_cache, k_scales, v_cache, v_scales, scores, out, n_past,
-                n_kv_heads * head_dim, head_dim, n_heads / n_kv_heads, score_stride, scale};
-    hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, (n_past + 63) / 64), dim3(64), 0, s, a);
+                         uint32_t head_dim, uint32_t n_past, float scale, const float *k_new,
+                         const float *v_new, const uint32_t *kv_absmax, hipStream_t s) {
+    const uint32_t kv_dim = n_kv_heads * head_dim;
+    int8_t *k_row = const_cast<int8_t *>(k_cache) + (uint64_t)(n_past - 1) * kv_dim;
+    int8_t *v_row = const_cast<int8_t *>(v_cache) + (uint64_t)(n_past - 1) * kv_dim;
+    attn_args a{q, k_cache, k_scales, v_cache, v_scales, scores, out, n_past, kv_dim, head_dim,
+                n_heads / n_kv_heads, score_stride, scale, k_new, v_new, kv_absmax, k_row, v_row,
+                const_cast<float *>(k_scales) + (n_past - 1), const_cast<float *>(v_scales) + (n_past - 1)};
+    hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, (n_past - 1 + 63) / 64 + 1), dim3(64), 0, s, a);
     const size_t npad = ((size_t)n_past + 3) & ~(size_t)3;
     const size_t lds = (size_t)wm::seq_sum_padded(n_past) * 4 + npad * (4 + 16) +
                        (size_t)2 * kDims * kPStride * 4;
-    hipLaunchKernelGGL(k_attn_softmax_v, dim3(n_heads, head_dim / kDims), dim3(kThreads), lds, s, a);
+    if (n_past > 22 * kThreads) return;  // unreachable: models are limited to 4096 positions
+    const dim3 grid(n_heads, head_dim / kDims);
+    if (n_past <= 8 * kThreads)
+        hipLaunchKernelGGL(k_attn_softmax_v<8>, grid, dim3(kThreads), lds, s, a);
+    else if (n_past <= 16 * kThreads)
+        hipLaunchKernelGGL(k_attn_softmax_v<16>, grid, dim3(kThreads), lds, s, a);
+    else  // n_past <= 4096 (the model's context limit) < 22 * kThreads
+        hipLaunchKernelGGL(k_attn_softmax_v<22>, grid, dim3(kThreads), lds, s, a);
 }

@@ -71,7 +71,7 @@ __global__ __launch_bounds__(1024) void k_quantize_act(const float *__restrict__
     for (uint32_t i = tid; i < n; i += blockDim.x) m = wm_max_nonan(m, fabsf(x[i]));
     m = wm_wave_max_nonan(m);
     if (lane == 0) s_max[wid] = m;
-    __syncthreads();
+    wm_sync_lds();
     float max_abs = 0.0f;
     for (int w = 0; w < (int)(blockDim.x >> 6); w++) max_abs = wm_max_nonan(max_abs, s_max[w]);
     int sum = 0;
@@ -87,7 +87,7 @@ __global__ __launch_bounds__(1024) void k_quantize_act(const float *__restrict__
     }
     sum = wm_wave_sum_i32(sum);
     if (lane == 0) s_sum[wid] = sum;
-    __syncthreads();
+    wm_sync_lds();
     if (tid == 0) {
         int t = 0;
         for (int w = 0; w < (int)(blockDim.x >> 6); w++) t += s_sum[w];
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(64) void k_i2s_partial(i2s_multi m, uint32_t n_chun
             cur[u][q] = wm_load_stream(wp + q * gstride + min((uint32_t)u, nc - 1) * I2S_GROUP_ROWS);
     const int4 *ag = reinterpret_cast<const int4 *>(act) + (uint64_t)c0 * 4;
     for (uint32_t i = r; i < nc * 4; i += 64) reinterpret_cast<int4 *>(act_s)[i] = ag[i];
-    __syncthreads();
+    wm_sync_lds();
     int acc16[RG], acc4[RG], acc1[RG];
 #pragma unroll
     for (int q = 0; q < RG; q++) acc16[q] = acc4[q] = acc1[q] = 0;
@@ -197,6 +197,169 @@ __global__ __launch_bounds__(64) void k_i2s_partial(i2s_multi m, uint32_t n_chun
     for (int q = 0; q < RG; q++)
         partial[(uint64_t)s * rows_total + (uint64_t)(gg + q) * I2S_GROUP_ROWS + r] =
             (acc16[q] >> 4) + (acc4[q] >> 2) + acc1[q];
+}
+
+// --------------------------------------------------------------------------
+// matvec with the K split inside the workgroup, and fused epilogues
+// --------------------------------------------------------------------------
+//
+// One workgroup per unit of UG 64-row groups; its W waves split the chunks
+// of K between them (wave w: chunks [n_chunks*w/W, n_chunks*(w+1)/W)), each
+// computing the unit's rows over its slice exactly as k_i2s_partial does;
+// the W partial dots meet in LDS (exact integers, so the split changes
+// nothing) and the unit's threads finish the rows:
+//   y = (w_scale * act_scale) * (float)(Σ c*a - Σ a)   (bitlinear_sse2.rs:327-339)
+// then, by MODE,
+//   WM_FUSED_PLAIN   y to out[t]
+//   WM_FUSED_GATEUP  units are row groups of gate (tensor 0) and up (tensor
+//                    1) together: h = relu(gate)^2 * up (ffn.rs:37-65) to out[0]
+//   WM_FUSED_ROPE    units are heads (UG = head_dim / 64 groups) of Q, K, V;
+//                    NEOX RoPE at `pos` on the tensors in rope_mask
+//                    (primitives.rs:285-345), then to out[t]
+struct i2s_fused_args {
+    const uint8_t *w[WM_FUSED_MAX_TENSORS];
+    float w_scale[WM_FUSED_MAX_TENSORS];
+    float *out[WM_FUSED_MAX_TENSORS];
+    uint32_t unit_end[WM_FUSED_MAX_TENSORS];  // cumulative units per tensor
+    int n_tensors;
+    uint32_t n_chunks;
+    const int *act;
+    const wm_act_meta *meta;
+    const float *rope_cos, *rope_sin;  // [pos][n_rot/2]
+    uint32_t pos, n_rot, rope_mask;
+    int32_t *dot_out;  // PLAIN: the i32 dots of tensor 0 (nullable)
+    uint32_t *absmax;  // ROPE: absmax of the outputs of tensors 1, 2 (float bits, nullable)
+};
+
+template <int MODE, int UG, int W>
+__global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
+    extern __shared__ __align__(16) int smem[];  // act [n_chunks*16] | red [W][UG][64] | ys [UG*64]
+    const uint32_t u = blockIdx.x;
+    int t = 0;
+#pragma unroll
+    for (int i = 1; i < WM_FUSED_MAX_TENSORS; i++)
+        if (i < a.n_tensors && u >= a.unit_end[i - 1]) t = i;
+    const uint32_t lu = u - (t ? a.unit_end[t - 1] : 0u);  // unit within its tensor
+    const uint32_t wid = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t n_chunks = a.n_chunks;
+    const uint32_t c0 = n_chunks * wid / W, c1 = n_chunks * (wid + 1) / W, nc = c1 - c0;
+    const uint64_t gstride = (uint64_t)n_chunks * I2S_GROUP_ROWS;  // uint4 per group
+    const uint4 *wp[UG];
+#pragma unroll
+    for (int q = 0; q < UG; q++) {
+        const int tq = MODE == WM_FUSED_GATEUP ? q : t;
+        const uint32_t g = MODE == WM_FUSED_GATEUP ? lu : lu * UG + q;
+        wp[q] = reinterpret_cast<const uint4 *>(a.w[tq]) + g * gstride + (uint64_t)c0 * I2S_GROUP_ROWS + lane;
+    }
+    uint4 cur[4][UG];
+#pragma unroll
+    for (int v = 0; v < 4; v++)
+#pragma unroll
+        for (int q = 0; q < UG; q++)
+            cur[v][q] = wm_load_stream(wp[q] + min((uint32_t)v, nc - 1) * I2S_GROUP_ROWS);
+    int *act_s = smem;
+    const int4 *ag = reinterpret_cast<const int4 *>(a.act) + (uint64_t)c0 * 4;
+    for (uint32_t i = lane; i < nc * 4; i += 64) reinterpret_cast<int4 *>(act_s + c0 * 16)[i] = ag[i];
+    wm_sync_lds();
+    int acc16[UG], acc4[UG], acc1[UG];
+#pragma unroll
+    for (int q = 0; q < UG; q++) acc16[q] = acc4[q] = acc1[q] = 0;
+    uint32_t c = 0;
+    for (; c + 4 <= nc; c += 4) {
+        uint4 nxt[4][UG];
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+#pragma unroll
+            for (int q = 0; q < UG; q++)
+                nxt[v][q] = wm_load_stream(wp[q] + min(c + 4 + (uint32_t)v, nc - 1) * I2S_GROUP_ROWS);
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int *av = act_s + (c0 + c + v) * 16;
+#pragma unroll
+            for (int q = 0; q < UG; q++) dot_chunk(cur[v][q], av, acc16[q], acc4[q], acc1[q]);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+#pragma unroll
+            for (int q = 0; q < UG; q++) cur[v][q] = nxt[v][q];
+    }
+#pragma unroll
+    for (int v = 0; v < 3; v++)
+        if (c + v < nc)
+#pragma unroll
+            for (int q = 0; q < UG; q++)
+                dot_chunk(cur[v][q], act_s + (c0 + c + v) * 16, acc16[q], acc4[q], acc1[q]);
+    int *red = smem + n_chunks * 16;
+#pragma unroll
+    for (int q = 0; q < UG; q++)
+        red[(wid * UG + q) * 64 + lane] = (acc16[q] >> 4) + (acc4[q] >> 2) + acc1[q];
+    wm_sync_lds();
+    const float act_scale = a.meta->scale;
+    const int asum = a.meta->asum;
+    const uint32_t tid = threadIdx.x;
+    if (MODE == WM_FUSED_GATEUP) {
+        if (tid < 64) {
+            int dg = -asum, du = -asum;
+#pragma unroll
+            for (int w = 0; w < W; w++) {
+                dg += red[(w * UG + 0) * 64 + tid];
+                du += red[(w * UG + 1) * 64 + tid];
+            }
+            const float g = (a.w_scale[0] * act_scale) * (float)dg;
+            const float up = (a.w_scale[1] * act_scale) * (float)du;
+            const float r = g > 0.0f ? g : 0.0f;
+            a.out[0][lu * 64 + tid] = (r * r) * up;
+        }
+        return;
+    }
+    float *out = a.out[t] + (uint64_t)lu * UG * 64;
+    float *ys = reinterpret_cast<float *>(red + W * UG * 64);
+    for (uint32_t row = tid; row < UG * 64; row += W * 64) {
+        const uint32_t q = row >> 6, rr = row & 63;
+        int dot = -asum;
+#pragma unroll
+        for (int w = 0; w < W; w++) dot += red[(w * UG + q) * 64 + rr];
+        const float y = (a.w_scale[t] * act_scale) * (float)dot;
+        if (MODE == WM_FUSED_PLAIN) {
+            out[row] = y;
+            if (a.dot_out && t == 0) a.dot_out[(uint64_t)lu * UG * 64 + row] = dot;
+        } else {
+            ys[row] = y;
+        }
+    }
+    if (MODE == WM_FUSED_PLAIN) return;
+    // WM_FUSED_ROPE: pairs (j, j + n_rot/2) of this head
+    wm_sync_lds();
+    const uint32_t half = a.n_rot / 2;
+    float mx = 0.0f;  // |output| maximum, NaN never raising it
+    if ((a.rope_mask >> t) & 1u) {
+        const float *cs = a.rope_cos + (uint64_t)a.pos * half, *sn = a.rope_sin + (uint64_t)a.pos * half;
+        for (uint32_t j = tid; j < half; j += W * 64) {
+            const float cc = cs[j], ss = sn[j];
+            const float x0 = ys[j], x1 = ys[j + half];
+            const float r0 = x0 * cc - x1 * ss, r1 = x0 * ss + x1 * cc;
+            out[j] = r0;
+            out[j + half] = r1;
+            mx = wm_max_nonan(wm_max_nonan(mx, fabsf(r0)), fabsf(r1));
+        }
+        for (uint32_t j = a.n_rot + tid; j < UG * 64; j += W * 64) {
+            out[j] = ys[j];
+            mx = wm_max_nonan(mx, fabsf(ys[j]));
+        }
+    } else {
+        for (uint32_t j = tid; j < UG * 64; j += W * 64) {
+            out[j] = ys[j];
+            mx = wm_max_nonan(mx, fabsf(ys[j]));
+        }
+    }
+    // KVCache::append needs each of K and V's absmax over all heads: the
+    // units publish theirs with an integer max of the float bits (non-negative
+    // floats order as their bits; the slots are cleared before the launch)
+    if (t >= 1 && a.absmax) {
+        mx = wm_wave_max_nonneg(mx);
+        if (lane == 0) atomicMax(a.absmax + (t - 1), __float_as_uint(mx));
+    }
 }
 
 __global__ void k_i2s_finalize(const int32_t *__restrict__ partial, uint32_t split,
@@ -291,4 +454,60 @@ void wm_launch_i2s_finalize(const int32_t *partial, uint32_t split, uint32_t row
                             const wm_act_meta *meta, float *y, int32_t *dot_out, hipStream_t s) {
     hipLaunchKernelGGL(k_i2s_finalize, dim3((out_dim + 255) / 256), dim3(256), 0, s, partial,
                        split, rows_total, row0, out_dim, w_scale, meta, y, dot_out);
+}
+
+// The fused matvec over the units of `n_tensors` tensors (see k_i2s_fused).
+// Waves per workgroup: n_chunks / 4 (one 4-chunk round each), at most 16.
+void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scales, float *const *outs,
+                         int n_tensors, uint32_t n_chunks, uint32_t groups_per_unit,
+                         const uint8_t *act, const wm_act_meta *meta, const float *rope_cos,
+                         const float *rope_sin, uint32_t pos, uint32_t n_rot, uint32_t rope_mask,
+                         int32_t *dot_out, uint32_t *absmax, hipStream_t s) {
+    i2s_fused_args a{};
+    uint32_t acc = 0;
+    a.n_tensors = n_tensors;
+    for (int i = 0; i < n_tensors; i++) {
+        a.w[i] = descs[i].w;
+        a.w_scale[i] = w_scales[i];
+        a.out[i] = outs[i];
+        // units: PLAIN one per group, ROPE one per head (UG groups), GATEUP one
+        // per group pair (counted on the gate tensor only)
+        const uint32_t units = mode == WM_FUSED_GATEUP ? (i == 0 ? descs[0].n_groups : 0)
+                                                       : descs[i].n_groups / groups_per_unit;
+        acc += units;
+        a.unit_end[i] = acc;
+    }
+    if (mode == WM_FUSED_GATEUP) a.n_tensors = 1;  // units all belong to the pair
+    a.n_chunks = n_chunks;
+    a.act = reinterpret_cast<const int *>(act);
+    a.meta = meta;
+    a.rope_cos = rope_cos;
+    a.rope_sin = rope_sin;
+    a.pos = pos;
+    a.n_rot = n_rot;
+    a.rope_mask = rope_mask;
+    a.dot_out = dot_out;
+    a.absmax = absmax;
+    int w = (int)(n_chunks / 4);
+    w = w < 1 ? 1 : (w > 16 ? 16 : w);
+#define WM_FUSED_CASE(MODE, UG, W)                                                                 \
+    if (w == W) {                                                                                  \
+        const size_t lds = (size_t)n_chunks * 64 + (size_t)W * UG * 64 * 4 + (size_t)UG * 64 * 4;  \
+        hipLaunchKernelGGL((k_i2s_fused<MODE, UG, W>), dim3(acc), dim3(W * 64), lds, s, a);        \
+        return;                                                                                    \
+    }
+#define WM_FUSED_WS(MODE, UG)                                                                      \
+    WM_FUSED_CASE(MODE, UG, 1) WM_FUSED_CASE(MODE, UG, 2) WM_FUSED_CASE(MODE, UG, 4)               \
+    WM_FUSED_CASE(MODE, UG, 6) WM_FUSED_CASE(MODE, UG, 8) WM_FUSED_CASE(MODE, UG, 10)              \
+    WM_FUSED_CASE(MODE, UG, 12) WM_FUSED_CASE(MODE, UG, 16)
+    // round the wave count down to an instantiated one
+    static const int kWs[] = {16, 12, 10, 8, 6, 4, 2, 1};
+    for (int x : kWs)
+        if (w >= x) { w = x; break; }
+    if (mode == WM_FUSED_PLAIN) { WM_FUSED_WS(WM_FUSED_PLAIN, 1) }
+    else if (mode == WM_FUSED_GATEUP) { WM_FUSED_WS(WM_FUSED_GATEUP, 2) }
+    else if (groups_per_unit == 2) { WM_FUSED_WS(WM_FUSED_ROPE, 2) }
+    else { WM_FUSED_WS(WM_FUSED_ROPE, 1) }
+#undef WM_FUSED_WS
+#undef WM_FUSED_CASE
 }

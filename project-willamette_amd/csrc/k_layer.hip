@@ -1,12 +1,12 @@
-// Per-layer kernels of the BitNet b1.58 decode step (gfx950).
+// Per-layer kernels of the BitNet b1.58 decode step (gfx950): the RMSNorms
+// (with the residual add and the int8 quantiser fused in) and the KV prefill.
+// RoPE and relu²·up run in the matvec epilogues (k_i2s.hip), attention in
+// k_attn.hip.
 //
 // Reference: src/model/cached_forward.rs:308-502 (forward_one_layer,
-// scaled_dot_product_attention_into, apply_ffn_block), with
+// apply_ffn_block), with
 //   rms_norm_f32      src/model/primitives.rs:227-255
-//   RoPE (NEOX)       src/model/primitives.rs:285-345
-//   softmax_inplace   src/model/attention.rs:45-73
 //   KV quantisation   src/model/kv_cache.rs:245-259, dequant :192-219
-//   relu_square, mul  src/model/ffn.rs:37-65
 //
 // The reference evaluates every f32 reduction left to right in one
 // accumulator.  Reproducing its results bit for bit requires the same
@@ -45,8 +45,10 @@ template <int PER, int NT>  // NT threads, values per thread: n <= PER * NT
 __global__ __launch_bounds__(NT) void k_rmsnorm_quant(
     float *__restrict__ x, residual_src res, const float *__restrict__ w, uint32_t n, float eps,
     uint8_t *__restrict__ act, wm_act_meta *__restrict__ meta_out, float *__restrict__ y_out,
-    uint32_t *__restrict__ err_flag, uint32_t layer_tag, uint8_t *__restrict__ q6k_prep) {
+    uint32_t *__restrict__ err_flag, uint32_t layer_tag, uint8_t *__restrict__ q6k_prep,
+    uint32_t *__restrict__ clear2) {
     constexpr int NW = NT / 64;
+    if (clear2 && threadIdx.x < 2) clear2[threadIdx.x] = 0;  // slots the next kernel accumulates into
     extern __shared__ __align__(16) float sq[];  // x[j]*x[j], n entries
     __shared__ float red_f[NW];
     __shared__ int red_i[NW], red_nf[NW];
@@ -99,7 +101,7 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant(
         else xv[i] = 0.0f;
     }
     if (err_flag && lane == 0) red_nf[wid] = __builtin_amdgcn_ballot_w64(nonfinite != 0) != 0;
-    __syncthreads();
+    wm_sync_lds();
     // sum_sq over x in order (primitives.rs:243-246), exactly, by the workgroup
     float v2[PER];
     {
@@ -140,7 +142,7 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant(
     // per-vector absmax int8 (src/model/bitlinear_sse2.rs:285-304)
     mx = wm_wave_max_nonneg(mx);
     if (lane == 0) red_f[wid] = mx;
-    __syncthreads();
+    wm_sync_lds();
     float max_abs = red_f[0];
 #pragma unroll
     for (int i = 1; i < NW; i++) max_abs = wm_max_nonan(max_abs, red_f[i]);
@@ -157,7 +159,7 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant(
     }
     sum = wm_wave_total_i32(sum);
     if (lane == 0) red_i[wid] = sum;
-    __syncthreads();
+    wm_sync_lds();
     if (tid == 0) {
         int t = 0;
 #pragma unroll
@@ -165,104 +167,6 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant(
         meta_out->scale = max_abs == 0.0f ? 1.0f : max_abs / 127.0f;
         meta_out->asum = t;
     }
-}
-
-struct qkv_args {
-    const int32_t *partial;
-    uint32_t split, rows_total;
-    uint32_t q_row0, k_row0, v_row0;
-    uint32_t n_q, n_kv;  // n_embd, kv_dim
-    float q_scale, k_scale, v_scale;
-    const wm_act_meta *meta;
-    const float *rope_cos, *rope_sin;  // [pos][n_rot/2]
-    uint32_t head_dim, n_rot, pos;
-    float *q_out;
-    int8_t *k_cache, *v_cache;  // this layer, this position
-    float *k_scale_out, *v_scale_out;
-};
-
-// QKV epilogue (one workgroup): finalise the three BitLinear outputs, apply
-// NEOX RoPE to Q and K at `pos`, write Q (f32) and append the quantised K,V
-// to the cache.
-__global__ __launch_bounds__(1024) void k_qkv_rope_kv(qkv_args a) {
-    extern __shared__ float sm[];
-    float *qs = sm, *ks = sm + a.n_q, *vs = ks + a.n_kv;
-    __shared__ float red[16];
-    const float in_scale = a.meta->scale;
-    const int asum = a.meta->asum;
-    const uint32_t total = a.n_q + 2 * a.n_kv;
-    constexpr int PER = 4;
-    for (uint32_t base = 0; base < total; base += PER * 1024) {
-        uint32_t row[PER];
-        float ws[PER];
-        int dot[PER];
-#pragma unroll
-        for (int k = 0; k < PER; k++) {
-            const uint32_t i = min(base + threadIdx.x + (uint32_t)k * 1024, total - 1);
-            if (i < a.n_q) { row[k] = a.q_row0 + i; ws[k] = a.q_scale; }
-            else if (i < a.n_q + a.n_kv) { row[k] = a.k_row0 + (i - a.n_q); ws[k] = a.k_scale; }
-            else { row[k] = a.v_row0 + (i - a.n_q - a.n_kv); ws[k] = a.v_scale; }
-            dot[k] = -asum;
-        }
-        // all partial loads unconditional, so they are in flight together
-#pragma unroll
-        for (int s = 0; s < kMaxSplit; s++) {
-            const uint32_t sc = min((uint32_t)s, a.split - 1);
-#pragma unroll
-            for (int k = 0; k < PER; k++) {
-                const int v = a.partial[(uint64_t)sc * a.rows_total + row[k]];
-                dot[k] += (uint32_t)s < a.split ? v : 0;
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < PER; k++) {
-            const uint32_t i = base + threadIdx.x + (uint32_t)k * 1024;
-            if (i < total) sm[i] = (ws[k] * in_scale) * (float)dot[k];
-        }
-    }
-    __syncthreads();
-    // RoPE pairs (j, j + n_rot/2) in every head of Q and K
-    const uint32_t half = a.n_rot / 2;
-    const float *cs = a.rope_cos + (uint64_t)a.pos * half, *sn = a.rope_sin + (uint64_t)a.pos * half;
-    const uint32_t n_pairs_q = (a.n_q / a.head_dim) * half, n_pairs_k = (a.n_kv / a.head_dim) * half;
-    for (uint32_t p = threadIdx.x; p < n_pairs_q + n_pairs_k; p += blockDim.x) {
-        float *base = p < n_pairs_q ? qs : ks;
-        uint32_t pp = p < n_pairs_q ? p : p - n_pairs_q;
-        uint32_t h = pp / half, j = pp % half;
-        float *xh = base + h * a.head_dim;
-        float c = cs[j], s = sn[j];
-        float x0 = xh[j], x1 = xh[j + half];
-        xh[j] = x0 * c - x1 * s;
-        xh[j + half] = x0 * s + x1 * c;
-    }
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < a.n_q; i += blockDim.x) a.q_out[i] = qs[i];
-    wm_kv_quantise_store(ks, a.n_kv, a.k_cache, a.k_scale_out, red);
-    __syncthreads();
-    wm_kv_quantise_store(vs, a.n_kv, a.v_cache, a.v_scale_out, red);
-}
-
-// relu(g)^2 * u over the gate/up BitLinear outputs (ffn.rs:37-65).
-__global__ void k_gateup_relu2(const int32_t *__restrict__ partial, uint32_t split,
-                               uint32_t rows_total, uint32_t gate_row0, uint32_t up_row0,
-                               uint32_t n_ff, float gate_scale, float up_scale,
-                               const wm_act_meta *__restrict__ meta, float *__restrict__ h) {
-    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= n_ff) return;
-    const int asum = meta->asum;
-    int dg = -asum, du = -asum;
-#pragma unroll
-    for (int s = 0; s < kMaxSplit; s++) {
-        const uint32_t sc = min((uint32_t)s, split - 1);
-        const int g = partial[(uint64_t)sc * rows_total + gate_row0 + j];
-        const int u = partial[(uint64_t)sc * rows_total + up_row0 + j];
-        dg += (uint32_t)s < split ? g : 0;
-        du += (uint32_t)s < split ? u : 0;
-    }
-    const float g = (gate_scale * meta->scale) * (float)dg;
-    const float u = (up_scale * meta->scale) * (float)du;
-    const float r = g > 0.0f ? g : 0.0f;
-    h[j] = (r * r) * u;
 }
 
 // KVCache::append for n_pos positions x n_layers (prefill from host f32).
@@ -278,7 +182,7 @@ __global__ __launch_bounds__(256) void k_kv_append(const float *__restrict__ k,
     const uint64_t src = ((uint64_t)p * n_layers + l) * kv_dim;
     const uint64_t dst = ((uint64_t)l * max_seq + pos0 + p);
     wm_kv_quantise_store(k + src, kv_dim, k_cache + dst * kv_dim, k_scales + dst, red);
-    __syncthreads();
+    wm_sync_lds();
     wm_kv_quantise_store(v + src, kv_dim, v_cache + dst * kv_dim, v_scales + dst, red);
 }
 
@@ -323,7 +227,7 @@ void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, u
                              uint32_t row0, float w_scale, const wm_act_meta *meta_in,
                              const float *w, uint32_t n, float eps, uint8_t *act,
                              wm_act_meta *meta_out, float *y_out, uint32_t *err_flag,
-                             uint32_t layer_tag, void *q6k_prep, hipStream_t s) {
+                             uint32_t layer_tag, void *q6k_prep, uint32_t *clear2, hipStream_t s) {
     residual_src res{partial, split, rows_total, row0, w_scale, meta_in};
     size_t lds = (size_t)wm::seq_sum_padded(n) * sizeof(float);
     const int per = (int)((n + kNormThreads - 1) / kNormThreads);
@@ -331,7 +235,8 @@ void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, u
     case P:                                                                                        \
         hipLaunchKernelGGL((k_rmsnorm_quant<P, kNormThreads>), dim3(1), dim3(kNormThreads), lds, s, \
                            x, res, w, n,                                                           \
-                           eps, act, meta_out, y_out, err_flag, layer_tag, (uint8_t *)q6k_prep);  \
+                           eps, act, meta_out, y_out, err_flag, layer_tag, (uint8_t *)q6k_prep,   \
+                           clear2);                                                                \
         break;
     switch (per) {
         WM_NORM_CASE(1) WM_NORM_CASE(2) WM_NORM_CASE(3) WM_NORM_CASE(4)
@@ -341,27 +246,6 @@ void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, u
         default: break;
     }
 #undef WM_NORM_CASE
-}
-
-void wm_launch_qkv_rope_kv(const int32_t *partial, uint32_t split, uint32_t rows_total,
-                           uint32_t q_row0, uint32_t k_row0, uint32_t v_row0, uint32_t n_q,
-                           uint32_t n_kv, float q_scale, float k_scale, float v_scale,
-                           const wm_act_meta *meta, const float *rope_cos, const float *rope_sin,
-                           uint32_t head_dim, uint32_t n_rot, uint32_t pos, float *q_out,
-                           int8_t *k_cache, int8_t *v_cache, float *k_scale_out,
-                           float *v_scale_out, hipStream_t s) {
-    qkv_args a{partial, split, rows_total, q_row0, k_row0, v_row0, n_q, n_kv, q_scale, k_scale,
-               v_scale, meta, rope_cos, rope_sin, head_dim, n_rot, pos, q_out, k_cache, v_cache,
-               k_scale_out, v_scale_out};
-    size_t lds = (size_t)(n_q + 2 * n_kv) * sizeof(float);
-    hipLaunchKernelGGL(k_qkv_rope_kv, dim3(1), dim3(1024), lds, s, a);
-}
-
-void wm_launch_gateup_relu2(const int32_t *partial, uint32_t split, uint32_t rows_total,
-                            uint32_t gate_row0, uint32_t up_row0, uint32_t n_ff, float gate_scale,
-                            float up_scale, const wm_act_meta *meta, float *h, hipStream_t s) {
-    hipLaunchKernelGGL(k_gateup_relu2, dim3((n_ff + 255) / 256), dim3(256), 0, s, partial, split,
-                       rows_total, gate_row0, up_row0, n_ff, gate_scale, up_scale, meta, h);
 }
 
 void wm_launch_kv_append(const float *k, const float *v, uint32_t kv_dim, uint32_t n_layers,

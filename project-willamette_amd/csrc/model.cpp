@@ -25,21 +25,12 @@ void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, u
                              uint32_t row0, float w_scale, const wm_act_meta *meta_in,
                              const float *w, uint32_t n, float eps, uint8_t *act,
                              wm_act_meta *meta_out, float *y_out, uint32_t *err_flag,
-                             uint32_t layer_tag, void *q6k_prep, hipStream_t s);
-void wm_launch_qkv_rope_kv(const int32_t *partial, uint32_t split, uint32_t rows_total,
-                           uint32_t q_row0, uint32_t k_row0, uint32_t v_row0, uint32_t n_q,
-                           uint32_t n_kv, float q_scale, float k_scale, float v_scale,
-                           const wm_act_meta *meta, const float *rope_cos, const float *rope_sin,
-                           uint32_t head_dim, uint32_t n_rot, uint32_t pos, float *q_out,
-                           int8_t *k_cache, int8_t *v_cache, float *k_scale_out,
-                           float *v_scale_out, hipStream_t s);
+                             uint32_t layer_tag, void *q6k_prep, uint32_t *clear2, hipStream_t s);
 void wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_scales,
                          const int8_t *v_cache, const float *v_scales, float *scores,
                          uint32_t score_stride, float *out, uint32_t n_heads, uint32_t n_kv_heads,
-                         uint32_t head_dim, uint32_t n_past, float scale, hipStream_t s);
-void wm_launch_gateup_relu2(const int32_t *partial, uint32_t split, uint32_t rows_total,
-                            uint32_t gate_row0, uint32_t up_row0, uint32_t n_ff, float gate_scale,
-                            float up_scale, const wm_act_meta *meta, float *h, hipStream_t s);
+                         uint32_t head_dim, uint32_t n_past, float scale, const float *k_new,
+                         const float *v_new, const uint32_t *kv_absmax, hipStream_t s);
 void wm_launch_kv_append(const float *k, const float *v, uint32_t kv_dim, uint32_t n_layers,
                          uint32_t pos0, uint32_t n_pos, uint32_t max_seq, int8_t *k_cache,
                          float *k_scales, int8_t *v_cache, float *v_scales, hipStream_t s);
@@ -77,14 +68,15 @@ struct wm_model {
     // workspace
     uint8_t *ws = nullptr;
     float *hidden = nullptr, *q = nullptr, *attn_out = nullptr, *h_ff = nullptr, *final_hidden = nullptr;
+    float *k_new = nullptr, *v_new = nullptr;  // this token's K (after RoPE) and V
     float *logits = nullptr, *scores = nullptr;
     uint8_t *act = nullptr;
     wm_act_meta *meta = nullptr;  // [4]: attn, sub, ffn, ffn_sub
     int32_t *partial = nullptr;
-    uint32_t *dscalars = nullptr;  // [0] token, [1] next token, [2] error flag
+    uint32_t *dscalars = nullptr;  // [0] token, [1] next token, [2] error flag, [4..5] K/V absmax
     void *lm_work = nullptr;
     // split choices
-    uint32_t split_qkv = 1, split_o = 1, split_gu = 1, split_down = 1;
+    uint32_t split_o = 1, split_down = 1;
     // ragged-batch workspace, grown on demand to b_cap tokens
     uint8_t *bws = nullptr;
     uint32_t b_cap = 0;
@@ -156,50 +148,54 @@ void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
     const uint32_t n_chunks_e = E / I2S_CHUNK_COLS, n_chunks_f = F / I2S_CHUNK_COLS;
     wm_launch_q6k_dequant_row_dev(m->embd, m->embd_blocks, m->dscalars, m->hidden, s);
     const float scale = 1.0f / sqrtf((float)c.head_dim);  // primitives.rs:354
+    // absmax of this token's K and V (float bits): cleared by attn_norm,
+    // raised by the QKV matvec, read by attention
+    uint32_t *kv_absmax = m->dscalars + 4;
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const dev_layer &L = m->layers[l];
         // residual of the previous layer's ffn_down, folded into attn_norm
         if (l == 0) {
             wm_launch_rmsnorm_quant(m->hidden, nullptr, 0, 0, 0, 0.0f, nullptr, L.attn_norm, E,
-                                    c.rms_eps, m->act, &m->meta[0], nullptr, nullptr, 0, nullptr, s);
+                                    c.rms_eps, m->act, &m->meta[0], nullptr, nullptr, 0, nullptr,
+                                    kv_absmax, s);
         } else {
             const dev_layer &P = m->layers[l - 1];
             wm_launch_rmsnorm_quant(m->hidden, m->partial, m->split_down, P.down.n_groups * 64, 0,
                                     P.down.scale, &m->meta[3], L.attn_norm, E, c.rms_eps, m->act,
-                                    &m->meta[0], nullptr, m->dscalars + 2, l, nullptr, s);
+                                    &m->meta[0], nullptr, m->dscalars + 2, l, nullptr, kv_absmax, s);
             if (layer_trace_dev)
                 hipMemcpyAsync(layer_trace_dev + (size_t)(l - 1) * E, m->hidden, (size_t)E * 4,
                                hipMemcpyDeviceToDevice, s);
         }
-        // Q, K, V: one launch over three tensors sharing the quantised input
+        // Q, K, V: one launch over the three tensors sharing the quantised
+        // input, whole heads per workgroup, NEOX RoPE on Q and K at `pos`
         wm_i2s_desc qkv[3] = {{L.q.w, L.q.n_groups}, {L.k.w, L.k.n_groups}, {L.v.w, L.v.n_groups}};
-        const uint32_t rows_qkv = (L.q.n_groups + L.k.n_groups + L.v.n_groups) * 64;
-        wm_launch_i2s_partial(qkv, 3, n_chunks_e, m->act, m->partial, m->split_qkv, rows_qkv, s);
-        const size_t kv_off = ((size_t)l * kv->max_seq + pos);
-        wm_launch_qkv_rope_kv(m->partial, m->split_qkv, rows_qkv, 0, L.q.n_groups * 64,
-                              (L.q.n_groups + L.k.n_groups) * 64, E, KV, L.q.scale, L.k.scale,
-                              L.v.scale, &m->meta[0], m->rope_cos, m->rope_sin, c.head_dim, c.n_rot,
-                              pos, m->q, kv->k + kv_off * KV, kv->v + kv_off * KV, kv->ks + kv_off,
-                              kv->vs + kv_off, s);
+        const float qkv_scales[3] = {L.q.scale, L.k.scale, L.v.scale};
+        float *qkv_out[3] = {m->q, m->k_new, m->v_new};
+        wm_launch_i2s_fused(WM_FUSED_ROPE, qkv, qkv_scales, qkv_out, 3, n_chunks_e, c.head_dim / 64,
+                            m->act, &m->meta[0], m->rope_cos, m->rope_sin, pos, c.n_rot, 0x3u,
+                            nullptr, kv_absmax, s);
+        // attention; this token's K/V row goes into the cache on the way
         const size_t lay = (size_t)l * kv->max_seq;
         wm_launch_attention(m->q, kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV, kv->vs + lay,
                             m->scores, c.context_length, m->attn_out, c.n_heads, c.n_kv_heads,
-                            c.head_dim, pos + 1, scale, s);
+                            c.head_dim, pos + 1, scale, m->k_new, m->v_new, kv_absmax, s);
         wm_launch_rmsnorm_quant(m->attn_out, nullptr, 0, 0, 0, 0.0f, nullptr, L.attn_sub_norm, E,
-                                c.rms_eps, m->act, &m->meta[1], nullptr, nullptr, 0, nullptr, s);
+                                c.rms_eps, m->act, &m->meta[1], nullptr, nullptr, 0, nullptr, nullptr, s);
         wm_i2s_desc od = {L.o.w, L.o.n_groups};
         wm_launch_i2s_partial(&od, 1, n_chunks_e, m->act, m->partial, m->split_o, L.o.n_groups * 64, s);
         // hidden += wo_out, then ffn_norm
         wm_launch_rmsnorm_quant(m->hidden, m->partial, m->split_o, L.o.n_groups * 64, 0, L.o.scale,
                                 &m->meta[1], L.ffn_norm, E, c.rms_eps, m->act, &m->meta[2], nullptr,
-                                nullptr, 0, nullptr, s);
+                                nullptr, 0, nullptr, nullptr, s);
+        // gate and up row groups together, h = relu(gate)^2 * up in the epilogue
         wm_i2s_desc gu[2] = {{L.gate.w, L.gate.n_groups}, {L.up.w, L.up.n_groups}};
-        const uint32_t rows_gu = (L.gate.n_groups + L.up.n_groups) * 64;
-        wm_launch_i2s_partial(gu, 2, n_chunks_e, m->act, m->partial, m->split_gu, rows_gu, s);
-        wm_launch_gateup_relu2(m->partial, m->split_gu, rows_gu, 0, L.gate.n_groups * 64, F,
-                               L.gate.scale, L.up.scale, &m->meta[2], m->h_ff, s);
+        const float gu_scales[2] = {L.gate.scale, L.up.scale};
+        float *gu_out[2] = {m->h_ff, nullptr};
+        wm_launch_i2s_fused(WM_FUSED_GATEUP, gu, gu_scales, gu_out, 2, n_chunks_e, 1, m->act,
+                            &m->meta[2], nullptr, nullptr, 0, 0, 0, nullptr, nullptr, s);
         wm_launch_rmsnorm_quant(m->h_ff, nullptr, 0, 0, 0, 0.0f, nullptr, L.ffn_sub_norm, F,
-                                c.rms_eps, m->act, &m->meta[3], nullptr, nullptr, 0, nullptr, s);
+                                c.rms_eps, m->act, &m->meta[3], nullptr, nullptr, 0, nullptr, nullptr, s);
         wm_i2s_desc dd = {L.down.w, L.down.n_groups};
         wm_launch_i2s_partial(&dd, 1, n_chunks_f, m->act, m->partial, m->split_down,
                               L.down.n_groups * 64, s);
@@ -209,7 +205,7 @@ void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
     wm_launch_rmsnorm_quant(m->hidden, m->partial, m->split_down, P.down.n_groups * 64, 0,
                             P.down.scale, &m->meta[3], m->output_norm, E, c.rms_eps, nullptr,
                             nullptr, m->final_hidden, m->dscalars + 2, c.n_layers,
-                            wm_q6k_prep_area(m->lm_work, c.vocab_size, m->embd_blocks), s);
+                            wm_q6k_prep_area(m->lm_work, c.vocab_size, m->embd_blocks), nullptr, s);
     if (layer_trace_dev)
         hipMemcpyAsync(layer_trace_dev + (size_t)(c.n_layers - 1) * E, m->hidden, (size_t)E * 4,
                        hipMemcpyDeviceToDevice, s);
@@ -446,7 +442,7 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
     if (c.n_heads % c.n_kv_heads)
         return wm_set_error(ctx, WM_E_SHAPE, "gqa_group_size: n_heads (%u) not divisible by n_kv_heads (%u)",
                             c.n_heads, c.n_kv_heads);
-    if (c.n_heads * c.head_dim != c.n_embd || c.head_dim % 64 || c.head_dim > 1024)
+    if (c.n_heads * c.head_dim != c.n_embd || (c.head_dim != 64 && c.head_dim != 128))
         return wm_set_error(ctx, WM_E_SHAPE, "model config: head_dim %u unsupported", c.head_dim);
     if (c.n_rot == 0 || c.n_rot % 2 || c.n_rot > c.head_dim)
         return wm_set_error(ctx, WM_E_SHAPE, "apply_rope_f32: n_rot=%u must be even and <= head_dim",
@@ -479,15 +475,11 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
         }
     }
     const uint32_t E = c.n_embd, F = c.n_ff;
-    const uint32_t eg = (E + 63) / 64, fg = (F + 63) / 64, kvg = (m->kv_dim + 63) / 64;
-    m->split_qkv = wm_i2s_pick_split(eg + 2 * kvg, E / 64);
+    const uint32_t eg = (E + 63) / 64;
     m->split_o = wm_i2s_pick_split(eg, E / 64);
-    m->split_gu = wm_i2s_pick_split(2 * fg, E / 64);
     m->split_down = wm_i2s_pick_split(eg, F / 64);
     size_t part = 0;
-    part = std::max(part, (size_t)m->split_qkv * (eg + 2 * kvg) * 64);
     part = std::max(part, (size_t)m->split_o * eg * 64);
-    part = std::max(part, (size_t)m->split_gu * 2 * fg * 64);
     part = std::max(part, (size_t)m->split_down * eg * 64);
     const size_t sizes[] = {
         align256((size_t)E * 4),                                  // hidden
@@ -495,6 +487,7 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
         align256((size_t)E * 4),                                  // attn_out
         align256((size_t)F * 4),                                  // h_ff
         align256((size_t)E * 4),                                  // final_hidden
+        align256((size_t)m->kv_dim * 4), align256((size_t)m->kv_dim * 4),  // k_new, v_new
         align256((size_t)c.vocab_size * 4),                       // logits
         align256((size_t)c.n_heads * c.context_length * 4),       // scores
         align256((size_t)std::max(E, F)),                         // act
@@ -513,7 +506,8 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
     }
     uint8_t *p = m->ws;
     void **slots[] = {(void **)&m->hidden, (void **)&m->q, (void **)&m->attn_out, (void **)&m->h_ff,
-                      (void **)&m->final_hidden, (void **)&m->logits, (void **)&m->scores,
+                      (void **)&m->final_hidden, (void **)&m->k_new, (void **)&m->v_new,
+                      (void **)&m->logits, (void **)&m->scores,
                       (void **)&m->act, (void **)&m->meta, (void **)&m->partial,
                       (void **)&m->dscalars, (void **)&m->lm_work, (void **)&m->rope_cos,
                       (void **)&m->rope_sin};

@@ -221,6 +221,14 @@ __device__ __forceinline__ float wm_wave_max_nonneg(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Workgroup barrier for LDS traffic: waits for this wave's LDS (and scalar)
+// operations, then s_barrier.  Unlike __syncthreads it does not wait for the
+// wave's global loads and stores, so a store issued before it stays in
+// flight; use it only where the waves exchange data through LDS alone.
+__device__ __forceinline__ void wm_sync_lds() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Wave-level helpers (wave64).
 __device__ __forceinline__ int wm_wave_sum_i32(int v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -238,9 +246,9 @@ __device__ __forceinline__ float wm_wave_max_nonan(float v) {
 __device__ __forceinline__ float wm_block_max_nonan(float v, float *red) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     v = wm_wave_max_nonan(v);
-    __syncthreads();
+    wm_sync_lds();
     if (lane == 0) red[wid] = v;
-    __syncthreads();
+    wm_sync_lds();
     float m = red[0];
     for (int w = 1; w < (int)(blockDim.x >> 6); w++) m = wm_max_nonan(m, red[w]);
     return m;
@@ -248,9 +256,9 @@ __device__ __forceinline__ float wm_block_max_nonan(float v, float *red) {
 __device__ __forceinline__ int wm_block_sum_i32(int v, int *red) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     v = wm_wave_sum_i32(v);
-    __syncthreads();
+    wm_sync_lds();
     if (lane == 0) red[wid] = v;
-    __syncthreads();
+    wm_sync_lds();
     int t = 0;
     for (int w = 0; w < (int)(blockDim.x >> 6); w++) t += red[w];
     return t;
@@ -303,12 +311,24 @@ void wm_launch_i2s_repack(const uint8_t *raw, uint8_t *out, uint32_t in_dim, uin
 // Quantise f32 x[n] -> permuted int8 act + meta (one workgroup).
 void wm_launch_quantize_act(const float *x, uint32_t n, uint8_t *act, wm_act_meta *meta,
                             hipStream_t s);
+// Fused matvec modes (k_i2s_fused).
+constexpr int WM_FUSED_MAX_TENSORS = 4;
+enum { WM_FUSED_PLAIN = 0, WM_FUSED_GATEUP = 1, WM_FUSED_ROPE = 2 };
+
 // Partial dots over K splits (one launch covers up to WM_I2S_MAX_MULTI
 // tensors sharing one input): partial[split][row], rows = n_groups*64.
 struct wm_i2s_desc {
     const uint8_t *w;  // library layout
     uint32_t n_groups;
 };
+// Matvec with the K split inside each workgroup and a fused epilogue (mode
+// WM_FUSED_*): rows of tensor i go to outs[i] as f32; see k_i2s_fused.
+// groups_per_unit: 1, or head_dim / 64 for WM_FUSED_ROPE.
+void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scales, float *const *outs,
+                         int n_tensors, uint32_t n_chunks, uint32_t groups_per_unit,
+                         const uint8_t *act, const wm_act_meta *meta, const float *rope_cos,
+                         const float *rope_sin, uint32_t pos, uint32_t n_rot, uint32_t rope_mask,
+                         int32_t *dot_out, uint32_t *absmax, hipStream_t s);
 void wm_launch_i2s_partial(const wm_i2s_desc *descs, int n_desc, uint32_t n_chunks,
                            const uint8_t *act, int32_t *partial, uint32_t split,
                            uint32_t rows_total, hipStream_t s);

@@ -259,7 +259,7 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
     double ex = __shfl_up(inc, 1, 64);
     if (lane == 0) ex = 0.0;
     if (lane == 63) sc->dw[wid] = inc;
-    __syncthreads();
+    wm_sync_lds();
     double off = 0.0;
 #pragma unroll
     for (int w = 0; w < NW; w++) off += w < (int)wid ? sc->dw[w] : 0.0;
@@ -318,7 +318,7 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
         }
     }
     if (lane == 63) sc->wt[wid] = pinc;
-    __syncthreads();
+    wm_sync_lds();
     // 3. the walk over the breaks (wave 0)
     if (wid == 0) {
         const long long wt = (int)lane < NW ? sc->wt[lane] : 0;
@@ -431,7 +431,7 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
         }
         if (lane == 0) sc->out = s;
     }
-    __syncthreads();
+    wm_sync_lds();
     return sc->out;
 }
 
