@@ -107,55 +107,60 @@ __global__ __launch_bounds__(64) void k_attn_scores(attn_args a) {
     a.scores[(uint64_t)h * a.score_stride + p] = s * a.scale;
 }
 
-constexpr int kThreads = 192;   // wave 0: the 16 chains; waves 1-2: products
-constexpr int kDims = 16;       // head dims per workgroup (one 16-byte V segment)
-constexpr int kTile = 64;       // positions per product tile
-constexpr int kPStride = 68;    // floats per dim row of a product tile
+constexpr int kSvThreads = 1024;  // wave 0: the 16 chains; waves 1-15: products
+constexpr int kSvDims = 16;        // head dims per workgroup (one 16-byte V segment)
+constexpr int kSvTile = 240;       // positions per product tile
+constexpr int kSvStride = 244;     // floats per dim row of a product tile (16-byte rows)
+static_assert(kSvTile * (kSvDims / 4) == kSvThreads - 64, "one 4-dim unit per producer thread");
 
 // softmax over scores[h][0..n_past) then out[h][d] = Σ_p w_p * v_p[d] for
 // the 16 dimensions d0..d0+15 of head h.  Grid (n_heads, head_dim / 16).
 //
-// The workgroup first pulls its whole V slice (n_past x 16 int8, 64 KB at
-// 4096 positions), the scores and the V scales into LDS with all loads in
-// flight at once; the softmax denominator is the exact sequential sum; then
-// waves 1-2 write tiles of products w_p * v_p[d] while wave 0 adds the
-// previous tile, one chain per dimension.
-template <int MAXM>  // n_past <= MAXM * kThreads (the exact sum's terms per thread)
-__global__ __launch_bounds__(kThreads) void k_attn_softmax_v(attn_args a) {
+// The workgroup first pulls its whole V slice (n_past x 16 int8: one
+// coalesced 16-byte load per position, 64 KB at 4096 positions), the scores
+// and the V scales into LDS with all loads in flight at once.  All 16 waves
+// then compute the softmax: max, exp, the exact sequential sum
+// (seq_sum_block_owned) and the normalisation.  Then, tile by tile, waves
+// 1-15 write products w_p * v_p[d] (4 dims of one position per thread)
+// while lanes 0-15 of wave 0 add the previous tile, one chain per
+// dimension, in position order.  Position n_past - 1 uses this token's V,
+// quantised from v_new (workgroup (0, 0) also writes the cache row).
+template <int MAXM>  // n_past <= MAXM * kSvThreads (the exact sum's terms per thread)
+__global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
     extern __shared__ __align__(16) float sm[];
-    const uint32_t n = a.n_past;
+    const uint32_t n = a.n_past, pnew = n - 1;
     const uint32_t npad = (n + 3) & ~3u;
-    float *wts = sm;                                        // [seq_sum_padded(n)]
-    float *vsc = wts + wm::seq_sum_padded(n);               // [npad]
-    int4 *vq = reinterpret_cast<int4 *>(vsc + npad);        // [npad] x 16 int8
-    float *prod = reinterpret_cast<float *>(vq + npad);     // [2][kDims][kPStride]
+    float *wts = sm;                                      // [seq_sum_padded(n)]
+    float *vsc = wts + wm::seq_sum_padded(n);             // [npad]
+    int4 *vq = reinterpret_cast<int4 *>(vsc + npad);      // [npad] x 16 int8
+    float *prod = reinterpret_cast<float *>(vq + npad);   // [2][kSvDims][kSvStride]
     __shared__ float red[16];
     __shared__ wm::seq_block_scratch seq_scratch;
-    const uint32_t h = blockIdx.x, d0 = blockIdx.y * kDims, tid = threadIdx.x;
+    __shared__ uint64_t exp_tab[32];
+    const uint32_t h = blockIdx.x, d0 = blockIdx.y * kSvDims, tid = threadIdx.x;
+    const uint32_t wid = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6)), lane = tid & 63;
     const uint32_t kvh = h / a.group;
     const int8_t *vseg = a.v_cache + kvh * a.head_dim + d0;
     const float *sc = a.scores + (uint64_t)h * a.score_stride;
-    __shared__ uint64_t exp_tab[32];
-    if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
-    // this token's V (position n_past - 1 is not in the cache yet)
-    const uint32_t pnew = n - 1;
     const float vabs = __uint_as_float(a.kv_absmax[1]);
-    // 1. the loads, 4 per thread per round with clamped indices so none is
-    //    conditional and all 12 of a round are in flight together
+    const bool v_writer = h == 0 && blockIdx.y == 0;
+    if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
+    // 1. the loads, 4 positions per thread per round, indices clamped so none
+    //    is conditional and all of a round are in flight together
     float m = -INFINITY;
-    for (uint32_t base = 0; base < n; base += 4 * kThreads) {
+    for (uint32_t base = 0; base < n; base += 4 * kSvThreads) {
         int4 vr[4];
         float sv[4], ss[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t p = min(base + tid + (uint32_t)i * kThreads, n - 1);
+            const uint32_t p = min(base + tid + (uint32_t)i * kSvThreads, n - 1);
             vr[i] = *reinterpret_cast<const int4 *>(vseg + (uint64_t)p * a.kv_dim);
             sv[i] = sc[p];
             ss[i] = a.v_scales[p];
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t p = base + tid + (uint32_t)i * kThreads;
+            const uint32_t p = base + tid + (uint32_t)i * kSvThreads;
             if (p < n) {
                 vq[p] = vr[i];
                 wts[p] = sv[i];
@@ -164,93 +169,88 @@ __global__ __launch_bounds__(kThreads) void k_attn_softmax_v(attn_args a) {
             }
         }
     }
-    // 2. softmax (attention.rs:45-73)
-    const float mx = wm_block_max_nonan(m, red);
-    if (tid < kDims)  // the new position's slice, quantised as KVCache::append does
+    // this token's V (position n_past - 1 is not in the cache yet)
+    if (tid < kSvDims)
         reinterpret_cast<int8_t *>(vq + pnew)[tid] = kv_q(a.v_new[kvh * a.head_dim + d0 + tid], vabs);
     if (tid == 0) vsc[pnew] = kv_scale(vabs);
-    if (h == 0 && blockIdx.y == 0) {
-        for (uint32_t i = tid; i < a.kv_dim; i += kThreads) a.v_row[i] = kv_q(a.v_new[i], vabs);
-        if (tid == 0) *a.v_row_scale = kv_scale(vabs);
-    }
+    // 2. softmax (attention.rs:45-73)
+    const float mx = wm_block_max_nonan(m, red);
     float *out = a.out + (uint64_t)h * a.head_dim + d0;
     if (!isfinite(mx)) {  // every weight becomes 0 -> output stays 0
-        if (tid < kDims) out[tid] = 0.0f;
-        return;
-    }
-    // exp(v - max) (attention.rs:62), 4 independent evaluations per round
-    for (uint32_t base = 0; base < n; base += 4 * kThreads) {
-        float e[4];
+        if (tid < kSvDims) out[tid] = 0.0f;
+    } else {
+        // exp(v - max) (attention.rs:62), each thread on its own positions
+        for (uint32_t p = tid; p < n; p += kSvThreads) wts[p] = wm::expf_glibc(wts[p] - mx, exp_tab);
+        wm_sync_lds();
+        // Σ exp left to right (attention.rs:63-66), exactly; thread t takes
+        // the terms t*m .. t*m+m-1
+        float ev[MAXM];
+        {
+            const uint32_t mm = (n + kSvThreads - 1) / kSvThreads, k0 = tid * mm;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t p = min(base + tid + (uint32_t)i * kThreads, n - 1);
-            e[i] = wm::expf_glibc(wts[p] - mx, exp_tab);
+            for (int j = 0; j < MAXM; j++)
+                ev[j] = ((uint32_t)j < mm && k0 + (uint32_t)j < n) ? wts[k0 + j] : 0.0f;
         }
-        wm_sync_lds();  // every read of this round before any write
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t p = base + tid + (uint32_t)i * kThreads;
-            if (p < n) wts[p] = e[i];
-        }
-    }
-    wm_sync_lds();
-    // Σ exp left to right (attention.rs:63-66), exactly, by the workgroup;
-    // thread t takes the terms t*m .. t*m+m-1
-    float ev[MAXM];
-    {
-        const uint32_t m = (n + kThreads - 1) / kThreads, k0 = tid * m;
-#pragma unroll
-        for (int j = 0; j < MAXM; j++)
-            ev[j] = ((uint32_t)j < m && k0 + (uint32_t)j < n) ? wts[k0 + j] : 0.0f;
-    }
-    const float sum = wm::seq_sum_block_owned<MAXM, kThreads>(ev, n, wts, &seq_scratch);
-    if (sum > 0.0f) {
-        const float inv = 1.0f / sum;
-        for (uint32_t p = tid; p < n; p += kThreads) wts[p] = wts[p] * inv;
-    }
-    wm_sync_lds();
-    // 3. products of tile t (waves 1-2) while wave 0 adds tile t - 1
-    const uint32_t n_tiles = (n + kTile - 1) / kTile;
-    const uint32_t pt = tid - 64, pl = pt >> 1, dh = (pt & 1) * 8;
-    float acc = 0.0f;
-    for (uint32_t t = 0; t <= n_tiles; t++) {
-        if (tid >= 64) {
-            if (t < n_tiles) {
-                const uint32_t p = t * kTile + pl;
-                float *dst = prod + (t & 1) * (kDims * kPStride) + dh * kPStride + pl;
-                if (p < n) {
-                    const int4 v4 = vq[p];
-                    // this thread's 8 bytes, selected by register (no byte-indexed stack copy)
-                    const uint32_t lo = dh ? (uint32_t)v4.z : (uint32_t)v4.x;
-                    const uint32_t hi = dh ? (uint32_t)v4.w : (uint32_t)v4.y;
-                    const float w = wts[p], s = vsc[p];
-#pragma unroll
-                    for (int i = 0; i < 8; i++) {
-                        const uint32_t word = i < 4 ? lo : hi;
-                        const float vd = (float)(int8_t)(word >> (8 * (i & 3))) * s;  // read_into: q * scale
-                        dst[i * kPStride] = w * vd;                                    // w * v_h[d]
-                    }
-                }
-            }
-        } else if (tid < kDims && t > 0) {
-            const float *src = prod + ((t - 1) & 1) * (kDims * kPStride) + tid * kPStride;
-            const uint32_t p0 = (t - 1) * kTile;
-            const uint32_t tn = n - p0 < (uint32_t)kTile ? n - p0 : (uint32_t)kTile;
-            if (tn == (uint32_t)kTile) {
-                float4 f[kTile / 4];  // the whole tile row first: one LDS latency, then the chain
-#pragma unroll
-                for (int i = 0; i < kTile / 4; i++) f[i] = *reinterpret_cast<const float4 *>(src + 4 * i);
-#pragma unroll
-                for (int i = 0; i < kTile / 4; i++) {
-                    acc = acc + f[i].x; acc = acc + f[i].y; acc = acc + f[i].z; acc = acc + f[i].w;
-                }
-            } else {
-                for (uint32_t q = 0; q < tn; q++) acc = acc + src[q];
-            }
+        const float sum = wm::seq_sum_block_owned<MAXM, kSvThreads>(ev, n, wts, &seq_scratch);
+        if (sum > 0.0f) {
+            const float inv = 1.0f / sum;
+            for (uint32_t p = tid; p < n; p += kSvThreads) wts[p] = wts[p] * inv;
         }
         wm_sync_lds();
+        // 3. products of tile t (waves 1-15) while wave 0 adds tile t - 1
+        const uint32_t n_tiles = (n + kSvTile - 1) / kSvTile;
+        const uint32_t pt = tid - 64, dq = pt / kSvTile, pl = pt % kSvTile;  // producer unit
+        float acc = 0.0f;
+        for (uint32_t t = 0; t <= n_tiles; t++) {
+            if (wid >= 1) {
+                if (t < n_tiles) {
+                    const uint32_t p = t * kSvTile + pl;
+                    if (p < n) {
+                        float *dst = prod + (t & 1) * (kSvDims * kSvStride) + dq * 4 * kSvStride + pl;
+                        const uint32_t word = reinterpret_cast<const uint32_t *>(vq + p)[dq];
+                        const float w = wts[p], s = vsc[p];
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const float vd = (float)(int8_t)(word >> (8 * i)) * s;  // read_into: q * scale
+                            dst[i * kSvStride] = w * vd;                             // w * v_h[d]
+                        }
+                    }
+                }
+            } else if (lane < kSvDims && t > 0) {
+                const float *src = prod + ((t - 1) & 1) * (kSvDims * kSvStride) + lane * kSvStride;
+                const uint32_t p0 = (t - 1) * kSvTile;
+                const uint32_t tn = n - p0 < (uint32_t)kSvTile ? n - p0 : (uint32_t)kSvTile;
+                if (tn == (uint32_t)kSvTile) {
+                    // 24 products per step, the next step's reads issued before this step's adds
+                    constexpr int kC = 6, kSteps = kSvTile / (4 * kC);
+                    float4 f[2][kC];
+#pragma unroll
+                    for (int i = 0; i < kC; i++) f[0][i] = *reinterpret_cast<const float4 *>(src + 4 * i);
+#pragma unroll
+                    for (int c = 0; c < kSteps; c++) {
+                        if (c + 1 < kSteps) {
+#pragma unroll
+                            for (int i = 0; i < kC; i++)
+                                f[(c + 1) & 1][i] = *reinterpret_cast<const float4 *>(src + (c + 1) * 4 * kC + 4 * i);
+                        }
+#pragma unroll
+                        for (int i = 0; i < kC; i++) {
+                            const float4 g = f[c & 1][i];
+                            acc = acc + g.x; acc = acc + g.y; acc = acc + g.z; acc = acc + g.w;
+                        }
+                    }
+                } else {
+                    for (uint32_t q = 0; q < tn; q++) acc = acc + src[q];
+                }
+            }
+            wm_sync_lds();
+        }
+        if (tid < kSvDims) out[tid] = acc;
     }
-    if (tid < kDims) out[tid] = acc;
+    if (v_writer) {  // the cache row of position n_past - 1
+        for (uint32_t i = tid; i < a.kv_dim; i += kSvThreads) a.v_row[i] = kv_q(a.v_new[i], vabs);
+        if (tid == 0) *a.v_row_scale = kv_scale(vabs);
+    }
 }
 
 }  // namespace
@@ -269,13 +269,10 @@ void wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
     hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, (n_past - 1 + 63) / 64 + 1), dim3(64), 0, s, a);
     const size_t npad = ((size_t)n_past + 3) & ~(size_t)3;
     const size_t lds = (size_t)wm::seq_sum_padded(n_past) * 4 + npad * (4 + 16) +
-                       (size_t)2 * kDims * kPStride * 4;
-    if (n_past > 22 * kThreads) return;  // unreachable: models are limited to 4096 positions
-    const dim3 grid(n_heads, head_dim / kDims);
-    if (n_past <= 8 * kThreads)
-        hipLaunchKernelGGL(k_attn_softmax_v<8>, grid, dim3(kThreads), lds, s, a);
-    else if (n_past <= 16 * kThreads)
-        hipLaunchKernelGGL(k_attn_softmax_v<16>, grid, dim3(kThreads), lds, s, a);
-    else  // n_past <= 4096 (the model's context limit) < 22 * kThreads
-        hipLaunchKernelGGL(k_attn_softmax_v<22>, grid, dim3(kThreads), lds, s, a);
+                       (size_t)2 * kSvDims * kSvStride * 4;
+    const dim3 grid(n_heads, head_dim / kSvDims);
+    if (n_past <= 2 * kSvThreads)
+        hipLaunchKernelGGL(k_attn_softmax_v<2>, grid, dim3(kSvThreads), lds, s, a);
+    else  // n_past <= 4096, the models' context limit
+        hipLaunchKernelGGL(k_attn_softmax_v<4>, grid, dim3(kSvThreads), lds, s, a);
 }
