@@ -41,7 +41,10 @@ struct residual_src {
 // from LDS with each thread owning consecutive terms.  Five barriers in all.
 constexpr int kMaxSplit = 16;  // K splits a residual source may carry
 
-template <int PER, int NT>  // NT threads, values per thread: n <= PER * NT
+// NT threads, values per thread: n <= PER * NT; RES: a residual source is
+// given (res.partial != nullptr).  Only RES kernels hold the partials'
+// registers, so the others keep their register budget.
+template <int PER, int NT, bool RES>
 __global__ __launch_bounds__(NT) void k_rmsnorm_quant(
     float *__restrict__ x, residual_src res, const float *__restrict__ w, uint32_t n, float eps,
     uint8_t *__restrict__ act, wm_act_meta *__restrict__ meta_out, float *__restrict__ y_out,
@@ -56,7 +59,7 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant(
     const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     float xv[PER], wv[PER];
     int nonfinite = 0;
-    const bool has_res = res.partial != nullptr;
+    const bool has_res = RES;
     // Every load below is issued before any is used (indices clamped to
     // n - 1); out-of-range values are masked after.
 #pragma unroll
@@ -71,15 +74,37 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant(
         const int asum = res.meta->asum;
         const int32_t *p = res.partial + res.row0;
         int dot[PER];
+        if constexpr (PER <= 4) {
+            // every split's loads issued before any is used (split indices
+            // clamped, the copies masked after): the partials come from other
+            // XCDs' caches, and one round trip per split would serialise them
+            int pv[kMaxSplit][PER];
 #pragma unroll
-        for (int i = 0; i < PER; i++) dot[i] = -asum;
-#pragma unroll
-        for (int s = 0; s < kMaxSplit; s++) {
-            if ((uint32_t)s < res.split) {
+            for (int s = 0; s < kMaxSplit; s++) {
+                const uint32_t sc = min((uint32_t)s, res.split - 1);
 #pragma unroll
                 for (int i = 0; i < PER; i++) {
                     const uint32_t j = min(tid + (uint32_t)i * NT, n - 1);
-                    dot[i] += p[(uint64_t)s * res.rows_total + j];
+                    pv[s][i] = p[(uint64_t)sc * res.rows_total + j];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < PER; i++) {
+                dot[i] = -asum;
+#pragma unroll
+                for (int s = 0; s < kMaxSplit; s++) dot[i] += (uint32_t)s < res.split ? pv[s][i] : 0;
+            }
+        } else {  // wider vectors: not enough registers to hold every partial
+#pragma unroll
+            for (int i = 0; i < PER; i++) dot[i] = -asum;
+#pragma unroll
+            for (int s = 0; s < kMaxSplit; s++) {
+                const uint32_t sc = min((uint32_t)s, res.split - 1);
+#pragma unroll
+                for (int i = 0; i < PER; i++) {
+                    const uint32_t j = min(tid + (uint32_t)i * NT, n - 1);
+                    const int v = p[(uint64_t)sc * res.rows_total + j];
+                    dot[i] += (uint32_t)s < res.split ? v : 0;
                 }
             }
         }
@@ -231,18 +256,41 @@ void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, u
     residual_src res{partial, split, rows_total, row0, w_scale, meta_in};
     size_t lds = (size_t)wm::seq_sum_padded(n) * sizeof(float);
     const int per = (int)((n + kNormThreads - 1) / kNormThreads);
-#define WM_NORM_CASE(P)                                                                            \
-    case P:                                                                                        \
-        hipLaunchKernelGGL((k_rmsnorm_quant<P, kNormThreads>), dim3(1), dim3(kNormThreads), lds, s, \
-                           x, res, w, n,                                                           \
-                           eps, act, meta_out, y_out, err_flag, layer_tag, (uint8_t *)q6k_prep,   \
-                           clear2);                                                                \
-        break;
+#define WM_NORM_CASE(P, R)                                                                         \
+    hipLaunchKernelGGL((k_rmsnorm_quant<P, kNormThreads, R>), dim3(1), dim3(kNormThreads), lds, s,  \
+                       x, res, w, n, eps, act, meta_out, y_out, err_flag, layer_tag,                \
+                       (uint8_t *)q6k_prep, clear2)
+    if (partial) {
+        switch (per) {  // residual sources: the hidden state, n_embd <= 8192
+            case 1: WM_NORM_CASE(1, true); break;
+            case 2: WM_NORM_CASE(2, true); break;
+            case 3: WM_NORM_CASE(3, true); break;
+            case 4: WM_NORM_CASE(4, true); break;
+            case 5: WM_NORM_CASE(5, true); break;
+            case 6: WM_NORM_CASE(6, true); break;
+            case 7: WM_NORM_CASE(7, true); break;
+            case 8: WM_NORM_CASE(8, true); break;
+            default: break;
+        }
+        return;
+    }
     switch (per) {
-        WM_NORM_CASE(1) WM_NORM_CASE(2) WM_NORM_CASE(3) WM_NORM_CASE(4)
-        WM_NORM_CASE(5) WM_NORM_CASE(6) WM_NORM_CASE(7) WM_NORM_CASE(8)
-        WM_NORM_CASE(9) WM_NORM_CASE(10) WM_NORM_CASE(11) WM_NORM_CASE(12)
-        WM_NORM_CASE(13) WM_NORM_CASE(14) WM_NORM_CASE(15) WM_NORM_CASE(16)
+        case 1: WM_NORM_CASE(1, false); break;
+        case 2: WM_NORM_CASE(2, false); break;
+        case 3: WM_NORM_CASE(3, false); break;
+        case 4: WM_NORM_CASE(4, false); break;
+        case 5: WM_NORM_CASE(5, false); break;
+        case 6: WM_NORM_CASE(6, false); break;
+        case 7: WM_NORM_CASE(7, false); break;
+        case 8: WM_NORM_CASE(8, false); break;
+        case 9: WM_NORM_CASE(9, false); break;
+        case 10: WM_NORM_CASE(10, false); break;
+        case 11: WM_NORM_CASE(11, false); break;
+        case 12: WM_NORM_CASE(12, false); break;
+        case 13: WM_NORM_CASE(13, false); break;
+        case 14: WM_NORM_CASE(14, false); break;
+        case 15: WM_NORM_CASE(15, false); break;
+        case 16: WM_NORM_CASE(16, false); break;
         default: break;
     }
 #undef WM_NORM_CASE
