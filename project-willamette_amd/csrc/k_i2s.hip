@@ -104,6 +104,7 @@ struct i2s_multi {
     uint32_t group_end[WM_I2S_MAX_MULTI];  // cumulative group counts
     int n;
     uint32_t uniform_groups;  // every tensor has this many groups (0: they differ)
+    const uint8_t *const *table;  // or: device array of n tensors of uniform_groups groups each
 };
 
 __device__ __forceinline__ void dot_chunk(const uint4 wv, const int *__restrict__ a,
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(64) void k_i2s_partial(i2s_multi m, uint32_t n_chun
         t = lo;
         g = gg - (t ? m.group_end[t - 1] : 0);
     }
-    const uint4 *__restrict__ W = reinterpret_cast<const uint4 *>(m.w[t]);
+    const uint4 *__restrict__ W = reinterpret_cast<const uint4 *>(m.table ? m.table[t] : m.w[t]);
     const uint32_t split = gridDim.y, s = blockIdx.y;
     const uint32_t c0 = (uint32_t)(((uint64_t)n_chunks * s) / split);
     const uint32_t c1 = (uint32_t)(((uint64_t)n_chunks * (s + 1)) / split);
@@ -447,6 +448,21 @@ void wm_launch_i2s_partial(const wm_i2s_desc *descs, int n_desc, uint32_t n_chun
     // One group per wave: measured faster than two (fewer waves hide less latency).
     hipLaunchKernelGGL(k_i2s_partial<1>, dim3(acc, split), dim3(64), lds, s, m, n_chunks,
                        reinterpret_cast<const int *>(act), partial, rows_total);
+}
+
+// n_tensors tensors of groups_per groups each, their device pointers in the
+// device array `table` (any count: no kernel-argument limit).
+void wm_launch_i2s_partial_table(const uint8_t *const *table, uint32_t n_tensors,
+                                 uint32_t groups_per, uint32_t n_chunks, const uint8_t *act,
+                                 int32_t *partial, uint32_t split, uint32_t rows_total,
+                                 hipStream_t s) {
+    i2s_multi m{};
+    m.n = (int)n_tensors;
+    m.uniform_groups = groups_per;
+    m.table = table;
+    const size_t lds = (size_t)((n_chunks + split - 1) / split) * 64;  // activation slice
+    hipLaunchKernelGGL(k_i2s_partial<1>, dim3(groups_per * n_tensors, split), dim3(64), lds, s, m,
+                       n_chunks, reinterpret_cast<const int *>(act), partial, rows_total);
 }
 
 void wm_launch_i2s_finalize(const int32_t *partial, uint32_t split, uint32_t rows_total,

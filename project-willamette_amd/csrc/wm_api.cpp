@@ -83,6 +83,7 @@ void wm_ctx_destroy(wm_ctx *ctx) {
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
     if (ctx->scratch) hipFree(ctx->scratch);
+    if (ctx->multi_dev) hipFree(ctx->multi_dev);
     if (ctx->pinned) hipHostFree(ctx->pinned);
     hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -360,36 +361,54 @@ wm_status wm_bitlinear_i2s_matvec_f32_multi_dev(wm_ctx *ctx, const wm_tensor *co
     }
     const wm_tensor *w0 = ws[0];
     const uint32_t per = w0->n_groups;
-    const uint32_t max_n = n_copies < WM_I2S_MAX_MULTI ? n_copies : WM_I2S_MAX_MULTI;
-    const uint32_t split = wm_i2s_pick_split(per * max_n, w0->n_chunks);
-    const size_t rows_max = (size_t)per * max_n * I2S_GROUP_ROWS;
-    const size_t need = align256(w0->in_dim) + 256 + align256(max_n * 4) +
-                        align256((size_t)split * rows_max * 4);
+    // one launch over every copy: the weight pointers in a device table.  The
+    // K split only until ~8K single-wave workgroups exist: a wave streaming a
+    // whole row group keeps its load pipeline full (320 copies of 2560x2560:
+    // 6.0 TB/s unsplit, 5.6 at split 2)
+    uint32_t split = (8192 + per * n_copies - 1) / (per * n_copies);
+    const uint32_t max_split = w0->n_chunks / 4 ? w0->n_chunks / 4 : 1;
+    split = split > max_split ? max_split : split;
+    split = split > 16 ? 16 : (split < 1 ? 1 : split);
+    const size_t rows_total = (size_t)per * n_copies * I2S_GROUP_ROWS;
+    const size_t need = align256(w0->in_dim) + 256 + align256((size_t)split * rows_total * 4);
     void *scratch;
     if ((st = wm_ctx_scratch(ctx, need, &scratch))) return st;
     uint8_t *act = (uint8_t *)scratch;
     wm_act_meta *meta = (wm_act_meta *)(act + align256(w0->in_dim));
-    float *scales = (float *)((uint8_t *)meta + 256);
-    int32_t *partial = (int32_t *)((uint8_t *)scales + align256(max_n * 4));
+    int32_t *partial = (int32_t *)((uint8_t *)meta + 256);
     WM_HIP(ctx, hipSetDevice(ctx->device));
-    wm_launch_quantize_act(d_input, (uint32_t)w0->in_dim, act, meta, ctx->stream);
-    for (uint32_t base = 0; base < n_copies; base += WM_I2S_MAX_MULTI) {
-        const uint32_t n = n_copies - base < WM_I2S_MAX_MULTI ? n_copies - base : WM_I2S_MAX_MULTI;
-        wm_i2s_desc desc[WM_I2S_MAX_MULTI];
-        float hs[WM_I2S_MAX_MULTI];
-        for (uint32_t i = 0; i < n; i++) {
-            desc[i] = {(const uint8_t *)ws[base + i]->d, per};
-            hs[i] = ws[base + i]->scale;
-        }
-        // the scales ride on the stream so a later chunk cannot overwrite them early
-        WM_HIP(ctx, hipMemcpyAsync(scales, hs, n * 4, hipMemcpyHostToDevice, ctx->stream));
-        const uint32_t rows_total = per * n * I2S_GROUP_ROWS;
-        const uint32_t sp = n == max_n ? split : wm_i2s_pick_split(per * n, w0->n_chunks);
-        wm_launch_i2s_partial(desc, (int)n, w0->n_chunks, act, partial, sp, rows_total, ctx->stream);
-        wm_launch_i2s_finalize_multi(partial, sp, rows_total, per * I2S_GROUP_ROWS,
-                                     (uint32_t)w0->out_dim, n, scales, meta,
-                                     d_outputs + (size_t)base * w0->out_dim, ctx->stream);
+    // weight pointers and scales on the device: kept from the last call when unchanged
+    std::vector<const void *> hp(n_copies);
+    std::vector<float> hs(n_copies);
+    for (uint32_t i = 0; i < n_copies; i++) {
+        hp[i] = ws[i]->d;
+        hs[i] = ws[i]->scale;
     }
+    const size_t tbytes = align256((size_t)n_copies * 8) + align256((size_t)n_copies * 4);
+    if (hp != ctx->multi_ptrs || hs != ctx->multi_scales) {
+        if (ctx->multi_bytes < tbytes) {
+            if (ctx->multi_dev) WM_HIP(ctx, hipFree(ctx->multi_dev));
+            ctx->multi_dev = nullptr;
+            ctx->multi_bytes = 0;
+            WM_HIP(ctx, hipMalloc(&ctx->multi_dev, tbytes));
+            ctx->multi_bytes = tbytes;
+        }
+        // pageable host sources: the runtime stages them before the calls return
+        WM_HIP(ctx, hipMemcpyAsync(ctx->multi_dev, hp.data(), n_copies * 8, hipMemcpyHostToDevice,
+                                   ctx->stream));
+        WM_HIP(ctx, hipMemcpyAsync((uint8_t *)ctx->multi_dev + align256((size_t)n_copies * 8),
+                                   hs.data(), n_copies * 4, hipMemcpyHostToDevice, ctx->stream));
+        ctx->multi_ptrs = hp;
+        ctx->multi_scales = hs;
+    }
+    const uint8_t *const *table = (const uint8_t *const *)ctx->multi_dev;
+    const float *scales = (const float *)((uint8_t *)ctx->multi_dev + align256((size_t)n_copies * 8));
+    wm_launch_quantize_act(d_input, (uint32_t)w0->in_dim, act, meta, ctx->stream);
+    wm_launch_i2s_partial_table(table, n_copies, per, w0->n_chunks, act, partial, split,
+                                (uint32_t)rows_total, ctx->stream);
+    wm_launch_i2s_finalize_multi(partial, split, (uint32_t)rows_total, per * I2S_GROUP_ROWS,
+                                 (uint32_t)w0->out_dim, n_copies, scales, meta, d_outputs,
+                                 ctx->stream);
     WM_HIP(ctx, hipGetLastError());
     return WM_OK;
 }

@@ -15,6 +15,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "willamette_hip.h"
 #define WM_HD __host__ __device__
@@ -33,6 +34,12 @@ struct wm_ctx {
     size_t scratch_bytes = 0;
     void *pinned = nullptr;  // pinned host staging
     size_t pinned_bytes = 0;
+    // Multi-tensor matvec: device copies of the last call's weight pointers
+    // and scales (re-sent only when they change).
+    void *multi_dev = nullptr;
+    size_t multi_bytes = 0;
+    std::vector<const void *> multi_ptrs;
+    std::vector<float> multi_scales;
 };
 
 // Objects created on a context keep their own device id: destroying them
@@ -329,6 +336,10 @@ void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
                          const uint8_t *act, const wm_act_meta *meta, const float *rope_cos,
                          const float *rope_sin, uint32_t pos, uint32_t n_rot, uint32_t rope_mask,
                          int32_t *dot_out, uint32_t *absmax, hipStream_t s);
+void wm_launch_i2s_partial_table(const uint8_t *const *table, uint32_t n_tensors,
+                                 uint32_t groups_per, uint32_t n_chunks, const uint8_t *act,
+                                 int32_t *partial, uint32_t split, uint32_t rows_total,
+                                 hipStream_t s);
 void wm_launch_i2s_partial(const wm_i2s_desc *descs, int n_desc, uint32_t n_chunks,
                            const uint8_t *act, int32_t *partial, uint32_t split,
                            uint32_t rows_total, hipStream_t s);

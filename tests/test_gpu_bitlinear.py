@@ -147,3 +147,24 @@ def test_device_and_multi_entry_points_agree(ctx):
     dy1 = ctx.alloc(out_dim * 4)
     ctx.check(wh.lib.wm_bitlinear_i2s_matvec_f32_dev(ctx.h, ws[3].h, dx.ptr, dy1.ptr))
     assert same_bits(dy1.to_host(np.float32), refs[3])
+
+
+def test_multi_entry_point_many_copies(ctx):
+    """More tensors than fit in one launch's argument block (64): the
+    pointers go through a device table."""
+    rng = np.random.default_rng(9)
+    in_dim, out_dim, n = 512, 128, 150
+    xs = rng.standard_normal(in_dim).astype(np.float32)
+    ws, refs = [], []
+    for i in range(n):
+        p = rng.integers(0, 256, in_dim // 4 * out_dim, dtype=np.uint8)
+        s = float(rng.uniform(0.5, 2))
+        ws.append(ctx.upload_i2s(p, s, in_dim, out_dim))
+        refs.append(orc.bitlinear_i8(p, np.float32(s), in_dim, out_dim, xs)[0])
+    dx = ctx.to_device(xs)
+    dy = ctx.alloc(n * out_dim * 4)
+    arr = (wh._vp * n)(*[w.h.value for w in ws])
+    ctx.check(wh.lib.wm_bitlinear_i2s_matvec_f32_multi_dev(ctx.h, arr, n, dx.ptr, dy.ptr))
+    got = dy.to_host(np.float32).reshape(n, out_dim)
+    for i in range(n):
+        assert same_bits(got[i], refs[i]), f"copy {i}"
