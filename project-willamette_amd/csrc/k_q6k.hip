@@ -16,18 +16,22 @@
 // The exact kernel gives each of those 16 partial sums to its own lane, so a
 // wave computes 4 rows with exactly the reference's roundings.
 //
-// Device layout (k_q6k_repack): rows in groups of 4; per (group, block) 840
-// bytes, the same byte count as the GGUF blocks:
-//   bytes 0..767   lane L' = 16*row + 4k + l holds, in 3 dwords A, B, C, the
-//                  16 six-bit quants it consumes in this block, q(hn, c) for
-//                  hn = 2*half + band, c = chunk: byte c of A / B / C holds
-//                  q(0, c) / q(1, c) / q(2, c) in bits 0-5, and bits 6-7 of
-//                  the three bytes hold q(3, c)'s bits 0-1 / 2-3 / 4-5; so
-//                  the quants come back as bytes (byte c of U[hn] = q(hn, c))
-//                  with three ANDs and six shift/AND-OR operations;
-//   bytes 768..831 per row the 16 sub-scales as 4 dwords (dword k, byte hn =
-//                  sc[8h + band + 2k]);
-//   bytes 832..839 the 4 f16 d values.
+// Device layout (k_q6k_repack): rows in groups of 4; a group of n_blocks
+// blocks takes 840 * n_blocks bytes, the same byte count as its GGUF blocks:
+//   quants   768 bytes per block b, at 768*b: lane L' = 16*row + 4k + l holds,
+//            in 3 dwords A, B, C, the 16 six-bit quants it consumes in this
+//            block, q(hn, c) for hn = 2*half + band, c = chunk: byte c of
+//            A / B / C holds q(0, c) / q(1, c) / q(2, c) in bits 0-5, and
+//            bits 6-7 of the three bytes hold q(3, c)'s bits 0-1 / 2-3 / 4-5;
+//            so the quants come back as bytes (byte c of U[hn] = q(hn, c))
+//            with three ANDs and six shift/AND-OR operations;
+//   scales   from 768*n_blocks, one dword per (class 4*row + k, block) in
+//            [class][block] order, byte hn = sc[8h + band + 2k];
+//   d        from 832*n_blocks, the f16 d values in [row][block] order.
+// Each class's scales and each row's d values are contiguous, so a lane
+// fetches a batch of blocks' side data with a few wide loads instead of two
+// narrow loads per block (the narrow loads cost about a tenth of the
+// lm-head pass's time).
 //
 // Two lm-head paths:
 //  * exact (k_q6k_logits): every logit bit-identical to the reference, one
@@ -70,15 +74,17 @@ __global__ void k_q6k_repack(const uint8_t *__restrict__ raw, uint8_t *__restric
         uint32_t b = gb % n_blocks;
         uint64_t G = gb / n_blocks;
         uint64_t row = G * Q6K_GROUP_ROWS + r;
-        uint8_t *dst = out + gb * Q6K_GROUP_BLOCK_BYTES;
-        uint32_t *q6 = reinterpret_cast<uint32_t *>(dst);
-        uint32_t *scw = reinterpret_cast<uint32_t *>(dst + Q6K_SC_OFFSET);
-        uint16_t *dw = reinterpret_cast<uint16_t *>(dst + Q6K_D_OFFSET);
+        uint8_t *grp = out + G * q6k_group_bytes(n_blocks);
+        uint32_t *q6 = reinterpret_cast<uint32_t *>(grp + b * Q6K_QUANT_BYTES);
+        uint32_t *scw = reinterpret_cast<uint32_t *>(grp + q6k_sc_base(n_blocks)) + b;  // + class*n_blocks
+        uint16_t *dw = reinterpret_cast<uint16_t *>(grp + q6k_d_base(n_blocks)) +
+                       r * q6k_d_stride(n_blocks) + b;
+        if (b + 1 == n_blocks && (n_blocks & 1)) dw[1] = 0;  // the row's padding half
         if (row >= n_rows) {
             for (int L = 0; L < 16; L++)
                 for (int j = 0; j < 3; j++) q6[(r * 16 + L) * 3 + j] = 0;
-            for (int k = 0; k < 4; k++) scw[r * 4 + k] = 0;
-            dw[r] = 0;
+            for (int k = 0; k < 4; k++) scw[(r * 4 + k) * n_blocks] = 0;
+            *dw = 0;
             continue;
         }
         const uint8_t *blk = raw + (row * n_blocks + b) * Q6K_BYTES;
@@ -100,9 +106,9 @@ __global__ void k_q6k_repack(const uint8_t *__restrict__ raw, uint8_t *__restric
                 int h = hn >> 1, n = hn & 1;
                 sc |= (uint32_t)blk[192 + h * 8 + n + 2 * k] << (8 * hn);
             }
-            scw[r * 4 + k] = sc;
+            scw[(r * 4 + k) * n_blocks] = sc;
         }
-        dw[r] = (uint16_t)(blk[208] | (blk[209] << 8));
+        *dw = (uint16_t)(blk[208] | (blk[209] << 8));
     }
 }
 
@@ -131,15 +137,17 @@ __global__ void k_q6k_dequant_row(const uint8_t *__restrict__ w, uint32_t n_bloc
     out += (uint64_t)blockIdx.y * ld;
     const uint32_t G = row / Q6K_GROUP_ROWS, r = row % Q6K_GROUP_ROWS;
     const uint32_t b = blockIdx.x, t = threadIdx.x;
-    const uint8_t *base = w + ((uint64_t)G * n_blocks + b) * Q6K_GROUP_BLOCK_BYTES;
+    const uint8_t *grp = w + (uint64_t)G * q6k_group_bytes(n_blocks);
     const int h = t >> 7, k = (t >> 5) & 3, n = (t >> 4) & 1, c = (t >> 2) & 3, l = t & 3;
     const int L = r * 16 + k * 4 + l, hn = h * 2 + n;
-    const uint32_t *q6 = reinterpret_cast<const uint32_t *>(base) + L * 3;
+    const uint32_t *q6 = reinterpret_cast<const uint32_t *>(grp + b * Q6K_QUANT_BYTES) + L * 3;
     const uint32_t wl[3] = {q6[0], q6[1], q6[2]};
     const uint32_t q = q6_get(wl, hn, c);
-    const uint32_t scw = reinterpret_cast<const uint32_t *>(base + Q6K_SC_OFFSET)[r * 4 + k];
+    const uint32_t scw =
+        reinterpret_cast<const uint32_t *>(grp + q6k_sc_base(n_blocks))[(r * 4 + k) * n_blocks + b];
     const int sc = (int)(int8_t)(scw >> (8 * hn));
-    const float d = wm_f16_bits_to_f32(reinterpret_cast<const uint16_t *>(base + Q6K_D_OFFSET)[r]);
+    const float d = wm_f16_bits_to_f32(
+        reinterpret_cast<const uint16_t *>(grp + q6k_d_base(n_blocks))[r * q6k_d_stride(n_blocks) + b]);
     out[b * Q6K_VALUES + t] = d * (float)sc * (float)((int)q - 32);
 }
 
@@ -171,44 +179,103 @@ __device__ void build_xs(const float *__restrict__ hidden, uint32_t n_blocks, fl
     }
 }
 
-// One lane's data for CH consecutive blocks of a 4-row group.
+// One lane's data for CH consecutive blocks of a 4-row group: its quants,
+// its class's scale dwords and its row's d values (two f16 per dword).
 template <int CH>
 struct q6_lane_blocks {
-    uint32_t w0[CH], w1[CH], w2[CH], scw[CH], db[CH];
+    uint32_t w0[CH], w1[CH], w2[CH], scw[CH], dw[(CH + 1) / 2];
 };
+template <int CH>
+__device__ __forceinline__ uint32_t q6_d_bits(const q6_lane_blocks<CH> &v, int j) {
+    return (v.dw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+}
+
+// Per-lane offsets within a group for lane (row r, lane-in-row L = 4k + l).
+struct q6_lane_offs {
+    uint32_t q, sc, d;
+};
+__device__ __forceinline__ q6_lane_offs q6_offs(uint32_t n_blocks, uint32_t r, uint32_t L) {
+    return q6_lane_offs{(16 * r + L) * 12, q6k_sc_base(n_blocks) + (4 * r + (L >> 2)) * 4 * n_blocks,
+                        q6k_d_base(n_blocks) + r * 2 * q6k_d_stride(n_blocks)};
+}
+
+typedef unsigned int q6_v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int q6_v2u __attribute__((ext_vector_type(2)));
+
+// N consecutive dwords at voff + soff through a buffer descriptor, in 16-,
+// 12-, 8- and 4-byte loads (buffer loads need dword alignment only).
+template <int N>
+__device__ __forceinline__ void q6_load_dwords(uint32_t *out, __amdgpu_buffer_rsrc_t rs,
+                                               uint32_t voff, uint32_t soff) {
+#pragma unroll
+    for (int i = 0; i + 4 <= N; i += 4) {
+        const q6_v4u q = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff + 4 * i, WM_LOAD_NT);
+        out[i] = q.x;
+        out[i + 1] = q.y;
+        out[i + 2] = q.z;
+        out[i + 3] = q.w;
+    }
+    constexpr int i = N & ~3;
+    if constexpr (N - i == 3) {
+        const wm_v3u q = __builtin_amdgcn_raw_buffer_load_b96(rs, voff, soff + 4 * i, WM_LOAD_NT);
+        out[i] = q.x;
+        out[i + 1] = q.y;
+        out[i + 2] = q.z;
+    } else if constexpr (N - i == 2) {
+        const q6_v2u q = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff + 4 * i, WM_LOAD_NT);
+        out[i] = q.x;
+        out[i + 1] = q.y;
+    } else if constexpr (N - i == 1) {
+        out[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff + 4 * i, WM_LOAD_NT);
+    }
+}
 
 // Loads through a buffer descriptor of a wave-uniform group base (streaming
-// kernels): lane offsets are per-lane constants, block offsets uniform.
+// kernels): lane offsets are per-lane constants, block offsets uniform.  Per
+// batch: the side data in a few wide loads (an even CH starts on an even
+// block, so its d values start on a dword), then CH 12-byte quant loads;
+// side data first, so the first block can be reduced as soon as its quants
+// arrive.
 template <int CH>
 __device__ __forceinline__ void q6_load_uniform(q6_lane_blocks<CH> &v, __amdgpu_buffer_rsrc_t rs,
-                                                uint32_t b0, uint32_t off_q, uint32_t off_sc,
-                                                uint32_t off_d) {
+                                                uint32_t b0, const q6_lane_offs &o) {
+    q6_load_dwords<CH>(v.scw, rs, o.sc, b0 * 4);
+    if constexpr (CH % 2 == 0) {
+        q6_load_dwords<CH / 2>(v.dw, rs, o.d, b0 * 2);
+    } else {
+#pragma unroll
+        for (int j = 0; j < (CH + 1) / 2; j++) v.dw[j] = 0;
+#pragma unroll
+        for (int j = 0; j < CH; j++)
+            v.dw[j >> 1] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, o.d, (b0 + j) * 2, 0)
+                            << (16 * (j & 1));
+    }
 #pragma unroll
     for (int j = 0; j < CH; j++) {
-        const uint32_t so = (b0 + j) * Q6K_GROUP_BLOCK_BYTES;
-        const wm_v3u q = __builtin_amdgcn_raw_buffer_load_b96(rs, off_q, so, WM_LOAD_NT);
+        const wm_v3u q =
+            __builtin_amdgcn_raw_buffer_load_b96(rs, o.q, (b0 + j) * Q6K_QUANT_BYTES, WM_LOAD_NT);
         v.w0[j] = q.x;
         v.w1[j] = q.y;
         v.w2[j] = q.z;
-        v.scw[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, off_sc, so, WM_LOAD_NT);
-        v.db[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, off_d, so, 0);
     }
 }
 
 // Loads from a per-lane group base (rows gathered from different groups).
 template <int CH>
 __device__ __forceinline__ void q6_load_lane(q6_lane_blocks<CH> &v, const uint8_t *gbase,
-                                             uint32_t b0, uint32_t off_q, uint32_t off_sc,
-                                             uint32_t off_d) {
+                                             uint32_t b0, const q6_lane_offs &o) {
+#pragma unroll
+    for (int j = 0; j < (CH + 1) / 2; j++) v.dw[j] = 0;
 #pragma unroll
     for (int j = 0; j < CH; j++) {
-        const uint8_t *base = gbase + (b0 + j) * Q6K_GROUP_BLOCK_BYTES;
-        const uint32_t *q6 = reinterpret_cast<const uint32_t *>(base + off_q);
+        const uint32_t *q6 =
+            reinterpret_cast<const uint32_t *>(gbase + (b0 + j) * Q6K_QUANT_BYTES + o.q);
         v.w0[j] = q6[0];
         v.w1[j] = q6[1];
         v.w2[j] = q6[2];
-        v.scw[j] = *reinterpret_cast<const uint32_t *>(base + off_sc);
-        v.db[j] = *reinterpret_cast<const uint16_t *>(base + off_d);
+        v.scw[j] = reinterpret_cast<const uint32_t *>(gbase + o.sc)[b0 + j];
+        v.dw[j >> 1] |= (uint32_t)reinterpret_cast<const uint16_t *>(gbase + o.d)[b0 + j]
+                        << (16 * (j & 1));
     }
 }
 
@@ -221,7 +288,7 @@ __device__ __forceinline__ void q6_exact_accum(const q6_lane_blocks<CH> &v, uint
     for (int j = 0; j < CH; j++) {
         uint32_t U[4];
         q6_unpack(v.w0[j], v.w1[j], v.w2[j], U);
-        const float d = wm_f16_bits_to_f32(v.db[j]);
+        const float d = wm_f16_bits_to_f32(q6_d_bits(v, j));
         const float *xb = xl + (b0 + j) * 16;
         if (__builtin_expect(isfinite(d), 1)) {
 #pragma unroll
@@ -272,9 +339,8 @@ __global__ __launch_bounds__(kLogitsBlock) void k_q6k_logits(
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t r = lane >> 4, L = lane & 15;
     const float *xl = xs + L * xs_stride(n_blocks);
-    const uint32_t off_q = lane * 12, off_sc = Q6K_SC_OFFSET + (r * 4 + (L >> 2)) * 4,
-                   off_d = Q6K_D_OFFSET + r * 2;
-    const uint32_t group_bytes = n_blocks * Q6K_GROUP_BLOCK_BYTES;
+    const q6_lane_offs o = q6_offs(n_blocks, r, L);
+    const uint32_t group_bytes = q6k_group_bytes(n_blocks);
     float best_v = -INFINITY;
     uint32_t best_i = 0xFFFFFFFFu;
     constexpr uint32_t kWaves = kLogitsBlock / 64;
@@ -284,7 +350,7 @@ __global__ __launch_bounds__(kLogitsBlock) void k_q6k_logits(
         float acc = 0.0f;
         for (uint32_t b0 = 0; b0 < n_blocks; b0 += CH) {
             q6_lane_blocks<CH> v;
-            q6_load_uniform<CH>(v, rs, b0, off_q, off_sc, off_d);
+            q6_load_uniform<CH>(v, rs, b0, o);
             q6_exact_accum<CH>(v, b0, xl, acc);
         }
         const float dot = q6_combine(acc);
@@ -408,7 +474,7 @@ __device__ __forceinline__ void q6_bounded_accum(const q6_lane_blocks<CH> &v, ui
             const int I = (int)(((uint32_t)dh << 8) + (uint32_t)dl);  // a VALU result
             T = mad_i24(sc, I, T);
         }
-        const float d = __half2float(__ushort_as_half((unsigned short)v.db[j]));
+        const float d = __half2float(__ushort_as_half((unsigned short)q6_d_bits(v, j)));
         acc = __builtin_fmaf(d, (float)T, acc);
     }
 }
@@ -436,10 +502,9 @@ __global__ __launch_bounds__(kBoundedBlock) void k_q6k_bounded(
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t r = lane >> 4, p = lane & 15, k = p >> 2;
-    const uint32_t off_q = lane * 12, off_sc = Q6K_SC_OFFSET + (r * 4 + k) * 4,
-                   off_d = Q6K_D_OFFSET + r * 2;
-    const uint32_t group_bytes = n_blocks * Q6K_GROUP_BLOCK_BYTES;
+    const uint32_t r = lane >> 4, p = lane & 15;
+    const q6_lane_offs o = q6_offs(n_blocks, r, p);
+    const uint32_t group_bytes = q6k_group_bytes(n_blocks);
     const uint32_t g0 = (uint32_t)((uint64_t)blockIdx.x * n_rowgroups / gridDim.x);
     const uint32_t g1 = (uint32_t)((uint64_t)(blockIdx.x + 1) * n_rowgroups / gridDim.x);
     float lb_max = -INFINITY, ub_max = -INFINITY;
@@ -467,44 +532,70 @@ __global__ __launch_bounds__(kBoundedBlock) void k_q6k_bounded(
         }
     };
     if (PIPE) {
-        // batches (group G, blocks bi*CH ..): the next batch's loads are in
-        // flight while this one is reduced; two register sets used in turn
-        // (the loop body covers two batches, so no set is ever copied)
+        // Batches (group G, blocks bi*CH ..) in the order the wave takes them;
+        // batch t+1's loads are in flight while batch t is reduced, in two
+        // register sets used in turn (the loop body covers two batches, so no
+        // set is ever copied).  The trip count is fixed before the loop and
+        // the last batch is reduced after it, so every path into the loop
+        // head has the same loads in flight and the wait for a batch never
+        // covers the one issued after it (an exit between the two halves
+        // would make the head's waits assume the other set still pending).
+        // A row's sigma goes out before its batch, so reading it waits for no
+        // weight bytes.
         const uint32_t nbat = n_blocks / CH;
-        uint32_t G = g0 + wave, bi = 0;
-        if (G < g1) {
+        const uint32_t G0 = g0 + wave;
+        if (G0 < g1) {
+            const uint32_t total = (g1 - G0 + kWaves - 1) / kWaves * nbat;
+            uint32_t G = G0, bi = 0;   // batch being reduced
+            uint32_t Gn = G0, bn = 0;  // batch last issued
             q6_lane_blocks<CH> A, B;
-            q6_load_uniform<CH>(A, wm_rsrc(w + (uint64_t)G * group_bytes, group_bytes), 0, off_q,
-                                off_sc, off_d);
-            float sg = sigma[min(G * Q6K_GROUP_ROWS + r, n_rows - 1)];
+            float sg = sigma[min(G0 * Q6K_GROUP_ROWS + r, n_rows - 1)], sg_n = sg;
+            q6_load_uniform<CH>(A, wm_rsrc(w + (uint64_t)G0 * group_bytes, group_bytes), 0, o);
             float acc = 0.0f;
-            // one batch: prefetch the next one into `nxt`, reduce `cur`;
-            // returns false after the wave's last batch
-            auto step = [&](const q6_lane_blocks<CH> &cur, q6_lane_blocks<CH> &nxt) -> bool {
-                uint32_t Gn = G, bn = bi + 1;
-                if (bn == nbat) {
+            // live = false: past the wave's last batch; the descriptor then
+            // holds no records, so the loads return zeros without a memory
+            // access (and the group index may run past g1)
+            auto issue = [&](q6_lane_blocks<CH> &nxt, bool live) {
+                if (++bn == nbat) {
                     bn = 0;
-                    Gn = G + kWaves;
+                    Gn += kWaves;
                 }
-                const bool more = Gn < g1;
-                float sg_n = sg;
-                if (more) {
-                    q6_load_uniform<CH>(nxt, wm_rsrc(w + (uint64_t)Gn * group_bytes, group_bytes),
-                                        bn * CH, off_q, off_sc, off_d);
-                    if (bn == 0) sg_n = sigma[min(Gn * Q6K_GROUP_ROWS + r, n_rows - 1)];
-                }
+                const uint32_t Gs = live ? Gn : G0;
+                sg_n = sigma[min(Gs * Q6K_GROUP_ROWS + r, n_rows - 1)];
+                q6_load_uniform<CH>(nxt, wm_rsrc(w + (uint64_t)Gs * group_bytes, live ? group_bytes : 0u),
+                                    bn * CH, o);
+                // keep the whole prefetch ahead of the reduction (the
+                // scheduler would otherwise sink loads into it to save
+                // registers)
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            auto reduce = [&](const q6_lane_blocks<CH> &cur) {
                 q6_bounded_accum<CH>(cur, bi * CH, xq, p, acc);
                 if (bi + 1 == nbat) {
                     epilogue(G * Q6K_GROUP_ROWS + r, acc, sg);
                     acc = 0.0f;
+                    bi = 0;
+                    G += kWaves;
+                } else {
+                    bi++;
                 }
-                G = Gn;
-                bi = bn;
-                sg = sg_n;
-                return more;
+                __builtin_amdgcn_sched_barrier(0);  // one batch's registers live at a time
             };
-            while (step(A, B) && step(B, A)) {
+            uint32_t t = 1;  // batches issued
+            for (; t + 1 < total; t += 2) {
+                issue(B, true);
+                reduce(A);
+                sg = sg_n;
+                issue(A, true);
+                reduce(B);
+                sg = sg_n;
             }
+            // the last one or two batches, on one code path
+            const bool two = t < total;
+            issue(B, two);
+            reduce(A);
+            sg = sg_n;
+            if (two) reduce(B);
         }
     } else {
         for (uint32_t G = g0 + wave; G < g1; G += kWaves) {
@@ -514,7 +605,7 @@ __global__ __launch_bounds__(kBoundedBlock) void k_q6k_bounded(
             float acc = 0.0f;
             for (uint32_t b0 = 0; b0 < n_blocks; b0 += CH) {
                 q6_lane_blocks<CH> v;
-                q6_load_uniform<CH>(v, rs, b0, off_q, off_sc, off_d);
+                q6_load_uniform<CH>(v, rs, b0, o);
                 q6_bounded_accum<CH>(v, b0, xq, p, acc);
             }
             epilogue(row, acc, sg);
@@ -604,15 +695,13 @@ __global__ __launch_bounds__(kSelectBlock) void k_q6k_select(
                     const uint32_t ci = min(c0 + slot, nc - 1);
                     const uint32_t crow = cand[ci];
                     const uint8_t *gbase =
-                        w + (uint64_t)(crow / Q6K_GROUP_ROWS) * n_blocks * Q6K_GROUP_BLOCK_BYTES;
+                        w + (uint64_t)(crow / Q6K_GROUP_ROWS) * q6k_group_bytes(n_blocks);
                     const uint32_t rr = crow % Q6K_GROUP_ROWS;
-                    const uint32_t off_q = (16 * rr + L) * 12,
-                                   off_sc = Q6K_SC_OFFSET + (rr * 4 + (L >> 2)) * 4,
-                                   off_d = Q6K_D_OFFSET + rr * 2;
+                    const q6_lane_offs o = q6_offs(n_blocks, rr, L);
                     float acc = 0.0f;
                     for (uint32_t b0 = 0; b0 < n_blocks; b0 += CH) {
                         q6_lane_blocks<CH> v;
-                        q6_load_lane<CH>(v, gbase, b0, off_q, off_sc, off_d);
+                        q6_load_lane<CH>(v, gbase, b0, o);
                         q6_exact_accum<CH>(v, b0, xl, acc);
                     }
                     const float dot = q6_combine(acc);

@@ -84,13 +84,22 @@ constexpr int Q6K_VALUES = 256;
 constexpr int Q6K_BYTES = 210;
 constexpr int Q6K_GROUP_ROWS = 4;         // rows per wave in the device layout
 constexpr int Q6K_GROUP_BLOCK_BYTES = 840;  // 4 rows x 210 bytes
-constexpr int Q6K_SC_OFFSET = 768;          // per (group, block): q6 768 B, sc 64 B, d 8 B
-constexpr int Q6K_D_OFFSET = 832;
+constexpr int Q6K_QUANT_BYTES = 768;        // six-bit quants of one (group, block)
+// Within a group of n_blocks blocks: the quants of block b at 768*b, then the
+// sub-scale dwords of class c = 4*row + quarter as [c][b] from 768*n_blocks,
+// then the f16 d values as [row][b] from 832*n_blocks, each row's run padded
+// to an even count (so an even run of blocks starts on a dword).
+__host__ __device__ inline uint32_t q6k_sc_base(uint32_t n_blocks) { return 768u * n_blocks; }
+__host__ __device__ inline uint32_t q6k_d_base(uint32_t n_blocks) { return 832u * n_blocks; }
+__host__ __device__ inline uint32_t q6k_d_stride(uint32_t n_blocks) { return (n_blocks + 1) & ~1u; }
+__host__ __device__ inline uint32_t q6k_group_bytes(uint32_t n_blocks) {
+    return 832u * n_blocks + 8u * q6k_d_stride(n_blocks);
+}
 // After the 4-row-group layout, 256-aligned: one f32 per row holding
 // sum_j |d * sc_j| rounded up (x-independent part of the id-only lm-head's
 // error bound).  Part of the same allocation, so copies of the tensor carry it.
 __host__ __device__ inline size_t wm_q6k_sigma_offset(uint32_t n_rowgroups, uint32_t n_blocks) {
-    return ((size_t)n_rowgroups * n_blocks * Q6K_GROUP_BLOCK_BYTES + 255) & ~(size_t)255;
+    return ((size_t)n_rowgroups * q6k_group_bytes(n_blocks) + 255) & ~(size_t)255;
 }
 
 // ---------------------------------------------------------------------------
