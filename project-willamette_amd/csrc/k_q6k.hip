@@ -462,15 +462,19 @@ __device__ __forceinline__ void q6_bounded_accum(const q6_lane_blocks<CH> &v, ui
     for (int j = 0; j < CH; j++) {
         uint32_t U[4];
         q6_unpack(v.w0[j], v.w1[j], v.w2[j], U);
-        const q6k_xq &xv = xq[(b0 + j) * 16 + p];
+        // the block's 48 bytes of x in three 16-byte LDS reads
+        const int4 *xp = reinterpret_cast<const int4 *>(xq + (b0 + j) * 16 + p);
+        const int4 h4 = xp[0], l4 = xp[1], c4 = xp[2];
+        const int xh[4] = {h4.x, h4.y, h4.z, h4.w}, xl[4] = {l4.x, l4.y, l4.z, l4.w},
+                  xc[4] = {c4.x, c4.y, c4.z, c4.w};
         int T = 0;
 #pragma unroll
         for (int hn = 0; hn < 4; hn++) {
             const int sc = (int)(int8_t)(v.scw[j] >> (8 * hn));
             // (clamp selects the three-operand encoding, which needs no zeroed
             // accumulator register; |dh| <= 32256 never saturates)
-            const int dh = __builtin_amdgcn_sdot4((int)U[hn], xv.xh[hn], 0, true);
-            const int dl = __builtin_amdgcn_sdot4((int)U[hn], xv.xl[hn], xv.c[hn], false);
+            const int dh = __builtin_amdgcn_sdot4((int)U[hn], xh[hn], 0, true);
+            const int dl = __builtin_amdgcn_sdot4((int)U[hn], xl[hn], xc[hn], false);
             const int I = (int)(((uint32_t)dh << 8) + (uint32_t)dl);  // a VALU result
             T = mad_i24(sc, I, T);
         }
