@@ -171,12 +171,14 @@ __device__ inline float seq_sum_nonneg(const float *a, uint32_t n) {
 //     E of the f32 running sum before term k.  (The f32 sum differs from P_k
 //     by accumulated rounding, far less than the distance to a power of two
 //     for almost every k; every prediction is checked in step 3.)
-//  2. Term k is a break if k = 0, if P_k or P_(k+1) is not positive and
-//     finite, if their binades differ, if P_k (k a thread's first term) or
-//     P_(k+1) (k its last) lies close to a power of two (below), if
-//     a_k / ulp(E) is halfway between integers (the rounding
-//     then depends on the running significand's parity) or if it is huge.
-//     Every other term contributes the integer increment RN_int(a_k / ulp(E)).
+//  2. A non-zero term k is a break if k = 0, if P_k or P_(k+1) is not
+//     positive and finite, if their binades differ, if a_k / ulp(E) is
+//     halfway between integers (the rounding then depends on the running
+//     significand's parity) or if it is huge; any term is one if P_k (k a
+//     thread's first term) or P_(k+1) (k its last) lies close to a power of
+//     two (below).  Every other term contributes the integer increment
+//     RN_int(a_k / ulp(E)) (0 for a zero term, which changes no running sum;
+//     the terms before the first break are therefore all zeros).
 //     A wave-wide integer scan places each wave's breaks in its own record
 //     list, with the increment total before each.
 //  3. One wave joins the lists and walks the breaks in order.  For a segment
@@ -281,9 +283,15 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
         const bool pb_ok = pb > 0.0 && pb < 1e300, pa_ok = pa > 0.0 && pa < 1e300;
         const int eb = pb_ok ? exp2floor_f64(pb) : 0;
         const int ea = pa_ok ? exp2floor_f64(pa) : -1000;
-        bool b = k == 0 || !pb_ok || !pa_ok || ea != eb;
-        if (j == 0) b = b || near_pow2_f64(pb, 34);
-        b = b || ((uint32_t)j == last && near_pow2_f64(pa, 36));
+        // a zero term leaves every running sum (+0, positive, inf or NaN)
+        // unchanged, so it is never a break on its own account: a run of
+        // zeros (an underflowed softmax tail, a zero prefix) costs nothing
+        const bool zero = v[j] == 0.0f;
+        bool b = !zero && (k == 0 || !pb_ok || !pa_ok || ea != eb);
+        // (a zero prefix is exact in both precisions: every term before it
+        // is zero, so no computation of it can land in another binade)
+        if (j == 0) b = b || (pb_ok && near_pow2_f64(pb, 34));
+        b = b || ((uint32_t)j == last && pa_ok && near_pow2_f64(pa, 36));
         int d = 0;
         if (!b) {
             const float r = ldexpf(v[j], 23 - eb);  // a_k / ulp; exact unless < 2^-126
@@ -381,7 +389,9 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
                 // per step, t = s + A; s = t + V (V: the break term, +0 past
                 // the last record); every lane checks its own step afterwards
                 // from the value s had on entry.
-                const bool seg = cnt > 0;
+                // the terms before the first break are all zeros (a non-zero
+                // term on a zero prefix is a break), so that segment adds nothing
+                const bool seg = cnt > 0 && r >= 1;
                 const bool e_ok = e0 >= -126 && e0 <= 127;
                 const float A = seg && e_ok ? ldexpf((float)D, e0 - 23) : 0.0f;
                 const float lo = seg ? (e_ok ? ldexpf(1.0f, e0) : __int_as_float(0x7F800000)) : 0.0f;
@@ -410,7 +420,7 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
                 if (__builtin_amdgcn_readfirstlane(bad) != 0) {
                     s = s0;
                     for (int i = 0; i < here; i++) {
-                        const int c = __builtin_amdgcn_readlane(cnt, i);
+                        const int c = base + i >= 1 ? __builtin_amdgcn_readlane(cnt, i) : 0;
                         if (c > 0) {
                             const int Di = __builtin_amdgcn_readlane(D, i);
                             const int e = __builtin_amdgcn_readlane(e0, i);

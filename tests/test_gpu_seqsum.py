@@ -74,6 +74,15 @@ def cases():
     ones = np.ones(4000, np.float32)
     ones[::7] = np.float32(2.0 ** -30)
     out.append(("ones_on_powers", ones))
+    # runs of exact zeros: a softmax whose older positions underflow (zero
+    # prefix, then the live terms), a zero lead-in, a sparse vector
+    for n, live in ((1088, 64), (4000, 5), (2049, 1)):
+        sc = np.concatenate([rng.standard_normal(n - live) * 4.0 - 200.0, rng.standard_normal(live) * 3.0])
+        out.append((f"softmax_underflow{n}_{live}", np.exp((sc - sc.max()).astype(np.float32)).astype(np.float32)))
+    out.append(("zero_lead", np.concatenate([np.zeros(700), rng.random(388) + 0.5]).astype(np.float32)))
+    sp = (rng.standard_normal(3000) ** 2).astype(np.float32)
+    sp[rng.random(3000) < 0.9] = 0.0
+    out.append(("sparse", sp))
     return out
 
 
@@ -96,5 +105,7 @@ def test_seq_sum_random_fuzz(ctx):
             a = (rng.integers(0, 8, n) * scale).astype(np.float32)
         else:
             a = rng.exponential(scale, n).astype(np.float32)
+        if i % 5 == 4:  # runs of zeros
+            a[rng.random(n) < rng.random()] = 0.0
         got, ref = wh.debug_seq_sum(ctx, a), seq_ref(a)
         assert same(got, ref), f"case {i} n={n} kind={kind}: {got!r} vs {ref!r}"

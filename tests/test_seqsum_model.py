@@ -127,13 +127,12 @@ def model_block_sum(a, stats=None, nt=BLOCK_THREADS, start_prefix=None, near_rul
             P = pa
             pb_ok = 0 < pb < 1e300
             pa_ok = 0 < pa < 1e300
-            brk = k == 0 or not pb_ok or not pa_ok
-            if not brk:
-                eb, ea = _exp2floor(pb), _exp2floor(pa)
-                brk = ea != eb
-                if near_rule:  # only where the prefix crosses a thread boundary
-                    brk = brk or (k == k0 and _near_pow2(pb, 34)) or \
-                        (k == min(k0 + m, n) - 1 and _near_pow2(pa, 36))
+            zero = v == 0  # changes no running sum: never a break on its own account
+            eb = _exp2floor(pb) if pb_ok else 0
+            brk = not zero and (k == 0 or not pb_ok or not pa_ok or _exp2floor(pa) != eb)
+            if near_rule:  # only where the prefix crosses a thread boundary
+                brk = brk or (k == k0 and pb_ok and _near_pow2(pb, 34)) or \
+                    (k == min(k0 + m, n) - 1 and pa_ok and _near_pow2(pa, 36))
             if not brk:
                 with np.errstate(all="ignore"):
                     r = np.float32(np.ldexp(v, 23 - eb))
@@ -157,7 +156,11 @@ def model_block_sum(a, stats=None, nt=BLOCK_THREADS, start_prefix=None, near_rul
     prev_t, prev_pi, e_seg = -1, 0, None
     for (t, ea, pit, v) in recs + [(n, None, off, None)]:
         cnt = t - prev_t - 1
-        if cnt > 0:
+        if cnt > 0 and prev_t < 0:
+            # before the first break: zeros only (a non-zero term on a zero
+            # prefix is a break), which add nothing
+            assert not np.any(a[:t]), "non-zero term before the first break"
+        elif cnt > 0:
             d = pit - prev_pi
             bits = int(np.array(s, np.float32).view(np.uint32))
             ef = bits >> 23
@@ -341,3 +344,41 @@ def test_block_model_boundary_fuzz():
         if not np.isfinite(a).all() or (a < 0).any():
             continue
         assert same(model_block_sum(a, start_prefix=_flip_across_pow2), sequential(a)), f"case {i}"
+
+
+def _softmax_underflow(rng, n, live):
+    """exp(s - max) of scores whose spread underflows all but the last `live`
+    terms to exactly zero (a softmax dominated by the newest positions)."""
+    s = np.concatenate([rng.standard_normal(n - live) * 4.0 - 200.0, rng.standard_normal(live) * 3.0])
+    e = np.exp((s - s.max()).astype(np.float32)).astype(np.float32)
+    assert (e[: n - live] == 0).all()
+    return e
+
+
+def test_block_model_zero_runs_are_not_breaks():
+    """Zero terms change no running sum, so runs of them (a zero prefix, an
+    underflowed softmax tail) cost no breaks; the sum stays exact."""
+    rng = np.random.default_rng(23)
+    cases = [np.zeros(1088, np.float32), _softmax_underflow(rng, 1088, 64),
+             _softmax_underflow(rng, 4000, 5), _softmax_underflow(rng, 2049, 1)]
+    sparse = (rng.standard_normal(3000) ** 2).astype(np.float32)
+    sparse[rng.random(3000) < 0.9] = 0.0
+    cases.append(sparse)
+    lead = np.concatenate([np.zeros(700), rng.random(388) + 0.5]).astype(np.float32)
+    cases.append(lead)
+    for i, a in enumerate(cases):
+        st = {}
+        assert same(model_block_sum(a, st), sequential(a)), f"case {i}"
+        nz = int(np.count_nonzero(a))
+        # breaks come from the non-zero terms (binade changes, the first
+        # non-zero term) and the rare near-power-of-two boundaries
+        assert st["breaks"] <= min(nz, 64) + 4, f"case {i}: {st['breaks']} breaks, {nz} non-zero"
+
+
+def test_block_model_zero_runs_fuzz():
+    rng = np.random.default_rng(29)
+    for i in range(200):
+        n = int(rng.integers(1, 4096))
+        a = (rng.standard_normal(n) ** 2 * 2.0 ** rng.integers(-30, 30)).astype(np.float32)
+        a[rng.random(n) < rng.random()] = 0.0
+        assert same(model_block_sum(a), sequential(a)), f"case {i}"
