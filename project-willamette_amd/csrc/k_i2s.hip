@@ -120,13 +120,66 @@ __device__ __forceinline__ void dot_chunk(const uint4 wv, const int *__restrict_
     }
 }
 
+// One round: chunks c .. c+3 of RG row groups (chunk u of group q at
+// wp[q] + u * I2S_GROUP_ROWS, uint4 units, this lane's row), the indices past
+// the slice clamped to its last chunk so every load is in range.
+template <int RG>
+struct i2s_round {
+    uint4 v[4][RG];
+};
+template <int RG>
+__device__ __forceinline__ void i2s_issue(i2s_round<RG> &R, const uint4 *const (&wp)[RG],
+                                          uint32_t c, uint32_t nc) {
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int q = 0; q < RG; q++)
+            R.v[u][q] = wm_load_stream(wp[q] + min(c + (uint32_t)u, nc - 1) * I2S_GROUP_ROWS);
+}
+template <int RG>
+__device__ __forceinline__ void i2s_reduce(const i2s_round<RG> &R, const int *act_s, uint32_t c,
+                                           uint32_t cnt, int (&acc16)[RG], int (&acc4)[RG],
+                                           int (&acc1)[RG]) {
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        if ((uint32_t)u < cnt)
+#pragma unroll
+            for (int q = 0; q < RG; q++)
+                dot_chunk(R.v[u][q], act_s + (c + u) * 16, acc16[q], acc4[q], acc1[q]);
+}
+// The dots over chunks 0 .. nc-1, round 0 already issued into A: the next
+// round's loads go out before the current one is reduced, into the other
+// register set (the loop body covers two rounds, so no set is copied); a
+// round past the slice is never issued, and the last one is reduced on its
+// own path.
+template <int RG>
+__device__ __forceinline__ void i2s_rounds(i2s_round<RG> &A, i2s_round<RG> &B,
+                                           const uint4 *const (&wp)[RG], uint32_t nc, const int *act_s,
+                                           int (&acc16)[RG], int (&acc4)[RG], int (&acc1)[RG]) {
+    for (uint32_t c = 0;; c += 8) {
+        if (c + 4 >= nc) {
+            i2s_reduce<RG>(A, act_s, c, nc - c, acc16, acc4, acc1);
+            return;
+        }
+        i2s_issue<RG>(B, wp, c + 4, nc);
+        __builtin_amdgcn_sched_barrier(0);  // the prefetch stays ahead of the reduction
+        i2s_reduce<RG>(A, act_s, c, 4, acc16, acc4, acc1);
+        if (c + 8 >= nc) {
+            i2s_reduce<RG>(B, act_s, c + 4, nc - c - 4, acc16, acc4, acc1);
+            return;
+        }
+        i2s_issue<RG>(A, wp, c + 8, nc);
+        __builtin_amdgcn_sched_barrier(0);
+        i2s_reduce<RG>(B, act_s, c + 4, 4, acc16, acc4, acc1);
+    }
+}
+
 // grid: x = (global group index over all tensors) / RG, y = K split.  One
 // wave, owning RG consecutive 64-row groups of one tensor: lane r computes
 // row r of each.  The wave's slice of the activation vector is staged in LDS
 // once; every activation read (a uniform broadcast) then serves RG weight
 // chunks.  Weights stream in rounds of 4 x RG 1 KiB loads, the next round in
-// flight while the current one is reduced; chunk indices past the slice are
-// clamped to its last chunk, so every load is in range and unconditional.
+// flight while the current one is reduced (i2s_rounds).
 template <int RG>
 __global__ __launch_bounds__(64) void k_i2s_partial(i2s_multi m, uint32_t n_chunks,
                                                     const int *__restrict__ act,
@@ -154,46 +207,18 @@ __global__ __launch_bounds__(64) void k_i2s_partial(i2s_multi m, uint32_t n_chun
     const uint32_t c1 = (uint32_t)(((uint64_t)n_chunks * (s + 1)) / split);
     const uint32_t r = threadIdx.x, nc = c1 - c0;
     const uint64_t gstride = (uint64_t)n_chunks * I2S_GROUP_ROWS;  // uint4 per group
-    const uint4 *wp = W + ((uint64_t)g * n_chunks + c0) * I2S_GROUP_ROWS + r;
-    uint4 cur[4][RG];
+    const uint4 *wp[RG];
 #pragma unroll
-    for (int u = 0; u < 4; u++)
-#pragma unroll
-        for (int q = 0; q < RG; q++)
-            cur[u][q] = wm_load_stream(wp + q * gstride + min((uint32_t)u, nc - 1) * I2S_GROUP_ROWS);
+    for (int q = 0; q < RG; q++) wp[q] = W + ((uint64_t)g * n_chunks + c0) * I2S_GROUP_ROWS + r + q * gstride;
+    i2s_round<RG> A, B;
+    i2s_issue<RG>(A, wp, 0, nc);
     const int4 *ag = reinterpret_cast<const int4 *>(act) + (uint64_t)c0 * 4;
     for (uint32_t i = r; i < nc * 4; i += 64) reinterpret_cast<int4 *>(act_s)[i] = ag[i];
     wm_sync_lds();
     int acc16[RG], acc4[RG], acc1[RG];
 #pragma unroll
     for (int q = 0; q < RG; q++) acc16[q] = acc4[q] = acc1[q] = 0;
-    uint32_t c = 0;
-    for (; c + 4 <= nc; c += 4) {
-        uint4 nxt[4][RG];
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-#pragma unroll
-            for (int q = 0; q < RG; q++)
-                nxt[u][q] = wm_load_stream(wp + q * gstride +
-                                           min(c + 4 + (uint32_t)u, nc - 1) * I2S_GROUP_ROWS);
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int *a = act_s + (c + u) * 16;
-#pragma unroll
-            for (int q = 0; q < RG; q++) dot_chunk(cur[u][q], a, acc16[q], acc4[q], acc1[q]);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-#pragma unroll
-            for (int q = 0; q < RG; q++) cur[u][q] = nxt[u][q];
-    }
-    // the last nc % 4 chunks are cur[0 .. nc%4-1] (loaded by the final round)
-#pragma unroll
-    for (int u = 0; u < 3; u++)
-        if (c + u < nc)
-#pragma unroll
-            for (int q = 0; q < RG; q++)
-                dot_chunk(cur[u][q], act_s + (c + u) * 16, acc16[q], acc4[q], acc1[q]);
+    i2s_rounds<RG>(A, B, wp, nc, act_s, acc16, acc4, acc1);
 #pragma unroll
     for (int q = 0; q < RG; q++)
         partial[(uint64_t)s * rows_total + (uint64_t)(gg + q) * I2S_GROUP_ROWS + r] =
@@ -253,51 +278,31 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
         const uint32_t g = MODE == WM_FUSED_GATEUP ? lu : lu * UG + q;
         wp[q] = reinterpret_cast<const uint4 *>(a.w[tq]) + g * gstride + (uint64_t)c0 * I2S_GROUP_ROWS + lane;
     }
-    uint4 cur[4][UG];
-#pragma unroll
-    for (int v = 0; v < 4; v++)
-#pragma unroll
-        for (int q = 0; q < UG; q++)
-            cur[v][q] = wm_load_stream(wp[q] + min((uint32_t)v, nc - 1) * I2S_GROUP_ROWS);
+    i2s_round<UG> A, B;
+    i2s_issue<UG>(A, wp, 0, nc);
     int *act_s = smem;
     const int4 *ag = reinterpret_cast<const int4 *>(a.act) + (uint64_t)c0 * 4;
     for (uint32_t i = lane; i < nc * 4; i += 64) reinterpret_cast<int4 *>(act_s + c0 * 16)[i] = ag[i];
+    // the epilogue's inputs, fetched now rather than after the reduction
+    const float act_scale = a.meta->scale;
+    const int asum = a.meta->asum;
+    const uint32_t half = a.n_rot / 2;  // ROPE: at most 64 <= W * 64 pairs, one per thread
+    const bool rope = MODE == WM_FUSED_ROPE && ((a.rope_mask >> t) & 1u);
+    float rc = 0.0f, rs = 0.0f;
+    if (rope && threadIdx.x < half) {
+        rc = a.rope_cos[(uint64_t)a.pos * half + threadIdx.x];
+        rs = a.rope_sin[(uint64_t)a.pos * half + threadIdx.x];
+    }
     wm_sync_lds();
     int acc16[UG], acc4[UG], acc1[UG];
 #pragma unroll
     for (int q = 0; q < UG; q++) acc16[q] = acc4[q] = acc1[q] = 0;
-    uint32_t c = 0;
-    for (; c + 4 <= nc; c += 4) {
-        uint4 nxt[4][UG];
-#pragma unroll
-        for (int v = 0; v < 4; v++)
-#pragma unroll
-            for (int q = 0; q < UG; q++)
-                nxt[v][q] = wm_load_stream(wp[q] + min(c + 4 + (uint32_t)v, nc - 1) * I2S_GROUP_ROWS);
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int *av = act_s + (c0 + c + v) * 16;
-#pragma unroll
-            for (int q = 0; q < UG; q++) dot_chunk(cur[v][q], av, acc16[q], acc4[q], acc1[q]);
-        }
-#pragma unroll
-        for (int v = 0; v < 4; v++)
-#pragma unroll
-            for (int q = 0; q < UG; q++) cur[v][q] = nxt[v][q];
-    }
-#pragma unroll
-    for (int v = 0; v < 3; v++)
-        if (c + v < nc)
-#pragma unroll
-            for (int q = 0; q < UG; q++)
-                dot_chunk(cur[v][q], act_s + (c0 + c + v) * 16, acc16[q], acc4[q], acc1[q]);
+    i2s_rounds<UG>(A, B, wp, nc, act_s + c0 * 16, acc16, acc4, acc1);
     int *red = smem + n_chunks * 16;
 #pragma unroll
     for (int q = 0; q < UG; q++)
         red[(wid * UG + q) * 64 + lane] = (acc16[q] >> 4) + (acc4[q] >> 2) + acc1[q];
     wm_sync_lds();
-    const float act_scale = a.meta->scale;
-    const int asum = a.meta->asum;
     const uint32_t tid = threadIdx.x;
     if (MODE == WM_FUSED_GATEUP) {
         if (tid < 64) {
@@ -332,14 +337,12 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
     if (MODE == WM_FUSED_PLAIN) return;
     // WM_FUSED_ROPE: pairs (j, j + n_rot/2) of this head
     wm_sync_lds();
-    const uint32_t half = a.n_rot / 2;
     float mx = 0.0f;  // |output| maximum, NaN never raising it
-    if ((a.rope_mask >> t) & 1u) {
-        const float *cs = a.rope_cos + (uint64_t)a.pos * half, *sn = a.rope_sin + (uint64_t)a.pos * half;
-        for (uint32_t j = tid; j < half; j += W * 64) {
-            const float cc = cs[j], ss = sn[j];
+    if (rope) {
+        if (tid < half) {
+            const uint32_t j = tid;
             const float x0 = ys[j], x1 = ys[j + half];
-            const float r0 = x0 * cc - x1 * ss, r1 = x0 * ss + x1 * cc;
+            const float r0 = x0 * rc - x1 * rs, r1 = x0 * rs + x1 * rc;
             out[j] = r0;
             out[j + half] = r1;
             mx = wm_max_nonan(wm_max_nonan(mx, fabsf(r0)), fabsf(r1));

@@ -145,12 +145,16 @@ __device__ __forceinline__ float wm_expf(float x) { return wm::expf_glibc(x); }
 // Streaming (non-temporal) 16-byte load for data read exactly once, such as
 // matvec weights: it keeps them from displacing reused lines in the caches.
 typedef unsigned int wm_v4u __attribute__((ext_vector_type(4)));
+// The pointer is taken as global memory: a generic (flat) load would also
+// count against the LDS wait counter, tying every LDS wait to the weights.
+typedef const wm_v4u __attribute__((address_space(1))) wm_global_v4u;
+typedef const uint32_t __attribute__((address_space(1))) wm_global_u32;
 __device__ __forceinline__ uint4 wm_load_stream(const void *p) {
-    const wm_v4u v = __builtin_nontemporal_load(reinterpret_cast<const wm_v4u *>(p));
+    const wm_v4u v = __builtin_nontemporal_load((wm_global_v4u *)p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ uint32_t wm_load_stream_u32(const void *p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
+    return __builtin_nontemporal_load((wm_global_u32 *)p);
 }
 
 // Buffer resource for raw (unformatted) loads from `bytes` bytes at `base`;
