@@ -201,7 +201,9 @@ __global__ __launch_bounds__(64) void k_i2s_partial(i2s_multi m, uint32_t n_chun
         t = lo;
         g = gg - (t ? m.group_end[t - 1] : 0);
     }
-    const uint4 *__restrict__ W = reinterpret_cast<const uint4 *>(m.table ? m.table[t] : m.w[t]);
+    typedef const uint8_t *const __attribute__((address_space(1))) table_entry;  // a global load
+    const uint4 *__restrict__ W =
+        reinterpret_cast<const uint4 *>(m.table ? ((table_entry *)m.table)[t] : m.w[t]);
     const uint32_t split = gridDim.y, s = blockIdx.y;
     const uint32_t c0 = (uint32_t)(((uint64_t)n_chunks * s) / split);
     const uint32_t c1 = (uint32_t)(((uint64_t)n_chunks * (s + 1)) / split);

@@ -25,10 +25,11 @@ constexpr int kNormThreads = 1024;
 
 // Residual source for k_rmsnorm_quant: y_j = (w_scale*act_scale)*(Σ_s partial[s][row0+j] - asum)
 struct residual_src {
-    const int32_t *partial;
+    const int32_t *partial;  // K-split i32 partials of the producing matvec, or
     uint32_t split, rows_total, row0;
     float w_scale;
     const wm_act_meta *meta;
+    const float *y;  // its finished f32 output (then partial is null)
 };
 
 // One workgroup.  x[n] (optionally x += residual first, written back),
@@ -42,7 +43,7 @@ struct residual_src {
 constexpr int kMaxSplit = 16;  // K splits a residual source may carry
 
 // NT threads, values per thread: n <= PER * NT; RES: a residual source is
-// given (res.partial != nullptr).  Only RES kernels hold the partials'
+// given (res.partial or res.y).  Only RES kernels hold the partials'
 // registers, so the others keep their register budget.
 template <int PER, int NT, bool RES>
 __global__ __launch_bounds__(NT) void k_rmsnorm_quant(
@@ -57,9 +58,10 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant(
     __shared__ int red_i[NW], red_nf[NW];
     __shared__ wm::seq_block_scratch seq_scratch;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    float xv[PER], wv[PER];
+    float xv[PER], wv[PER], rv[PER];
     int nonfinite = 0;
     const bool has_res = RES;
+    const bool res_vec = RES && res.y != nullptr;
     // Every load below is issued before any is used (indices clamped to
     // n - 1); out-of-range values are masked after.
 #pragma unroll
@@ -67,8 +69,23 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant(
         const uint32_t j = min(tid + (uint32_t)i * NT, n - 1);
         xv[i] = x[j];
         wv[i] = w[j];
+        rv[i] = res_vec ? res.y[j] : 0.0f;
     }
-    if (has_res) {
+    if (res_vec) {
+        // hidden += wo_out / down as finished f32 vectors; the producing
+        // kernel computed them as (w_scale * act_scale) * (float)dot, the
+        // same value the partial path below forms
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const uint32_t j = tid + (uint32_t)i * NT;
+            const float v = xv[i] + rv[i];
+            xv[i] = v;
+            if (j < n) {
+                x[j] = v;
+                nonfinite |= !isfinite(v);
+            }
+        }
+    } else if (has_res) {
         // hidden += wo_out / down (cached_forward.rs:405-408, :496-500)
         const float combined = res.w_scale * res.meta->scale;
         const int asum = res.meta->asum;
@@ -250,17 +267,18 @@ void wm_launch_debug_seq_sum(const float *a, uint32_t n, float *out, hipStream_t
 
 void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, uint32_t rows_total,
                              uint32_t row0, float w_scale, const wm_act_meta *meta_in,
-                             const float *w, uint32_t n, float eps, uint8_t *act,
-                             wm_act_meta *meta_out, float *y_out, uint32_t *err_flag,
-                             uint32_t layer_tag, void *q6k_prep, uint32_t *clear2, hipStream_t s) {
-    residual_src res{partial, split, rows_total, row0, w_scale, meta_in};
+                             const float *res_y, const float *w, uint32_t n, float eps,
+                             uint8_t *act, wm_act_meta *meta_out, float *y_out,
+                             uint32_t *err_flag, uint32_t layer_tag, void *q6k_prep,
+                             uint32_t *clear2, hipStream_t s) {
+    residual_src res{partial, split, rows_total, row0, w_scale, meta_in, res_y};
     size_t lds = (size_t)wm::seq_sum_padded(n) * sizeof(float);
     const int per = (int)((n + kNormThreads - 1) / kNormThreads);
 #define WM_NORM_CASE(P, R)                                                                         \
     hipLaunchKernelGGL((k_rmsnorm_quant<P, kNormThreads, R>), dim3(1), dim3(kNormThreads), lds, s,  \
                        x, res, w, n, eps, act, meta_out, y_out, err_flag, layer_tag,                \
                        (uint8_t *)q6k_prep, clear2)
-    if (partial) {
+    if (partial || res_y) {
         switch (per) {  // residual sources: the hidden state, n_embd <= 8192
             case 1: WM_NORM_CASE(1, true); break;
             case 2: WM_NORM_CASE(2, true); break;

@@ -7,12 +7,14 @@
 //
 // One decode step is a fixed sequence of kernels on the context's stream:
 //   embed (Q6_K row) ->
-//   per layer: [residual +] attn_norm+quant -> QKV partial dots -> QKV epilogue
-//              (RoPE, KV append) -> scores -> softmax+V -> attn_sub_norm+quant
-//              -> O partial dots -> residual + ffn_norm+quant -> gate/up partial
-//              dots -> relu^2*up -> ffn_sub_norm+quant -> down partial dots
-//   -> residual + output_norm -> lm-head logits + argmax.
-// The residual of each BitLinear is folded into the next norm kernel.
+//   per layer: [residual +] attn_norm+quant -> Q, K, V with RoPE and the K/V
+//              absmax -> scores (new K row appended) -> softmax+V (new V row
+//              appended) -> attn_sub_norm+quant -> O -> residual +
+//              ffn_norm+quant -> gate/up with relu^2*up -> ffn_sub_norm+quant
+//              -> down
+//   -> residual + output_norm -> lm-head argmax (or logits).
+// Every matvec keeps whole rows in one workgroup (its waves split K), so its
+// f32 output is final; the residual add is folded into the next norm kernel.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -23,9 +25,10 @@
 // launchers from k_layer.hip
 void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, uint32_t rows_total,
                              uint32_t row0, float w_scale, const wm_act_meta *meta_in,
-                             const float *w, uint32_t n, float eps, uint8_t *act,
-                             wm_act_meta *meta_out, float *y_out, uint32_t *err_flag,
-                             uint32_t layer_tag, void *q6k_prep, uint32_t *clear2, hipStream_t s);
+                             const float *res_y, const float *w, uint32_t n, float eps,
+                             uint8_t *act, wm_act_meta *meta_out, float *y_out,
+                             uint32_t *err_flag, uint32_t layer_tag, void *q6k_prep,
+                             uint32_t *clear2, hipStream_t s);
 void wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_scales,
                          const int8_t *v_cache, const float *v_scales, float *scores,
                          uint32_t score_stride, float *out, uint32_t n_heads, uint32_t n_kv_heads,
@@ -69,14 +72,12 @@ struct wm_model {
     uint8_t *ws = nullptr;
     float *hidden = nullptr, *q = nullptr, *attn_out = nullptr, *h_ff = nullptr, *final_hidden = nullptr;
     float *k_new = nullptr, *v_new = nullptr;  // this token's K (after RoPE) and V
+    float *proj_out = nullptr;  // O's, then down's f32 output (the next norm adds it to hidden)
     float *logits = nullptr, *scores = nullptr;
     uint8_t *act = nullptr;
     wm_act_meta *meta = nullptr;  // [4]: attn, sub, ffn, ffn_sub
-    int32_t *partial = nullptr;
     uint32_t *dscalars = nullptr;  // [0] token, [1] next token, [2] error flag, [4..5] K/V absmax
     void *lm_work = nullptr;
-    // split choices
-    uint32_t split_o = 1, split_down = 1;
     // ragged-batch workspace, grown on demand to b_cap tokens
     uint8_t *bws = nullptr;
     uint32_t b_cap = 0;
@@ -155,14 +156,14 @@ void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
         const dev_layer &L = m->layers[l];
         // residual of the previous layer's ffn_down, folded into attn_norm
         if (l == 0) {
-            wm_launch_rmsnorm_quant(m->hidden, nullptr, 0, 0, 0, 0.0f, nullptr, L.attn_norm, E,
-                                    c.rms_eps, m->act, &m->meta[0], nullptr, nullptr, 0, nullptr,
+            wm_launch_rmsnorm_quant(m->hidden, nullptr, 0, 0, 0, 0.0f, nullptr, nullptr, L.attn_norm,
+                                    E, c.rms_eps, m->act, &m->meta[0], nullptr, nullptr, 0, nullptr,
                                     kv_absmax, s);
         } else {
-            const dev_layer &P = m->layers[l - 1];
-            wm_launch_rmsnorm_quant(m->hidden, m->partial, m->split_down, P.down.n_groups * 64, 0,
-                                    P.down.scale, &m->meta[3], L.attn_norm, E, c.rms_eps, m->act,
-                                    &m->meta[0], nullptr, m->dscalars + 2, l, nullptr, kv_absmax, s);
+            // hidden += the previous layer's ffn_down
+            wm_launch_rmsnorm_quant(m->hidden, nullptr, 0, 0, 0, 0.0f, nullptr, m->proj_out,
+                                    L.attn_norm, E, c.rms_eps, m->act, &m->meta[0], nullptr,
+                                    m->dscalars + 2, l, nullptr, kv_absmax, s);
             if (layer_trace_dev)
                 hipMemcpyAsync(layer_trace_dev + (size_t)(l - 1) * E, m->hidden, (size_t)E * 4,
                                hipMemcpyDeviceToDevice, s);
@@ -180,31 +181,36 @@ void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
         wm_launch_attention(m->q, kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV, kv->vs + lay,
                             m->scores, c.context_length, m->attn_out, c.n_heads, c.n_kv_heads,
                             c.head_dim, pos + 1, scale, m->k_new, m->v_new, kv_absmax, s);
-        wm_launch_rmsnorm_quant(m->attn_out, nullptr, 0, 0, 0, 0.0f, nullptr, L.attn_sub_norm, E,
-                                c.rms_eps, m->act, &m->meta[1], nullptr, nullptr, 0, nullptr, nullptr, s);
+        wm_launch_rmsnorm_quant(m->attn_out, nullptr, 0, 0, 0, 0.0f, nullptr, nullptr,
+                                L.attn_sub_norm, E, c.rms_eps, m->act, &m->meta[1], nullptr, nullptr,
+                                0, nullptr, nullptr, s);
+        // O: whole rows per workgroup (the K split inside it), finished f32 out
         wm_i2s_desc od = {L.o.w, L.o.n_groups};
-        wm_launch_i2s_partial(&od, 1, n_chunks_e, m->act, m->partial, m->split_o, L.o.n_groups * 64, s);
+        float *o_out[1] = {m->proj_out};
+        wm_launch_i2s_fused(WM_FUSED_PLAIN, &od, &L.o.scale, o_out, 1, n_chunks_e, 1, m->act,
+                            &m->meta[1], nullptr, nullptr, 0, 0, 0, nullptr, nullptr, s);
         // hidden += wo_out, then ffn_norm
-        wm_launch_rmsnorm_quant(m->hidden, m->partial, m->split_o, L.o.n_groups * 64, 0, L.o.scale,
-                                &m->meta[1], L.ffn_norm, E, c.rms_eps, m->act, &m->meta[2], nullptr,
-                                nullptr, 0, nullptr, nullptr, s);
+        wm_launch_rmsnorm_quant(m->hidden, nullptr, 0, 0, 0, 0.0f, nullptr, m->proj_out, L.ffn_norm,
+                                E, c.rms_eps, m->act, &m->meta[2], nullptr, nullptr, 0, nullptr,
+                                nullptr, s);
         // gate and up row groups together, h = relu(gate)^2 * up in the epilogue
         wm_i2s_desc gu[2] = {{L.gate.w, L.gate.n_groups}, {L.up.w, L.up.n_groups}};
         const float gu_scales[2] = {L.gate.scale, L.up.scale};
         float *gu_out[2] = {m->h_ff, nullptr};
         wm_launch_i2s_fused(WM_FUSED_GATEUP, gu, gu_scales, gu_out, 2, n_chunks_e, 1, m->act,
                             &m->meta[2], nullptr, nullptr, 0, 0, 0, nullptr, nullptr, s);
-        wm_launch_rmsnorm_quant(m->h_ff, nullptr, 0, 0, 0, 0.0f, nullptr, L.ffn_sub_norm, F,
-                                c.rms_eps, m->act, &m->meta[3], nullptr, nullptr, 0, nullptr, nullptr, s);
+        wm_launch_rmsnorm_quant(m->h_ff, nullptr, 0, 0, 0, 0.0f, nullptr, nullptr, L.ffn_sub_norm,
+                                F, c.rms_eps, m->act, &m->meta[3], nullptr, nullptr, 0, nullptr,
+                                nullptr, s);
         wm_i2s_desc dd = {L.down.w, L.down.n_groups};
-        wm_launch_i2s_partial(&dd, 1, n_chunks_f, m->act, m->partial, m->split_down,
-                              L.down.n_groups * 64, s);
+        float *d_out[1] = {m->proj_out};
+        wm_launch_i2s_fused(WM_FUSED_PLAIN, &dd, &L.down.scale, d_out, 1, n_chunks_f, 1, m->act,
+                            &m->meta[3], nullptr, nullptr, 0, 0, 0, nullptr, nullptr, s);
     }
     // last residual + output_norm (f32 out, no quantisation)
-    const dev_layer &P = m->layers[c.n_layers - 1];
-    wm_launch_rmsnorm_quant(m->hidden, m->partial, m->split_down, P.down.n_groups * 64, 0,
-                            P.down.scale, &m->meta[3], m->output_norm, E, c.rms_eps, nullptr,
-                            nullptr, m->final_hidden, m->dscalars + 2, c.n_layers,
+    wm_launch_rmsnorm_quant(m->hidden, nullptr, 0, 0, 0, 0.0f, nullptr, m->proj_out,
+                            m->output_norm, E, c.rms_eps, nullptr, nullptr, m->final_hidden,
+                            m->dscalars + 2, c.n_layers,
                             wm_q6k_prep_area(m->lm_work, c.vocab_size, m->embd_blocks), nullptr, s);
     if (layer_trace_dev)
         hipMemcpyAsync(layer_trace_dev + (size_t)(c.n_layers - 1) * E, m->hidden, (size_t)E * 4,
@@ -475,12 +481,6 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
         }
     }
     const uint32_t E = c.n_embd, F = c.n_ff;
-    const uint32_t eg = (E + 63) / 64;
-    m->split_o = wm_i2s_pick_split(eg, E / 64);
-    m->split_down = wm_i2s_pick_split(eg, F / 64);
-    size_t part = 0;
-    part = std::max(part, (size_t)m->split_o * eg * 64);
-    part = std::max(part, (size_t)m->split_down * eg * 64);
     const size_t sizes[] = {
         align256((size_t)E * 4),                                  // hidden
         align256((size_t)E * 4),                                  // q
@@ -488,11 +488,11 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
         align256((size_t)F * 4),                                  // h_ff
         align256((size_t)E * 4),                                  // final_hidden
         align256((size_t)m->kv_dim * 4), align256((size_t)m->kv_dim * 4),  // k_new, v_new
+        align256((size_t)E * 4),                                  // proj_out
         align256((size_t)c.vocab_size * 4),                       // logits
         align256((size_t)c.n_heads * c.context_length * 4),       // scores
         align256((size_t)std::max(E, F)),                         // act
         256,                                                      // meta[4]
-        align256(part * 4),                                       // partial
         256,                                                      // device scalars
         align256(wm_q6k_logits_work_bytes(c.vocab_size, c.n_embd / Q6K_VALUES)),  // lm-head work
         align256(cs.size() * 4), align256(cs.size() * 4),         // rope tables
@@ -507,8 +507,8 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
     uint8_t *p = m->ws;
     void **slots[] = {(void **)&m->hidden, (void **)&m->q, (void **)&m->attn_out, (void **)&m->h_ff,
                       (void **)&m->final_hidden, (void **)&m->k_new, (void **)&m->v_new,
-                      (void **)&m->logits, (void **)&m->scores,
-                      (void **)&m->act, (void **)&m->meta, (void **)&m->partial,
+                      (void **)&m->proj_out, (void **)&m->logits, (void **)&m->scores,
+                      (void **)&m->act, (void **)&m->meta,
                       (void **)&m->dscalars, (void **)&m->lm_work, (void **)&m->rope_cos,
                       (void **)&m->rope_sin};
     for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); i++) {
