@@ -22,6 +22,7 @@
 // Integer sums are exact, so the K-split, lane order and block order do not
 // change the i32 result the reference produces.
 #include "wm_internal.h"
+#include "wm_norm.h"
 
 namespace {
 
@@ -228,14 +229,22 @@ __global__ __launch_bounds__(64) void k_i2s_partial(i2s_multi m, uint32_t n_chun
 }
 
 // --------------------------------------------------------------------------
-// matvec with the K split inside the workgroup, and fused epilogues
+// matvec that starts from its input's RMSNorm, with the K split inside the
+// workgroup, and fused epilogues
 // --------------------------------------------------------------------------
 //
-// One workgroup per unit of UG 64-row groups; its W waves split the chunks
-// of K between them (wave w: chunks [n_chunks*w/W, n_chunks*(w+1)/W)), each
-// computing the unit's rows over its slice exactly as k_i2s_partial does;
-// the W partial dots meet in LDS (exact integers, so the split changes
-// nothing) and the unit's threads finish the rows:
+// One workgroup per unit of UG 64-row groups.  It first issues its weights'
+// first round, then computes the input's RMSNorm and int8 quantisation
+// itself (wm_norm.h, the same operations as k_rmsnorm_quant) straight into
+// LDS while those loads are in flight: every workgroup evaluates the same
+// norm, so their codes agree bit for bit, and the norm costs no launch and
+// no trip through memory.  Workgroup 0 also writes what the norm leaves
+// behind for later kernels (x + y, the codes and their meta, cleared slots).
+// Its W waves then split the chunks of K between them (wave w: chunks
+// [n_chunks*w/W, n_chunks*(w+1)/W)), each computing the unit's rows over its
+// slice exactly as k_i2s_partial does; the W partial dots meet in LDS (exact
+// integers, so the split changes nothing) and the unit's threads finish the
+// rows:
 //   y = (w_scale * act_scale) * (float)(Σ c*a - Σ a)   (bitlinear_sse2.rs:327-339)
 // then, by MODE,
 //   WM_FUSED_PLAIN   y to out[t]
@@ -251,17 +260,17 @@ struct i2s_fused_args {
     uint32_t unit_end[WM_FUSED_MAX_TENSORS];  // cumulative units per tensor
     int n_tensors;
     uint32_t n_chunks;
-    const int *act;
-    const wm_act_meta *meta;
+    wm_fused_norm norm;                // the input's norm (n = n_chunks * 64)
     const float *rope_cos, *rope_sin;  // [pos][n_rot/2]
     uint32_t pos, n_rot, rope_mask;
-    int32_t *dot_out;  // PLAIN: the i32 dots of tensor 0 (nullable)
     uint32_t *absmax;  // ROPE: absmax of the outputs of tensors 1, 2 (float bits, nullable)
 };
 
-template <int MODE, int UG, int W>
+template <int MODE, int UG, int W, int NP>  // NP >= ceil(n / (W * 64)): the norm's terms per thread
 __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
-    extern __shared__ __align__(16) int smem[];  // act [n_chunks*16] | red [W][UG][64] | ys [UG*64]
+    // act [n_chunks*16 ints] | red [W][UG][64] | ys [UG*64] | squares [seq_sum_padded(n)]
+    extern __shared__ __align__(16) int smem[];
+    __shared__ wm::norm_lds<W> nl;
     const uint32_t u = blockIdx.x;
     int t = 0;
 #pragma unroll
@@ -280,27 +289,53 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
         const uint32_t g = MODE == WM_FUSED_GATEUP ? lu : lu * UG + q;
         wp[q] = reinterpret_cast<const uint4 *>(a.w[tq]) + g * gstride + (uint64_t)c0 * I2S_GROUP_ROWS + lane;
     }
+    // loads in this order: the norm's inputs (so that waiting for them waits
+    // for nothing else), the first round of weights, the RoPE factors
+    const wm_fused_norm &nm = a.norm;
+    const uint32_t n = n_chunks * 64;
+    float xv[NP], wv[NP], rv[NP];
+    wm::norm_load<NP, W * 64>(nm.x, nm.y, nm.w, n, xv, wv, rv);
+    __builtin_amdgcn_sched_barrier(0);
     i2s_round<UG> A, B;
     i2s_issue<UG>(A, wp, 0, nc);
-    int *act_s = smem;
-    const int4 *ag = reinterpret_cast<const int4 *>(a.act) + (uint64_t)c0 * 4;
-    for (uint32_t i = lane; i < nc * 4; i += 64) reinterpret_cast<int4 *>(act_s + c0 * 16)[i] = ag[i];
-    // the epilogue's inputs, fetched now rather than after the reduction
-    const float act_scale = a.meta->scale;
-    const int asum = a.meta->asum;
+    __builtin_amdgcn_sched_barrier(0);
+    // the epilogue's RoPE factors, fetched now rather than after the reduction
     const uint32_t half = a.n_rot / 2;  // ROPE: at most 64 <= W * 64 pairs, one per thread
     const bool rope = MODE == WM_FUSED_ROPE && ((a.rope_mask >> t) & 1u);
-    float rc = 0.0f, rs = 0.0f;
+    float rc = 0.0f, rsn = 0.0f;
     if (rope && threadIdx.x < half) {
         rc = a.rope_cos[(uint64_t)a.pos * half + threadIdx.x];
-        rs = a.rope_sin[(uint64_t)a.pos * half + threadIdx.x];
+        rsn = a.rope_sin[(uint64_t)a.pos * half + threadIdx.x];
     }
-    wm_sync_lds();
+    int *act_s = smem;
+    int *red = smem + n_chunks * 16;
+    float *ys = reinterpret_cast<float *>(red + W * UG * 64);
+    float *sq = ys + UG * 64;
+    // the input's norm and int8 codes, into LDS (the weights stay in flight)
+    const bool first = blockIdx.x == 0;
+    float act_scale;
+    int asum;
+    {
+        const float rsq = wm::norm_rsqrt_loaded<NP, W * 64>(
+            nm.y != nullptr, n, nm.eps, first ? nm.x_out : nullptr, first ? nm.err_flag : nullptr,
+            nm.layer_tag, sq, nl, xv, wv, rv);
+        wm::norm_quant<NP, W * 64>(rsq, n, xv, wv, reinterpret_cast<uint8_t *>(act_s), nl,
+                                   act_scale, asum);
+    }
+    if (first) {
+        if (nm.act_out)
+            for (uint32_t i = threadIdx.x; i < n / 16; i += W * 64)
+                reinterpret_cast<int4 *>(nm.act_out)[i] = reinterpret_cast<const int4 *>(act_s)[i];
+        if (threadIdx.x == 0 && nm.meta_out) {
+            nm.meta_out->scale = act_scale;
+            nm.meta_out->asum = asum;
+        }
+        if (nm.clear2 && threadIdx.x < 2) nm.clear2[threadIdx.x] = 0;
+    }
     int acc16[UG], acc4[UG], acc1[UG];
 #pragma unroll
     for (int q = 0; q < UG; q++) acc16[q] = acc4[q] = acc1[q] = 0;
     i2s_rounds<UG>(A, B, wp, nc, act_s + c0 * 16, acc16, acc4, acc1);
-    int *red = smem + n_chunks * 16;
 #pragma unroll
     for (int q = 0; q < UG; q++)
         red[(wid * UG + q) * 64 + lane] = (acc16[q] >> 4) + (acc4[q] >> 2) + acc1[q];
@@ -322,7 +357,6 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
         return;
     }
     float *out = a.out[t] + (uint64_t)lu * UG * 64;
-    float *ys = reinterpret_cast<float *>(red + W * UG * 64);
     for (uint32_t row = tid; row < UG * 64; row += W * 64) {
         const uint32_t q = row >> 6, rr = row & 63;
         int dot = -asum;
@@ -331,7 +365,6 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
         const float y = (a.w_scale[t] * act_scale) * (float)dot;
         if (MODE == WM_FUSED_PLAIN) {
             out[row] = y;
-            if (a.dot_out && t == 0) a.dot_out[(uint64_t)lu * UG * 64 + row] = dot;
         } else {
             ys[row] = y;
         }
@@ -344,7 +377,7 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
         if (tid < half) {
             const uint32_t j = tid;
             const float x0 = ys[j], x1 = ys[j + half];
-            const float r0 = x0 * rc - x1 * rs, r1 = x0 * rs + x1 * rc;
+            const float r0 = x0 * rc - x1 * rsn, r1 = x0 * rsn + x1 * rc;
             out[j] = r0;
             out[j + half] = r1;
             mx = wm_max_nonan(wm_max_nonan(mx, fabsf(r0)), fabsf(r1));
@@ -481,9 +514,9 @@ void wm_launch_i2s_finalize(const int32_t *partial, uint32_t split, uint32_t row
 // Waves per workgroup: n_chunks / 4 (one 4-chunk round each), at most 16.
 void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scales, float *const *outs,
                          int n_tensors, uint32_t n_chunks, uint32_t groups_per_unit,
-                         const uint8_t *act, const wm_act_meta *meta, const float *rope_cos,
-                         const float *rope_sin, uint32_t pos, uint32_t n_rot, uint32_t rope_mask,
-                         int32_t *dot_out, uint32_t *absmax, hipStream_t s) {
+                         const wm_fused_norm &norm, const float *rope_cos, const float *rope_sin,
+                         uint32_t pos, uint32_t n_rot, uint32_t rope_mask, uint32_t *absmax,
+                         hipStream_t s) {
     i2s_fused_args a{};
     uint32_t acc = 0;
     a.n_tensors = n_tensors;
@@ -500,31 +533,37 @@ void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
     }
     if (mode == WM_FUSED_GATEUP) a.n_tensors = 1;  // units all belong to the pair
     a.n_chunks = n_chunks;
-    a.act = reinterpret_cast<const int *>(act);
-    a.meta = meta;
+    a.norm = norm;
     a.rope_cos = rope_cos;
     a.rope_sin = rope_sin;
     a.pos = pos;
     a.n_rot = n_rot;
     a.rope_mask = rope_mask;
-    a.dot_out = dot_out;
     a.absmax = absmax;
-    int w = (int)(n_chunks / 4);
-    w = w < 1 ? 1 : (w > 16 ? 16 : w);
-#define WM_FUSED_CASE(MODE, UG, W)                                                                 \
-    if (w == W) {                                                                                  \
-        const size_t lds = (size_t)n_chunks * 64 + (size_t)W * UG * 64 * 4 + (size_t)UG * 64 * 4;  \
-        hipLaunchKernelGGL((k_i2s_fused<MODE, UG, W>), dim3(acc), dim3(W * 64), lds, s, a);        \
-        return;                                                                                    \
-    }
-#define WM_FUSED_WS(MODE, UG)                                                                      \
-    WM_FUSED_CASE(MODE, UG, 1) WM_FUSED_CASE(MODE, UG, 2) WM_FUSED_CASE(MODE, UG, 4)               \
-    WM_FUSED_CASE(MODE, UG, 6) WM_FUSED_CASE(MODE, UG, 8) WM_FUSED_CASE(MODE, UG, 10)              \
-    WM_FUSED_CASE(MODE, UG, 12) WM_FUSED_CASE(MODE, UG, 16)
-    // round the wave count down to an instantiated one
+    // Waves: as many as the chunks allow, up to 16 (the norm at the start is
+    // latency-bound and runs best on the widest workgroup; each wave still
+    // has its own chunks), rounded down to an instantiated count.
+    int w = (int)(n_chunks < 16 ? n_chunks : 16);
     static const int kWs[] = {16, 12, 10, 8, 6, 4, 2, 1};
     for (int x : kWs)
         if (w >= x) { w = x; break; }
+    // the norm's terms per thread, rounded up to an instantiated bound: at
+    // most 2 below 16 waves, at most 16 with 16 (n_chunks <= 256)
+    const uint32_t per = (n_chunks + (uint32_t)w - 1) / (uint32_t)w;
+    const int np = per <= 4 ? 4 : (per <= 8 ? 8 : 16);
+    const size_t sq_bytes = (size_t)wm::seq_sum_padded(n_chunks * 64) * 4;
+#define WM_FUSED_CASE(MODE, UG, W, NP)                                                             \
+    if (w == W && np == NP) {                                                                      \
+        const size_t lds = (size_t)n_chunks * 64 + (size_t)W * UG * 64 * 4 + (size_t)UG * 64 * 4 + \
+                           sq_bytes;                                                               \
+        hipLaunchKernelGGL((k_i2s_fused<MODE, UG, W, NP>), dim3(acc), dim3(W * 64), lds, s, a);    \
+        return;                                                                                    \
+    }
+#define WM_FUSED_WS(MODE, UG)                                                                      \
+    WM_FUSED_CASE(MODE, UG, 1, 4) WM_FUSED_CASE(MODE, UG, 2, 4) WM_FUSED_CASE(MODE, UG, 4, 4)      \
+    WM_FUSED_CASE(MODE, UG, 6, 4) WM_FUSED_CASE(MODE, UG, 8, 4) WM_FUSED_CASE(MODE, UG, 10, 4)     \
+    WM_FUSED_CASE(MODE, UG, 12, 4) WM_FUSED_CASE(MODE, UG, 16, 4) WM_FUSED_CASE(MODE, UG, 16, 8)   \
+    WM_FUSED_CASE(MODE, UG, 16, 16)
     if (mode == WM_FUSED_PLAIN) { WM_FUSED_WS(WM_FUSED_PLAIN, 1) }
     else if (mode == WM_FUSED_GATEUP) { WM_FUSED_WS(WM_FUSED_GATEUP, 2) }
     else if (groups_per_unit == 2) { WM_FUSED_WS(WM_FUSED_ROPE, 2) }

@@ -23,9 +23,7 @@
 #include "wm_internal.h"
 
 // launchers from k_layer.hip
-void wm_launch_rmsnorm_quant(float *x, const int32_t *partial, uint32_t split, uint32_t rows_total,
-                             uint32_t row0, float w_scale, const wm_act_meta *meta_in,
-                             const float *res_y, const float *w, uint32_t n, float eps,
+void wm_launch_rmsnorm_quant(float *x, const float *res_y, const float *w, uint32_t n, float eps,
                              uint8_t *act, wm_act_meta *meta_out, float *y_out,
                              uint32_t *err_flag, uint32_t layer_tag, void *q6k_prep,
                              uint32_t *clear2, hipStream_t s);
@@ -70,12 +68,11 @@ struct wm_model {
     float *rope_cos = nullptr, *rope_sin = nullptr;
     // workspace
     uint8_t *ws = nullptr;
-    float *hidden = nullptr, *q = nullptr, *attn_out = nullptr, *h_ff = nullptr, *final_hidden = nullptr;
+    float *hidden = nullptr, *hidden2 = nullptr;  // the residual stream, in two buffers
+    float *q = nullptr, *attn_out = nullptr, *h_ff = nullptr, *final_hidden = nullptr;
     float *k_new = nullptr, *v_new = nullptr;  // this token's K (after RoPE) and V
     float *proj_out = nullptr;  // O's, then down's f32 output (the next norm adds it to hidden)
     float *logits = nullptr, *scores = nullptr;
-    uint8_t *act = nullptr;
-    wm_act_meta *meta = nullptr;  // [4]: attn, sub, ffn, ffn_sub
     uint32_t *dscalars = nullptr;  // [0] token, [1] next token, [2] error flag, [4..5] K/V absmax
     void *lm_work = nullptr;
     // ragged-batch workspace, grown on demand to b_cap tokens
@@ -147,73 +144,83 @@ void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
     hipStream_t s = m->ctx->stream;
     const uint32_t E = c.n_embd, F = c.n_ff, KV = m->kv_dim;
     const uint32_t n_chunks_e = E / I2S_CHUNK_COLS, n_chunks_f = F / I2S_CHUNK_COLS;
-    wm_launch_q6k_dequant_row_dev(m->embd, m->embd_blocks, m->dscalars, m->hidden, s);
+    // The residual stream lives in two buffers: a norm that adds a matvec's
+    // output reads one and writes the sum to the other (in one workgroup,
+    // while the launch's other workgroups still read the first).
+    float *H[2] = {m->hidden, m->hidden2};
+    int cur = 0;
+    wm_launch_q6k_dequant_row_dev(m->embd, m->embd_blocks, m->dscalars, H[0], s);
     const float scale = 1.0f / sqrtf((float)c.head_dim);  // primitives.rs:354
-    // absmax of this token's K and V (float bits): cleared by attn_norm,
-    // raised by the QKV matvec, read by attention
+    // absmax of this token's K and V (float bits): zero at creation and after
+    // every O launch, raised by the QKV launch, read by attention
     uint32_t *kv_absmax = m->dscalars + 4;
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const dev_layer &L = m->layers[l];
-        // residual of the previous layer's ffn_down, folded into attn_norm
-        if (l == 0) {
-            wm_launch_rmsnorm_quant(m->hidden, nullptr, 0, 0, 0, 0.0f, nullptr, nullptr, L.attn_norm,
-                                    E, c.rms_eps, m->act, &m->meta[0], nullptr, nullptr, 0, nullptr,
-                                    kv_absmax, s);
-        } else {
-            // hidden += the previous layer's ffn_down
-            wm_launch_rmsnorm_quant(m->hidden, nullptr, 0, 0, 0, 0.0f, nullptr, m->proj_out,
-                                    L.attn_norm, E, c.rms_eps, m->act, &m->meta[0], nullptr,
-                                    m->dscalars + 2, l, nullptr, kv_absmax, s);
-            if (layer_trace_dev)
-                hipMemcpyAsync(layer_trace_dev + (size_t)(l - 1) * E, m->hidden, (size_t)E * 4,
-                               hipMemcpyDeviceToDevice, s);
+        // attn_norm, on hidden + the previous layer's ffn_down, then Q, K, V
+        // (whole heads per workgroup, NEOX RoPE on Q and K at `pos`)
+        wm_fused_norm an{};
+        an.x = H[cur];
+        an.w = L.attn_norm;
+        an.eps = c.rms_eps;
+        if (l > 0) {
+            an.y = m->proj_out;
+            an.x_out = H[cur ^ 1];
+            an.err_flag = m->dscalars + 2;
+            an.layer_tag = l;
+            cur ^= 1;
         }
-        // Q, K, V: one launch over the three tensors sharing the quantised
-        // input, whole heads per workgroup, NEOX RoPE on Q and K at `pos`
         wm_i2s_desc qkv[3] = {{L.q.w, L.q.n_groups}, {L.k.w, L.k.n_groups}, {L.v.w, L.v.n_groups}};
         const float qkv_scales[3] = {L.q.scale, L.k.scale, L.v.scale};
         float *qkv_out[3] = {m->q, m->k_new, m->v_new};
         wm_launch_i2s_fused(WM_FUSED_ROPE, qkv, qkv_scales, qkv_out, 3, n_chunks_e, c.head_dim / 64,
-                            m->act, &m->meta[0], m->rope_cos, m->rope_sin, pos, c.n_rot, 0x3u,
-                            nullptr, kv_absmax, s);
+                            an, m->rope_cos, m->rope_sin, pos, c.n_rot, 0x3u, kv_absmax, s);
+        if (layer_trace_dev && l > 0)
+            hipMemcpyAsync(layer_trace_dev + (size_t)(l - 1) * E, H[cur], (size_t)E * 4,
+                           hipMemcpyDeviceToDevice, s);
         // attention; this token's K/V row goes into the cache on the way
         const size_t lay = (size_t)l * kv->max_seq;
         wm_launch_attention(m->q, kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV, kv->vs + lay,
                             m->scores, c.context_length, m->attn_out, c.n_heads, c.n_kv_heads,
                             c.head_dim, pos + 1, scale, m->k_new, m->v_new, kv_absmax, s);
-        wm_launch_rmsnorm_quant(m->attn_out, nullptr, 0, 0, 0, 0.0f, nullptr, nullptr,
-                                L.attn_sub_norm, E, c.rms_eps, m->act, &m->meta[1], nullptr, nullptr,
-                                0, nullptr, nullptr, s);
-        // O: whole rows per workgroup (the K split inside it), finished f32 out
+        // attn_sub_norm, then O (the launch also clears the K/V absmax slots)
+        wm_fused_norm sn{};
+        sn.x = m->attn_out;
+        sn.w = L.attn_sub_norm;
+        sn.eps = c.rms_eps;
+        sn.clear2 = kv_absmax;
         wm_i2s_desc od = {L.o.w, L.o.n_groups};
         float *o_out[1] = {m->proj_out};
-        wm_launch_i2s_fused(WM_FUSED_PLAIN, &od, &L.o.scale, o_out, 1, n_chunks_e, 1, m->act,
-                            &m->meta[1], nullptr, nullptr, 0, 0, 0, nullptr, nullptr, s);
-        // hidden += wo_out, then ffn_norm
-        wm_launch_rmsnorm_quant(m->hidden, nullptr, 0, 0, 0, 0.0f, nullptr, m->proj_out, L.ffn_norm,
-                                E, c.rms_eps, m->act, &m->meta[2], nullptr, nullptr, 0, nullptr,
-                                nullptr, s);
-        // gate and up row groups together, h = relu(gate)^2 * up in the epilogue
+        wm_launch_i2s_fused(WM_FUSED_PLAIN, &od, &L.o.scale, o_out, 1, n_chunks_e, 1, sn, nullptr,
+                            nullptr, 0, 0, 0, nullptr, s);
+        // ffn_norm on hidden + wo_out, then gate and up (relu^2 * up)
+        wm_fused_norm fn{};
+        fn.x = H[cur];
+        fn.y = m->proj_out;
+        fn.x_out = H[cur ^ 1];
+        fn.w = L.ffn_norm;
+        fn.eps = c.rms_eps;
+        cur ^= 1;
         wm_i2s_desc gu[2] = {{L.gate.w, L.gate.n_groups}, {L.up.w, L.up.n_groups}};
         const float gu_scales[2] = {L.gate.scale, L.up.scale};
         float *gu_out[2] = {m->h_ff, nullptr};
-        wm_launch_i2s_fused(WM_FUSED_GATEUP, gu, gu_scales, gu_out, 2, n_chunks_e, 1, m->act,
-                            &m->meta[2], nullptr, nullptr, 0, 0, 0, nullptr, nullptr, s);
-        wm_launch_rmsnorm_quant(m->h_ff, nullptr, 0, 0, 0, 0.0f, nullptr, nullptr, L.ffn_sub_norm,
-                                F, c.rms_eps, m->act, &m->meta[3], nullptr, nullptr, 0, nullptr,
-                                nullptr, s);
+        wm_launch_i2s_fused(WM_FUSED_GATEUP, gu, gu_scales, gu_out, 2, n_chunks_e, 1, fn, nullptr,
+                            nullptr, 0, 0, 0, nullptr, s);
+        // ffn_sub_norm, then down
+        wm_fused_norm dn{};
+        dn.x = m->h_ff;
+        dn.w = L.ffn_sub_norm;
+        dn.eps = c.rms_eps;
         wm_i2s_desc dd = {L.down.w, L.down.n_groups};
         float *d_out[1] = {m->proj_out};
-        wm_launch_i2s_fused(WM_FUSED_PLAIN, &dd, &L.down.scale, d_out, 1, n_chunks_f, 1, m->act,
-                            &m->meta[3], nullptr, nullptr, 0, 0, 0, nullptr, nullptr, s);
+        wm_launch_i2s_fused(WM_FUSED_PLAIN, &dd, &L.down.scale, d_out, 1, n_chunks_f, 1, dn, nullptr,
+                            nullptr, 0, 0, 0, nullptr, s);
     }
     // last residual + output_norm (f32 out, no quantisation)
-    wm_launch_rmsnorm_quant(m->hidden, nullptr, 0, 0, 0, 0.0f, nullptr, m->proj_out,
-                            m->output_norm, E, c.rms_eps, nullptr, nullptr, m->final_hidden,
-                            m->dscalars + 2, c.n_layers,
+    wm_launch_rmsnorm_quant(H[cur], m->proj_out, m->output_norm, E, c.rms_eps, nullptr, nullptr,
+                            m->final_hidden, m->dscalars + 2, c.n_layers,
                             wm_q6k_prep_area(m->lm_work, c.vocab_size, m->embd_blocks), nullptr, s);
     if (layer_trace_dev)
-        hipMemcpyAsync(layer_trace_dev + (size_t)(c.n_layers - 1) * E, m->hidden, (size_t)E * 4,
+        hipMemcpyAsync(layer_trace_dev + (size_t)(c.n_layers - 1) * E, H[cur], (size_t)E * 4,
                        hipMemcpyDeviceToDevice, s);
 }
 
@@ -482,7 +489,7 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
     }
     const uint32_t E = c.n_embd, F = c.n_ff;
     const size_t sizes[] = {
-        align256((size_t)E * 4),                                  // hidden
+        align256((size_t)E * 4), align256((size_t)E * 4),         // hidden, hidden2
         align256((size_t)E * 4),                                  // q
         align256((size_t)E * 4),                                  // attn_out
         align256((size_t)F * 4),                                  // h_ff
@@ -491,8 +498,6 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
         align256((size_t)E * 4),                                  // proj_out
         align256((size_t)c.vocab_size * 4),                       // logits
         align256((size_t)c.n_heads * c.context_length * 4),       // scores
-        align256((size_t)std::max(E, F)),                         // act
-        256,                                                      // meta[4]
         256,                                                      // device scalars
         align256(wm_q6k_logits_work_bytes(c.vocab_size, c.n_embd / Q6K_VALUES)),  // lm-head work
         align256(cs.size() * 4), align256(cs.size() * 4),         // rope tables
@@ -505,12 +510,13 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
         return wm_hip_error(ctx, e, "wm_model_create workspace");
     }
     uint8_t *p = m->ws;
-    void **slots[] = {(void **)&m->hidden, (void **)&m->q, (void **)&m->attn_out, (void **)&m->h_ff,
-                      (void **)&m->final_hidden, (void **)&m->k_new, (void **)&m->v_new,
-                      (void **)&m->proj_out, (void **)&m->logits, (void **)&m->scores,
-                      (void **)&m->act, (void **)&m->meta,
-                      (void **)&m->dscalars, (void **)&m->lm_work, (void **)&m->rope_cos,
-                      (void **)&m->rope_sin};
+    void **slots[] = {(void **)&m->hidden,   (void **)&m->hidden2,  (void **)&m->q,
+                      (void **)&m->attn_out, (void **)&m->h_ff,     (void **)&m->final_hidden,
+                      (void **)&m->k_new,    (void **)&m->v_new,    (void **)&m->proj_out,
+                      (void **)&m->logits,   (void **)&m->scores,   (void **)&m->dscalars,
+                      (void **)&m->lm_work,  (void **)&m->rope_cos, (void **)&m->rope_sin};
+    static_assert(sizeof(slots) / sizeof(slots[0]) == sizeof(sizes) / sizeof(sizes[0]),
+                  "one slot per workspace size");
     for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); i++) {
         *slots[i] = p;
         p += sizes[i];

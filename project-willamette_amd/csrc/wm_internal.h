@@ -341,14 +341,29 @@ struct wm_i2s_desc {
     const uint8_t *w;  // library layout
     uint32_t n_groups;
 };
-// Matvec with the K split inside each workgroup and a fused epilogue (mode
-// WM_FUSED_*): rows of tensor i go to outs[i] as f32; see k_i2s_fused.
-// groups_per_unit: 1, or head_dim / 64 for WM_FUSED_ROPE.
+// The RMSNorm a fused matvec starts from (see k_i2s_fused); its length is
+// the matvec's in_dim.
+struct wm_fused_norm {
+    const float *x;         // the norm's input
+    const float *y;         // nullable: residual, the norm runs on x + y
+    float *x_out;           // nullable: x + y written here (by one workgroup; never x itself)
+    const float *w;         // norm weight
+    float eps;
+    uint32_t *err_flag;     // nullable: set to layer_tag when x + y is not all finite
+    uint32_t layer_tag;
+    uint8_t *act_out;       // nullable: a copy of the int8 codes (permuted layout)
+    wm_act_meta *meta_out;  // nullable: their scale and sum
+    uint32_t *clear2;       // nullable: two slots zeroed
+};
+// Matvec that starts from its input's norm, with the K split inside each
+// workgroup and a fused epilogue (mode WM_FUSED_*): rows of tensor i go to
+// outs[i] as f32; see k_i2s_fused.  groups_per_unit: 1, or head_dim / 64
+// for WM_FUSED_ROPE.
 void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scales, float *const *outs,
                          int n_tensors, uint32_t n_chunks, uint32_t groups_per_unit,
-                         const uint8_t *act, const wm_act_meta *meta, const float *rope_cos,
-                         const float *rope_sin, uint32_t pos, uint32_t n_rot, uint32_t rope_mask,
-                         int32_t *dot_out, uint32_t *absmax, hipStream_t s);
+                         const wm_fused_norm &norm, const float *rope_cos, const float *rope_sin,
+                         uint32_t pos, uint32_t n_rot, uint32_t rope_mask, uint32_t *absmax,
+                         hipStream_t s);
 void wm_launch_i2s_partial_table(const uint8_t *const *table, uint32_t n_tensors,
                                  uint32_t groups_per, uint32_t n_chunks, const uint8_t *act,
                                  int32_t *partial, uint32_t split, uint32_t rows_total,
