@@ -289,12 +289,21 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
         const uint32_t g = MODE == WM_FUSED_GATEUP ? lu : lu * UG + q;
         wp[q] = reinterpret_cast<const uint4 *>(a.w[tq]) + g * gstride + (uint64_t)c0 * I2S_GROUP_ROWS + lane;
     }
-    // loads in this order: the norm's inputs (so that waiting for them waits
-    // for nothing else), the first round of weights, the RoPE factors
+    int *act_s = smem;
+    int *red = smem + n_chunks * 16;
+    float *ys = reinterpret_cast<float *>(red + W * UG * 64);
+    float *sq = ys + UG * 64;
+    // The norm's inputs first, alone: they come back quickly while nothing
+    // else is queued (every workgroup's weight loads would otherwise be ahead
+    // of them in the memory system); then the first round of weights, in
+    // flight during the exact sum.
     const wm_fused_norm &nm = a.norm;
     const uint32_t n = n_chunks * 64;
+    const bool first = blockIdx.x == 0;
     float xv[NP], wv[NP], rv[NP];
     wm::norm_load<NP, W * 64>(nm.x, nm.y, nm.w, n, xv, wv, rv);
+    const bool nonfinite =
+        wm::norm_prep<NP, W * 64>(nm.y != nullptr, n, first ? nm.x_out : nullptr, sq, xv, wv, rv);
     __builtin_amdgcn_sched_barrier(0);
     i2s_round<UG> A, B;
     i2s_issue<UG>(A, wp, 0, nc);
@@ -307,18 +316,13 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
         rc = a.rope_cos[(uint64_t)a.pos * half + threadIdx.x];
         rsn = a.rope_sin[(uint64_t)a.pos * half + threadIdx.x];
     }
-    int *act_s = smem;
-    int *red = smem + n_chunks * 16;
-    float *ys = reinterpret_cast<float *>(red + W * UG * 64);
-    float *sq = ys + UG * 64;
     // the input's norm and int8 codes, into LDS (the weights stay in flight)
-    const bool first = blockIdx.x == 0;
     float act_scale;
     int asum;
     {
-        const float rsq = wm::norm_rsqrt_loaded<NP, W * 64>(
-            nm.y != nullptr, n, nm.eps, first ? nm.x_out : nullptr, first ? nm.err_flag : nullptr,
-            nm.layer_tag, sq, nl, xv, wv, rv);
+        const float rsq = wm::norm_sum_rsqrt<NP, W * 64>(nonfinite, n, nm.eps,
+                                                         first ? nm.err_flag : nullptr,
+                                                         nm.layer_tag, sq, nl);
         wm::norm_quant<NP, W * 64>(rsq, n, xv, wv, reinterpret_cast<uint8_t *>(act_s), nl,
                                    act_scale, asum);
     }

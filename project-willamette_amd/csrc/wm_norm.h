@@ -41,19 +41,14 @@ __device__ __forceinline__ void norm_load(const float *x, const float *__restric
 }
 
 // From the loaded values: x + y (hidden += the producing matvec's output,
-// when has_y), written back to x_out when given; Σx² exactly, in order
-// (primitives.rs:243-246); returns 1/sqrt(Σx²/n + eps).  Thread t then holds
-// element j = t + i*NT in xv[i] and its weight in wv[i] (0 past n).
-// err_flag (nullable, with y): set to layer_tag when x + y is not all finite
-// and the flag is still clear.
+// when has_y), written back to x_out when given, and the squares into sq.
+// Thread t then holds element j = t + i*NT in xv[i] and its weight in wv[i]
+// (0 past n).  Returns whether any of its x + y is not finite.
 template <int PER, int NT>
-__device__ __forceinline__ float norm_rsqrt_loaded(bool has_y, uint32_t n, float eps, float *x_out,
-                                                   uint32_t *err_flag, uint32_t layer_tag,
-                                                   float *sq, norm_lds<NT / 64> &L,
-                                                   float (&xv)[PER], float (&wv)[PER],
-                                                   const float (&rv)[PER]) {
-    constexpr int NW = NT / 64;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+__device__ __forceinline__ bool norm_prep(bool has_y, uint32_t n, float *x_out, float *sq,
+                                          float (&xv)[PER], float (&wv)[PER],
+                                          const float (&rv)[PER]) {
+    const uint32_t tid = threadIdx.x;
     int nonfinite = 0;
     if (has_y) {
 #pragma unroll
@@ -77,7 +72,19 @@ __device__ __forceinline__ float norm_rsqrt_loaded(bool has_y, uint32_t n, float
             wv[i] = 0.0f;
         }
     }
-    if (err_flag && lane == 0) L.red_nf[wid] = __builtin_amdgcn_ballot_w64(nonfinite != 0) != 0;
+    return nonfinite != 0;
+}
+
+// After norm_prep: Σx² exactly, in order (primitives.rs:243-246); returns
+// 1/sqrt(Σx²/n + eps).  err_flag (nullable): set to layer_tag when some
+// thread's x + y was not finite and the flag is still clear.
+template <int PER, int NT>
+__device__ __forceinline__ float norm_sum_rsqrt(bool nonfinite, uint32_t n, float eps,
+                                                uint32_t *err_flag, uint32_t layer_tag,
+                                                float *sq, norm_lds<NT / 64> &L) {
+    constexpr int NW = NT / 64;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    if (err_flag && lane == 0) L.red_nf[wid] = __builtin_amdgcn_ballot_w64(nonfinite) != 0;
     wm_sync_lds();
     float v2[PER];
     {
@@ -97,8 +104,8 @@ __device__ __forceinline__ float norm_rsqrt_loaded(bool has_y, uint32_t n, float
     return 1.0f / sqrtf(mean + eps);
 }
 
-// norm_load then norm_rsqrt_loaded (x may be x_out itself: every load is
-// issued before any store).
+// norm_load, norm_prep and norm_sum_rsqrt in one (x may be x_out itself:
+// every load is issued before any store).
 template <int PER, int NT>
 __device__ __forceinline__ float norm_rsqrt(const float *x, const float *__restrict__ y,
                                             const float *__restrict__ w, uint32_t n, float eps,
@@ -107,8 +114,8 @@ __device__ __forceinline__ float norm_rsqrt(const float *x, const float *__restr
                                             float (&wv)[PER]) {
     float rv[PER];
     norm_load<PER, NT>(x, y, w, n, xv, wv, rv);
-    return norm_rsqrt_loaded<PER, NT>(y != nullptr, n, eps, x_out, err_flag, layer_tag, sq, L, xv,
-                                      wv, rv);
+    const bool nf = norm_prep<PER, NT>(y != nullptr, n, x_out, sq, xv, wv, rv);
+    return norm_sum_rsqrt<PER, NT>(nf, n, eps, err_flag, layer_tag, sq, L);
 }
 
 // y = x * rsqrt * w (primitives.rs:249-252) into xv, then the absmax int8
