@@ -302,8 +302,7 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
     const bool first = blockIdx.x == 0;
     float xv[NP], wv[NP], rv[NP];
     wm::norm_load<NP, W * 64>(nm.x, nm.y, nm.w, n, xv, wv, rv);
-    const bool nonfinite =
-        wm::norm_prep<NP, W * 64>(nm.y != nullptr, n, first ? nm.x_out : nullptr, sq, xv, wv, rv);
+    wm::norm_prep<NP, W * 64>(nm.y != nullptr, n, nullptr, sq, xv, wv, rv);
     __builtin_amdgcn_sched_barrier(0);
     i2s_round<UG> A, B;
     i2s_issue<UG>(A, wp, 0, nc);
@@ -316,26 +315,41 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
         rc = a.rope_cos[(uint64_t)a.pos * half + threadIdx.x];
         rsn = a.rope_sin[(uint64_t)a.pos * half + threadIdx.x];
     }
-    // the input's norm and int8 codes, into LDS (the weights stay in flight)
+    // the input's norm and int8 codes, into LDS (the weights stay in flight;
+    // no global memory access until the dots, so no wait the compiler places
+    // for one can wait on the weights)
     float act_scale;
     int asum;
     {
-        const float rsq = wm::norm_sum_rsqrt<NP, W * 64>(nonfinite, n, nm.eps,
-                                                         first ? nm.err_flag : nullptr,
-                                                         nm.layer_tag, sq, nl);
+        const float rsq = wm::norm_sum_rsqrt<NP, W * 64>(false, n, nm.eps, nullptr, 0, sq, nl);
         wm::norm_quant<NP, W * 64>(rsq, n, xv, wv, reinterpret_cast<uint8_t *>(act_s), nl,
                                    act_scale, asum);
     }
-    if (first) {
+    // What the norm leaves for later kernels, written by workgroup 0 once its
+    // own work is done: x + y (the same f32 adds as above) with the
+    // non-finite check, the codes and their meta, the cleared slots.
+    auto finish = [&]() {
+        if (!first) return;
+        const uint32_t tid0 = threadIdx.x;
         if (nm.act_out)
-            for (uint32_t i = threadIdx.x; i < n / 16; i += W * 64)
+            for (uint32_t i = tid0; i < n / 16; i += W * 64)
                 reinterpret_cast<int4 *>(nm.act_out)[i] = reinterpret_cast<const int4 *>(act_s)[i];
-        if (threadIdx.x == 0 && nm.meta_out) {
+        if (tid0 == 0 && nm.meta_out) {
             nm.meta_out->scale = act_scale;
             nm.meta_out->asum = asum;
         }
-        if (nm.clear2 && threadIdx.x < 2) nm.clear2[threadIdx.x] = 0;
-    }
+        if (nm.clear2 && tid0 < 2) nm.clear2[tid0] = 0;
+        if (nm.x_out && nm.y) {
+            int nonfinite = 0;
+            for (uint32_t j = tid0; j < n; j += W * 64) {
+                const float v = nm.x[j] + nm.y[j];
+                nm.x_out[j] = v;
+                nonfinite |= !isfinite(v);
+            }
+            if (nm.err_flag && __syncthreads_or(nonfinite) && tid0 == 0 && *nm.err_flag == 0)
+                *nm.err_flag = nm.layer_tag;
+        }
+    };
     int acc16[UG], acc4[UG], acc1[UG];
 #pragma unroll
     for (int q = 0; q < UG; q++) acc16[q] = acc4[q] = acc1[q] = 0;
@@ -358,6 +372,7 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
             const float r = g > 0.0f ? g : 0.0f;
             a.out[0][lu * 64 + tid] = (r * r) * up;
         }
+        finish();
         return;
     }
     float *out = a.out[t] + (uint64_t)lu * UG * 64;
@@ -373,7 +388,10 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
             ys[row] = y;
         }
     }
-    if (MODE == WM_FUSED_PLAIN) return;
+    if (MODE == WM_FUSED_PLAIN) {
+        finish();
+        return;
+    }
     // WM_FUSED_ROPE: pairs (j, j + n_rot/2) of this head
     wm_sync_lds();
     float mx = 0.0f;  // |output| maximum, NaN never raising it
@@ -403,6 +421,7 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
         mx = wm_wave_max_nonneg(mx);
         if (lane == 0) atomicMax(a.absmax + (t - 1), __float_as_uint(mx));
     }
+    finish();
 }
 
 __global__ void k_i2s_finalize(const int32_t *__restrict__ partial, uint32_t split,
@@ -551,10 +570,11 @@ void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
     static const int kWs[] = {16, 12, 10, 8, 6, 4, 2, 1};
     for (int x : kWs)
         if (w >= x) { w = x; break; }
-    // the norm's terms per thread, rounded up to an instantiated bound: at
-    // most 2 below 16 waves, at most 16 with 16 (n_chunks <= 256)
+    // the norm's terms per thread, rounded up to an instantiated bound (the
+    // exact sum's work grows with the bound): at most 2 below 16 waves, at
+    // most 16 with 16 (n_chunks <= 256)
     const uint32_t per = (n_chunks + (uint32_t)w - 1) / (uint32_t)w;
-    const int np = per <= 4 ? 4 : (per <= 8 ? 8 : 16);
+    const int np = (per <= 3 && w == 16) ? 3 : (per <= 4 ? 4 : (per <= 8 ? 8 : 16));
     const size_t sq_bytes = (size_t)wm::seq_sum_padded(n_chunks * 64) * 4;
 #define WM_FUSED_CASE(MODE, UG, W, NP)                                                             \
     if (w == W && np == NP) {                                                                      \
@@ -566,8 +586,8 @@ void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
 #define WM_FUSED_WS(MODE, UG)                                                                      \
     WM_FUSED_CASE(MODE, UG, 1, 4) WM_FUSED_CASE(MODE, UG, 2, 4) WM_FUSED_CASE(MODE, UG, 4, 4)      \
     WM_FUSED_CASE(MODE, UG, 6, 4) WM_FUSED_CASE(MODE, UG, 8, 4) WM_FUSED_CASE(MODE, UG, 10, 4)     \
-    WM_FUSED_CASE(MODE, UG, 12, 4) WM_FUSED_CASE(MODE, UG, 16, 4) WM_FUSED_CASE(MODE, UG, 16, 8)   \
-    WM_FUSED_CASE(MODE, UG, 16, 16)
+    WM_FUSED_CASE(MODE, UG, 12, 4) WM_FUSED_CASE(MODE, UG, 16, 3) WM_FUSED_CASE(MODE, UG, 16, 4)   \
+    WM_FUSED_CASE(MODE, UG, 16, 8) WM_FUSED_CASE(MODE, UG, 16, 16)
     if (mode == WM_FUSED_PLAIN) { WM_FUSED_WS(WM_FUSED_PLAIN, 1) }
     else if (mode == WM_FUSED_GATEUP) { WM_FUSED_WS(WM_FUSED_GATEUP, 2) }
     else if (groups_per_unit == 2) { WM_FUSED_WS(WM_FUSED_ROPE, 2) }
