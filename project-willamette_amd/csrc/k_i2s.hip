@@ -148,21 +148,22 @@ __device__ __forceinline__ void i2s_reduce(const i2s_round<RG> &R, const int *ac
             for (int q = 0; q < RG; q++)
                 dot_chunk(R.v[u][q], act_s + (c + u) * 16, acc16[q], acc4[q], acc1[q]);
 }
-// The dots over chunks 0 .. nc-1, round 0 already issued into A: the next
-// round's loads go out before the current one is reduced, into the other
-// register set (the loop body covers two rounds, so no set is copied); a
-// round past the slice is never issued, and the last one is reduced on its
-// own path.
+// The dots over chunks 0 .. nc-1, round 0 already issued into A (and round
+// 1 into B when b_issued, nc > 4): the next round's loads go out before the
+// current one is reduced, into the other register set (the loop body covers
+// two rounds, so no set is copied); a round past the slice is never issued,
+// and the last one is reduced on its own path.
 template <int RG>
 __device__ __forceinline__ void i2s_rounds(i2s_round<RG> &A, i2s_round<RG> &B,
                                            const uint4 *const (&wp)[RG], uint32_t nc, const int *act_s,
-                                           int (&acc16)[RG], int (&acc4)[RG], int (&acc1)[RG]) {
+                                           int (&acc16)[RG], int (&acc4)[RG], int (&acc1)[RG],
+                                           bool b_issued = false) {
     for (uint32_t c = 0;; c += 8) {
         if (c + 4 >= nc) {
             i2s_reduce<RG>(A, act_s, c, nc - c, acc16, acc4, acc1);
             return;
         }
-        i2s_issue<RG>(B, wp, c + 4, nc);
+        if (c > 0 || !b_issued) i2s_issue<RG>(B, wp, c + 4, nc);
         __builtin_amdgcn_sched_barrier(0);  // the prefetch stays ahead of the reduction
         i2s_reduce<RG>(A, act_s, c, 4, acc16, acc4, acc1);
         if (c + 8 >= nc) {
@@ -322,6 +323,10 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
     int asum;
     {
         const float rsq = wm::norm_sum_rsqrt<NP, W * 64>(false, n, nm.eps, nullptr, 0, sq, nl);
+        // a second round, if the slice has one, goes out now: in flight
+        // during the quantiser instead of after it
+        if (nc > 4) i2s_issue<UG>(B, wp, 4, nc);
+        __builtin_amdgcn_sched_barrier(0);
         wm::norm_quant<NP, W * 64>(rsq, n, xv, wv, reinterpret_cast<uint8_t *>(act_s), nl,
                                    act_scale, asum);
     }
@@ -353,7 +358,7 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
     int acc16[UG], acc4[UG], acc1[UG];
 #pragma unroll
     for (int q = 0; q < UG; q++) acc16[q] = acc4[q] = acc1[q] = 0;
-    i2s_rounds<UG>(A, B, wp, nc, act_s + c0 * 16, acc16, acc4, acc1);
+    i2s_rounds<UG>(A, B, wp, nc, act_s + c0 * 16, acc16, acc4, acc1, nc > 4);
 #pragma unroll
     for (int q = 0; q < UG; q++)
         red[(wid * UG + q) * 64 + lane] = (acc16[q] >> 4) + (acc4[q] >> 2) + acc1[q];
@@ -571,10 +576,11 @@ void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
     for (int x : kWs)
         if (w >= x) { w = x; break; }
     // the norm's terms per thread, rounded up to an instantiated bound (the
-    // exact sum's work grows with the bound): at most 2 below 16 waves, at
-    // most 16 with 16 (n_chunks <= 256)
+    // exact sum's work grows with the bound; 3 and 7 are BitNet-2B's 2560 and
+    // 6912): at most 2 below 16 waves, at most 16 with 16 (n_chunks <= 256)
     const uint32_t per = (n_chunks + (uint32_t)w - 1) / (uint32_t)w;
-    const int np = (per <= 3 && w == 16) ? 3 : (per <= 4 ? 4 : (per <= 8 ? 8 : 16));
+    const int np = w == 16 && (per == 3 || per == 7) ? (int)per
+                                                     : (per <= 4 ? 4 : (per <= 8 ? 8 : 16));
     const size_t sq_bytes = (size_t)wm::seq_sum_padded(n_chunks * 64) * 4;
 #define WM_FUSED_CASE(MODE, UG, W, NP)                                                             \
     if (w == W && np == NP) {                                                                      \
@@ -587,7 +593,7 @@ void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
     WM_FUSED_CASE(MODE, UG, 1, 4) WM_FUSED_CASE(MODE, UG, 2, 4) WM_FUSED_CASE(MODE, UG, 4, 4)      \
     WM_FUSED_CASE(MODE, UG, 6, 4) WM_FUSED_CASE(MODE, UG, 8, 4) WM_FUSED_CASE(MODE, UG, 10, 4)     \
     WM_FUSED_CASE(MODE, UG, 12, 4) WM_FUSED_CASE(MODE, UG, 16, 3) WM_FUSED_CASE(MODE, UG, 16, 4)   \
-    WM_FUSED_CASE(MODE, UG, 16, 8) WM_FUSED_CASE(MODE, UG, 16, 16)
+    WM_FUSED_CASE(MODE, UG, 16, 7) WM_FUSED_CASE(MODE, UG, 16, 8) WM_FUSED_CASE(MODE, UG, 16, 16)
     if (mode == WM_FUSED_PLAIN) { WM_FUSED_WS(WM_FUSED_PLAIN, 1) }
     else if (mode == WM_FUSED_GATEUP) { WM_FUSED_WS(WM_FUSED_GATEUP, 2) }
     else if (groups_per_unit == 2) { WM_FUSED_WS(WM_FUSED_ROPE, 2) }
