@@ -195,7 +195,7 @@ __device__ inline float seq_sum_nonneg(const float *a, uint32_t n) {
 // is bitwise P before term k+1, but across a thread boundary the two values
 // come from different additions: the owner of k adds a_k to its own prefix,
 // the next thread builds its prefix from the wave scan.  Every such value is
-// a sum of non-negative doubles through at most 2*MAXM + 6 + NT/64 + 1 < 2^7
+// a sum of non-negative doubles through at most 2*MAXM + 6 + 4 + 1 < 2^7
 // additions along any path (MAXM <= 32), so it lies within relative
 // 2^7 * 2^-53 = 2^-46 of the exact prefix, and two computations of one
 // prefix within 2^-45 of each other.  A P_(k+1) farther than 2^-36 from
@@ -262,45 +262,89 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
     if (lane == 0) ex = 0.0;
     if (lane == 63) sc->dw[wid] = inc;
     wm_sync_lds();
-    double off = 0.0;
-#pragma unroll
-    for (int w = 0; w < NW; w++) off += w < (int)wid ? sc->dw[w] : 0.0;
+    // the waves before this one: lane w < wid holds wave w's total, and a
+    // scan along row 0 (NW <= 16 lanes) leaves their sum in lane 15
+    double dl = (lane < (uint32_t)NW && lane < wid) ? sc->dw[lane] : 0.0;
+#define WM_ROW_STEP(C) dl += __longlong_as_double(wm_dpp_i64<C, 0xF>(__double_as_longlong(dl)))
+    WM_ROW_STEP(WM_DPP_ROW_SHR1);
+    WM_ROW_STEP(WM_DPP_ROW_SHR2);
+    WM_ROW_STEP(WM_DPP_ROW_SHR4);
+    WM_ROW_STEP(WM_DPP_ROW_SHR8);
+#undef WM_ROW_STEP
+    const long long offb = __double_as_longlong(dl);
+    const double off = __longlong_as_double(
+        (long long)(((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(offb >> 32), 15) << 32) |
+                    (unsigned)__builtin_amdgcn_readlane((int)offb, 15)));
     double P = off + ex;
     // 2. breaks and increments.  Inside a thread P after term k is bitwise P
     // before term k+1, so the closeness test is needed only where the prefix
     // comes from another thread: before the first term and after the last.
     bool brk[MAXM];
     int incr[MAXM], eaf[MAXM];
+    const uint32_t last = min(m, n > k0 ? n - k0 : 0u) - 1;  // index of the last valid term
+    // The prefix after the thread's last term, by the same chain of adds as
+    // the per-term loop below (adding the zeros past the last term leaves it
+    // as is).  Non-negative terms make the chain non-decreasing, so when its
+    // two ends are positive and finite, every prefix in between is too: the
+    // ok tests all hold, and k == 0 is not among the terms (its prefix is
+    // +0).  That is every thread but those whose prefix starts at zero (the
+    // first, and any inside a leading run of zeros) or reaches inf / NaN;
+    // they take the full test, which the one path below reduces to here.
+    double Pe = P;
+#pragma unroll
+    for (int j = 0; j < MAXM; j++) Pe = Pe + (double)v[j];
+    if (P > 0.0 && Pe < 1e300) {
+        const bool close0 = near_pow2_f64(P, 34), close1 = near_pow2_f64(Pe, 36);
+        int eb = exp2floor_f64(P);
+#pragma unroll
+        for (int j = 0; j < MAXM; j++) {
+            const bool valid = (uint32_t)j < m && k0 + (uint32_t)j < n;
+            P = P + (double)v[j];
+            const int ea = exp2floor_f64(P);
+            bool b = v[j] != 0.0f && ea != eb;
+            if (j == 0) b = b || close0;
+            b = b || ((uint32_t)j == last && close1);
+            const float r = ldexpf(v[j], 23 - eb);  // a_k / ulp; exact unless < 2^-126
+            b = b || !(r < 0x1p22f) || r - floorf(r) == 0.5f;
+            brk[j] = valid && b;
+            incr[j] = valid && !b ? (int)rintf(r) : 0;
+            eaf[j] = ea;
+            eb = ea;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < MAXM; j++) {
+            const uint32_t k = k0 + (uint32_t)j;
+            const bool valid = (uint32_t)j < m && k < n;
+            const double pb = P, pa = P + (double)v[j];
+            P = pa;
+            const bool pb_ok = pb > 0.0 && pb < 1e300, pa_ok = pa > 0.0 && pa < 1e300;
+            const int eb = pb_ok ? exp2floor_f64(pb) : 0;
+            const int ea = pa_ok ? exp2floor_f64(pa) : -1000;
+            // a zero term leaves every running sum (+0, positive, inf or NaN)
+            // unchanged, so it is never a break on its own account: a run of
+            // zeros (an underflowed softmax tail, a zero prefix) costs nothing
+            const bool zero = v[j] == 0.0f;
+            bool b = !zero && (k == 0 || !pb_ok || !pa_ok || ea != eb);
+            // (a zero prefix is exact in both precisions: every term before
+            // it is zero, so no computation of it can land in another binade)
+            if (j == 0) b = b || (pb_ok && near_pow2_f64(pb, 34));
+            b = b || ((uint32_t)j == last && pa_ok && near_pow2_f64(pa, 36));
+            int d = 0;
+            if (!b) {
+                const float r = ldexpf(v[j], 23 - eb);  // a_k / ulp; exact unless < 2^-126
+                b = !(r < 0x1p22f) || r - floorf(r) == 0.5f;
+                d = b ? 0 : (int)rintf(r);
+            }
+            brk[j] = valid && b;
+            incr[j] = valid ? d : 0;
+            eaf[j] = ea;
+        }
+    }
     long long pi_loc = 0;
     int nb = 0;
-    const uint32_t last = min(m, n > k0 ? n - k0 : 0u) - 1;  // index of the last valid term
 #pragma unroll
     for (int j = 0; j < MAXM; j++) {
-        const uint32_t k = k0 + (uint32_t)j;
-        const bool valid = (uint32_t)j < m && k < n;
-        const double pb = P, pa = P + (double)v[j];
-        P = pa;
-        const bool pb_ok = pb > 0.0 && pb < 1e300, pa_ok = pa > 0.0 && pa < 1e300;
-        const int eb = pb_ok ? exp2floor_f64(pb) : 0;
-        const int ea = pa_ok ? exp2floor_f64(pa) : -1000;
-        // a zero term leaves every running sum (+0, positive, inf or NaN)
-        // unchanged, so it is never a break on its own account: a run of
-        // zeros (an underflowed softmax tail, a zero prefix) costs nothing
-        const bool zero = v[j] == 0.0f;
-        bool b = !zero && (k == 0 || !pb_ok || !pa_ok || ea != eb);
-        // (a zero prefix is exact in both precisions: every term before it
-        // is zero, so no computation of it can land in another binade)
-        if (j == 0) b = b || (pb_ok && near_pow2_f64(pb, 34));
-        b = b || ((uint32_t)j == last && pa_ok && near_pow2_f64(pa, 36));
-        int d = 0;
-        if (!b) {
-            const float r = ldexpf(v[j], 23 - eb);  // a_k / ulp; exact unless < 2^-126
-            b = !(r < 0x1p22f) || r - floorf(r) == 0.5f;
-            d = b ? 0 : (int)rintf(r);
-        }
-        brk[j] = valid && b;
-        incr[j] = valid ? d : 0;
-        eaf[j] = ea;
         nb += brk[j] ? 1 : 0;
         pi_loc += incr[j];
     }
