@@ -382,3 +382,86 @@ def test_block_model_zero_runs_fuzz():
         a = (rng.standard_normal(n) ** 2 * 2.0 ** rng.integers(-30, 30)).astype(np.float32)
         a[rng.random(n) < rng.random()] = 0.0
         assert same(model_block_sum(a), sequential(a)), f"case {i}"
+
+
+def _thread_breaks_full(P, v, k0, last):
+    """One thread's (break, increment, binade after) per term by the full
+    test of wm::seq_sum_block_owned (every ok check, k == 0, zero terms)."""
+    out = []
+    with np.errstate(all="ignore"):
+        for j, x in enumerate(v):
+            k = k0 + j
+            pb, pa = P, np.float64(P) + np.float64(x)
+            P = pa
+            pb_ok, pa_ok = 0 < pb < 1e300, 0 < pa < 1e300
+            eb = _exp2floor(pb) if pb_ok else 0
+            ea = _exp2floor(pa) if pa_ok else -1000
+            b = x != 0 and (k == 0 or not pb_ok or not pa_ok or ea != eb)
+            b = b or (j == 0 and pb_ok and _near_pow2(pb, 34))
+            b = b or (j == last and pa_ok and _near_pow2(pa, 36))
+            d = 0
+            if not b:
+                r = np.float32(np.ldexp(np.float32(x), 23 - eb))
+                b = not (r < f32(2.0 ** 22)) or (r - np.floor(r)) == f32(0.5)
+                d = 0 if b else int(np.rint(r))
+            out.append((bool(j <= last and b), d if j <= last else 0, ea))
+    return out
+
+
+def _thread_breaks_posfin(P, v, last):
+    """The same by the device's shortcut for a thread whose prefix starts
+    positive and ends finite: one binade test per term, no ok checks."""
+    with np.errstate(all="ignore"):
+        Pe = P
+        for x in v:
+            Pe = np.float64(Pe) + np.float64(x)
+        assert P > 0 and Pe < 1e300
+        close0, close1 = _near_pow2(P, 34), _near_pow2(Pe, 36)
+        eb = _exp2floor(P)
+        out = []
+        for j, x in enumerate(v):
+            P = np.float64(P) + np.float64(x)
+            ea = _exp2floor(P)
+            b = (x != 0 and ea != eb) or (j == 0 and close0) or (j == last and close1)
+            r = np.float32(np.ldexp(np.float32(x), 23 - eb))
+            b = b or not (r < f32(2.0 ** 22)) or (r - np.floor(r)) == f32(0.5)
+            out.append((bool(j <= last and b), int(np.rint(r)) if j <= last and not b else 0, ea))
+            eb = ea
+    return out
+
+
+def test_positive_prefix_shortcut_matches_full_test():
+    """A thread whose float64 prefix starts above zero and stays finite gets
+    the same breaks, increments and binades from the shortcut as from the
+    full test: prefixes that cross powers of two, sit next to one, terms
+    that are ties, zeros, subnormal or too large for a run."""
+    rng = np.random.default_rng(11)
+    cases = 0
+    for _ in range(3000):
+        m = int(rng.integers(1, 17))
+        kind = rng.integers(0, 5)
+        if kind == 0:  # squares of N(0,1)
+            v = (rng.standard_normal(m).astype(np.float32) ** 2).astype(np.float32)
+        elif kind == 1:  # wide exponents, some zeros and subnormals
+            v = np.ldexp(rng.random(m), rng.integers(-150, 40, m)).astype(np.float32)
+            v[rng.random(m) < 0.3] = 0
+        elif kind == 2:  # small integers: ties and exact sums
+            v = rng.integers(0, 9, m).astype(np.float32) * f32(0.5)
+        elif kind == 3:  # a term far above the prefix
+            v = rng.random(m).astype(np.float32)
+            v[rng.integers(0, m)] = f32(2.0 ** 40)
+        else:  # powers of two
+            v = np.ldexp(np.ones(m), rng.integers(-10, 10, m)).astype(np.float32)
+        # a starting prefix near a power of two, or anywhere
+        e = int(rng.integers(-20, 30))
+        P = float(np.ldexp(1.0, e)) * (1 + float(rng.choice([0.0, 2.0 ** -40, -(2.0 ** -40), rng.random()])))
+        if rng.random() < 0.2:
+            P = float(np.ldexp(1.0, e)) - float(v.astype(np.float64).sum()) * float(rng.random())
+        if not P > 0:
+            continue
+        last = int(rng.integers(0, m)) if rng.random() < 0.3 else m - 1
+        v[last + 1:] = 0  # terms past the last valid one are zeros on the device
+        k0 = int(rng.integers(1, 10000))
+        assert _thread_breaks_posfin(P, v, last) == _thread_breaks_full(P, v, k0, last)
+        cases += 1
+    assert cases > 2500
