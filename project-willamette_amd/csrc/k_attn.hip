@@ -201,6 +201,9 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
         const uint32_t n_tiles = (n + kSvTile - 1) / kSvTile;
         const uint32_t pt = tid - 64, dq = pt / kSvTile, pl = pt % kSvTile;  // producer unit
         float acc = 0.0f;
+        // the chains are the critical path: wave 0's instructions go first
+        // on its SIMD when a producer wave is ready at the same time
+        if (wid == 0) __builtin_amdgcn_s_setprio(3);
         for (uint32_t t = 0; t <= n_tiles; t++) {
             if (wid >= 1) {
                 if (t < n_tiles) {
@@ -245,6 +248,7 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
             }
             wm_sync_lds();
         }
+        if (wid == 0) __builtin_amdgcn_s_setprio(0);
         if (tid < kSvDims) out[tid] = acc;
     }
     if (v_writer) {  // the cache row of position n_past - 1

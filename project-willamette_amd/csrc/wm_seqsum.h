@@ -212,17 +212,46 @@ __device__ inline float seq_sum_nonneg(const float *a, uint32_t n) {
 constexpr int kSeqWaveRecords = 32;
 constexpr int kSeqMaxWaves = 16;
 
+// Increments are counted modulo 2^32: only differences over one segment are
+// used, and a segment's increments add up to less than 2^24 + n / 2 (its
+// terms sum to less than its binade's width, 2^23 ulps, each rounded by at
+// most half an ulp), so the modular difference is the true one.
 struct seq_block_scratch {
     double dw[kSeqMaxWaves];     // per wave: float64 total of its terms
-    long long wt[kSeqMaxWaves];  // per wave: (breaks << 48) + increment total
-    int idx[kSeqMaxWaves][kSeqWaveRecords];        // term index of the break
-    int eaf[kSeqMaxWaves][kSeqWaveRecords];        // predicted binade after it
-    long long pi[kSeqMaxWaves][kSeqWaveRecords];   // wave's increments before it
-    float val[kSeqMaxWaves][kSeqWaveRecords];      // the term
-    long long woff[kSeqMaxWaves];  // increments of the waves before each wave
-    short map[kSeqMaxWaves * kSeqWaveRecords];    // record r -> wave * R + slot
+    int wcnt[kSeqMaxWaves];      // per wave: breaks
+    uint32_t wpi[kSeqMaxWaves];  // per wave: increment total (mod 2^32)
+    int idx[kSeqMaxWaves][kSeqWaveRecords];       // term index of the break
+    int eaf[kSeqMaxWaves][kSeqWaveRecords];       // predicted binade after it
+    uint32_t pi[kSeqMaxWaves][kSeqWaveRecords];   // wave's increments before it
+    float val[kSeqMaxWaves][kSeqWaveRecords];     // the term
+    int first[64];  // walk: wave + 1 at the chunk lane of its first record, else 0
     float out;
 };
+
+// a 32-bit inclusive prefix sum (modulo 2^32) over the wave, and a running
+// maximum of non-negative values
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x) {
+    x += (uint32_t)wm_dpp<WM_DPP_ROW_SHR1, 0xF>((int)x);
+    x += (uint32_t)wm_dpp<WM_DPP_ROW_SHR2, 0xF>((int)x);
+    x += (uint32_t)wm_dpp<WM_DPP_ROW_SHR4, 0xF>((int)x);
+    x += (uint32_t)wm_dpp<WM_DPP_ROW_SHR8, 0xF>((int)x);
+    x += (uint32_t)wm_dpp<WM_DPP_ROW_BCAST15, 0xA>((int)x);
+    x += (uint32_t)wm_dpp<WM_DPP_ROW_BCAST31, 0xC>((int)x);
+    return x;
+}
+__device__ __forceinline__ int wave_max_scan_nonneg(int x) {
+    x = max(x, wm_dpp<WM_DPP_ROW_SHR1, 0xF>(x));
+    x = max(x, wm_dpp<WM_DPP_ROW_SHR2, 0xF>(x));
+    x = max(x, wm_dpp<WM_DPP_ROW_SHR4, 0xF>(x));
+    x = max(x, wm_dpp<WM_DPP_ROW_SHR8, 0xF>(x));
+    x = max(x, wm_dpp<WM_DPP_ROW_BCAST15, 0xA>(x));
+    x = max(x, wm_dpp<WM_DPP_ROW_BCAST31, 0xC>(x));
+    return x;
+}
+// lane l - 1's value of x; lane 0 gets `first`
+__device__ __forceinline__ int wave_shr1(int x, int first) {
+    return __builtin_amdgcn_update_dpp(first, x, 0x138, 0xF, 0xF, false);  // wave_shr:1
+}
 
 // floor(log2 x) of a positive, finite, normal double
 __device__ __forceinline__ int exp2floor_f64(double x) {
@@ -246,7 +275,6 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
     static_assert(MAXM >= 1 && MAXM <= 32, "terms per thread");
     constexpr int NW = NT / 64;
     constexpr int R = kSeqWaveRecords;
-    constexpr long long kLow48 = (1LL << 48) - 1;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wid = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
     if (n == 0) return 0.0f;
@@ -341,20 +369,18 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
             eaf[j] = ea;
         }
     }
-    long long pi_loc = 0;
+    uint32_t pi_loc = 0;
     int nb = 0;
 #pragma unroll
     for (int j = 0; j < MAXM; j++) {
         nb += brk[j] ? 1 : 0;
-        pi_loc += incr[j];
+        pi_loc += (uint32_t)incr[j];
     }
-    // wave-local exclusive scan of (break count << 48) + increment sum; a
-    // wave has at most 64 * MAXM * 2^22 < 2^48 of increments
-    const long long packed = ((long long)nb << 48) + pi_loc;
-    const long long pinc = wm_wave_scan_i64(packed);
-    const long long pex = pinc - packed;
-    int pos = (int)(pex >> 48);
-    long long pi = pex & kLow48;
+    // wave-local exclusive scans of the break counts and the increments
+    const int nb_inc = wm_wave_scan_i32(nb);
+    const uint32_t pi_inc = wave_scan_u32(pi_loc);
+    int pos = nb_inc - nb;
+    uint32_t pi = pi_inc - pi_loc;
 #pragma unroll
     for (int j = 0; j < MAXM; j++) {
         if (brk[j]) {
@@ -366,65 +392,72 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
             }
             pos++;
         } else {
-            pi += incr[j];
+            pi += (uint32_t)incr[j];
         }
     }
-    if (lane == 63) sc->wt[wid] = pinc;
+    if (lane == 63) {
+        sc->wcnt[wid] = nb_inc;
+        sc->wpi[wid] = pi_inc;
+    }
     wm_sync_lds();
     // 3. the walk over the breaks (wave 0)
     if (wid == 0) {
-        const long long wt = (int)lane < NW ? sc->wt[lane] : 0;
-        const int wc = (int)(wt >> 48);
-        const long long wp = wt & kLow48;
+        const int wc = (int)lane < NW ? sc->wcnt[lane] : 0;
+        const uint32_t wp = (int)lane < NW ? sc->wpi[lane] : 0u;
         float s = 0.0f;
         if (__builtin_amdgcn_ballot_w64(wc > R) != 0) {
             s = seq_sum_nonneg_from(0.0f, a, n);
         } else {
             const int cinc = wm_wave_scan_i32(wc);
-            const long long winc = wm_wave_scan_i64(wp);
-            const int cex = cinc - wc;  // first record of wave `lane`
+            const uint32_t winc = wave_scan_u32(wp);
+            const int cex = cinc - wc;        // first record of wave `lane`
+            const uint32_t wex = winc - wp;   // increments of the waves before it
             const int nbrk = __builtin_amdgcn_readlane(cinc, 63);
-            const long long pi_tot =
-                (long long)(((unsigned long long)(unsigned)__builtin_amdgcn_readlane(
-                                 (int)((unsigned long long)winc >> 32), 63)
-                             << 32) |
-                            (unsigned)__builtin_amdgcn_readlane((int)winc, 63));
-            // record index -> (wave, slot), and each wave's increment offset
-            if ((int)lane < NW) {
-                sc->woff[lane] = winc - wp;
-                for (int j = 0; j < wc; j++) sc->map[cex + j] = (short)(lane * R + j);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const uint32_t pi_tot = (uint32_t)__builtin_amdgcn_readlane((int)winc, 63);
             const int *idx = &sc->idx[0][0], *eafp = &sc->eaf[0][0];
-            const long long *pis = &sc->pi[0][0];
+            const uint32_t *pis = &sc->pi[0][0];
             const float *vals = &sc->val[0][0];
+            // record base - 1, carried from the previous chunk: its wave + 1,
+            // term index, binade after it, increments before it
+            int c_w = 0, c_t = -1, c_e = -1000, c_p = 0;
             for (int base = 0; base <= nbrk; base += 64) {
                 // lane l prepares step r = base + l: the segment between
                 // records r-1 and r, then record r's term (r == nbrk: the
                 // end; r > nbrk: a step that changes nothing)
                 const int r = base + (int)lane;
-                int t1 = (int)n, cnt = 0;
-                long long p1 = pi_tot;
+                // the wave holding record r: every wave with records marks
+                // the lane of its first one, and a running maximum carries
+                // the mark forward (waves are in record order)
+                sc->first[lane] = 0;
+                if ((int)lane < NW && wc > 0 && cex >= base && cex < base + 64)
+                    sc->first[cex - base] = (int)lane + 1;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const int wr = max(wave_max_scan_nonneg(sc->first[lane]), c_w);
+                const int w = max(wr - 1, 0);
+                const int cw = __shfl(cex, w, 64);
+                const uint32_t wo = (uint32_t)__shfl((int)wex, w, 64);
+                int t1 = (int)n, e1 = -1000, cnt = 0;
+                uint32_t p1 = pi_tot;
                 float v1 = 0.0f;
                 if (r < nbrk) {
-                    const int f = sc->map[r];
+                    const int f = w * R + (r - cw);
                     t1 = idx[f];
-                    p1 = sc->woff[f / R] + pis[f];
+                    e1 = eafp[f];
+                    p1 = wo + pis[f];
                     v1 = vals[f];
                 }
-                int t0 = -1, e0 = -1000;
-                long long p0 = 0;
-                if (r >= 1 && r - 1 < nbrk) {
-                    const int f = sc->map[r - 1];
-                    t0 = idx[f];
-                    e0 = eafp[f];
-                    p0 = sc->woff[f / R] + pis[f];
-                }
+                // record r - 1: the lane below's (lane 0: the carry)
+                const int t0 = wave_shr1(t1, c_t), e0 = wave_shr1(e1, c_e);
+                const uint32_t p0 = (uint32_t)wave_shr1((int)p1, c_p);
+                c_w = __builtin_amdgcn_readlane(wr, 63);
+                c_t = __builtin_amdgcn_readlane(t1, 63);
+                c_e = __builtin_amdgcn_readlane(e1, 63);
+                c_p = __builtin_amdgcn_readlane((int)p1, 63);
                 if (r <= nbrk) cnt = t1 - t0 - 1;  // terms in the segment
-                const long long dl = p1 - p0;      // their increments
-                const int D = (dl >= 0 && dl <= (1LL << 24)) ? (int)dl : (1 << 30);
+                const uint32_t dl = p1 - p0;       // their increments
+                const int D = dl <= (1u << 24) ? (int)dl : (1 << 30);
                 const int here = min(64, nbrk + 1 - base);
                 // When step r's check holds (s normal in binade e, s >= 2^e,
                 // s + D*ulp <= (2^24 - 2) * ulp), its segment adds exactly
