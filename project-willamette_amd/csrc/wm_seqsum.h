@@ -253,7 +253,7 @@ __device__ __forceinline__ int wave_shr1(int x, int first) {
     return __builtin_amdgcn_update_dpp(first, x, 0x138, 0xF, 0xF, false);  // wave_shr:1
 }
 
-// floor(log2 x) of a positive, finite, normal double
+// floor(log2 x) of a positive, finite, normal double (-1023 for +0)
 __device__ __forceinline__ int exp2floor_f64(double x) {
     return (int)((__double_as_longlong(x) >> 52) & 0x7FF) - 1023;
 }
@@ -312,17 +312,19 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
     const uint32_t last = min(m, n > k0 ? n - k0 : 0u) - 1;  // index of the last valid term
     // The prefix after the thread's last term, by the same chain of adds as
     // the per-term loop below (adding the zeros past the last term leaves it
-    // as is).  Non-negative terms make the chain non-decreasing, so when its
-    // two ends are positive and finite, every prefix in between is too: the
-    // ok tests all hold, and k == 0 is not among the terms (its prefix is
-    // +0).  That is every thread but those whose prefix starts at zero (the
-    // first, and any inside a leading run of zeros) or reaches inf / NaN;
-    // they take the full test, which the one path below reduces to here.
+    // as is).  Non-negative terms make the chain non-decreasing, so when it
+    // ends finite every prefix is finite and >= +0, and the full test below
+    // reduces to one comparison of binades: the binade field of +0 reads
+    // -1023, below every positive term's (>= -149), so a non-zero term on a
+    // zero prefix (k == 0 among them) differs from its prefix's binade and
+    // is a break, a zero term on it is not, and its increment is 0.  Only
+    // sums that reach inf or NaN take the full test.
     double Pe = P;
 #pragma unroll
     for (int j = 0; j < MAXM; j++) Pe = Pe + (double)v[j];
-    if (P > 0.0 && Pe < 1e300) {
-        const bool close0 = near_pow2_f64(P, 34), close1 = near_pow2_f64(Pe, 36);
+    if (Pe < 1e300) {
+        const bool close0 = P > 0.0 && near_pow2_f64(P, 34);
+        const bool close1 = Pe > 0.0 && near_pow2_f64(Pe, 36);
         int eb = exp2floor_f64(P);
 #pragma unroll
         for (int j = 0; j < MAXM; j++) {

@@ -385,8 +385,9 @@ def test_block_model_zero_runs_fuzz():
 
 
 def _thread_breaks_full(P, v, k0, last):
-    """One thread's (break, increment, binade after) per term by the full
-    test of wm::seq_sum_block_owned (every ok check, k == 0, zero terms)."""
+    """One thread's (break, increment, binade after a break) per term by the
+    full test of wm::seq_sum_block_owned (every ok check, k == 0, zero
+    terms); the binade is recorded, and used, only at breaks."""
     out = []
     with np.errstate(all="ignore"):
         for j, x in enumerate(v):
@@ -404,37 +405,46 @@ def _thread_breaks_full(P, v, k0, last):
                 r = np.float32(np.ldexp(np.float32(x), 23 - eb))
                 b = not (r < f32(2.0 ** 22)) or (r - np.floor(r)) == f32(0.5)
                 d = 0 if b else int(np.rint(r))
-            out.append((bool(j <= last and b), d if j <= last else 0, ea))
+            brk = bool(j <= last and b)
+            out.append((brk, d if j <= last else 0, ea if brk else None))
     return out
 
 
+def _binade_field(x):
+    """The device's exp2floor_f64: the biased exponent field minus 1023 (-1023 for +0)."""
+    return int((int(np.array(x, np.float64).view(np.uint64)) >> 52) & 0x7FF) - 1023
+
+
 def _thread_breaks_posfin(P, v, last):
-    """The same by the device's shortcut for a thread whose prefix starts
-    positive and ends finite: one binade test per term, no ok checks."""
+    """The same by the device's shortcut for a thread whose prefix chain
+    ends finite: one binade comparison per term, no ok checks."""
     with np.errstate(all="ignore"):
         Pe = P
         for x in v:
             Pe = np.float64(Pe) + np.float64(x)
-        assert P > 0 and Pe < 1e300
-        close0, close1 = _near_pow2(P, 34), _near_pow2(Pe, 36)
-        eb = _exp2floor(P)
+        assert Pe < 1e300
+        close0 = P > 0 and _near_pow2(P, 34)
+        close1 = Pe > 0 and _near_pow2(Pe, 36)
+        eb = _binade_field(P)
         out = []
         for j, x in enumerate(v):
             P = np.float64(P) + np.float64(x)
-            ea = _exp2floor(P)
+            ea = _binade_field(P)
             b = (x != 0 and ea != eb) or (j == 0 and close0) or (j == last and close1)
             r = np.float32(np.ldexp(np.float32(x), 23 - eb))
             b = b or not (r < f32(2.0 ** 22)) or (r - np.floor(r)) == f32(0.5)
-            out.append((bool(j <= last and b), int(np.rint(r)) if j <= last and not b else 0, ea))
+            brk = bool(j <= last and b)
+            out.append((brk, int(np.rint(r)) if j <= last and not b else 0, ea if brk else None))
             eb = ea
     return out
 
 
 def test_positive_prefix_shortcut_matches_full_test():
-    """A thread whose float64 prefix starts above zero and stays finite gets
-    the same breaks, increments and binades from the shortcut as from the
-    full test: prefixes that cross powers of two, sit next to one, terms
-    that are ties, zeros, subnormal or too large for a run."""
+    """A thread whose float64 prefix chain stays finite gets the same breaks,
+    increments and binades from the shortcut as from the full test:
+    prefixes that start at zero (the first term of the sum, leading zeros),
+    cross powers of two or sit next to one, terms that are ties, zeros,
+    subnormal or too large for a run."""
     rng = np.random.default_rng(11)
     cases = 0
     for _ in range(3000):
@@ -457,11 +467,15 @@ def test_positive_prefix_shortcut_matches_full_test():
         P = float(np.ldexp(1.0, e)) * (1 + float(rng.choice([0.0, 2.0 ** -40, -(2.0 ** -40), rng.random()])))
         if rng.random() < 0.2:
             P = float(np.ldexp(1.0, e)) - float(v.astype(np.float64).sum()) * float(rng.random())
-        if not P > 0:
+        k0 = int(rng.integers(1, 10000))
+        if rng.random() < 0.15:  # the first thread, or one inside a run of leading zeros
+            P, k0 = 0.0, int(rng.choice([0, k0]))
+            if rng.random() < 0.5:
+                v[: int(rng.integers(0, m + 1))] = 0
+        if not P >= 0:
             continue
         last = int(rng.integers(0, m)) if rng.random() < 0.3 else m - 1
         v[last + 1:] = 0  # terms past the last valid one are zeros on the device
-        k0 = int(rng.integers(1, 10000))
         assert _thread_breaks_posfin(P, v, last) == _thread_breaks_full(P, v, k0, last)
         cases += 1
     assert cases > 2500
