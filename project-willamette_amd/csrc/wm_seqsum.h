@@ -253,10 +253,13 @@ __device__ __forceinline__ int wave_shr1(int x, int first) {
     return __builtin_amdgcn_update_dpp(first, x, 0x138, 0xF, 0xF, false);  // wave_shr:1
 }
 
-// floor(log2 x) of a positive, finite, normal double (-1023 for +0)
-__device__ __forceinline__ int exp2floor_f64(double x) {
-    return (int)((__double_as_longlong(x) >> 52) & 0x7FF) - 1023;
+// the biased exponent field of a non-negative double: floor(log2 x) + 1023
+// for a positive, finite, normal x, 0 for +0
+__device__ __forceinline__ int exp2field_f64(double x) {
+    return (int)((__double_as_longlong(x) >> 52) & 0x7FF);
 }
+// floor(log2 x) of a positive, finite, normal double
+__device__ __forceinline__ int exp2floor_f64(double x) { return exp2field_f64(x) - 1023; }
 // x (positive, finite, normal) within relative 2^-T of a power of two
 __device__ __forceinline__ bool near_pow2_f64(double x, int T) {
     const unsigned long long mant = (unsigned long long)__double_as_longlong(x) & ((1ull << 52) - 1);
@@ -309,13 +312,14 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
     // comes from another thread: before the first term and after the last.
     bool brk[MAXM];
     int incr[MAXM], eaf[MAXM];
-    const uint32_t last = min(m, n > k0 ? n - k0 : 0u) - 1;  // index of the last valid term
+    const uint32_t nval = min(m, n > k0 ? n - k0 : 0u);  // the thread's terms
+    const uint32_t last = nval - 1;                        // index of the last one
     // The prefix after the thread's last term, by the same chain of adds as
     // the per-term loop below (adding the zeros past the last term leaves it
     // as is).  Non-negative terms make the chain non-decreasing, so when it
     // ends finite every prefix is finite and >= +0, and the full test below
-    // reduces to one comparison of binades: the binade field of +0 reads
-    // -1023, below every positive term's (>= -149), so a non-zero term on a
+    // reduces to one comparison of binades: the exponent field of +0 reads
+    // 0, below every positive term's (>= 874), so a non-zero term on a
     // zero prefix (k == 0 among them) differs from its prefix's binade and
     // is a break, a zero term on it is not, and its increment is 0.  Only
     // sums that reach inf or NaN take the full test.
@@ -325,19 +329,19 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
     if (Pe < 1e300) {
         const bool close0 = P > 0.0 && near_pow2_f64(P, 34);
         const bool close1 = Pe > 0.0 && near_pow2_f64(Pe, 36);
-        int eb = exp2floor_f64(P);
+        int eb = exp2field_f64(P);  // biased: the binade is eb - 1023
 #pragma unroll
         for (int j = 0; j < MAXM; j++) {
-            const bool valid = (uint32_t)j < m && k0 + (uint32_t)j < n;
             P = P + (double)v[j];
-            const int ea = exp2floor_f64(P);
-            bool b = v[j] != 0.0f && ea != eb;
+            const int ea = exp2field_f64(P);
+            // (a zero term leaves P, and so its binade, as it was)
+            bool b = ea != eb;
             if (j == 0) b = b || close0;
             b = b || ((uint32_t)j == last && close1);
-            const float r = ldexpf(v[j], 23 - eb);  // a_k / ulp; exact unless < 2^-126
-            b = b || !(r < 0x1p22f) || r - floorf(r) == 0.5f;
-            brk[j] = valid && b;
-            incr[j] = valid && !b ? (int)rintf(r) : 0;
+            const float r = ldexpf(v[j], 1046 - eb);  // a_k / ulp; exact unless < 2^-126
+            b = b || !(r < 0x1p22f) || __builtin_amdgcn_fractf(r) == 0.5f;
+            brk[j] = (uint32_t)j < nval && b;
+            incr[j] = (uint32_t)j < nval && !b ? (int)rintf(r) : 0;
             eaf[j] = ea;
             eb = ea;
         }
@@ -368,7 +372,7 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
             }
             brk[j] = valid && b;
             incr[j] = valid ? d : 0;
-            eaf[j] = ea;
+            eaf[j] = ea + 1023;
         }
     }
     uint32_t pi_loc = 0;
@@ -388,7 +392,7 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
         if (brk[j]) {
             if (pos < R) {
                 sc->idx[wid][pos] = (int)(k0 + (uint32_t)j);
-                sc->eaf[wid][pos] = eaf[j];
+                sc->eaf[wid][pos] = eaf[j] - 1023;
                 sc->pi[wid][pos] = pi;
                 sc->val[wid][pos] = v[j];
             }
