@@ -115,6 +115,19 @@ __device__ __forceinline__ int wm_round_clamp_i8(float v) {
     r = r > 127.0f ? 127.0f : r;
     return (r != r) ? 0 : (int)r;
 }
+// The same value in fewer operations: round half away from zero of |v| is
+// trunc(|v|) + (fract(|v|) >= 0.5), both exact (floor(|v| + 0.5) is not: the
+// add rounds 0.5 - 2^-25 up to 1); v_cvt_u32_f32 truncates, gives 0 for NaN
+// and saturates (a C cast would leave NaN and overflow undefined), and the
+// fraction of inf, NaN or anything at or above 2^23 is not >= 0.5, so one
+// min makes the clamp.
+__device__ __forceinline__ int wm_round_clamp_i8_fast(float v) {
+    const float a = fabsf(v);
+    uint32_t t;
+    asm("v_cvt_u32_f32 %0, %1" : "=v"(t) : "v"(a));
+    const uint32_t m = min(t + (__builtin_amdgcn_fractf(a) >= 0.5f ? 1u : 0u), 127u);
+    return __float_as_int(v) < 0 ? -(int)m : (int)m;
+}
 
 // Exact IEEE binary16 -> binary32 in integer arithmetic
 // (src/model/primitives.rs:61-88); no dependence on the FP unit's

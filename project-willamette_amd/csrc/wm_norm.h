@@ -143,12 +143,14 @@ __device__ __forceinline__ void norm_quant(float rsqrt_, uint32_t n, float (&xv)
     for (int i = 1; i < NW; i++) max_abs = wm_max_nonan(max_abs, L.red_f[i]);
     int sum = 0;
     const float inv = 127.0f / max_abs;
+    // with NT a multiple of 128, element tid + i*NT sits at perm(tid) + i*NT
+    const uint32_t pb = wm_act_perm(tid);
 #pragma unroll
     for (int i = 0; i < PER; i++) {
         const uint32_t j = tid + (uint32_t)i * NT;
         if (j < n) {
-            const int q = max_abs == 0.0f ? 0 : wm_round_clamp_i8(xv[i] * inv);
-            act[wm_act_perm(j)] = (uint8_t)(int8_t)q;
+            const int q = max_abs == 0.0f ? 0 : wm_round_clamp_i8_fast(xv[i] * inv);
+            act[NT % 128 == 0 ? pb + (uint32_t)i * NT : wm_act_perm(j)] = (uint8_t)(int8_t)q;
             sum += q;
         }
     }

@@ -479,3 +479,36 @@ def test_positive_prefix_shortcut_matches_full_test():
         assert _thread_breaks_posfin(P, v, last) == _thread_breaks_full(P, v, k0, last)
         cases += 1
     assert cases > 2500
+
+
+def test_round_clamp_fast_formula():
+    """wm_round_clamp_i8_fast: min(trunc_sat_u32(|v|) + (fract(|v|) >= 0.5),
+    127) with v's sign equals wm_round_clamp_i8 (round half away from zero,
+    clamp to +-127, NaN -> 0) on a dense sample of float bit patterns, every
+    value next to a half-integer in range, and the special values."""
+    def reference(v):
+        with np.errstate(all="ignore"):
+            r = np.where(np.abs(v - np.trunc(v)) >= 0.5, np.trunc(v) + np.sign(v), np.trunc(v))
+            r = np.clip(r, -127, 127)
+        return np.where(np.isnan(r), 0, r).astype(np.int64)
+
+    def fast(v):
+        with np.errstate(all="ignore"):
+            a = np.abs(v).astype(np.float64)
+            # v_cvt_u32_f32: truncate, NaN -> 0, saturate to [0, 2^32 - 1]
+            u = np.where(np.isnan(a), 0, np.minimum(np.trunc(a), 2.0 ** 32 - 1))
+            fract = a - np.floor(a)  # v_fract_f32 (NaN for inf and NaN)
+            u = u + np.where(fract >= 0.5, 1, 0)
+        m = np.minimum(u.astype(np.int64), 127)
+        return np.where(np.signbit(v), -m, m)
+
+    bits = np.arange(0, 2 ** 32, 251, dtype=np.uint64).astype(np.uint32)
+    halves = np.arange(-140, 141, dtype=np.float64) + 0.5
+    near = np.concatenate([np.nextafter(halves.astype(np.float32), np.float32(np.inf)),
+                           np.nextafter(halves.astype(np.float32), np.float32(-np.inf)),
+                           halves.astype(np.float32), np.arange(-140, 141, dtype=np.float32)])
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 2.0 ** 22, 2.0 ** 23, 2.0 ** 24,
+                        127.49999, 127.5, -127.5, 1e-45, -1e-45, 3e38, -3e38,
+                        0.49999997, -0.49999997, 0.5, -0.5], np.float32)
+    for v in (bits.view(np.float32), near, special):
+        assert np.array_equal(fast(v), reference(v))
