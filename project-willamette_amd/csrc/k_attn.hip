@@ -125,6 +125,30 @@ static_assert(kSvTile * (kSvDims / 4) == kSvThreads - 64, "one 4-dim unit per pr
 // while lanes 0-15 of wave 0 add the previous tile, one chain per
 // dimension, in position order.  Position n_past - 1 uses this token's V,
 // quantised from v_new (workgroup (0, 0) also writes the cache row).
+// The largest of the workgroup's values (none of them NaN; -inf where a
+// thread has none), in every thread: a DPP reduction per wave (-inf fills
+// the lanes a shift leaves empty), one LDS exchange.  `red` is not in use
+// before the call, so one barrier suffices.
+__device__ __forceinline__ float sv_block_max(float v, float *red) {
+    const int ninf = __float_as_int(-INFINITY);
+#define SV_MAX_STEP(C, R) \
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), C, R, 0xF, false)))
+    SV_MAX_STEP(0x111, 0xF);  // row_shr:1
+    SV_MAX_STEP(0x112, 0xF);  // row_shr:2
+    SV_MAX_STEP(0x114, 0xF);  // row_shr:4
+    SV_MAX_STEP(0x118, 0xF);  // row_shr:8
+    SV_MAX_STEP(0x142, 0xA);  // row_bcast:15
+    SV_MAX_STEP(0x143, 0xC);  // row_bcast:31
+#undef SV_MAX_STEP
+    const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (lane == 63) red[wid] = v;
+    wm_sync_lds();
+    float m = red[0];
+#pragma unroll
+    for (int w = 1; w < kSvThreads / 64; w++) m = fmaxf(m, red[w]);
+    return m;
+}
+
 template <int MAXM>  // n_past <= MAXM * kSvThreads (the exact sum's terms per thread)
 __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
     extern __shared__ __align__(16) float sm[];
@@ -174,7 +198,10 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
         reinterpret_cast<int8_t *>(vq + pnew)[tid] = kv_q(a.v_new[kvh * a.head_dim + d0 + tid], vabs);
     if (tid == 0) vsc[pnew] = kv_scale(vabs);
     // 2. softmax (attention.rs:45-73)
-    const float mx = wm_block_max_nonan(m, red);
+    // (the thread maxima are never NaN: a NaN score never wins above; a zero
+    // maximum's sign, which the reduction order could change, does not reach
+    // exp(s - max))
+    const float mx = sv_block_max(m, red);
     float *out = a.out + (uint64_t)h * a.head_dim + d0;
     if (!isfinite(mx)) {  // every weight becomes 0 -> output stays 0
         if (tid < kSvDims) out[tid] = 0.0f;
