@@ -303,7 +303,7 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
     const bool first = blockIdx.x == 0;
     float xv[NP], wv[NP], rv[NP];
     wm::norm_load<NP, W * 64>(nm.x, nm.y, nm.w, n, xv, wv, rv);
-    wm::norm_prep<NP, W * 64>(nm.y != nullptr, n, nullptr, sq, xv, wv, rv);
+    wm::norm_prep<NP, W * 64>(nm.y != nullptr, n, nullptr, sq, xv, wv, rv, nm.relu2_mul != 0);
     __builtin_amdgcn_sched_barrier(0);
     i2s_round<UG> A, B;
     i2s_issue<UG>(A, wp, 0, nc);

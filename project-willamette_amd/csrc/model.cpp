@@ -69,7 +69,8 @@ struct wm_model {
     // workspace
     uint8_t *ws = nullptr;
     float *hidden = nullptr, *hidden2 = nullptr;  // the residual stream, in two buffers
-    float *q = nullptr, *attn_out = nullptr, *h_ff = nullptr, *final_hidden = nullptr;
+    float *q = nullptr, *attn_out = nullptr, *final_hidden = nullptr;
+    float *h_ff = nullptr, *h_up = nullptr;  // the FFN's gate and up projections
     float *k_new = nullptr, *v_new = nullptr;  // this token's K (after RoPE) and V
     float *proj_out = nullptr;  // O's, then down's f32 output (the next norm adds it to hidden)
     float *logits = nullptr, *scores = nullptr;
@@ -202,12 +203,18 @@ void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
         cur ^= 1;
         wm_i2s_desc gu[2] = {{L.gate.w, L.gate.n_groups}, {L.up.w, L.up.n_groups}};
         const float gu_scales[2] = {L.gate.scale, L.up.scale};
-        float *gu_out[2] = {m->h_ff, nullptr};
-        wm_launch_i2s_fused(WM_FUSED_GATEUP, gu, gu_scales, gu_out, 2, n_chunks_e, 1, fn, nullptr,
+        // gate and up as two plain tensors, one 64-row group per workgroup
+        // (twice the workgroups of a gate+up pairing, half the weight bytes
+        // in flight per wave); relu(gate)^2 * up is formed where it is read,
+        // in the down matvec's norm
+        float *gu_out[2] = {m->h_ff, m->h_up};
+        wm_launch_i2s_fused(WM_FUSED_PLAIN, gu, gu_scales, gu_out, 2, n_chunks_e, 1, fn, nullptr,
                             nullptr, 0, 0, 0, nullptr, s);
-        // ffn_sub_norm, then down
+        // ffn_sub_norm of relu(gate)^2 * up, then down
         wm_fused_norm dn{};
         dn.x = m->h_ff;
+        dn.y = m->h_up;
+        dn.relu2_mul = 1;
         dn.w = L.ffn_sub_norm;
         dn.eps = c.rms_eps;
         wm_i2s_desc dd = {L.down.w, L.down.n_groups};
@@ -492,7 +499,7 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
         align256((size_t)E * 4), align256((size_t)E * 4),         // hidden, hidden2
         align256((size_t)E * 4),                                  // q
         align256((size_t)E * 4),                                  // attn_out
-        align256((size_t)F * 4),                                  // h_ff
+        align256((size_t)F * 4), align256((size_t)F * 4),         // h_ff, h_up
         align256((size_t)E * 4),                                  // final_hidden
         align256((size_t)m->kv_dim * 4), align256((size_t)m->kv_dim * 4),  // k_new, v_new
         align256((size_t)E * 4),                                  // proj_out
@@ -511,7 +518,8 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
     }
     uint8_t *p = m->ws;
     void **slots[] = {(void **)&m->hidden,   (void **)&m->hidden2,  (void **)&m->q,
-                      (void **)&m->attn_out, (void **)&m->h_ff,     (void **)&m->final_hidden,
+                      (void **)&m->attn_out, (void **)&m->h_ff,     (void **)&m->h_up,
+                      (void **)&m->final_hidden,
                       (void **)&m->k_new,    (void **)&m->v_new,    (void **)&m->proj_out,
                       (void **)&m->logits,   (void **)&m->scores,   (void **)&m->dscalars,
                       (void **)&m->lm_work,  (void **)&m->rope_cos, (void **)&m->rope_sin};

@@ -367,6 +367,9 @@ struct wm_fused_norm {
     uint8_t *act_out;       // nullable: a copy of the int8 codes (permuted layout)
     wm_act_meta *meta_out;  // nullable: their scale and sum
     uint32_t *clear2;       // nullable: two slots zeroed
+    // nonzero: x is the gate projection and y the up projection of the FFN,
+    // and the norm runs on relu(x)^2 * y (ffn.rs:37-65) instead of x + y
+    uint32_t relu2_mul;
 };
 // Matvec that starts from its input's norm, with the K split inside each
 // workgroup and a fused epilogue (mode WM_FUSED_*): rows of tensor i go to

@@ -41,20 +41,22 @@ __device__ __forceinline__ void norm_load(const float *x, const float *__restric
 }
 
 // From the loaded values: x + y (hidden += the producing matvec's output,
-// when has_y), written back to x_out when given, and the squares into sq.
+// when has_y; with relu2, relu(x)^2 * y: the FFN's gate x and up y,
+// ffn.rs:37-65), written back to x_out when given, and the squares into sq.
 // Thread t then holds element j = t + i*NT in xv[i] and its weight in wv[i]
 // (0 past n).  Returns whether any of its x + y is not finite.
 template <int PER, int NT>
 __device__ __forceinline__ bool norm_prep(bool has_y, uint32_t n, float *x_out, float *sq,
                                           float (&xv)[PER], float (&wv)[PER],
-                                          const float (&rv)[PER]) {
+                                          const float (&rv)[PER], bool relu2 = false) {
     const uint32_t tid = threadIdx.x;
     int nonfinite = 0;
     if (has_y) {
 #pragma unroll
         for (int i = 0; i < PER; i++) {
             const uint32_t j = tid + (uint32_t)i * NT;
-            const float v = xv[i] + rv[i];
+            const float r = xv[i] > 0.0f ? xv[i] : 0.0f;
+            const float v = relu2 ? (r * r) * rv[i] : xv[i] + rv[i];
             xv[i] = v;
             if (j < n) {
                 if (x_out) x_out[j] = v;
