@@ -296,8 +296,8 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
     float *sq = ys + UG * 64;
     // The norm's inputs first, alone: they come back quickly while nothing
     // else is queued (every workgroup's weight loads would otherwise be ahead
-    // of them in the memory system); then the first round of weights, in
-    // flight during the exact sum.
+    // of them in the memory system).  The first round of weights follows
+    // inside the exact sum, once its per-term work is done.
     const wm_fused_norm &nm = a.norm;
     const uint32_t n = n_chunks * 64;
     const bool first = blockIdx.x == 0;
@@ -306,8 +306,6 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
     wm::norm_prep<NP, W * 64>(nm.y != nullptr, n, nullptr, sq, xv, wv, rv, nm.relu2_mul != 0);
     __builtin_amdgcn_sched_barrier(0);
     i2s_round<UG> A, B;
-    i2s_issue<UG>(A, wp, 0, nc);
-    __builtin_amdgcn_sched_barrier(0);
     // the epilogue's RoPE factors, fetched now rather than after the reduction
     const uint32_t half = a.n_rot / 2;  // ROPE: at most 64 <= W * 64 pairs, one per thread
     const bool rope = MODE == WM_FUSED_ROPE && ((a.rope_mask >> t) & 1u);
@@ -322,7 +320,15 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
     float act_scale;
     int asum;
     {
-        const float rsq = wm::norm_sum_rsqrt<NP, W * 64>(false, n, nm.eps, nullptr, 0, sq, nl);
+        // the first round of weights goes out once the sum's per-term work
+        // is done (data arriving during that work slows it), in flight
+        // during the record walk and the quantiser
+        const auto issue_first = [&]() {
+            __builtin_amdgcn_sched_barrier(0);
+            i2s_issue<UG>(A, wp, 0, nc);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        const float rsq = wm::norm_sum_rsqrt<NP, W * 64>(false, n, nm.eps, nullptr, 0, sq, nl, issue_first);
         // a second round, if the slice has one, goes out now: in flight
         // during the quantiser instead of after it
         if (nc > 4) i2s_issue<UG>(B, wp, 4, nc);

@@ -78,12 +78,13 @@ __device__ __forceinline__ bool norm_prep(bool has_y, uint32_t n, float *x_out, 
 }
 
 // After norm_prep: Σx² exactly, in order (primitives.rs:243-246); returns
-// 1/sqrt(Σx²/n + eps).  err_flag (nullable): set to layer_tag when some
+// 1/sqrt(Σx²/n + eps).  before_walk: see seq_sum_block_owned.  err_flag (nullable): set to layer_tag when some
 // thread's x + y was not finite and the flag is still clear.
-template <int PER, int NT>
+template <int PER, int NT, typename Hook = seq_no_hook>
 __device__ __forceinline__ float norm_sum_rsqrt(bool nonfinite, uint32_t n, float eps,
                                                 uint32_t *err_flag, uint32_t layer_tag,
-                                                float *sq, norm_lds<NT / 64> &L) {
+                                                float *sq, norm_lds<NT / 64> &L,
+                                                const Hook &before_walk = Hook()) {
     constexpr int NW = NT / 64;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     if (err_flag && lane == 0) L.red_nf[wid] = __builtin_amdgcn_ballot_w64(nonfinite) != 0;
@@ -95,7 +96,7 @@ __device__ __forceinline__ float norm_sum_rsqrt(bool nonfinite, uint32_t n, floa
         for (int i = 0; i < PER; i++)
             v2[i] = ((uint32_t)i < m && k0 + (uint32_t)i < n) ? sq[k0 + i] : 0.0f;
     }
-    const float sum_sq = seq_sum_block_owned<PER, NT>(v2, n, sq, &L.seq);
+    const float sum_sq = seq_sum_block_owned<PER, NT>(v2, n, sq, &L.seq, before_walk);
     if (err_flag && tid == 0) {
         int any = 0;
 #pragma unroll

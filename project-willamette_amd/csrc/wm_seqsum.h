@@ -271,9 +271,18 @@ __device__ __forceinline__ bool near_pow2_f64(double x, int T) {
 // k = threadIdx.x * m + j for j < m = ceil(n / NT) <= MAXM and k < n, and 0
 // otherwise; `a` holds all n terms, readable by wave 0 after a barrier (the
 // caller writes it before the call).  The sum comes back in every thread.
-template <int MAXM, int NT>
+// No work to slot in before the walk.
+struct seq_no_hook {
+    __device__ void operator()() const {}
+};
+
+// `before_walk` runs in every thread once the per-term work is done, while
+// wave 0 walks the records and the other waves wait (the fused matvecs issue
+// their weight loads there, so that the data does not arrive during the
+// per-term work).
+template <int MAXM, int NT, typename Hook = seq_no_hook>
 __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const float *a,
-                                     seq_block_scratch *sc) {
+                                     seq_block_scratch *sc, const Hook &before_walk = Hook()) {
     static_assert(NT % 64 == 0 && NT <= 64 * kSeqMaxWaves, "workgroup size");
     static_assert(MAXM >= 1 && MAXM <= 32, "terms per thread");
     constexpr int NW = NT / 64;
@@ -406,6 +415,7 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
         sc->wpi[wid] = pi_inc;
     }
     wm_sync_lds();
+    before_walk();
     // 3. the walk over the breaks (wave 0)
     if (wid == 0) {
         const int wc = (int)lane < NW ? sc->wcnt[lane] : 0;
