@@ -326,13 +326,10 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
         const auto issue_first = [&]() {
             __builtin_amdgcn_sched_barrier(0);
             i2s_issue<UG>(A, wp, 0, nc);
+            if (nc > 4) i2s_issue<UG>(B, wp, 4, nc);  // and the second, if the slice has one
             __builtin_amdgcn_sched_barrier(0);
         };
         const float rsq = wm::norm_sum_rsqrt<NP, W * 64>(false, n, nm.eps, nullptr, 0, sq, nl, issue_first);
-        // a second round, if the slice has one, goes out now: in flight
-        // during the quantiser instead of after it
-        if (nc > 4) i2s_issue<UG>(B, wp, 4, nc);
-        __builtin_amdgcn_sched_barrier(0);
         wm::norm_quant<NP, W * 64>(rsq, n, xv, wv, reinterpret_cast<uint8_t *>(act_s), nl,
                                    act_scale, asum);
     }
