@@ -49,31 +49,36 @@ __device__ __forceinline__ int8_t kv_q(float v, float absmax) {
 }
 __device__ __forceinline__ float kv_scale(float absmax) { return kv_zero(absmax) ? 0.0f : absmax / 127.0f; }
 
-// scores[h][p] = (Σ_i q_h[i] * k_p[i]) * scale.  One lane per cached
-// position, blocks of 64; grid (n_heads, ceil((n_past - 1) / 64) + 1).  The
-// last block of each head scores position n_past - 1, whose K row is this
-// token's k_new quantised here exactly as KVCache::append does (head 0's also
-// writes the row to the cache): the products q_i * k_i lane-parallel, then
-// their sum in order by one lane.  It runs beside the cached blocks instead of
-// after its own loads.
-__global__ __launch_bounds__(64) void k_attn_scores(attn_args a) {
-    const uint32_t h = blockIdx.x, lane = threadIdx.x;
+// scores[h][p] = (Σ_i q_h[i] * k_p[i]) * scale.  64 cached positions per
+// workgroup of 256 threads; grid (n_heads, ceil((n_past - 1) / 64) + 1).
+// Wave w computes the products q_i * k_i of dims [w*hd/4, (w+1)*hd/4) for
+// the workgroup's 64 positions into LDS, then wave 0 adds each position's
+// products in order, one lane per position (the sum is a dependent chain;
+// the products are not, so four waves share them).  The last block of each
+// head scores position n_past - 1, whose K row is this token's k_new
+// quantised here exactly as KVCache::append does (head 0's also writes the
+// row to the cache).  It runs beside the cached blocks instead of after its
+// own loads.
+constexpr int kScThreads = 256;
+constexpr int kScStride = kMaxHeadDim + 4;  // floats per position row (16-byte rows, spread banks)
+__global__ __launch_bounds__(kScThreads) void k_attn_scores(attn_args a) {
+    __shared__ __align__(16) float prod[64 * kScStride];
+    const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const uint32_t kvh = h / a.group, pnew = a.n_past - 1;
     const float *qh = a.q + (uint64_t)h * a.head_dim;
     if (blockIdx.y == gridDim.y - 1) {
-        __shared__ float prod[kMaxHeadDim];
         const float kabs = __uint_as_float(a.kv_absmax[0]);
         const float ksn = kv_scale(kabs);
-        for (uint32_t i = lane; i < a.head_dim; i += 64) {
+        for (uint32_t i = tid; i < a.head_dim; i += kScThreads) {
             const float kd = (float)kv_q(a.k_new[kvh * a.head_dim + i], kabs) * ksn;  // read_into
             prod[i] = qh[i] * kd;
         }
         if (h == 0) {
-            for (uint32_t i = lane; i < a.kv_dim; i += 64) a.k_row[i] = kv_q(a.k_new[i], kabs);
-            if (lane == 0) *a.k_row_scale = ksn;
+            for (uint32_t i = tid; i < a.kv_dim; i += kScThreads) a.k_row[i] = kv_q(a.k_new[i], kabs);
+            if (tid == 0) *a.k_row_scale = ksn;
         }
         wm_sync_lds();
-        if (lane == 0) {
+        if (tid == 0) {
             float s = 0.0f;
             for (uint32_t i = 0; i < a.head_dim; i += 4) {
                 const float4 f = *reinterpret_cast<const float4 *>(prod + i);
@@ -84,27 +89,41 @@ __global__ __launch_bounds__(64) void k_attn_scores(attn_args a) {
         return;
     }
     const uint32_t p = blockIdx.y * 64 + lane;
-    if (p >= pnew) return;
-    const uint32_t nb = a.head_dim / 16;  // 4 or 8 sixteen-byte segments
-    const int8_t *kp = a.k_cache + (uint64_t)p * a.kv_dim + kvh * a.head_dim;
-    const float ksc = a.k_scales[p];
-    int4 raw[kMaxHeadDim / 16];
+    const bool live = p < pnew;
+    // this wave's 16-byte segments of the K row: hd/64 of them (2 or 1)
+    const uint32_t nseg = a.head_dim / 64, seg0 = wid * nseg;
+    const int8_t *kp = a.k_cache + (uint64_t)(live ? p : 0) * a.kv_dim + kvh * a.head_dim;
+    const float ksc = a.k_scales[live ? p : 0];
+    int4 raw[2];
 #pragma unroll
-    for (int b = 0; b < (int)(kMaxHeadDim / 16); b++)  // all 16-byte loads in flight together
-        raw[b] = *reinterpret_cast<const int4 *>(kp + (b < (int)nb ? b : 0) * 16);
-    float s = 0.0f;
+    for (int b = 0; b < 2; b++)  // both loads in flight together
+        raw[b] = *reinterpret_cast<const int4 *>(kp + (seg0 + (b < (int)nseg ? b : 0)) * 16);
+    float *row = prod + lane * kScStride;
 #pragma unroll
-    for (int b = 0; b < (int)(kMaxHeadDim / 16); b++) {
-        if (b < (int)nb) {
+    for (int b = 0; b < 2; b++) {
+        if (b < (int)nseg) {
             const int8_t *kb = reinterpret_cast<const int8_t *>(&raw[b]);
+            const uint32_t d0 = (seg0 + b) * 16;
 #pragma unroll
-            for (int t = 0; t < 16; t++) {
-                const float kd = (float)kb[t] * ksc;  // read_into: q as f32 * scale
-                s = s + qh[b * 16 + t] * kd;
+            for (int t = 0; t < 16; t += 4) {
+                float4 f;
+                f.x = qh[d0 + t] * ((float)kb[t] * ksc);  // read_into: q as f32 * scale
+                f.y = qh[d0 + t + 1] * ((float)kb[t + 1] * ksc);
+                f.z = qh[d0 + t + 2] * ((float)kb[t + 2] * ksc);
+                f.w = qh[d0 + t + 3] * ((float)kb[t + 3] * ksc);
+                *reinterpret_cast<float4 *>(row + d0 + t) = f;
             }
         }
     }
-    a.scores[(uint64_t)h * a.score_stride + p] = s * a.scale;
+    wm_sync_lds();
+    if (wid == 0 && live) {
+        float s = 0.0f;
+        for (uint32_t i = 0; i < a.head_dim; i += 4) {
+            const float4 f = *reinterpret_cast<const float4 *>(row + i);
+            s = s + f.x; s = s + f.y; s = s + f.z; s = s + f.w;
+        }
+        a.scores[(uint64_t)h * a.score_stride + p] = s * a.scale;
+    }
 }
 
 constexpr int kSvThreads = 1024;  // wave 0: the 16 chains; waves 1-15: products
@@ -297,7 +316,7 @@ void wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
     attn_args a{q, k_cache, k_scales, v_cache, v_scales, scores, out, n_past, kv_dim, head_dim,
                 n_heads / n_kv_heads, score_stride, scale, k_new, v_new, kv_absmax, k_row, v_row,
                 const_cast<float *>(k_scales) + (n_past - 1), const_cast<float *>(v_scales) + (n_past - 1)};
-    hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, (n_past - 1 + 63) / 64 + 1), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, (n_past - 1 + 63) / 64 + 1), dim3(kScThreads), 0, s, a);
     const size_t npad = ((size_t)n_past + 3) & ~(size_t)3;
     const size_t lds = (size_t)wm::seq_sum_padded(n_past) * 4 + npad * (4 + 16) +
                        (size_t)2 * kSvDims * kSvStride * 4;
