@@ -141,15 +141,14 @@ def ragged_batch(ctx, wh, bs, dev, cfg, steps: int):
     ~U[1, 32] new tokens each in one wm_batch_forward call.  Also times the
     batched BitLinear (per-row int8 quantiser + int8 MFMA GEMM) at the
     three BitNet-2B GEMM shapes with M = the batch's token count."""
-    rng = np.random.default_rng(bs.master_seed(5))
-    n_seq = 16
-    ctxs = [int(c) for c in rng.integers(128, 4064 + 1, n_seq)]
-    news = [int(n) for n in rng.integers(1, 32 + 1, n_seq)]
-    seqs = [[int(t) for t in rng.integers(0, cfg.vocab, n)] for n in news]
+    wl = bs.ragged_workload(cfg)
+    n_seq = len(wl.contexts)
+    ctxs, seqs = list(wl.contexts), [list(t) for t in wl.new_tokens]
+    news = [len(t) for t in seqs]
     kvs = []
     for i, c in enumerate(ctxs):
         kv = dev.kv_cache(cfg.context_length)
-        k, v = bs.kv_prefill(cfg, bs.master_seed(5) + 1 + i, c)
+        k, v = bs.kv_prefill(cfg, wl.prefill_seeds[i], c)
         kv.append_positions(k, v)
         del k, v
         kvs.append(kv)
@@ -194,11 +193,13 @@ def ragged_batch(ctx, wh, bs, dev, cfg, steps: int):
         w.close()
         x.free()
         y.free()
+    gold = json.loads((ROOT / "tests" / "golden" / "bitnet2b_ragged16.json").read_text())
     return {"sequences": n_seq, "new_tokens": m_tok, "context_min": min(ctxs),
             "context_max": max(ctxs), "ms_per_step": round(wall_ms, 3),
             "gpu_event_ms_per_step": round(ev_ms, 3),
             "tokens_per_s": round(m_tok / (wall_ms / 1000.0), 1),
             "next_token_checksum": int(np.bitwise_xor.reduce(np.array(nxt, np.uint64))),
+            "next_ids_match_oracle": [int(i) for i in nxt] == [s["next_id"] for s in gold["sequences"]],
             "bitlinear_gemm_incl_row_quantiser": gemm}
 
 
@@ -222,6 +223,23 @@ def cpu_baseline(hm, cfg, n_tokens: int, threads: int):
     dt = time.perf_counter() - t0
     orm.close()
     return n_tokens / dt, dt
+
+
+def host_info():
+    """nproc and the CPU model of this host (BASELINE's CPU-baseline record)."""
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count()
+    return {"nproc": nproc, "logical_cpus": os.cpu_count(), "cpu_model": model}
 
 
 COPY_BYTES = 1 << 30  # calibration copy for the HBM byte counters
@@ -379,7 +397,10 @@ def main():
         cpu_tok_s, cpu_s = cpu_baseline(hm, cfg, args.cpu_tokens, threads)
         cpu = {"value": round(cpu_tok_s, 4), "unit": "tok/s", "cores": threads, "kind": "port",
                "sample": f"{args.cpu_tokens} greedy tokens of the same workload (positions 1024..), "
-                         f"{cpu_s:.1f} s; BitLinear single-threaded, lm-head over {threads} threads"}
+                         f"{cpu_s:.1f} s; BitLinear single-threaded, lm-head over {threads} threads",
+               "label": "C restatement of the reference's x86 SSE2 path (oracle/wm_oracle.c)",
+               "host": host_info(),
+               "compiler_flags": "gcc -O2 -ffp-contract=off -fno-fast-math (no -march=native)"}
         log(f"cpu baseline: {cpu_tok_s:.3f} tok/s")
 
     out = {

@@ -58,6 +58,8 @@ _SIGS = {
                            C.c_float, _f32p, _f32p, _f32p, _f32p),
     "or_model_set_output": (C.c_int, _vp, _u8p, _f32p),
     "or_model_set_threads": (None, _vp, C.c_int),
+    "or_sdpa": (None, _f32p, _f32p, _f32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _f32p,
+                _f32p),
     "or_kv_create": (_vp, C.c_uint32, C.c_uint32, C.c_uint32),
     "or_kv_destroy": (None, _vp),
     "or_kv_position": (C.c_uint32, _vp),
@@ -183,6 +185,22 @@ def softmax(x):
     x = np.array(x, dtype=np.float32)
     lib.or_softmax_inplace(P(x, C.c_float), x.size)
     return x
+
+
+def sdpa(q, kd, vd, n_heads: int, n_kv_heads: int, head_dim: int):
+    """Attention of q [n_heads*head_dim] over f32 K/V rows kd, vd
+    [n_past][n_kv_heads*head_dim] (src/model/cached_forward.rs:417-449)."""
+    q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1)
+    kd = np.ascontiguousarray(kd, dtype=np.float32)
+    vd = np.ascontiguousarray(vd, dtype=np.float32)
+    kvd = n_kv_heads * head_dim
+    assert q.size == n_heads * head_dim and kd.size % kvd == 0 and kd.shape == vd.shape
+    n_past = kd.size // kvd
+    out = np.empty(n_heads * head_dim, np.float32)
+    scores = np.empty(max(n_past, 1), np.float32)
+    lib.or_sdpa(P(q, C.c_float), P(kd, C.c_float), P(vd, C.c_float), n_past, n_heads, n_kv_heads,
+                head_dim, P(out, C.c_float), P(scores, C.c_float))
+    return out
 
 
 def kv_quantise(x):

@@ -600,10 +600,38 @@ static int linear(const or_lin *w, size_t in_dim, size_t out_dim, const float *x
                                                out_dim, x, y, NULL, NULL, NULL);
 }
 
-/* src/model/cached_forward.rs:417-449 on the dequantised window of
- * kv_cache.rs:192-219 (q as f32 * scale). */
+/* src/model/cached_forward.rs:417-449: attention of one query vector over
+ * n_past dequantised K/V rows (row p = kv_dim values, kv head j at
+ * j*head_dim), out[n_heads*head_dim]; scores is n_past floats of scratch. */
+void or_sdpa(const float *q, const float *kd, const float *vd, uint32_t n_past, uint32_t n_heads,
+             uint32_t n_kv_heads, uint32_t head_dim, float *out, float *scores) {
+    const size_t hd = head_dim, kvd = (size_t)n_kv_heads * head_dim;
+    const float scale = 1.0f / sqrtf((float)hd); /* primitives.rs:354 */
+    const uint32_t group = n_heads / n_kv_heads;
+    memset(out, 0, (size_t)n_heads * hd * 4);
+    for (uint32_t h = 0; h < n_heads; h++) {
+        const uint32_t kvh = h / group; /* primitives.rs:377 */
+        const float *qh = q + h * hd;
+        for (uint32_t p = 0; p < n_past; p++) {
+            const float *kh = kd + p * kvd + kvh * hd;
+            float s = 0.0f;
+            for (size_t i = 0; i < hd; i++) s += qh[i] * kh[i];
+            scores[p] = s * scale;
+        }
+        or_softmax_inplace(scores, n_past);
+        float *oh = out + h * hd;
+        for (uint32_t p = 0; p < n_past; p++) {
+            const float *vh = vd + p * kvd + kvh * hd;
+            const float w = scores[p];
+            for (size_t d = 0; d < hd; d++) oh[d] += w * vh[d];
+        }
+    }
+}
+
+/* The attention of forward_one_layer on the window that KVCache::read_into
+ * dequantises (src/model/kv_cache.rs:192-219: q as f32 * scale). */
 static void sdpa(or_model *m, const or_kv *kv, uint32_t layer, uint32_t n_past) {
-    size_t kvd = m->kv_dim, hd = m->head_dim;
+    size_t kvd = m->kv_dim;
     size_t need = (size_t)n_past * kvd;
     if (m->kd_cap < need) {
         free(m->kd); free(m->vd);
@@ -624,26 +652,8 @@ static void sdpa(or_model *m, const or_kv *kv, uint32_t layer, uint32_t n_past) 
             m->vd[p * kvd + d] = (float)kv->v[off + p * kvd + d] * sv;
         }
     }
-    float scale = 1.0f / sqrtf((float)hd); /* primitives.rs:354 */
-    uint32_t group = m->n_heads / m->n_kv_heads;
-    memset(m->attn_out, 0, (size_t)m->n_embd * 4);
-    for (uint32_t h = 0; h < m->n_heads; h++) {
-        uint32_t kvh = h / group; /* primitives.rs:377 */
-        const float *qh = m->q + h * hd;
-        for (uint32_t p = 0; p < n_past; p++) {
-            const float *kh = m->kd + p * kvd + kvh * hd;
-            float s = 0.0f;
-            for (size_t i = 0; i < hd; i++) s += qh[i] * kh[i];
-            m->scores[p] = s * scale;
-        }
-        or_softmax_inplace(m->scores, n_past);
-        float *oh = m->attn_out + h * hd;
-        for (uint32_t p = 0; p < n_past; p++) {
-            const float *vh = m->vd + p * kvd + kvh * hd;
-            float w = m->scores[p];
-            for (size_t d = 0; d < hd; d++) oh[d] += w * vh[d];
-        }
-    }
+    or_sdpa(m->q, m->kd, m->vd, n_past, m->n_heads, m->n_kv_heads, m->head_dim, m->attn_out,
+            m->scores);
 }
 
 static int finite_all(const float *x, size_t n) {

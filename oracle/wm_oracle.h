@@ -69,6 +69,11 @@ void or_softmax_inplace(float *x, size_t n);
 void or_relu_square_mul(const float *gate, const float *up, size_t n, float *out);
 /* src/model/kv_cache.rs:245-259: q + scale for one token; returns the scale */
 float or_kv_quantise(const float *x, size_t n, int8_t *q);
+/* src/model/cached_forward.rs:417-449: q[n_heads*head_dim] attends to n_past
+ * f32 K/V rows of n_kv_heads*head_dim values; out[n_heads*head_dim];
+ * scores: n_past floats of scratch. */
+void or_sdpa(const float *q, const float *kd, const float *vd, uint32_t n_past, uint32_t n_heads,
+             uint32_t n_kv_heads, uint32_t head_dim, float *out, float *scores);
 
 /* ---- model-level ------------------------------------------------------- */
 typedef struct or_model or_model;

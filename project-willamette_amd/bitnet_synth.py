@@ -252,3 +252,30 @@ class DeviceKV:
                                                  prompt.size, max_new, eos,
                                                  wh._ptr(out, wh.C.c_uint32), wh.C.byref(n)))
         return out[: n.value].tolist()
+
+
+@dataclass(frozen=True)
+class RaggedWorkload:
+    """A continuous-batching step: sequence i holds contexts[i] pre-filled
+    positions (N(0,1) K/V through the int8 KV quantiser, stream seed
+    prefill_seeds[i]) and appends the token ids new_tokens[i]."""
+    contexts: tuple
+    new_tokens: tuple
+    prefill_seeds: tuple
+
+    @property
+    def n_tokens(self) -> int:
+        return sum(len(t) for t in self.new_tokens)
+
+
+def ragged_workload(cfg: BitNetConfig, n_seq: int = 16, ctx_lo: int = 128, ctx_hi: int = 4064,
+                    new_lo: int = 1, new_hi: int = 32) -> RaggedWorkload:
+    """The ragged multi-sequence batch at BitNet-2B shape: n_seq sequences
+    with contexts ~U[ctx_lo, ctx_hi] and ~U[new_lo, new_hi] new tokens each
+    (ids uniform over the vocabulary), all drawn from master seed 5."""
+    rng = np.random.default_rng(master_seed(5))
+    ctxs = tuple(int(c) for c in rng.integers(ctx_lo, ctx_hi + 1, n_seq))
+    news = [int(n) for n in rng.integers(new_lo, new_hi + 1, n_seq)]
+    seqs = tuple(tuple(int(t) for t in rng.integers(0, cfg.vocab, n)) for n in news)
+    seeds = tuple(master_seed(5) + 1 + i for i in range(n_seq))
+    return RaggedWorkload(ctxs, seqs, seeds)

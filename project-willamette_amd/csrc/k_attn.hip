@@ -205,10 +205,15 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
         for (int i = 0; i < 4; i++) {
             const uint32_t p = base + tid + (uint32_t)i * kSvThreads;
             if (p < n) {
-                vq[p] = vr[i];
                 wts[p] = sv[i];
-                vsc[p] = ss[i];
                 m = wm_max_nonan(m, sv[i]);
+            }
+            // the cache row of position n_past - 1 is stale (this token's V
+            // is written below, by other threads, with no barrier between):
+            // only the rows before it are copied
+            if (p < pnew) {
+                vq[p] = vr[i];
+                vsc[p] = ss[i];
             }
         }
     }
@@ -305,11 +310,15 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
 
 }  // namespace
 
-void wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_scales,
+// Returns false (nothing launched) for a shape the kernels do not cover:
+// head_dim 64 or 128 (the scores kernel's four waves take head_dim / 64
+// 16-byte segments each), n_past in [1, 4096].
+bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_scales,
                          const int8_t *v_cache, const float *v_scales, float *scores,
                          uint32_t score_stride, float *out, uint32_t n_heads, uint32_t n_kv_heads,
                          uint32_t head_dim, uint32_t n_past, float scale, const float *k_new,
                          const float *v_new, const uint32_t *kv_absmax, hipStream_t s) {
+    if ((head_dim != 64 && head_dim != 128) || n_past == 0 || n_past > 4 * kSvThreads) return false;
     const uint32_t kv_dim = n_kv_heads * head_dim;
     int8_t *k_row = const_cast<int8_t *>(k_cache) + (uint64_t)(n_past - 1) * kv_dim;
     int8_t *v_row = const_cast<int8_t *>(v_cache) + (uint64_t)(n_past - 1) * kv_dim;
@@ -325,4 +334,5 @@ void wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
         hipLaunchKernelGGL(k_attn_softmax_v<2>, grid, dim3(kSvThreads), lds, s, a);
     else  // n_past <= 4096, the models' context limit
         hipLaunchKernelGGL(k_attn_softmax_v<4>, grid, dim3(kSvThreads), lds, s, a);
+    return true;
 }

@@ -492,7 +492,7 @@ void wm_launch_quantize_rows(const float *x, uint32_t ldx, uint32_t n, uint32_t 
                        meta);
 }
 
-void wm_launch_rmsnorm_rows(const wm_norm_rows &a, uint32_t m, hipStream_t s) {
+bool wm_launch_rmsnorm_rows(const wm_norm_rows &a, uint32_t m, hipStream_t s) {
     const size_t lds = (size_t)wm::seq_sum_padded(a.n) * sizeof(float);
     const int per = (int)((a.n + kRowThreads - 1) / kRowThreads);
     const bool gu = a.gu != nullptr;
@@ -500,13 +500,14 @@ void wm_launch_rmsnorm_rows(const wm_norm_rows &a, uint32_t m, hipStream_t s) {
     case P:                                                                                      \
         if (gu) hipLaunchKernelGGL((k_rmsnorm_rows<P, true>), dim3(m), dim3(kRowThreads), lds, s, a); \
         else hipLaunchKernelGGL((k_rmsnorm_rows<P, false>), dim3(m), dim3(kRowThreads), lds, s, a);   \
-        break;
+        return true;
     switch (per) {
         WM_ROWS_CASE(1) WM_ROWS_CASE(2) WM_ROWS_CASE(3) WM_ROWS_CASE(4)
         WM_ROWS_CASE(5) WM_ROWS_CASE(6) WM_ROWS_CASE(7) WM_ROWS_CASE(8)
         default: break;
     }
 #undef WM_ROWS_CASE
+    return false;  // n above 8192: no instantiation
 }
 
 void wm_launch_qkv_rows(const float *y, uint32_t ldy, const float *rope_cos, const float *rope_sin,

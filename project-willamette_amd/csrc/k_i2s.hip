@@ -543,7 +543,8 @@ void wm_launch_i2s_finalize(const int32_t *partial, uint32_t split, uint32_t row
 
 // The fused matvec over the units of `n_tensors` tensors (see k_i2s_fused).
 // Waves per workgroup: n_chunks / 4 (one 4-chunk round each), at most 16.
-void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scales, float *const *outs,
+// Returns false (and launches nothing) when no instantiation fits the shape.
+bool wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scales, float *const *outs,
                          int n_tensors, uint32_t n_chunks, uint32_t groups_per_unit,
                          const wm_fused_norm &norm, const float *rope_cos, const float *rope_sin,
                          uint32_t pos, uint32_t n_rot, uint32_t rope_mask, uint32_t *absmax,
@@ -590,7 +591,7 @@ void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
         const size_t lds = (size_t)n_chunks * 64 + (size_t)W * UG * 64 * 4 + (size_t)UG * 64 * 4 + \
                            sq_bytes;                                                               \
         hipLaunchKernelGGL((k_i2s_fused<MODE, UG, W, NP>), dim3(acc), dim3(W * 64), lds, s, a);    \
-        return;                                                                                    \
+        return true;                                                                               \
     }
 #define WM_FUSED_WS(MODE, UG)                                                                      \
     WM_FUSED_CASE(MODE, UG, 1, 4) WM_FUSED_CASE(MODE, UG, 2, 4) WM_FUSED_CASE(MODE, UG, 4, 4)      \
@@ -600,7 +601,8 @@ void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
     if (mode == WM_FUSED_PLAIN) { WM_FUSED_WS(WM_FUSED_PLAIN, 1) }
     else if (mode == WM_FUSED_GATEUP) { WM_FUSED_WS(WM_FUSED_GATEUP, 2) }
     else if (groups_per_unit == 2) { WM_FUSED_WS(WM_FUSED_ROPE, 2) }
-    else { WM_FUSED_WS(WM_FUSED_ROPE, 1) }
+    else if (groups_per_unit == 1) { WM_FUSED_WS(WM_FUSED_ROPE, 1) }
 #undef WM_FUSED_WS
 #undef WM_FUSED_CASE
+    return false;
 }

@@ -121,7 +121,7 @@ void wm_launch_debug_seq_sum(const float *a, uint32_t n, float *out, hipStream_t
     hipLaunchKernelGGL(k_debug_seq_sum, dim3(1), dim3(1024), lds, s, a, n, out);
 }
 
-void wm_launch_rmsnorm_quant(float *x, const float *res_y, const float *w, uint32_t n, float eps,
+bool wm_launch_rmsnorm_quant(float *x, const float *res_y, const float *w, uint32_t n, float eps,
                              uint8_t *act, wm_act_meta *meta_out, float *y_out,
                              uint32_t *err_flag, uint32_t layer_tag, void *q6k_prep,
                              uint32_t *clear2, hipStream_t s) {
@@ -132,7 +132,7 @@ void wm_launch_rmsnorm_quant(float *x, const float *res_y, const float *w, uint3
         hipLaunchKernelGGL((k_rmsnorm_quant<P, kNormThreads>), dim3(1), dim3(kNormThreads), lds, s, \
                            x, res_y, w, n, eps, act, meta_out, y_out, err_flag, layer_tag,          \
                            (uint8_t *)q6k_prep, clear2);                                            \
-        break;
+        return true;
     switch (per) {  // n <= 16384
         WM_NORM_CASE(1) WM_NORM_CASE(2) WM_NORM_CASE(3) WM_NORM_CASE(4)
         WM_NORM_CASE(5) WM_NORM_CASE(6) WM_NORM_CASE(7) WM_NORM_CASE(8)
@@ -141,6 +141,7 @@ void wm_launch_rmsnorm_quant(float *x, const float *res_y, const float *w, uint3
         default: break;
     }
 #undef WM_NORM_CASE
+    return false;  // n above 16384: no instantiation
 }
 
 void wm_launch_kv_append(const float *k, const float *v, uint32_t kv_dim, uint32_t n_layers,

@@ -23,11 +23,11 @@
 #include "wm_internal.h"
 
 // launchers from k_layer.hip
-void wm_launch_rmsnorm_quant(float *x, const float *res_y, const float *w, uint32_t n, float eps,
+bool wm_launch_rmsnorm_quant(float *x, const float *res_y, const float *w, uint32_t n, float eps,
                              uint8_t *act, wm_act_meta *meta_out, float *y_out,
                              uint32_t *err_flag, uint32_t layer_tag, void *q6k_prep,
                              uint32_t *clear2, hipStream_t s);
-void wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_scales,
+bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_scales,
                          const int8_t *v_cache, const float *v_scales, float *scores,
                          uint32_t score_stride, float *out, uint32_t n_heads, uint32_t n_kv_heads,
                          uint32_t head_dim, uint32_t n_past, float scale, const float *k_new,
@@ -139,8 +139,9 @@ bool model_ready(const wm_model *m) {
 }
 
 // Enqueue the layers + output norm for one token at `pos`; the token id is
-// read from m->dscalars[0] on the device.
-void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_trace_dev) {
+// read from m->dscalars[0] on the device.  Returns false when some launcher
+// had no kernel for the model's shape (nothing after it was enqueued).
+bool enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_trace_dev) {
     const wm_model_config &c = m->cfg;
     hipStream_t s = m->ctx->stream;
     const uint32_t E = c.n_embd, F = c.n_ff, KV = m->kv_dim;
@@ -173,16 +174,20 @@ void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
         wm_i2s_desc qkv[3] = {{L.q.w, L.q.n_groups}, {L.k.w, L.k.n_groups}, {L.v.w, L.v.n_groups}};
         const float qkv_scales[3] = {L.q.scale, L.k.scale, L.v.scale};
         float *qkv_out[3] = {m->q, m->k_new, m->v_new};
-        wm_launch_i2s_fused(WM_FUSED_ROPE, qkv, qkv_scales, qkv_out, 3, n_chunks_e, c.head_dim / 64,
-                            an, m->rope_cos, m->rope_sin, pos, c.n_rot, 0x3u, kv_absmax, s);
+        if (!wm_launch_i2s_fused(WM_FUSED_ROPE, qkv, qkv_scales, qkv_out, 3, n_chunks_e,
+                                 c.head_dim / 64, an, m->rope_cos, m->rope_sin, pos, c.n_rot, 0x3u,
+                                 kv_absmax, s))
+            return false;
         if (layer_trace_dev && l > 0)
             hipMemcpyAsync(layer_trace_dev + (size_t)(l - 1) * E, H[cur], (size_t)E * 4,
                            hipMemcpyDeviceToDevice, s);
         // attention; this token's K/V row goes into the cache on the way
         const size_t lay = (size_t)l * kv->max_seq;
-        wm_launch_attention(m->q, kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV, kv->vs + lay,
-                            m->scores, c.context_length, m->attn_out, c.n_heads, c.n_kv_heads,
-                            c.head_dim, pos + 1, scale, m->k_new, m->v_new, kv_absmax, s);
+        if (!wm_launch_attention(m->q, kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV,
+                                 kv->vs + lay, m->scores, c.context_length, m->attn_out, c.n_heads,
+                                 c.n_kv_heads, c.head_dim, pos + 1, scale, m->k_new, m->v_new,
+                                 kv_absmax, s))
+            return false;
         // attn_sub_norm, then O (the launch also clears the K/V absmax slots)
         wm_fused_norm sn{};
         sn.x = m->attn_out;
@@ -191,8 +196,9 @@ void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
         sn.clear2 = kv_absmax;
         wm_i2s_desc od = {L.o.w, L.o.n_groups};
         float *o_out[1] = {m->proj_out};
-        wm_launch_i2s_fused(WM_FUSED_PLAIN, &od, &L.o.scale, o_out, 1, n_chunks_e, 1, sn, nullptr,
-                            nullptr, 0, 0, 0, nullptr, s);
+        if (!wm_launch_i2s_fused(WM_FUSED_PLAIN, &od, &L.o.scale, o_out, 1, n_chunks_e, 1, sn,
+                                 nullptr, nullptr, 0, 0, 0, nullptr, s))
+            return false;
         // ffn_norm on hidden + wo_out, then gate and up (relu^2 * up)
         wm_fused_norm fn{};
         fn.x = H[cur];
@@ -208,8 +214,9 @@ void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
         // in flight per wave); relu(gate)^2 * up is formed where it is read,
         // in the down matvec's norm
         float *gu_out[2] = {m->h_ff, m->h_up};
-        wm_launch_i2s_fused(WM_FUSED_PLAIN, gu, gu_scales, gu_out, 2, n_chunks_e, 1, fn, nullptr,
-                            nullptr, 0, 0, 0, nullptr, s);
+        if (!wm_launch_i2s_fused(WM_FUSED_PLAIN, gu, gu_scales, gu_out, 2, n_chunks_e, 1, fn,
+                                 nullptr, nullptr, 0, 0, 0, nullptr, s))
+            return false;
         // ffn_sub_norm of relu(gate)^2 * up, then down
         wm_fused_norm dn{};
         dn.x = m->h_ff;
@@ -219,16 +226,20 @@ void enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
         dn.eps = c.rms_eps;
         wm_i2s_desc dd = {L.down.w, L.down.n_groups};
         float *d_out[1] = {m->proj_out};
-        wm_launch_i2s_fused(WM_FUSED_PLAIN, &dd, &L.down.scale, d_out, 1, n_chunks_f, 1, dn, nullptr,
-                            nullptr, 0, 0, 0, nullptr, s);
+        if (!wm_launch_i2s_fused(WM_FUSED_PLAIN, &dd, &L.down.scale, d_out, 1, n_chunks_f, 1, dn,
+                                 nullptr, nullptr, 0, 0, 0, nullptr, s))
+            return false;
     }
     // last residual + output_norm (f32 out, no quantisation)
-    wm_launch_rmsnorm_quant(H[cur], m->proj_out, m->output_norm, E, c.rms_eps, nullptr, nullptr,
-                            m->final_hidden, m->dscalars + 2, c.n_layers,
-                            wm_q6k_prep_area(m->lm_work, c.vocab_size, m->embd_blocks), nullptr, s);
+    if (!wm_launch_rmsnorm_quant(H[cur], m->proj_out, m->output_norm, E, c.rms_eps, nullptr,
+                                 nullptr, m->final_hidden, m->dscalars + 2, c.n_layers,
+                                 wm_q6k_prep_area(m->lm_work, c.vocab_size, m->embd_blocks),
+                                 nullptr, s))
+        return false;
     if (layer_trace_dev)
         hipMemcpyAsync(layer_trace_dev + (size_t)(c.n_layers - 1) * E, H[cur], (size_t)E * 4,
                        hipMemcpyDeviceToDevice, s);
+    return true;
 }
 
 wm_status check_step(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t pos) {
@@ -268,6 +279,10 @@ wm_status finish_step(wm_model *m, wm_kv_cache *kv, uint32_t pos, bool *failed) 
 }
 
 constexpr uint32_t kBatchMaxTokens = 16384;
+
+wm_status rows_unsupported(wm_ctx *ctx) {
+    return wm_set_error(ctx, WM_E_SHAPE, "batch_forward: no row-norm kernel for this model shape");
+}
 
 // Grow the ragged-batch workspace to hold `M` tokens.
 wm_status ensure_batch_ws(wm_model *m, uint32_t M) {
@@ -392,7 +407,7 @@ wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_s
         // [hidden += down of the previous layer], attn_norm, int8
         wm_norm_rows nr{m->b_hidden, E, l ? m->b_ydown : nullptr, E, nullptr, 0, L.attn_norm, E,
                         c.rms_eps, m->b_act, m_pad, m->b_meta, nullptr, 0, l ? err : nullptr, l};
-        wm_launch_rmsnorm_rows(nr, M, s);
+        if (!wm_launch_rmsnorm_rows(nr, M, s)) return rows_unsupported(ctx);
         const wm_gemm_desc qkv[3] = {{L.q.w, L.q.n_groups, E, 0, L.q.scale},
                                      {L.k.w, L.k.n_groups, KV, E, L.k.scale},
                                      {L.v.w, L.v.n_groups, KV, E + KV, L.v.scale}};
@@ -403,27 +418,27 @@ wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_s
                             m->b_scores, m->b_attn, s);
         nr = wm_norm_rows{m->b_attn, E, nullptr, 0, nullptr, 0, L.attn_sub_norm, E, c.rms_eps,
                           m->b_act, m_pad, m->b_meta, nullptr, 0, nullptr, 0};
-        wm_launch_rmsnorm_rows(nr, M, s);
+        if (!wm_launch_rmsnorm_rows(nr, M, s)) return rows_unsupported(ctx);
         const wm_gemm_desc od = {L.o.w, L.o.n_groups, E, 0, L.o.scale};
         wm_launch_i2s_gemm(&od, 1, nce, m->b_act, M, m_pad, m->b_meta, m->b_yo, E, s);
         // hidden += wo, ffn_norm, int8
         nr = wm_norm_rows{m->b_hidden, E, m->b_yo, E, nullptr, 0, L.ffn_norm, E, c.rms_eps,
                           m->b_act, m_pad, m->b_meta, nullptr, 0, nullptr, 0};
-        wm_launch_rmsnorm_rows(nr, M, s);
+        if (!wm_launch_rmsnorm_rows(nr, M, s)) return rows_unsupported(ctx);
         const wm_gemm_desc gu[2] = {{L.gate.w, L.gate.n_groups, F, 0, L.gate.scale},
                                     {L.up.w, L.up.n_groups, F, F, L.up.scale}};
         wm_launch_i2s_gemm(gu, 2, nce, m->b_act, M, m_pad, m->b_meta, m->b_ygu, 2 * F, s);
         // relu^2(gate) * up, ffn_sub_norm, int8
         nr = wm_norm_rows{nullptr, 0, nullptr, 0, m->b_ygu, 2 * F, L.ffn_sub_norm, F, c.rms_eps,
                           m->b_act, m_pad, m->b_meta, nullptr, 0, nullptr, 0};
-        wm_launch_rmsnorm_rows(nr, M, s);
+        if (!wm_launch_rmsnorm_rows(nr, M, s)) return rows_unsupported(ctx);
         const wm_gemm_desc dd = {L.down.w, L.down.n_groups, E, 0, L.down.scale};
         wm_launch_i2s_gemm(&dd, 1, ncf, m->b_act, M, m_pad, m->b_meta, m->b_ydown, E, s);
     }
     // hidden += down of the last layer, output_norm (f32)
     wm_norm_rows fin{m->b_hidden, E, m->b_ydown, E, nullptr, 0, m->output_norm, E, c.rms_eps,
                      nullptr, m_pad, nullptr, m->b_final, E, err, c.n_layers};
-    wm_launch_rmsnorm_rows(fin, M, s);
+    if (!wm_launch_rmsnorm_rows(fin, M, s)) return rows_unsupported(ctx);
     if (next_tokens)
         for (uint32_t i = 0; i < n_seqs; i++)
             wm_launch_q6k_argmax_fast(m->embd, m->embd_blocks, c.vocab_size, m->embd_rowgroups,
@@ -735,7 +750,8 @@ wm_status wm_forward_with_cache(wm_model *m, wm_kv_cache *kv, uint32_t token, ui
         trace_dev = (float *)scratch;
     }
     WM_HIP(ctx, hipMemcpyAsync(m->dscalars, &token, 4, hipMemcpyHostToDevice, ctx->stream));
-    enqueue_forward(m, kv, position, trace_dev);
+    if (!enqueue_forward(m, kv, position, trace_dev))
+        return wm_set_error(ctx, WM_E_SHAPE, "forward_with_cache: no kernel for this model shape");
     WM_HIP(ctx, hipGetLastError());
     bool failed = false;
     if ((st = finish_step(m, kv, position, &failed))) return st;
@@ -756,7 +772,8 @@ wm_status wm_decode_step(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t 
     if (st) return st;
     WM_HIP(ctx, hipSetDevice(ctx->device));
     WM_HIP(ctx, hipMemcpyAsync(m->dscalars, &token, 4, hipMemcpyHostToDevice, ctx->stream));
-    enqueue_forward(m, kv, position, nullptr);
+    if (!enqueue_forward(m, kv, position, nullptr))
+        return wm_set_error(ctx, WM_E_SHAPE, "decode_step: no kernel for this model shape");
     // logits wanted: all of them in the reference's order; else the id-only path
     if (logits_out)
         wm_launch_q6k_logits_argmax(m->embd, m->embd_blocks, m->cfg.vocab_size, m->embd_rowgroups,

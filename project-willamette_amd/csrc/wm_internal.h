@@ -375,7 +375,7 @@ struct wm_fused_norm {
 // workgroup and a fused epilogue (mode WM_FUSED_*): rows of tensor i go to
 // outs[i] as f32; see k_i2s_fused.  groups_per_unit: 1, or head_dim / 64
 // for WM_FUSED_ROPE.
-void wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scales, float *const *outs,
+bool wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scales, float *const *outs,
                          int n_tensors, uint32_t n_chunks, uint32_t groups_per_unit,
                          const wm_fused_norm &norm, const float *rope_cos, const float *rope_sin,
                          uint32_t pos, uint32_t n_rot, uint32_t rope_mask, uint32_t *absmax,
@@ -484,7 +484,7 @@ struct wm_norm_rows {
     float *y_out; uint32_t ldo;
     uint32_t *err_flag; uint32_t tag;
 };
-void wm_launch_rmsnorm_rows(const wm_norm_rows &a, uint32_t m, hipStream_t s);
+bool wm_launch_rmsnorm_rows(const wm_norm_rows &a, uint32_t m, hipStream_t s);
 // RoPE + K/V append per token of a batch for one layer.
 void wm_launch_qkv_rows(const float *y, uint32_t ldy, const float *rope_cos, const float *rope_sin,
                         const wm_batch_tok *tok, uint32_t m, uint32_t layer, uint32_t n_q,

@@ -9,6 +9,10 @@ forward_with_cache in order.  Bar: every row of the batched BitLinear equals
 the single-row SSE2-i8 path bit for bit; each sequence's last hidden, its
 next greedy token and the new cache codes equal the oracle's bit for bit.
 """
+import hashlib
+import json
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -185,3 +189,43 @@ def test_batch_bitnet2b_shape(ctx):
     finally:
         dev.close()
         orm.close()
+
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def test_batch_bitnet2b_ragged16_matches_oracle_fixture(ctx):
+    """The benchmark's ragged step at its own size: BitNet-2B shape, 16
+    sequences with contexts 1002-3842 appending 3-25 tokens each (257 in
+    all), one wm_batch_forward.  Each sequence's next id, the SHA-256 of its
+    last hidden and of its new cache rows must equal the oracle's
+    token-by-token run recorded in tests/golden/bitnet2b_ragged16.json."""
+    gold = json.loads((GOLDEN / "bitnet2b_ragged16.json").read_text())
+    cfg = bs.BITNET_2B
+    wl = bs.ragged_workload(cfg)
+    assert [s["context"] for s in gold["sequences"]] == list(wl.contexts)
+    hm = bs.make_host_model(cfg, bs.master_seed(4))
+    dev = bs.load_device_model(ctx, hm)
+    kvs = []
+    for i, c in enumerate(wl.contexts):
+        kv = dev.kv_cache(cfg.context_length)
+        k, v = bs.kv_prefill(cfg, wl.prefill_seeds[i], c)
+        kv.append_positions(k, v)
+        del k, v
+        kvs.append(kv)
+    hidden, nxt = dev.batch_forward(kvs, wl.new_tokens)
+    for i, rec in enumerate(gold["sequences"]):
+        c, n = wl.contexts[i], len(wl.new_tokens[i])
+        assert kvs[i].position == c + n
+        assert nxt[i] == rec["next_id"], f"sequence {i}: next id"
+        assert hashlib.sha256(np.ascontiguousarray(hidden[i], np.float32).tobytes()).hexdigest() == \
+            rec["hidden_sha256"], f"sequence {i}: last hidden"
+        h = hashlib.sha256()
+        for layer in range(cfg.n_layers):
+            k, ks, v, vs = kvs[i].read_raw(layer, c + n)
+            for a in (k[c:], ks[c:], v[c:], vs[c:]):
+                h.update(np.ascontiguousarray(a).tobytes())
+        assert h.hexdigest() == rec["kv_sha256"], f"sequence {i}: new cache rows"
+    for kv in kvs:
+        kv.close()
+    dev.close()

@@ -180,3 +180,51 @@ def test_bitnet2b_decode64_matches_oracle_fixture(ctx):
         tok, pos = nxt, pos + 1
     assert ids == gold["ids"]
     assert shas == gold["logits_sha256"]
+    # the id-only lm-head (bounded pass + exact rescoring), the path the
+    # benchmark times, over the same 64 steps from the rolled-back cache
+    dkv.rollback(gold["prefill"])
+    tok, pos = gold["start_token"], gold["prefill"]
+    fast = []
+    for step in range(gold["steps"]):
+        _, _, nxt = dkv.decode_step(tok, pos, want_logits=False)
+        fast.append(nxt)
+        tok, pos = nxt, pos + 1
+    assert fast == gold["ids"]
+
+
+LONG = bs.BitNetConfig(n_layers=2, n_embd=256, n_ff=384, n_heads=2, n_kv_heads=1, head_dim=128,
+                       vocab=500, context_length=4096)
+
+
+@pytest.mark.parametrize("n_pre", [3500, 4092])
+def test_long_context_decode_bit_exact(ctx, n_pre):
+    """Positions past 2048, up to the 4096-position context (the attention
+    kernels' largest instantiation, above 64 KB of LDS), with a stale cache
+    row at the decoded position: the row is first written with other values
+    and rolled back, so the step must use this token's K/V, not the row's
+    old contents (n_pre % 1024 is in [64, 1024): the row is loaded by a
+    wave other than the one that writes the new V)."""
+    cfg = LONG
+    hm = bs.make_host_model(cfg, seed=31)
+    dev = bs.load_device_model(ctx, hm)
+    orm = OracleModel(hm)
+    k, v = bs.kv_prefill(cfg, seed=32, n_pos=n_pre + 1)
+    dkv, okv = dev.kv_cache(cfg.context_length), orm.kv(cfg.context_length)
+    dkv.append_positions(k, v)  # one row past the prefill ...
+    dkv.rollback(n_pre)         # ... left behind as a stale row
+    okv.append_positions(k[:n_pre], v[:n_pre])
+    tok, pos = 17, n_pre
+    while pos < min(n_pre + 12, cfg.context_length):
+        h, logits, nxt = dkv.decode_step(tok, pos)
+        rh = okv.forward(tok, pos)
+        rlogits, rnxt = okv.logits_argmax(rh)
+        assert bits_equal(h, rh) and bits_equal(logits, rlogits), f"position {pos}"
+        assert nxt == rnxt
+        tok, pos = nxt, pos + 1
+    for l in range(cfg.n_layers):
+        dk, dks, dv, dvs = dkv.read_raw(l, pos)
+        ok, oks, ov, ovs = okv.read_raw(l, pos)
+        assert np.array_equal(dk[n_pre:], ok[n_pre:]) and np.array_equal(dv[n_pre:], ov[n_pre:])
+        assert bits_equal(dks, oks) and bits_equal(dvs, ovs)
+    dev.close()
+    orm.close()

@@ -1,0 +1,270 @@
+"""CPU tests that pin the oracle's composition: its attention (or_sdpa), the
+layer order inside or_forward_with_cache, and the greedy loop.
+
+The leaves (quantisers, BitLinear, Q6_K, RMSNorm, RoPE, softmax, KV
+quantiser) are pinned in test_oracle.py.  Here the oracle's model is checked
+against the reference's own known answers (attention at position 0 returns V
+of each query head's kv head, src/model/attention.rs:397-414; the zero-weight
+closed form and the EOS / position / rollback rules of
+tests/synthetic_model.rs:378-550 and src/model/cached_forward.rs:256-259) and
+against tests/np_bitnet.py, an independent float64 restatement of the
+forward.  Each comparison with np_bitnet also runs with one planted
+composition mistake (wrong kv-head map, attn_sub_norm skipped, O residual
+dropped, adjacent RoPE pairs, ReLU instead of ReLU^2, no RoPE on K) and
+requires that mistake to miss the tolerance by a wide margin, so the
+tolerance is known to be tight enough to catch it.
+"""
+import numpy as np
+import pytest
+
+import bitnet_synth as bs
+import np_bitnet as nb
+import oracle.oracle as orc
+from oracle.oracle_model import OracleModel
+
+f32 = np.float32
+
+GQA4 = bs.BitNetConfig(n_layers=3, n_embd=256, n_ff=384, n_heads=8, n_kv_heads=2, head_dim=32,
+                       vocab=300, context_length=64)
+MHA1 = bs.BitNetConfig(n_layers=2, n_embd=256, n_ff=512, n_heads=4, n_kv_heads=1, head_dim=64,
+                       vocab=257, context_length=64)
+
+MISTAKES = {
+    "kv_head_mod": nb.Mistakes(kv_head_of="mod"),
+    "no_attn_sub_norm": nb.Mistakes(sub_norm=False),
+    "no_o_residual": nb.Mistakes(o_residual=False),
+    "adjacent_rope_pairs": nb.Mistakes(rope_pairs="adjacent"),
+    "relu_not_squared": nb.Mistakes(relu_square=False),
+    "no_rope_on_k": nb.Mistakes(rope_on_k=False),
+}
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+
+def test_sdpa_position_zero_returns_v_per_kv_head():
+    """src/model/attention.rs:397-414: 4 query heads, 2 kv heads, head_dim 2;
+    one position, so every softmax is [1.0] and head h returns V of kv head
+    h // 2 exactly."""
+    q = np.ones(8, np.float32)
+    k = np.full(4, 0.1, np.float32)
+    v = np.array([5.0, 6.0, 70.0, 80.0], np.float32)
+    out = orc.sdpa(q, k, v, n_heads=4, n_kv_heads=2, head_dim=2)
+    assert out.tolist() == [5.0, 6.0, 5.0, 6.0, 70.0, 80.0, 70.0, 80.0]
+
+
+def np_attention(q, K, V, n_heads, n_kv_heads, hd, head_of=lambda h, g, nkv: h // g):
+    g = n_heads // n_kv_heads
+    K = K.astype(np.float64).reshape(-1, n_kv_heads, hd)
+    V = V.astype(np.float64).reshape(-1, n_kv_heads, hd)
+    out = np.empty((n_heads, hd))
+    for h in range(n_heads):
+        kvh = head_of(h, g, n_kv_heads)
+        s = K[:, kvh, :] @ q.astype(np.float64).reshape(n_heads, hd)[h] / np.sqrt(hd)
+        w = np.exp(s - s.max())
+        out[h] = (w / w.sum()) @ V[:, kvh, :]
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd,n_past", [(8, 2, 16, 37), (20, 5, 128, 300), (4, 4, 32, 1)])
+def test_sdpa_matches_float64_attention(n_heads, n_kv, hd, n_past):
+    rng = np.random.default_rng(n_heads * 100 + n_past)
+    q = rng.standard_normal(n_heads * hd).astype(np.float32) * np.float32(2.0)
+    K = rng.standard_normal((n_past, n_kv * hd)).astype(np.float32)
+    V = rng.standard_normal((n_past, n_kv * hd)).astype(np.float32)
+    got = orc.sdpa(q, K, V, n_heads, n_kv, hd).astype(np.float64)
+    ref = np_attention(q, K, V, n_heads, n_kv, hd)
+    tol = 1e-5 * np.abs(ref).max()
+    assert np.abs(got - ref).max() <= tol
+    if n_kv > 1 and n_heads > n_kv:  # the mapping h % n_kv would not pass
+        wrong = np_attention(q, K, V, n_heads, n_kv, hd, head_of=lambda h, g, nkv: h % nkv)
+        assert np.abs(got - wrong).max() > 1000 * tol
+
+
+def test_sdpa_peaked_softmax_and_zero_query():
+    """A zero query gives equal weights (the mean of V); a dominant score
+    gives that position's V."""
+    rng = np.random.default_rng(3)
+    V = rng.standard_normal((10, 8)).astype(np.float32)
+    K = rng.standard_normal((10, 8)).astype(np.float32)
+    out = orc.sdpa(np.zeros(8, np.float32), K, V, 1, 1, 8)
+    assert np.allclose(out, V.astype(np.float64).mean(axis=0), atol=1e-6)
+    K2 = np.zeros((10, 8), np.float32)
+    K2[6] = 1000.0
+    out = orc.sdpa(np.ones(8, np.float32), K2, V, 1, 1, 8)
+    assert np.array_equal(out, V[6])
+
+
+# ---------------------------------------------------------------------------
+# layer composition against the float64 restatement
+# ---------------------------------------------------------------------------
+
+def teacher_forced_deviation(hm, mistakes, n_pre, tokens):
+    """Runs the oracle, then every layer of np_bitnet on the oracle's input
+    hidden and cache rows.  Returns (largest relative deviation of a layer's
+    output or the final hidden, largest distance in codes between np_bitnet's
+    new K/V before quantisation and the oracle's new cache row)."""
+    cfg = hm.cfg
+    orm = OracleModel(hm)
+    okv = orm.kv(cfg.context_length)
+    if n_pre:
+        k, v = bs.kv_prefill(cfg, seed=17, n_pos=n_pre)
+        okv.append_positions(k, v)
+    npm = nb.NpModel(hm, mistakes)
+    dev, kv_codes = 0.0, 0.0
+    for i, tok in enumerate(tokens):
+        pos = n_pre + i
+        rh, rtr = okv.forward(tok, pos, trace=True)
+        x = npm.embed(tok)
+        for l in range(cfg.n_layers):
+            kk, ks, vv, vs = okv.read_raw(l, pos + 1)
+            K = kk.astype(np.float64) * ks[:, None]
+            V = vv.astype(np.float64) * vs[:, None]
+            npm.k[l], npm.v[l] = list(K[:pos]), list(V[:pos])
+            xo, kn, vn = npm.layer(l, x, pos, kv_row=(K[pos], V[pos]))
+            dev = max(dev, np.abs(xo - rtr[l]).max() / np.abs(rtr[l]).max())
+            kv_codes = max(kv_codes, np.abs(kn - K[pos]).max() / ks[pos],
+                           np.abs(vn - V[pos]).max() / vs[pos])
+            x = rtr[l].astype(np.float64)
+        dev = max(dev, np.abs(npm.output(x) - rh).max() / np.abs(rh).max())
+    orm.close()
+    return dev, kv_codes
+
+
+LAYER_TOL = 1e-5     # relative max-abs deviation of a layer's output
+KV_CODE_TOL = 0.501  # a value rounds to its nearest code: at most half a step away
+
+
+@pytest.mark.parametrize("cfg,n_pre", [(GQA4, 12), (MHA1, 5)], ids=["gqa4_prefill12", "mha1_prefill5"])
+def test_layer_composition_matches_float64_model(cfg, n_pre):
+    hm = bs.make_host_model(cfg, seed=4242)
+    dev, kv_codes = teacher_forced_deviation(hm, None, n_pre, [5, 77, 123, 9, 250, 1])
+    assert dev <= LAYER_TOL, f"oracle layer output off the float64 model by {dev:.3g}"
+    assert kv_codes <= KV_CODE_TOL, f"new K/V row {kv_codes:.3f} codes from the float64 model"
+
+
+@pytest.mark.parametrize("name", list(MISTAKES))
+def test_planted_composition_mistake_is_caught(name):
+    hm = bs.make_host_model(GQA4, seed=4242)
+    dev, kv_codes = teacher_forced_deviation(hm, MISTAKES[name], 12, [5, 77, 123])
+    assert dev > 1000 * LAYER_TOL or kv_codes > 10 * KV_CODE_TOL, name
+
+
+def test_forward_from_empty_cache_matches_float64_model():
+    """Free-running (no teacher forcing) from an empty cache: every layer's
+    hidden and the final hidden agree with the float64 model."""
+    hm = bs.make_host_model(GQA4, seed=4242)
+    orm = OracleModel(hm)
+    okv = orm.kv(GQA4.context_length)
+    npm = nb.NpModel(hm)
+    for pos, tok in enumerate([5, 77, 123, 9, 250, 1]):
+        rh, rtr = okv.forward(tok, pos, trace=True)
+        h, tr = npm.forward(tok, pos)
+        for l in range(GQA4.n_layers):
+            assert np.abs(tr[l] - rtr[l]).max() <= LAYER_TOL * np.abs(rtr[l]).max(), (pos, l)
+        assert np.abs(h - rh).max() <= LAYER_TOL * np.abs(rh).max()
+    orm.close()
+
+
+def test_logits_match_float64_lm_head():
+    hm = bs.make_host_model(GQA4, seed=4242)
+    orm = OracleModel(hm)
+    okv = orm.kv(GQA4.context_length)
+    h = okv.forward(11, 0)
+    logits, nxt = okv.logits_argmax(h)
+    ref = nb.NpModel(hm).logits(h.astype(np.float64))
+    assert np.abs(logits - ref).max() <= 1e-5 * np.abs(ref).max()
+    top2 = np.sort(ref)[-2:]
+    assert top2[1] - top2[0] > 1e-3 * np.abs(ref).max() and nxt == int(np.argmax(ref))
+    orm.close()
+
+
+# ---------------------------------------------------------------------------
+# generation loop, positions, EOS, rollback
+# ---------------------------------------------------------------------------
+
+def test_greedy_equals_forward_logits_argmax_loop():
+    """or_greedy_generate is the loop of generate.rs:111-189: prefill the
+    prompt, then logits -> argmax -> forward on the new token."""
+    hm = bs.make_host_model(GQA4, seed=99)
+    orm = OracleModel(hm)
+    a, b = orm.kv(GQA4.context_length), orm.kv(GQA4.context_length)
+    ids = a.greedy([3, 1, 4], max_new=10)
+    pos = 0
+    for t in [3, 1, 4]:
+        h = b.forward(t, pos)
+        pos += 1
+    loop = []
+    for _ in range(10):
+        _, nxt = b.logits_argmax(h)
+        loop.append(nxt)
+        h = b.forward(nxt, pos)
+        pos += 1
+    assert ids == loop and len(ids) == 10
+    assert a.position == 3 + 9  # the last id is returned, not fed back
+    orm.close()
+
+
+def test_greedy_eos_rules():
+    """tests/synthetic_model.rs:530-550: an EOS first token yields nothing; an
+    EOS later truncates the ids before it."""
+    hm = bs.make_host_model(GQA4, seed=99)
+    orm = OracleModel(hm)
+    ids = orm.kv(64).greedy([3, 1, 4], max_new=10)
+    assert orm.kv(64).greedy([3, 1, 4], max_new=10, eos=ids[0]) == []
+    k = next(i for i in range(1, 10) if ids[i] not in ids[:i])
+    assert orm.kv(64).greedy([3, 1, 4], max_new=10, eos=ids[k]) == ids[:k]
+    orm.close()
+
+
+def test_positions_and_rollback():
+    """tests/synthetic_model.rs:393-411 (two positions advance the cache to 2),
+    cached_forward.rs:271-305 (tokens in order), :256-259 and :511-521
+    (a non-finite hidden rolls the cache back)."""
+    hm = bs.make_host_model(GQA4, seed=5)
+    orm = OracleModel(hm)
+    kv = orm.kv(8)
+    h0 = kv.forward(0, 0)
+    h1 = kv.forward(1, 1)
+    assert kv.position == 2 and np.all(np.isfinite(h0)) and np.all(np.isfinite(h1))
+    with pytest.raises(RuntimeError):
+        kv.forward(1, 5)
+    with pytest.raises(RuntimeError):
+        kv.forward(GQA4.vocab, 2)
+    assert kv.position == 2
+    orm.close()
+    hm.layers[1].norms["ffn_sub_norm"][:] = np.inf
+    bad = OracleModel(hm)
+    bkv = bad.kv(8)
+    with pytest.raises(RuntimeError):
+        bkv.forward(0, 0)
+    assert bkv.position == 0
+    bad.close()
+
+
+def test_zero_weight_model_closed_form():
+    """tests/synthetic_model.rs:378-391 with values: all-zero ternary weights
+    and unit norms make every BitLinear output exactly 0, so the hidden stays
+    the all-ones embedding row and output_norm gives 1/sqrt(1 + eps); every
+    logit is then equal and the argmax is token 0."""
+    cfg = GQA4
+    hm = bs.make_host_model(cfg, seed=6)
+    for hl in hm.layers:
+        for r in bs.ROLES:
+            hl.packed[r][:] = 0x55
+        for n in bs.NORMS:
+            hl.norms[n][:] = 1.0
+    ones = np.concatenate([np.full(128, 0x11, np.uint8), np.full(64, 0xAA, np.uint8),
+                           np.full(16, 1, np.uint8), np.array([0x00, 0x3C], np.uint8)])
+    hm.token_embd = np.tile(ones, cfg.vocab * (cfg.n_embd // 256))
+    hm.output_norm[:] = 1.0
+    orm = OracleModel(hm)
+    kv = orm.kv(8)
+    expect = f32(1.0) * (f32(1.0) / np.sqrt(f32(1.0) + f32(1e-5)))
+    for pos in range(3):
+        h, tr = kv.forward(3, pos, trace=True)
+        assert np.all(tr == 1.0) and np.all(h == expect)
+    logits, nxt = kv.logits_argmax(h)
+    assert np.all(logits == logits[0]) and nxt == 0
+    orm.close()
