@@ -118,6 +118,18 @@ wm_status wm_bitlinear_i2s_matvec_f32_multi_dev(wm_ctx *ctx, const wm_tensor *co
                                                 uint32_t n_copies, const float *d_input,
                                                 float *d_outputs);
 
+/* No counterpart in the reference: wm_bitlinear_i2s_matvec_f32_dev without
+ * any device allocation, for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Its
+ * working memory is a fixed 4 MiB device array per GPU, held until the
+ * process ends; shapes whose activation codes, scale record and partial dots
+ * need more (far above BitNet-2B's, e.g. more than 65536 output rows) are
+ * rejected with WM_E_SHAPE.  Calls that overlap on one GPU (other streams or
+ * contexts) share that array and race.  Output identical to
+ * wm_bitlinear_i2s_matvec_f32_dev. */
+wm_status wm_bitlinear_i2s_matvec_f32_dev_noalloc(wm_ctx *ctx, const wm_tensor *w,
+                                                  const float *d_input, float *d_output);
+
 /* Batched BitLinear: m activation rows x [m][in_dim] (device), each row
  * quantised on its own (per-token absmax int8, src/model/bitlinear_sse2.rs:285-304),
  * y[m][out_dim] (device).  Row r of y is bit-identical to

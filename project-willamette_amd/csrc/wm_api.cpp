@@ -74,6 +74,11 @@ wm_status wm_ctx_create(int device, wm_ctx **out) {
         delete c;
         return WM_E_HIP;
     }
+    if (wm_noalloc_setup(c) != WM_OK) {
+        hipStreamDestroy(c->stream);
+        delete c;
+        return WM_E_HIP;
+    }
     *out = c;
     return WM_OK;
 }

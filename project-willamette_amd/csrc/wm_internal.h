@@ -40,6 +40,9 @@ struct wm_ctx {
     size_t multi_bytes = 0;
     std::vector<const void *> multi_ptrs;
     std::vector<float> multi_scales;
+    // Device address, on this context's device, of the file-scope scratch
+    // array of wm_bitlinear_i2s_matvec_f32_dev_noalloc (wm_noalloc.hip).
+    void *noalloc_scratch = nullptr;
 };
 
 // Objects created on a context keep their own device id: destroying them
@@ -68,6 +71,8 @@ wm_status wm_hip_error(wm_ctx *ctx, hipError_t e, const char *what);
         if (e_ != hipSuccess) return wm_hip_error((ctx), e_, #expr); \
     } while (0)
 
+// Looks up ctx->noalloc_scratch (called by wm_ctx_create, device current).
+wm_status wm_noalloc_setup(wm_ctx *ctx);
 // Grows ctx->scratch to at least `bytes` and returns it.
 wm_status wm_ctx_scratch(wm_ctx *ctx, size_t bytes, void **out);
 wm_status wm_ctx_pinned(wm_ctx *ctx, size_t bytes, void **out);
