@@ -136,14 +136,19 @@ static_assert(kSvTile * (kSvDims / 4) == kSvThreads - 64, "one 4-dim unit per pr
 // the 16 dimensions d0..d0+15 of head h.  Grid (n_heads, head_dim / 16).
 //
 // The workgroup first pulls its whole V slice (n_past x 16 int8: one
-// coalesced 16-byte load per position, 64 KB at 4096 positions), the scores
-// and the V scales into LDS with all loads in flight at once.  All 16 waves
-// then compute the softmax: max, exp, the exact sequential sum
-// (seq_sum_block_owned) and the normalisation.  Then, tile by tile, waves
-// 1-15 write products w_p * v_p[d] (4 dims of one position per thread)
-// while lanes 0-15 of wave 0 add the previous tile, one chain per
-// dimension, in position order.  Position n_past - 1 uses this token's V,
-// quantised from v_new (workgroup (0, 0) also writes the cache row).
+// coalesced 16-byte load per position, 64 KB at 4096 positions) and the V
+// scales into LDS and its head's scores into registers, all loads in flight
+// at once.  All 16 waves then compute the softmax: max, exp, and the list of
+// positions whose exp is not exactly 0 (kept in position order; a zero term
+// changes neither the exp sum nor any output sum, so the reference's sums
+// over all positions equal the sums over this list).  The exp sum runs over
+// the list, left to right (one wave for a short list, the workgroup's exact
+// sum seq_sum_block_owned for a long one), then the normalisation.  Then,
+// tile by tile, waves 1-15 write products w_p * v_p[d] (4 dims of one listed
+// position per thread) while lanes 0-15 of wave 0 add the previous tile, one
+// chain per dimension, in position order.  Position n_past - 1 uses this
+// token's V, quantised from v_new (workgroup (0, 0) also writes the cache
+// row).
 // The largest of the workgroup's values (none of them NaN; -inf where a
 // thread has none), in every thread: a DPP reduction per wave (-inf fills
 // the lanes a shift leaves empty), one LDS exchange.  `red` is not in use
@@ -168,16 +173,19 @@ __device__ __forceinline__ float sv_block_max(float v, float *red) {
     return m;
 }
 
-template <int MAXM>  // n_past <= MAXM * kSvThreads (the exact sum's terms per thread)
+template <int MAXM>  // n_past <= MAXM * kSvThreads
 __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
     extern __shared__ __align__(16) float sm[];
     const uint32_t n = a.n_past, pnew = n - 1;
     const uint32_t npad = (n + 3) & ~3u;
-    float *wts = sm;                                      // [seq_sum_padded(n)]
-    float *vsc = wts + wm::seq_sum_padded(n);             // [npad]
+    float *cval = sm;                                     // [seq_sum_padded(n)] nonzero exps, then weights
+    float *vsc = cval + wm::seq_sum_padded(n);            // [npad]
     int4 *vq = reinterpret_cast<int4 *>(vsc + npad);      // [npad] x 16 int8
     float *prod = reinterpret_cast<float *>(vq + npad);   // [2][kSvDims][kSvStride]
+    uint16_t *cidx = reinterpret_cast<uint16_t *>(prod + 2 * kSvDims * kSvStride);  // [npad]
     __shared__ float red[16];
+    __shared__ int wcnt[MAXM * 16];
+    __shared__ float ssum;
     __shared__ wm::seq_block_scratch seq_scratch;
     __shared__ uint64_t exp_tab[32];
     const uint32_t h = blockIdx.x, d0 = blockIdx.y * kSvDims, tid = threadIdx.x;
@@ -188,26 +196,25 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
     const float vabs = __uint_as_float(a.kv_absmax[1]);
     const bool v_writer = h == 0 && blockIdx.y == 0;
     if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
-    // 1. the loads, 4 positions per thread per round, indices clamped so none
-    //    is conditional and all of a round are in flight together
+    // 1. the loads: thread t takes positions t + i * kSvThreads, its scores in
+    //    registers, the V slice and scales into LDS; indices clamped so that
+    //    every load is unconditional and all of them are in flight together
+    float sv[MAXM];
     float m = -INFINITY;
-    for (uint32_t base = 0; base < n; base += 4 * kSvThreads) {
-        int4 vr[4];
-        float sv[4], ss[4];
+    {
+        int4 vr[MAXM];
+        float ss[MAXM];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t p = min(base + tid + (uint32_t)i * kSvThreads, n - 1);
+        for (int i = 0; i < MAXM; i++) {
+            const uint32_t p = min(tid + (uint32_t)i * kSvThreads, n - 1);
             vr[i] = *reinterpret_cast<const int4 *>(vseg + (uint64_t)p * a.kv_dim);
             sv[i] = sc[p];
             ss[i] = a.v_scales[p];
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t p = base + tid + (uint32_t)i * kSvThreads;
-            if (p < n) {
-                wts[p] = sv[i];
-                m = wm_max_nonan(m, sv[i]);
-            }
+        for (int i = 0; i < MAXM; i++) {
+            const uint32_t p = tid + (uint32_t)i * kSvThreads;
+            if (p < n) m = wm_max_nonan(m, sv[i]);
             // the cache row of position n_past - 1 is stale (this token's V
             // is written below, by other threads, with no barrier between):
             // only the rows before it are copied
@@ -230,26 +237,68 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
     if (!isfinite(mx)) {  // every weight becomes 0 -> output stays 0
         if (tid < kSvDims) out[tid] = 0.0f;
     } else {
-        // exp(v - max) (attention.rs:62), each thread on its own positions
-        for (uint32_t p = tid; p < n; p += kSvThreads) wts[p] = wm::expf_glibc(wts[p] - mx, exp_tab);
+        // exp(v - max) (attention.rs:62), then the positions whose exp is not
+        // exactly 0, compacted in position order: a zero exp adds nothing to
+        // the sum (s + 0 = s for every s the sum can hold), its weight
+        // 0 * inv is 0 and its products w * v_p[d] are +-0, which leave every
+        // output sum as it was (it starts at +0 and is never -0), so the
+        // sum and the outputs over the compacted list are the reference's
+        float e[MAXM];
+        uint64_t mask[MAXM];
+#pragma unroll
+        for (int i = 0; i < MAXM; i++) {
+            const uint32_t p = tid + (uint32_t)i * kSvThreads;
+            e[i] = p < n ? wm::expf_glibc(sv[i] - mx, exp_tab) : 0.0f;
+            mask[i] = __builtin_amdgcn_ballot_w64(e[i] != 0.0f);
+            if (lane == 0) wcnt[i * 16 + wid] = __builtin_popcountll(mask[i]);
+        }
         wm_sync_lds();
-        // Σ exp left to right (attention.rs:63-66), exactly; thread t takes
-        // the terms t*m .. t*m+m-1
-        float ev[MAXM];
-        {
-            const uint32_t mm = (n + kSvThreads - 1) / kSvThreads, k0 = tid * mm;
+        // exclusive offsets of the (round, wave) groups, in position order
+        const int c = lane < (uint32_t)(MAXM * 16) ? wcnt[lane] : 0;
+        const int cinc = wm_wave_scan_i32(c);
+        const uint32_t count = (uint32_t)__builtin_amdgcn_readlane(cinc, 63);
+        const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+        for (int i = 0; i < MAXM; i++) {
+            const int base = __builtin_amdgcn_readlane(cinc - c, i * 16 + (int)wid);
+            if (e[i] != 0.0f) {
+                const int k = base + __builtin_popcountll(mask[i] & below);
+                cval[k] = e[i];
+                cidx[k] = (uint16_t)(tid + (uint32_t)i * kSvThreads);
+            }
+        }
+        wm_sync_lds();
+        // Σ exp left to right (attention.rs:63-66) over the compacted terms:
+        // a short list by one wave, one add at a time; a long one by the
+        // workgroup's exact sum (thread t takes terms t*m .. t*m+m-1)
+        float sum;
+        if (count <= 64) {
+            if (wid == 0) {
+                const float v = lane < count ? cval[lane] : 0.0f;
+                float s;
+                asm volatile("v_mov_b32 %0, 0" : "=v"(s));
+                for (uint32_t k = 0; k < count; k++)
+                    s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)k));
+                if (lane == 0) ssum = s;
+            }
+            wm_sync_lds();
+            sum = ssum;
+        } else {
+            float ev[MAXM];
+            const uint32_t mm = (count + kSvThreads - 1) / kSvThreads, k0 = tid * mm;
 #pragma unroll
             for (int j = 0; j < MAXM; j++)
-                ev[j] = ((uint32_t)j < mm && k0 + (uint32_t)j < n) ? wts[k0 + j] : 0.0f;
+                ev[j] = ((uint32_t)j < mm && k0 + (uint32_t)j < count) ? cval[k0 + j] : 0.0f;
+            sum = wm::seq_sum_block_owned<MAXM, kSvThreads>(ev, count, cval, &seq_scratch);
         }
-        const float sum = wm::seq_sum_block_owned<MAXM, kSvThreads>(ev, n, wts, &seq_scratch);
         if (sum > 0.0f) {
             const float inv = 1.0f / sum;
-            for (uint32_t p = tid; p < n; p += kSvThreads) wts[p] = wts[p] * inv;
+            for (uint32_t k = tid; k < count; k += kSvThreads) cval[k] = cval[k] * inv;
         }
         wm_sync_lds();
-        // 3. products of tile t (waves 1-15) while wave 0 adds tile t - 1
-        const uint32_t n_tiles = (n + kSvTile - 1) / kSvTile;
+        // 3. products of tile t (waves 1-15) while wave 0 adds tile t - 1,
+        //    over the compacted positions in order
+        const uint32_t n_tiles = (count + kSvTile - 1) / kSvTile;
         const uint32_t pt = tid - 64, dq = pt / kSvTile, pl = pt % kSvTile;  // producer unit
         float acc = 0.0f;
         // the chains are the critical path: wave 0's instructions go first
@@ -258,11 +307,12 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
         for (uint32_t t = 0; t <= n_tiles; t++) {
             if (wid >= 1) {
                 if (t < n_tiles) {
-                    const uint32_t p = t * kSvTile + pl;
-                    if (p < n) {
+                    const uint32_t k = t * kSvTile + pl;
+                    if (k < count) {
+                        const uint32_t p = cidx[k];
                         float *dst = prod + (t & 1) * (kSvDims * kSvStride) + dq * 4 * kSvStride + pl;
                         const uint32_t word = reinterpret_cast<const uint32_t *>(vq + p)[dq];
-                        const float w = wts[p], s = vsc[p];
+                        const float w = cval[k], s = vsc[p];
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
                             const float vd = (float)(int8_t)(word >> (8 * i)) * s;  // read_into: q * scale
@@ -272,8 +322,8 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
                 }
             } else if (lane < kSvDims && t > 0) {
                 const float *src = prod + ((t - 1) & 1) * (kSvDims * kSvStride) + lane * kSvStride;
-                const uint32_t p0 = (t - 1) * kSvTile;
-                const uint32_t tn = n - p0 < (uint32_t)kSvTile ? n - p0 : (uint32_t)kSvTile;
+                const uint32_t k0 = (t - 1) * kSvTile;
+                const uint32_t tn = count - k0 < (uint32_t)kSvTile ? count - k0 : (uint32_t)kSvTile;
                 if (tn == (uint32_t)kSvTile) {
                     // 24 products per step, the next step's reads issued before this step's adds
                     constexpr int kC = 6, kSteps = kSvTile / (4 * kC);
@@ -281,20 +331,25 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
 #pragma unroll
                     for (int i = 0; i < kC; i++) f[0][i] = *reinterpret_cast<const float4 *>(src + 4 * i);
 #pragma unroll
-                    for (int c = 0; c < kSteps; c++) {
-                        if (c + 1 < kSteps) {
+                    for (int c4 = 0; c4 < kSteps; c4++) {
+                        if (c4 + 1 < kSteps) {
 #pragma unroll
                             for (int i = 0; i < kC; i++)
-                                f[(c + 1) & 1][i] = *reinterpret_cast<const float4 *>(src + (c + 1) * 4 * kC + 4 * i);
+                                f[(c4 + 1) & 1][i] = *reinterpret_cast<const float4 *>(src + (c4 + 1) * 4 * kC + 4 * i);
                         }
 #pragma unroll
                         for (int i = 0; i < kC; i++) {
-                            const float4 g = f[c & 1][i];
+                            const float4 g = f[c4 & 1][i];
                             acc = acc + g.x; acc = acc + g.y; acc = acc + g.z; acc = acc + g.w;
                         }
                     }
                 } else {
-                    for (uint32_t q = 0; q < tn; q++) acc = acc + src[q];
+                    uint32_t q = 0;
+                    for (; q + 4 <= tn; q += 4) {
+                        const float4 g = *reinterpret_cast<const float4 *>(src + q);
+                        acc = acc + g.x; acc = acc + g.y; acc = acc + g.z; acc = acc + g.w;
+                    }
+                    for (; q < tn; q++) acc = acc + src[q];
                 }
             }
             wm_sync_lds();
@@ -328,7 +383,7 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
     hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, (n_past - 1 + 63) / 64 + 1), dim3(kScThreads), 0, s, a);
     const size_t npad = ((size_t)n_past + 3) & ~(size_t)3;
     const size_t lds = (size_t)wm::seq_sum_padded(n_past) * 4 + npad * (4 + 16) +
-                       (size_t)2 * kSvDims * kSvStride * 4;
+                       (size_t)2 * kSvDims * kSvStride * 4 + npad * 2;
     const dim3 grid(n_heads, head_dim / kSvDims);
     if (n_past <= 2 * kSvThreads)
         hipLaunchKernelGGL(k_attn_softmax_v<2>, grid, dim3(kSvThreads), lds, s, a);

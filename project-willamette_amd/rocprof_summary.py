@@ -6,6 +6,13 @@
 
 `stats` prints the per-kernel table of a --kernel-trace --stats run.
 
+`roles` splits a --kernel-trace run's dispatches (run_kernel_trace.csv) of
+the decode step into per-role averages: every dispatch gets the name of its
+kernel plus its ordinal since the last dispatch of the `--anchor` kernel (the
+first kernel of a layer), so the same kernel launched twice per layer shows
+as two rows; the mean gap between a dispatch's start and the previous one's
+end is printed beside it.
+
 `traffic` turns two counter passes (--pmc FETCH_SIZE, then --pmc
 WRITE_SIZE; both report KiB per dispatch) into HBM bytes per launch of one
 kernel.  Each counter is scaled by what it reads for the largest
@@ -58,6 +65,40 @@ def per_dispatch_kib(rows, kernel: str):
     return sum(k) / len(k), len(k), sum(c) / len(c)
 
 
+def roles(path: str, anchor: str, skip: int) -> str:
+    rows = list(csv.DictReader(open(path)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    first = next((i for i, r in enumerate(rows) if anchor in r["Kernel_Name"]), None)
+    if first is None:
+        raise SystemExit(f"no dispatch of {anchor!r}")
+    acc, order = {}, []
+    k, prev_end, n_anchor = 0, None, 0
+    for r in rows[first:]:
+        name = short(r["Kernel_Name"])
+        start, end = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        if anchor in r["Kernel_Name"]:
+            k, n_anchor = 0, n_anchor + 1
+        role = f"{name} #{k}"
+        k += 1
+        gap = (start - prev_end) if prev_end is not None else 0
+        prev_end = end
+        if n_anchor <= skip:
+            continue
+        if role not in acc:
+            acc[role] = []
+            order.append(role)
+        acc[role].append((end - start, gap))
+    out = [f"{'role (kernel #ordinal in layer)':44s} {'calls':>6s} {'avg_us':>8s} {'min_us':>8s} "
+           f"{'gap_us':>7s}"]
+    for role in order:
+        v = acc[role]
+        d = [x[0] for x in v]
+        g = [x[1] for x in v]
+        out.append(f"{role[:44]:44s} {len(v):6d} {sum(d) / len(d) / 1e3:8.2f} {min(d) / 1e3:8.2f} "
+                   f"{sum(g) / len(g) / 1e3:7.2f}")
+    return "\n".join(out)
+
+
 def traffic(args) -> str:
     fk, fn, fc = per_dispatch_kib(counter_rows(args.fetch), args.kernel)
     wk, wn, wc = per_dispatch_kib(counter_rows(args.write), args.kernel)
@@ -89,6 +130,10 @@ def main():
     s = sub.add_parser("stats")
     s.add_argument("csv")
     s.add_argument("--top", type=int, default=20)
+    r = sub.add_parser("roles")
+    r.add_argument("csv")
+    r.add_argument("--anchor", required=True, help="substring of the first kernel of a layer")
+    r.add_argument("--skip", type=int, default=0, help="layers to skip (warm-up)")
     t = sub.add_parser("traffic")
     t.add_argument("--fetch", required=True)
     t.add_argument("--write", required=True)
@@ -97,7 +142,12 @@ def main():
     t.add_argument("--record")
     t.add_argument("--source")
     args = ap.parse_args()
-    print(stats(args.csv, args.top) if args.cmd == "stats" else traffic(args))
+    if args.cmd == "stats":
+        print(stats(args.csv, args.top))
+    elif args.cmd == "roles":
+        print(roles(args.csv, args.anchor, args.skip))
+    else:
+        print(traffic(args))
 
 
 if __name__ == "__main__":

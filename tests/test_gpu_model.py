@@ -228,3 +228,30 @@ def test_long_context_decode_bit_exact(ctx, n_pre):
         assert bits_equal(dks, oks) and bits_equal(dvs, ovs)
     dev.close()
     orm.close()
+
+
+@pytest.mark.parametrize("n_pre", [40, 1500, 3000])
+def test_dense_softmax_decode_bit_exact(ctx, n_pre):
+    """attn_q scaled down to 1e-6, so every score is tiny and no softmax
+    weight underflows: the attention sums run over every position (the
+    workgroup's exact exp sum, above 64 terms), against the oracle."""
+    cfg = LONG
+    hm = bs.make_host_model(cfg, seed=41)
+    for hl in hm.layers:
+        hl.scales["attn_q"] = 1e-6
+    dev = bs.load_device_model(ctx, hm)
+    orm = OracleModel(hm)
+    k, v = bs.kv_prefill(cfg, seed=42, n_pos=n_pre)
+    dkv, okv = dev.kv_cache(cfg.context_length), orm.kv(cfg.context_length)
+    dkv.append_positions(k, v)
+    okv.append_positions(k, v)
+    tok, pos = 3, n_pre
+    for _ in range(4):
+        h, tr = dkv.forward(tok, pos, trace=True)
+        rh, rtr = okv.forward(tok, pos, trace=True)
+        for l in range(cfg.n_layers):
+            assert bits_equal(tr[l], rtr[l]), f"position {pos}: layer {l}"
+        assert bits_equal(h, rh)
+        tok, pos = (tok * 7 + 1) % cfg.vocab, pos + 1
+    dev.close()
+    orm.close()
