@@ -130,6 +130,7 @@ constexpr int kSvThreads = 1024;  // wave 0: the 16 chains; waves 1-15: products
 constexpr int kSvDims = 16;        // head dims per workgroup (one 16-byte V segment)
 constexpr int kSvTile = 240;       // positions per product tile
 constexpr int kSvStride = 244;     // floats per dim row of a product tile (16-byte rows)
+constexpr uint32_t kSvSerialSum = 64;  // longest exp list summed by one wave, one add at a time
 static_assert(kSvTile * (kSvDims / 4) == kSvThreads - 64, "one 4-dim unit per producer thread");
 
 // softmax over scores[h][0..n_past) then out[h][d] = Σ_p w_p * v_p[d] for
@@ -142,8 +143,9 @@ static_assert(kSvTile * (kSvDims / 4) == kSvThreads - 64, "one 4-dim unit per pr
 // positions whose exp is not exactly 0 (kept in position order; a zero term
 // changes neither the exp sum nor any output sum, so the reference's sums
 // over all positions equal the sums over this list).  The exp sum runs over
-// the list, left to right (one wave for a short list, the workgroup's exact
-// sum seq_sum_block_owned for a long one), then the normalisation.  Then,
+// the list, left to right (one wave, one add at a time, for up to 64
+// terms; the workgroup's exact sum seq_sum_block_owned beyond), then the
+// normalisation.  Then,
 // tile by tile, waves 1-15 write products w_p * v_p[d] (4 dims of one listed
 // position per thread) while lanes 0-15 of wave 0 add the previous tile, one
 // chain per dimension, in position order.  Position n_past - 1 uses this
@@ -269,16 +271,24 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
         }
         wm_sync_lds();
         // Σ exp left to right (attention.rs:63-66) over the compacted terms:
-        // a short list by one wave, one add at a time; a long one by the
-        // workgroup's exact sum (thread t takes terms t*m .. t*m+m-1)
+        // up to kSvSerialSum by one wave, one add at a time; a longer list by
+        // the workgroup's exact sum (thread t takes terms t*m .. t*m+m-1)
         float sum;
-        if (count <= 64) {
+        if (count <= kSvSerialSum) {
             if (wid == 0) {
-                const float v = lane < count ? cval[lane] : 0.0f;
+                // 64 terms per step, one per lane; the next step's terms are
+                // read while this step's are added
                 float s;
                 asm volatile("v_mov_b32 %0, 0" : "=v"(s));
-                for (uint32_t k = 0; k < count; k++)
-                    s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)k));
+                float v = lane < count ? cval[lane] : 0.0f;
+                for (uint32_t c = 0; c < count; c += 64) {
+                    const uint32_t nx = c + 64 + lane;
+                    const float vn = nx < count ? cval[nx] : 0.0f;
+                    const uint32_t here = count - c < 64u ? count - c : 64u;
+                    for (uint32_t k = 0; k < here; k++)
+                        s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)k));
+                    v = vn;
+                }
                 if (lane == 0) ssum = s;
             }
             wm_sync_lds();

@@ -239,8 +239,8 @@ __global__ __launch_bounds__(64) void k_i2s_partial(i2s_multi m, uint32_t n_chun
 // itself (wm_norm.h, the same operations as k_rmsnorm_quant) straight into
 // LDS while those loads are in flight: every workgroup evaluates the same
 // norm, so their codes agree bit for bit, and the norm costs no launch and
-// no trip through memory.  Workgroup 0 also writes what the norm leaves
-// behind for later kernels (x + y, the codes and their meta, cleared slots).
+// no trip through memory.  Each workgroup writes its share of what the norm
+// leaves behind for later kernels (x + y), workgroup 0 the cleared slots.
 // Its W waves then split the chunks of K between them (wave w: chunks
 // [n_chunks*w/W, n_chunks*(w+1)/W)), each computing the unit's rows over its
 // slice exactly as k_i2s_partial does; the W partial dots meet in LDS (exact
@@ -333,29 +333,25 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
         wm::norm_quant<NP, W * 64>(rsq, n, xv, wv, reinterpret_cast<uint8_t *>(act_s), nl,
                                    act_scale, asum);
     }
-    // What the norm leaves for later kernels, written by workgroup 0 once its
-    // own work is done: x + y (the same f32 adds as above) with the
-    // non-finite check, the codes and their meta, the cleared slots.
-    auto finish = [&]() {
-        if (!first) return;
+    // What the norm leaves for later kernels, written once this workgroup's
+    // own work is done, each workgroup its contiguous share of the elements:
+    // x + y (the same f32 adds as above) with the non-finite check; and by
+    // workgroup 0 the cleared slots.
+    const auto finish = [&]() {
         const uint32_t tid0 = threadIdx.x;
-        if (nm.act_out)
-            for (uint32_t i = tid0; i < n / 16; i += W * 64)
-                reinterpret_cast<int4 *>(nm.act_out)[i] = reinterpret_cast<const int4 *>(act_s)[i];
-        if (tid0 == 0 && nm.meta_out) {
-            nm.meta_out->scale = act_scale;
-            nm.meta_out->asum = asum;
-        }
-        if (nm.clear2 && tid0 < 2) nm.clear2[tid0] = 0;
+        if (first && nm.clear2 && tid0 < 2) nm.clear2[tid0] = 0;
         if (nm.x_out && nm.y) {
-            int nonfinite = 0;
-            for (uint32_t j = tid0; j < n; j += W * 64) {
+            const uint32_t lo = (uint32_t)((uint64_t)n * blockIdx.x / gridDim.x);
+            const uint32_t hi = (uint32_t)((uint64_t)n * (blockIdx.x + 1) / gridDim.x);
+            bool nonfinite = false;
+            for (uint32_t j = lo + tid0; j < hi; j += W * 64) {
                 const float v = nm.x[j] + nm.y[j];
                 nm.x_out[j] = v;
                 nonfinite |= !isfinite(v);
             }
-            if (nm.err_flag && __syncthreads_or(nonfinite) && tid0 == 0 && *nm.err_flag == 0)
-                *nm.err_flag = nm.layer_tag;
+            // every writer of this launch writes the same tag; a flag already
+            // raised by an earlier layer is kept
+            if (nonfinite && nm.err_flag && *nm.err_flag == 0) *nm.err_flag = nm.layer_tag;
         }
     };
     int acc16[UG], acc4[UG], acc1[UG];

@@ -369,8 +369,6 @@ struct wm_fused_norm {
     float eps;
     uint32_t *err_flag;     // nullable: set to layer_tag when x + y is not all finite
     uint32_t layer_tag;
-    uint8_t *act_out;       // nullable: a copy of the int8 codes (permuted layout)
-    wm_act_meta *meta_out;  // nullable: their scale and sum
     uint32_t *clear2;       // nullable: two slots zeroed
     // nonzero: x is the gate projection and y the up projection of the FFN,
     // and the norm runs on relu(x)^2 * y (ffn.rs:37-65) instead of x + y

@@ -230,7 +230,7 @@ def test_long_context_decode_bit_exact(ctx, n_pre):
     orm.close()
 
 
-@pytest.mark.parametrize("n_pre", [40, 1500, 3000])
+@pytest.mark.parametrize("n_pre", [40, 300, 1500, 3000])
 def test_dense_softmax_decode_bit_exact(ctx, n_pre):
     """attn_q scaled down to 1e-6, so every score is tiny and no softmax
     weight underflows: the attention sums run over every position (the
