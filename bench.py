@@ -33,6 +33,10 @@ sys.path.insert(0, str(ROOT / "project-willamette_amd"))
 sys.path.insert(0, str(ROOT))
 
 METRIC = "i2_s/Q6_K matvec GB/s (% HBM peak) + decode tok/s, BitNet-2B shape, 1 GPU"
+# the kernel behind each role of the decode step (names as rocprofv3 prints them)
+ROLE_KERNEL = {"qkv": "k_i2s_fused<2, 2, 16, 3>", "attention": "k_attn_scores + k_attn_softmax_v<2>",
+               "o": "k_i2s_fused<0, 1, 16, 3>", "gate_up": "k_i2s_fused<0, 1, 16, 3>",
+               "down": "k_i2s_fused<0, 1, 16, 7>"}
 HBM_PEAK_GBPS = 8000.0
 PREFILL, START_TOKEN = 1024, 15339
 
@@ -72,6 +76,47 @@ def decode_tokens(dkv, n: int, tok: int, pos: int):
         ids.append(nxt)
         tok, pos = nxt, pos + 1
     return ids
+
+
+# the decode step's per-layer roles, in launch order (wm_debug_rerun_role numbers)
+ROLES = ("qkv", "attention", "o", "gate_up", "down")
+
+
+def role_bytes(cfg, n_past: int) -> dict:
+    """Algorithmic bytes of one launch of each per-layer role of the decode
+    step: the I2_S weights (2 bits each), the norm's f32 inputs (x, the
+    residual y, the weight), the int8 K and V rows and their scales at n_past
+    positions, the f32 scores (written once, read once) and the f32 outputs,
+    each counted once."""
+    E, F, KV, H = cfg.n_embd, cfg.n_ff, cfg.kv_dim, cfg.n_heads
+    return {
+        "qkv": E * (E + 2 * KV) // 4 + 3 * E * 4 + (E + 2 * KV) * 4,
+        "attention": 2 * n_past * (KV + 4) + E * 4 + 2 * H * n_past * 4 + E * 4,
+        "o": E * E // 4 + 2 * E * 4 + E * 4,
+        "gate_up": 2 * F * E // 4 + 3 * E * 4 + 2 * F * 4,
+        "down": E * F // 4 + 3 * F * 4 + E * 4,
+    }
+
+
+def decode_roles(ctx, wh, dev, dkv, cfg, reps: int):
+    """Each per-layer role of the decode step just run, relaunched `reps`
+    times back to back (layer 1, the cache's last position) and timed with
+    hipEvents on the library's stream: microseconds per launch and the HBM
+    rate its algorithmic bytes imply."""
+    timer = HipTimer(ctx.stream)
+    n_past = dkv.position
+    nb = role_bytes(cfg, n_past)
+    out = {}
+    for i, name in enumerate(ROLES):
+        ctx.check(wh.lib.wm_debug_rerun_role(dev.h, dkv.h, 1, i, 3))
+        timer.start()
+        ctx.check(wh.lib.wm_debug_rerun_role(dev.h, dkv.h, 1, i, reps))
+        us = timer.stop_ms() * 1000.0 / reps
+        gbps = nb[name] / (us * 1e-6) / 1e9
+        out[name] = {"us_per_launch": round(us, 3), "launches_per_token": cfg.n_layers,
+                     "bytes_per_launch": int(nb[name]), "gbps": round(gbps, 1),
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "us_per_token": round(us * cfg.n_layers, 1)}
+    return out
 
 
 def lm_head_kernels(ctx, wh, hm, cfg, reps: int):
@@ -272,6 +317,21 @@ def probe(kind: str, reps: int):
                                                                  bound.ptr, turn[0] > 1))
             else:
                 ctx.check(wh.lib.wm_logits_argmax_dev(ctx.h, t.h, h.ptr, logits.ptr, None))
+    elif kind == "decode":  # the decode step's kernels, id-only lm-head
+        import bitnet_synth as bs2
+        hm = bs2.make_host_model(cfg, bs2.master_seed(4))
+        dev = bs2.load_device_model(ctx, hm)
+        del hm
+        dkv = dev.kv_cache(cfg.context_length)
+        k, v = bs2.kv_prefill(cfg, bs2.master_seed(4), PREFILL)
+        dkv.append_positions(k, v)
+        del k, v
+        held += [dkv, dev]
+        st = {"tok": START_TOKEN, "pos": PREFILL}
+
+        def launch():
+            _, _, st["tok"] = dkv.decode_step(st["tok"], st["pos"], want_logits=False)
+            st["pos"] += 1
     elif kind == "i2s":
         copies = 320
         seed = 0x5749_4C4C_0000_0001
@@ -303,6 +363,13 @@ def probe(kind: str, reps: int):
 
 
 def traffic_record(kernel: str):
+    """HBM bytes per launch of `kernel` (or of the decode role "decode:<role>")
+    from the committed counter summary, used only while the kernel source it
+    was measured on is unchanged."""
+    return _traffic(kernel)
+
+
+def _traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed counter summary,
     used only while the kernel source it was measured on is unchanged."""
     import hashlib
@@ -327,7 +394,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batch", action="store_true", help="skip the ragged-batch measurement")
     ap.add_argument("--batch-steps", type=int, default=5)
-    ap.add_argument("--probe", choices=["lm_head", "lm_head_exact", "i2s"],
+    ap.add_argument("--probe", choices=["lm_head", "lm_head_exact", "i2s", "decode"],
                     help="only run one kernel (and a calibration copy) for counter passes")
     ap.add_argument("--probe-reps", type=int, default=5)
     args = ap.parse_args()
@@ -370,6 +437,10 @@ def main():
     tok_s = args.steps / (wall_ms / 1000.0)
     log(f"decode: {tok_s:.1f} tok/s ({ms_tok:.3f} ms/token wall, {gpu_ms / args.steps:.3f} ms/token events)")
 
+    roles = decode_roles(ctx, wh, dev, dkv, cfg, reps=50)
+    dkv.rollback(PREFILL)
+    dominant = max(roles, key=lambda k: roles[k]["us_per_token"])
+    log("roles (us per launch): " + ", ".join(f"{k} {v['us_per_launch']:.2f}" for k, v in roles.items()))
     lm, lm_bytes = lm_head_kernels(ctx, wh, hm, cfg, reps=50)
     lm_ms = lm["bounded"]
     lm_gbps = lm_bytes / (lm_ms / 1000.0) / 1e9
@@ -420,11 +491,16 @@ def main():
                    "n_embd": cfg.n_embd, "n_ff": cfg.n_ff, "heads": cfg.n_heads,
                    "kv_heads": cfg.n_kv_heads, "vocab": cfg.vocab, "kv_prefill": PREFILL,
                    "decode_tokens": args.steps, "start_token": START_TOKEN, "exact": True},
-        "roofline": {"bound": "hbm", "achieved": round(lm_gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(lm_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic_record("k_q6k_bounded<10, true>"),
-                     "kernel": "k_q6k_bounded (Q6_K lm-head 128256x2560, id-only pass)",
-                     "us_per_launch": round(lm_ms * 1000, 2)},
+        "roofline": {"bound": "hbm", "achieved": roles[dominant]["gbps"], "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": roles[dominant]["frac"],
+                     "traffic": traffic_record("decode:" + dominant),
+                     "kernel": f"{ROLE_KERNEL[dominant]} ({dominant}: the decode role with the "
+                               f"largest time per token)",
+                     "us_per_launch": roles[dominant]["us_per_launch"],
+                     "bytes_per_launch": roles[dominant]["bytes_per_launch"]},
+        "decode_roles": roles,
+        "step_roofline": {"bytes_per_token": int(token_bytes), "achieved_gbps": round(decode_gbps, 1),
+                          "frac": round(decode_gbps / HBM_PEAK_GBPS, 4)},
         "cpu_baseline": cpu,
         "matvec": {
             "q6k_lm_head_128256x2560": {

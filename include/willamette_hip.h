@@ -284,6 +284,16 @@ wm_status wm_debug_q6k_bounded_logits_dev(wm_ctx *ctx, const wm_tensor *token_em
                                           const float *d_hidden, float *d_approx, float *d_bound,
                                           int reuse_prep);
 
+/* No counterpart in the reference: enqueue `reps` more launches of one
+ * role of layer `layer` of the decode step just run (role 0 norm + Q/K/V,
+ * 1 attention scores + softmax-V, 2 norm + O, 3 norm + gate/up, 4 norm +
+ * down) at the cache's last position, on the context's stream, without
+ * waiting, so that a caller can time that role's kernels back to back with
+ * events.  The launches rewrite the same buffers and cache row the step
+ * wrote; the results are not meant to be used. */
+wm_status wm_debug_rerun_role(wm_model *m, wm_kv_cache *kv, uint32_t layer, uint32_t role,
+                              uint32_t reps);
+
 /* ---- synthetic BitNet-shaped inputs (src/synth.rs) ------------------- */
 
 /* Counter-based SplitMix64 streams, identical on every host: value i of

@@ -138,98 +138,116 @@ bool model_ready(const wm_model *m) {
     return true;
 }
 
+// The kernels of one layer, in order (wm_debug_rerun_role's role numbers).
+enum layer_role { ROLE_QKV = 0, ROLE_SCORES_SOFTMAX_V, ROLE_O, ROLE_GATE_UP, ROLE_DOWN, ROLE_ALL };
+
+// Enqueue layer l at `pos`, the residual stream in H[cur] on entry (cur is
+// updated as the layer's two residual adds move it).  With only < ROLE_ALL
+// just that role's launches are enqueued (the buffers stay as they are).
+// Returns false when a launcher had no kernel for the model's shape.
+bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, uint32_t pos, float *const H[2],
+                   int &cur, float *layer_trace_dev, int only = ROLE_ALL) {
+    const wm_model_config &c = m->cfg;
+    hipStream_t s = m->ctx->stream;
+    const uint32_t E = c.n_embd, KV = m->kv_dim;
+    const uint32_t n_chunks_e = E / I2S_CHUNK_COLS, n_chunks_f = c.n_ff / I2S_CHUNK_COLS;
+    const float scale = 1.0f / sqrtf((float)c.head_dim);  // primitives.rs:354
+    // absmax of this token's K and V (float bits): zero at creation and after
+    // every O launch, raised by the QKV launch, read by attention
+    uint32_t *kv_absmax = m->dscalars + 4;
+    const auto want = [&](int r) { return only == ROLE_ALL || only == r; };
+    const dev_layer &L = m->layers[l];
+    // attn_norm, on hidden + the previous layer's ffn_down, then Q, K, V
+    // (whole heads per workgroup, NEOX RoPE on Q and K at `pos`)
+    wm_fused_norm an{};
+    an.x = H[cur];
+    an.w = L.attn_norm;
+    an.eps = c.rms_eps;
+    if (l > 0) {
+        an.y = m->proj_out;
+        an.x_out = H[cur ^ 1];
+        an.err_flag = m->dscalars + 2;
+        an.layer_tag = l;
+        cur ^= 1;
+    }
+    wm_i2s_desc qkv[3] = {{L.q.w, L.q.n_groups}, {L.k.w, L.k.n_groups}, {L.v.w, L.v.n_groups}};
+    const float qkv_scales[3] = {L.q.scale, L.k.scale, L.v.scale};
+    float *qkv_out[3] = {m->q, m->k_new, m->v_new};
+    if (want(ROLE_QKV) &&
+        !wm_launch_i2s_fused(WM_FUSED_ROPE, qkv, qkv_scales, qkv_out, 3, n_chunks_e, c.head_dim / 64,
+                             an, m->rope_cos, m->rope_sin, pos, c.n_rot, 0x3u, kv_absmax, s))
+        return false;
+    if (layer_trace_dev && l > 0)
+        hipMemcpyAsync(layer_trace_dev + (size_t)(l - 1) * E, H[cur], (size_t)E * 4,
+                       hipMemcpyDeviceToDevice, s);
+    // attention; this token's K/V row goes into the cache on the way
+    const size_t lay = (size_t)l * kv->max_seq;
+    if (want(ROLE_SCORES_SOFTMAX_V) &&
+        !wm_launch_attention(m->q, kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV, kv->vs + lay,
+                             m->scores, c.context_length, m->attn_out, c.n_heads, c.n_kv_heads,
+                             c.head_dim, pos + 1, scale, m->k_new, m->v_new, kv_absmax, s))
+        return false;
+    // attn_sub_norm, then O (the launch also clears the K/V absmax slots)
+    wm_fused_norm sn{};
+    sn.x = m->attn_out;
+    sn.w = L.attn_sub_norm;
+    sn.eps = c.rms_eps;
+    sn.clear2 = kv_absmax;
+    wm_i2s_desc od = {L.o.w, L.o.n_groups};
+    float *o_out[1] = {m->proj_out};
+    if (want(ROLE_O) && !wm_launch_i2s_fused(WM_FUSED_PLAIN, &od, &L.o.scale, o_out, 1, n_chunks_e,
+                                             1, sn, nullptr, nullptr, 0, 0, 0, nullptr, s))
+        return false;
+    // ffn_norm on hidden + wo_out, then gate and up (relu^2 * up)
+    wm_fused_norm fn{};
+    fn.x = H[cur];
+    fn.y = m->proj_out;
+    fn.x_out = H[cur ^ 1];
+    fn.w = L.ffn_norm;
+    fn.eps = c.rms_eps;
+    cur ^= 1;
+    wm_i2s_desc gu[2] = {{L.gate.w, L.gate.n_groups}, {L.up.w, L.up.n_groups}};
+    const float gu_scales[2] = {L.gate.scale, L.up.scale};
+    // gate and up as two plain tensors, one 64-row group per workgroup
+    // (twice the workgroups of a gate+up pairing, half the weight bytes
+    // in flight per wave); relu(gate)^2 * up is formed where it is read,
+    // in the down matvec's norm
+    float *gu_out[2] = {m->h_ff, m->h_up};
+    if (want(ROLE_GATE_UP) && !wm_launch_i2s_fused(WM_FUSED_PLAIN, gu, gu_scales, gu_out, 2,
+                                                   n_chunks_e, 1, fn, nullptr, nullptr, 0, 0, 0,
+                                                   nullptr, s))
+        return false;
+    // ffn_sub_norm of relu(gate)^2 * up, then down
+    wm_fused_norm dn{};
+    dn.x = m->h_ff;
+    dn.y = m->h_up;
+    dn.relu2_mul = 1;
+    dn.w = L.ffn_sub_norm;
+    dn.eps = c.rms_eps;
+    wm_i2s_desc dd = {L.down.w, L.down.n_groups};
+    float *d_out[1] = {m->proj_out};
+    if (want(ROLE_DOWN) && !wm_launch_i2s_fused(WM_FUSED_PLAIN, &dd, &L.down.scale, d_out, 1,
+                                                n_chunks_f, 1, dn, nullptr, nullptr, 0, 0, 0,
+                                                nullptr, s))
+        return false;
+    return true;
+}
+
 // Enqueue the layers + output norm for one token at `pos`; the token id is
 // read from m->dscalars[0] on the device.  Returns false when some launcher
 // had no kernel for the model's shape (nothing after it was enqueued).
 bool enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_trace_dev) {
     const wm_model_config &c = m->cfg;
     hipStream_t s = m->ctx->stream;
-    const uint32_t E = c.n_embd, F = c.n_ff, KV = m->kv_dim;
-    const uint32_t n_chunks_e = E / I2S_CHUNK_COLS, n_chunks_f = F / I2S_CHUNK_COLS;
+    const uint32_t E = c.n_embd;
     // The residual stream lives in two buffers: a norm that adds a matvec's
-    // output reads one and writes the sum to the other (in one workgroup,
-    // while the launch's other workgroups still read the first).
-    float *H[2] = {m->hidden, m->hidden2};
+    // output reads one and writes the sum to the other (each workgroup its
+    // share, while the launch's other workgroups still read the first).
+    float *const H[2] = {m->hidden, m->hidden2};
     int cur = 0;
     wm_launch_q6k_dequant_row_dev(m->embd, m->embd_blocks, m->dscalars, H[0], s);
-    const float scale = 1.0f / sqrtf((float)c.head_dim);  // primitives.rs:354
-    // absmax of this token's K and V (float bits): zero at creation and after
-    // every O launch, raised by the QKV launch, read by attention
-    uint32_t *kv_absmax = m->dscalars + 4;
-    for (uint32_t l = 0; l < c.n_layers; l++) {
-        const dev_layer &L = m->layers[l];
-        // attn_norm, on hidden + the previous layer's ffn_down, then Q, K, V
-        // (whole heads per workgroup, NEOX RoPE on Q and K at `pos`)
-        wm_fused_norm an{};
-        an.x = H[cur];
-        an.w = L.attn_norm;
-        an.eps = c.rms_eps;
-        if (l > 0) {
-            an.y = m->proj_out;
-            an.x_out = H[cur ^ 1];
-            an.err_flag = m->dscalars + 2;
-            an.layer_tag = l;
-            cur ^= 1;
-        }
-        wm_i2s_desc qkv[3] = {{L.q.w, L.q.n_groups}, {L.k.w, L.k.n_groups}, {L.v.w, L.v.n_groups}};
-        const float qkv_scales[3] = {L.q.scale, L.k.scale, L.v.scale};
-        float *qkv_out[3] = {m->q, m->k_new, m->v_new};
-        if (!wm_launch_i2s_fused(WM_FUSED_ROPE, qkv, qkv_scales, qkv_out, 3, n_chunks_e,
-                                 c.head_dim / 64, an, m->rope_cos, m->rope_sin, pos, c.n_rot, 0x3u,
-                                 kv_absmax, s))
-            return false;
-        if (layer_trace_dev && l > 0)
-            hipMemcpyAsync(layer_trace_dev + (size_t)(l - 1) * E, H[cur], (size_t)E * 4,
-                           hipMemcpyDeviceToDevice, s);
-        // attention; this token's K/V row goes into the cache on the way
-        const size_t lay = (size_t)l * kv->max_seq;
-        if (!wm_launch_attention(m->q, kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV,
-                                 kv->vs + lay, m->scores, c.context_length, m->attn_out, c.n_heads,
-                                 c.n_kv_heads, c.head_dim, pos + 1, scale, m->k_new, m->v_new,
-                                 kv_absmax, s))
-            return false;
-        // attn_sub_norm, then O (the launch also clears the K/V absmax slots)
-        wm_fused_norm sn{};
-        sn.x = m->attn_out;
-        sn.w = L.attn_sub_norm;
-        sn.eps = c.rms_eps;
-        sn.clear2 = kv_absmax;
-        wm_i2s_desc od = {L.o.w, L.o.n_groups};
-        float *o_out[1] = {m->proj_out};
-        if (!wm_launch_i2s_fused(WM_FUSED_PLAIN, &od, &L.o.scale, o_out, 1, n_chunks_e, 1, sn,
-                                 nullptr, nullptr, 0, 0, 0, nullptr, s))
-            return false;
-        // ffn_norm on hidden + wo_out, then gate and up (relu^2 * up)
-        wm_fused_norm fn{};
-        fn.x = H[cur];
-        fn.y = m->proj_out;
-        fn.x_out = H[cur ^ 1];
-        fn.w = L.ffn_norm;
-        fn.eps = c.rms_eps;
-        cur ^= 1;
-        wm_i2s_desc gu[2] = {{L.gate.w, L.gate.n_groups}, {L.up.w, L.up.n_groups}};
-        const float gu_scales[2] = {L.gate.scale, L.up.scale};
-        // gate and up as two plain tensors, one 64-row group per workgroup
-        // (twice the workgroups of a gate+up pairing, half the weight bytes
-        // in flight per wave); relu(gate)^2 * up is formed where it is read,
-        // in the down matvec's norm
-        float *gu_out[2] = {m->h_ff, m->h_up};
-        if (!wm_launch_i2s_fused(WM_FUSED_PLAIN, gu, gu_scales, gu_out, 2, n_chunks_e, 1, fn,
-                                 nullptr, nullptr, 0, 0, 0, nullptr, s))
-            return false;
-        // ffn_sub_norm of relu(gate)^2 * up, then down
-        wm_fused_norm dn{};
-        dn.x = m->h_ff;
-        dn.y = m->h_up;
-        dn.relu2_mul = 1;
-        dn.w = L.ffn_sub_norm;
-        dn.eps = c.rms_eps;
-        wm_i2s_desc dd = {L.down.w, L.down.n_groups};
-        float *d_out[1] = {m->proj_out};
-        if (!wm_launch_i2s_fused(WM_FUSED_PLAIN, &dd, &L.down.scale, d_out, 1, n_chunks_f, 1, dn,
-                                 nullptr, nullptr, 0, 0, 0, nullptr, s))
-            return false;
-    }
+    for (uint32_t l = 0; l < c.n_layers; l++)
+        if (!enqueue_layer(m, kv, l, pos, H, cur, layer_trace_dev)) return false;
     // last residual + output_norm (f32 out, no quantisation)
     if (!wm_launch_rmsnorm_quant(H[cur], m->proj_out, m->output_norm, E, c.rms_eps, nullptr,
                                  nullptr, m->final_hidden, m->dscalars + 2, c.n_layers,
@@ -796,6 +814,26 @@ wm_status wm_decode_step(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t 
     WM_HIP(ctx, hipMemcpyAsync(&next, m->dscalars + 1, 4, hipMemcpyDeviceToHost, ctx->stream));
     WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     if (next_token) *next_token = next;
+    return WM_OK;
+}
+
+wm_status wm_debug_rerun_role(wm_model *m, wm_kv_cache *kv, uint32_t layer, uint32_t role,
+                              uint32_t reps) {
+    if (!m || !kv) return WM_E_ARG;
+    wm_ctx *ctx = m->ctx;
+    if (!model_ready(m)) return wm_set_error(ctx, WM_E_STATE, "model: weights not fully set");
+    if (kv->m != m) return wm_set_error(ctx, WM_E_ARG, "kv cache belongs to another model");
+    if (kv->pos == 0) return wm_set_error(ctx, WM_E_STATE, "rerun_role: no decode step has run");
+    if (layer >= m->cfg.n_layers || role >= ROLE_ALL)
+        return wm_set_error(ctx, WM_E_ARG, "rerun_role: layer %u / role %u out of range", layer, role);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    float *const H[2] = {m->hidden, m->hidden2};
+    for (uint32_t i = 0; i < reps; i++) {
+        int cur = layer == 0 ? 0 : 1;  // the residual buffer layer `layer` starts from
+        if (!enqueue_layer(m, kv, layer, kv->pos - 1, H, cur, nullptr, (int)role))
+            return wm_set_error(ctx, WM_E_SHAPE, "rerun_role: no kernel for this model shape");
+    }
+    WM_HIP(ctx, hipGetLastError());
     return WM_OK;
 }
 

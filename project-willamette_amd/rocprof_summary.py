@@ -13,6 +13,11 @@ first kernel of a layer), so the same kernel launched twice per layer shows
 as two rows; the mean gap between a dispatch's start and the previous one's
 end is printed beside it.
 
+`traffic-roles` does the same for the decode step: the dispatches of each
+pass are put in order and named by role as in `roles` (--names maps
+"kernel #ordinal" to a role name, "a #1+b #2" adding two kernels into one
+role), and each role's bytes per launch are recorded under "decode:<role>".
+
 `traffic` turns two counter passes (--pmc FETCH_SIZE, then --pmc
 WRITE_SIZE; both report KiB per dispatch) into HBM bytes per launch of one
 kernel.  Each counter is scaled by what it reads for the largest
@@ -55,13 +60,19 @@ def counter_rows(run_dir: str):
 
 
 def per_dispatch_kib(rows, kernel: str):
-    """(mean KiB per dispatch of `kernel`, dispatches, mean KiB of the largest copy)."""
+    """(mean KiB per dispatch of `kernel`, dispatches, mean KiB of a calibration
+    copy).  The calibration copies are the largest device-to-device copies
+    after the run's last other dispatch (the probe ends with them; earlier
+    copies, such as weight uploads, and the small copies of a decode step's
+    results are not calibration)."""
     k = [float(r["Counter_Value"]) for r in rows if short(r["Kernel_Name"]) == kernel]
-    copies = [r for r in rows if "copyBuffer" in r["Kernel_Name"]]
-    if not k or not copies:
+    rows = sorted(rows, key=lambda r: int(r["Dispatch_Id"]))
+    last_other = max((i for i, r in enumerate(rows) if "copyBuffer" not in r["Kernel_Name"]), default=-1)
+    tail = rows[last_other + 1:]
+    big = max((int(r["Grid_Size"]) for r in tail), default=0)
+    c = [float(r["Counter_Value"]) for r in tail if int(r["Grid_Size"]) == big]
+    if not k or not c:
         raise SystemExit(f"kernel {kernel!r} or the calibration copy is missing")
-    big = max(int(r["Grid_Size"]) for r in copies)
-    c = [float(r["Counter_Value"]) for r in copies if int(r["Grid_Size"]) == big]
     return sum(k) / len(k), len(k), sum(c) / len(c)
 
 
@@ -124,6 +135,58 @@ def traffic(args) -> str:
     return "\n".join(lines)
 
 
+def role_kib(rows, anchor: str, skip: int):
+    """Mean KiB per dispatch of every 'kernel #ordinal' role after `skip`
+    layers, dispatches in Dispatch_Id order."""
+    rows = sorted(rows, key=lambda r: int(r["Dispatch_Id"]))
+    first = next((i for i, r in enumerate(rows) if anchor in r["Kernel_Name"]), None)
+    if first is None:
+        raise SystemExit(f"no dispatch of {anchor!r}")
+    acc, k, n_anchor = {}, 0, 0
+    for r in rows[first:]:
+        if anchor in r["Kernel_Name"]:
+            k, n_anchor = 0, n_anchor + 1
+        role = f"{short(r['Kernel_Name'])} #{k}"
+        k += 1
+        if n_anchor > skip:
+            acc.setdefault(role, []).append(float(r["Counter_Value"]))
+    return {role: sum(v) / len(v) for role, v in acc.items()}
+
+
+def traffic_roles(args) -> str:
+    frows, wrows = counter_rows(args.fetch), counter_rows(args.write)
+    _, _, fc = per_dispatch_kib(frows, short(next(r["Kernel_Name"] for r in frows)))
+    _, _, wc = per_dispatch_kib(wrows, short(next(r["Kernel_Name"] for r in wrows)))
+    f_scale = args.copy_bytes / (fc * 1024.0)
+    w_scale = args.copy_bytes / (wc * 1024.0)
+    fk = role_kib(frows, args.anchor, args.skip)
+    wk = role_kib(wrows, args.anchor, args.skip)
+    names = dict(n.split("=", 1) for n in args.names)
+    lines = [f"copy of {args.copy_bytes} B: FETCH_SIZE scale {f_scale:.4f}, WRITE_SIZE scale {w_scale:.4f}",
+             f"{'role':12s} {'kernel #ordinal':36s} {'fetch_B':>12s} {'write_B':>10s} {'total_B':>12s}"]
+    rec = {}
+    if args.record:
+        rec_path = Path(args.record)
+        rec = json.loads(rec_path.read_text()) if rec_path.exists() else {}
+    for key, role in names.items():
+        parts = key.split("+")  # several kernels making one role: their bytes add up
+        for k in parts:
+            if k not in fk or k not in wk:
+                raise SystemExit(f"no dispatches of {k!r}")
+        fb = sum(fk[k] for k in parts) * 1024.0 * f_scale
+        wb = sum(wk[k] for k in parts) * 1024.0 * w_scale
+        lines.append(f"{role:12s} {key:36s} {fb:12.0f} {wb:10.0f} {fb + wb:12.0f}")
+        if args.record:
+            src = Path(args.source)
+            rec["decode:" + role] = {"source": src.name, "bytes_per_launch": round(fb + wb),
+                                     "fetch_bytes": round(fb), "write_bytes": round(wb),
+                                     "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
+                                     "source_sha256": hashlib.sha256(src.read_bytes()).hexdigest()}
+    if args.record:
+        Path(args.record).write_text(json.dumps(rec, indent=1, sort_keys=True) + "\n")
+    return "\n".join(lines)
+
+
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -134,6 +197,16 @@ def main():
     r.add_argument("csv")
     r.add_argument("--anchor", required=True, help="substring of the first kernel of a layer")
     r.add_argument("--skip", type=int, default=0, help="layers to skip (warm-up)")
+    tr = sub.add_parser("traffic-roles")
+    tr.add_argument("--fetch", required=True)
+    tr.add_argument("--write", required=True)
+    tr.add_argument("--anchor", required=True)
+    tr.add_argument("--skip", type=int, default=0)
+    tr.add_argument("--names", nargs="+", required=True,
+                    help="'kernel #ordinal=role' pairs ('a #1+b #2=role' adds kernels up)")
+    tr.add_argument("--copy-bytes", type=int, default=1 << 30)
+    tr.add_argument("--record")
+    tr.add_argument("--source")
     t = sub.add_parser("traffic")
     t.add_argument("--fetch", required=True)
     t.add_argument("--write", required=True)
@@ -146,6 +219,8 @@ def main():
         print(stats(args.csv, args.top))
     elif args.cmd == "roles":
         print(roles(args.csv, args.anchor, args.skip))
+    elif args.cmd == "traffic-roles":
+        print(traffic_roles(args))
     else:
         print(traffic(args))
 

@@ -108,6 +108,7 @@ EXPORTS = {
                                           C.c_size_t, _i8p, _f32p, _i32p),
     "wm_bitlinear_i2s_matvec_f32_dev": (C.c_int, _vp, _vp, _vp, _vp),
     "wm_bitlinear_i2s_matvec_f32_dev_noalloc": (C.c_int, _vp, _vp, _vp, _vp),
+    "wm_debug_rerun_role": (C.c_int, _vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32),
     "wm_bitlinear_i2s_matvec_f32_multi_dev": (C.c_int, _vp, C.POINTER(_vp), C.c_uint32, _vp, _vp),
     "wm_bitlinear_i2s_matmul_f32_dev": (C.c_int, _vp, _vp, _vp, C.c_uint32, _vp),
     "wm_bitlinear_i2s_matmul_f32": (C.c_int, _vp, _vp, _f32p, C.c_size_t, C.c_uint32, _f32p,
