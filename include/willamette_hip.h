@@ -39,8 +39,18 @@ typedef enum wm_status {
     WM_E_OOM = 4,              /* device allocation failed */
     WM_E_HIP = 5,              /* HIP runtime error; wm_last_error() has the text */
     WM_E_ARG = 6,              /* null pointer / out-of-range argument */
-    WM_E_STATE = 7             /* call out of protocol order (e.g. KV position mismatch,
+    WM_E_STATE = 7,            /* call out of protocol order (e.g. KV position mismatch,
                                   src/model/cached_forward.rs:271-305) */
+    WM_E_PARSE = 8,            /* WillametteError::GgufParse from the GGUF reader and the
+                                  model graph's dtype checks (src/error.rs:13-14) */
+    WM_E_MAGIC = 9,            /* WillametteError::InvalidMagic (src/error.rs:16-17) */
+    WM_E_VERSION = 10,         /* WillametteError::UnsupportedVersion (src/error.rs:19-20) */
+    WM_E_ARCH = 11,            /* WillametteError::UnsupportedArchitecture (src/error.rs:22-23) */
+    WM_E_METADATA = 12,        /* WillametteError::MissingMetadata: a metadata key or a
+                                  required tensor (src/error.rs:25-26) */
+    WM_E_BOUNDS = 13,          /* WillametteError::TensorOutOfBounds (src/error.rs:40-46) */
+    WM_E_IO = 14,              /* WillametteError::Io / InvalidPath (src/error.rs:10-11, 37-38) */
+    WM_E_NOT_IMPLEMENTED = 15  /* WillametteError::NotImplemented (src/error.rs:34-35) */
 } wm_status;
 
 typedef enum wm_tensor_type {
@@ -52,6 +62,7 @@ typedef struct wm_ctx wm_ctx;
 typedef struct wm_tensor wm_tensor;
 typedef struct wm_model wm_model;
 typedef struct wm_kv_cache wm_kv_cache;
+typedef struct wm_gguf wm_gguf;
 
 /* ---- context --------------------------------------------------------- */
 
@@ -260,6 +271,58 @@ wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *promp
 wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_seqs,
                            const uint32_t *n_new, const uint32_t *tokens, float *last_hidden,
                            uint32_t *next_tokens);
+
+/* ---- GGUF files (src/gguf/reader.rs, src/model/graph.rs) ------------- */
+
+/* GgufFile::parse (src/gguf/reader.rs:120-415): the header, metadata and
+ * tensor directory of a GGUF v2/v3 image with the reference's checks
+ * (counts and array sizes against the bytes left, strings <= 1 MiB and
+ * UTF-8, alignment a power of two, tensor byte lengths by type, every
+ * tensor and I2_S trailing scale block inside the file and before the next
+ * tensor).  Host-only: needs no device.  The result points into `data`,
+ * which must outlive it.  On failure returns the error kind and writes the
+ * reference's message into err (may be null). */
+wm_status wm_gguf_parse(const uint8_t *data, size_t len, wm_gguf **out, char *err, size_t err_len);
+/* ModelMmap::open (src/memory/mmap.rs:27-36) then GgufFile::parse: the
+ * same over a read-only mapping of the file at path, owned by the result. */
+wm_status wm_gguf_open(const char *path, wm_gguf **out, char *err, size_t err_len);
+void wm_gguf_close(wm_gguf *g);
+uint32_t wm_gguf_version(const wm_gguf *g);
+uint64_t wm_gguf_alignment(const wm_gguf *g);
+uint64_t wm_gguf_tensor_count(const wm_gguf *g);
+/* Absolute offset of the tensor data section (reader.rs:244-256). */
+uint64_t wm_gguf_data_offset(const wm_gguf *g);
+/* Index of the tensor with this name, -1 if none. */
+int64_t wm_gguf_find_tensor(const wm_gguf *g, const char *name);
+/* TensorView (src/gguf/tensor.rs:21-54) of tensor `index`: name (owned by
+ * g), raw GGML type id, dims, GGUF shape (unused dims 0), absolute offset,
+ * byte length, data pointer, and for I2_S the 32-byte trailing scale block
+ * (else null).  Any out pointer may be null. */
+wm_status wm_gguf_tensor_info(const wm_gguf *g, uint64_t index, const char **name, uint32_t *type,
+                              uint32_t *n_dims, uint64_t shape[4], uint64_t *offset, uint64_t *bytes,
+                              const uint8_t **data, const uint8_t **scale_block);
+/* GgufValue::as_u64 / as_f32 / as_str (src/gguf/reader.rs:48-76) of a
+ * metadata key; WM_E_METADATA if absent or of another type. */
+wm_status wm_gguf_meta_u64(const wm_gguf *g, const char *key, uint64_t *out);
+wm_status wm_gguf_meta_f32(const wm_gguf *g, const char *key, float *out);
+wm_status wm_gguf_meta_str(const wm_gguf *g, const char *key, const char **out);
+/* ModelConfig::from_gguf_metadata (src/model/config.rs:61-160) for the
+ * BitNet architectures "bitnet-b1.58", "bitnet-25", "bitnet"
+ * (src/model/architecture/bitnet.rs:29-43); host-only. */
+wm_status wm_gguf_bitnet_config(const wm_gguf *g, wm_model_config *cfg, char *err, size_t err_len);
+/* ModelGraph::from_gguf's checks (src/model/graph.rs:79-237, :368-503)
+ * without the upload, host-only: the config, unique names, no bias tensors,
+ * every BitNet role present with its dtype and shape. */
+wm_status wm_gguf_bitnet_check(const wm_gguf *g, char *err, size_t err_len);
+/* ModelGraph::from_gguf (src/model/graph.rs:79-237) then the upload: every
+ * tensor is found and checked (dtype, shape, no bias tensors, unique names)
+ * before any device memory is taken; then the I2_S BitLinears with their
+ * scale blocks, the f32 norms and the tied Q6_K token_embd go to the device
+ * as by wm_model_create / wm_model_set_layer / wm_model_set_output.
+ * max_context (0: the file's context_length) caps the KV caches the model
+ * will serve.  token_embd in F16 (accepted by the reference) is
+ * WM_E_UNSUPPORTED_TYPE here: the embedding and lm-head kernels read Q6_K. */
+wm_status wm_model_from_gguf(wm_ctx *ctx, const wm_gguf *g, uint32_t max_context, wm_model **out);
 
 /* ---- test hook ------------------------------------------------------- */
 

@@ -148,6 +148,23 @@ class DeviceModel:
         ctx.check(wh.lib.wm_model_set_output(self.h, emb.h, wh._ptr(on, wh.C.c_float)))
         emb.close()
 
+    @classmethod
+    def from_gguf(cls, ctx: wh.Context, gf: "wh.GgufFile", max_context: int = 0) -> "DeviceModel":
+        """ModelGraph::from_gguf (src/model/graph.rs:79-237) through
+        wm_model_from_gguf: config, checks and upload in the library."""
+        c = gf.bitnet_config()
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        self.cfg = BitNetConfig(c.n_layers, c.n_embd, c.n_ff, c.n_heads, c.n_kv_heads, c.head_dim,
+                                c.vocab_size,
+                                min(c.context_length, max_context) if max_context else c.context_length,
+                                c.rms_eps, c.rope_freq_base)
+        h = wh._vp()
+        ctx.check(wh.lib.wm_model_from_gguf(ctx.h, gf.h, max_context, wh.C.byref(h)))
+        self.h = h
+        ctx.adopt(self)
+        return self
+
     def close(self):
         if self.h:
             wh.lib.wm_model_destroy(self.h)
@@ -279,3 +296,107 @@ def ragged_workload(cfg: BitNetConfig, n_seq: int = 16, ctx_lo: int = 128, ctx_h
     seqs = tuple(tuple(int(t) for t in rng.integers(0, cfg.vocab, n)) for n in news)
     seeds = tuple(master_seed(5) + 1 + i for i in range(n_seq))
     return RaggedWorkload(ctxs, seqs, seeds)
+
+
+# ---------------------------------------------------------------------------
+# GGUF images of host models (the file format src/gguf/reader.rs reads)
+# ---------------------------------------------------------------------------
+
+GGUF_MAGIC = 0x46554747
+_GGUF_U32, _GGUF_F32, _GGUF_STR, _GGUF_ARR, _GGUF_U64 = 4, 6, 8, 9, 10
+
+
+def _gguf_str(s: str) -> bytes:
+    b = s.encode()
+    return len(b).to_bytes(8, "little") + b
+
+
+def _gguf_kv(key: str, vtype: int, value) -> bytes:
+    out = _gguf_str(key) + vtype.to_bytes(4, "little")
+    if vtype == _GGUF_U32:
+        return out + int(value).to_bytes(4, "little")
+    if vtype == _GGUF_U64:
+        return out + int(value).to_bytes(8, "little")
+    if vtype == _GGUF_F32:
+        return out + np.float32(value).tobytes()
+    if vtype == _GGUF_STR:
+        return out + _gguf_str(value)
+    if vtype == _GGUF_ARR:  # array of strings
+        return out + _GGUF_STR.to_bytes(4, "little") + len(value).to_bytes(8, "little") + \
+            b"".join(_gguf_str(v) for v in value)
+    raise ValueError(vtype)
+
+
+def gguf_tensors(hm: HostModel):
+    """(name, GGUF shape, GGML type, bytes) of every tensor, token_embd and
+    output_norm first, then each layer's roles; I2_S data is followed by its
+    32-byte trailing scale block (src/gguf/tensor.rs:278-309)."""
+    cfg = hm.cfg
+    out = [("token_embd.weight", [cfg.n_embd, cfg.vocab], wh.TYPE_Q6K, hm.token_embd.tobytes()),
+           ("output_norm.weight", [cfg.n_embd], 0, np.ascontiguousarray(hm.output_norm, np.float32).tobytes())]
+    for l, hl in enumerate(hm.layers):
+        for name in ("attn_norm", "attn_sub_norm"):
+            out.append((f"blk.{l}.{name}.weight", [hl.norms[name].size], 0, hl.norms[name].tobytes()))
+        for role in ROLES:
+            ind, outd = role_shape(cfg, role)
+            blk = hl.packed[role].tobytes() + wh.scale_block(hl.scales[role]).tobytes()
+            out.append((f"blk.{l}.{role}.weight", [ind, outd], wh.TYPE_I2S, blk))
+        for name in ("ffn_norm", "ffn_sub_norm"):
+            out.append((f"blk.{l}.{name}.weight", [hl.norms[name].size], 0, hl.norms[name].tobytes()))
+    return out
+
+
+def gguf_metadata(cfg: BitNetConfig, arch: str = "bitnet-b1.58", alignment=None) -> list:
+    """The metadata keys ModelConfig::from_gguf_metadata_with_prefix reads
+    (src/model/config.rs:81-160), prefixed by the architecture string."""
+    kv = [("general.architecture", _GGUF_STR, arch),
+          ("general.name", _GGUF_STR, "synthetic BitNet b1.58"),
+          (f"{arch}.block_count", _GGUF_U32, cfg.n_layers),
+          (f"{arch}.embedding_length", _GGUF_U32, cfg.n_embd),
+          (f"{arch}.feed_forward_length", _GGUF_U32, cfg.n_ff),
+          (f"{arch}.context_length", _GGUF_U32, cfg.context_length),
+          (f"{arch}.attention.head_count", _GGUF_U32, cfg.n_heads),
+          (f"{arch}.attention.head_count_kv", _GGUF_U32, cfg.n_kv_heads),
+          (f"{arch}.attention.layer_norm_rms_epsilon", _GGUF_F32, cfg.rms_eps),
+          (f"{arch}.rope.dimension_count", _GGUF_U32, cfg.head_dim),
+          (f"{arch}.rope.freq_base", _GGUF_F32, cfg.rope_base),
+          (f"{arch}.vocab_size", _GGUF_U32, cfg.vocab),
+          ("tokenizer.ggml.model", _GGUF_STR, "gpt2"),
+          ("tokenizer.ggml.tokens", _GGUF_ARR, ["<s>", "</s>", "a", "b"])]
+    if alignment is not None:
+        kv.append(("general.alignment", _GGUF_U32, alignment))
+    return kv
+
+
+def gguf_image(tensors, metadata, alignment: int = 32, version: int = 3):
+    """Yield the bytes of a GGUF file: header, metadata, tensor directory,
+    padding to the alignment, tensor data (each tensor's offset aligned)."""
+    head = [GGUF_MAGIC.to_bytes(4, "little"), version.to_bytes(4, "little"),
+            len(tensors).to_bytes(8, "little"), len(metadata).to_bytes(8, "little")]
+    head += [_gguf_kv(*kv) for kv in metadata]
+    off = 0
+    offsets = []
+    for name, shape, typ, data in tensors:
+        offsets.append(off)
+        head.append(_gguf_str(name) + len(shape).to_bytes(4, "little") +
+                    b"".join(int(d).to_bytes(8, "little") for d in shape) +
+                    typ.to_bytes(4, "little") + off.to_bytes(8, "little"))
+        off += len(data)
+        off += -off % alignment
+    h = b"".join(head)
+    yield h + bytes(-len(h) % alignment)
+    for name, shape, typ, data in tensors:
+        yield data
+        yield bytes(-len(data) % alignment)
+
+
+def gguf_bytes(hm: HostModel, arch: str = "bitnet-b1.58", alignment: int = 32, version: int = 3) -> bytes:
+    meta = gguf_metadata(hm.cfg, arch, None if alignment == 32 else alignment)
+    return b"".join(gguf_image(gguf_tensors(hm), meta, alignment, version))
+
+
+def write_gguf(path, hm: HostModel, arch: str = "bitnet-b1.58", alignment: int = 32) -> None:
+    meta = gguf_metadata(hm.cfg, arch, None if alignment == 32 else alignment)
+    with open(path, "wb") as f:
+        for chunk in gguf_image(gguf_tensors(hm), meta, alignment):
+            f.write(chunk)

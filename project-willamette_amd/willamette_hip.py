@@ -42,6 +42,14 @@ STATUS = {
     5: "Hip",
     6: "Arg",
     7: "State",
+    8: "GgufParse",
+    9: "InvalidMagic",
+    10: "UnsupportedVersion",
+    11: "UnsupportedArchitecture",
+    12: "MissingMetadata",
+    13: "TensorOutOfBounds",
+    14: "Io",
+    15: "NotImplemented",
 }
 TYPE_I2S = 36
 TYPE_Q6K = 14
@@ -138,6 +146,23 @@ EXPORTS = {
     "wm_debug_seq_sum": (C.c_int, _vp, _f32p, C.c_size_t, _f32p),
     "wm_debug_q6k_bounded_logits": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p, _f32p),
     "wm_debug_q6k_bounded_logits_dev": (C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int),
+    "wm_gguf_parse": (C.c_int, _u8p, C.c_size_t, C.POINTER(_vp), C.c_char_p, C.c_size_t),
+    "wm_gguf_open": (C.c_int, C.c_char_p, C.POINTER(_vp), C.c_char_p, C.c_size_t),
+    "wm_gguf_close": (None, _vp),
+    "wm_gguf_version": (C.c_uint32, _vp),
+    "wm_gguf_alignment": (C.c_uint64, _vp),
+    "wm_gguf_tensor_count": (C.c_uint64, _vp),
+    "wm_gguf_data_offset": (C.c_uint64, _vp),
+    "wm_gguf_find_tensor": (C.c_int64, _vp, C.c_char_p),
+    "wm_gguf_tensor_info": (C.c_int, _vp, C.c_uint64, C.POINTER(C.c_char_p), _u32p, _u32p,
+                            C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                            C.POINTER(_u8p), C.POINTER(_u8p)),
+    "wm_gguf_meta_u64": (C.c_int, _vp, C.c_char_p, C.POINTER(C.c_uint64)),
+    "wm_gguf_meta_f32": (C.c_int, _vp, C.c_char_p, _f32p),
+    "wm_gguf_meta_str": (C.c_int, _vp, C.c_char_p, C.POINTER(C.c_char_p)),
+    "wm_gguf_bitnet_config": (C.c_int, _vp, C.POINTER(ModelConfig), C.c_char_p, C.c_size_t),
+    "wm_gguf_bitnet_check": (C.c_int, _vp, C.c_char_p, C.c_size_t),
+    "wm_model_from_gguf": (C.c_int, _vp, _vp, C.c_uint32, C.POINTER(_vp)),
     "wm_synth_stream_seed": (C.c_uint64, C.c_uint64, C.c_uint64),
     "wm_synth_i2s": (None, C.c_uint64, C.c_uint64, _u8p, C.c_size_t),
     "wm_synth_normal": (None, C.c_uint64, C.c_uint64, _f32p, C.c_size_t, C.c_double),
@@ -397,3 +422,108 @@ def q6k_bounded_logits(ctx: Context, t: Tensor, hidden: np.ndarray):
     ctx.check(lib.wm_debug_q6k_bounded_logits(ctx.h, t.h, _ptr(hidden, C.c_float), hidden.size,
                                               _ptr(approx, C.c_float), _ptr(bound, C.c_float)))
     return approx, bound
+
+
+# ---------------------------------------------------------------------------
+# GGUF files (src/gguf/reader.rs; host only, no GPU needed)
+# ---------------------------------------------------------------------------
+
+class GgufFile:
+    """GgufFile (src/gguf/reader.rs:120-415) over bytes (parse) or a path
+    (open).  Tensor data is read in place; `data` must outlive the object."""
+
+    def __init__(self, h, keep=None):
+        self.h = h
+        self._keep = keep
+
+    @staticmethod
+    def _raise(st: int, err) -> None:
+        raise WillametteError(st, err.value.decode("utf-8", "replace"))
+
+    @classmethod
+    def parse(cls, data) -> "GgufFile":
+        buf = np.frombuffer(bytes(data), dtype=np.uint8) if not isinstance(data, np.ndarray) else data
+        buf = np.ascontiguousarray(buf, dtype=np.uint8)
+        h, err = _vp(), C.create_string_buffer(512)
+        st = lib.wm_gguf_parse(_ptr(buf, C.c_uint8), buf.size, C.byref(h), err, 512)
+        if st:
+            cls._raise(st, err)
+        return cls(h, buf)
+
+    @classmethod
+    def open(cls, path) -> "GgufFile":
+        h, err = _vp(), C.create_string_buffer(512)
+        st = lib.wm_gguf_open(str(path).encode(), C.byref(h), err, 512)
+        if st:
+            cls._raise(st, err)
+        return cls(h)
+
+    def close(self):
+        if self.h:
+            lib.wm_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def version(self) -> int:
+        return int(lib.wm_gguf_version(self.h))
+
+    @property
+    def alignment(self) -> int:
+        return int(lib.wm_gguf_alignment(self.h))
+
+    @property
+    def data_offset(self) -> int:
+        return int(lib.wm_gguf_data_offset(self.h))
+
+    def __len__(self) -> int:
+        return int(lib.wm_gguf_tensor_count(self.h))
+
+    def find(self, name: str) -> int:
+        return int(lib.wm_gguf_find_tensor(self.h, name.encode()))
+
+    def tensor(self, index: int) -> dict:
+        name, typ, nd = C.c_char_p(), C.c_uint32(), C.c_uint32()
+        shape = (C.c_uint64 * 4)()
+        off, nb = C.c_uint64(), C.c_uint64()
+        data, sb = _u8p(), _u8p()
+        st = lib.wm_gguf_tensor_info(self.h, index, C.byref(name), C.byref(typ), C.byref(nd), shape,
+                                     C.byref(off), C.byref(nb), C.byref(data), C.byref(sb))
+        if st:
+            raise WillametteError(st, f"tensor index {index}")
+        n = nb.value
+        raw = np.ctypeslib.as_array(data, shape=(n,)).copy() if n else np.empty(0, np.uint8)
+        scale = np.ctypeslib.as_array(sb, shape=(32,)).copy() if sb else None
+        return {"name": name.value.decode(), "type": typ.value,
+                "shape": [int(shape[d]) for d in range(nd.value)], "offset": off.value,
+                "bytes": n, "data": raw, "scale_block": scale}
+
+    def meta_u64(self, key: str):
+        v = C.c_uint64()
+        return int(v.value) if lib.wm_gguf_meta_u64(self.h, key.encode(), C.byref(v)) == 0 else None
+
+    def meta_f32(self, key: str):
+        v = C.c_float()
+        return float(v.value) if lib.wm_gguf_meta_f32(self.h, key.encode(), C.byref(v)) == 0 else None
+
+    def meta_str(self, key: str):
+        v = C.c_char_p()
+        return v.value.decode() if lib.wm_gguf_meta_str(self.h, key.encode(), C.byref(v)) == 0 else None
+
+    def bitnet_check(self) -> None:
+        err = C.create_string_buffer(512)
+        st = lib.wm_gguf_bitnet_check(self.h, err, 512)
+        if st:
+            self._raise(st, err)
+
+    def bitnet_config(self) -> ModelConfig:
+        cfg, err = ModelConfig(), C.create_string_buffer(512)
+        st = lib.wm_gguf_bitnet_config(self.h, C.byref(cfg), err, 512)
+        if st:
+            self._raise(st, err)
+        return cfg
