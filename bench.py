@@ -8,13 +8,16 @@ b1.58-2B-shaped weights (30 layers, 2560/6912, 20/5 heads, vocab 128256),
 the KV cache pre-filled to 1024 positions with N(0,1) values, start token
 15339 at position 1024.  W warm-up tokens run first and are rolled back, so
 the K timed tokens occupy positions 1024..1024+K-1 (K = 64 by default: the
-64-token decode).  Inputs are resident in HBM before timing starts.
+64-token decode).  The timed region is one greedy-generate call of K tokens
+(wm_greedy_generate); the same K tokens one wm_decode_step call at a time
+are timed beside it.  Inputs are resident in HBM before timing starts.
 
-Printed JSON line: decode tokens/s (value) plus, for the dominant kernel
-(the Q6_K lm-head matvec, one launch over 269.3 MB), achieved HBM GB/s
-against the 8 TB/s peak, measured with HIP events on the library's stream;
-the i2_s matvec's streaming GB/s over weight copies rotated through more
-than the 256 MB Infinity Cache; and the oracle's CPU time on this host.
+Printed JSON line: decode tokens/s (value); per-layer roles of the step
+relaunched back to back and timed with HIP events on the library's stream,
+with the dominant role's achieved HBM GB/s against the 8 TB/s peak as
+`roofline`; the Q6_K lm-head passes; the i2_s matvec's streaming GB/s over
+weight copies rotated through more than the 256 MB Infinity Cache; the
+ragged continuous-batching step; and the oracle's CPU time on this host.
 """
 from __future__ import annotations
 
@@ -423,19 +426,31 @@ def main():
     del k, v
     log(f"model + KV prefill ready in {time.time() - t0:.1f}s")
 
-    decode_tokens(dkv, args.warmup, START_TOKEN, PREFILL)
+    # the timed region: one greedy_generate_with_cache call of `steps`
+    # tokens from the prefilled cache (the library keeps up to 8 steps in
+    # flight and reads each id back behind the device)
+    if args.warmup:
+        dkv.greedy([START_TOKEN], args.warmup)
     dkv.rollback(PREFILL)
     ctx.synchronize()
     timer = HipTimer(ctx.stream)
     w0 = time.perf_counter()
     timer.start()
-    ids = decode_tokens(dkv, args.steps, START_TOKEN, PREFILL)
+    ids = dkv.greedy([START_TOKEN], args.steps)
     gpu_ms = timer.stop_ms()
     ctx.synchronize()
     wall_ms = (time.perf_counter() - w0) * 1000.0
     ms_tok = wall_ms / args.steps
     tok_s = args.steps / (wall_ms / 1000.0)
     log(f"decode: {tok_s:.1f} tok/s ({ms_tok:.3f} ms/token wall, {gpu_ms / args.steps:.3f} ms/token events)")
+    # the same tokens one decode_step call at a time (a host round trip each)
+    dkv.rollback(PREFILL)
+    ctx.synchronize()
+    w1 = time.perf_counter()
+    ids_step = decode_tokens(dkv, args.steps, START_TOKEN, PREFILL)
+    step_ms = (time.perf_counter() - w1) * 1000.0 / args.steps
+    assert ids_step == ids, "decode_step and greedy_generate disagree"
+    log(f"decode, one call per token: {1000.0 / step_ms:.1f} tok/s ({step_ms:.3f} ms/token)")
 
     roles = decode_roles(ctx, wh, dev, dkv, cfg, reps=50)
     dkv.rollback(PREFILL)
@@ -513,6 +528,7 @@ def main():
         "ragged_batch": batch,
         "decode_effective_gbps": round(decode_gbps, 1),
         "gpu_event_ms_per_token": round(gpu_ms / args.steps, 4),
+        "decode_step_per_call_ms": round(step_ms, 4),
         "token_checksum": int(np.bitwise_xor.reduce(np.array(ids, np.uint64))),
     }
     print(json.dumps(out), flush=True)

@@ -87,6 +87,10 @@ struct wm_model {
     uint32_t *b_ids = nullptr, *b_next = nullptr;
     float *b_scores = nullptr;  // attention scores [t][head][context], grown on demand
     size_t b_scores_bytes = 0;
+    // greedy decode's read-back ring: per step in flight, the next id and the
+    // error flag (pinned host memory) and the event after that step's copy
+    uint32_t *ring = nullptr;
+    hipEvent_t ring_ev[16] = {};
 };
 
 struct wm_kv_cache {
@@ -236,7 +240,8 @@ bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, uint32_t pos, float
 // Enqueue the layers + output norm for one token at `pos`; the token id is
 // read from m->dscalars[0] on the device.  Returns false when some launcher
 // had no kernel for the model's shape (nothing after it was enqueued).
-bool enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_trace_dev) {
+bool enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_trace_dev,
+                     const uint32_t *token_dev = nullptr) {
     const wm_model_config &c = m->cfg;
     hipStream_t s = m->ctx->stream;
     const uint32_t E = c.n_embd;
@@ -245,7 +250,8 @@ bool enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
     // share, while the launch's other workgroups still read the first).
     float *const H[2] = {m->hidden, m->hidden2};
     int cur = 0;
-    wm_launch_q6k_dequant_row_dev(m->embd, m->embd_blocks, m->dscalars, H[0], s);
+    wm_launch_q6k_dequant_row_dev(m->embd, m->embd_blocks, token_dev ? token_dev : m->dscalars,
+                                  H[0], s);
     for (uint32_t l = 0; l < c.n_layers; l++)
         if (!enqueue_layer(m, kv, l, pos, H, cur, layer_trace_dev)) return false;
     // last residual + output_norm (f32 out, no quantisation)
@@ -592,6 +598,9 @@ void wm_model_destroy(wm_model *m) {
     if (m->ws) hipFree(m->ws);
     if (m->bws) hipFree(m->bws);
     if (m->b_scores) hipFree(m->b_scores);
+    if (m->ring) hipHostFree(m->ring);
+    for (hipEvent_t e : m->ring_ev)
+        if (e) hipEventDestroy(e);
     delete m;
 }
 
@@ -860,23 +869,77 @@ wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *promp
             kv->pos = start;
             return st;
         }
-    uint32_t next = 0;
-    if ((st = wm_decode_step(m, kv, prompt[n_prompt - 1], kv->pos, nullptr, nullptr, &next))) {
+    if ((st = check_step(m, kv, prompt[n_prompt - 1], kv->pos))) {
         kv->pos = start;
         return st;
     }
-    uint32_t n = 0;
-    for (uint32_t step = 0; step < max_new; step++) {
-        if (eos >= 0 && (int64_t)next == eos) break;
-        out_ids[n++] = next;
-        if (step + 1 < max_new) {
-            uint32_t tok = next;
-            if ((st = wm_decode_step(m, kv, tok, kv->pos, nullptr, nullptr, &next))) {
-                kv->pos = start;
-                return st;
-            }
-        }
+    // The decode steps are enqueued ahead of the host, up to kAhead in
+    // flight: step k embeds the id in dscalars[1] (the prompt's last token
+    // for k = 0) and its lm-head writes the next id there, so no step waits
+    // for the host.  After each step the id and the cumulative error flag
+    // (dscalars[1..2]) are copied to a pinned ring slot and an event is
+    // recorded; the host reads slot k after that event and applies
+    // generate_with_cache's rules (generate.rs:111-189) in order: a
+    // non-finite step fails the call, EOS ends it.  Steps enqueued past the
+    // end only wrote cache rows beyond the final position, which the cache
+    // treats as free (kv_cache.rs:141-149).
+    constexpr uint32_t kRing = 16, kAhead = 8;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    if (!m->ring) {
+        WM_HIP(ctx, hipHostMalloc((void **)&m->ring, kRing * 2 * sizeof(uint32_t), hipHostMallocDefault));
+        for (hipEvent_t &e : m->ring_ev) WM_HIP(ctx, hipEventCreateWithFlags(&e, hipEventDisableTiming));
     }
+    const uint32_t pos0 = kv->pos;
+    // steps needed: step k yields id k; ids 0..max_new-1 are wanted, and at
+    // least step 0 runs (it also appends the prompt's last token)
+    const uint32_t n_steps = max_new ? max_new : 1;
+    m->ring[0] = prompt[n_prompt - 1];
+    WM_HIP(ctx, hipMemcpyAsync(m->dscalars + 1, m->ring, 4, hipMemcpyHostToDevice, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));  // ring[0] is reused below
+    uint32_t enq = 0, n = 0, done = 0;
+    bool stop = false;
+    uint32_t failed_flag = 0;
+    const auto enqueue = [&](uint32_t k) -> bool {
+        if (!enqueue_forward(m, kv, pos0 + k, nullptr, m->dscalars + 1)) return false;
+        wm_launch_q6k_argmax_fast(m->embd, m->embd_blocks, m->cfg.vocab_size, m->embd_rowgroups,
+                                  m->final_hidden, m->logits, m->dscalars + 1, m->lm_work, true,
+                                  ctx->stream);
+        uint32_t *slot = m->ring + 2 * (k % kRing);
+        return hipMemcpyAsync(slot, m->dscalars + 1, 8, hipMemcpyDeviceToHost, ctx->stream) == hipSuccess &&
+               hipEventRecord(m->ring_ev[k % kRing], ctx->stream) == hipSuccess;
+    };
+    while (done < n_steps && !stop) {
+        while (enq < n_steps && enq < done + kAhead) {
+            if (!enqueue(enq)) {
+                hipStreamSynchronize(ctx->stream);
+                kv->pos = start;
+                return wm_set_error(ctx, WM_E_SHAPE, "greedy_generate: could not enqueue a decode step");
+            }
+            enq++;
+        }
+        WM_HIP(ctx, hipEventSynchronize(m->ring_ev[done % kRing]));
+        const uint32_t id = m->ring[2 * (done % kRing)], flag = m->ring[2 * (done % kRing) + 1];
+        if (flag) {
+            failed_flag = flag;
+            break;
+        }
+        done++;  // step done-1 succeeded: the cache holds its position
+        // the reference's loop: stop at EOS, else record the id and decode it
+        if (eos >= 0 && (int64_t)id == eos) stop = true;
+        else if (n < max_new) out_ids[n++] = id;
+    }
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    WM_HIP(ctx, hipGetLastError());
+    if (failed_flag) {
+        uint32_t *zero = m->ring;  // all reads of the ring are over
+        zero[0] = 0;
+        WM_HIP(ctx, hipMemcpyAsync(m->dscalars + 2, zero, 4, hipMemcpyHostToDevice, ctx->stream));
+        WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        kv->pos = start;
+        return wm_set_error(ctx, WM_E_NONFINITE, "forward_with_cache: non-finite hidden after layer %u",
+                            failed_flag - 1);
+    }
+    kv->pos = pos0 + done;
     *n_out = n;
     return WM_OK;
 }

@@ -130,6 +130,35 @@ def test_position_protocol_and_nonfinite_rollback(ctx):
     assert okv.position == 0
 
 
+def test_greedy_nonfinite_step_with_steps_in_flight(ctx):
+    """The greedy loop enqueues steps ahead of the host.  Token T's
+    embedding row has an infinite Q6_K d, so the step that embeds T makes
+    layer 1's residual non-finite: the call fails with NonFinite, the cache
+    is back at its starting position although later steps were already
+    enqueued, and the error flag is cleared, so the next call decodes like
+    the oracle."""
+    cfg = SMALL
+    hm = bs.make_host_model(cfg, seed=6)
+    T = 77
+    nb = cfg.n_embd // 256
+    row0 = T * nb * 210
+    hm.token_embd.reshape(-1)[row0 + 208:row0 + 210] = [0x00, 0x7C]  # d = +inf (f16)
+    dev = bs.load_device_model(ctx, hm)
+    dkv = dev.kv_cache(cfg.context_length)
+    dkv.forward(1, 0)
+    with pytest.raises(wh.WillametteError) as e:
+        dkv.greedy([2, T], max_new=12)
+    assert e.value.kind == "NonFinite" and dkv.position == 1
+    ids = dkv.greedy([3], max_new=10)
+    orm = OracleModel(hm)
+    okv = orm.kv(cfg.context_length)
+    okv.forward(1, 0)
+    assert T not in ids and ids == okv.greedy([3], max_new=10)
+    assert dkv.position == okv.position == 11
+    dev.close()
+    orm.close()
+
+
 def test_zero_weight_model_closed_form(ctx):
     """tests/synthetic_model.rs analogue: all-zero ternary weights, unit norms,
     an all-ones embedding -> every BitLinear outputs 0, the hidden stays the
@@ -190,6 +219,18 @@ def test_bitnet2b_decode64_matches_oracle_fixture(ctx):
         fast.append(nxt)
         tok, pos = nxt, pos + 1
     assert fast == gold["ids"]
+    # the library's greedy loop (steps enqueued ahead of the host), the
+    # benchmark's timed call: the start token as a one-token prompt
+    dkv.rollback(gold["prefill"])
+    ids = dkv.greedy([gold["start_token"]], gold["steps"])
+    assert ids == gold["ids"] and dkv.position == gold["prefill"] + gold["steps"]
+    # EOS inside the window of steps in flight: the loop stops at it and the
+    # cache ends one past the EOS step, whatever was enqueued after it
+    dkv.rollback(gold["prefill"])
+    eos_at = 5
+    ids = dkv.greedy([gold["start_token"]], gold["steps"], eos=gold["ids"][eos_at])
+    first = gold["ids"].index(gold["ids"][eos_at])
+    assert ids == gold["ids"][:first] and dkv.position == gold["prefill"] + first + 1
 
 
 LONG = bs.BitNetConfig(n_layers=2, n_embd=256, n_ff=384, n_heads=2, n_kv_heads=1, head_dim=128,
