@@ -66,6 +66,9 @@ class OracleKV:
     def position(self):
         return int(orc.lib.or_kv_position(self.h))
 
+    def rollback(self, pos: int):
+        orc.lib.or_kv_rollback(self.h, pos)
+
     def append_positions(self, k: np.ndarray, v: np.ndarray):
         for p in range(k.shape[0]):
             kp = np.ascontiguousarray(k[p], np.float32)

@@ -31,12 +31,19 @@ struct attn_args {
     // This token's K (after RoPE) and V, [kv_dim] f32: position n_past - 1
     // is not in the cache yet.  Each kernel quantises what it needs of them
     // exactly as KVCache::append does; one workgroup of each writes the
-    // cache row (k_row / v_row, kv_dim bytes) and its scale.
+    // cache row (kv_dim bytes) and its scale.
     const float *k_new, *v_new;
     const uint32_t *kv_absmax;  // [2]: absmax of k_new, v_new (float bits), by the QKV matvec
-    int8_t *k_row, *v_row;
-    float *k_row_scale, *v_row_scale;
+    // nullable: the token's position on the device (n_past = *pos_dev + 1,
+    // for launches that are replayed at successive positions); the grid and
+    // LDS are then sized for n_max, and a larger n_past launches nothing
+    const uint32_t *pos_dev;
+    uint32_t n_max;
 };
+
+__device__ __forceinline__ uint32_t attn_n_past(const attn_args &a) {
+    return a.pos_dev ? *a.pos_dev + 1 : a.n_past;
+}
 
 constexpr uint32_t kMaxHeadDim = 128;
 
@@ -64,9 +71,13 @@ constexpr int kScStride = kMaxHeadDim + 4;  // floats per position row (16-byte 
 __global__ __launch_bounds__(kScThreads) void k_attn_scores(attn_args a) {
     __shared__ __align__(16) float prod[64 * kScStride];
     const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const uint32_t kvh = h / a.group, pnew = a.n_past - 1;
+    const uint32_t n_past = attn_n_past(a);
+    if (n_past > a.n_max) return;
+    const uint32_t kvh = h / a.group, pnew = n_past - 1;
+    const uint32_t n_cached_blocks = (pnew + 63) / 64;  // the block after them scores pnew
+    if (blockIdx.y > n_cached_blocks) return;
     const float *qh = a.q + (uint64_t)h * a.head_dim;
-    if (blockIdx.y == gridDim.y - 1) {
+    if (blockIdx.y == n_cached_blocks) {
         const float kabs = __uint_as_float(a.kv_absmax[0]);
         const float ksn = kv_scale(kabs);
         for (uint32_t i = tid; i < a.head_dim; i += kScThreads) {
@@ -74,8 +85,9 @@ __global__ __launch_bounds__(kScThreads) void k_attn_scores(attn_args a) {
             prod[i] = qh[i] * kd;
         }
         if (h == 0) {
-            for (uint32_t i = tid; i < a.kv_dim; i += kScThreads) a.k_row[i] = kv_q(a.k_new[i], kabs);
-            if (tid == 0) *a.k_row_scale = ksn;
+            int8_t *k_row = const_cast<int8_t *>(a.k_cache) + (uint64_t)pnew * a.kv_dim;
+            for (uint32_t i = tid; i < a.kv_dim; i += kScThreads) k_row[i] = kv_q(a.k_new[i], kabs);
+            if (tid == 0) const_cast<float *>(a.k_scales)[pnew] = ksn;
         }
         wm_sync_lds();
         if (tid == 0) {
@@ -178,7 +190,8 @@ __device__ __forceinline__ float sv_block_max(float v, float *red) {
 template <int MAXM>  // n_past <= MAXM * kSvThreads
 __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
     extern __shared__ __align__(16) float sm[];
-    const uint32_t n = a.n_past, pnew = n - 1;
+    const uint32_t n = attn_n_past(a), pnew = n - 1;
+    if (n > a.n_max) return;
     const uint32_t npad = (n + 3) & ~3u;
     float *cval = sm;                                     // [seq_sum_padded(n)] nonzero exps, then weights
     float *vsc = cval + wm::seq_sum_padded(n);            // [npad]
@@ -368,8 +381,9 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
         if (tid < kSvDims) out[tid] = acc;
     }
     if (v_writer) {  // the cache row of position n_past - 1
-        for (uint32_t i = tid; i < a.kv_dim; i += kSvThreads) a.v_row[i] = kv_q(a.v_new[i], vabs);
-        if (tid == 0) *a.v_row_scale = kv_scale(vabs);
+        int8_t *v_row = const_cast<int8_t *>(a.v_cache) + (uint64_t)pnew * a.kv_dim;
+        for (uint32_t i = tid; i < a.kv_dim; i += kSvThreads) v_row[i] = kv_q(a.v_new[i], vabs);
+        if (tid == 0) const_cast<float *>(a.v_scales)[pnew] = kv_scale(vabs);
     }
 }
 
@@ -382,22 +396,24 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
                          const int8_t *v_cache, const float *v_scales, float *scores,
                          uint32_t score_stride, float *out, uint32_t n_heads, uint32_t n_kv_heads,
                          uint32_t head_dim, uint32_t n_past, float scale, const float *k_new,
-                         const float *v_new, const uint32_t *kv_absmax, hipStream_t s) {
-    if ((head_dim != 64 && head_dim != 128) || n_past == 0 || n_past > 4 * kSvThreads) return false;
+                         const float *v_new, const uint32_t *kv_absmax, hipStream_t s,
+                         const uint32_t *pos_dev, uint32_t n_max) {
+    // with pos_dev, n_past comes from the device and n_max bounds it
+    const uint32_t nb = pos_dev ? n_max : n_past;
+    if ((head_dim != 64 && head_dim != 128) || nb == 0 || nb > 4 * kSvThreads ||
+        nb > score_stride)
+        return false;
     const uint32_t kv_dim = n_kv_heads * head_dim;
-    int8_t *k_row = const_cast<int8_t *>(k_cache) + (uint64_t)(n_past - 1) * kv_dim;
-    int8_t *v_row = const_cast<int8_t *>(v_cache) + (uint64_t)(n_past - 1) * kv_dim;
     attn_args a{q, k_cache, k_scales, v_cache, v_scales, scores, out, n_past, kv_dim, head_dim,
-                n_heads / n_kv_heads, score_stride, scale, k_new, v_new, kv_absmax, k_row, v_row,
-                const_cast<float *>(k_scales) + (n_past - 1), const_cast<float *>(v_scales) + (n_past - 1)};
-    hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, (n_past - 1 + 63) / 64 + 1), dim3(kScThreads), 0, s, a);
-    const size_t npad = ((size_t)n_past + 3) & ~(size_t)3;
-    const size_t lds = (size_t)wm::seq_sum_padded(n_past) * 4 + npad * (4 + 16) +
+                n_heads / n_kv_heads, score_stride, scale, k_new, v_new, kv_absmax, pos_dev, nb};
+    hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, (nb - 1 + 63) / 64 + 1), dim3(kScThreads), 0, s, a);
+    const size_t npad = ((size_t)nb + 3) & ~(size_t)3;
+    const size_t lds = (size_t)wm::seq_sum_padded(nb) * 4 + npad * (4 + 16) +
                        (size_t)2 * kSvDims * kSvStride * 4 + npad * 2;
     const dim3 grid(n_heads, head_dim / kSvDims);
-    if (n_past <= 2 * kSvThreads)
+    if (nb <= 2 * kSvThreads)
         hipLaunchKernelGGL(k_attn_softmax_v<2>, grid, dim3(kSvThreads), lds, s, a);
-    else  // n_past <= 4096, the models' context limit
+    else  // nb <= 4096, the models' context limit
         hipLaunchKernelGGL(k_attn_softmax_v<4>, grid, dim3(kSvThreads), lds, s, a);
     return true;
 }

@@ -264,6 +264,7 @@ struct i2s_fused_args {
     wm_fused_norm norm;                // the input's norm (n = n_chunks * 64)
     const float *rope_cos, *rope_sin;  // [pos][n_rot/2]
     uint32_t pos, n_rot, rope_mask;
+    const uint32_t *pos_dev;  // nullable: the position is read here instead of `pos`
     uint32_t *absmax;  // ROPE: absmax of the outputs of tensors 1, 2 (float bits, nullable)
 };
 
@@ -311,8 +312,9 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
     const bool rope = MODE == WM_FUSED_ROPE && ((a.rope_mask >> t) & 1u);
     float rc = 0.0f, rsn = 0.0f;
     if (rope && threadIdx.x < half) {
-        rc = a.rope_cos[(uint64_t)a.pos * half + threadIdx.x];
-        rsn = a.rope_sin[(uint64_t)a.pos * half + threadIdx.x];
+        const uint32_t pos = a.pos_dev ? *a.pos_dev : a.pos;
+        rc = a.rope_cos[(uint64_t)pos * half + threadIdx.x];
+        rsn = a.rope_sin[(uint64_t)pos * half + threadIdx.x];
     }
     // the input's norm and int8 codes, into LDS (the weights stay in flight;
     // no global memory access until the dots, so no wait the compiler places
@@ -544,7 +546,7 @@ bool wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
                          int n_tensors, uint32_t n_chunks, uint32_t groups_per_unit,
                          const wm_fused_norm &norm, const float *rope_cos, const float *rope_sin,
                          uint32_t pos, uint32_t n_rot, uint32_t rope_mask, uint32_t *absmax,
-                         hipStream_t s) {
+                         hipStream_t s, const uint32_t *pos_dev) {
     i2s_fused_args a{};
     uint32_t acc = 0;
     a.n_tensors = n_tensors;
@@ -565,6 +567,7 @@ bool wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
     a.rope_cos = rope_cos;
     a.rope_sin = rope_sin;
     a.pos = pos;
+    a.pos_dev = pos_dev;
     a.n_rot = n_rot;
     a.rope_mask = rope_mask;
     a.absmax = absmax;

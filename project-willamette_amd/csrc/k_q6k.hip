@@ -650,7 +650,7 @@ __global__ __launch_bounds__(kSelectBlock) void k_q6k_select(
     const uint8_t *__restrict__ w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
     const float *__restrict__ hidden, float *__restrict__ logits, const float *__restrict__ bound,
     const float *__restrict__ wg_lb, const float *__restrict__ wg_ub, uint32_t n_wg,
-    uint32_t *__restrict__ argmax_out) {
+    uint32_t *__restrict__ argmax_out, wm_step_tail tail) {
     extern __shared__ float xs[];  // [16][n_blocks*16 + 4]
     __shared__ uint32_t wg_list[kBoundedMaxBlocks];
     __shared__ uint32_t cand[kSelectCap];
@@ -740,7 +740,18 @@ __global__ __launch_bounds__(kSelectBlock) void k_q6k_select(
             if (cand_better(s_c[i].v, s_c[i].i, bc.v, bc.i)) bc = s_c[i];
         // a NaN logit at index 0 wins (the reference's scan starts from
         // logits[0] and NaN compares false); all -inf/NaN keeps index 0
-        *argmax_out = (s_f0 != s_f0 || bc.i == 0xFFFFFFFFu) ? 0u : bc.i;
+        const uint32_t id = (s_f0 != s_f0 || bc.i == 0xFFFFFFFFu) ? 0u : bc.i;
+        *argmax_out = id;
+        if (tail.pos) {
+            const uint32_t p = *tail.pos;
+            if (tail.ring) {
+                uint32_t *slot = tail.ring + 2 * (p & tail.ring_mask);
+                slot[0] = id;
+                slot[1] = *tail.err_flag;
+                __threadfence_system();
+            }
+            *tail.pos = p + 1;
+        }
     }
 }
 
@@ -811,7 +822,8 @@ uint32_t launch_bounded_ch(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
 template <int CH>
 void launch_argmax_fast_ch(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                            uint32_t n_rowgroups, const float *hidden, float *logits,
-                           uint32_t *argmax_out, void *work, bool prepared, hipStream_t s) {
+                           uint32_t *argmax_out, void *work, bool prepared, hipStream_t s,
+                           const wm_step_tail &tail) {
     const work_layout lay = layout_of(n_rows, n_blocks);
     uint8_t *wb = (uint8_t *)work;
     float *bound = reinterpret_cast<float *>(wb + lay.bound);
@@ -823,7 +835,7 @@ void launch_argmax_fast_ch(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                                                 logits, bound, wg_lb, wg_ub, s);
     const size_t lds = sizeof(float) * 16 * xs_stride(n_blocks);
     hipLaunchKernelGGL(k_q6k_select<CH>, dim3(1), dim3(kSelectBlock), lds, s, w, n_blocks, n_rows,
-                       n_rowgroups, hidden, logits, bound, wg_lb, wg_ub, n_wg, argmax_out);
+                       n_rowgroups, hidden, logits, bound, wg_lb, wg_ub, n_wg, argmax_out, tail);
 }
 
 }  // namespace
@@ -900,11 +912,13 @@ void wm_launch_q6k_logits_argmax(const uint8_t *w, uint32_t n_blocks, uint32_t n
 // point (written by the kernel that produced it).
 void wm_launch_q6k_argmax_fast(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                                uint32_t n_rowgroups, const float *hidden, float *logits,
-                               uint32_t *argmax_out, void *work, bool prepared, hipStream_t s) {
+                               uint32_t *argmax_out, void *work, bool prepared, hipStream_t s,
+                               const wm_step_tail *tail) {
+    const wm_step_tail t = tail ? *tail : wm_step_tail{};
 #define WM_F_CASE(C)                                                                               \
     case C:                                                                                        \
         launch_argmax_fast_ch<C>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, argmax_out,    \
-                                 work, prepared, s);                                               \
+                                 work, prepared, s, t);                                            \
         break;
     switch (pick_ch(n_blocks)) {
         WM_F_CASE(10) WM_F_CASE(8) WM_F_CASE(5) WM_F_CASE(4) WM_F_CASE(2) default: WM_F_CASE(1)

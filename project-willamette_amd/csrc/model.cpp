@@ -31,7 +31,8 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
                          const int8_t *v_cache, const float *v_scales, float *scores,
                          uint32_t score_stride, float *out, uint32_t n_heads, uint32_t n_kv_heads,
                          uint32_t head_dim, uint32_t n_past, float scale, const float *k_new,
-                         const float *v_new, const uint32_t *kv_absmax, hipStream_t s);
+                         const float *v_new, const uint32_t *kv_absmax, hipStream_t s,
+                         const uint32_t *pos_dev = nullptr, uint32_t n_max = 0);
 void wm_launch_kv_append(const float *k, const float *v, uint32_t kv_dim, uint32_t n_layers,
                          uint32_t pos0, uint32_t n_pos, uint32_t max_seq, int8_t *k_cache,
                          float *k_scales, int8_t *v_cache, float *v_scales, hipStream_t s);
@@ -89,7 +90,7 @@ struct wm_model {
     size_t b_scores_bytes = 0;
     // greedy decode's read-back ring: per step in flight, the next id and the
     // error flag (pinned host memory) and the event after that step's copy
-    uint32_t *ring = nullptr;
+    uint32_t *ring = nullptr, *ring_dev = nullptr;
     hipEvent_t ring_ev[16] = {};
 };
 
@@ -149,8 +150,17 @@ enum layer_role { ROLE_QKV = 0, ROLE_SCORES_SOFTMAX_V, ROLE_O, ROLE_GATE_UP, ROL
 // updated as the layer's two residual adds move it).  With only < ROLE_ALL
 // just that role's launches are enqueued (the buffers stay as they are).
 // Returns false when a launcher had no kernel for the model's shape.
-bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, uint32_t pos, float *const H[2],
+// The position of a step: a value, or (pos_dev) a device word read by the
+// kernels, whose attention launches are then sized for n_max positions.
+struct step_pos {
+    uint32_t pos;
+    const uint32_t *dev;
+    uint32_t n_max;
+};
+
+bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, step_pos sp, float *const H[2],
                    int &cur, float *layer_trace_dev, int only = ROLE_ALL) {
+    const uint32_t pos = sp.pos;
     const wm_model_config &c = m->cfg;
     hipStream_t s = m->ctx->stream;
     const uint32_t E = c.n_embd, KV = m->kv_dim;
@@ -179,7 +189,7 @@ bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, uint32_t pos, float
     float *qkv_out[3] = {m->q, m->k_new, m->v_new};
     if (want(ROLE_QKV) &&
         !wm_launch_i2s_fused(WM_FUSED_ROPE, qkv, qkv_scales, qkv_out, 3, n_chunks_e, c.head_dim / 64,
-                             an, m->rope_cos, m->rope_sin, pos, c.n_rot, 0x3u, kv_absmax, s))
+                             an, m->rope_cos, m->rope_sin, pos, c.n_rot, 0x3u, kv_absmax, s, sp.dev))
         return false;
     if (layer_trace_dev && l > 0)
         hipMemcpyAsync(layer_trace_dev + (size_t)(l - 1) * E, H[cur], (size_t)E * 4,
@@ -189,7 +199,8 @@ bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, uint32_t pos, float
     if (want(ROLE_SCORES_SOFTMAX_V) &&
         !wm_launch_attention(m->q, kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV, kv->vs + lay,
                              m->scores, c.context_length, m->attn_out, c.n_heads, c.n_kv_heads,
-                             c.head_dim, pos + 1, scale, m->k_new, m->v_new, kv_absmax, s))
+                             c.head_dim, pos + 1, scale, m->k_new, m->v_new, kv_absmax, s, sp.dev,
+                             sp.n_max))
         return false;
     // attn_sub_norm, then O (the launch also clears the K/V absmax slots)
     wm_fused_norm sn{};
@@ -240,7 +251,7 @@ bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, uint32_t pos, float
 // Enqueue the layers + output norm for one token at `pos`; the token id is
 // read from m->dscalars[0] on the device.  Returns false when some launcher
 // had no kernel for the model's shape (nothing after it was enqueued).
-bool enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_trace_dev,
+bool enqueue_forward(wm_model *m, wm_kv_cache *kv, step_pos sp, float *layer_trace_dev,
                      const uint32_t *token_dev = nullptr) {
     const wm_model_config &c = m->cfg;
     hipStream_t s = m->ctx->stream;
@@ -253,7 +264,7 @@ bool enqueue_forward(wm_model *m, wm_kv_cache *kv, uint32_t pos, float *layer_tr
     wm_launch_q6k_dequant_row_dev(m->embd, m->embd_blocks, token_dev ? token_dev : m->dscalars,
                                   H[0], s);
     for (uint32_t l = 0; l < c.n_layers; l++)
-        if (!enqueue_layer(m, kv, l, pos, H, cur, layer_trace_dev)) return false;
+        if (!enqueue_layer(m, kv, l, sp, H, cur, layer_trace_dev)) return false;
     // last residual + output_norm (f32 out, no quantisation)
     if (!wm_launch_rmsnorm_quant(H[cur], m->proj_out, m->output_norm, E, c.rms_eps, nullptr,
                                  nullptr, m->final_hidden, m->dscalars + 2, c.n_layers,
@@ -777,7 +788,7 @@ wm_status wm_forward_with_cache(wm_model *m, wm_kv_cache *kv, uint32_t token, ui
         trace_dev = (float *)scratch;
     }
     WM_HIP(ctx, hipMemcpyAsync(m->dscalars, &token, 4, hipMemcpyHostToDevice, ctx->stream));
-    if (!enqueue_forward(m, kv, position, trace_dev))
+    if (!enqueue_forward(m, kv, step_pos{position, nullptr, 0}, trace_dev))
         return wm_set_error(ctx, WM_E_SHAPE, "forward_with_cache: no kernel for this model shape");
     WM_HIP(ctx, hipGetLastError());
     bool failed = false;
@@ -799,7 +810,7 @@ wm_status wm_decode_step(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t 
     if (st) return st;
     WM_HIP(ctx, hipSetDevice(ctx->device));
     WM_HIP(ctx, hipMemcpyAsync(m->dscalars, &token, 4, hipMemcpyHostToDevice, ctx->stream));
-    if (!enqueue_forward(m, kv, position, nullptr))
+    if (!enqueue_forward(m, kv, step_pos{position, nullptr, 0}, nullptr))
         return wm_set_error(ctx, WM_E_SHAPE, "decode_step: no kernel for this model shape");
     // logits wanted: all of them in the reference's order; else the id-only path
     if (logits_out)
@@ -839,7 +850,7 @@ wm_status wm_debug_rerun_role(wm_model *m, wm_kv_cache *kv, uint32_t layer, uint
     float *const H[2] = {m->hidden, m->hidden2};
     for (uint32_t i = 0; i < reps; i++) {
         int cur = layer == 0 ? 0 : 1;  // the residual buffer layer `layer` starts from
-        if (!enqueue_layer(m, kv, layer, kv->pos - 1, H, cur, nullptr, (int)role))
+        if (!enqueue_layer(m, kv, layer, step_pos{kv->pos - 1, nullptr, 0}, H, cur, nullptr, (int)role))
             return wm_set_error(ctx, WM_E_SHAPE, "rerun_role: no kernel for this model shape");
     }
     WM_HIP(ctx, hipGetLastError());
@@ -874,11 +885,12 @@ wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *promp
         return st;
     }
     // The decode steps are enqueued ahead of the host, up to kAhead in
-    // flight: step k embeds the id in dscalars[1] (the prompt's last token
-    // for k = 0) and its lm-head writes the next id there, so no step waits
-    // for the host.  After each step the id and the cumulative error flag
-    // (dscalars[1..2]) are copied to a pinned ring slot and an event is
-    // recorded; the host reads slot k after that event and applies
+    // flight.  The step's token and position live on the device
+    // (dscalars[1] and [3]): step k embeds the id in dscalars[1] (the
+    // prompt's last token for k = 0), its lm-head writes the next id there,
+    // copies it with the cumulative error flag to ring slot (position % 16)
+    // in pinned host memory and advances the position, so no step waits for
+    // the host.  The host reads slot k after step k's event and applies
     // generate_with_cache's rules (generate.rs:111-189) in order: a
     // non-finite step fails the call, EOS ends it.  Steps enqueued past the
     // end only wrote cache rows beyond the final position, which the cache
@@ -886,31 +898,36 @@ wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *promp
     constexpr uint32_t kRing = 16, kAhead = 8;
     WM_HIP(ctx, hipSetDevice(ctx->device));
     if (!m->ring) {
-        WM_HIP(ctx, hipHostMalloc((void **)&m->ring, kRing * 2 * sizeof(uint32_t), hipHostMallocDefault));
+        WM_HIP(ctx, hipHostMalloc((void **)&m->ring, kRing * 2 * sizeof(uint32_t), hipHostMallocMapped));
+        WM_HIP(ctx, hipHostGetDevicePointer((void **)&m->ring_dev, m->ring, 0));
         for (hipEvent_t &e : m->ring_ev) WM_HIP(ctx, hipEventCreateWithFlags(&e, hipEventDisableTiming));
     }
     const uint32_t pos0 = kv->pos;
     // steps needed: step k yields id k; ids 0..max_new-1 are wanted, and at
     // least step 0 runs (it also appends the prompt's last token)
     const uint32_t n_steps = max_new ? max_new : 1;
+    const wm_step_tail tail{m->dscalars + 3, m->ring_dev, m->dscalars + 2, kRing - 1};
+    // step k at position pos0 + k: the kernels read the position from the
+    // device, and the host sizes the attention launches for it
+    const auto enqueue_step = [&](uint32_t k) -> bool {
+        if (!enqueue_forward(m, kv, step_pos{0, m->dscalars + 3, pos0 + k + 1}, nullptr, m->dscalars + 1))
+            return false;
+        wm_launch_q6k_argmax_fast(m->embd, m->embd_blocks, m->cfg.vocab_size, m->embd_rowgroups,
+                                  m->final_hidden, m->logits, m->dscalars + 1, m->lm_work, true,
+                                  ctx->stream, &tail);
+        return hipEventRecord(m->ring_ev[k % kRing], ctx->stream) == hipSuccess;
+    };
     m->ring[0] = prompt[n_prompt - 1];
-    WM_HIP(ctx, hipMemcpyAsync(m->dscalars + 1, m->ring, 4, hipMemcpyHostToDevice, ctx->stream));
-    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));  // ring[0] is reused below
+    m->ring[1] = 0;
+    m->ring[2] = pos0;
+    WM_HIP(ctx, hipMemcpyAsync(m->dscalars + 1, m->ring, 12, hipMemcpyHostToDevice, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));  // the ring is written by the steps below
     uint32_t enq = 0, n = 0, done = 0;
     bool stop = false;
     uint32_t failed_flag = 0;
-    const auto enqueue = [&](uint32_t k) -> bool {
-        if (!enqueue_forward(m, kv, pos0 + k, nullptr, m->dscalars + 1)) return false;
-        wm_launch_q6k_argmax_fast(m->embd, m->embd_blocks, m->cfg.vocab_size, m->embd_rowgroups,
-                                  m->final_hidden, m->logits, m->dscalars + 1, m->lm_work, true,
-                                  ctx->stream);
-        uint32_t *slot = m->ring + 2 * (k % kRing);
-        return hipMemcpyAsync(slot, m->dscalars + 1, 8, hipMemcpyDeviceToHost, ctx->stream) == hipSuccess &&
-               hipEventRecord(m->ring_ev[k % kRing], ctx->stream) == hipSuccess;
-    };
     while (done < n_steps && !stop) {
         while (enq < n_steps && enq < done + kAhead) {
-            if (!enqueue(enq)) {
+            if (!enqueue_step(enq)) {
                 hipStreamSynchronize(ctx->stream);
                 kv->pos = start;
                 return wm_set_error(ctx, WM_E_SHAPE, "greedy_generate: could not enqueue a decode step");
@@ -918,7 +935,8 @@ wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *promp
             enq++;
         }
         WM_HIP(ctx, hipEventSynchronize(m->ring_ev[done % kRing]));
-        const uint32_t id = m->ring[2 * (done % kRing)], flag = m->ring[2 * (done % kRing) + 1];
+        const uint32_t *slot = m->ring + 2 * ((pos0 + done) % kRing);
+        const uint32_t id = slot[0], flag = slot[1];
         if (flag) {
             failed_flag = flag;
             break;
@@ -931,9 +949,8 @@ wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *promp
     WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     WM_HIP(ctx, hipGetLastError());
     if (failed_flag) {
-        uint32_t *zero = m->ring;  // all reads of the ring are over
-        zero[0] = 0;
-        WM_HIP(ctx, hipMemcpyAsync(m->dscalars + 2, zero, 4, hipMemcpyHostToDevice, ctx->stream));
+        m->ring[0] = 0;  // all reads of the ring are over
+        WM_HIP(ctx, hipMemcpyAsync(m->dscalars + 2, m->ring, 4, hipMemcpyHostToDevice, ctx->stream));
         WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
         kv->pos = start;
         return wm_set_error(ctx, WM_E_NONFINITE, "forward_with_cache: non-finite hidden after layer %u",

@@ -382,7 +382,7 @@ bool wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
                          int n_tensors, uint32_t n_chunks, uint32_t groups_per_unit,
                          const wm_fused_norm &norm, const float *rope_cos, const float *rope_sin,
                          uint32_t pos, uint32_t n_rot, uint32_t rope_mask, uint32_t *absmax,
-                         hipStream_t s);
+                         hipStream_t s, const uint32_t *pos_dev = nullptr);
 void wm_launch_i2s_partial_table(const uint8_t *const *table, uint32_t n_tensors,
                                  uint32_t groups_per, uint32_t n_chunks, const uint8_t *act,
                                  int32_t *partial, uint32_t split, uint32_t rows_total,
@@ -425,9 +425,19 @@ void wm_launch_q6k_logits_argmax(const uint8_t *w, uint32_t n_blocks, uint32_t n
 // exact on the rescored rows.
 // prepared: the work buffer's prep area (wm_q6k_prep_area) already holds the
 // fixed-point copy of `hidden` (the output-norm kernel writes it).
+// After the argmax of a decode step whose position lives on the device:
+// the id and the error flag go to ring slot (position & ring_mask) (two
+// words, host memory; nullable) and the position advances by one.
+struct wm_step_tail {
+    uint32_t *pos;              // the step's position (device)
+    uint32_t *ring;             // nullable: [ring_mask + 1][2] (id, error flag)
+    const uint32_t *err_flag;   // the step's error flag (device)
+    uint32_t ring_mask;
+};
 void wm_launch_q6k_argmax_fast(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                                uint32_t n_rowgroups, const float *hidden, float *logits,
-                               uint32_t *argmax_out, void *work, bool prepared, hipStream_t s);
+                               uint32_t *argmax_out, void *work, bool prepared, hipStream_t s,
+                               const wm_step_tail *tail = nullptr);
 // test hook: the bounded pass alone (values and their error bounds)
 void wm_launch_q6k_bounded_only(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                                 uint32_t n_rowgroups, const float *hidden, float *approx,

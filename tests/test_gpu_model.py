@@ -271,6 +271,30 @@ def test_long_context_decode_bit_exact(ctx, n_pre):
     orm.close()
 
 
+def test_greedy_across_attention_sizes(ctx):
+    """The greedy loop's steps read their position on the device: 24 tokens
+    from position 2040 cross from the attention instantiation for up to
+    2048 positions to the larger one in one call, then more run after a
+    rollback, against the oracle."""
+    cfg = LONG
+    hm = bs.make_host_model(cfg, seed=51)
+    dev = bs.load_device_model(ctx, hm)
+    orm = OracleModel(hm)
+    n_pre = 2040
+    k, v = bs.kv_prefill(cfg, seed=52, n_pos=n_pre)
+    dkv, okv = dev.kv_cache(cfg.context_length), orm.kv(cfg.context_length)
+    dkv.append_positions(k, v)
+    okv.append_positions(k, v)
+    ids = dkv.greedy([9], max_new=24)
+    assert ids == okv.greedy([9], max_new=24) and dkv.position == okv.position == n_pre + 24
+    for kv in (dkv, okv):
+        kv.rollback(2050)
+    ids = dkv.greedy([4, 5], max_new=10)
+    assert ids == okv.greedy([4, 5], max_new=10) and dkv.position == okv.position == 2050 + 11
+    dev.close()
+    orm.close()
+
+
 @pytest.mark.parametrize("n_pre", [40, 300, 1500, 3000])
 def test_dense_softmax_decode_bit_exact(ctx, n_pre):
     """attn_q scaled down to 1e-6, so every score is tiny and no softmax
