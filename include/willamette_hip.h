@@ -230,6 +230,12 @@ wm_status wm_kv_cache_append_positions(wm_kv_cache *kv, const float *k, const fl
  * may be NULL). */
 wm_status wm_kv_cache_read_raw(wm_kv_cache *kv, uint32_t layer, int8_t *k, float *k_scales,
                                int8_t *v, float *v_scales, uint32_t n_pos);
+/* KVCache::read_into (src/model/kv_cache.rs:192-219): one layer's K and V
+ * dequantised (code as f32 * the position's scale) for positions
+ * [0, wm_kv_cache_position): out_k and out_v (host) each hold position x
+ * kv_dim floats.  A layer out of range is WM_E_SHAPE (the reference's
+ * GgufParse). */
+wm_status wm_kv_cache_read_into(wm_kv_cache *kv, uint32_t layer, float *out_k, float *out_v);
 
 /* forward_with_cache_into (src/model/cached_forward.rs:164-261): embed
  * `token`, run every layer at `position` (== wm_kv_cache_position), apply
@@ -239,6 +245,13 @@ wm_status wm_kv_cache_read_raw(wm_kv_cache *kv, uint32_t layer, int8_t *k, float
  * WM_E_NONFINITE returned with outputs untouched. */
 wm_status wm_forward_with_cache(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t position,
                                 float *hidden_out, float *layer_trace);
+/* forward_single_token_position_zero (src/model/forward.rs:29-69): `token`
+ * at position 0 with no cache (transformer_block_forward_position_zero,
+ * src/model/block.rs:38-105: each head attends to this token's own K and V
+ * as computed, f32, not through the int8 cache), then output_norm into
+ * hidden_out (n_embd, host).  A non-finite hidden after a layer is
+ * WM_E_NONFINITE (the reference's GgufParse). */
+wm_status wm_forward_single_token_position_zero(wm_model *m, uint32_t token, float *hidden_out);
 /* One greedy step: forward_with_cache + compute_logits + argmax
  * (src/model/generate.rs:165-187).  logits_out (vocab) and hidden_out may be
  * NULL. */

@@ -68,6 +68,7 @@ _SIGS = {
     "or_kv_read_raw": (C.c_int, _vp, C.c_uint32, _i8p, _f32p, _i8p, _f32p, C.c_uint32),
     "or_forward_with_cache": (C.c_int, _vp, _vp, C.c_uint32, C.c_uint32, _f32p, _f32p),
     "or_logits_argmax": (C.c_int, _vp, _f32p, _f32p, _u32p),
+    "or_forward_single_token_position_zero": (C.c_int, _vp, C.c_uint32, _f32p, _f32p),
     "or_greedy_generate": (C.c_int, _vp, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_int64, _u32p,
                            _u32p, _f32p),
 }

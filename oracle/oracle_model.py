@@ -47,6 +47,18 @@ class OracleModel:
     def kv(self, max_seq: int) -> "OracleKV":
         return OracleKV(self, max_seq)
 
+    def forward_position_zero(self, token: int, trace: bool = False):
+        """forward_single_token_position_zero: (hidden after output_norm[,
+        hidden after each layer]); RuntimeError on a non-finite layer."""
+        cfg = self.cfg
+        hidden = np.empty(cfg.n_embd, np.float32)
+        tr = np.empty((cfg.n_layers, cfg.n_embd), np.float32) if trace else None
+        rc = orc.lib.or_forward_single_token_position_zero(self.h, token, orc.P(hidden, C.c_float),
+                                                           orc.P(tr, C.c_float) if trace else None)
+        if rc:
+            raise RuntimeError(f"oracle position-zero forward failed rc={rc}")
+        return (hidden, tr) if trace else hidden
+
 
 class OracleKV:
     def __init__(self, m: OracleModel, max_seq: int):

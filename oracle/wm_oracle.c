@@ -662,7 +662,28 @@ static int finite_all(const float *x, size_t n) {
     return 1;
 }
 
-/* src/model/cached_forward.rs:308-415 + apply_ffn_block :451-502 */
+/* single_token_attention_position_zero (src/model/attention.rs:135-194):
+ * one position, K and V as computed (f32, not through the cache): per head
+ * s = dot_f32(q_h, k_kvh) * scale (left to right), softmax_inplace([s])
+ * (1 for a finite s, else 0), out_h[i] = w * v_kvh[i]. */
+static void attention_position_zero(or_model *m) {
+    const size_t hd = m->head_dim;
+    const float scale = 1.0f / sqrtf((float)hd);
+    const uint32_t group = m->n_heads / m->n_kv_heads;
+    for (uint32_t h = 0; h < m->n_heads; h++) {
+        const uint32_t kvh = h / group;
+        const float *qh = m->q + h * hd, *kh = m->k + kvh * hd, *vh = m->v + kvh * hd;
+        float s = 0.0f;
+        for (size_t i = 0; i < hd; i++) s += qh[i] * kh[i];
+        float w = s * scale;
+        or_softmax_inplace(&w, 1);
+        for (size_t i = 0; i < hd; i++) m->attn_out[h * hd + i] = w * vh[i];
+    }
+}
+
+/* src/model/cached_forward.rs:308-415 + apply_ffn_block :451-502; with kv
+ * NULL, transformer_block_forward_position_zero (src/model/block.rs:38-105):
+ * the same layer at position 0 with attention_position_zero and no cache */
 static int forward_one_layer(or_model *m, or_kv *kv, uint32_t l, uint32_t pos) {
     or_layer *L = &m->layers[l];
     size_t E = m->n_embd, F = m->n_ff, KV = m->kv_dim;
@@ -675,13 +696,17 @@ static int forward_one_layer(or_model *m, or_kv *kv, uint32_t l, uint32_t pos) {
         or_rope_neox(m->q + h * m->head_dim, m->head_dim, m->head_dim, pos, m->rope_base);
     for (uint32_t h = 0; h < m->n_kv_heads; h++)
         or_rope_neox(m->k + h * m->head_dim, m->head_dim, m->head_dim, pos, m->rope_base);
-    /* append at this position, layer l */
-    if (kv->pos != pos) return -2;
-    if (pos >= kv->max_seq) return -5;
-    size_t off = ((size_t)l * kv->max_seq + pos) * KV, so = (size_t)l * kv->max_seq + pos;
-    kv->ks[so] = or_kv_quantise(m->k, KV, kv->k + off);
-    kv->vs[so] = or_kv_quantise(m->v, KV, kv->v + off);
-    sdpa(m, kv, l, pos + 1);
+    if (kv) {
+        /* append at this position, layer l */
+        if (kv->pos != pos) return -2;
+        if (pos >= kv->max_seq) return -5;
+        size_t off = ((size_t)l * kv->max_seq + pos) * KV, so = (size_t)l * kv->max_seq + pos;
+        kv->ks[so] = or_kv_quantise(m->k, KV, kv->k + off);
+        kv->vs[so] = or_kv_quantise(m->v, KV, kv->v + off);
+        sdpa(m, kv, l, pos + 1);
+    } else {
+        attention_position_zero(m);
+    }
     or_rms_norm(m->attn_out, L->attn_sub_norm, E, m->eps, m->sub);
     if ((rc = linear(&L->o, E, E, m->sub, m->wo))) return rc;
     for (size_t d = 0; d < E; d++) m->hidden[d] += m->wo[d];
@@ -714,6 +739,23 @@ int or_forward_with_cache(or_model *m, or_kv *kv, uint32_t token, uint32_t pos,
         return rc;
     }
     kv->pos = pos + 1;
+    or_rms_norm(m->hidden, m->output_norm, m->n_embd, m->eps, out_hidden);
+    return 0;
+}
+
+/* forward_single_token_position_zero (src/model/forward.rs:29-69): the
+ * token at position 0 with no cache; a non-finite hidden after any layer
+ * fails the call (-3). */
+int or_forward_single_token_position_zero(or_model *m, uint32_t token, float *out_hidden,
+                                          float *layer_trace) {
+    if (!m || !m->token_embd || !m->output_norm || token >= m->vocab) return -2;
+    size_t rb = m->n_embd / Q6K_VALUES * Q6K_BYTES;
+    int rc = or_q6k_dequantize_row(m->token_embd + (size_t)token * rb, rb, m->hidden, m->n_embd);
+    for (uint32_t l = 0; !rc && l < m->n_layers; l++) {
+        rc = forward_one_layer(m, NULL, l, 0);
+        if (!rc && layer_trace) memcpy(layer_trace + (size_t)l * m->n_embd, m->hidden, m->n_embd * 4);
+    }
+    if (rc) return rc;
     or_rms_norm(m->hidden, m->output_norm, m->n_embd, m->eps, out_hidden);
     return 0;
 }

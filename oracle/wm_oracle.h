@@ -113,6 +113,11 @@ int or_kv_read_raw(const or_kv *kv, uint32_t layer, int8_t *k, float *ks, int8_t
 int or_forward_with_cache(or_model *m, or_kv *kv, uint32_t token, uint32_t pos,
                           float *out_hidden, float *layer_trace);
 /* src/model/lm_head.rs:112-122 + argmax. */
+/* forward_single_token_position_zero (src/model/forward.rs:29-69): no
+ * cache, attention over the one position with f32 K/V; -3 on a non-finite
+ * hidden after a layer. */
+int or_forward_single_token_position_zero(or_model *m, uint32_t token, float *out_hidden,
+                                          float *layer_trace);
 int or_logits_argmax(or_model *m, const float *hidden, float *logits, uint32_t *next);
 /* src/model/generate.rs:111-189 on an existing cache (prefill of `prompt`,
  * then greedy steps).  logits_trace (nullable) gets max_new x vocab. */

@@ -179,6 +179,14 @@ class DeviceModel:
     def kv_cache(self, max_seq: int) -> "DeviceKV":
         return DeviceKV(self, max_seq)
 
+    def forward_position_zero(self, token: int) -> np.ndarray:
+        """forward_single_token_position_zero (src/model/forward.rs:29): the
+        hidden after output_norm, no cache."""
+        hidden = np.empty(self.cfg.n_embd, np.float32)
+        self.ctx.check(wh.lib.wm_forward_single_token_position_zero(self.h, token,
+                                                                    wh._ptr(hidden, wh.C.c_float)))
+        return hidden
+
     def batch_forward(self, kvs, seqs, want_hidden: bool = True, want_next: bool = True):
         """Ragged step: seqs[i] (token ids) appended to kvs[i] in one batch.
         Returns (last hidden per sequence, next token per sequence)."""
@@ -240,6 +248,15 @@ class DeviceKV:
                                                    wh._ptr(ks, wh.C.c_float), wh._ptr(v, wh.C.c_int8),
                                                    wh._ptr(vs, wh.C.c_float), n_pos))
         return k.reshape(n_pos, kvd), ks, v.reshape(n_pos, kvd), vs
+
+    def read_into(self, layer: int):
+        """KVCache::read_into: (K, V) dequantised, [position][kv_dim] f32."""
+        n = self.position * self.model.cfg.kv_dim
+        k = np.empty(n, np.float32)
+        v = np.empty(n, np.float32)
+        self.ctx.check(wh.lib.wm_kv_cache_read_into(self.h, layer, wh._ptr(k, wh.C.c_float),
+                                                    wh._ptr(v, wh.C.c_float)))
+        return k.reshape(-1, self.model.cfg.kv_dim), v.reshape(-1, self.model.cfg.kv_dim)
 
     def forward(self, token: int, pos: int, trace: bool = False):
         cfg = self.model.cfg

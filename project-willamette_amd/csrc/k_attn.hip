@@ -387,6 +387,30 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
     }
 }
 
+// single_token_attention_position_zero (src/model/attention.rs:135-194):
+// one position, this token's K (after RoPE) and V as computed, not through
+// the cache.  Per head h (one workgroup of head_dim threads): s =
+// dot_f32(q_h, k_kvh) left to right, times scale; softmax of the one score
+// is 1 for a finite s and 0 otherwise (attention.rs:45-73); out = w * v_kvh.
+__global__ __launch_bounds__(kMaxHeadDim) void k_attn_position_zero(const float *q, const float *k,
+                                                                    const float *v, float *out,
+                                                                    uint32_t head_dim, uint32_t group,
+                                                                    float scale) {
+    __shared__ float w_s;
+    const uint32_t h = blockIdx.x, kvh = h / group, tid = threadIdx.x;
+    if (tid == 0) {
+        const float *qh = q + (uint64_t)h * head_dim, *kh = k + (uint64_t)kvh * head_dim;
+        float s = 0.0f;
+        for (uint32_t i = 0; i < head_dim; i++) s = s + qh[i] * kh[i];
+        const float sc = s * scale;
+        // max over [sc] is sc unless sc is NaN (-inf stays); a non-finite
+        // max zeroes the weights, else exp(sc - sc) / 1 = 1
+        w_s = isfinite(sc) ? 1.0f : 0.0f;
+    }
+    wm_sync_lds();
+    if (tid < head_dim) out[(uint64_t)h * head_dim + tid] = w_s * v[(uint64_t)kvh * head_dim + tid];
+}
+
 }  // namespace
 
 // Returns false (nothing launched) for a shape the kernels do not cover:
@@ -415,5 +439,14 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
         hipLaunchKernelGGL(k_attn_softmax_v<2>, grid, dim3(kSvThreads), lds, s, a);
     else  // nb <= 4096, the models' context limit
         hipLaunchKernelGGL(k_attn_softmax_v<4>, grid, dim3(kSvThreads), lds, s, a);
+    return true;
+}
+
+bool wm_launch_attention_position_zero(const float *q, const float *k_new, const float *v_new,
+                                       float *out, uint32_t n_heads, uint32_t n_kv_heads,
+                                       uint32_t head_dim, float scale, hipStream_t s) {
+    if (head_dim == 0 || head_dim > kMaxHeadDim || n_kv_heads == 0 || n_heads % n_kv_heads) return false;
+    hipLaunchKernelGGL(k_attn_position_zero, dim3(n_heads), dim3(kMaxHeadDim), 0, s, q, k_new, v_new,
+                       out, head_dim, n_heads / n_kv_heads, scale);
     return true;
 }

@@ -144,6 +144,33 @@ bool wm_launch_rmsnorm_quant(float *x, const float *res_y, const float *w, uint3
     return false;  // n above 16384: no instantiation
 }
 
+// KVCache::read_into (src/model/kv_cache.rs:192-219) for one layer: rows
+// [0, n_pos) of K and V as f32, q as f32 * the row's scale.
+__global__ __launch_bounds__(256) void k_kv_dequant(const int8_t *__restrict__ k_cache,
+                                                    const float *__restrict__ k_scales,
+                                                    const int8_t *__restrict__ v_cache,
+                                                    const float *__restrict__ v_scales,
+                                                    uint64_t n, uint32_t kv_dim,
+                                                    float *__restrict__ k_out,
+                                                    float *__restrict__ v_out) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t p = i / kv_dim;
+        k_out[i] = (float)k_cache[i] * k_scales[p];
+        v_out[i] = (float)v_cache[i] * v_scales[p];
+    }
+}
+
+void wm_launch_kv_dequant(const int8_t *k_cache, const float *k_scales, const int8_t *v_cache,
+                          const float *v_scales, uint32_t n_pos, uint32_t kv_dim, float *k_out,
+                          float *v_out, hipStream_t s) {
+    const uint64_t n = (uint64_t)n_pos * kv_dim;
+    if (!n) return;
+    const uint32_t blocks = (uint32_t)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+    hipLaunchKernelGGL(k_kv_dequant, dim3(blocks), dim3(256), 0, s, k_cache, k_scales, v_cache,
+                       v_scales, n, kv_dim, k_out, v_out);
+}
+
 void wm_launch_kv_append(const float *k, const float *v, uint32_t kv_dim, uint32_t n_layers,
                          uint32_t pos0, uint32_t n_pos, uint32_t max_seq, int8_t *k_cache,
                          float *k_scales, int8_t *v_cache, float *v_scales, hipStream_t s) {

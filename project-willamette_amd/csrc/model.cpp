@@ -33,9 +33,15 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
                          uint32_t head_dim, uint32_t n_past, float scale, const float *k_new,
                          const float *v_new, const uint32_t *kv_absmax, hipStream_t s,
                          const uint32_t *pos_dev = nullptr, uint32_t n_max = 0);
+bool wm_launch_attention_position_zero(const float *q, const float *k_new, const float *v_new,
+                                       float *out, uint32_t n_heads, uint32_t n_kv_heads,
+                                       uint32_t head_dim, float scale, hipStream_t s);
 void wm_launch_kv_append(const float *k, const float *v, uint32_t kv_dim, uint32_t n_layers,
                          uint32_t pos0, uint32_t n_pos, uint32_t max_seq, int8_t *k_cache,
                          float *k_scales, int8_t *v_cache, float *v_scales, hipStream_t s);
+void wm_launch_kv_dequant(const int8_t *k_cache, const float *k_scales, const int8_t *v_cache,
+                          const float *v_scales, uint32_t n_pos, uint32_t kv_dim, float *k_out,
+                          float *v_out, hipStream_t s);
 
 namespace {
 
@@ -194,14 +200,22 @@ bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, step_pos sp, float 
     if (layer_trace_dev && l > 0)
         hipMemcpyAsync(layer_trace_dev + (size_t)(l - 1) * E, H[cur], (size_t)E * 4,
                        hipMemcpyDeviceToDevice, s);
-    // attention; this token's K/V row goes into the cache on the way
-    const size_t lay = (size_t)l * kv->max_seq;
-    if (want(ROLE_SCORES_SOFTMAX_V) &&
-        !wm_launch_attention(m->q, kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV, kv->vs + lay,
-                             m->scores, c.context_length, m->attn_out, c.n_heads, c.n_kv_heads,
-                             c.head_dim, pos + 1, scale, m->k_new, m->v_new, kv_absmax, s, sp.dev,
-                             sp.n_max))
-        return false;
+    // attention; this token's K/V row goes into the cache on the way (no
+    // cache: the position-zero attention on this token's own K and V)
+    if (want(ROLE_SCORES_SOFTMAX_V)) {
+        if (!kv) {
+            if (!wm_launch_attention_position_zero(m->q, m->k_new, m->v_new, m->attn_out, c.n_heads,
+                                                   c.n_kv_heads, c.head_dim, scale, s))
+                return false;
+        } else {
+            const size_t lay = (size_t)l * kv->max_seq;
+            if (!wm_launch_attention(m->q, kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV,
+                                     kv->vs + lay, m->scores, c.context_length, m->attn_out,
+                                     c.n_heads, c.n_kv_heads, c.head_dim, pos + 1, scale, m->k_new,
+                                     m->v_new, kv_absmax, s, sp.dev, sp.n_max))
+                return false;
+        }
+    }
     // attn_sub_norm, then O (the launch also clears the K/V absmax slots)
     wm_fused_norm sn{};
     sn.x = m->attn_out;
@@ -773,6 +787,28 @@ wm_status wm_kv_cache_read_raw(wm_kv_cache *kv, uint32_t layer, int8_t *k, float
     return WM_OK;
 }
 
+wm_status wm_kv_cache_read_into(wm_kv_cache *kv, uint32_t layer, float *out_k, float *out_v) {
+    if (!kv || !out_k || !out_v) return WM_E_ARG;
+    wm_ctx *ctx = kv->m->ctx;
+    if (layer >= kv->m->cfg.n_layers)
+        return wm_set_error(ctx, WM_E_SHAPE, "KVCache::read_into: layer_idx %u >= n_layers %u", layer,
+                            kv->m->cfg.n_layers);
+    const size_t KV = kv->m->kv_dim, lay = (size_t)layer * kv->max_seq, n = (size_t)kv->pos * KV;
+    if (!n) return WM_OK;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    void *buf = nullptr;
+    wm_status st = wm_ctx_scratch(ctx, 2 * n * 4, &buf);
+    if (st) return st;
+    float *dk = static_cast<float *>(buf), *dv = dk + n;
+    wm_launch_kv_dequant(kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV, kv->vs + lay, kv->pos,
+                         (uint32_t)KV, dk, dv, ctx->stream);
+    WM_HIP(ctx, hipGetLastError());
+    WM_HIP(ctx, hipMemcpyAsync(out_k, dk, n * 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipMemcpyAsync(out_v, dv, n * 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return WM_OK;
+}
+
 wm_status wm_forward_with_cache(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t position,
                                 float *hidden_out, float *layer_trace) {
     if (!m || !kv) return WM_E_ARG;
@@ -799,6 +835,33 @@ wm_status wm_forward_with_cache(wm_model *m, wm_kv_cache *kv, uint32_t token, ui
         WM_HIP(ctx, hipMemcpyAsync(layer_trace, trace_dev, (size_t)m->cfg.n_layers * E * 4,
                                    hipMemcpyDeviceToHost, ctx->stream));
     WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return WM_OK;
+}
+
+wm_status wm_forward_single_token_position_zero(wm_model *m, uint32_t token, float *hidden_out) {
+    if (!m || !hidden_out) return WM_E_ARG;
+    wm_ctx *ctx = m->ctx;
+    if (!model_ready(m)) return wm_set_error(ctx, WM_E_STATE, "model: weights not fully set");
+    if (token >= m->cfg.vocab_size)
+        return wm_set_error(ctx, WM_E_SHAPE, "forward_single_token: token_id %u out of vocab range %u",
+                            token, m->cfg.vocab_size);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    WM_HIP(ctx, hipMemcpyAsync(m->dscalars, &token, 4, hipMemcpyHostToDevice, ctx->stream));
+    if (!enqueue_forward(m, nullptr, step_pos{0, nullptr, 0}, nullptr))
+        return wm_set_error(ctx, WM_E_SHAPE, "forward_single_token: no kernel for this model shape");
+    WM_HIP(ctx, hipGetLastError());
+    uint32_t flag = 0;
+    WM_HIP(ctx, hipMemcpyAsync(&flag, m->dscalars + 2, 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipMemcpyAsync(hidden_out, m->final_hidden, (size_t)m->cfg.n_embd * 4,
+                               hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (flag) {
+        uint32_t zero = 0;
+        WM_HIP(ctx, hipMemcpyAsync(m->dscalars + 2, &zero, 4, hipMemcpyHostToDevice, ctx->stream));
+        WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        return wm_set_error(ctx, WM_E_NONFINITE, "forward_single_token: non-finite hidden after layer %u",
+                            flag - 1);
+    }
     return WM_OK;
 }
 

@@ -139,6 +139,8 @@ EXPORTS = {
     "wm_kv_cache_append_positions": (C.c_int, _vp, _f32p, _f32p, C.c_uint32),
     "wm_kv_cache_read_raw": (C.c_int, _vp, C.c_uint32, _i8p, _f32p, _i8p, _f32p, C.c_uint32),
     "wm_forward_with_cache": (C.c_int, _vp, _vp, C.c_uint32, C.c_uint32, _f32p, _f32p),
+    "wm_forward_single_token_position_zero": (C.c_int, _vp, C.c_uint32, _f32p),
+    "wm_kv_cache_read_into": (C.c_int, _vp, C.c_uint32, _f32p, _f32p),
     "wm_decode_step": (C.c_int, _vp, _vp, C.c_uint32, C.c_uint32, _f32p, _f32p, _u32p),
     "wm_greedy_generate": (C.c_int, _vp, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_int64, _u32p,
                            _u32p),

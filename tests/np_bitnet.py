@@ -185,5 +185,20 @@ class NpModel:
             trace.append(x.copy())
         return self.output(x), np.stack(trace)
 
+    def layer_position_zero(self, l: int, x: np.ndarray) -> np.ndarray:
+        """forward_single_token_position_zero's layer (src/model/block.rs:38-105):
+        position 0, no cache: the attention sees only this token's own K and V
+        as computed (no int8 round trip)."""
+        saved = self.k[l], self.v[l]
+        self.k[l], self.v[l] = [], []
+        T, sc = self.t[l], self.hm.layers[l].scales
+        xn = rms_norm(x, self.hm.layers[l].norms["attn_norm"].astype(np.float64), self.cfg.rms_eps)
+        k = self.rope(bitlinear(T["attn_k"], sc["attn_k"], xn), 0) if self.mk.rope_on_k else \
+            bitlinear(T["attn_k"], sc["attn_k"], xn)
+        v = bitlinear(T["attn_v"], sc["attn_v"], xn)
+        out, _, _ = self.layer(l, x, 0, kv_row=(k, v))
+        self.k[l], self.v[l] = saved
+        return out
+
     def logits(self, hidden: np.ndarray) -> np.ndarray:
         return q6k_dequant(self.hm.token_embd, self.cfg.n_embd) @ hidden

@@ -98,6 +98,40 @@ def test_greedy_eos_stops(pair):
     assert ids == okv.greedy([1, 2, 3], max_new=8)
 
 
+def test_position_zero_forward_bit_exact(pair):
+    """forward_single_token_position_zero: no cache, each head attends to the
+    token's own f32 K/V; the final hidden is bit-identical to the oracle's,
+    and differs from the cached step at position 0 (whose V goes through
+    the int8 cache)."""
+    cfg, hm, dev, orm = pair
+    for tok in [0, 3, 17, cfg.vocab - 1]:
+        h = dev.forward_position_zero(tok)
+        assert bits_equal(h, orm.forward_position_zero(tok)), f"token {tok}"
+    dkv = dev.kv_cache(cfg.context_length)
+    assert not bits_equal(dev.forward_position_zero(3), dkv.forward(3, 0))
+
+
+def test_kv_read_into_dequantises(pair):
+    """KVCache::read_into: every cached row as code * the row's scale, for
+    positions [0, position), equal to the raw codes and scales dequantised
+    on the host; a layer out of range is rejected."""
+    cfg, hm, dev, orm = pair
+    dkv = dev.kv_cache(cfg.context_length)
+    k, v = bs.kv_prefill(cfg, seed=8, n_pos=9)
+    dkv.append_positions(k, v)
+    dkv.forward(4, 9)
+    for l in range(cfg.n_layers):
+        K, V = dkv.read_into(l)
+        kk, ks, vv, vs = dkv.read_raw(l, 10)
+        assert K.shape == (10, cfg.kv_dim)
+        assert bits_equal(K, kk.astype(np.float32) * ks[:, None])
+        assert bits_equal(V, vv.astype(np.float32) * vs[:, None])
+    with pytest.raises(wh.WillametteError) as e:
+        dkv.read_into(cfg.n_layers)
+    assert e.value.kind == "Shape"
+    assert dev.kv_cache(cfg.context_length).read_into(0)[0].shape == (0, cfg.kv_dim)
+
+
 def test_position_protocol_and_nonfinite_rollback(ctx):
     cfg = SMALL
     hm = bs.make_host_model(cfg, seed=5)
@@ -128,6 +162,15 @@ def test_position_protocol_and_nonfinite_rollback(ctx):
     with pytest.raises(RuntimeError):
         okv.forward(1, 0)
     assert okv.position == 0
+    # the no-cache position-0 forward fails the same way, then leaves the
+    # error flag clear for the next call
+    with pytest.raises(wh.WillametteError) as e:
+        bad.forward_position_zero(1)
+    assert e.value.kind == "NonFinite"
+    with pytest.raises(RuntimeError):
+        orm.forward_position_zero(1)
+    h = dev.forward_position_zero(2)
+    assert np.all(np.isfinite(h))
 
 
 def test_greedy_nonfinite_step_with_steps_in_flight(ctx):

@@ -268,3 +268,77 @@ def test_zero_weight_model_closed_form():
     logits, nxt = kv.logits_argmax(h)
     assert np.all(logits == logits[0]) and nxt == 0
     orm.close()
+
+
+# ---------------------------------------------------------------------------
+# forward_single_token_position_zero (no cache, f32 K/V at position 0)
+# ---------------------------------------------------------------------------
+
+def position_zero_deviation(hm, mistakes, tokens, quantised_v=False):
+    """The oracle's no-cache position-0 forward against np_bitnet's
+    layer_position_zero, teacher-forced layer by layer; with quantised_v the
+    float64 side runs the cached layer instead (K/V through the int8 round
+    trip), the mistake of treating position zero like a cached step."""
+    cfg = hm.cfg
+    orm = OracleModel(hm)
+    npm = nb.NpModel(hm, mistakes)
+    dev = 0.0
+    for tok in tokens:
+        rh, rtr = orm.forward_position_zero(tok, trace=True)
+        x = npm.embed(tok)
+        for l in range(cfg.n_layers):
+            if quantised_v:
+                npm.k[l], npm.v[l] = [], []
+                xo, _, _ = npm.layer(l, x, 0)
+            else:
+                xo = npm.layer_position_zero(l, x)
+            dev = max(dev, np.abs(xo - rtr[l]).max() / np.abs(rtr[l]).max())
+            x = rtr[l].astype(np.float64)
+        dev = max(dev, np.abs(npm.output(x) - rh).max() / np.abs(rh).max())
+    orm.close()
+    return dev
+
+
+def test_position_zero_matches_float64_model():
+    hm = bs.make_host_model(GQA4, seed=808)
+    assert position_zero_deviation(hm, None, [5, 77, 299]) <= LAYER_TOL
+
+
+@pytest.mark.parametrize("name", ["kv_head_mod", "no_attn_sub_norm", "no_o_residual", "relu_not_squared"])
+def test_position_zero_planted_mistake_is_caught(name):
+    hm = bs.make_host_model(GQA4, seed=808)
+    assert position_zero_deviation(hm, MISTAKES[name], [5, 77]) > 1000 * LAYER_TOL, name
+
+
+def test_position_zero_is_not_the_cached_step():
+    """The no-cache path attends to the f32 K/V it just computed; the cached
+    step at position 0 attends to their int8 round trip.  Comparing the
+    oracle's position-zero forward with the cached layer misses the
+    tolerance by far, so the comparison above would catch an oracle that
+    quantised V here."""
+    hm = bs.make_host_model(GQA4, seed=808)
+    assert position_zero_deviation(hm, None, [5, 77], quantised_v=True) > 100 * LAYER_TOL
+
+
+def test_position_zero_zero_weights_agree_with_cache():
+    """tests/synthetic_model.rs:497-523: with all-zero ternary weights both
+    paths compute the same hidden (every BitLinear returns exact 0)."""
+    hm = bs.make_host_model(GQA4, seed=6)
+    for hl in hm.layers:
+        for r in bs.ROLES:
+            hl.packed[r][:] = 0x55
+    orm = OracleModel(hm)
+    h0 = orm.forward_position_zero(3)
+    h1 = orm.kv(8).forward(3, 0)
+    assert np.array_equal(h0, h1) and np.all(np.isfinite(h0))
+    orm.close()
+
+
+def test_position_zero_nonfinite_fails():
+    """forward.rs:47-55: a non-finite hidden after a layer fails the call."""
+    hm = bs.make_host_model(GQA4, seed=5)
+    hm.layers[1].norms["ffn_sub_norm"][:] = np.inf
+    orm = OracleModel(hm)
+    with pytest.raises(RuntimeError):
+        orm.forward_position_zero(1)
+    orm.close()
