@@ -11,7 +11,10 @@
 //     (v_mfma_i32_16x16x64_i8) over all tokens at once;
 //   * RMSNorm, the int8 quantiser, RoPE, the KV quantiser and attention run
 //     per token exactly as in the decode kernels (exact sequential sums).
+#include <algorithm>
+
 #include "wm_internal.h"
+#include "wm_norm.h"
 #include "wm_seqsum.h"
 
 namespace {
@@ -22,19 +25,27 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // I2_S x int8 GEMM on MFMA
 // ---------------------------------------------------------------------------
 //
-// One workgroup = one 64-row group of one weight tensor x 64 tokens; wave w
-// owns rows 16w..16w+15 and runs four 16x16x64 MFMAs (tokens 0-15, 16-31,
-// 32-47, 48-63) per 64-column chunk.  MFMA operands, lane l = 16 * seg + r:
-//   A (weights): row r of the wave's 16, dword seg of the row's 16-byte chunk
-//                = 16 codes, expanded to one byte each ({0,1,2} = ternary+1);
-//   B (activations): token r of the 16, the 16 bytes of the same columns
-//                (the GEMM activation layout stores them contiguously);
+// One workgroup = four 64-row groups x 64 tokens: wave w owns group
+// 4 * blockIdx.x + w (of whichever tensor it falls in) and all 64 tokens,
+// i.e. 4 row tiles x 4 token tiles = 16 MFMAs (v_mfma_i32_16x16x64_i8) per
+// 64-column chunk.  MFMA operands, lane l = 16 * seg + r:
+//   A (weights): row r of a 16-row tile, dword seg of the row's 16-byte
+//                chunk = 16 codes, expanded to one byte each ({0,1,2} =
+//                ternary + 1);
+//   B (activations): token r of a 16-token tile, the 16 bytes of the same
+//                columns (the GEMM activation layout stores them
+//                contiguously);
 //   D: lane l holds rows 4*seg .. 4*seg+3 of token r.
 // Σ_k (t_k + 1)·a_k - Σ_k a_k = Σ_k t_k·a_k is exact in i32 for any k order.
+// Activations and weights go through LDS in blocks of kGemmKB chunks,
+// double-buffered (direct global->LDS loads of the next block run while the
+// waves compute the current one), so each activation byte is read from L2
+// once per four groups, and each B fragment read from LDS feeds four MFMAs.
 struct gemm_args {
     wm_gemm_desc d[WM_GEMM_MAX_DESC];
     uint32_t group_end[WM_GEMM_MAX_DESC];
     int n_desc;
+    uint32_t n_groups;  // over all tensors
     uint32_t n_chunks;
     const uint8_t *act;
     uint32_t m, m_pad;
@@ -55,80 +66,177 @@ __device__ __forceinline__ v4i expand_codes(uint32_t w) {
     return a;
 }
 
-__global__ __launch_bounds__(256) void k_i2s_gemm(gemm_args a) {
-    const uint32_t gid = blockIdx.x;
-    // tensor of this group, by selects (no dynamic index into the argument block)
-    const uint8_t *w = a.d[0].w;
-    uint32_t g0 = 0, row0 = a.d[0].out_row0, out_dim = a.d[0].out_dim;
-    float wscale = a.d[0].scale;
+constexpr uint32_t kGemmKB = 4;  // chunks per LDS block
+constexpr uint32_t kGemmActChunk = WM_GEMM_TILE_TOKENS * 64;  // bytes of a chunk's activation tile
+// LDS of a workgroup over NG 64-row groups: two blocks of kGemmKB chunks
+// (activations, then the groups' weights), later the output tile
+template <int NG>
+constexpr uint32_t gemm_block_bytes() { return kGemmKB * (kGemmActChunk + NG * 1024u); }
+template <int NG>
+constexpr uint32_t gemm_out_stride() { return NG * 64u + 4u; }  // floats per token row of the output tile
+template <int NG>
+constexpr size_t gemm_lds_bytes() {
+    return 2 * gemm_block_bytes<NG>() > (size_t)WM_GEMM_TILE_TOKENS * gemm_out_stride<NG>() * 4
+               ? 2 * gemm_block_bytes<NG>()
+               : (size_t)WM_GEMM_TILE_TOKENS * gemm_out_stride<NG>() * 4;
+}
+
+// 16-byte slot of (token t, segment g) in a chunk's activation tile in LDS:
+// the segment is XOR-swizzled by bits 3:2 of the token, so that the 16 lanes
+// reading segment g of tokens r..r+15 hit 16 different bank groups.
+__device__ __forceinline__ uint32_t gemm_act_slot(uint32_t t, uint32_t g) {
+    return t * 4 + (g ^ ((t >> 2) & 3u));
+}
+
+struct gemm_group {
+    const uint8_t *w;
+    uint32_t g, row0, out_dim;
+    float scale;
+    bool live;
+};
+
+__device__ __forceinline__ gemm_group gemm_group_of(const gemm_args &a, uint32_t gid) {
+    // the tensor of global group gid, by selects (no dynamic index into the argument block)
+    gemm_group r{a.d[0].w, gid, a.d[0].out_row0, a.d[0].out_dim, a.d[0].scale, gid < a.n_groups};
 #pragma unroll
     for (int i = 1; i < WM_GEMM_MAX_DESC; i++) {
         const bool in = i < a.n_desc && gid >= a.group_end[i - 1];
-        w = in ? a.d[i].w : w;
-        g0 = in ? a.group_end[i - 1] : g0;
-        row0 = in ? a.d[i].out_row0 : row0;
-        out_dim = in ? a.d[i].out_dim : out_dim;
-        wscale = in ? a.d[i].scale : wscale;
+        r.w = in ? a.d[i].w : r.w;
+        r.g = in ? gid - a.group_end[i - 1] : r.g;
+        r.row0 = in ? a.d[i].out_row0 : r.row0;
+        r.out_dim = in ? a.d[i].out_dim : r.out_dim;
+        r.scale = in ? a.d[i].scale : r.scale;
     }
-    const uint32_t g = gid - g0;
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    return r;
+}
+
+// NG 64-row groups per workgroup of four waves: wave w works on group
+// w / (4 / NG) and on TPW = NG token tiles of 16 (NG = 4: one group and all
+// 64 tokens per wave; NG = 1: the workgroup's one group, 16 tokens per wave).
+template <int NG>
+__global__ __launch_bounds__(256) void k_i2s_gemm(gemm_args a) {
+    constexpr uint32_t WPG = 4 / NG, TPW = 4 / WPG;  // waves per group, token tiles per wave
+    constexpr uint32_t kBlock = gemm_block_bytes<NG>(), kWChunk = NG * 1024u;
+    constexpr uint32_t kOutStride = gemm_out_stride<NG>();
+    extern __shared__ __align__(16) uint8_t gl[];  // [2] blocks (activations, weights), then the output tile
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6)), lane = tid & 63;
     const uint32_t r16 = lane & 15, seg = lane >> 4;
+    const uint32_t q = wave / WPG, s0 = (wave % WPG) * TPW;  // this wave's group and first token tile
+    const gemm_group G = gemm_group_of(a, blockIdx.x * NG + q);
     const uint32_t n0 = blockIdx.y * WM_GEMM_TILE_TOKENS;
-    const uint8_t *wp = w + (uint64_t)g * a.n_chunks * 1024 + (wave * 16 + r16) * 16 + seg * 4;
-    const uint8_t *ap = a.act + (uint64_t)(n0 + r16) * 64 + seg * 16;
+    // Both operands reach LDS by direct global->LDS loads (global_load_lds:
+    // lane l of a wave writes 16 bytes at the wave's LDS base + 16 l), a
+    // block of kGemmKB chunks at a time, double-buffered.  Per chunk:
+    //   activations: wave w fills slots 64 w .. 64 w + 63 of the 256-slot
+    //     tile; slot p holds token p / 4, segment (p % 4) ^ bits 3:2 of the
+    //     token (gemm_act_slot);
+    //   weights: wave w < NG copies group w's 1024-byte chunk (row r's 16
+    //     bytes to slot r); a group past the last is group 0's copy, its
+    //     sums discarded.
+    const gemm_group GW = gemm_group_of(a, blockIdx.x * NG + (wave < NG ? wave : 0));
+    const uint8_t *wsrc = (GW.live ? GW.w + (uint64_t)GW.g * a.n_chunks * 1024 : a.d[0].w) + lane * 16;
+    const uint32_t p_act = wave * 64 + lane, t_act = p_act >> 2;
+    const uint32_t g_act = (p_act & 3u) ^ ((t_act >> 2) & 3u);
+    const uint8_t *asrc = a.act + (uint64_t)(n0 + t_act) * 64 + g_act * 16;
     const uint64_t cstride = (uint64_t)a.m_pad * 64;
-    v4i acc[4];
+    const uint32_t nc = a.n_chunks, nblocks = (nc + kGemmKB - 1) / kGemmKB;
+#define WM_GEMM_ISSUE(BLK, BUF)                                                                  \
+    do {                                                                                         \
+        uint8_t *blk_ = gl + (BUF) * kBlock;                                                     \
+        _Pragma("unroll") for (uint32_t kb = 0; kb < kGemmKB; kb++) {                            \
+            const uint32_t c = min((BLK) * kGemmKB + kb, nc - 1); /* past the end: last chunk */ \
+            __builtin_amdgcn_global_load_lds(asrc + c * cstride,                                 \
+                                             blk_ + kb * kGemmActChunk + wave * 1024, 16, 0, 0); \
+            if (wave < NG)                                                                       \
+                __builtin_amdgcn_global_load_lds(wsrc + (uint64_t)c * 1024,                      \
+                                                 blk_ + kGemmKB * kGemmActChunk + kb * kWChunk + \
+                                                     wave * 1024, 16, 0, 0);                     \
+        }                                                                                        \
+    } while (0)
+    v4i acc[4][TPW];
 #pragma unroll
-    for (int s = 0; s < 4; s++) acc[s] = v4i{0, 0, 0, 0};
-    uint32_t c = 0;
-    for (; c + 4 <= a.n_chunks; c += 4) {
-        uint32_t wv[4];
-        v4i b[4][4];
+    for (int rt = 0; rt < 4; rt++)
 #pragma unroll
-        for (int u = 0; u < 4; u++) wv[u] = *reinterpret_cast<const uint32_t *>(wp + (uint64_t)(c + u) * 1024);
+        for (uint32_t s = 0; s < TPW; s++) acc[rt][s] = v4i{0, 0, 0, 0};
+    // this lane's B slots (token tile s0 + s: token 16 (s0 + s) + r16,
+    // segment seg) and A words (row tile rt: row 16 rt + r16, dword seg)
+    uint32_t b_off[TPW];
 #pragma unroll
-        for (int u = 0; u < 4; u++)
+    for (uint32_t s = 0; s < TPW; s++) b_off[s] = gemm_act_slot((s0 + s) * 16 + r16, seg) * 16;
+    const uint32_t a_off = kGemmKB * kGemmActChunk + q * 1024 + r16 * 16 + seg * 4;
+    WM_GEMM_ISSUE(0u, 0u);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (uint32_t b = 0; b < nblocks; b++) {
+        const bool more = b + 1 < nblocks;
+        if (more) WM_GEMM_ISSUE(b + 1, (b + 1) & 1);
+        const uint8_t *blk = gl + (b & 1) * kBlock;
+        const uint32_t kbn = min(kGemmKB, nc - b * kGemmKB);
 #pragma unroll
-            for (int s = 0; s < 4; s++)
-                b[u][s] = *reinterpret_cast<const v4i *>(ap + (c + u) * cstride + s * 1024);
+        for (uint32_t kb = 0; kb < kGemmKB; kb++) {
+            if (kb < kbn) {
+                v4i bv[TPW];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const v4i av = expand_codes(wv[u]);
+                for (uint32_t s = 0; s < TPW; s++)
+                    bv[s] = *reinterpret_cast<const v4i *>(blk + kb * kGemmActChunk + b_off[s]);
 #pragma unroll
-            for (int s = 0; s < 4; s++)
-                acc[s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b[u][s], acc[s], 0, 0, 0);
+                for (int rt = 0; rt < 4; rt++) {
+                    const uint32_t wv =
+                        *reinterpret_cast<const uint32_t *>(blk + a_off + kb * kWChunk + rt * 256);
+                    const v4i av = expand_codes(wv);
+#pragma unroll
+                    for (uint32_t s = 0; s < TPW; s++)
+                        acc[rt][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[s], acc[rt][s], 0, 0, 0);
+                }
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of block b + 1
+        __syncthreads();  // everyone's, and block b fully read
+    }
+#undef WM_GEMM_ISSUE
+    // epilogue: y = (w_scale * act_scale) * (dot as f32)   (bitlinear_sse2.rs:327-339),
+    // through LDS so that every token's outputs of a group leave as 256
+    // contiguous bytes (the MFMA layout gives each lane 4 rows of one token)
+    float *ot = reinterpret_cast<float *>(gl);  // [64 tokens][kOutStride]; the K loop ended on a barrier
+#pragma unroll
+    for (uint32_t s = 0; s < TPW; s++) {
+        const uint32_t tl = (s0 + s) * 16 + r16;
+        const wm_act_meta mt = a.meta[min(n0 + tl, a.m - 1)];
+        const float comb = G.scale * mt.scale;
+#pragma unroll
+        for (int rt = 0; rt < 4; rt++) {
+            float4 o;
+            o.x = comb * (float)(acc[rt][s].x - mt.asum);
+            o.y = comb * (float)(acc[rt][s].y - mt.asum);
+            o.z = comb * (float)(acc[rt][s].z - mt.asum);
+            o.w = comb * (float)(acc[rt][s].w - mt.asum);
+            *reinterpret_cast<float4 *>(ot + tl * kOutStride + q * 64 + rt * 16 + seg * 4) = o;
         }
     }
-    for (; c < a.n_chunks; c++) {
-        const uint32_t wv = *reinterpret_cast<const uint32_t *>(wp + (uint64_t)c * 1024);
-        v4i b[4];
+    __syncthreads();
+    // the 64 x 64 outputs of group g: 1024 float4, four per thread
 #pragma unroll
-        for (int s = 0; s < 4; s++) b[s] = *reinterpret_cast<const v4i *>(ap + c * cstride + s * 1024);
-        const v4i av = expand_codes(wv);
+    for (uint32_t g = 0; g < (uint32_t)NG; g++) {
+        const gemm_group Q = gemm_group_of(a, blockIdx.x * NG + g);
+        if (!Q.live) break;
+        const uint32_t base = Q.g * 64;
+        const bool vec = ((Q.row0 | a.ldy) & 3u) == 0;
 #pragma unroll
-        for (int s = 0; s < 4; s++)
-            acc[s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b[s], acc[s], 0, 0, 0);
-    }
-    // epilogue: y = (w_scale * act_scale) * (dot as f32)   (bitlinear_sse2.rs:327-339)
-    const uint32_t r_local = g * 64 + wave * 16 + seg * 4;
+        for (uint32_t k = 0; k < 4; k++) {
+            const uint32_t idx = tid + k * 256, tl = idx >> 4, c4 = (idx & 15) * 4;
+            const uint32_t t = n0 + tl;
+            if (t >= a.m) continue;
+            const float4 o = *reinterpret_cast<const float4 *>(ot + tl * kOutStride + g * 64 + c4);
+            float *dst = a.y + (uint64_t)t * a.ldy + Q.row0 + base + c4;
+            if (vec && base + c4 + 4 <= Q.out_dim) {
+                *reinterpret_cast<float4 *>(dst) = o;
+            } else {
+                const float ov[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-        const uint32_t t = n0 + s * 16 + r16;
-        if (t >= a.m) continue;
-        const wm_act_meta mt = a.meta[t];
-        const float comb = wscale * mt.scale;
-        float o[4];
-        o[0] = comb * (float)(acc[s].x - mt.asum);
-        o[1] = comb * (float)(acc[s].y - mt.asum);
-        o[2] = comb * (float)(acc[s].z - mt.asum);
-        o[3] = comb * (float)(acc[s].w - mt.asum);
-        float *dst = a.y + (uint64_t)t * a.ldy + row0 + r_local;
-        if (r_local + 4 <= out_dim && ((row0 | a.ldy) & 3u) == 0) {
-            *reinterpret_cast<float4 *>(dst) = make_float4(o[0], o[1], o[2], o[3]);
-        } else {
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                if (r_local + r < out_dim) dst[r] = o[r];
+                for (int r = 0; r < 4; r++)
+                    if (base + c4 + r < Q.out_dim) dst[r] = ov[r];
+            }
         }
     }
 }
@@ -167,73 +275,37 @@ __global__ __launch_bounds__(kRowThreads) void k_quantize_rows(const float *__re
 // ---------------------------------------------------------------------------
 // RMSNorm per row (primitives.rs:227-255), one workgroup per token
 // ---------------------------------------------------------------------------
+// The decode norms' building blocks (wm_norm.h): the exact Σx² by the
+// workgroup (seq_sum_block_owned), then y = x * rsqrt * w and the absmax
+// int8 quantiser, here into the GEMM activation layout.
 template <int PER, bool GU>
 __global__ __launch_bounds__(kRowThreads) void k_rmsnorm_rows(wm_norm_rows a) {
     extern __shared__ __align__(16) float sq[];  // x[j]^2, seq_sum_padded(n) entries
-    __shared__ float red_f[16];
-    __shared__ int red_i[16];
-    __shared__ float s_sum;
-    const uint32_t t = blockIdx.x, tid = threadIdx.x, n = a.n;
-    float xv[PER], wv[PER];
-    int nonfinite = 0;
+    __shared__ wm::norm_lds<kRowThreads / 64> nl;
+    const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, n = a.n;
+    float xv[PER], wv[PER], rv[PER];
+    bool nonfinite = false;
     if (GU) {
         // relu_square(gate) * up (ffn.rs:37-65)
         const float *g = a.gu + (uint64_t)t * a.ldgu;
-        float gv[PER], uv[PER];
 #pragma unroll
         for (int i = 0; i < PER; i++) {
             const uint32_t j = min(tid + (uint32_t)i * kRowThreads, n - 1);
-            gv[i] = g[j];
-            uv[i] = g[n + j];
+            xv[i] = g[j];
+            rv[i] = g[n + j];
             wv[i] = a.w[j];
         }
-#pragma unroll
-        for (int i = 0; i < PER; i++) {
-            const float r = gv[i] > 0.0f ? gv[i] : 0.0f;
-            xv[i] = (r * r) * uv[i];
-        }
+        wm::norm_prep<PER, kRowThreads>(true, n, nullptr, sq, xv, wv, rv, true);
     } else {
         float *xr = a.x + (uint64_t)t * a.ldx;
-        float rv[PER];
-#pragma unroll
-        for (int i = 0; i < PER; i++) {
-            const uint32_t j = min(tid + (uint32_t)i * kRowThreads, n - 1);
-            xv[i] = xr[j];
-            wv[i] = a.w[j];
-            rv[i] = a.res ? a.res[(uint64_t)t * a.ldr + j] : 0.0f;
-        }
-        if (a.res) {
-            // hidden += BitLinear output (cached_forward.rs:405-408, :496-500)
-#pragma unroll
-            for (int i = 0; i < PER; i++) {
-                const uint32_t j = tid + (uint32_t)i * kRowThreads;
-                const float v = xv[i] + rv[i];
-                xv[i] = v;
-                if (j < n) {
-                    xr[j] = v;
-                    nonfinite |= !isfinite(v);
-                }
-            }
-        }
+        wm::norm_load<PER, kRowThreads>(xr, a.res ? a.res + (uint64_t)t * a.ldr : nullptr, a.w, n,
+                                        xv, wv, rv);
+        // hidden += BitLinear output (cached_forward.rs:405-408, :496-500)
+        nonfinite = wm::norm_prep<PER, kRowThreads>(a.res != nullptr, n, a.res ? xr : nullptr, sq,
+                                                    xv, wv, rv);
     }
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-        const uint32_t j = tid + (uint32_t)i * kRowThreads;
-        if (j < n) sq[j] = xv[i] * xv[i];
-        else xv[i] = 0.0f;
-    }
-    if (a.err_flag) {
-        const int any = wm_block_sum_i32(nonfinite, red_i);
-        if (any && tid == 0 && *a.err_flag == 0) *a.err_flag = a.tag;
-    }
-    __syncthreads();
-    if (tid < 64) {
-        const float s = wm::seq_sum_nonneg(sq, n);
-        if (tid == 0) s_sum = s;
-    }
-    __syncthreads();
-    const float mean = s_sum / (float)n;
-    const float rs = 1.0f / sqrtf(mean + a.eps);
+    const float rs = wm::norm_sum_rsqrt<PER, kRowThreads>(nonfinite, n, a.eps, a.err_flag, a.tag,
+                                                          sq, nl);
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
@@ -245,22 +317,32 @@ __global__ __launch_bounds__(kRowThreads) void k_rmsnorm_rows(wm_norm_rows a) {
         }
     }
     if (!a.act) return;
-    const float max_abs = wm_block_max_nonan(m, red_f);
+    m = wm_wave_max_nonneg(m);
+    if (lane == 0) nl.red_f[wid] = m;
+    wm_sync_lds();
+    float max_abs = nl.red_f[0];
+#pragma unroll
+    for (int i = 1; i < kRowThreads / 64; i++) max_abs = wm_max_nonan(max_abs, nl.red_f[i]);
     const float inv = 127.0f / max_abs;
     int sum = 0;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
         const uint32_t j = tid + (uint32_t)i * kRowThreads;
         if (j < n) {
-            const int q = max_abs == 0.0f ? 0 : wm_round_clamp_i8(xv[i] * inv);
+            const int q = max_abs == 0.0f ? 0 : wm_round_clamp_i8_fast(xv[i] * inv);
             a.act[wm_gemm_act_offset(j, t, a.m_pad)] = (uint8_t)(int8_t)q;
             sum += q;
         }
     }
-    sum = wm_block_sum_i32(sum, red_i);
+    sum = wm_wave_total_i32(sum);
+    if (lane == 0) nl.red_i[wid] = sum;
+    wm_sync_lds();
     if (tid == 0) {
+        int tot = 0;
+#pragma unroll
+        for (int i = 0; i < kRowThreads / 64; i++) tot += nl.red_i[i];
         a.meta[t].scale = max_abs == 0.0f ? 1.0f : max_abs / 127.0f;
-        a.meta[t].asum = sum;
+        a.meta[t].asum = tot;
     }
 }
 
@@ -368,94 +450,148 @@ __global__ __launch_bounds__(kScoreThreads) void k_attn_scores_rows(attn_rows_ar
     for (int h = 0; h < G; h++) dst[(uint64_t)h * a.score_stride] = s[h] * a.scale;
 }
 
-constexpr int kVTile = 64;  // V rows per LDS tile
+// out[t][h][d] = Σ_p w_h[p] * v_p[d] in position order (cached_forward.rs:
+// 417-449; v_p[d] = q8 * scale, read_into) for one token and G query heads
+// of one KV head, on the softmax weights k_attn_softmax_rows left in place
+// of the scores.  Thread d runs the G chains: the rows share every V value,
+// and G independent chains per thread keep the adder busy.  Tiles of kSvPos
+// positions go through LDS: V (the next tile's loads in flight while the
+// current one is summed) and the rows' weights.
+constexpr uint32_t kSvPos = 64;
+constexpr uint32_t kSvHeads = 4;  // query heads per workgroup (of one KV head's group)
 
+// The loads of V tile rows p0 .. p0 + kSvPos - 1 (indices clamped to n - 1):
+// thread tid takes 16-byte pieces tid, tid + HD, tid + 2HD, tid + 3HD
+// (piece = row * HD/16 + column), in named registers (an array would be kept
+// in scratch memory), threads below kSvPos one scale each.
+struct sv_regs {
+    int4 v0, v1, v2, v3;
+    float s;
+};
 template <int HD>
-__global__ __launch_bounds__(HD) void k_attn_softmax_v_rows(attn_rows_args a) {
-    // LDS: weights [seq_sum_padded(n_max)] | V tile [kVTile][HD] bytes | V scales [kVTile]
-    extern __shared__ __align__(16) float wts[];
+__device__ __forceinline__ void sv_fetch(sv_regs &r, const int8_t *vg, const float *vsg, uint32_t kv_dim,
+                                         uint32_t p0, uint32_t n) {
+    static_assert(kSvPos * HD / 16 == 4 * HD, "four pieces per thread");
+    const uint32_t tid = threadIdx.x;
+    const auto piece = [&](uint32_t i) {
+        const uint32_t pc = i * HD + tid, row = pc / (HD / 16), col = (pc % (HD / 16)) * 16;
+        return *reinterpret_cast<const int4 *>(vg + (uint64_t)min(p0 + row, n - 1) * kv_dim + col);
+    };
+    r.v0 = piece(0);
+    r.v1 = piece(1);
+    r.v2 = piece(2);
+    r.v3 = piece(3);
+    if (tid < kSvPos) r.s = vsg[min(p0 + tid, n - 1)];
+}
+template <int HD>
+__device__ __forceinline__ void sv_stage(const sv_regs &r, int8_t *vt, float *vst) {
+    const uint32_t tid = threadIdx.x;
+    *reinterpret_cast<int4 *>(vt + tid * 16) = r.v0;
+    *reinterpret_cast<int4 *>(vt + (HD + tid) * 16) = r.v1;
+    *reinterpret_cast<int4 *>(vt + (2 * HD + tid) * 16) = r.v2;
+    *reinterpret_cast<int4 *>(vt + (3 * HD + tid) * 16) = r.v3;
+    if (tid < kSvPos) vst[tid] = r.s;
+}
+
+// Softmax of one (token, head) row of scores in place (attention.rs:45-73):
+// max, exp (glibc expf), the exact sequential sum by the workgroup (thread t
+// owning the m = ceil(n / 256) consecutive terms from t*m), * (1/sum) (left
+// unnormalised when the sum is not positive); a row whose maximum is not
+// finite becomes all zero (its output is then 0).
+constexpr uint32_t kSmThreads = 256;
+__global__ __launch_bounds__(kSmThreads) void k_attn_softmax_rows(attn_rows_args a) {
+    constexpr int M = 16;  // terms per thread: n <= 4096
     __shared__ uint64_t exp_tab[32];
-    __shared__ float red[2];
-    __shared__ float s_inv;
-    __shared__ int s_mode;
-    const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-    const uint32_t group = a.n_heads / (a.kv_dim / HD), kvh = h / group;
-    const wm_batch_tok tk = a.tok[t];
-    const uint32_t n = tk.pos + 1;
-    int8_t *vt = reinterpret_cast<int8_t *>(wts + wm::seq_sum_padded(a.n_max));
-    float *st = reinterpret_cast<float *>(vt + kVTile * HD);
-    const float *sc = a.scores + ((uint64_t)t * a.n_heads + h) * a.score_stride;
+    __shared__ float red[kSmThreads / 64];
+    __shared__ wm::seq_block_scratch seq_scratch;
+    const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const uint32_t n = a.tok[t].pos + 1;
+    float *w = a.scores + ((uint64_t)t * a.n_heads + h) * a.score_stride;
     if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
+    const uint32_t mm = (n + kSmThreads - 1) / kSmThreads, k0 = tid * mm;
+    float v[M];
     float m = -INFINITY;
-    for (uint32_t p = tid; p < n; p += HD) {
-        const float v = sc[p];
-        wts[p] = v;
-        m = wm_max_nonan(m, v);
+#pragma unroll
+    for (int j = 0; j < M; j++) {
+        v[j] = ((uint32_t)j < mm && k0 + j < n) ? w[k0 + j] : -INFINITY;
+        m = wm_max_nonan(m, v[j]);
     }
     m = wm_wave_max_nonan(m);
-    if ((tid & 63) == 0) red[tid >> 6] = m;
+    if (lane == 0) red[wid] = m;
     __syncthreads();
-    const float mx = HD > 64 ? wm_max_nonan(red[0], red[1]) : red[0];
-    float *out = a.out + (uint64_t)t * a.n_heads * HD + (uint64_t)h * HD;
-    if (!isfinite(mx)) {  // every weight is 0 or NaN: the output stays 0
-        out[tid] = 0.0f;
+    float mx = red[0];
+#pragma unroll
+    for (uint32_t i = 1; i < kSmThreads / 64; i++) mx = wm_max_nonan(mx, red[i]);
+    if (!isfinite(mx)) {  // every weight becomes 0 (or the row held a NaN)
+#pragma unroll
+        for (int j = 0; j < M; j++)
+            if ((uint32_t)j < mm && k0 + j < n) w[k0 + j] = 0.0f;
         return;
     }
-    for (uint32_t p = tid; p < n; p += HD) wts[p] = wm::expf_glibc(wts[p] - mx, exp_tab);
-    __syncthreads();
-    if (tid < 64) {
-        const float sum = wm::seq_sum_nonneg(wts, n);
-        if (tid == 0) {
-            s_mode = sum > 0.0f;
-            s_inv = 1.0f / sum;
-        }
+#pragma unroll
+    for (int j = 0; j < M; j++) {
+        const bool in = (uint32_t)j < mm && k0 + j < n;
+        v[j] = in ? wm::expf_glibc(v[j] - mx, exp_tab) : 0.0f;
+        if (in) w[k0 + j] = v[j];
     }
-    __syncthreads();
-    if (s_mode) {
-        const float inv = s_inv;
-        for (uint32_t p = tid; p < n; p += HD) wts[p] = wts[p] * inv;
+    __syncthreads();  // the exps in memory for the sum's walk
+    const float sum = wm::seq_sum_block_owned<M, kSmThreads>(v, n, w, &seq_scratch);
+    if (sum > 0.0f) {
+        const float inv = 1.0f / sum;
+#pragma unroll
+        for (int j = 0; j < M; j++)
+            if ((uint32_t)j < mm && k0 + j < n) w[k0 + j] = v[j] * inv;
     }
-    // V rows of this KV head go through LDS a tile at a time: every thread
-    // loads 16-byte pieces (all in flight together, the next tile's while the
-    // current one is consumed), then thread d runs its chain from LDS.
+}
+
+// G: query heads per workgroup, HG: per KV head (blockIdx.x = kv head * HG/G + part)
+template <int HD, int G, int HG>
+__global__ __launch_bounds__(HD) void k_attn_sv_rows(attn_rows_args a) {
+    __shared__ __align__(16) int8_t vt[kSvPos * HD];
+    __shared__ __align__(16) float vst[kSvPos];
+    __shared__ __align__(16) float wt[G][kSvPos];
+    const uint32_t kvh = blockIdx.x / (HG / G), h0 = blockIdx.x * G;  // first query head
+    const uint32_t t = blockIdx.y, tid = threadIdx.x;
+    const wm_batch_tok tk = a.tok[t];
+    const uint32_t n = tk.pos + 1;
+    float *rows = a.scores + ((uint64_t)t * a.n_heads + h0) * a.score_stride;  // row g at g * stride
+    // the chains, a tile at a time
     const uint64_t lay = (uint64_t)a.layer * tk.max_seq;
     const int8_t *vg = tk.v + lay * a.kv_dim + kvh * HD;
     const float *vsg = tk.vs + lay;
-    // Tile rows p0 .. p0+63, indices clamped to n-1 so every load is in range
-    // and unconditional: thread tid takes 16-byte pieces tid, tid+HD, tid+2HD,
-    // tid+3HD (piece = row * HD/16 + column) and threads < 64 one scale each.
-    constexpr uint32_t kPR = HD / 16;  // pieces per row
-    const uint32_t r0 = tid / kPR, c0 = (tid % kPR) * 16, rstep = HD / kPR;
-    int4 pre0, pre1, pre2, pre3;
-    float spre = 0.0f;
-#define WM_FETCH_V(P0)                                                                       \
-    do {                                                                                     \
-        const uint32_t q0 = (P0) + r0;                                                       \
-        pre0 = *reinterpret_cast<const int4 *>(vg + (uint64_t)min(q0, n - 1) * a.kv_dim + c0); \
-        pre1 = *reinterpret_cast<const int4 *>(vg + (uint64_t)min(q0 + rstep, n - 1) * a.kv_dim + c0); \
-        pre2 = *reinterpret_cast<const int4 *>(vg + (uint64_t)min(q0 + 2 * rstep, n - 1) * a.kv_dim + c0); \
-        pre3 = *reinterpret_cast<const int4 *>(vg + (uint64_t)min(q0 + 3 * rstep, n - 1) * a.kv_dim + c0); \
-        if (tid < (uint32_t)kVTile) spre = vsg[min((P0) + tid, n - 1)];                       \
-    } while (0)
-    WM_FETCH_V(0u);
-    float acc = 0.0f;
-    for (uint32_t p0 = 0; p0 < n; p0 += kVTile) {
-        __syncthreads();  // previous tile consumed (and, first time, the weights written)
-        int4 *vt4 = reinterpret_cast<int4 *>(vt);
-        vt4[tid] = pre0;
-        vt4[tid + HD] = pre1;
-        vt4[tid + 2 * HD] = pre2;
-        vt4[tid + 3 * HD] = pre3;
-        if (tid < (uint32_t)kVTile) st[tid] = spre;
+    sv_regs pr{};
+    sv_fetch<HD>(pr, vg, vsg, a.kv_dim, 0u, n);
+    float acc[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) acc[g] = 0.0f;
+    for (uint32_t p0 = 0; p0 < n; p0 += kSvPos) {
+        __syncthreads();  // the previous tile is summed
+        sv_stage<HD>(pr, vt, vst);
+        for (uint32_t e = tid; e < G * kSvPos; e += HD) {
+            const uint32_t g = e / kSvPos, q = e % kSvPos;
+            wt[g][q] = p0 + q < n ? rows[(uint64_t)g * a.score_stride + p0 + q] : 0.0f;
+        }
         __syncthreads();
-        WM_FETCH_V(p0 + kVTile);  // next tile; past the end the clamped rows re-read row n-1
-        const uint32_t tn = n - p0 < (uint32_t)kVTile ? n - p0 : (uint32_t)kVTile;
-        const float *wp = wts + p0;
-        for (uint32_t q = 0; q < tn; q++)
-            acc = acc + wp[q] * ((float)vt[q * HD + tid] * st[q]);  // w * (q8 * scale)
+        if (p0 + kSvPos < n) sv_fetch<HD>(pr, vg, vsg, a.kv_dim, p0 + kSvPos, n);
+        const uint32_t tn = min(kSvPos, n - p0);
+        if (tn == kSvPos) {
+#pragma unroll 4
+            for (uint32_t q = 0; q < kSvPos; q++) {
+                const float vd = (float)vt[q * HD + tid] * vst[q];  // read_into: q8 * scale
+#pragma unroll
+                for (int g = 0; g < G; g++) acc[g] = acc[g] + wt[g][q] * vd;
+            }
+        } else {
+            for (uint32_t q = 0; q < tn; q++) {
+                const float vd = (float)vt[q * HD + tid] * vst[q];
+#pragma unroll
+                for (int g = 0; g < G; g++) acc[g] = acc[g] + wt[g][q] * vd;
+            }
+        }
     }
-    out[tid] = acc;
-#undef WM_FETCH_V
+    float *out = a.out + (uint64_t)t * a.n_heads * HD + (uint64_t)h0 * HD + tid;
+#pragma unroll
+    for (int g = 0; g < G; g++) out[g * HD] = acc[g];
 }
 
 }  // namespace
@@ -475,6 +611,7 @@ void wm_launch_i2s_gemm(const wm_gemm_desc *d, int n_desc, uint32_t n_chunks, co
         a.group_end[i] = groups;
     }
     a.n_desc = n_desc;
+    a.n_groups = groups;
     a.n_chunks = n_chunks;
     a.act = act;
     a.m = m;
@@ -483,7 +620,16 @@ void wm_launch_i2s_gemm(const wm_gemm_desc *d, int n_desc, uint32_t n_chunks, co
     a.y = y;
     a.ldy = ldy;
     const uint32_t tiles = (m + WM_GEMM_TILE_TOKENS - 1) / WM_GEMM_TILE_TOKENS;
-    hipLaunchKernelGGL(k_i2s_gemm, dim3(groups, tiles), dim3(256), 0, s, a);
+    // groups per workgroup: four (each activation byte read from L2 once per
+    // four groups) when that still gives the chip about one workgroup per
+    // CU, else fewer, for more workgroups
+    const uint32_t cus = 256;
+    if ((groups + 3) / 4 * tiles >= cus)
+        hipLaunchKernelGGL(k_i2s_gemm<4>, dim3((groups + 3) / 4, tiles), dim3(256), gemm_lds_bytes<4>(), s, a);
+    else if ((groups + 1) / 2 * tiles >= cus / 2)
+        hipLaunchKernelGGL(k_i2s_gemm<2>, dim3((groups + 1) / 2, tiles), dim3(256), gemm_lds_bytes<2>(), s, a);
+    else
+        hipLaunchKernelGGL(k_i2s_gemm<1>, dim3(groups, tiles), dim3(256), gemm_lds_bytes<1>(), s, a);
 }
 
 void wm_launch_quantize_rows(const float *x, uint32_t ldx, uint32_t n, uint32_t m, uint32_t m_pad,
@@ -541,10 +687,12 @@ void wm_launch_attn_rows(const float *q, const wm_batch_tok *tok, uint32_t m, ui
     WM_SCORES_CASE(128, 1) WM_SCORES_CASE(128, 2) WM_SCORES_CASE(128, 4) WM_SCORES_CASE(128, 8)
     WM_SCORES_CASE(64, 1) WM_SCORES_CASE(64, 2) WM_SCORES_CASE(64, 4) WM_SCORES_CASE(64, 8)
 #undef WM_SCORES_CASE
-    const size_t lds = (size_t)wm::seq_sum_padded(n_max) * sizeof(float) +
-                       (size_t)kVTile * head_dim + kVTile * sizeof(float);
-    if (head_dim == 128)
-        hipLaunchKernelGGL(k_attn_softmax_v_rows<128>, dim3(n_heads, m), dim3(128), lds, s, a);
-    else
-        hipLaunchKernelGGL(k_attn_softmax_v_rows<64>, dim3(n_heads, m), dim3(64), lds, s, a);
+    hipLaunchKernelGGL(k_attn_softmax_rows, dim3(n_heads, m), dim3(kSmThreads), 0, s, a);
+#define WM_SV_CASE(HD, G)                                                                      \
+    if (head_dim == HD && group == G)                                                          \
+        hipLaunchKernelGGL((k_attn_sv_rows<HD, (G < kSvHeads ? G : kSvHeads), G>),             \
+                           dim3(n_kv_heads * (G < kSvHeads ? 1 : G / kSvHeads), m), dim3(HD), 0, s, a);
+    WM_SV_CASE(128, 1) WM_SV_CASE(128, 2) WM_SV_CASE(128, 4) WM_SV_CASE(128, 8)
+    WM_SV_CASE(64, 1) WM_SV_CASE(64, 2) WM_SV_CASE(64, 4) WM_SV_CASE(64, 8)
+#undef WM_SV_CASE
 }
