@@ -335,6 +335,25 @@ def probe(kind: str, reps: int):
         def launch():
             _, _, st["tok"] = dkv.decode_step(st["tok"], st["pos"], want_logits=False)
             st["pos"] += 1
+    elif kind == "batch":  # the ragged continuous-batching step (16 sequences)
+        hm = bs.make_host_model(cfg, bs.master_seed(4))
+        dev = bs.load_device_model(ctx, hm)
+        del hm
+        wl = bs.ragged_workload(cfg)
+        kvs = []
+        for i, c in enumerate(wl.contexts):
+            kv = dev.kv_cache(cfg.context_length)
+            k, v = bs.kv_prefill(cfg, wl.prefill_seeds[i], c)
+            kv.append_positions(k, v)
+            kvs.append(kv)
+        del k, v
+        held += kvs + [dev]
+        seqs = [list(t) for t in wl.new_tokens]
+
+        def launch():
+            dev.batch_forward(kvs, seqs, want_hidden=False, want_next=True)
+            for kv, c in zip(kvs, wl.contexts):
+                kv.rollback(c)
     elif kind == "i2s":
         copies = 320
         seed = 0x5749_4C4C_0000_0001
@@ -397,7 +416,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batch", action="store_true", help="skip the ragged-batch measurement")
     ap.add_argument("--batch-steps", type=int, default=5)
-    ap.add_argument("--probe", choices=["lm_head", "lm_head_exact", "i2s", "decode"],
+    ap.add_argument("--probe", choices=["lm_head", "lm_head_exact", "i2s", "decode", "batch"],
                     help="only run one kernel (and a calibration copy) for counter passes")
     ap.add_argument("--probe-reps", type=int, default=5)
     args = ap.parse_args()

@@ -119,6 +119,17 @@ wm_status wm_bitlinear_i2s_matvec_f32(wm_ctx *ctx, const wm_tensor *w, const flo
 wm_status wm_bitlinear_i2s_matvec_f32_debug(wm_ctx *ctx, const wm_tensor *w, const float *input,
                                             size_t input_len, float *output, size_t output_len,
                                             int8_t *act, float *act_scale, int32_t *acc);
+/* The scalar f32 path: no int8 activations; per row, f32 sums of the
+ * inputs under +1 and under -1 codes in the packed byte order, then
+ * out = scale * (pos - neg).  Replaces bitlinear_i2s_matvec_f32_scalar
+ * (src/model/bitlinear.rs:146-233), the dispatcher's fallback arm
+ * (src/model/bitlinear.rs:140); bit-identical to it, NaN/inf inputs
+ * included (a NaN under a 0 code is skipped, as there). */
+wm_status wm_bitlinear_i2s_matvec_f32_scalar(wm_ctx *ctx, const wm_tensor *w, const float *input,
+                                             size_t input_len, float *output, size_t output_len);
+/* Device-pointer form of the scalar path (one launch, no workspace). */
+wm_status wm_bitlinear_i2s_matvec_f32_scalar_dev(wm_ctx *ctx, const wm_tensor *w,
+                                                 const float *d_input, float *d_output);
 /* Device-pointer form: d_input[in_dim] f32 -> d_output[out_dim] f32. */
 wm_status wm_bitlinear_i2s_matvec_f32_dev(wm_ctx *ctx, const wm_tensor *w, const float *d_input,
                                           float *d_output);
@@ -284,6 +295,58 @@ wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *promp
 wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_seqs,
                            const uint32_t *n_new, const uint32_t *tokens, float *last_hidden,
                            uint32_t *next_tokens);
+
+/* Batched prefill: `tokens` appended to `kv` at its current position through
+ * the ragged-batch kernels (chunks of up to 512 tokens), bit-identical to
+ * the token-by-token prefill of src/model/generate.rs:151-160.  On an
+ * error the cache is left at its starting position.
+ * last_hidden (n_embd, host, nullable): the last token after output_norm. */
+wm_status wm_prefill(wm_model *m, wm_kv_cache *kv, const uint32_t *tokens, uint32_t n,
+                     float *last_hidden);
+
+/* ---- sampler (src/model/sampler.rs) ---------------------------------- */
+
+/* SamplingParams (src/model/sampler.rs:40-79); the Option fields carry a
+ * has_* flag. */
+typedef struct wm_sampling_params {
+    float temperature;                /* |t| < 1e-9 and no other knob: greedy */
+    uint32_t has_top_k;
+    uint64_t top_k;
+    float top_p;
+    uint32_t has_top_p;
+    float repetition_penalty;
+    uint32_t has_repetition_penalty;
+} wm_sampling_params;
+typedef struct wm_sampler wm_sampler;
+/* Sampler::new (src/model/sampler.rs:94-101): xorshift64 seeded with `seed`
+ * (0 -> 0xdeadbeefcafebabe, :18-25), empty history. */
+wm_status wm_sampler_create(wm_ctx *ctx, const wm_sampling_params *params, uint64_t seed,
+                            wm_sampler **out);
+void wm_sampler_destroy(wm_sampler *s);
+/* Sampler::observe (:105-107) */
+wm_status wm_sampler_observe(wm_sampler *s, uint32_t id);
+/* Sampler::checkpoint / rollback (:109-120) */
+wm_status wm_sampler_checkpoint(const wm_sampler *s, uint64_t *rng_state, uint64_t *history_len);
+wm_status wm_sampler_rollback(wm_sampler *s, uint64_t rng_state, uint64_t history_len);
+/* Sampler::sample (:133-149): repetition penalty, temperature, top-k,
+ * softmax, top-p and the multinomial draw (:178-196) on the device,
+ * bit-identical to the reference (greedy: argmax, lm_head.rs:161-174).
+ * Probabilities equal at the top-p cut are taken in index order (the
+ * reference's unstable sort leaves it open), and NaN probabilities under
+ * top-p with 0 < p < 1 are WM_E_NONFINITE (order unspecified there).  The
+ * multinomial error (total not positive and finite) is WM_E_PARSE with the
+ * reference's message; the xorshift state advances only when the draw runs.
+ * _dev: logits on the device. */
+wm_status wm_sampler_sample(wm_sampler *s, const float *logits, size_t n, uint32_t *out_id);
+wm_status wm_sampler_sample_dev(wm_sampler *s, const float *d_logits, size_t n, uint32_t *out_id);
+/* generate_with_cache_and_sampler (src/model/generate.rs:195-277) on an
+ * existing cache: observe the prompt, prefill it (batched), then up to
+ * max_new sampled tokens (logits and sampling on the device), stopping at
+ * `eos` (< 0: none) or any of stop_ids; each accepted id is observed. */
+wm_status wm_generate_with_sampler(wm_model *m, wm_kv_cache *kv, const uint32_t *prompt,
+                                   uint32_t n_prompt, uint32_t max_new, int64_t eos,
+                                   const uint32_t *stop_ids, uint32_t n_stop, wm_sampler *s,
+                                   uint32_t *out_ids, uint32_t *n_out);
 
 /* ---- GGUF files (src/gguf/reader.rs, src/model/graph.rs) ------------- */
 

@@ -71,6 +71,15 @@ _SIGS = {
     "or_forward_single_token_position_zero": (C.c_int, _vp, C.c_uint32, _f32p, _f32p),
     "or_greedy_generate": (C.c_int, _vp, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_int64, _u32p,
                            _u32p, _f32p),
+    "or_xorshift64_seed": (C.c_uint64, C.c_uint64),
+    "or_xorshift64_next": (C.c_uint64, C.POINTER(C.c_uint64)),
+    "or_xorshift64_next_unit": (C.c_float, C.POINTER(C.c_uint64)),
+    "or_apply_repetition_penalty": (None, _f32p, _sz, _u32p, _sz, C.c_float),
+    "or_apply_temperature": (None, _f32p, _sz, C.c_float),
+    "or_apply_top_k": (None, _f32p, _sz, C.c_uint64),
+    "or_softmax_to_probs": (None, _f32p, _sz, _f32p),
+    "or_apply_top_p": (None, _f32p, _sz, C.c_float),
+    "or_sample": (C.c_int, _vp, C.POINTER(C.c_uint64), _u32p, _sz, _f32p, _sz, _u32p, _f32p),
 }
 for _n, (_r, *_a) in _SIGS.items():
     _f = getattr(lib, _n)
@@ -209,3 +218,74 @@ def kv_quantise(x):
     q = np.empty(x.size, dtype=np.int8)
     s = lib.or_kv_quantise(P(x, C.c_float), x.size, P(q, C.c_int8))
     return q, np.float32(s)
+
+
+# ---- sampler (src/model/sampler.rs) --------------------------------------
+
+class SamplingParams(C.Structure):
+    """SamplingParams (sampler.rs:40-79) with the Option fields as flags;
+    the same layout as the library's wm_sampling_params."""
+    _fields_ = [("temperature", C.c_float), ("has_top_k", C.c_uint32), ("top_k", C.c_uint64),
+                ("top_p", C.c_float), ("has_top_p", C.c_uint32),
+                ("repetition_penalty", C.c_float), ("has_repetition_penalty", C.c_uint32)]
+
+    @classmethod
+    def make(cls, temperature=0.0, top_k=None, top_p=None, repetition_penalty=None):
+        return cls(temperature, top_k is not None, top_k or 0, 0.0 if top_p is None else top_p,
+                   top_p is not None, 0.0 if repetition_penalty is None else repetition_penalty,
+                   repetition_penalty is not None)
+
+
+class Sampler:
+    """Sampler (sampler.rs:81-149) over the oracle's restatement."""
+
+    def __init__(self, params: SamplingParams, seed: int):
+        self.params = params
+        self.state = C.c_uint64(lib.or_xorshift64_seed(seed))
+        self.history: list[int] = []
+
+    def observe(self, tok: int):
+        self.history.append(int(tok))
+
+    def checkpoint(self):
+        return self.state.value, len(self.history)
+
+    def rollback(self, cp):
+        self.state.value, n = cp
+        del self.history[n:]
+
+    def sample(self, logits):
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        hist = np.ascontiguousarray(self.history, dtype=np.uint32)
+        out, total = C.c_uint32(), C.c_float()
+        rc = lib.or_sample(C.byref(self.params), C.byref(self.state), P(hist, C.c_uint32), hist.size,
+                           P(logits, C.c_float), logits.size, C.byref(out), C.byref(total))
+        if rc:
+            raise ValueError(f"oracle sample failed rc={rc} total={total.value}")
+        return int(out.value)
+
+
+def apply_top_k(logits, k):
+    x = np.array(logits, dtype=np.float32)
+    lib.or_apply_top_k(P(x, C.c_float), x.size, k)
+    return x
+
+
+def apply_top_p(probs, p):
+    x = np.array(probs, dtype=np.float32)
+    lib.or_apply_top_p(P(x, C.c_float), x.size, p)
+    return x
+
+
+def softmax_to_probs(logits):
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    out = np.empty_like(x)
+    lib.or_softmax_to_probs(P(x, C.c_float), x.size, P(out, C.c_float))
+    return out
+
+
+def apply_repetition_penalty(logits, history, r):
+    x = np.array(logits, dtype=np.float32)
+    h = np.ascontiguousarray(history, dtype=np.uint32)
+    lib.or_apply_repetition_penalty(P(x, C.c_float), x.size, P(h, C.c_uint32), h.size, r)
+    return x

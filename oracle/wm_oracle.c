@@ -793,3 +793,201 @@ int or_greedy_generate(or_model *m, or_kv *kv, const uint32_t *prompt, uint32_t 
     free(logits);
     return rc;
 }
+
+/* ------------------------------------------------------------------------ */
+/* sampler (src/model/sampler.rs)                                           */
+/* ------------------------------------------------------------------------ */
+
+/* XorShift64::new (sampler.rs:18-25) */
+uint64_t or_xorshift64_seed(uint64_t seed) { return seed ? seed : 0xdeadbeefcafebabeull; }
+
+/* XorShift64::next_u64 (sampler.rs:26-33): shifts 13, 7, 17 */
+uint64_t or_xorshift64_next(uint64_t *state) {
+    uint64_t x = *state;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *state = x;
+    return x;
+}
+
+/* XorShift64::next_unit (sampler.rs:34-37): high 24 bits / 2^24 */
+float or_xorshift64_next_unit(uint64_t *state) {
+    return (float)(or_xorshift64_next(state) >> 40) / (float)(1ull << 24);
+}
+
+/* SamplingParams::is_greedy (sampler.rs:71-78) */
+int or_sampling_is_greedy(const or_sampling_params *p) {
+    return fabsf(p->temperature) < 1e-9f && !p->has_top_k && !p->has_top_p &&
+           !p->has_repetition_penalty;
+}
+
+/* Sampler::apply_repetition_penalty (sampler.rs:151-164): each distinct
+ * history id below n once, in history order. */
+void or_apply_repetition_penalty(float *logits, size_t n, const uint32_t *history,
+                                 size_t n_history, float r) {
+    if (r <= 0.0f || fabsf(r - 1.0f) < 1e-9f) return;
+    for (size_t h = 0; h < n_history; h++) {
+        uint32_t id = history[h];
+        if (id >= n) continue;
+        int seen = 0;
+        for (size_t j = 0; j < h && !seen; j++) seen = history[j] == id;
+        if (seen) continue;
+        float l = logits[id];
+        logits[id] = l > 0.0f ? l / r : l * r;
+    }
+}
+
+/* Sampler::apply_temperature (sampler.rs:166-176) */
+void or_apply_temperature(float *logits, size_t n, float t) {
+    if (t <= 0.0f || fabsf(t - 1.0f) < 1e-9f) return;
+    float inv = 1.0f / t;
+    for (size_t i = 0; i < n; i++) logits[i] *= inv;
+}
+
+static int desc_float(const void *a, const void *b) {
+    float x = *(const float *)a, y = *(const float *)b;
+    if (isnan(x) || isnan(y)) return isnan(x) - isnan(y); /* NaN last (order open in the reference) */
+    return (x < y) - (x > y);
+}
+
+/* apply_top_k (sampler.rs:201-223): the k-th largest value is the
+ * threshold; everything strictly below it becomes -inf. */
+void or_apply_top_k(float *logits, size_t n, uint64_t k) {
+    if (k > n) k = n;
+    if (k == 0) {
+        for (size_t i = 0; i < n; i++) logits[i] = -INFINITY;
+        return;
+    }
+    if (k == n) return;
+    float *v = (float *)malloc(n * sizeof(float));
+    memcpy(v, logits, n * sizeof(float));
+    qsort(v, n, sizeof(float), desc_float);
+    float thr = v[k - 1];
+    free(v);
+    for (size_t i = 0; i < n; i++)
+        if (logits[i] < thr) logits[i] = -INFINITY;
+}
+
+/* softmax_to_probs (sampler.rs:225-252) */
+void or_softmax_to_probs(const float *logits, size_t n, float *out) {
+    if (!n) return;
+    float max = -INFINITY;
+    for (size_t i = 0; i < n; i++)
+        if (logits[i] > max) max = logits[i];
+    if (!isfinite(max)) {
+        for (size_t i = 0; i < n; i++) out[i] = 0.0f;
+        return;
+    }
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        float e = expf(logits[i] - max);
+        sum += e;
+        out[i] = e;
+    }
+    if (sum > 0.0f) {
+        float inv = 1.0f / sum;
+        for (size_t i = 0; i < n; i++) out[i] *= inv;
+    }
+}
+
+typedef struct { float v; uint32_t i; } prob_idx;
+static int desc_prob(const void *a, const void *b) {
+    const prob_idx *x = (const prob_idx *)a, *y = (const prob_idx *)b;
+    if (x->v != y->v) return x->v < y->v ? 1 : -1;
+    return (x->i > y->i) - (x->i < y->i);
+}
+
+/* apply_top_p (sampler.rs:254-311); equal probabilities in index order. */
+void or_apply_top_p(float *probs, size_t n, float p) {
+    if (!n) return;
+    if (p <= 0.0f) {
+        size_t am = 0;
+        float av = probs[0];
+        for (size_t i = 1; i < n; i++)
+            if (probs[i] > av) {
+                av = probs[i];
+                am = i;
+            }
+        for (size_t i = 0; i < n; i++) probs[i] = i == am ? 1.0f : 0.0f;
+        return;
+    }
+    if (p >= 1.0f) return;
+    prob_idx *o = (prob_idx *)malloc(n * sizeof(prob_idx));
+    unsigned char *keep = (unsigned char *)calloc(n, 1);
+    for (size_t i = 0; i < n; i++) {
+        o[i].v = probs[i];
+        o[i].i = (uint32_t)i;
+    }
+    qsort(o, n, sizeof(prob_idx), desc_prob);
+    float acc = 0.0f;
+    for (size_t s = 0; s < n; s++) {
+        acc += o[s].v;
+        keep[o[s].i] = 1;
+        if (acc >= p) break;
+    }
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        if (!keep[i]) probs[i] = 0.0f;
+        sum += probs[i];
+    }
+    if (sum > 0.0f) {
+        float inv = 1.0f / sum;
+        for (size_t i = 0; i < n; i++) probs[i] *= inv;
+    }
+    free(o);
+    free(keep);
+}
+
+/* Sampler::sample (sampler.rs:133-149) + multinomial (:178-196) */
+int or_sample(const or_sampling_params *p, uint64_t *state, const uint32_t *history,
+              size_t n_history, const float *logits, size_t n, uint32_t *out, float *total_out) {
+    if (or_sampling_is_greedy(p)) {
+        int64_t a = or_argmax(logits, n);
+        if (a < 0) return -1;
+        *out = (uint32_t)a;
+        return 0;
+    }
+    if (!n) { /* multinomial over no probabilities: total 0 */
+        if (total_out) *total_out = 0.0f;
+        return -2;
+    }
+    float *buf = (float *)malloc(n * sizeof(float));
+    float *probs = (float *)malloc(n * sizeof(float));
+    memcpy(buf, logits, n * sizeof(float));
+    if (p->has_repetition_penalty)
+        or_apply_repetition_penalty(buf, n, history, n_history, p->repetition_penalty);
+    or_apply_temperature(buf, n, p->temperature);
+    if (p->has_top_k) or_apply_top_k(buf, n, p->top_k);
+    or_softmax_to_probs(buf, n, probs);
+    int rc = 0;
+    if (p->has_top_p) {
+        if (p->top_p > 0.0f && p->top_p < 1.0f)
+            for (size_t i = 0; i < n && !rc; i++)
+                if (isnan(probs[i])) rc = -3;
+        if (!rc) or_apply_top_p(probs, n, p->top_p);
+    }
+    if (!rc) {
+        float total = 0.0f;
+        for (size_t i = 0; i < n; i++) total += probs[i];
+        if (total_out) *total_out = total;
+        if (total <= 0.0f || !isfinite(total)) {
+            rc = -2;
+        } else {
+            float r = or_xorshift64_next_unit(state) * total;
+            float acc = 0.0f;
+            size_t pick = n - 1;
+            for (size_t i = 0; i < n; i++) {
+                acc += probs[i];
+                if (r <= acc) {
+                    pick = i;
+                    break;
+                }
+            }
+            *out = (uint32_t)pick;
+        }
+    }
+    free(buf);
+    free(probs);
+    return rc;
+}

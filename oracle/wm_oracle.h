@@ -125,6 +125,39 @@ int or_greedy_generate(or_model *m, or_kv *kv, const uint32_t *prompt, uint32_t 
                        uint32_t max_new, int64_t eos, uint32_t *out_ids, uint32_t *n_out,
                        float *logits_trace);
 
+/* ---- sampler (src/model/sampler.rs) ------------------------------------ */
+/* XorShift64 (sampler.rs:13-38): the state a seed gives (0 -> 0xdeadbeefcafebabe),
+ * the next value (state updated) and the unit draw from its high 24 bits. */
+uint64_t or_xorshift64_seed(uint64_t seed);
+uint64_t or_xorshift64_next(uint64_t *state);
+float or_xorshift64_next_unit(uint64_t *state);
+/* SamplingParams (sampler.rs:40-79); the Option fields as has_* flags. */
+typedef struct or_sampling_params {
+    float temperature;
+    uint32_t has_top_k;
+    uint64_t top_k;
+    float top_p;
+    uint32_t has_top_p;
+    float repetition_penalty;
+    uint32_t has_repetition_penalty;
+} or_sampling_params;
+int or_sampling_is_greedy(const or_sampling_params *p);                  /* :71-78 */
+void or_apply_repetition_penalty(float *logits, size_t n, const uint32_t *history,
+                                 size_t n_history, float r);             /* :151-164 */
+void or_apply_temperature(float *logits, size_t n, float t);              /* :166-176 */
+void or_apply_top_k(float *logits, size_t n, uint64_t k);                 /* :201-223 */
+void or_softmax_to_probs(const float *logits, size_t n, float *out);      /* :225-252 */
+/* :254-311; entries of equal probability are taken in index order (the
+ * reference's unstable sort leaves their order open). */
+void or_apply_top_p(float *probs, size_t n, float p);
+/* Sampler::sample (:133-149) with multinomial (:178-196).  Returns 0 and
+ * *out; -1 empty logits; -2 the multinomial error (probabilities not
+ * summing to a positive finite value, *total_out set); -3 NaN
+ * probabilities under top-p with 0 < p < 1 (where the reference's sort
+ * order is unspecified).  *state advances only when the draw runs. */
+int or_sample(const or_sampling_params *p, uint64_t *state, const uint32_t *history,
+              size_t n_history, const float *logits, size_t n, uint32_t *out, float *total_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -287,6 +287,28 @@ class DeviceKV:
                                                  wh._ptr(out, wh.C.c_uint32), wh.C.byref(n)))
         return out[: n.value].tolist()
 
+    def prefill(self, tokens, want_hidden: bool = True):
+        """Batched prefill of `tokens` at the cache's position; the last
+        token's hidden after output_norm."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+        hidden = np.empty(self.model.cfg.n_embd, np.float32) if want_hidden else None
+        self.ctx.check(wh.lib.wm_prefill(self.model.h, self.h, wh._ptr(tokens, wh.C.c_uint32),
+                                         tokens.size,
+                                         wh._ptr(hidden, wh.C.c_float) if want_hidden else None))
+        return hidden
+
+    def generate_sampled(self, prompt, max_new: int, sampler, eos: int = -1, stop_ids=()):
+        """generate_with_cache_and_sampler (src/model/generate.rs:195-277)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        stops = np.ascontiguousarray(list(stop_ids) or [0], dtype=np.uint32)
+        out = np.empty(max(max_new, 1), np.uint32)
+        n = wh.C.c_uint32()
+        self.ctx.check(wh.lib.wm_generate_with_sampler(
+            self.model.h, self.h, wh._ptr(prompt, wh.C.c_uint32), prompt.size, max_new, eos,
+            wh._ptr(stops, wh.C.c_uint32), len(stop_ids), sampler.h, wh._ptr(out, wh.C.c_uint32),
+            wh.C.byref(n)))
+        return out[: n.value].tolist()
+
 
 @dataclass(frozen=True)
 class RaggedWorkload:

@@ -460,7 +460,78 @@ __global__ void k_i2s_finalize_multi(const int32_t *__restrict__ partial, uint32
     y[idx] = (w_scales[c] * meta->scale) * (float)dot;
 }
 
+// --------------------------------------------------------------------------
+// scalar f32 matvec (bitlinear_i2s_matvec_f32_scalar, src/model/bitlinear.rs:146-233)
+// --------------------------------------------------------------------------
+// No int8 activations: per row, two f32 accumulators, pos += x for code 10
+// and neg += x for code 00, over the row's bytes in order and, in each byte,
+// the codes of columns gp, gp+32, gp+64, gp+96 (bits 7:6 down to 1:0); then
+// out = scale * (pos - neg).  Each accumulator is a dependent chain, so one
+// lane owns one row (lane r of workgroup g: row 64g + r, its 16-byte chunks
+// coalesced across the wave).  A skipped code adds +0.0 instead: pos and
+// neg start at +0.0 and an f32 sum is -0.0 only when both operands are, so
+// they never hold -0.0 and x + (+0.0) == x for every other value (NaN and
+// inf included): the result is the reference's bit for bit.
+// Chunk c of a row is bytes [16c, 16c+16): byte b of it is byte
+// gp = 16(c%2) + b of block c/2, i.e. columns 128(c/2) + gp + {0,32,64,96}.
+constexpr uint32_t kScalarTile = 1024;  // x columns staged in LDS per round (8 blocks, 16 chunks)
+
+// Bytes b .. b+3 of a block (one little-endian dword; xb points at column
+// gp = b of the block in LDS) in the reference's order.
+__device__ __forceinline__ void scalar_dword(uint32_t wd, const float *xb, float &pos, float &neg) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t byte = (wd >> (8 * e)) & 0xffu;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t code = (byte >> (6 - 2 * q)) & 3u;
+            const float xv = xb[e + 32 * q];
+            pos += code == 2u ? xv : 0.0f;
+            neg += code == 0u ? xv : 0.0f;
+        }
+    }
+}
+
+typedef uint32_t scalar_u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(64) void k_i2s_scalar_f32(const scalar_u32x4 *__restrict__ w, uint32_t n_chunks,
+                                                       uint32_t out_dim, float scale,
+                                                       const float *__restrict__ x,
+                                                       float *__restrict__ y) {
+    __shared__ __align__(16) float xs[kScalarTile];
+    const uint32_t lane = threadIdx.x, g = blockIdx.x;
+    const scalar_u32x4 *wg = w + (uint64_t)g * n_chunks * I2S_GROUP_ROWS + lane;
+    const uint32_t in_dim = n_chunks * I2S_CHUNK_COLS;
+    float pos = 0.0f, neg = 0.0f;
+    for (uint32_t base = 0; base < in_dim; base += kScalarTile) {
+        const uint32_t cols = min(kScalarTile, in_dim - base);  // a multiple of 128
+        __syncthreads();
+        for (uint32_t i = lane; i < cols; i += 64) xs[i] = x[base + i];
+        __syncthreads();
+        const uint32_t c0 = base / I2S_CHUNK_COLS, c1 = c0 + cols / I2S_CHUNK_COLS;
+        scalar_u32x4 cur = wg[(uint64_t)c0 * I2S_GROUP_ROWS];
+        for (uint32_t c = c0; c < c1; c++) {
+            const scalar_u32x4 nxt = c + 1 < c1 ? wg[(uint64_t)(c + 1) * I2S_GROUP_ROWS] : cur;
+            const float *xb = xs + ((c - c0) / 2) * 128 + (c & 1) * 16;
+            scalar_dword(cur.x, xb, pos, neg);
+            scalar_dword(cur.y, xb + 4, pos, neg);
+            scalar_dword(cur.z, xb + 8, pos, neg);
+            scalar_dword(cur.w, xb + 12, pos, neg);
+            cur = nxt;
+        }
+    }
+    const uint32_t row = g * I2S_GROUP_ROWS + lane;
+    if (row < out_dim) y[row] = scale * (pos - neg);
+}
+
 }  // namespace
+
+void wm_launch_i2s_scalar_f32(const uint8_t *w, uint32_t n_groups, uint32_t n_chunks,
+                              uint32_t out_dim, float scale, const float *x, float *y,
+                              hipStream_t s) {
+    hipLaunchKernelGGL(k_i2s_scalar_f32, dim3(n_groups), dim3(64), 0, s,
+                       reinterpret_cast<const scalar_u32x4 *>(w), n_chunks, out_dim, scale, x, y);
+}
 
 void wm_launch_i2s_finalize_multi(const int32_t *partial, uint32_t split, uint32_t rows_total,
                                   uint32_t rows_per_copy, uint32_t out_dim, uint32_t n_copies,

@@ -333,6 +333,19 @@ wm_status rows_unsupported(wm_ctx *ctx) {
     return wm_set_error(ctx, WM_E_SHAPE, "batch_forward: no row-norm kernel for this model shape");
 }
 
+// The ragged-batch kernels cover this model shape (else prompts are
+// prefilled token by token).
+bool batch_supported(const wm_model *m) {
+    const wm_model_config &c = m->cfg;
+    return wm_attn_rows_supported(c.head_dim, c.n_heads / c.n_kv_heads) && c.n_embd <= 8192 &&
+           c.n_ff <= 8192;
+}
+
+constexpr uint32_t kPrefillChunk = 512;  // tokens per batched prefill call
+
+wm_status prefill_tokens(wm_model *m, wm_kv_cache *kv, const uint32_t *tokens, uint32_t n,
+                         float *last_hidden);
+
 // Grow the ragged-batch workspace to hold `M` tokens.
 wm_status ensure_batch_ws(wm_model *m, uint32_t M) {
     if (M <= m->b_cap) return WM_OK;
@@ -938,11 +951,7 @@ wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *promp
                             kv->max_seq);
     const uint32_t start = kv->pos;
     wm_status st;
-    for (uint32_t i = 0; i + 1 < n_prompt; i++)
-        if ((st = wm_forward_with_cache(m, kv, prompt[i], kv->pos, nullptr, nullptr))) {
-            kv->pos = start;
-            return st;
-        }
+    if ((st = prefill_tokens(m, kv, prompt, n_prompt - 1, nullptr))) return st;
     if ((st = check_step(m, kv, prompt[n_prompt - 1], kv->pos))) {
         kv->pos = start;
         return st;
@@ -1022,6 +1031,116 @@ wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *promp
     kv->pos = pos0 + done;
     *n_out = n;
     return WM_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Prefill `n` tokens at the cache's position: ragged-batch calls of up to
+// kPrefillChunk tokens (bit-identical to the token-by-token prefill of
+// generate.rs:151-160), or forward_with_cache per token where the batch
+// kernels do not cover the shape.  On an error the cache goes back to where
+// it started.
+wm_status prefill_tokens(wm_model *m, wm_kv_cache *kv, const uint32_t *tokens, uint32_t n,
+                         float *last_hidden) {
+    const uint32_t start = kv->pos;
+    const bool batched = batch_supported(m);
+    for (uint32_t off = 0; off < n;) {
+        const uint32_t len = batched ? std::min(n - off, kPrefillChunk) : 1;
+        float *lh = off + len == n ? last_hidden : nullptr;
+        const wm_status st = batched ? wm_batch_forward(m, &kv, 1, &len, tokens + off, lh, nullptr)
+                                     : wm_forward_with_cache(m, kv, tokens[off], kv->pos, lh, nullptr);
+        if (st) {
+            kv->pos = start;
+            return st;
+        }
+        off += len;
+    }
+    return WM_OK;
+}
+
+// One decode step whose exact logits stay in m->logits on the device
+// (forward_with_cache + compute_logits_from_graph).
+wm_status step_with_logits(wm_model *m, wm_kv_cache *kv, uint32_t token) {
+    wm_ctx *ctx = m->ctx;
+    const uint32_t position = kv->pos;
+    wm_status st = check_step(m, kv, token, position);
+    if (st) return st;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    WM_HIP(ctx, hipMemcpyAsync(m->dscalars, &token, 4, hipMemcpyHostToDevice, ctx->stream));
+    if (!enqueue_forward(m, kv, step_pos{position, nullptr, 0}, nullptr))
+        return wm_set_error(ctx, WM_E_SHAPE, "decode_step: no kernel for this model shape");
+    wm_launch_q6k_logits_argmax(m->embd, m->embd_blocks, m->cfg.vocab_size, m->embd_rowgroups,
+                                m->final_hidden, m->logits, m->dscalars + 1, m->lm_work, ctx->stream);
+    WM_HIP(ctx, hipGetLastError());
+    bool failed = false;
+    return finish_step(m, kv, position, &failed);
+}
+
+}  // namespace
+
+extern "C" {
+
+wm_status wm_prefill(wm_model *m, wm_kv_cache *kv, const uint32_t *tokens, uint32_t n,
+                     float *last_hidden) {
+    if (!m || !kv) return WM_E_ARG;
+    wm_ctx *ctx = m->ctx;
+    if (!tokens || n == 0) return wm_set_error(ctx, WM_E_ARG, "prefill: token_ids must not be empty");
+    if (!model_ready(m)) return wm_set_error(ctx, WM_E_STATE, "model: weights not fully set");
+    if (kv->m != m) return wm_set_error(ctx, WM_E_ARG, "kv cache belongs to another model");
+    for (uint32_t i = 0; i < n; i++)
+        if (tokens[i] >= m->cfg.vocab_size)
+            return wm_set_error(ctx, WM_E_SHAPE, "forward_with_cache: token_id %u out of vocab range %u",
+                                tokens[i], m->cfg.vocab_size);
+    if ((uint64_t)kv->pos + n > kv->max_seq)
+        return wm_set_error(ctx, WM_E_SHAPE, "KVCache::append: %u tokens would pass max_seq_len %u", n,
+                            kv->max_seq);
+    return prefill_tokens(m, kv, tokens, n, last_hidden);
+}
+
+wm_status wm_generate_with_sampler(wm_model *m, wm_kv_cache *kv, const uint32_t *prompt,
+                                   uint32_t n_prompt, uint32_t max_new, int64_t eos,
+                                   const uint32_t *stop_ids, uint32_t n_stop, wm_sampler *s,
+                                   uint32_t *out_ids, uint32_t *n_out) {
+    if (!m || !kv || !s || !n_out || (max_new && !out_ids) || (n_stop && !stop_ids)) return WM_E_ARG;
+    wm_ctx *ctx = m->ctx;
+    *n_out = 0;
+    if (wm_sampler_ctx(s) != ctx) return wm_set_error(ctx, WM_E_ARG, "sampler of another context");
+    if (!prompt || n_prompt == 0)
+        return wm_set_error(ctx, WM_E_ARG, "generate_with_cache_and_sampler: prompt_ids must not be empty");
+    for (uint32_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= m->cfg.vocab_size)
+            return wm_set_error(ctx, WM_E_SHAPE,
+                                "generate_with_cache_and_sampler: prompt token %u (idx %u) out of vocab range %u",
+                                prompt[i], i, m->cfg.vocab_size);
+    if ((uint64_t)kv->pos + n_prompt + (max_new ? max_new - 1 : 0) > kv->max_seq)
+        return wm_set_error(ctx, WM_E_SHAPE,
+                            "generate_with_cache_and_sampler: budget exceeds max_seq_len %u", kv->max_seq);
+    if (!model_ready(m)) return wm_set_error(ctx, WM_E_STATE, "model: weights not fully set");
+    if (kv->m != m) return wm_set_error(ctx, WM_E_ARG, "kv cache belongs to another model");
+    // the prompt enters the repetition-penalty history (generate.rs:229-233)
+    for (uint32_t i = 0; i < n_prompt; i++) wm_sampler_observe(s, prompt[i]);
+    const uint32_t start = kv->pos;
+    wm_status st = prefill_tokens(m, kv, prompt, n_prompt - 1, nullptr);
+    if (!st) st = step_with_logits(m, kv, prompt[n_prompt - 1]);
+    if (st) {
+        kv->pos = start;
+        return st;
+    }
+    uint32_t n = 0;
+    for (uint32_t step = 0; step < max_new; step++) {
+        uint32_t next = 0;
+        if ((st = wm_sampler_run(s, m->logits, m->cfg.vocab_size, &next))) break;
+        bool stop = eos >= 0 && (int64_t)next == eos;
+        for (uint32_t j = 0; j < n_stop && !stop; j++) stop = stop_ids[j] == next;
+        if (stop) break;
+        out_ids[n++] = next;
+        wm_sampler_observe(s, next);
+        if (step + 1 < max_new && (st = step_with_logits(m, kv, next))) break;
+    }
+    *n_out = n;
+    return st;
 }
 
 }  // extern "C"

@@ -349,6 +349,42 @@ wm_status wm_bitlinear_i2s_matvec_f32(wm_ctx *ctx, const wm_tensor *w, const flo
                                              nullptr, nullptr);
 }
 
+wm_status wm_bitlinear_i2s_matvec_f32_scalar_dev(wm_ctx *ctx, const wm_tensor *w,
+                                                 const float *d_input, float *d_output) {
+    wm_status st = check_i2s(ctx, w);
+    if (st) return st;
+    if (!d_input || !d_output) return wm_set_error(ctx, WM_E_ARG, "bitlinear scalar: null input/output");
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    wm_launch_i2s_scalar_f32((const uint8_t *)w->d, w->n_groups, w->n_chunks, (uint32_t)w->out_dim,
+                             w->scale, d_input, d_output, ctx->stream);
+    WM_HIP(ctx, hipGetLastError());
+    return WM_OK;
+}
+
+wm_status wm_bitlinear_i2s_matvec_f32_scalar(wm_ctx *ctx, const wm_tensor *w, const float *input,
+                                             size_t input_len, float *output, size_t output_len) {
+    wm_status st = check_i2s(ctx, w);
+    if (st) return st;
+    if (!input || !output) return wm_set_error(ctx, WM_E_ARG, "bitlinear scalar: null input/output");
+    if (input_len != w->in_dim)
+        return wm_set_error(ctx, WM_E_SHAPE, "bitlinear_i2s_matvec_f32: input.len()=%zu != in_dim=%llu",
+                            input_len, (unsigned long long)w->in_dim);
+    if (output_len != w->out_dim)
+        return wm_set_error(ctx, WM_E_SHAPE, "bitlinear_i2s_matvec_f32: output.len()=%zu != out_dim=%llu",
+                            output_len, (unsigned long long)w->out_dim);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    const size_t in_b = align256(w->in_dim * 4);
+    void *scratch;
+    if ((st = wm_ctx_scratch(ctx, in_b + align256(w->out_dim * 4), &scratch))) return st;
+    float *d_x = (float *)scratch;
+    float *d_y = (float *)((uint8_t *)scratch + in_b);
+    WM_HIP(ctx, hipMemcpyAsync(d_x, input, w->in_dim * 4, hipMemcpyHostToDevice, ctx->stream));
+    if ((st = wm_bitlinear_i2s_matvec_f32_scalar_dev(ctx, w, d_x, d_y))) return st;
+    WM_HIP(ctx, hipMemcpyAsync(output, d_y, w->out_dim * 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return WM_OK;
+}
+
 wm_status wm_bitlinear_i2s_matvec_f32_dev(wm_ctx *ctx, const wm_tensor *w, const float *d_input,
                                           float *d_output) {
     return wm_bitlinear_i2s_matvec_f32_multi_dev(ctx, &w, 1, d_input, d_output);

@@ -395,6 +395,16 @@ void wm_launch_i2s_finalize(const int32_t *partial, uint32_t split, uint32_t row
                             uint32_t row0, uint32_t out_dim, float w_scale,
                             const wm_act_meta *meta, float *y, int32_t *dot_out, hipStream_t s);
 uint32_t wm_i2s_pick_split(uint32_t n_groups, uint32_t n_chunks);
+// The device sampler (k_sample.hip): one Sampler::sample over n logits on
+// the device, on the sampler's context stream (synchronous).
+struct wm_sampler;
+wm_status wm_sampler_run(wm_sampler *s, const float *d_logits, uint32_t n, uint32_t *out_id);
+wm_ctx *wm_sampler_ctx(const wm_sampler *s);
+// Scalar f32 matvec (no int8 activations), one lane per row:
+// y[j] = scale * (pos_j - neg_j) in the reference's accumulation order.
+void wm_launch_i2s_scalar_f32(const uint8_t *w, uint32_t n_groups, uint32_t n_chunks,
+                              uint32_t out_dim, float scale, const float *x, float *y,
+                              hipStream_t s);
 void wm_launch_i2s_finalize_multi(const int32_t *partial, uint32_t split, uint32_t rows_total,
                                   uint32_t rows_per_copy, uint32_t out_dim, uint32_t n_copies,
                                   const float *w_scales, const wm_act_meta *meta, float *y,

@@ -86,6 +86,20 @@ class ModelConfig(C.Structure):
     ]
 
 
+class SamplingParams(C.Structure):
+    """wm_sampling_params: SamplingParams (src/model/sampler.rs:40-79) with
+    each Option as a has_* flag."""
+    _fields_ = [("temperature", C.c_float), ("has_top_k", C.c_uint32), ("top_k", C.c_uint64),
+                ("top_p", C.c_float), ("has_top_p", C.c_uint32),
+                ("repetition_penalty", C.c_float), ("has_repetition_penalty", C.c_uint32)]
+
+    @classmethod
+    def make(cls, temperature=0.0, top_k=None, top_p=None, repetition_penalty=None):
+        return cls(temperature, top_k is not None, top_k or 0, 0.0 if top_p is None else top_p,
+                   top_p is not None, 0.0 if repetition_penalty is None else repetition_penalty,
+                   repetition_penalty is not None)
+
+
 def _sig(name, restype, *argtypes):
     f = getattr(lib, name)
     f.restype = restype
@@ -115,6 +129,8 @@ EXPORTS = {
     "wm_bitlinear_i2s_matvec_f32_debug": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p,
                                           C.c_size_t, _i8p, _f32p, _i32p),
     "wm_bitlinear_i2s_matvec_f32_dev": (C.c_int, _vp, _vp, _vp, _vp),
+    "wm_bitlinear_i2s_matvec_f32_scalar": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p, C.c_size_t),
+    "wm_bitlinear_i2s_matvec_f32_scalar_dev": (C.c_int, _vp, _vp, _vp, _vp),
     "wm_bitlinear_i2s_matvec_f32_dev_noalloc": (C.c_int, _vp, _vp, _vp, _vp),
     "wm_debug_rerun_role": (C.c_int, _vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32),
     "wm_bitlinear_i2s_matvec_f32_multi_dev": (C.c_int, _vp, C.POINTER(_vp), C.c_uint32, _vp, _vp),
@@ -145,6 +161,16 @@ EXPORTS = {
     "wm_greedy_generate": (C.c_int, _vp, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_int64, _u32p,
                            _u32p),
     "wm_batch_forward": (C.c_int, _vp, C.POINTER(_vp), C.c_uint32, _u32p, _u32p, _f32p, _u32p),
+    "wm_prefill": (C.c_int, _vp, _vp, _u32p, C.c_uint32, _f32p),
+    "wm_sampler_create": (C.c_int, _vp, C.POINTER(SamplingParams), C.c_uint64, C.POINTER(_vp)),
+    "wm_sampler_destroy": (None, _vp),
+    "wm_sampler_observe": (C.c_int, _vp, C.c_uint32),
+    "wm_sampler_checkpoint": (C.c_int, _vp, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)),
+    "wm_sampler_rollback": (C.c_int, _vp, C.c_uint64, C.c_uint64),
+    "wm_sampler_sample": (C.c_int, _vp, _f32p, C.c_size_t, _u32p),
+    "wm_sampler_sample_dev": (C.c_int, _vp, _vp, C.c_size_t, _u32p),
+    "wm_generate_with_sampler": (C.c_int, _vp, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_int64,
+                                 _u32p, C.c_uint32, _vp, _u32p, _u32p),
     "wm_debug_seq_sum": (C.c_int, _vp, _f32p, C.c_size_t, _f32p),
     "wm_debug_q6k_bounded_logits": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p, _f32p),
     "wm_debug_q6k_bounded_logits_dev": (C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int),
@@ -295,6 +321,52 @@ class Context:
         return Tensor(self, h)
 
 
+class Sampler:
+    """Sampler (src/model/sampler.rs:81-149) whose sample() runs on the device."""
+    _close_rank = 0
+
+    def __init__(self, ctx: Context, params: SamplingParams, seed: int):
+        self.ctx, self.params = ctx, params
+        h = _vp()
+        ctx.check(lib.wm_sampler_create(ctx.h, C.byref(params), seed, C.byref(h)))
+        self.h = h
+        ctx.adopt(self)
+
+    def close(self):
+        if self.h:
+            lib.wm_sampler_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def observe(self, tok: int):
+        self.ctx.check(lib.wm_sampler_observe(self.h, tok))
+
+    def checkpoint(self):
+        st, n = C.c_uint64(), C.c_uint64()
+        self.ctx.check(lib.wm_sampler_checkpoint(self.h, C.byref(st), C.byref(n)))
+        return st.value, n.value
+
+    def rollback(self, cp):
+        self.ctx.check(lib.wm_sampler_rollback(self.h, cp[0], cp[1]))
+
+    def sample(self, logits: np.ndarray) -> int:
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        out = C.c_uint32()
+        self.ctx.check(lib.wm_sampler_sample(self.h, _ptr(logits, C.c_float), logits.size,
+                                             C.byref(out)))
+        return int(out.value)
+
+    def sample_dev(self, buf: "DeviceBuffer", n: int) -> int:
+        out = C.c_uint32()
+        self.ctx.check(lib.wm_sampler_sample_dev(self.h, buf.ptr, n, C.byref(out)))
+        return int(out.value)
+
+
 class DeviceBuffer:
     _close_rank = 2
 
@@ -371,6 +443,16 @@ def bitlinear_i2s_matvec_f32(ctx: Context, w: Tensor, x: np.ndarray, debug: bool
                                                     _ptr(y, C.c_float), y.size, _ptr(act, C.c_int8),
                                                     C.byref(sc), _ptr(acc, C.c_int32)))
     return y, act, float(np.float32(sc.value)), acc
+
+
+def bitlinear_i2s_matvec_f32_scalar(ctx: Context, w: Tensor, x: np.ndarray) -> np.ndarray:
+    """bitlinear_i2s_matvec_f32_scalar (src/model/bitlinear.rs:146-233): f32
+    inputs, no int8 quantiser."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(w.shape[1], dtype=np.float32)
+    ctx.check(lib.wm_bitlinear_i2s_matvec_f32_scalar(ctx.h, w.h, _ptr(x, C.c_float), x.size,
+                                                     _ptr(y, C.c_float), y.size))
+    return y
 
 
 def bitlinear_i2s_matmul_f32(ctx: Context, w: Tensor, x: np.ndarray) -> np.ndarray:

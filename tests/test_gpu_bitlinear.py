@@ -168,3 +168,96 @@ def test_multi_entry_point_many_copies(ctx):
     got = dy.to_host(np.float32).reshape(n, out_dim)
     for i in range(n):
         assert same_bits(got[i], refs[i]), f"copy {i}"
+
+
+# ---- the scalar f32 path (src/model/bitlinear.rs:146-233) -----------------
+
+def same_bits_nan(a, b):
+    """Bit-identical except that any NaN matches any NaN: IEEE 754 leaves a
+    NaN result's sign and payload open (x86 passes the operand's through,
+    the GPU returns the canonical one), and the reference never inspects
+    them."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    na, nb = np.isnan(a), np.isnan(b)
+    return a.shape == b.shape and np.array_equal(na, nb) and \
+        np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32))
+
+
+SCALAR_SHAPES = [(128, 1), (128, 64), (256, 100), (1152, 65), (2560, 2560), (6912, 2560),
+                 (4096, 128)]
+
+
+@pytest.mark.parametrize("in_dim,out_dim", SCALAR_SHAPES)
+def test_scalar_matvec_bit_exact(ctx, in_dim, out_dim):
+    """f32 outputs bit-identical to the oracle's scalar restatement; random
+    bytes include the degenerate code 11; 1152 columns leave a partial LDS
+    round of x."""
+    rng = np.random.default_rng(in_dim * 13 + out_dim)
+    packed = rng.integers(0, 256, in_dim // 4 * out_dim, dtype=np.uint8)
+    x = (rng.standard_normal(in_dim) * rng.uniform(0.1, 10)).astype(np.float32)
+    scale = float(rng.uniform(0.5, 2))
+    w = ctx.upload_i2s(packed, scale, in_dim, out_dim)
+    y = wh.bitlinear_i2s_matvec_f32_scalar(ctx, w, x)
+    ry = orc.bitlinear_scalar(packed, np.float32(scale), in_dim, out_dim, x)
+    assert same_bits(y, ry)
+
+
+@pytest.mark.parametrize("kind", ["kat_aa", "kat_00", "kat_55", "nan_skipped", "nan_used", "inf",
+                                  "neg_zero", "huge"])
+def test_scalar_matvec_edges(ctx, kind):
+    """Reference KATs (0xAA -> scale * Σx, 0x00 -> -scale * Σx, 0x55 -> 0,
+    bitlinear.rs:343-428) and non-finite inputs: a NaN under a 0 code is
+    skipped, under a +-1 code it reaches the output; -0.0 inputs leave +0.0
+    sums."""
+    rng = np.random.default_rng(5)
+    in_dim, out_dim = 256, 70
+    x = rng.standard_normal(in_dim).astype(np.float32)
+    packed = rng.integers(0, 256, in_dim // 4 * out_dim, dtype=np.uint8)
+    if kind.startswith("kat"):
+        packed[:] = {"kat_aa": 0xAA, "kat_00": 0x00, "kat_55": 0x55}[kind]
+    elif kind == "nan_skipped":
+        packed[:] = 0x55
+        packed[1::7] = 0xAA
+        x[0] = np.nan  # column 0: bits 7:6 of byte 0 of each row, code 01 unless byte 0 was set
+    elif kind == "nan_used":
+        x[37] = np.nan
+    elif kind == "inf":
+        x[3], x[200] = np.inf, -np.inf
+    elif kind == "neg_zero":
+        x[:] = -0.0
+    elif kind == "huge":
+        x *= np.float32(3e37)
+    w = ctx.upload_i2s(packed, 1.5, in_dim, out_dim)
+    y = wh.bitlinear_i2s_matvec_f32_scalar(ctx, w, x)
+    ry = orc.bitlinear_scalar(packed, np.float32(1.5), in_dim, out_dim, x)
+    assert same_bits_nan(y, ry)
+    if kind in ("kat_aa", "kat_00"):
+        # the block walk's column order: byte gp of block bk, then its four codes
+        order = [128 * bk + gp + 32 * q for bk in range(in_dim // 128) for gp in range(32)
+                 for q in range(4)]
+        s = np.float32(0)
+        for j in order:
+            s = np.float32(s + x[j])
+        want = np.float32(1.5) * (s if kind == "kat_aa" else np.float32(np.float32(0) - s))
+        assert np.all(y == want)
+    if kind in ("kat_55", "neg_zero"):
+        assert np.all(y == 0) and not np.any(np.signbit(y))
+    if kind == "nan_skipped":
+        assert np.all(np.isfinite(y[(packed.reshape(out_dim, -1)[:, 0] >> 6) != 2]))
+
+
+def test_scalar_matvec_rejects(ctx):
+    """Length and type checks of bitlinear.rs:157-199, before any launch."""
+    w = ctx.upload_i2s(np.zeros(256 // 4 * 8, np.uint8), 1.0, 256, 8)
+    y = np.empty(8, np.float32)
+    for xn, yn in ((255, 8), (256, 7)):
+        x = np.zeros(xn, np.float32)
+        yy = np.empty(yn, np.float32)
+        with pytest.raises(wh.WillametteError) as ei:
+            ctx.check(wh.lib.wm_bitlinear_i2s_matvec_f32_scalar(
+                ctx.h, w.h, wh._ptr(x, wh.C.c_float), x.size, wh._ptr(yy, wh.C.c_float), yy.size))
+        assert ei.value.kind == "Shape"
+    q = ctx.upload_q6k(np.zeros(210, np.uint8), 256, 1)
+    with pytest.raises(wh.WillametteError) as ei:
+        wh.bitlinear_i2s_matvec_f32_scalar(ctx, q, np.zeros(256, np.float32))
+    assert ei.value.kind == "UnsupportedTensorType"

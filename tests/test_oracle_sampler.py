@@ -1,0 +1,223 @@
+"""CPU pins of the oracle's sampler restatement (src/model/sampler.rs).
+
+The reference's own tests (sampler.rs:313-469) are applied to the oracle,
+plus checks a plausible mistake would fail: the published xorshift64
+sequence, the draw's `r <= acc` boundary (a state chosen so that r lands
+exactly on a cumulative sum), draw frequencies against the probabilities,
+the softmax against float64, top-k / top-p against brute force.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle.oracle as orc
+
+SP = orc.SamplingParams.make
+
+
+def test_xorshift64_published_sequence():
+    """Marsaglia's xorshift64 (shifts 13, 7, 17) from the seed
+    88172645463325252: the first outputs are the published ones."""
+    s = C.c_uint64(88172645463325252)
+    got = [orc.lib.or_xorshift64_next(C.byref(s)) for _ in range(3)]
+    assert got == [8748534153485358512, 3040900993826735515, 3453997556048239312]
+    assert orc.lib.or_xorshift64_seed(0) == 0xDEADBEEFCAFEBABE  # sampler.rs:19-23
+    assert orc.lib.or_xorshift64_seed(5) == 5
+
+
+def test_next_unit_is_high_24_bits():
+    s = C.c_uint64(88172645463325252)
+    u = orc.lib.or_xorshift64_next_unit(C.byref(s))
+    assert u == np.float32((8748534153485358512 >> 40) / 2.0**24)
+
+
+def test_greedy_default_returns_argmax():  # sampler.rs:317-325
+    s = orc.Sampler(SP(), 0xABAD1DEA)
+    for _ in range(5):
+        assert s.sample([0.1, 0.5, 0.3, 0.9]) == 3
+    # argmax rules (lm_head.rs:161-174): first of equal maxima, NaN at 0 wins
+    assert s.sample([1.0, 2.0, 2.0]) == 1
+    assert s.sample([np.nan, 5.0]) == 0
+    assert s.sample([1.0, np.nan, 0.5]) == 0
+
+
+def test_seed_makes_sampling_deterministic():  # sampler.rs:327-346
+    p = SP(temperature=1.0)
+    a, b = orc.Sampler(p, 12345), orc.Sampler(p, 12345)
+    logits = np.full(16, 0.1, np.float32)
+    assert [a.sample(logits) for _ in range(20)] == [b.sample(logits) for _ in range(20)]
+
+
+def test_rollback_restores_history_and_rng():  # sampler.rs:348-372
+    p = SP(temperature=1.0, repetition_penalty=1.1)
+    logits = np.full(16, 0.1, np.float32)
+    s = orc.Sampler(p, 12345)
+    s.observe(2)
+    cp = s.checkpoint()
+    s.observe(s.sample(logits))
+    s.rollback(cp)
+    clean = orc.Sampler(p, 12345)
+    clean.observe(2)
+    assert s.history == clean.history
+    assert s.sample(logits) == clean.sample(logits)
+
+
+def test_temperature_one_uniform_shape():  # sampler.rs:374-393
+    s = orc.Sampler(SP(temperature=1.0), 7)
+    hits = np.zeros(4, int)
+    for _ in range(4000):
+        hits[s.sample([0.0, 0.0, 0.0, 0.0])] += 1
+    assert np.all((hits > 700) & (hits < 1300)), hits
+
+
+def test_draw_frequencies_follow_probabilities():
+    """An off-by-one in the cumulative walk shifts mass between neighbours."""
+    s = orc.Sampler(SP(temperature=1.0), 99)
+    logits = np.log(np.array([0.5, 0.125, 0.25, 0.125], np.float64)).astype(np.float32)
+    n = 40000
+    hits = np.bincount([s.sample(logits) for _ in range(n)], minlength=4)
+    want = np.array([0.5, 0.125, 0.25, 0.125]) * n
+    assert np.all(np.abs(hits - want) < 5 * np.sqrt(want)), hits
+
+
+def _state_before(output: int) -> int:
+    """The xorshift64 state whose next output is `output` (each step
+    x ^= x << a / x ^= x >> b is invertible)."""
+    M = (1 << 64) - 1
+
+    def inv_left(y, a):
+        x = y
+        for _ in range(64 // a + 1):
+            x = (y ^ (x << a)) & M
+        return x
+
+    def inv_right(y, b):
+        x = y
+        for _ in range(64 // b + 1):
+            x = y ^ (x >> b)
+        return x
+
+    x = inv_left(output, 17)
+    x = inv_right(x, 7)
+    return inv_left(x, 13)
+
+
+def test_state_inversion_round_trips():
+    s = C.c_uint64(_state_before(0x123456789ABCDEF0))
+    assert orc.lib.or_xorshift64_next(C.byref(s)) == 0x123456789ABCDEF0
+
+
+@pytest.mark.parametrize("unit,expect", [(0.25, 0), (0.25 + 2**-24, 1), (0.5, 1), (0.75, 2)])
+def test_draw_boundary_is_r_le_acc(unit, expect):
+    """probs [0.25, 0.25, 0.5] (exact in f32, total 1): r = unit exactly; the
+    reference returns the first i with r <= acc_i (sampler.rs:187-194)."""
+    logits = np.log(np.array([0.25, 0.25, 0.5])).astype(np.float32)
+    probs = orc.softmax_to_probs(logits)
+    assert list(probs) == [0.25, 0.25, 0.5]
+    top = int(unit * 2**24)
+    assert top / 2**24 == unit
+    s = orc.Sampler(SP(temperature=1.0), 1)
+    s.state.value = _state_before((top << 40) | 0x12345)
+    assert s.sample(logits) == expect
+
+
+def test_top_k_kats():  # sampler.rs:395-417
+    x = orc.apply_top_k([1.0, 2.0, 3.0, 4.0, 5.0], 2)
+    assert np.all(np.isneginf(x[:3])) and x[3] == 4.0 and x[4] == 5.0
+    assert np.all(np.isneginf(orc.apply_top_k([1.0, 2.0, 3.0], 0)))
+    # ties at the threshold are all kept; k >= n changes nothing
+    x = orc.apply_top_k([1.0, 3.0, 3.0, 2.0], 1)
+    assert list(x[[1, 2]]) == [3.0, 3.0] and np.all(np.isneginf(x[[0, 3]]))
+    assert list(orc.apply_top_k([1.0, 2.0], 5)) == [1.0, 2.0]
+
+
+def test_top_k_matches_partition():
+    rng = np.random.default_rng(3)
+    for _ in range(50):
+        n = int(rng.integers(1, 300))
+        v = rng.standard_normal(n).astype(np.float32)
+        v[rng.integers(0, n, n // 5)] = v[0]  # ties
+        k = int(rng.integers(1, n + 1))
+        thr = np.sort(v)[::-1][k - 1]
+        want = np.where(v < thr, -np.inf, v).astype(np.float32)
+        assert np.array_equal(orc.apply_top_k(v, k), want)
+
+
+def test_top_p_kat():  # sampler.rs:419-434
+    p = orc.apply_top_p([0.4, 0.3, 0.2, 0.1], 0.7)
+    assert p[0] > 0 and p[1] > 0 and p[2] == 0 and p[3] == 0
+    assert abs(float(np.sum(p, dtype=np.float32)) - 1.0) < 1e-6
+
+
+def test_top_p_edges():
+    # p <= 0: one-hot at the first maximum; p >= 1: unchanged
+    assert list(orc.apply_top_p([0.2, 0.4, 0.4], 0.0)) == [0.0, 1.0, 0.0]
+    assert list(orc.apply_top_p([0.2, 0.3, 0.5], 1.0)) == [np.float32(0.2), np.float32(0.3), 0.5]
+    # equal probabilities at the cut: the lowest indices are kept
+    assert list(orc.apply_top_p([0.25, 0.25, 0.25, 0.25], 0.5)) == [0.5, 0.5, 0.0, 0.0]
+
+
+def test_top_p_matches_brute_force():
+    """Kept set = the smallest prefix of the descending order whose f32
+    running sum reaches p, checked against a float64 cumulative sum where
+    the two cannot disagree."""
+    rng = np.random.default_rng(4)
+    checked = 0
+    for _ in range(200):
+        n = int(rng.integers(2, 200))
+        pr = rng.dirichlet(np.ones(n) * 0.3).astype(np.float32)
+        p = float(rng.uniform(0.05, 0.95))
+        order = np.argsort(-pr, kind="stable")
+        cum = np.cumsum(pr[order].astype(np.float64))
+        j = int(np.searchsorted(cum, p))
+        if j < n and (abs(cum[j] - p) < 1e-5 or (j and abs(cum[j - 1] - p) < 1e-5)):
+            continue
+        keep = np.zeros(n, bool)
+        keep[order[: min(j + 1, n)]] = True
+        got = orc.apply_top_p(pr, p)
+        assert np.array_equal(got > 0, keep & (pr > 0))
+        checked += 1
+    assert checked > 150
+
+
+def test_softmax_to_probs_against_float64():
+    rng = np.random.default_rng(5)
+    for _ in range(20):
+        v = (rng.standard_normal(500) * 4).astype(np.float32)
+        got = orc.softmax_to_probs(v)
+        e = np.exp(v.astype(np.float64) - v.max())
+        assert np.allclose(got, e / e.sum(), rtol=1e-5, atol=1e-9)
+    assert not np.any(orc.softmax_to_probs([-np.inf, -np.inf]))
+    assert not np.any(orc.softmax_to_probs([1.0, np.inf]))
+
+
+def test_repetition_penalty_once_per_unique():  # sampler.rs:451-468
+    got = orc.apply_repetition_penalty([0.0, 8.0, -3.0], [1, 1, 2, 2], 2.0)
+    assert list(got) == [0.0, 4.0, -6.0]
+    # ids past the vocab are ignored; r <= 0 or r == 1 changes nothing
+    assert list(orc.apply_repetition_penalty([1.0, 2.0], [5, 0], 2.0)) == [0.5, 2.0]
+    assert list(orc.apply_repetition_penalty([1.0, 2.0], [0], 1.0)) == [1.0, 2.0]
+    assert list(orc.apply_repetition_penalty([1.0, 2.0], [0], -1.0)) == [1.0, 2.0]
+
+
+def test_repetition_penalty_kat_sample():  # sampler.rs:436-449
+    s = orc.Sampler(SP(temperature=1.0, repetition_penalty=2.0), 7)
+    s.observe(2)
+    assert s.sample([0.5, 0.5, 1.0, 0.5]) < 4
+
+
+def test_errors_and_state():
+    """The multinomial error leaves the rng untouched; NaN under top-p in
+    (0, 1) is refused (the reference's order is open there)."""
+    s = orc.Sampler(SP(temperature=1.0, top_k=0), 3)
+    st = s.state.value
+    with pytest.raises(ValueError, match="rc=-2"):
+        s.sample([1.0, 2.0])
+    assert s.state.value == st
+    with pytest.raises(ValueError, match="rc=-2"):
+        orc.Sampler(SP(temperature=1.0), 3).sample([1.0, np.nan])
+    with pytest.raises(ValueError, match="rc=-3"):
+        orc.Sampler(SP(temperature=1.0, top_p=0.5), 3).sample([1.0, np.nan])
+    # all -inf with p <= 0: the one-hot picks index 0 (probs were all zero)
+    assert orc.Sampler(SP(temperature=1.0, top_p=0.0), 3).sample([-np.inf, -np.inf]) == 0
