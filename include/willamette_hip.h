@@ -348,6 +348,36 @@ wm_status wm_generate_with_sampler(wm_model *m, wm_kv_cache *kv, const uint32_t 
                                    const uint32_t *stop_ids, uint32_t n_stop, wm_sampler *s,
                                    uint32_t *out_ids, uint32_t *n_out);
 
+/* ---- continuous batching --------------------------------------------- */
+
+/* No single counterpart in the reference: a driver that runs many
+ * generate_with_cache_and_sampler requests (src/model/generate.rs:195-277)
+ * at once.  Each step packs every active request's next prompt chunk or
+ * pending token into one ragged batch (wm_batch_forward); each request keeps
+ * its own cache and sampler, so its ids equal wm_generate_with_sampler's on
+ * its own (wm_greedy_generate's for greedy parameters).  At most max_seqs
+ * requests are active (caches of max_seq_len positions, pooled); a step
+ * feeds at most step_tokens tokens (max_seqs <= step_tokens <= 16384),
+ * decoding requests first.  Single-threaded, like the context. */
+typedef struct wm_server wm_server;
+wm_status wm_server_create(wm_model *m, uint32_t max_seqs, uint32_t max_seq_len, uint32_t step_tokens,
+                           wm_server **out);
+void wm_server_destroy(wm_server *s);
+/* Queue a request (prompt checks and budget as generate_with_cache_and_sampler,
+ * generate.rs:209-226, against max_seq_len); *request_id identifies it. */
+wm_status wm_server_submit(wm_server *s, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_new,
+                           int64_t eos, const uint32_t *stop_ids, uint32_t n_stop,
+                           const wm_sampling_params *params, uint64_t seed, uint64_t *request_id);
+/* One batch step; *n_active (nullable): requests still active or waiting. */
+wm_status wm_server_step(wm_server *s, uint32_t *n_active);
+/* The ids so far (up to cap copied, *n_out = all), whether the request has
+ * finished, and its error status if it failed (a non-finite hidden, a
+ * sampler error). */
+wm_status wm_server_result(wm_server *s, uint64_t request_id, uint32_t *out_ids, uint32_t cap,
+                           uint32_t *n_out, int *finished);
+/* Forget a request (finished or not); its cache returns to the pool. */
+wm_status wm_server_release(wm_server *s, uint64_t request_id);
+
 /* ---- GGUF files (src/gguf/reader.rs, src/model/graph.rs) ------------- */
 
 /* GgufFile::parse (src/gguf/reader.rs:120-415): the header, metadata and

@@ -310,6 +310,57 @@ class DeviceKV:
         return out[: n.value].tolist()
 
 
+class Server:
+    """Continuous-batching driver (wm_server_*) over a DeviceModel."""
+    _close_rank = -1
+
+    def __init__(self, model: DeviceModel, max_seqs: int, max_seq_len: int, step_tokens: int):
+        self.model, self.ctx = model, model.ctx
+        h = wh._vp()
+        self.ctx.check(wh.lib.wm_server_create(model.h, max_seqs, max_seq_len, step_tokens,
+                                               wh.C.byref(h)))
+        self.h = h
+        self.ctx.adopt(self)
+
+    def close(self):
+        if self.h:
+            wh.lib.wm_server_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def submit(self, prompt, max_new: int, params, seed: int, eos: int = -1, stop_ids=()) -> int:
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        stops = np.ascontiguousarray(list(stop_ids) or [0], dtype=np.uint32)
+        rid = wh.C.c_uint64()
+        self.ctx.check(wh.lib.wm_server_submit(self.h, wh._ptr(prompt, wh.C.c_uint32), prompt.size,
+                                               max_new, eos, wh._ptr(stops, wh.C.c_uint32),
+                                               len(stop_ids), wh.C.byref(params), seed,
+                                               wh.C.byref(rid)))
+        return rid.value
+
+    def step(self) -> int:
+        n = wh.C.c_uint32()
+        self.ctx.check(wh.lib.wm_server_step(self.h, wh.C.byref(n)))
+        return n.value
+
+    def result(self, rid: int):
+        """(ids so far, finished); raises the request's error if it failed."""
+        n, fin = wh.C.c_uint32(), wh.C.c_int()
+        self.ctx.check(wh.lib.wm_server_result(self.h, rid, None, 0, wh.C.byref(n), wh.C.byref(fin)))
+        out = np.empty(max(n.value, 1), np.uint32)
+        self.ctx.check(wh.lib.wm_server_result(self.h, rid, wh._ptr(out, wh.C.c_uint32), n.value,
+                                               wh.C.byref(n), wh.C.byref(fin)))
+        return out[: n.value].tolist(), bool(fin.value)
+
+    def release(self, rid: int):
+        self.ctx.check(wh.lib.wm_server_release(self.h, rid))
+
+
 @dataclass(frozen=True)
 class RaggedWorkload:
     """A continuous-batching step: sequence i holds contexts[i] pre-filled

@@ -393,11 +393,13 @@ wm_status ensure_batch_ws(wm_model *m, uint32_t M) {
 
 }  // namespace
 
-extern "C" {
-
-wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_seqs,
-                           const uint32_t *n_new, const uint32_t *tokens, float *last_hidden,
-                           uint32_t *next_tokens) {
+// The ragged step with its results left on the device: row last_rows[i] of
+// m->b_final is sequence i's last token after output_norm and, with
+// want_next, m->b_next[i] its id-only argmax.  The caches advance on
+// success; on a non-finite hidden none does.
+wm_status batch_forward_dev(wm_model *m, wm_kv_cache *const *caches, uint32_t n_seqs,
+                            const uint32_t *n_new, const uint32_t *tokens, bool want_next,
+                            std::vector<uint32_t> &last_rows) {
     if (!m) return WM_E_ARG;
     wm_ctx *ctx = m->ctx;
     if (!caches || !n_new || !tokens || n_seqs == 0)
@@ -501,7 +503,7 @@ wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_s
     wm_norm_rows fin{m->b_hidden, E, m->b_ydown, E, nullptr, 0, m->output_norm, E, c.rms_eps,
                      nullptr, m_pad, nullptr, m->b_final, E, err, c.n_layers};
     if (!wm_launch_rmsnorm_rows(fin, M, s)) return rows_unsupported(ctx);
-    if (next_tokens)
+    if (want_next)
         for (uint32_t i = 0; i < n_seqs; i++)
             wm_launch_q6k_argmax_fast(m->embd, m->embd_blocks, c.vocab_size, m->embd_rowgroups,
                                       m->b_final + (size_t)last[i] * E, m->logits, m->b_next + i,
@@ -518,14 +520,29 @@ wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_s
                             "multi_token_forward: non-finite hidden after layer %u; no cache advanced",
                             flag - 1);
     }
+    for (uint32_t i = 0; i < n_seqs; i++) caches[i]->pos += n_new[i];
+    last_rows = last;
+    return WM_OK;
+}
+
+extern "C" {
+
+wm_status wm_batch_forward(wm_model *m, wm_kv_cache *const *caches, uint32_t n_seqs,
+                           const uint32_t *n_new, const uint32_t *tokens, float *last_hidden,
+                           uint32_t *next_tokens) {
+    std::vector<uint32_t> last;
+    wm_status st = batch_forward_dev(m, caches, n_seqs, n_new, tokens, next_tokens != nullptr, last);
+    if (st) return st;
+    wm_ctx *ctx = m->ctx;
+    hipStream_t s = ctx->stream;
+    const size_t E = m->cfg.n_embd;
     if (last_hidden)
         for (uint32_t i = 0; i < n_seqs; i++)
-            WM_HIP(ctx, hipMemcpyAsync(last_hidden + (size_t)i * E, m->b_final + (size_t)last[i] * E,
-                                       (size_t)E * 4, hipMemcpyDeviceToHost, s));
+            WM_HIP(ctx, hipMemcpyAsync(last_hidden + i * E, m->b_final + (size_t)last[i] * E, E * 4,
+                                       hipMemcpyDeviceToHost, s));
     if (next_tokens)
         WM_HIP(ctx, hipMemcpyAsync(next_tokens, m->b_next, n_seqs * 4, hipMemcpyDeviceToHost, s));
     WM_HIP(ctx, hipStreamSynchronize(s));
-    for (uint32_t i = 0; i < n_seqs; i++) caches[i]->pos += n_new[i];
     return WM_OK;
 }
 
@@ -1144,3 +1161,33 @@ wm_status wm_generate_with_sampler(wm_model *m, wm_kv_cache *kv, const uint32_t 
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// internal interface for the continuous-batching driver (server.cpp)
+// ---------------------------------------------------------------------------
+
+wm_ctx *wm_model_ctx(const wm_model *m) { return m->ctx; }
+const wm_model_config &wm_model_cfg(const wm_model *m) { return m->cfg; }
+bool wm_model_batch_ready(const wm_model *m) { return model_ready(m) && batch_supported(m); }
+uint32_t wm_kv_max_seq(const wm_kv_cache *kv) { return kv->max_seq; }
+
+// Exact logits (compute_logits' order) of row `row` of the last batch step's
+// final hidden rows, into the model's logits buffer on the device.
+wm_status wm_batch_row_logits(wm_model *m, uint32_t row, const float **d_logits) {
+    wm_ctx *ctx = m->ctx;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    wm_launch_q6k_logits_argmax(m->embd, m->embd_blocks, m->cfg.vocab_size, m->embd_rowgroups,
+                                m->b_final + (size_t)row * m->cfg.n_embd, m->logits, m->dscalars + 1,
+                                m->lm_work, ctx->stream);
+    WM_HIP(ctx, hipGetLastError());
+    *d_logits = m->logits;
+    return WM_OK;
+}
+
+// The id-only argmax of each sequence of the last batch step (want_next).
+wm_status wm_batch_next_ids(wm_model *m, uint32_t n, uint32_t *out) {
+    wm_ctx *ctx = m->ctx;
+    WM_HIP(ctx, hipMemcpyAsync(out, m->b_next, (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return WM_OK;
+}

@@ -395,6 +395,19 @@ void wm_launch_i2s_finalize(const int32_t *partial, uint32_t split, uint32_t row
                             uint32_t row0, uint32_t out_dim, float w_scale,
                             const wm_act_meta *meta, float *y, int32_t *dot_out, hipStream_t s);
 uint32_t wm_i2s_pick_split(uint32_t n_groups, uint32_t n_chunks);
+// Model internals the continuous-batching driver (server.cpp) uses
+// (model.cpp).
+struct wm_model;
+struct wm_kv_cache;
+wm_status batch_forward_dev(wm_model *m, wm_kv_cache *const *caches, uint32_t n_seqs,
+                            const uint32_t *n_new, const uint32_t *tokens, bool want_next,
+                            std::vector<uint32_t> &last_rows);
+wm_ctx *wm_model_ctx(const wm_model *m);
+const wm_model_config &wm_model_cfg(const wm_model *m);
+bool wm_model_batch_ready(const wm_model *m);
+uint32_t wm_kv_max_seq(const wm_kv_cache *kv);
+wm_status wm_batch_row_logits(wm_model *m, uint32_t row, const float **d_logits);
+wm_status wm_batch_next_ids(wm_model *m, uint32_t n, uint32_t *out);
 // The device sampler (k_sample.hip): one Sampler::sample over n logits on
 // the device, on the sampler's context stream (synchronous).
 struct wm_sampler;

@@ -171,6 +171,13 @@ EXPORTS = {
     "wm_sampler_sample_dev": (C.c_int, _vp, _vp, C.c_size_t, _u32p),
     "wm_generate_with_sampler": (C.c_int, _vp, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_int64,
                                  _u32p, C.c_uint32, _vp, _u32p, _u32p),
+    "wm_server_create": (C.c_int, _vp, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(_vp)),
+    "wm_server_destroy": (None, _vp),
+    "wm_server_submit": (C.c_int, _vp, _u32p, C.c_uint32, C.c_uint32, C.c_int64, _u32p, C.c_uint32,
+                         C.POINTER(SamplingParams), C.c_uint64, C.POINTER(C.c_uint64)),
+    "wm_server_step": (C.c_int, _vp, _u32p),
+    "wm_server_result": (C.c_int, _vp, C.c_uint64, _u32p, C.c_uint32, _u32p, C.POINTER(C.c_int)),
+    "wm_server_release": (C.c_int, _vp, C.c_uint64),
     "wm_debug_seq_sum": (C.c_int, _vp, _f32p, C.c_size_t, _f32p),
     "wm_debug_q6k_bounded_logits": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p, _f32p),
     "wm_debug_q6k_bounded_logits_dev": (C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_int),
