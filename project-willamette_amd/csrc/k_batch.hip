@@ -404,110 +404,152 @@ __global__ __launch_bounds__(256) void k_qkv_rows(qkv_rows_args a) {
 struct attn_rows_args {
     const float *q;  // [t][n_heads * head_dim]
     const wm_batch_tok *tok;
-    float *scores;   // [t][n_heads][score_stride]
+    float *scores;   // [t][n_heads][score_stride]: the scores, then exp(s - max)
     float *out;      // [t][n_heads * head_dim]
     uint32_t layer, kv_dim, n_heads, score_stride, n_max;
     float scale;
+    float *row_scale;  // [t][n_heads]: 1 / Σexp (1 when Σ is not positive)
+    uint8_t *live;     // [t][n_heads][kAttnTiles]: the tile of kSvPos positions holds a non-zero exp
+    const wm_attn_item *sc_items, *sv_items;  // work items of the scores and V kernels
 };
 
-constexpr int kScoreThreads = 256;
+constexpr int kScoreThreads = 256;  // positions per scores item, one per thread
+constexpr int kScoreTok = 8;        // tokens (of one sequence) per scores item
 
+// scores[t][h][p] for the kScoreTok tokens t0 .. t0+nt-1 of one sequence
+// (item blockIdx.x), the G query heads of the item's KV head and positions
+// p0 .. p0+255 below p1: thread p loads its K row once, dequantises it (read_into:
+// q8 * scale) and runs the nt*G chains Σ_i q[i] * k[i], each in dimension
+// order, then * (1/sqrt(head_dim)).  Positions past a token's own are
+// computed from rows other tokens of the batch have written and never read.
 template <int HD, int G>
 __global__ __launch_bounds__(kScoreThreads) void k_attn_scores_rows(attn_rows_args a) {
-    __shared__ float qs[G * HD];
-    const uint32_t kvh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
-    const wm_batch_tok tk = a.tok[t];
-    const uint32_t n = tk.pos + 1;
-    const uint32_t p0 = blockIdx.x * kScoreThreads;
-    if (p0 >= n) return;  // the whole block lies past this token's context
-    const float *qsrc = a.q + (uint64_t)t * a.n_heads * HD + (uint64_t)kvh * G * HD;
-    for (uint32_t i = tid; i < (uint32_t)(G * HD); i += kScoreThreads) qs[i] = qsrc[i];
+    __shared__ __align__(16) float qs[kScoreTok][G][HD];
+    const wm_attn_item it = a.sc_items[blockIdx.x];
+    if (it.nt == 0) return;
+    const uint32_t kvh = it.unit, tid = threadIdx.x;
+    for (uint32_t i = tid; i < (uint32_t)(kScoreTok * G * HD); i += kScoreThreads) {
+        const uint32_t tt = i / (G * HD), r = i % (G * HD);
+        qs[tt][r / HD][r % HD] =
+            tt < it.nt ? a.q[(uint64_t)(it.t0 + tt) * a.n_heads * HD + (uint64_t)kvh * G * HD + r] : 0.0f;
+    }
     __syncthreads();
-    const uint32_t p = p0 + tid;
-    if (p >= n) return;
+    const uint32_t p = it.p0 + tid;
+    if (p >= it.p1) return;
+    const wm_batch_tok tk = a.tok[it.t0];  // every token of the item: the same cache
     const uint64_t lay = (uint64_t)a.layer * tk.max_seq;
     const int8_t *kp = tk.k + (lay + p) * a.kv_dim + kvh * HD;
-    int4 raw[HD / 16];
-#pragma unroll
-    for (int b = 0; b < HD / 16; b++) raw[b] = *reinterpret_cast<const int4 *>(kp + b * 16);
     const float kscale = tk.ks[lay + p];
-    float s[G];
+    float s[kScoreTok][G];
 #pragma unroll
-    for (int h = 0; h < G; h++) s[h] = 0.0f;
+    for (int tt = 0; tt < kScoreTok; tt++)
 #pragma unroll
+        for (int g = 0; g < G; g++) s[tt][g] = 0.0f;
+#pragma unroll 1
     for (int b = 0; b < HD / 16; b++) {
-        const uint32_t wd[4] = {(uint32_t)raw[b].x, (uint32_t)raw[b].y, (uint32_t)raw[b].z,
-                                (uint32_t)raw[b].w};
+        const int4 raw = *reinterpret_cast<const int4 *>(kp + b * 16);
+        float kd[16];
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-            const float kd = (float)(int8_t)(wd[e >> 2] >> (8 * (e & 3))) * kscale;  // read_into
-#pragma unroll
-            for (int h = 0; h < G; h++) s[h] = s[h] + qs[h * HD + b * 16 + e] * kd;
+            const uint32_t wd = e < 4 ? (uint32_t)raw.x : e < 8 ? (uint32_t)raw.y : e < 12 ? (uint32_t)raw.z : (uint32_t)raw.w;
+            kd[e] = (float)(int8_t)(wd >> (8 * (e & 3))) * kscale;  // read_into
         }
-    }
-    float *dst = a.scores + ((uint64_t)t * a.n_heads + kvh * G) * a.score_stride + p;
 #pragma unroll
-    for (int h = 0; h < G; h++) dst[(uint64_t)h * a.score_stride] = s[h] * a.scale;
+        for (int tt = 0; tt < kScoreTok; tt++)
+#pragma unroll
+            for (int g = 0; g < G; g++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) s[tt][g] = s[tt][g] + qs[tt][g][b * 16 + e] * kd[e];
+    }
+#pragma unroll
+    for (int tt = 0; tt < kScoreTok; tt++)
+        if ((uint32_t)tt < it.nt) {
+            float *dst = a.scores + ((uint64_t)(it.t0 + tt) * a.n_heads + kvh * G) * a.score_stride + p;
+#pragma unroll
+            for (int g = 0; g < G; g++) dst[(uint64_t)g * a.score_stride] = s[tt][g] * a.scale;
+        }
 }
 
 // out[t][h][d] = Σ_p w_h[p] * v_p[d] in position order (cached_forward.rs:
-// 417-449; v_p[d] = q8 * scale, read_into) for one token and G query heads
-// of one KV head, on the softmax weights k_attn_softmax_rows left in place
-// of the scores.  Thread d runs the G chains: the rows share every V value,
-// and G independent chains per thread keep the adder busy.  Tiles of kSvPos
-// positions go through LDS: V (the next tile's loads in flight while the
-// current one is summed) and the rows' weights.
+// 417-449; v_p[d] = q8 * scale, read_into) for kSvTok tokens of one sequence
+// (item blockIdx.x) and G query heads of one KV head, on the exps
+// k_attn_softmax_rows left in place of the scores times each row's 1/sum.
+// Thread d runs the kSvTok * G chains: they share every V value.  Tiles of
+// kSvPos positions go through LDS: the V codes and scales (the next tile's
+// loads in flight while the current one is summed) and the rows' weights; a
+// token's positions past its own get weight 0 (exact: a zero term leaves
+// the sum unchanged), so every tile runs in full.
 constexpr uint32_t kSvPos = 64;
 constexpr uint32_t kSvHeads = 4;  // query heads per workgroup (of one KV head's group)
+constexpr uint32_t kSvTok = 1;    // tokens per V item
+constexpr uint32_t kAttnTiles = 64;  // tiles of kSvPos positions per row (contexts <= 4096)
 
 // The loads of V tile rows p0 .. p0 + kSvPos - 1 (indices clamped to n - 1):
 // thread tid takes 16-byte pieces tid, tid + HD, tid + 2HD, tid + 3HD
-// (piece = row * HD/16 + column), in named registers (an array would be kept
-// in scratch memory), threads below kSvPos one scale each.
+// (piece = row * HD/16 + column) and their rows' scales, in named registers
+// (an array would be kept in scratch memory).
 struct sv_regs {
     int4 v0, v1, v2, v3;
-    float s;
+    float s0, s1, s2, s3;
 };
+template <int HD>
+__device__ __forceinline__ uint32_t sv_row(uint32_t i) { return (i * HD + threadIdx.x) / (HD / 16); }
+template <int HD>
+__device__ __forceinline__ uint32_t sv_col(uint32_t i) { return ((i * HD + threadIdx.x) % (HD / 16)) * 16; }
 template <int HD>
 __device__ __forceinline__ void sv_fetch(sv_regs &r, const int8_t *vg, const float *vsg, uint32_t kv_dim,
                                          uint32_t p0, uint32_t n) {
     static_assert(kSvPos * HD / 16 == 4 * HD, "four pieces per thread");
-    const uint32_t tid = threadIdx.x;
     const auto piece = [&](uint32_t i) {
-        const uint32_t pc = i * HD + tid, row = pc / (HD / 16), col = (pc % (HD / 16)) * 16;
-        return *reinterpret_cast<const int4 *>(vg + (uint64_t)min(p0 + row, n - 1) * kv_dim + col);
+        return *reinterpret_cast<const int4 *>(vg + (uint64_t)min(p0 + sv_row<HD>(i), n - 1) * kv_dim +
+                                               sv_col<HD>(i));
     };
     r.v0 = piece(0);
     r.v1 = piece(1);
     r.v2 = piece(2);
     r.v3 = piece(3);
-    if (tid < kSvPos) r.s = vsg[min(p0 + tid, n - 1)];
+    r.s0 = vsg[min(p0 + sv_row<HD>(0), n - 1)];
+    r.s1 = vsg[min(p0 + sv_row<HD>(1), n - 1)];
+    r.s2 = vsg[min(p0 + sv_row<HD>(2), n - 1)];
+    r.s3 = vsg[min(p0 + sv_row<HD>(3), n - 1)];
 }
+// the tile's codes into vt[row][col] as loaded, and each row's scale into vst[row]
 template <int HD>
-__device__ __forceinline__ void sv_stage(const sv_regs &r, int8_t *vt, float *vst) {
-    const uint32_t tid = threadIdx.x;
-    *reinterpret_cast<int4 *>(vt + tid * 16) = r.v0;
-    *reinterpret_cast<int4 *>(vt + (HD + tid) * 16) = r.v1;
-    *reinterpret_cast<int4 *>(vt + (2 * HD + tid) * 16) = r.v2;
-    *reinterpret_cast<int4 *>(vt + (3 * HD + tid) * 16) = r.v3;
-    if (tid < kSvPos) vst[tid] = r.s;
+__device__ __forceinline__ void sv_stage(const sv_regs &r, int8_t (*vt)[HD], float *vst) {
+    *reinterpret_cast<int4 *>(&vt[sv_row<HD>(0)][sv_col<HD>(0)]) = r.v0;
+    *reinterpret_cast<int4 *>(&vt[sv_row<HD>(1)][sv_col<HD>(1)]) = r.v1;
+    *reinterpret_cast<int4 *>(&vt[sv_row<HD>(2)][sv_col<HD>(2)]) = r.v2;
+    *reinterpret_cast<int4 *>(&vt[sv_row<HD>(3)][sv_col<HD>(3)]) = r.v3;
+    if (sv_col<HD>(0) == 0) vst[sv_row<HD>(0)] = r.s0;
+    if (sv_col<HD>(1) == 0) vst[sv_row<HD>(1)] = r.s1;
+    if (sv_col<HD>(2) == 0) vst[sv_row<HD>(2)] = r.s2;
+    if (sv_col<HD>(3) == 0) vst[sv_row<HD>(3)] = r.s3;
 }
 
-// Softmax of one (token, head) row of scores in place (attention.rs:45-73):
-// max, exp (glibc expf), the exact sequential sum by the workgroup (thread t
-// owning the m = ceil(n / 256) consecutive terms from t*m), * (1/sum) (left
-// unnormalised when the sum is not positive); a row whose maximum is not
+// Softmax of one (token, head) row of scores (attention.rs:45-73): max, exp
+// (glibc expf) in place, the exact sequential sum by the workgroup (thread t
+// owning the m = ceil(n / 256) consecutive terms from t*m), and the row's
+// scale 1/sum (1 when the sum is not positive: the reference leaves the row
+// unnormalised); the V pass forms each weight as exp * scale, the same f32
+// product the reference's `*= inv` makes.  Tiles of kSvPos positions whose
+// exps are all exactly zero are flagged dead: their weights are zero, and a
+// zero term leaves each of the V pass's sums unchanged (those sums start at
+// +0 and can never be -0), so it skips them.  A row whose maximum is not
 // finite becomes all zero (its output is then 0).
 constexpr uint32_t kSmThreads = 256;
 __global__ __launch_bounds__(kSmThreads) void k_attn_softmax_rows(attn_rows_args a) {
     constexpr int M = 16;  // terms per thread: n <= 4096
     __shared__ uint64_t exp_tab[32];
     __shared__ float red[kSmThreads / 64];
+    __shared__ uint8_t tile_live[kAttnTiles];
     __shared__ wm::seq_block_scratch seq_scratch;
     const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const uint32_t n = a.tok[t].pos + 1;
-    float *w = a.scores + ((uint64_t)t * a.n_heads + h) * a.score_stride;
+    const uint32_t n = a.tok[t].pos + 1, n_tiles = (n + kSvPos - 1) / kSvPos;
+    const uint64_t row = (uint64_t)t * a.n_heads + h;
+    float *w = a.scores + row * a.score_stride;
+    uint8_t *live = a.live + row * kAttnTiles;
     if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
+    if (tid < kAttnTiles) tile_live[tid] = 0;
     const uint32_t mm = (n + kSmThreads - 1) / kSmThreads, k0 = tid * mm;
     float v[M];
     float m = -INFINITY;
@@ -526,6 +568,8 @@ __global__ __launch_bounds__(kSmThreads) void k_attn_softmax_rows(attn_rows_args
 #pragma unroll
         for (int j = 0; j < M; j++)
             if ((uint32_t)j < mm && k0 + j < n) w[k0 + j] = 0.0f;
+        if (tid < n_tiles) live[tid] = 0;
+        if (tid == 0) a.row_scale[row] = 0.0f;
         return;
     }
 #pragma unroll
@@ -533,65 +577,89 @@ __global__ __launch_bounds__(kSmThreads) void k_attn_softmax_rows(attn_rows_args
         const bool in = (uint32_t)j < mm && k0 + j < n;
         v[j] = in ? wm::expf_glibc(v[j] - mx, exp_tab) : 0.0f;
         if (in) w[k0 + j] = v[j];
+        if (in && v[j] != 0.0f) tile_live[(k0 + j) / kSvPos] = 1;
     }
-    __syncthreads();  // the exps in memory for the sum's walk
+    __syncthreads();  // the exps in memory for the sum's walk, the tile flags in LDS
+    if (tid < n_tiles) live[tid] = tile_live[tid];
     const float sum = wm::seq_sum_block_owned<M, kSmThreads>(v, n, w, &seq_scratch);
-    if (sum > 0.0f) {
-        const float inv = 1.0f / sum;
-#pragma unroll
-        for (int j = 0; j < M; j++)
-            if ((uint32_t)j < mm && k0 + j < n) w[k0 + j] = v[j] * inv;
-    }
+    if (tid == 0) a.row_scale[row] = sum > 0.0f ? 1.0f / sum : 1.0f;
 }
 
-// G: query heads per workgroup, HG: per KV head (blockIdx.x = kv head * HG/G + part)
+// G: query heads per workgroup, HG: per KV head (item unit = kv head * HG/G + part)
 template <int HD, int G, int HG>
 __global__ __launch_bounds__(HD) void k_attn_sv_rows(attn_rows_args a) {
-    __shared__ __align__(16) int8_t vt[kSvPos * HD];
+    constexpr uint32_t C = kSvTok * G;  // chains per thread: c = token * G + head
+    __shared__ __align__(16) int8_t vt[kSvPos][HD];
     __shared__ __align__(16) float vst[kSvPos];
-    __shared__ __align__(16) float wt[G][kSvPos];
-    const uint32_t kvh = blockIdx.x / (HG / G), h0 = blockIdx.x * G;  // first query head
-    const uint32_t t = blockIdx.y, tid = threadIdx.x;
-    const wm_batch_tok tk = a.tok[t];
-    const uint32_t n = tk.pos + 1;
-    float *rows = a.scores + ((uint64_t)t * a.n_heads + h0) * a.score_stride;  // row g at g * stride
-    // the chains, a tile at a time
+    __shared__ __align__(16) float wt[C][kSvPos];
+    __shared__ uint64_t live_mask;
+    const wm_attn_item it = a.sv_items[blockIdx.x];
+    if (it.nt == 0) return;
+    const uint32_t kvh = it.unit / (HG / G), h0 = it.unit * G;  // first query head
+    const uint32_t tid = threadIdx.x;
+    const wm_batch_tok tk = a.tok[it.t0];  // the item's tokens share this cache
+    const uint32_t n = it.p1;              // the last token's context: every tile any chain needs
+    uint32_t nt_ctx[kSvTok];
+#pragma unroll
+    for (uint32_t tt = 0; tt < kSvTok; tt++) nt_ctx[tt] = tt < it.nt ? a.tok[it.t0 + tt].pos + 1 : 0u;
+    // the tiles where any chain has a non-zero exp, in position order
+    const uint32_t n_tiles = (n + kSvPos - 1) / kSvPos;
+    if (tid < 64) {
+        bool lv = false;
+        if (tid < n_tiles)
+#pragma unroll
+            for (uint32_t c = 0; c < C; c++)
+                if (c / G < it.nt && tid * kSvPos < nt_ctx[c / G])
+                    lv = lv || a.live[((uint64_t)(it.t0 + c / G) * a.n_heads + h0 + c % G) * kAttnTiles + tid];
+        const uint64_t mask = __ballot(lv);
+        if (tid == 0) live_mask = mask;
+    }
     const uint64_t lay = (uint64_t)a.layer * tk.max_seq;
     const int8_t *vg = tk.v + lay * a.kv_dim + kvh * HD;
     const float *vsg = tk.vs + lay;
-    sv_regs pr{};
-    sv_fetch<HD>(pr, vg, vsg, a.kv_dim, 0u, n);
-    float acc[G];
+    float acc[C];
 #pragma unroll
-    for (int g = 0; g < G; g++) acc[g] = 0.0f;
-    for (uint32_t p0 = 0; p0 < n; p0 += kSvPos) {
+    for (uint32_t c = 0; c < C; c++) acc[c] = 0.0f;
+    __syncthreads();
+    uint64_t mask = live_mask;
+    sv_regs pr{};
+    if (mask) sv_fetch<HD>(pr, vg, vsg, a.kv_dim, (uint32_t)__builtin_ctzll(mask) * kSvPos, n);
+    while (mask) {
+        const uint32_t p0 = (uint32_t)__builtin_ctzll(mask) * kSvPos;
+        mask &= mask - 1;
         __syncthreads();  // the previous tile is summed
         sv_stage<HD>(pr, vt, vst);
-        for (uint32_t e = tid; e < G * kSvPos; e += HD) {
-            const uint32_t g = e / kSvPos, q = e % kSvPos;
-            wt[g][q] = p0 + q < n ? rows[(uint64_t)g * a.score_stride + p0 + q] : 0.0f;
+        for (uint32_t e = tid; e < C * kSvPos; e += HD) {
+            const uint32_t c = e / kSvPos, q = e % kSvPos, tt = c / G, p = p0 + q;
+            float w = 0.0f;
+            if (tt < it.nt && p < nt_ctx[tt]) {
+                const uint64_t row = (uint64_t)(it.t0 + tt) * a.n_heads + h0 + c % G;
+                w = a.scores[row * a.score_stride + p] * a.row_scale[row];  // exp * (1/sum)
+            }
+            wt[c][q] = w;
         }
         __syncthreads();
-        if (p0 + kSvPos < n) sv_fetch<HD>(pr, vg, vsg, a.kv_dim, p0 + kSvPos, n);
-        const uint32_t tn = min(kSvPos, n - p0);
-        if (tn == kSvPos) {
-#pragma unroll 4
-            for (uint32_t q = 0; q < kSvPos; q++) {
-                const float vd = (float)vt[q * HD + tid] * vst[q];  // read_into: q8 * scale
+        if (mask) sv_fetch<HD>(pr, vg, vsg, a.kv_dim, (uint32_t)__builtin_ctzll(mask) * kSvPos, n);
+#pragma unroll 2
+        for (uint32_t q = 0; q < kSvPos; q += 4) {
+            const float4 sc = *reinterpret_cast<const float4 *>(&vst[q]);
+            // read_into: q8 * scale
+            const float v0 = (float)vt[q][tid] * sc.x, v1 = (float)vt[q + 1][tid] * sc.y;
+            const float v2 = (float)vt[q + 2][tid] * sc.z, v3 = (float)vt[q + 3][tid] * sc.w;
 #pragma unroll
-                for (int g = 0; g < G; g++) acc[g] = acc[g] + wt[g][q] * vd;
-            }
-        } else {
-            for (uint32_t q = 0; q < tn; q++) {
-                const float vd = (float)vt[q * HD + tid] * vst[q];
-#pragma unroll
-                for (int g = 0; g < G; g++) acc[g] = acc[g] + wt[g][q] * vd;
+            for (uint32_t c = 0; c < C; c++) {
+                const float4 w4 = *reinterpret_cast<const float4 *>(&wt[c][q]);
+                acc[c] = acc[c] + w4.x * v0;
+                acc[c] = acc[c] + w4.y * v1;
+                acc[c] = acc[c] + w4.z * v2;
+                acc[c] = acc[c] + w4.w * v3;
             }
         }
     }
-    float *out = a.out + (uint64_t)t * a.n_heads * HD + (uint64_t)h0 * HD + tid;
 #pragma unroll
-    for (int g = 0; g < G; g++) out[g * HD] = acc[g];
+    for (uint32_t c = 0; c < C; c++)
+        if (c / G < it.nt)
+            a.out[(uint64_t)(it.t0 + c / G) * a.n_heads * HD + (uint64_t)(h0 + c % G) * HD + tid] = acc[c];
 }
 
 }  // namespace
@@ -670,17 +738,101 @@ bool wm_attn_rows_supported(uint32_t head_dim, uint32_t group) {
            (group == 1 || group == 2 || group == 4 || group == 8);
 }
 
-size_t wm_attn_rows_scores_bytes(uint32_t m, uint32_t n_heads, uint32_t n_max) {
-    return (size_t)m * n_heads * ((n_max + 3u) & ~3u) * sizeof(float);
+// scores [m][n_heads][stride] | row scales [m][n_heads] | live tiles [m][n_heads][kAttnTiles]
+static size_t attn_scores_part(uint32_t m, uint32_t n_heads, uint32_t n_max) {
+    return ((size_t)m * n_heads * ((n_max + 3u) & ~3u) * sizeof(float) + 255) & ~(size_t)255;
+}
+static size_t attn_scale_part(uint32_t m, uint32_t n_heads) {
+    return ((size_t)m * n_heads * sizeof(float) + 255) & ~(size_t)255;
+}
+static size_t attn_live_part(uint32_t m, uint32_t n_heads) {
+    return ((size_t)m * n_heads * kAttnTiles + 255) & ~(size_t)255;
+}
+size_t wm_attn_rows_scores_bytes(uint32_t m, uint32_t n_heads, uint32_t n_max, uint32_t n_items) {
+    return attn_scores_part(m, n_heads, n_max) + attn_scale_part(m, n_heads) +
+           attn_live_part(m, n_heads) + (size_t)n_items * sizeof(wm_attn_item);
+}
+wm_attn_item *wm_attn_rows_items(float *scores, uint32_t m, uint32_t n_heads, uint32_t n_max) {
+    return reinterpret_cast<wm_attn_item *>(reinterpret_cast<uint8_t *>(scores) +
+                                            attn_scores_part(m, n_heads, n_max) +
+                                            attn_scale_part(m, n_heads) + attn_live_part(m, n_heads));
+}
+
+uint32_t wm_attn_rows_sv_parts(uint32_t group) { return group < kSvHeads ? 1u : group / kSvHeads; }
+
+// Items in launch order.  Workgroup i runs on XCD i % 8, so the items of one
+// (sequence, unit) group, which read the same K or V rows, are all given
+// the same i % 8 and share that XCD's L2; groups go to the least-loaded XCD,
+// largest first, and the shorter lists are padded with empty items.
+static void attn_place(std::vector<std::vector<wm_attn_item>> &groups, std::vector<uint64_t> &work,
+                       std::vector<wm_attn_item> &out) {
+    constexpr uint32_t kXcds = 8;
+    std::vector<uint32_t> order(groups.size());
+    for (uint32_t i = 0; i < order.size(); i++) order[i] = i;
+    std::sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) { return work[x] > work[y]; });
+    std::vector<std::vector<wm_attn_item>> lists(kXcds);
+    uint64_t load[kXcds] = {};
+    for (uint32_t g : order) {
+        uint32_t x = 0;
+        for (uint32_t k = 1; k < kXcds; k++)
+            if (load[k] < load[x]) x = k;
+        load[x] += work[g];
+        lists[x].insert(lists[x].end(), groups[g].begin(), groups[g].end());
+    }
+    size_t len = 0;
+    for (auto &l : lists) len = std::max(len, l.size());
+    out.assign(len * kXcds, wm_attn_item{0, 0, 0, 0, 0, 0});
+    for (uint32_t x = 0; x < kXcds; x++)
+        for (size_t k = 0; k < lists[x].size(); k++) out[k * kXcds + x] = lists[x][k];
+}
+
+void wm_attn_rows_plan(const wm_batch_tok *tok, uint32_t m, uint32_t sc_units, uint32_t sv_units,
+                       std::vector<wm_attn_item> &sc, std::vector<wm_attn_item> &sv) {
+    std::vector<std::vector<wm_attn_item>> sc_groups, sv_groups;
+    std::vector<uint64_t> sc_work, sv_work;
+    for (uint32_t t = 0; t < m;) {
+        uint32_t e = t + 1;  // the sequence's tokens: same cache, consecutive positions
+        while (e < m && tok[e].k == tok[t].k && tok[e].pos == tok[e - 1].pos + 1) e++;
+        for (uint32_t u = 0; u < sc_units; u++) {
+            std::vector<wm_attn_item> g;
+            uint64_t w = 0;
+            for (uint32_t b = t; b < e; b += kScoreTok) {
+                const uint32_t nt = std::min<uint32_t>(kScoreTok, e - b), p1 = tok[b + nt - 1].pos + 1;
+                for (uint32_t p0 = 0; p0 < p1; p0 += kScoreThreads) g.push_back({b, nt, p0, p1, u, 0});
+                w += (uint64_t)nt * p1;
+            }
+            sc_groups.push_back(g);
+            sc_work.push_back(w);
+        }
+        for (uint32_t u = 0; u < sv_units; u++) {
+            std::vector<wm_attn_item> g;
+            uint64_t w = 0;
+            for (uint32_t b = t; b < e; b += kSvTok) {
+                const uint32_t nt = std::min<uint32_t>(kSvTok, e - b), p1 = tok[b + nt - 1].pos + 1;
+                g.push_back({b, nt, 0, p1, u, 0});
+                w += (uint64_t)nt * p1;
+            }
+            sv_groups.push_back(g);
+            sv_work.push_back(w);
+        }
+        t = e;
+    }
+    attn_place(sc_groups, sc_work, sc);
+    attn_place(sv_groups, sv_work, sv);
 }
 
 void wm_launch_attn_rows(const float *q, const wm_batch_tok *tok, uint32_t m, uint32_t n_max,
                          uint32_t layer, uint32_t n_kv_heads, uint32_t head_dim, uint32_t group,
-                         float scale, float *scores, float *out, hipStream_t s) {
+                         float scale, float *scores, float *out, uint32_t n_sc, uint32_t n_sv,
+                         hipStream_t s) {
     const uint32_t n_heads = n_kv_heads * group;
+    uint8_t *base = reinterpret_cast<uint8_t *>(scores);
+    float *row_scale = reinterpret_cast<float *>(base + attn_scores_part(m, n_heads, n_max));
+    uint8_t *live = base + attn_scores_part(m, n_heads, n_max) + attn_scale_part(m, n_heads);
+    const wm_attn_item *items = wm_attn_rows_items(scores, m, n_heads, n_max);
     attn_rows_args a{q, tok, scores, out, layer, n_kv_heads * head_dim, n_heads,
-                     (n_max + 3u) & ~3u, n_max, scale};
-    const dim3 sgrid((n_max + kScoreThreads - 1) / kScoreThreads, n_kv_heads, m);
+                     (n_max + 3u) & ~3u, n_max, scale, row_scale, live, items, items + n_sc};
+    const dim3 sgrid(n_sc);
 #define WM_SCORES_CASE(HD, G)                                                                  \
     if (head_dim == HD && group == G)                                                          \
         hipLaunchKernelGGL((k_attn_scores_rows<HD, G>), sgrid, dim3(kScoreThreads), 0, s, a);
@@ -691,7 +843,7 @@ void wm_launch_attn_rows(const float *q, const wm_batch_tok *tok, uint32_t m, ui
 #define WM_SV_CASE(HD, G)                                                                      \
     if (head_dim == HD && group == G)                                                          \
         hipLaunchKernelGGL((k_attn_sv_rows<HD, (G < kSvHeads ? G : kSvHeads), G>),             \
-                           dim3(n_kv_heads * (G < kSvHeads ? 1 : G / kSvHeads), m), dim3(HD), 0, s, a);
+                           dim3(n_sv), dim3(HD), 0, s, a);
     WM_SV_CASE(128, 1) WM_SV_CASE(128, 2) WM_SV_CASE(128, 4) WM_SV_CASE(128, 8)
     WM_SV_CASE(64, 1) WM_SV_CASE(64, 2) WM_SV_CASE(64, 4) WM_SV_CASE(64, 8)
 #undef WM_SV_CASE

@@ -448,7 +448,12 @@ wm_status batch_forward_dev(wm_model *m, wm_kv_cache *const *caches, uint32_t n_
     }
     hipStream_t s = ctx->stream;
     WM_HIP(ctx, hipSetDevice(m->device));
-    const size_t sc_bytes = wm_attn_rows_scores_bytes(M, c.n_heads, n_max);
+    std::vector<wm_attn_item> sc_items, sv_items;
+    wm_attn_rows_plan(tok.data(), M, c.n_kv_heads, c.n_kv_heads * wm_attn_rows_sv_parts(group),
+                      sc_items, sv_items);
+    const uint32_t n_sc = (uint32_t)sc_items.size(), n_sv = (uint32_t)sv_items.size();
+    sc_items.insert(sc_items.end(), sv_items.begin(), sv_items.end());
+    const size_t sc_bytes = wm_attn_rows_scores_bytes(M, c.n_heads, n_max, n_sc + n_sv);
     if (sc_bytes > m->b_scores_bytes) {
         WM_HIP(ctx, hipStreamSynchronize(s));
         if (m->b_scores) WM_HIP(ctx, hipFree(m->b_scores));
@@ -458,6 +463,8 @@ wm_status batch_forward_dev(wm_model *m, wm_kv_cache *const *caches, uint32_t n_
         m->b_scores_bytes = sc_bytes;
     }
     WM_HIP(ctx, hipMemcpyAsync(m->b_tok, tok.data(), M * sizeof(wm_batch_tok), hipMemcpyHostToDevice, s));
+    WM_HIP(ctx, hipMemcpyAsync(wm_attn_rows_items(m->b_scores, M, c.n_heads, n_max), sc_items.data(),
+                               sc_items.size() * sizeof(wm_attn_item), hipMemcpyHostToDevice, s));
     WM_HIP(ctx, hipMemcpyAsync(m->b_ids, tokens, M * 4, hipMemcpyHostToDevice, s));
 
     const uint32_t E = c.n_embd, F = c.n_ff, KV = m->kv_dim, QKV = E + 2 * KV;
@@ -479,7 +486,7 @@ wm_status batch_forward_dev(wm_model *m, wm_kv_cache *const *caches, uint32_t n_
         wm_launch_qkv_rows(m->b_yqkv, QKV, m->rope_cos, m->rope_sin, m->b_tok, M, l, E, KV,
                            c.head_dim, c.n_rot, m->b_q, s);
         wm_launch_attn_rows(m->b_q, m->b_tok, M, n_max, l, c.n_kv_heads, c.head_dim, group, scale,
-                            m->b_scores, m->b_attn, s);
+                            m->b_scores, m->b_attn, n_sc, n_sv, s);
         nr = wm_norm_rows{m->b_attn, E, nullptr, 0, nullptr, 0, L.attn_sub_norm, E, c.rms_eps,
                           m->b_act, m_pad, m->b_meta, nullptr, 0, nullptr, 0};
         if (!wm_launch_rmsnorm_rows(nr, M, s)) return rows_unsupported(ctx);

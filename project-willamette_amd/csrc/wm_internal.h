@@ -528,8 +528,26 @@ void wm_launch_qkv_rows(const float *y, uint32_t ldy, const float *rope_cos, con
                         hipStream_t s);
 // Causal GQA attention of every token of a batch over its own sequence cache.
 bool wm_attn_rows_supported(uint32_t head_dim, uint32_t group);
-size_t wm_attn_rows_scores_bytes(uint32_t m, uint32_t n_heads, uint32_t n_max);
+// Work items of the batch attention, one per workgroup: tokens t0 .. t0+nt-1
+// of one sequence (nt = 0: nothing to do), positions [p0, p1) (scores) or
+// every position below p1 (V), KV head (scores) or KV-head part (V) `unit`.
+struct wm_attn_item {
+    uint32_t t0, nt, p0, p1, unit, pad;
+};
+// From the step's tokens (host copy; a sequence's tokens are consecutive):
+// scores items per (sequence, KV head, 8 tokens, 256 positions) and V items
+// per (sequence, KV-head part, token), ordered so that every item of one
+// (sequence, unit) runs on the same XCD.
+void wm_attn_rows_plan(const wm_batch_tok *tok, uint32_t m, uint32_t sc_units, uint32_t sv_units,
+                       std::vector<wm_attn_item> &sc, std::vector<wm_attn_item> &sv);
+// V-kernel units per KV head for a query group size
+uint32_t wm_attn_rows_sv_parts(uint32_t group);
+// Device workspace of one step: scores, row scales, live-tile flags and the
+// n_items work items (wm_attn_rows_items: where the items go).
+size_t wm_attn_rows_scores_bytes(uint32_t m, uint32_t n_heads, uint32_t n_max, uint32_t n_items);
+wm_attn_item *wm_attn_rows_items(float *scores, uint32_t m, uint32_t n_heads, uint32_t n_max);
 void wm_launch_attn_rows(const float *q, const wm_batch_tok *tok, uint32_t m, uint32_t n_max,
                          uint32_t layer, uint32_t n_kv_heads, uint32_t head_dim, uint32_t group,
-                         float scale, float *scores, float *out, hipStream_t s);
+                         float scale, float *scores, float *out, uint32_t n_sc, uint32_t n_sv,
+                         hipStream_t s);
 void wm_launch_debug_seq_sum(const float *a, uint32_t n, float *out, hipStream_t s);
