@@ -542,6 +542,7 @@ __global__ __launch_bounds__(kSmThreads) void k_attn_softmax_rows(attn_rows_args
     __shared__ uint64_t exp_tab[32];
     __shared__ float red[kSmThreads / 64];
     __shared__ uint8_t tile_live[kAttnTiles];
+    __shared__ float ex[M * kSmThreads];  // the exps, for the sum's walk
     __shared__ wm::seq_block_scratch seq_scratch;
     const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const uint32_t n = a.tok[t].pos + 1, n_tiles = (n + kSvPos - 1) / kSvPos;
@@ -576,12 +577,15 @@ __global__ __launch_bounds__(kSmThreads) void k_attn_softmax_rows(attn_rows_args
     for (int j = 0; j < M; j++) {
         const bool in = (uint32_t)j < mm && k0 + j < n;
         v[j] = in ? wm::expf_glibc(v[j] - mx, exp_tab) : 0.0f;
-        if (in) w[k0 + j] = v[j];
+        if (in) {
+            w[k0 + j] = v[j];
+            ex[k0 + j] = v[j];
+        }
         if (in && v[j] != 0.0f) tile_live[(k0 + j) / kSvPos] = 1;
     }
-    __syncthreads();  // the exps in memory for the sum's walk, the tile flags in LDS
+    wm_sync_lds();  // the exps and the tile flags in LDS (the global stores need not wait)
     if (tid < n_tiles) live[tid] = tile_live[tid];
-    const float sum = wm::seq_sum_block_owned<M, kSmThreads>(v, n, w, &seq_scratch);
+    const float sum = wm::seq_sum_block_owned<M, kSmThreads>(v, n, ex, &seq_scratch);
     if (tid == 0) a.row_scale[row] = sum > 0.0f ? 1.0f / sum : 1.0f;
 }
 

@@ -225,6 +225,7 @@ struct seq_block_scratch {
     uint32_t pi[kSeqMaxWaves][kSeqWaveRecords];   // wave's increments before it
     float val[kSeqMaxWaves][kSeqWaveRecords];     // the term
     int first[64];  // walk: wave + 1 at the chunk lane of its first record, else 0
+    float2 step[64];  // walk: (segment increment, break term) of each step of a chunk
     float out;
 };
 
@@ -491,19 +492,28 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
                 const float hi = seg ? (e_ok ? ldexpf(16777214.0f, e0 - 23) : -1.0f)
                                      : __int_as_float(0x7F800000);
                 const float s0 = s;
+                // The steps' (A, V) through LDS, read back by every lane as
+                // broadcasts: the chain then runs on vector registers with
+                // no lane reads between its adds.  Steps past `here` add
+                // +0 twice, which changes no running sum (never -0).
+                sc->step[lane] = make_float2(A, v1);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 // s as a per-lane value, so the compiler keeps the chain on
                 // the vector unit (all lanes hold the same number)
                 float sv;
                 asm volatile("v_mov_b32 %0, %1" : "=v"(sv) : "v"(s));
                 float s_in = 0.0f;
-                for (int g = 0; g < here; g += 8) {
+                for (int g = 0; g < here; g += 16) {
+                    float2 st[16];
 #pragma unroll
-                    for (int u = 0; u < 8; u++) {
-                        const int i = g + u;
-                        const float Ai = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(A), i));
-                        const float Vi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v1), i));
-                        s_in = (int)lane == i ? sv : s_in;
-                        sv = (sv + Ai) + Vi;
+                    for (int u = 0; u < 16; u++) st[u] = sc->step[g + u];
+                    const int lg = (int)lane - g;  // this lane's step within the block
+#pragma unroll
+                    for (int u = 0; u < 16; u++) {
+                        s_in = lg == u ? sv : s_in;
+                        sv = (sv + st[u].x) + st[u].y;
                     }
                 }
                 s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sv)));
