@@ -3,6 +3,7 @@
     python rocprof_summary.py stats <run_kernel_stats.csv> [--top N]
     python rocprof_summary.py traffic --fetch DIR --write DIR --kernel NAME
                                       --copy-bytes B [--record JSON --source FILE]
+    python rocprof_summary.py mfma --pmc DIR --trace run_kernel_trace.csv
 
 `stats` prints the per-kernel table of a --kernel-trace --stats run.
 
@@ -187,6 +188,38 @@ def traffic_roles(args) -> str:
     return "\n".join(lines)
 
 
+def mfma(args) -> str:
+    """Per kernel of a --pmc SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_VALU_MFMA_BUSY_CYCLES
+    pass, with durations from a --kernel-trace run of the same command: int8
+    MFMA operations per dispatch (the counter counts units of 512), the MFMA
+    busy cycles per SIMD (the counter sums over every SIMD), and their share
+    of the kernel's duration at the given clock."""
+    rows = counter_rows(args.pmc)
+    ops, busy = {}, {}
+    for r in rows:
+        k = short(r["Kernel_Name"])
+        if r["Counter_Name"] == "SQ_INSTS_VALU_MFMA_MOPS_I8":
+            ops.setdefault(k, []).append(float(r["Counter_Value"]) * 512)
+        elif r["Counter_Name"] == "SQ_VALU_MFMA_BUSY_CYCLES":
+            busy.setdefault(k, []).append(float(r["Counter_Value"]))
+    dur = {}
+    for r in csv.DictReader(open(args.trace)):
+        dur.setdefault(short(r["Kernel_Name"]), []).append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    out = [f"{'kernel':24s} {'dispatches':>10s} {'GOP/disp':>9s} {'us/disp':>8s} {'TOP/s':>8s} "
+           f"{'of peak':>8s} {'MFMA busy/SIMD us':>18s} {'busy share':>10s}"]
+    for k in sorted(ops):
+        if not any(ops[k]):
+            continue
+        o = sum(ops[k]) / len(ops[k])
+        b = sum(busy.get(k, [0])) / max(len(busy.get(k, [1])), 1) / args.simds / (args.clock_ghz * 1e3)
+        d = sum(dur.get(k, [0])) / max(len(dur.get(k, [1])), 1)
+        tops = o / (d * 1e-6) / 1e12 if d else 0.0
+        out.append(f"{k[:24]:24s} {len(ops[k]):10d} {o / 1e9:9.2f} {d:8.2f} {tops:8.1f} "
+                   f"{tops / args.peak_tops:8.3f} {b:18.2f} {b / d if d else 0:10.3f}")
+    return "\n".join(out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -214,7 +247,16 @@ def main():
     t.add_argument("--copy-bytes", type=int, default=1 << 30)
     t.add_argument("--record")
     t.add_argument("--source")
+    m = sub.add_parser("mfma")
+    m.add_argument("--pmc", required=True, help="run directory of the counter pass")
+    m.add_argument("--trace", required=True, help="run_kernel_trace.csv of the same command")
+    m.add_argument("--simds", type=int, default=1024)
+    m.add_argument("--clock-ghz", type=float, default=2.4)
+    m.add_argument("--peak-tops", type=float, default=5000.0)
     args = ap.parse_args()
+    if args.cmd == "mfma":
+        print(mfma(args))
+        return
     if args.cmd == "stats":
         print(stats(args.csv, args.top))
     elif args.cmd == "roles":
