@@ -43,13 +43,19 @@ COMMON = [
 ]
 
 
+# The batched GEMM keeps its MFMA accumulators in VGPRs: with the compiler's
+# default (AGPRs) its wave-split-K loop copies them between the two register
+# files on every chunk.
+PER_FILE = {"k_batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.name + ".o")
-    cmd = [HIPCC, *COMMON]
+    cmd = [HIPCC, *COMMON, *PER_FILE.get(src.name, [])]
     if src.suffix == ".hip":
         cmd += ["-x", "hip"]
     cmd += ["-c", str(src), "-o", str(obj)]

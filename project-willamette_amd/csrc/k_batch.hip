@@ -37,10 +37,11 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 //                contiguously);
 //   D: lane l holds rows 4*seg .. 4*seg+3 of token r.
 // Σ_k (t_k + 1)·a_k - Σ_k a_k = Σ_k t_k·a_k is exact in i32 for any k order.
-// Activations and weights go through LDS in blocks of kGemmKB chunks,
-// double-buffered (direct global->LDS loads of the next block run while the
-// waves compute the current one), so each activation byte is read from L2
-// once per four groups, and each B fragment read from LDS feeds four MFMAs.
+// Activations and weights go through LDS in blocks of kGemmKB chunks, in a
+// ring of ST blocks: ST - 1 blocks of direct global->LDS loads are in flight
+// while the waves compute the oldest one.  Each activation byte is read
+// from L2 once per NG groups, and each B fragment read from LDS feeds four
+// MFMAs.  Launches with few workgroups use k_i2s_gemm_kw below instead.
 struct gemm_args {
     wm_gemm_desc d[WM_GEMM_MAX_DESC];
     uint32_t group_end[WM_GEMM_MAX_DESC];
@@ -68,18 +69,37 @@ __device__ __forceinline__ v4i expand_codes(uint32_t w) {
 
 constexpr uint32_t kGemmKB = 4;  // chunks per LDS block
 constexpr uint32_t kGemmActChunk = WM_GEMM_TILE_TOKENS * 64;  // bytes of a chunk's activation tile
-// LDS of a workgroup over NG 64-row groups: two blocks of kGemmKB chunks
-// (activations, then the groups' weights), later the output tile
+// LDS of a workgroup over NG 64-row groups: a ring of ST blocks of kGemmKB
+// chunks (activations, then the groups' weights), later the output tile
 template <int NG>
 constexpr uint32_t gemm_block_bytes() { return kGemmKB * (kGemmActChunk + NG * 1024u); }
 template <int NG>
 constexpr uint32_t gemm_out_stride() { return NG * 64u + 4u; }  // floats per token row of the output tile
-template <int NG>
+template <int NG, int ST>
 constexpr size_t gemm_lds_bytes() {
-    return 2 * gemm_block_bytes<NG>() > (size_t)WM_GEMM_TILE_TOKENS * gemm_out_stride<NG>() * 4
-               ? 2 * gemm_block_bytes<NG>()
+    return (size_t)ST * gemm_block_bytes<NG>() > (size_t)WM_GEMM_TILE_TOKENS * gemm_out_stride<NG>() * 4
+               ? (size_t)ST * gemm_block_bytes<NG>()
                : (size_t)WM_GEMM_TILE_TOKENS * gemm_out_stride<NG>() * 4;
 }
+
+// s_waitcnt vmcnt(N), the other counters left alone (gfx9 encoding: vmcnt
+// in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+template <uint32_t N>
+__device__ __forceinline__ void gemm_vm_wait() {
+    static_assert(N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((int)((N & 15u) | ((N >> 4) << 14) | (7u << 4) | (15u << 8)));
+}
+// wait until at most `blocks` blocks of this wave's loads, PER loads each,
+// are still in flight (loads complete in issue order)
+template <uint32_t PER>
+__device__ __forceinline__ void gemm_wait_blocks(uint32_t blocks) {
+    if (blocks == 0) gemm_vm_wait<0>();
+    else if (blocks == 1) gemm_vm_wait<PER>();
+    else if (blocks == 2) gemm_vm_wait<2 * PER>();
+    else if (blocks == 3) gemm_vm_wait<3 * PER>();
+    else gemm_vm_wait<4 * PER>();
+}
+constexpr int kGemmMaxStages = 6;  // gemm_wait_blocks covers up to 4 blocks ahead of the one waited for
 
 // 16-byte slot of (token t, segment g) in a chunk's activation tile in LDS:
 // the segment is XOR-swizzled by bits 3:2 of the token, so that the 16 lanes
@@ -113,21 +133,24 @@ __device__ __forceinline__ gemm_group gemm_group_of(const gemm_args &a, uint32_t
 // NG 64-row groups per workgroup of four waves: wave w works on group
 // w / (4 / NG) and on TPW = NG token tiles of 16 (NG = 4: one group and all
 // 64 tokens per wave; NG = 1: the workgroup's one group, 16 tokens per wave).
-template <int NG>
+// ST: blocks in the LDS ring.
+template <int NG, int ST>
 __global__ __launch_bounds__(256) void k_i2s_gemm(gemm_args a) {
+    static_assert(ST >= 2 && ST <= kGemmMaxStages, "ring size");
     constexpr uint32_t WPG = 4 / NG, TPW = 4 / WPG;  // waves per group, token tiles per wave
     constexpr uint32_t kBlock = gemm_block_bytes<NG>(), kWChunk = NG * 1024u;
     constexpr uint32_t kOutStride = gemm_out_stride<NG>();
-    extern __shared__ __align__(16) uint8_t gl[];  // [2] blocks (activations, weights), then the output tile
+    extern __shared__ __align__(16) uint8_t gl[];  // [ST] blocks (activations, weights), then the output tile
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6)), lane = tid & 63;
     const uint32_t r16 = lane & 15, seg = lane >> 4;
     const uint32_t q = wave / WPG, s0 = (wave % WPG) * TPW;  // this wave's group and first token tile
     const gemm_group G = gemm_group_of(a, blockIdx.x * NG + q);
     const uint32_t n0 = blockIdx.y * WM_GEMM_TILE_TOKENS;
+    const uint32_t c0 = 0, c1 = a.n_chunks;  // the chunks [c0, c1)
     // Both operands reach LDS by direct global->LDS loads (global_load_lds:
     // lane l of a wave writes 16 bytes at the wave's LDS base + 16 l), a
-    // block of kGemmKB chunks at a time, double-buffered.  Per chunk:
+    // block of kGemmKB chunks at a time.  Per chunk:
     //   activations: wave w fills slots 64 w .. 64 w + 63 of the 256-slot
     //     tile; slot p holds token p / 4, segment (p % 4) ^ bits 3:2 of the
     //     token (gemm_act_slot);
@@ -140,12 +163,13 @@ __global__ __launch_bounds__(256) void k_i2s_gemm(gemm_args a) {
     const uint32_t g_act = (p_act & 3u) ^ ((t_act >> 2) & 3u);
     const uint8_t *asrc = a.act + (uint64_t)(n0 + t_act) * 64 + g_act * 16;
     const uint64_t cstride = (uint64_t)a.m_pad * 64;
-    const uint32_t nc = a.n_chunks, nblocks = (nc + kGemmKB - 1) / kGemmKB;
+    const uint32_t nblocks = (c1 - c0 + kGemmKB - 1) / kGemmKB;
 #define WM_GEMM_ISSUE(BLK, BUF)                                                                  \
     do {                                                                                         \
         uint8_t *blk_ = gl + (BUF) * kBlock;                                                     \
         _Pragma("unroll") for (uint32_t kb = 0; kb < kGemmKB; kb++) {                            \
-            const uint32_t c = min((BLK) * kGemmKB + kb, nc - 1); /* past the end: last chunk */ \
+            /* past the range: its last chunk again, never read */                               \
+            const uint32_t c = min(c0 + (BLK) * kGemmKB + kb, c1 - 1);                           \
             __builtin_amdgcn_global_load_lds(asrc + c * cstride,                                 \
                                              blk_ + kb * kGemmActChunk + wave * 1024, 16, 0, 0); \
             if (wave < NG)                                                                       \
@@ -165,40 +189,58 @@ __global__ __launch_bounds__(256) void k_i2s_gemm(gemm_args a) {
 #pragma unroll
     for (uint32_t s = 0; s < TPW; s++) b_off[s] = gemm_act_slot((s0 + s) * 16 + r16, seg) * 16;
     const uint32_t a_off = kGemmKB * kGemmActChunk + q * 1024 + r16 * 16 + seg * 4;
-    WM_GEMM_ISSUE(0u, 0u);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    // blocks 0 .. ST - 2 in flight before the loop; block b + ST - 1 goes out
+    // once every wave has finished block b - 1, whose slot it takes
+#pragma unroll
+    for (uint32_t b = 0; b + 1 < (uint32_t)ST; b++)
+        if (b < nblocks) WM_GEMM_ISSUE(b, b);
+    uint32_t slot = 0;  // b % ST
     for (uint32_t b = 0; b < nblocks; b++) {
-        const bool more = b + 1 < nblocks;
-        if (more) WM_GEMM_ISSUE(b + 1, (b + 1) & 1);
-        const uint8_t *blk = gl + (b & 1) * kBlock;
-        const uint32_t kbn = min(kGemmKB, nc - b * kGemmKB);
+        // this wave's loads of block b: the blocks issued after it may stay in flight
+        const uint32_t ahead = min((uint32_t)ST - 2, nblocks - 1 - b);
+        if (wave < NG) gemm_wait_blocks<2 * kGemmKB>(ahead);
+        else gemm_wait_blocks<kGemmKB>(ahead);
+        // everyone's loads of block b, and block b - 1 fully read.  A bare
+        // barrier: __syncthreads()' release fence would wait for every load
+        // in flight (vmcnt(0)), the later blocks' included.
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (b + ST - 1 < nblocks) WM_GEMM_ISSUE(b + ST - 1, slot == 0 ? ST - 1 : slot - 1);
+        const uint8_t *blk = gl + slot * kBlock;
+        slot = slot + 1 == (uint32_t)ST ? 0u : slot + 1;
+        const uint32_t kbn = min(kGemmKB, c1 - c0 - b * kGemmKB);
+        // The block's fragments first, then its MFMAs.  A chunk past the
+        // range (a copy of the last one) gets zero codes, which add nothing:
+        // no branch around the MFMAs, so the sums stay in their registers.
+        v4i bv[kGemmKB][TPW];
+        uint32_t wv[kGemmKB][4];
 #pragma unroll
         for (uint32_t kb = 0; kb < kGemmKB; kb++) {
-            if (kb < kbn) {
-                v4i bv[TPW];
 #pragma unroll
-                for (uint32_t s = 0; s < TPW; s++)
-                    bv[s] = *reinterpret_cast<const v4i *>(blk + kb * kGemmActChunk + b_off[s]);
+            for (uint32_t s = 0; s < TPW; s++)
+                bv[kb][s] = *reinterpret_cast<const v4i *>(blk + kb * kGemmActChunk + b_off[s]);
 #pragma unroll
-                for (int rt = 0; rt < 4; rt++) {
-                    const uint32_t wv =
-                        *reinterpret_cast<const uint32_t *>(blk + a_off + kb * kWChunk + rt * 256);
-                    const v4i av = expand_codes(wv);
-#pragma unroll
-                    for (uint32_t s = 0; s < TPW; s++)
-                        acc[rt][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[s], acc[rt][s], 0, 0, 0);
-                }
+            for (int rt = 0; rt < 4; rt++) {
+                const uint32_t w = *reinterpret_cast<const uint32_t *>(blk + a_off + kb * kWChunk + rt * 256);
+                wv[kb][rt] = kb < kbn ? w : 0u;
             }
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of block b + 1
-        __syncthreads();  // everyone's, and block b fully read
+#pragma unroll
+        for (uint32_t kb = 0; kb < kGemmKB; kb++) {
+#pragma unroll
+            for (int rt = 0; rt < 4; rt++) {
+                const v4i av = expand_codes(wv[kb][rt]);
+#pragma unroll
+                for (uint32_t s = 0; s < TPW; s++)
+                    acc[rt][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[kb][s], acc[rt][s], 0, 0, 0);
+            }
+        }
     }
 #undef WM_GEMM_ISSUE
+    __syncthreads();  // every wave is done with the ring before the output tile reuses it
     // epilogue: y = (w_scale * act_scale) * (dot as f32)   (bitlinear_sse2.rs:327-339),
     // through LDS so that every token's outputs of a group leave as 256
     // contiguous bytes (the MFMA layout gives each lane 4 rows of one token)
-    float *ot = reinterpret_cast<float *>(gl);  // [64 tokens][kOutStride]; the K loop ended on a barrier
+    float *ot = reinterpret_cast<float *>(gl);  // [64 tokens][kOutStride]
 #pragma unroll
     for (uint32_t s = 0; s < TPW; s++) {
         const uint32_t tl = (s0 + s) * 16 + r16;
@@ -212,6 +254,197 @@ __global__ __launch_bounds__(256) void k_i2s_gemm(gemm_args a) {
             o.z = comb * (float)(acc[rt][s].z - mt.asum);
             o.w = comb * (float)(acc[rt][s].w - mt.asum);
             *reinterpret_cast<float4 *>(ot + tl * kOutStride + q * 64 + rt * 16 + seg * 4) = o;
+        }
+    }
+    __syncthreads();
+    // the 64 x 64 outputs of group g: 1024 float4, four per thread
+#pragma unroll
+    for (uint32_t g = 0; g < (uint32_t)NG; g++) {
+        const gemm_group Q = gemm_group_of(a, blockIdx.x * NG + g);
+        if (!Q.live) break;
+        const uint32_t base = Q.g * 64;
+        const bool vec = ((Q.row0 | a.ldy) & 3u) == 0;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; k++) {
+            const uint32_t idx = tid + k * 256, tl = idx >> 4, c4 = (idx & 15) * 4;
+            const uint32_t t = n0 + tl;
+            if (t >= a.m) continue;
+            const float4 o = *reinterpret_cast<const float4 *>(ot + tl * kOutStride + g * 64 + c4);
+            float *dst = a.y + (uint64_t)t * a.ldy + Q.row0 + base + c4;
+            if (vec && base + c4 + 4 <= Q.out_dim) {
+                *reinterpret_cast<float4 *>(dst) = o;
+            } else {
+                const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (base + c4 + r < Q.out_dim) dst[r] = ov[r];
+            }
+        }
+    }
+}
+
+// The same GEMM with the K dimension split over the four waves instead of
+// the tokens: every wave computes the workgroup's whole NG*64-row x 64-token
+// tile over chunks w, w + 4, w + 8, ..., so each code word is expanded once
+// per workgroup and feeds 4 MFMAs.  A wave's operands are its own: each
+// wave keeps a private ring of ST chunk slots in LDS, filled by direct
+// global->LDS loads, and needs no barrier in the K loop.  While the MFMAs of
+// chunk j run, chunk j + 1's fragments are read from LDS and chunk j + ST
+// is in flight.  The four partial tiles are added through LDS at the end
+// (exact: integers).
+template <int NG>
+constexpr uint32_t gemm_kw_slot_bytes() { return 4096u + NG * 1024u; }  // B tile, then NG groups' codes
+template <int NG, int ST>
+constexpr size_t gemm_kw_lds_bytes() {
+    constexpr size_t ring = (size_t)4 * ST * gemm_kw_slot_bytes<NG>();
+    constexpr size_t red = (size_t)4 * 16 * 64 * 16;  // one group's four partial tiles
+    constexpr size_t out = (size_t)WM_GEMM_TILE_TOKENS * gemm_out_stride<NG>() * 4;
+    return ring > red ? (ring > out ? ring : out) : (red > out ? red : out);
+}
+template <int NG, int ST>
+__global__ __launch_bounds__(256) void k_i2s_gemm_kw(gemm_args a) {
+    static_assert(ST >= 2 && ST <= kGemmMaxStages, "ring size");
+    constexpr uint32_t kOutStride = gemm_out_stride<NG>();
+    constexpr uint32_t kSlot = gemm_kw_slot_bytes<NG>();
+    constexpr uint32_t kLoads = 4 + NG;  // global->LDS loads per chunk and wave
+    extern __shared__ __align__(16) uint8_t gl[];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6)), lane = tid & 63;
+    const uint32_t r16 = lane & 15, seg = lane >> 4;
+    const uint32_t n0 = blockIdx.y * WM_GEMM_TILE_TOKENS;
+    const uint32_t nc = a.n_chunks;
+    uint8_t *ring = gl + wave * ST * kSlot;
+    // Loads, lane l: B tile s: LDS slot l of 16 bytes holds token 16 s + l / 4,
+    // segment (l % 4) ^ bits 3:2 of the token (gemm_act_slot, so that the
+    // MFMA reads below hit distinct banks); A of group g: row l's 16 bytes.
+    const uint32_t t_act = lane >> 2, g_act = (lane & 3u) ^ ((t_act >> 2) & 3u);
+    const uint8_t *bsrc = a.act + (uint64_t)(n0 + t_act) * 64 + g_act * 16;
+    const uint64_t cstride = (uint64_t)a.m_pad * 64;
+    const uint8_t *wsrc[NG];
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+        const gemm_group Gg = gemm_group_of(a, blockIdx.x * NG + g);
+        // a group past the last reads group 0's codes; its sums are discarded
+        wsrc[g] = (Gg.live ? Gg.w + (uint64_t)Gg.g * nc * 1024 : a.d[0].w) + lane * 16;
+    }
+    // this wave's chunk j is wave + 4 j; past the end: the last chunk again
+    // (its codes are zeroed before use)
+#define WM_KW_ISSUE(J, SLOT)                                                                      \
+    do {                                                                                          \
+        const uint32_t c_ = min(wave + 4u * (J), nc - 1);                                         \
+        uint8_t *d_ = ring + (SLOT) * kSlot;                                                      \
+        _Pragma("unroll") for (int s_ = 0; s_ < 4; s_++)                                          \
+            __builtin_amdgcn_global_load_lds(bsrc + c_ * cstride + s_ * 1024, d_ + s_ * 1024, 16, 0, 0); \
+        /* (the source through a local: an array element passed to the builtin                   \
+           makes the host pass drop the kernel's launch stub) */                                  \
+        _Pragma("unroll") for (int g_ = 0; g_ < NG; g_++) {                                       \
+            const uint8_t *w_ = wsrc[g_] + (uint64_t)c_ * 1024;                                   \
+            __builtin_amdgcn_global_load_lds(w_, d_ + 4096 + g_ * 1024, 16, 0, 0);                \
+        }                                                                                         \
+    } while (0)
+    // this lane's fragments in a slot: B of token tile s (token 16 s + r16,
+    // segment seg), A of group g, row tile rt (row 16 rt + r16, dword seg)
+    const uint32_t b_off = gemm_act_slot(r16, seg) * 16;
+    const uint32_t a_off = 4096u + r16 * 16 + seg * 4;
+#define WM_KW_READ(SLOT, BV, AV)                                                                  \
+    do {                                                                                          \
+        const uint8_t *q_ = ring + (SLOT) * kSlot;                                                \
+        _Pragma("unroll") for (int s_ = 0; s_ < 4; s_++)                                          \
+            BV[s_] = *reinterpret_cast<const v4i *>(q_ + s_ * 1024 + b_off);                      \
+        _Pragma("unroll") for (int g_ = 0; g_ < NG; g_++)                                         \
+            _Pragma("unroll") for (int rt_ = 0; rt_ < 4; rt_++)                                   \
+                AV[g_][rt_] = *reinterpret_cast<const uint32_t *>(q_ + a_off + g_ * 1024 + rt_ * 256); \
+    } while (0)
+    v4i acc[NG][4][4];
+#pragma unroll
+    for (int g = 0; g < NG; g++)
+#pragma unroll
+        for (int rt = 0; rt < 4; rt++)
+#pragma unroll
+            for (int s = 0; s < 4; s++) acc[g][rt][s] = v4i{0, 0, 0, 0};
+    const uint32_t J = (nc + 3) / 4;  // steps (the waves with fewer chunks zero their last codes)
+    // chunks 0 .. ST - 1 in flight, chunk 0 read
+#pragma unroll
+    for (int u = 0; u < ST; u++)
+        if ((uint32_t)u < J) WM_KW_ISSUE((uint32_t)u, (uint32_t)u);
+    if (J > 1) gemm_wait_blocks<kLoads>(min((uint32_t)ST - 1, J - 1));
+    else gemm_vm_wait<0>();
+    // two register sets, used alternately (no copies between steps)
+    v4i b0[4], b1[4];
+    uint32_t a0[NG][4], a1[NG][4];
+    WM_KW_READ(0u, b0, a0);
+    uint32_t slot = 0;  // j % ST
+#define WM_KW_STEP(JJ, BC, AC, BN, AN)                                                            \
+    do {                                                                                          \
+        const uint32_t j_ = (JJ);                                                                 \
+        const uint32_t nslot_ = slot + 1 == (uint32_t)ST ? 0u : slot + 1;                         \
+        /* chunk j + 1 has landed when at most the chunks issued after it are in                 \
+           flight: j + 2 .. min(j + ST - 1, J - 1).  Past the last chunk the read                \
+           is of a stale slot, never used. */                                                     \
+        gemm_wait_blocks<kLoads>(j_ + 1 < J ? min((uint32_t)ST - 2, J - 2 - j_) : 0u);            \
+        asm volatile("" ::: "memory");                                                            \
+        WM_KW_READ(nslot_, BN, AN);                                                               \
+        __builtin_amdgcn_sched_barrier(0); /* the reads go out before this chunk's MFMAs */       \
+        const bool live_ = wave + 4u * j_ < nc;                                                   \
+        _Pragma("unroll") for (int g = 0; g < NG; g++)                                            \
+            _Pragma("unroll") for (int rt = 0; rt < 4; rt++) {                                    \
+                const v4i av = expand_codes(live_ ? AC[g][rt] : 0u);                              \
+                _Pragma("unroll") for (int s = 0; s < 4; s++)                                     \
+                    acc[g][rt][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, BC[s], acc[g][rt][s], 0, 0, 0); \
+            }                                                                                     \
+        /* slot j is free once its fragments are in registers (the MFMAs above                   \
+           have them); chunk j + ST takes it.  The wait is for chunk j + 1's reads               \
+           too, which had this chunk's MFMAs to land. */                                          \
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                        \
+        if (j_ + ST < J) WM_KW_ISSUE(j_ + ST, slot);                                              \
+        slot = nslot_;                                                                            \
+    } while (0)
+    // an even number of steps: a step past J has zero codes and adds nothing
+    // (no branch around the MFMAs, so the sums stay in place)
+    for (uint32_t j = 0; j < J; j += 2) {
+        WM_KW_STEP(j, b0, a0, b1, a1);
+        WM_KW_STEP(j + 1, b1, a1, b0, a0);
+    }
+#undef WM_KW_STEP
+#undef WM_KW_ISSUE
+#undef WM_KW_READ
+    __syncthreads();  // every wave is done with its ring
+    // the four waves' tiles through LDS, one group at a time; wave w then
+    // owns row tile w
+    v4i *red = reinterpret_cast<v4i *>(gl);  // [4 waves][4 rt][4 s][64 lanes]
+    v4i sum[NG][4];
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+        if (g > 0) __syncthreads();  // the previous group's sums are read
+#pragma unroll
+        for (int rt = 0; rt < 4; rt++)
+#pragma unroll
+            for (int s = 0; s < 4; s++) red[((wave * 4 + rt) * 4 + s) * 64 + lane] = acc[g][rt][s];
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            v4i t = red[((0 * 4 + wave) * 4 + s) * 64 + lane];
+#pragma unroll
+            for (uint32_t v = 1; v < 4; v++) t += red[((v * 4 + wave) * 4 + s) * 64 + lane];
+            sum[g][s] = t;
+        }
+    }
+    __syncthreads();  // the output tile reuses the reduction area
+    // epilogue: y = (w_scale * act_scale) * (dot as f32)   (bitlinear_sse2.rs:327-339)
+    float *ot = reinterpret_cast<float *>(gl);  // [64 tokens][kOutStride]
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const uint32_t tl = (uint32_t)s * 16 + r16;
+        const wm_act_meta mt = a.meta[min(n0 + tl, a.m - 1)];
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            const float comb = gemm_group_of(a, blockIdx.x * NG + g).scale * mt.scale;
+            float4 o;
+            o.x = comb * (float)(sum[g][s].x - mt.asum);
+            o.y = comb * (float)(sum[g][s].y - mt.asum);
+            o.z = comb * (float)(sum[g][s].z - mt.asum);
+            o.w = comb * (float)(sum[g][s].w - mt.asum);
+            *reinterpret_cast<float4 *>(ot + tl * kOutStride + g * 64 + wave * 16 + seg * 4) = o;
         }
     }
     __syncthreads();
@@ -672,6 +905,32 @@ __global__ __launch_bounds__(HD) void k_attn_sv_rows(attn_rows_args a) {
 // launchers
 // ---------------------------------------------------------------------------
 
+namespace {
+constexpr uint32_t kGemmCus = 256;
+}  // namespace
+
+wm_gemm_plan wm_gemm_make_plan(uint32_t groups, uint32_t n_chunks, uint32_t m) {
+    (void)n_chunks;
+    wm_gemm_plan p;
+    p.tiles = (m + WM_GEMM_TILE_TOKENS - 1) / WM_GEMM_TILE_TOKENS;
+    // Up to two 64 x 64 output tiles per CU: the waves split K
+    // (k_i2s_gemm_kw, 3 chunks in flight per wave; two workgroups fit a
+    // CU's LDS).  More: the waves split the tokens of two groups per
+    // workgroup (k_i2s_gemm, double-buffered).  These were the faster
+    // choices in a sweep of both kernels, NG and ring depth over the
+    // BitNet-2B shapes at M = 257.
+    if (groups * p.tiles <= 2 * kGemmCus) {
+        p.kw = true;
+        p.ng = 1;
+        p.st = 3;
+    } else {  // more than 512 tiles: at least 256 workgroups of two groups
+        p.ng = 2;
+        p.st = 2;
+    }
+    p.gx = (groups + p.ng - 1) / p.ng;
+    return p;
+}
+
 void wm_launch_i2s_gemm(const wm_gemm_desc *d, int n_desc, uint32_t n_chunks, const uint8_t *act,
                         uint32_t m, uint32_t m_pad, const wm_act_meta *meta, float *y,
                         uint32_t ldy, hipStream_t s) {
@@ -691,17 +950,19 @@ void wm_launch_i2s_gemm(const wm_gemm_desc *d, int n_desc, uint32_t n_chunks, co
     a.meta = meta;
     a.y = y;
     a.ldy = ldy;
-    const uint32_t tiles = (m + WM_GEMM_TILE_TOKENS - 1) / WM_GEMM_TILE_TOKENS;
-    // groups per workgroup: four (each activation byte read from L2 once per
-    // four groups) when that still gives the chip about one workgroup per
-    // CU, else fewer, for more workgroups
-    const uint32_t cus = 256;
-    if ((groups + 3) / 4 * tiles >= cus)
-        hipLaunchKernelGGL(k_i2s_gemm<4>, dim3((groups + 3) / 4, tiles), dim3(256), gemm_lds_bytes<4>(), s, a);
-    else if ((groups + 1) / 2 * tiles >= cus / 2)
-        hipLaunchKernelGGL(k_i2s_gemm<2>, dim3((groups + 1) / 2, tiles), dim3(256), gemm_lds_bytes<2>(), s, a);
-    else
-        hipLaunchKernelGGL(k_i2s_gemm<1>, dim3(groups, tiles), dim3(256), gemm_lds_bytes<1>(), s, a);
+    const wm_gemm_plan p = wm_gemm_make_plan(groups, n_chunks, m);
+    const dim3 grid(p.gx, p.tiles);
+#define WM_GEMM_CASE(KW, NG, ST)                                                                 \
+    if (p.kw == KW && p.ng == NG && p.st == ST) {                                                \
+        if (KW)                                                                                  \
+            hipLaunchKernelGGL((k_i2s_gemm_kw<NG, ST>), grid, dim3(256), (gemm_kw_lds_bytes<NG, ST>()), s, a); \
+        else                                                                                     \
+            hipLaunchKernelGGL((k_i2s_gemm<NG, ST>), grid, dim3(256), (gemm_lds_bytes<NG, ST>()), s, a); \
+        return;                                                                                  \
+    }
+    WM_GEMM_CASE(true, 1, 3)
+    WM_GEMM_CASE(false, 2, 2)
+#undef WM_GEMM_CASE
 }
 
 void wm_launch_quantize_rows(const float *x, uint32_t ldx, uint32_t n, uint32_t m, uint32_t m_pad,

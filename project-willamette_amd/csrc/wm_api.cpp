@@ -1,4 +1,5 @@
 // C ABI: context, device buffers, tensors, BitLinear and Q6_K entry points.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -6,6 +7,8 @@
 #include <vector>
 
 #include "wm_internal.h"
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // ---------------------------------------------------------------------------
 // errors
@@ -280,7 +283,6 @@ struct mv_ws {
     int32_t *dot;
 };
 
-static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 static void run_matvec(wm_ctx *ctx, const wm_tensor *w, const float *d_x, float *d_y,
                        int32_t *d_dot, uint8_t *act, wm_act_meta *meta, int32_t *partial) {

@@ -502,6 +502,14 @@ struct wm_gemm_desc {
     uint32_t out_row0;  // first output column of this tensor in y
     float scale;        // per-tensor weight scale
 };
+// How a GEMM launch is laid out: which kernel (kw: the waves split K), NG
+// 64-row groups per workgroup, ST chunks or blocks in flight.
+struct wm_gemm_plan {
+    bool kw = false;
+    int ng = 1, st = 2;
+    uint32_t gx = 0, tiles = 0;  // grid: row-group sets x token tiles
+};
+wm_gemm_plan wm_gemm_make_plan(uint32_t groups, uint32_t n_chunks, uint32_t m);
 // y[t * ldy + out_row0 + r] = (scale * meta[t].scale) * (Σ_k code·act - meta[t].asum)
 void wm_launch_i2s_gemm(const wm_gemm_desc *d, int n_desc, uint32_t n_chunks, const uint8_t *act,
                         uint32_t m, uint32_t m_pad, const wm_act_meta *meta, float *y,

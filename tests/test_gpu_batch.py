@@ -33,8 +33,11 @@ def bits_equal(a, b):
 # batched BitLinear (one GEMM over m token rows)
 # --------------------------------------------------------------------------
 
+# up to 512 output tiles of 64 x 64: the kernel whose waves split K; more
+# (the last two): the kernel whose waves split the tokens
 MATMUL_SHAPES = [(128, 64, 1), (256, 100, 5), (2560, 640, 16), (2560, 2560, 63), (2560, 2560, 64),
-                 (2560, 2560, 65), (2560, 6912, 200), (6912, 2560, 37), (640, 65, 130)]
+                 (2560, 2560, 65), (2560, 6912, 200), (6912, 2560, 37), (640, 65, 130),
+                 (2560, 13824, 200), (1024, 13000, 150)]
 
 
 @pytest.mark.parametrize("in_dim,out_dim,m", MATMUL_SHAPES)
