@@ -19,6 +19,15 @@ const FLAGS: &[&str] = &[
     "--offload-arch=gfx950",
 ];
 
+/// Extra flags of single sources (as PER_FILE in build.py): the batched GEMM
+/// keeps its MFMA accumulators in VGPRs.
+fn per_file(name: &str) -> &'static [&'static str] {
+    match name {
+        "k_batch.hip" => &["-mllvm", "-amdgpu-mfma-vgpr-form"],
+        _ => &[],
+    }
+}
+
 fn main() {
     println!("cargo:rerun-if-env-changed=WILLAMETTE_HIP_LIB_DIR");
     println!("cargo:rerun-if-env-changed=HIPCC");
@@ -47,7 +56,8 @@ fn main() {
     for src in &sources {
         let obj = out.join(format!("{}.o", src.file_name().unwrap().to_string_lossy()));
         let mut cmd = Command::new(&hipcc);
-        cmd.args(FLAGS).arg("-I").arg(&include).arg("-I").arg(&csrc);
+        cmd.args(FLAGS).args(per_file(&src.file_name().unwrap().to_string_lossy()));
+        cmd.arg("-I").arg(&include).arg("-I").arg(&csrc);
         if src.extension().and_then(|e| e.to_str()) == Some("hip") {
             cmd.arg("-x").arg("hip");
         }
