@@ -477,7 +477,9 @@ __global__ __launch_bounds__(256) void k_i2s_gemm_kw(gemm_args a) {
 // ---------------------------------------------------------------------------
 // per-row absmax int8 (bitlinear_sse2.rs:285-304) into the GEMM layout
 // ---------------------------------------------------------------------------
-constexpr int kRowThreads = 1024;
+// 512 threads per row: two rows per CU (at up to 128 VGPRs a thread), so
+// that a batch of up to 512 rows runs in one round over the 256 CUs
+constexpr int kRowThreads = 512;
 
 __global__ __launch_bounds__(kRowThreads) void k_quantize_rows(const float *__restrict__ x,
                                                                uint32_t ldx, uint32_t n,
@@ -857,26 +859,46 @@ __global__ __launch_bounds__(HD) void k_attn_sv_rows(attn_rows_args a) {
     float acc[C];
 #pragma unroll
     for (uint32_t c = 0; c < C; c++) acc[c] = 0.0f;
+    // this thread's weight slots e = tid + k * HD of a tile: chain e / kSvPos,
+    // position e % kSvPos; the row's exps and its 1/sum
+    constexpr uint32_t WK = (C * kSvPos + HD - 1) / HD;
+    const float *wrow[WK];
+    float wscale[WK];
+    uint32_t wlim[WK];
+#pragma unroll
+    for (uint32_t k = 0; k < WK; k++) {
+        const uint32_t e = min(tid + k * HD, C * kSvPos - 1), c = e / kSvPos, tt = c / G;
+        const uint64_t row = (uint64_t)(it.t0 + min(tt, it.nt - 1)) * a.n_heads + h0 + c % G;
+        wrow[k] = a.scores + row * a.score_stride + e % kSvPos;
+        wscale[k] = a.row_scale[row];
+        // positions below this one count (none for a slot past the tile)
+        wlim[k] = tt < it.nt && tid + k * HD < C * kSvPos ? nt_ctx[tt] : 0u;
+    }
+    float wr[WK];  // the next tile's exps, loaded with its V codes
+    const auto wfetch = [&](uint32_t p0) {
+#pragma unroll
+        for (uint32_t k = 0; k < WK; k++)
+            wr[k] = p0 + (tid + k * HD) % kSvPos < wlim[k] ? wrow[k][p0] : 0.0f;
+    };
     __syncthreads();
     uint64_t mask = live_mask;
     sv_regs pr{};
-    if (mask) sv_fetch<HD>(pr, vg, vsg, a.kv_dim, (uint32_t)__builtin_ctzll(mask) * kSvPos, n);
+    if (mask) {
+        sv_fetch<HD>(pr, vg, vsg, a.kv_dim, (uint32_t)__builtin_ctzll(mask) * kSvPos, n);
+        wfetch((uint32_t)__builtin_ctzll(mask) * kSvPos);
+    }
     while (mask) {
-        const uint32_t p0 = (uint32_t)__builtin_ctzll(mask) * kSvPos;
         mask &= mask - 1;
         __syncthreads();  // the previous tile is summed
         sv_stage<HD>(pr, vt, vst);
-        for (uint32_t e = tid; e < C * kSvPos; e += HD) {
-            const uint32_t c = e / kSvPos, q = e % kSvPos, tt = c / G, p = p0 + q;
-            float w = 0.0f;
-            if (tt < it.nt && p < nt_ctx[tt]) {
-                const uint64_t row = (uint64_t)(it.t0 + tt) * a.n_heads + h0 + c % G;
-                w = a.scores[row * a.score_stride + p] * a.row_scale[row];  // exp * (1/sum)
-            }
-            wt[c][q] = w;
-        }
+#pragma unroll
+        for (uint32_t k = 0; k < WK; k++)
+            if (tid + k * HD < C * kSvPos) (&wt[0][0])[tid + k * HD] = wr[k] * wscale[k];  // exp * (1/sum)
         __syncthreads();
-        if (mask) sv_fetch<HD>(pr, vg, vsg, a.kv_dim, (uint32_t)__builtin_ctzll(mask) * kSvPos, n);
+        if (mask) {
+            sv_fetch<HD>(pr, vg, vsg, a.kv_dim, (uint32_t)__builtin_ctzll(mask) * kSvPos, n);
+            wfetch((uint32_t)__builtin_ctzll(mask) * kSvPos);
+        }
 #pragma unroll 2
         for (uint32_t q = 0; q < kSvPos; q += 4) {
             const float4 sc = *reinterpret_cast<const float4 *>(&vst[q]);
@@ -983,6 +1005,8 @@ bool wm_launch_rmsnorm_rows(const wm_norm_rows &a, uint32_t m, hipStream_t s) {
     switch (per) {
         WM_ROWS_CASE(1) WM_ROWS_CASE(2) WM_ROWS_CASE(3) WM_ROWS_CASE(4)
         WM_ROWS_CASE(5) WM_ROWS_CASE(6) WM_ROWS_CASE(7) WM_ROWS_CASE(8)
+        WM_ROWS_CASE(9) WM_ROWS_CASE(10) WM_ROWS_CASE(11) WM_ROWS_CASE(12)
+        WM_ROWS_CASE(13) WM_ROWS_CASE(14) WM_ROWS_CASE(15) WM_ROWS_CASE(16)
         default: break;
     }
 #undef WM_ROWS_CASE
