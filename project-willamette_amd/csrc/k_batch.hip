@@ -772,20 +772,23 @@ __device__ __forceinline__ void sv_stage(const sv_regs &r, int8_t (*vt)[HD], flo
 // +0 and can never be -0), so it skips them.  A row whose maximum is not
 // finite becomes all zero (its output is then 0).
 constexpr uint32_t kSmThreads = 256;
-__global__ __launch_bounds__(kSmThreads) void k_attn_softmax_rows(attn_rows_args a) {
-    constexpr int M = 16;  // terms per thread: n <= 4096
-    __shared__ uint64_t exp_tab[32];
-    __shared__ float red[kSmThreads / 64];
-    __shared__ uint8_t tile_live[kAttnTiles];
-    __shared__ float ex[M * kSmThreads];  // the exps, for the sum's walk
-    __shared__ wm::seq_block_scratch seq_scratch;
-    const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+constexpr int kSmMaxM = 16;  // terms per thread: n <= 4096
+struct softmax_lds {
+    uint64_t exp_tab[32];
+    float red[kSmThreads / 64];
+    uint8_t tile_live[kAttnTiles];
+    float ex[kSmMaxM * kSmThreads];  // the exps, for the sum's walk
+    wm::seq_block_scratch seq_scratch;
+};
+// One row with M >= ceil(n / kSmThreads) terms per thread (the per-term
+// work runs over M slots, so the kernel picks the smallest M of a few).
+template <int M>
+__device__ __forceinline__ void softmax_row(const attn_rows_args &a, softmax_lds &L, uint32_t h, uint32_t t) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const uint32_t n = a.tok[t].pos + 1, n_tiles = (n + kSvPos - 1) / kSvPos;
     const uint64_t row = (uint64_t)t * a.n_heads + h;
     float *w = a.scores + row * a.score_stride;
     uint8_t *live = a.live + row * kAttnTiles;
-    if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
-    if (tid < kAttnTiles) tile_live[tid] = 0;
     const uint32_t mm = (n + kSmThreads - 1) / kSmThreads, k0 = tid * mm;
     float v[M];
     float m = -INFINITY;
@@ -795,11 +798,11 @@ __global__ __launch_bounds__(kSmThreads) void k_attn_softmax_rows(attn_rows_args
         m = wm_max_nonan(m, v[j]);
     }
     m = wm_wave_max_nonan(m);
-    if (lane == 0) red[wid] = m;
+    if (lane == 0) L.red[wid] = m;
     __syncthreads();
-    float mx = red[0];
+    float mx = L.red[0];
 #pragma unroll
-    for (uint32_t i = 1; i < kSmThreads / 64; i++) mx = wm_max_nonan(mx, red[i]);
+    for (uint32_t i = 1; i < kSmThreads / 64; i++) mx = wm_max_nonan(mx, L.red[i]);
     if (!isfinite(mx)) {  // every weight becomes 0 (or the row held a NaN)
 #pragma unroll
         for (int j = 0; j < M; j++)
@@ -811,17 +814,28 @@ __global__ __launch_bounds__(kSmThreads) void k_attn_softmax_rows(attn_rows_args
 #pragma unroll
     for (int j = 0; j < M; j++) {
         const bool in = (uint32_t)j < mm && k0 + j < n;
-        v[j] = in ? wm::expf_glibc(v[j] - mx, exp_tab) : 0.0f;
+        v[j] = in ? wm::expf_glibc(v[j] - mx, L.exp_tab) : 0.0f;
         if (in) {
             w[k0 + j] = v[j];
-            ex[k0 + j] = v[j];
+            L.ex[k0 + j] = v[j];
         }
-        if (in && v[j] != 0.0f) tile_live[(k0 + j) / kSvPos] = 1;
+        if (in && v[j] != 0.0f) L.tile_live[(k0 + j) / kSvPos] = 1;
     }
     wm_sync_lds();  // the exps and the tile flags in LDS (the global stores need not wait)
-    if (tid < n_tiles) live[tid] = tile_live[tid];
-    const float sum = wm::seq_sum_block_owned<M, kSmThreads>(v, n, ex, &seq_scratch);
+    if (tid < n_tiles) live[tid] = L.tile_live[tid];
+    const float sum = wm::seq_sum_block_owned<M, kSmThreads>(v, n, L.ex, &L.seq_scratch);
     if (tid == 0) a.row_scale[row] = sum > 0.0f ? 1.0f / sum : 1.0f;
+}
+__global__ __launch_bounds__(kSmThreads) void k_attn_softmax_rows(attn_rows_args a) {
+    __shared__ softmax_lds L;
+    const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    if (tid < 32) L.exp_tab[tid] = wm::kExp2Tab[tid];
+    if (tid < kAttnTiles) L.tile_live[tid] = 0;
+    const uint32_t mm = (a.tok[t].pos + 1 + kSmThreads - 1) / kSmThreads;  // uniform
+    if (mm <= 4) softmax_row<4>(a, L, h, t);
+    else if (mm <= 8) softmax_row<8>(a, L, h, t);
+    else if (mm <= 12) softmax_row<12>(a, L, h, t);
+    else softmax_row<kSmMaxM>(a, L, h, t);
 }
 
 // G: query heads per workgroup, HG: per KV head (item unit = kv head * HG/G + part)
