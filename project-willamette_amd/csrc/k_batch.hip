@@ -967,7 +967,7 @@ wm_gemm_plan wm_gemm_make_plan(uint32_t groups, uint32_t n_chunks, uint32_t m) {
     return p;
 }
 
-void wm_launch_i2s_gemm(const wm_gemm_desc *d, int n_desc, uint32_t n_chunks, const uint8_t *act,
+bool wm_launch_i2s_gemm(const wm_gemm_desc *d, int n_desc, uint32_t n_chunks, const uint8_t *act,
                         uint32_t m, uint32_t m_pad, const wm_act_meta *meta, float *y,
                         uint32_t ldy, hipStream_t s) {
     gemm_args a{};
@@ -994,11 +994,12 @@ void wm_launch_i2s_gemm(const wm_gemm_desc *d, int n_desc, uint32_t n_chunks, co
             hipLaunchKernelGGL((k_i2s_gemm_kw<NG, ST>), grid, dim3(256), (gemm_kw_lds_bytes<NG, ST>()), s, a); \
         else                                                                                     \
             hipLaunchKernelGGL((k_i2s_gemm<NG, ST>), grid, dim3(256), (gemm_lds_bytes<NG, ST>()), s, a); \
-        return;                                                                                  \
+        return true;                                                                             \
     }
     WM_GEMM_CASE(true, 1, 3)
     WM_GEMM_CASE(false, 2, 2)
 #undef WM_GEMM_CASE
+    return false;  // a plan with no instantiation: nothing launched
 }
 
 void wm_launch_quantize_rows(const float *x, uint32_t ldx, uint32_t n, uint32_t m, uint32_t m_pad,

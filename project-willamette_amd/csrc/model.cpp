@@ -330,7 +330,7 @@ wm_status finish_step(wm_model *m, wm_kv_cache *kv, uint32_t pos, bool *failed) 
 constexpr uint32_t kBatchMaxTokens = 16384;
 
 wm_status rows_unsupported(wm_ctx *ctx) {
-    return wm_set_error(ctx, WM_E_SHAPE, "batch_forward: no row-norm kernel for this model shape");
+    return wm_set_error(ctx, WM_E_SHAPE, "batch_forward: no row-norm or GEMM kernel for this model shape");
 }
 
 // The ragged-batch kernels cover this model shape (else prompts are
@@ -482,7 +482,8 @@ wm_status batch_forward_dev(wm_model *m, wm_kv_cache *const *caches, uint32_t n_
         const wm_gemm_desc qkv[3] = {{L.q.w, L.q.n_groups, E, 0, L.q.scale},
                                      {L.k.w, L.k.n_groups, KV, E, L.k.scale},
                                      {L.v.w, L.v.n_groups, KV, E + KV, L.v.scale}};
-        wm_launch_i2s_gemm(qkv, 3, nce, m->b_act, M, m_pad, m->b_meta, m->b_yqkv, QKV, s);
+        if (!wm_launch_i2s_gemm(qkv, 3, nce, m->b_act, M, m_pad, m->b_meta, m->b_yqkv, QKV, s))
+            return rows_unsupported(ctx);
         wm_launch_qkv_rows(m->b_yqkv, QKV, m->rope_cos, m->rope_sin, m->b_tok, M, l, E, KV,
                            c.head_dim, c.n_rot, m->b_q, s);
         wm_launch_attn_rows(m->b_q, m->b_tok, M, n_max, l, c.n_kv_heads, c.head_dim, group, scale,
@@ -491,20 +492,23 @@ wm_status batch_forward_dev(wm_model *m, wm_kv_cache *const *caches, uint32_t n_
                           m->b_act, m_pad, m->b_meta, nullptr, 0, nullptr, 0};
         if (!wm_launch_rmsnorm_rows(nr, M, s)) return rows_unsupported(ctx);
         const wm_gemm_desc od = {L.o.w, L.o.n_groups, E, 0, L.o.scale};
-        wm_launch_i2s_gemm(&od, 1, nce, m->b_act, M, m_pad, m->b_meta, m->b_yo, E, s);
+        if (!wm_launch_i2s_gemm(&od, 1, nce, m->b_act, M, m_pad, m->b_meta, m->b_yo, E, s))
+            return rows_unsupported(ctx);
         // hidden += wo, ffn_norm, int8
         nr = wm_norm_rows{m->b_hidden, E, m->b_yo, E, nullptr, 0, L.ffn_norm, E, c.rms_eps,
                           m->b_act, m_pad, m->b_meta, nullptr, 0, nullptr, 0};
         if (!wm_launch_rmsnorm_rows(nr, M, s)) return rows_unsupported(ctx);
         const wm_gemm_desc gu[2] = {{L.gate.w, L.gate.n_groups, F, 0, L.gate.scale},
                                     {L.up.w, L.up.n_groups, F, F, L.up.scale}};
-        wm_launch_i2s_gemm(gu, 2, nce, m->b_act, M, m_pad, m->b_meta, m->b_ygu, 2 * F, s);
+        if (!wm_launch_i2s_gemm(gu, 2, nce, m->b_act, M, m_pad, m->b_meta, m->b_ygu, 2 * F, s))
+            return rows_unsupported(ctx);
         // relu^2(gate) * up, ffn_sub_norm, int8
         nr = wm_norm_rows{nullptr, 0, nullptr, 0, m->b_ygu, 2 * F, L.ffn_sub_norm, F, c.rms_eps,
                           m->b_act, m_pad, m->b_meta, nullptr, 0, nullptr, 0};
         if (!wm_launch_rmsnorm_rows(nr, M, s)) return rows_unsupported(ctx);
         const wm_gemm_desc dd = {L.down.w, L.down.n_groups, E, 0, L.down.scale};
-        wm_launch_i2s_gemm(&dd, 1, ncf, m->b_act, M, m_pad, m->b_meta, m->b_ydown, E, s);
+        if (!wm_launch_i2s_gemm(&dd, 1, ncf, m->b_act, M, m_pad, m->b_meta, m->b_ydown, E, s))
+            return rows_unsupported(ctx);
     }
     // hidden += down of the last layer, output_norm (f32)
     wm_norm_rows fin{m->b_hidden, E, m->b_ydown, E, nullptr, 0, m->output_norm, E, c.rms_eps,

@@ -472,8 +472,9 @@ wm_status wm_bitlinear_i2s_matmul_f32_dev(wm_ctx *ctx, const wm_tensor *w, const
     wm_launch_quantize_rows(d_x, (uint32_t)w->in_dim, (uint32_t)w->in_dim, m, m_pad, act, meta,
                             ctx->stream);
     wm_gemm_desc d{(const uint8_t *)w->d, w->n_groups, (uint32_t)w->out_dim, 0, w->scale};
-    wm_launch_i2s_gemm(&d, 1, w->n_chunks, act, m, m_pad, meta, d_y, (uint32_t)w->out_dim,
-                       ctx->stream);
+    if (!wm_launch_i2s_gemm(&d, 1, w->n_chunks, act, m, m_pad, meta, d_y, (uint32_t)w->out_dim,
+                            ctx->stream))
+        return wm_set_error(ctx, WM_E_SHAPE, "bitlinear matmul: no GEMM kernel for this shape");
     WM_HIP(ctx, hipGetLastError());
     return WM_OK;
 }

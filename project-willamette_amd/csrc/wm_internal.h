@@ -510,8 +510,9 @@ struct wm_gemm_plan {
     uint32_t gx = 0, tiles = 0;  // grid: row-group sets x token tiles
 };
 wm_gemm_plan wm_gemm_make_plan(uint32_t groups, uint32_t n_chunks, uint32_t m);
-// y[t * ldy + out_row0 + r] = (scale * meta[t].scale) * (Σ_k code·act - meta[t].asum)
-void wm_launch_i2s_gemm(const wm_gemm_desc *d, int n_desc, uint32_t n_chunks, const uint8_t *act,
+// y[t * ldy + out_row0 + r] = (scale * meta[t].scale) * (Σ_k code·act - meta[t].asum).
+// Returns false (and launches nothing) when the plan has no instantiation.
+bool wm_launch_i2s_gemm(const wm_gemm_desc *d, int n_desc, uint32_t n_chunks, const uint8_t *act,
                         uint32_t m, uint32_t m_pad, const wm_act_meta *meta, float *y,
                         uint32_t ldy, hipStream_t s);
 // Per-row absmax int8 of x[t * ldx + 0..n) into the GEMM layout + meta[t].
