@@ -646,11 +646,11 @@ constexpr int kSelectBlock = 1024;
 constexpr uint32_t kSelectCap = 2048;  // candidate rows held at once
 
 template <int CH>
-__global__ __launch_bounds__(kSelectBlock) void k_q6k_select(
+__device__ __forceinline__ void q6_select(
     const uint8_t *__restrict__ w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
     const float *__restrict__ hidden, float *__restrict__ logits, const float *__restrict__ bound,
     const float *__restrict__ wg_lb, const float *__restrict__ wg_ub, uint32_t n_wg,
-    uint32_t *__restrict__ argmax_out, wm_step_tail tail) {
+    uint32_t *__restrict__ argmax_out, const wm_step_tail &tail) {
     extern __shared__ float xs[];  // [16][n_blocks*16 + 4]
     __shared__ uint32_t wg_list[kBoundedMaxBlocks];
     __shared__ uint32_t cand[kSelectCap];
@@ -754,6 +754,215 @@ __global__ __launch_bounds__(kSelectBlock) void k_q6k_select(
         }
     }
 }
+template <int CH>
+__global__ __launch_bounds__(kSelectBlock) void k_q6k_select(
+    const uint8_t *__restrict__ w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
+    const float *__restrict__ hidden, float *__restrict__ logits, const float *__restrict__ bound,
+    const float *__restrict__ wg_lb, const float *__restrict__ wg_ub, uint32_t n_wg,
+    uint32_t *__restrict__ argmax_out, wm_step_tail tail) {
+    q6_select<CH>(w, n_blocks, n_rows, n_rowgroups, hidden, logits, bound, wg_lb, wg_ub, n_wg,
+                  argmax_out, tail);
+}
+
+// ---------------------------------------------------------------------------
+// the id-only lm-head of several hidden vectors at once (the ragged batch's
+// next tokens): one bounded pass reads the table once for up to
+// kMultiVec vectors, then one selection workgroup per vector
+// ---------------------------------------------------------------------------
+constexpr int kMultiVec = 4;
+struct q6_multi {
+    const float *hidden[kMultiVec];
+    uint8_t *prep[kMultiVec];  // each vector's fixed-point copy and header
+    float *approx[kMultiVec];  // [n_rows]: the bounded values, exact on rescored rows
+    float *bound[kMultiVec];   // [n_rows]
+    float *wg_lb[kMultiVec], *wg_ub[kMultiVec];  // [workgroups of the bounded pass]
+    uint32_t *argmax_out[kMultiVec];
+    int nv;
+};
+// vector v's entry of one of the arrays, by selects (no dynamic index into
+// the argument block)
+template <typename T>
+__device__ __forceinline__ T q6_pick(const T (&arr)[kMultiVec], uint32_t v) {
+    T r = arr[0];
+#pragma unroll
+    for (int i = 1; i < kMultiVec; i++) r = v == (uint32_t)i ? arr[i] : r;
+    return r;
+}
+
+__global__ __launch_bounds__(256) void k_q6k_xprep_multi(q6_multi m, uint32_t n_blocks) {
+    __shared__ float red[4];
+    __shared__ int redi[4];
+    const uint32_t v = blockIdx.x;
+    uint8_t *prep = q6_pick(m.prep, v);
+    const q6k_xhdr h = q6k_xprep_block(q6_pick(m.hidden, v), n_blocks, reinterpret_cast<q6k_xq *>(prep), red, redi);
+    if (threadIdx.x == 0) *reinterpret_cast<q6k_xhdr *>(prep + q6k_xq_bytes(n_blocks)) = h;
+}
+
+template <int CH>
+__global__ __launch_bounds__(kSelectBlock) void k_q6k_select_multi(
+    const uint8_t *__restrict__ w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
+    q6_multi m, uint32_t n_wg) {
+    const uint32_t v = blockIdx.x;
+    q6_select<CH>(w, n_blocks, n_rows, n_rowgroups, q6_pick(m.hidden, v), q6_pick(m.approx, v),
+                  q6_pick(m.bound, v), q6_pick(m.wg_lb, v), q6_pick(m.wg_ub, v), n_wg,
+                  q6_pick(m.argmax_out, v), wm_step_tail{});
+}
+
+// q6_bounded_accum for V vectors: each block's quants are unpacked once.
+template <int CH, int V>
+__device__ __forceinline__ void q6_bounded_accum_multi(const q6_lane_blocks<CH> &v, uint32_t b0,
+                                                       const q6k_xq *xq, uint32_t xq_stride,
+                                                       uint32_t p, float (&acc)[V]) {
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+        uint32_t U[4];
+        q6_unpack(v.w0[j], v.w1[j], v.w2[j], U);
+        const float d = __half2float(__ushort_as_half((unsigned short)q6_d_bits(v, j)));
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            const int4 *xp = reinterpret_cast<const int4 *>(xq + k * xq_stride + (b0 + j) * 16 + p);
+            const int4 h4 = xp[0], l4 = xp[1], c4 = xp[2];
+            const int xh[4] = {h4.x, h4.y, h4.z, h4.w}, xl[4] = {l4.x, l4.y, l4.z, l4.w},
+                      xc[4] = {c4.x, c4.y, c4.z, c4.w};
+            int T = 0;
+#pragma unroll
+            for (int hn = 0; hn < 4; hn++) {
+                const int sc = (int)(int8_t)(v.scw[j] >> (8 * hn));
+                const int dh = __builtin_amdgcn_sdot4((int)U[hn], xh[hn], 0, true);
+                const int dl = __builtin_amdgcn_sdot4((int)U[hn], xl[hn], xc[hn], false);
+                const int I = (int)(((uint32_t)dh << 8) + (uint32_t)dl);  // a VALU result
+                T = mad_i24(sc, I, T);
+            }
+            acc[k] = __builtin_fmaf(d, (float)T, acc[k]);
+        }
+    }
+}
+
+// The bounded pass of k_q6k_bounded (pipelined) for V vectors at once: the
+// same batches, rows, bounds and per-workgroup maxima, per vector.
+template <int CH, int V>
+__global__ __launch_bounds__(kBoundedBlock) void k_q6k_bounded_multi(
+    const uint8_t *__restrict__ w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
+    const float *__restrict__ sigma, q6_multi m) {
+    extern __shared__ __align__(16) q6k_xq xq[];  // [V][n_blocks][16]
+    __shared__ float red[V][kBoundedBlock / 64], red2[V][kBoundedBlock / 64];
+    const uint32_t xq_stride = n_blocks * 16;
+    q6k_xhdr hdr[V];
+#pragma unroll
+    for (int k = 0; k < V; k++) {
+        const uint8_t *prep = m.prep[k];
+        for (uint32_t i = threadIdx.x; i < n_blocks * 16 * 3; i += blockDim.x)
+            reinterpret_cast<int4 *>(xq + k * xq_stride)[i] = reinterpret_cast<const int4 *>(prep)[i];
+        hdr[k] = *reinterpret_cast<const q6k_xhdr *>(prep + q6k_xq_bytes(n_blocks));
+    }
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t r = lane >> 4, p = lane & 15;
+    const q6_lane_offs o = q6_offs(n_blocks, r, p);
+    const uint32_t group_bytes = q6k_group_bytes(n_blocks);
+    const uint32_t g0 = (uint32_t)((uint64_t)blockIdx.x * n_rowgroups / gridDim.x);
+    const uint32_t g1 = (uint32_t)((uint64_t)(blockIdx.x + 1) * n_rowgroups / gridDim.x);
+    float lb_max[V], ub_max[V];
+#pragma unroll
+    for (int k = 0; k < V; k++) lb_max[k] = ub_max[k] = -INFINITY;
+    constexpr uint32_t kWaves = kBoundedBlock / 64;
+    auto epilogue = [&](uint32_t row, float (&acc)[V], float sg) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            float a_ = acc[k];
+#pragma unroll
+            for (int o2 = 1; o2 < 16; o2 <<= 1) a_ = a_ + __shfl_xor(a_, o2, 64);
+            if (p == 0 && row < n_rows) {
+                float a, eb;
+                if (hdr[k].ok) {
+                    a = ldexpf(a_, hdr[k].e);
+                    eb = hdr[k].bound_k * sg;
+                    eb = eb + eb * 0x1p-20f + fabsf(a) * 0x1p-22f + 1e-35f;
+                    if (!(hdr[k].mag_k * sg < 1e37f)) eb = INFINITY;
+                } else {
+                    a = NAN;
+                    eb = INFINITY;
+                }
+                m.approx[k][row] = a;
+                m.bound[k][row] = eb;
+                const float lb = a - eb, ub = a + eb;
+                if (lb > lb_max[k]) lb_max[k] = lb;
+                if (!(ub <= ub_max[k])) ub_max[k] = ub == ub ? ub : INFINITY;
+            }
+        }
+    };
+    const uint32_t nbat = n_blocks / CH;
+    const uint32_t G0 = g0 + wave;
+    if (G0 < g1) {
+        const uint32_t total = (g1 - G0 + kWaves - 1) / kWaves * nbat;
+        uint32_t G = G0, bi = 0;
+        uint32_t Gn = G0, bn = 0;
+        q6_lane_blocks<CH> A, B;
+        float sg = sigma[min(G0 * Q6K_GROUP_ROWS + r, n_rows - 1)], sg_n = sg;
+        q6_load_uniform<CH>(A, wm_rsrc(w + (uint64_t)G0 * group_bytes, group_bytes), 0, o);
+        float acc[V];
+#pragma unroll
+        for (int k = 0; k < V; k++) acc[k] = 0.0f;
+        auto issue = [&](q6_lane_blocks<CH> &nxt, bool live) __attribute__((always_inline)) {
+            if (++bn == nbat) {
+                bn = 0;
+                Gn += kWaves;
+            }
+            const uint32_t Gs = live ? Gn : G0;
+            sg_n = sigma[min(Gs * Q6K_GROUP_ROWS + r, n_rows - 1)];
+            q6_load_uniform<CH>(nxt, wm_rsrc(w + (uint64_t)Gs * group_bytes, live ? group_bytes : 0u),
+                                bn * CH, o);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        auto reduce = [&](const q6_lane_blocks<CH> &cur) __attribute__((always_inline)) {
+            q6_bounded_accum_multi<CH, V>(cur, bi * CH, xq, xq_stride, p, acc);
+            if (bi + 1 == nbat) {
+                epilogue(G * Q6K_GROUP_ROWS + r, acc, sg);
+#pragma unroll
+                for (int k = 0; k < V; k++) acc[k] = 0.0f;
+                bi = 0;
+                G += kWaves;
+            } else {
+                bi++;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        uint32_t t = 1;
+        for (; t + 1 < total; t += 2) {
+            issue(B, true);
+            reduce(A);
+            sg = sg_n;
+            issue(A, true);
+            reduce(B);
+            sg = sg_n;
+        }
+        const bool two = t < total;
+        issue(B, two);
+        reduce(A);
+        sg = sg_n;
+        if (two) reduce(B);
+    }
+#pragma unroll
+    for (int k = 0; k < V; k++) {
+        const float a1 = wm_wave_max_nonan(lb_max[k]), a2 = wm_wave_max_nonan(ub_max[k]);
+        if (lane == 0) {
+            red[k][wave] = a1;
+            red2[k][wave] = a2;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < (uint32_t)V) {
+        const uint32_t k = threadIdx.x;
+        float mm = red[k][0], mu = red2[k][0];
+        for (int i = 1; i < (int)kWaves; i++) {
+            mm = wm_max_nonan(mm, red[k][i]);
+            mu = wm_max_nonan(mu, red2[k][i]);
+        }
+        q6_pick(m.wg_lb, k)[blockIdx.x] = mm;
+        q6_pick(m.wg_ub, k)[blockIdx.x] = mu;
+    }
+}
 
 int pick_ch(uint32_t n_blocks) {
     for (int ch : {10, 8, 5, 4, 2})
@@ -838,7 +1047,99 @@ void launch_argmax_fast_ch(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                        n_rowgroups, hidden, logits, bound, wg_lb, wg_ub, n_wg, argmax_out, tail);
 }
 
+// The multi-vector work area: per vector slot, its prep area, the bounded
+// values and bounds, and the per-workgroup maxima.
+struct multi_layout {
+    size_t prep, approx, bound, wg_lb, wg_ub, slot;
+};
+multi_layout multi_layout_of(uint32_t n_rows, uint32_t n_blocks) {
+    multi_layout l;
+    size_t o = 0;
+    l.prep = o; o += al256(q6k_prep_bytes(n_blocks));
+    l.approx = o; o += al256((size_t)n_rows * 4);
+    l.bound = o; o += al256((size_t)n_rows * 4);
+    l.wg_lb = o; o += al256(4 * kBoundedMaxBlocks);
+    l.wg_ub = o; o += al256(4 * kBoundedMaxBlocks);
+    l.slot = o;
+    return l;
+}
+
+template <int CH>
+uint32_t bounded_multi_blocks_for(uint32_t n_rowgroups, size_t lds) {
+    static int cached[16] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    int per = dev < 16 ? cached[dev] : 0;
+    if (per == 0) {
+        int occ = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_q6k_bounded_multi<CH, kMultiVec>, kBoundedBlock, lds) !=
+                hipSuccess || occ < 1)
+            occ = 1;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            cus = 256;
+        per = occ * cus;
+        if (dev < 16) cached[dev] = per;
+    }
+    uint32_t blocks = (n_rowgroups + 3) / 4;
+    if (blocks > (uint32_t)per) blocks = (uint32_t)per;
+    if (blocks > kBoundedMaxBlocks) blocks = kBoundedMaxBlocks;
+    return blocks ? blocks : 1;
+}
+
+// Up to kMultiVec vectors per pass over the table; a group with fewer
+// fills its empty slots with the last vector's prep area (their results go
+// to the slots' own areas and are not read).
+template <int CH>
+void launch_argmax_multi_ch(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
+                            const float *hidden, uint32_t ld, const uint32_t *rows, uint32_t n_vec,
+                            uint32_t *argmax_out, void *work, hipStream_t s) {
+    const multi_layout lay = multi_layout_of(n_rows, n_blocks);
+    const float *sigma = reinterpret_cast<const float *>(w + wm_q6k_sigma_offset(n_rowgroups, n_blocks));
+    const size_t lds = sizeof(q6k_xq) * 16 * n_blocks * kMultiVec;
+    const uint32_t blocks = bounded_multi_blocks_for<CH>(n_rowgroups, lds);
+    const size_t sel_lds = sizeof(float) * 16 * xs_stride(n_blocks);
+    for (uint32_t v0 = 0; v0 < n_vec; v0 += kMultiVec) {
+        const int nv = (int)min((uint32_t)kMultiVec, n_vec - v0);
+        q6_multi m{};
+        m.nv = nv;
+        for (int k = 0; k < kMultiVec; k++) {
+            uint8_t *slot = (uint8_t *)work + (size_t)k * lay.slot;
+            const int kr = k < nv ? k : nv - 1;  // an empty slot reads the last vector
+            m.hidden[k] = hidden + (size_t)rows[v0 + kr] * ld;
+            m.prep[k] = (uint8_t *)work + (size_t)kr * lay.slot + lay.prep;
+            m.approx[k] = reinterpret_cast<float *>(slot + lay.approx);
+            m.bound[k] = reinterpret_cast<float *>(slot + lay.bound);
+            m.wg_lb[k] = reinterpret_cast<float *>(slot + lay.wg_lb);
+            m.wg_ub[k] = reinterpret_cast<float *>(slot + lay.wg_ub);
+            m.argmax_out[k] = argmax_out + v0 + kr;
+        }
+        hipLaunchKernelGGL(k_q6k_xprep_multi, dim3(nv), dim3(256), 0, s, m, n_blocks);
+        hipLaunchKernelGGL((k_q6k_bounded_multi<CH, kMultiVec>), dim3(blocks), dim3(kBoundedBlock), lds, s, w,
+                           n_blocks, n_rows, n_rowgroups, sigma, m);
+        hipLaunchKernelGGL(k_q6k_select_multi<CH>, dim3(nv), dim3(kSelectBlock), sel_lds, s, w, n_blocks,
+                           n_rows, n_rowgroups, m, blocks);
+    }
+}
+
 }  // namespace
+
+size_t wm_q6k_multi_work_bytes(uint32_t n_rows, uint32_t n_blocks) {
+    return (size_t)kMultiVec * multi_layout_of(n_rows, n_blocks).slot;
+}
+
+void wm_launch_q6k_argmax_multi(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
+                                const float *hidden, uint32_t ld, const uint32_t *rows, uint32_t n_vec,
+                                uint32_t *argmax_out, void *work, hipStream_t s) {
+#define WM_M_CASE(C)                                                                               \
+    case C:                                                                                        \
+        launch_argmax_multi_ch<C>(w, n_blocks, n_rows, n_rowgroups, hidden, ld, rows, n_vec,       \
+                                  argmax_out, work, s);                                            \
+        break;
+    switch (pick_ch(n_blocks)) {
+        WM_M_CASE(10) WM_M_CASE(8) WM_M_CASE(5) WM_M_CASE(4) WM_M_CASE(2) default: WM_M_CASE(1)
+    }
+#undef WM_M_CASE
+}
 
 void wm_launch_q6k_repack(const uint8_t *raw, uint8_t *out, uint32_t n_rows, uint32_t n_blocks,
                           uint32_t n_rowgroups, hipStream_t s) {

@@ -92,6 +92,7 @@ struct wm_model {
     wm_act_meta *b_meta = nullptr;
     wm_batch_tok *b_tok = nullptr;
     uint32_t *b_ids = nullptr, *b_next = nullptr;
+    void *b_lmw = nullptr;  // the multi-vector lm-head's work area
     float *b_scores = nullptr;  // attention scores [t][head][context], grown on demand
     size_t b_scores_bytes = 0;
     // greedy decode's read-back ring: per step in flight, the next id and the
@@ -366,6 +367,7 @@ wm_status ensure_batch_ws(wm_model *m, uint32_t M) {
         align256(cap * sizeof(wm_batch_tok)),
         align256(cap * 4),                 // token ids
         align256(cap * 4),                 // next tokens
+        align256(wm_q6k_multi_work_bytes(m->cfg.vocab_size, m->embd_blocks)),  // lm-head, 4 vectors
     };
     size_t total = 0;
     for (size_t sz : sizes) total += sz;
@@ -382,7 +384,7 @@ wm_status ensure_batch_ws(wm_model *m, uint32_t M) {
                       (void **)&m->b_attn,   (void **)&m->b_yo,   (void **)&m->b_ygu,
                       (void **)&m->b_ydown,  (void **)&m->b_final, (void **)&m->b_act,
                       (void **)&m->b_meta,   (void **)&m->b_tok,  (void **)&m->b_ids,
-                      (void **)&m->b_next};
+                      (void **)&m->b_next,   (void **)&m->b_lmw};
     for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); i++) {
         *slots[i] = p;
         p += sizes[i];
@@ -514,11 +516,9 @@ wm_status batch_forward_dev(wm_model *m, wm_kv_cache *const *caches, uint32_t n_
     wm_norm_rows fin{m->b_hidden, E, m->b_ydown, E, nullptr, 0, m->output_norm, E, c.rms_eps,
                      nullptr, m_pad, nullptr, m->b_final, E, err, c.n_layers};
     if (!wm_launch_rmsnorm_rows(fin, M, s)) return rows_unsupported(ctx);
-    if (want_next)
-        for (uint32_t i = 0; i < n_seqs; i++)
-            wm_launch_q6k_argmax_fast(m->embd, m->embd_blocks, c.vocab_size, m->embd_rowgroups,
-                                      m->b_final + (size_t)last[i] * E, m->logits, m->b_next + i,
-                                      m->lm_work, false, s);
+    if (want_next)  // every sequence's id-only lm-head, four per pass over the table
+        wm_launch_q6k_argmax_multi(m->embd, m->embd_blocks, c.vocab_size, m->embd_rowgroups, m->b_final, E,
+                                   last.data(), n_seqs, m->b_next, m->b_lmw, s);
     WM_HIP(ctx, hipGetLastError());
     uint32_t flag = 0;
     WM_HIP(ctx, hipMemcpyAsync(&flag, err, 4, hipMemcpyDeviceToHost, s));

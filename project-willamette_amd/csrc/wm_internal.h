@@ -457,6 +457,13 @@ struct wm_step_tail {
     const uint32_t *err_flag;   // the step's error flag (device)
     uint32_t ring_mask;
 };
+// The id-only lm-head of n_vec hidden vectors (hidden + rows[i] * ld), ids
+// to argmax_out[i], each equal to wm_launch_q6k_argmax_fast's: one bounded
+// pass over the table per four vectors.  work: wm_q6k_multi_work_bytes.
+size_t wm_q6k_multi_work_bytes(uint32_t n_rows, uint32_t n_blocks);
+void wm_launch_q6k_argmax_multi(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
+                                const float *hidden, uint32_t ld, const uint32_t *rows, uint32_t n_vec,
+                                uint32_t *argmax_out, void *work, hipStream_t s);
 void wm_launch_q6k_argmax_fast(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
                                uint32_t n_rowgroups, const float *hidden, float *logits,
                                uint32_t *argmax_out, void *work, bool prepared, hipStream_t s,
