@@ -761,81 +761,98 @@ __device__ __forceinline__ void sv_stage(const sv_regs &r, int8_t (*vt)[HD], flo
     if (sv_col<HD>(3) == 0) vst[sv_row<HD>(3)] = r.s3;
 }
 
-// Softmax of one (token, head) row of scores (attention.rs:45-73): max, exp
-// (glibc expf) in place, the exact sequential sum by the workgroup (thread t
-// owning the m = ceil(n / 256) consecutive terms from t*m), and the row's
-// scale 1/sum (1 when the sum is not positive: the reference leaves the row
-// unnormalised); the V pass forms each weight as exp * scale, the same f32
-// product the reference's `*= inv` makes.  Tiles of kSvPos positions whose
-// exps are all exactly zero are flagged dead: their weights are zero, and a
-// zero term leaves each of the V pass's sums unchanged (those sums start at
-// +0 and can never be -0), so it skips them.  A row whose maximum is not
-// finite becomes all zero (its output is then 0).
-constexpr uint32_t kSmThreads = 256;
-constexpr int kSmMaxM = 16;  // terms per thread: n <= 4096
-struct softmax_lds {
-    uint64_t exp_tab[32];
-    float red[kSmThreads / 64];
-    uint8_t tile_live[kAttnTiles];
-    float ex[kSmMaxM * kSmThreads];  // the exps, for the sum's walk
-    wm::seq_block_scratch seq_scratch;
-};
-// One row with M >= ceil(n / kSmThreads) terms per thread (the per-term
-// work runs over M slots, so the kernel picks the smallest M of a few).
-template <int M>
-__device__ __forceinline__ void softmax_row(const attn_rows_args &a, softmax_lds &L, uint32_t h, uint32_t t) {
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const uint32_t n = a.tok[t].pos + 1, n_tiles = (n + kSvPos - 1) / kSvPos;
+// Softmax of one (token, head) row of scores per wave (attention.rs:45-73):
+// max, exp (glibc expf) in place, the exact sequential sum of the exps by the
+// one-wave algorithm (512 exps per step, summed from the registers that
+// computed them) and the row's scale 1/sum (1 when the sum is not positive:
+// the reference leaves the row unnormalised); the V pass forms each weight as
+// exp * scale, the same f32 product the reference's `*= inv` makes.  Tiles of
+// kSvPos positions whose exps are all exactly zero are flagged dead: their
+// weights are zero, and a zero term leaves each of the V pass's sums
+// unchanged (those sums start at +0 and can never be -0), so it skips them.
+// A row whose maximum is not finite becomes all zero (its output is then 0).
+// The rows of a workgroup are heads of one token, so its waves have equal
+// work; a row's sum has no barrier and no idle wave, and the many rows of a
+// batch keep every SIMD busy.
+constexpr uint32_t kSmRows = 4;  // rows per workgroup, one per wave
+static_assert(kSvPos % 8 == 0 && wm::kSeqBatch / kSvPos == 8, "a step's tiles are 8-lane groups");
+__global__ __launch_bounds__(kSmRows * 64) void k_attn_softmax_rows(attn_rows_args a) {
+    __shared__ uint64_t exp_tab[32];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wid = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
+    if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
+    __syncthreads();
+    const uint32_t h = blockIdx.x * kSmRows + wid, t = blockIdx.y;
+    if (h >= a.n_heads) return;
+    const uint32_t n = a.tok[t].pos + 1, n_tiles = (n + kSvPos - 1) / kSvPos;  // n_tiles <= 64
     const uint64_t row = (uint64_t)t * a.n_heads + h;
     float *w = a.scores + row * a.score_stride;
     uint8_t *live = a.live + row * kAttnTiles;
-    const uint32_t mm = (n + kSmThreads - 1) / kSmThreads, k0 = tid * mm;
-    float v[M];
-    float m = -INFINITY;
+    // The row's float4s below n4 = ceil(n / 4) lie inside it (rows start
+    // 16-byte aligned and score_stride >= n rounded up to 4); indices are
+    // clamped to n4 - 1 and components at n and beyond are masked.
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    const uint32_t n4 = (n + 3) / 4;
+    float mx = -INFINITY;
+    for (uint32_t q0 = 0; q0 < n4; q0 += 256) {  // lane l: float4s q0 + l + 64i
+        float4 x[4];
 #pragma unroll
-    for (int j = 0; j < M; j++) {
-        v[j] = ((uint32_t)j < mm && k0 + j < n) ? w[k0 + j] : -INFINITY;
-        m = wm_max_nonan(m, v[j]);
+        for (int i = 0; i < 4; i++) {
+            const uint32_t q = q0 + lane + 64 * i;
+            x[i] = w4[min(q, n4 - 1)];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t p = 4 * (q0 + lane + 64 * i);
+            mx = wm_max_nonan(mx, p < n ? x[i].x : -INFINITY);
+            mx = wm_max_nonan(mx, p + 1 < n ? x[i].y : -INFINITY);
+            mx = wm_max_nonan(mx, p + 2 < n ? x[i].z : -INFINITY);
+            mx = wm_max_nonan(mx, p + 3 < n ? x[i].w : -INFINITY);
+        }
     }
-    m = wm_wave_max_nonan(m);
-    if (lane == 0) L.red[wid] = m;
-    __syncthreads();
-    float mx = L.red[0];
-#pragma unroll
-    for (uint32_t i = 1; i < kSmThreads / 64; i++) mx = wm_max_nonan(mx, L.red[i]);
+    mx = wm_wave_max_nonan(mx);
     if (!isfinite(mx)) {  // every weight becomes 0 (or the row held a NaN)
-#pragma unroll
-        for (int j = 0; j < M; j++)
-            if ((uint32_t)j < mm && k0 + j < n) w[k0 + j] = 0.0f;
-        if (tid < n_tiles) live[tid] = 0;
-        if (tid == 0) a.row_scale[row] = 0.0f;
+        for (uint32_t k = lane; k < n; k += 64) w[k] = 0.0f;
+        if (lane < n_tiles) live[lane] = 0;
+        if (lane == 0) a.row_scale[row] = 0.0f;
         return;
     }
-#pragma unroll
-    for (int j = 0; j < M; j++) {
-        const bool in = (uint32_t)j < mm && k0 + j < n;
-        v[j] = in ? wm::expf_glibc(v[j] - mx, L.exp_tab) : 0.0f;
-        if (in) {
-            w[k0 + j] = v[j];
-            L.ex[k0 + j] = v[j];
+    // steps of 512: lane l takes positions k + 8l .. k + 8l + 7; the next
+    // step's scores are loaded before this step's sum
+    float4 c0 = w4[min(2 * lane, n4 - 1)], c1 = w4[min(2 * lane + 1, n4 - 1)];
+    float sum = 0.0f;
+    for (uint32_t k = 0; k < n; k += wm::kSeqBatch) {
+        const uint32_t base = k + 8 * lane;
+        float4 n0 = c0, n1 = c1;
+        if (k + wm::kSeqBatch < n) {
+            const uint32_t nq = (base + wm::kSeqBatch) / 4;
+            n0 = w4[min(nq, n4 - 1)];
+            n1 = w4[min(nq + 1, n4 - 1)];
         }
-        if (in && v[j] != 0.0f) L.tile_live[(k0 + j) / kSvPos] = 1;
+        float v[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        bool nz = false;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            v[j] = base + j < n ? wm::expf_glibc(v[j] - mx, exp_tab) : 0.0f;
+            nz = nz || v[j] != 0.0f;
+        }
+        if (base + 8 <= n) {
+            *reinterpret_cast<float4 *>(w + base) = make_float4(v[0], v[1], v[2], v[3]);
+            *reinterpret_cast<float4 *>(w + base + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (base + j < n) w[base + j] = v[j];
+        }
+        // lanes 8i .. 8i+7 hold tile k / kSvPos + i
+        const uint64_t nzm = __ballot(nz);
+        const uint32_t tile = k / kSvPos + lane;
+        if (lane < 8 && tile < n_tiles) live[tile] = ((nzm >> (8 * lane)) & 0xFFu) != 0 ? 1 : 0;
+        sum = wm::seq_sum_step(sum, v, k == 0);
+        c0 = n0;
+        c1 = n1;
     }
-    wm_sync_lds();  // the exps and the tile flags in LDS (the global stores need not wait)
-    if (tid < n_tiles) live[tid] = L.tile_live[tid];
-    const float sum = wm::seq_sum_block_owned<M, kSmThreads>(v, n, L.ex, &L.seq_scratch);
-    if (tid == 0) a.row_scale[row] = sum > 0.0f ? 1.0f / sum : 1.0f;
-}
-__global__ __launch_bounds__(kSmThreads) void k_attn_softmax_rows(attn_rows_args a) {
-    __shared__ softmax_lds L;
-    const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-    if (tid < 32) L.exp_tab[tid] = wm::kExp2Tab[tid];
-    if (tid < kAttnTiles) L.tile_live[tid] = 0;
-    const uint32_t mm = (a.tok[t].pos + 1 + kSmThreads - 1) / kSmThreads;  // uniform
-    if (mm <= 4) softmax_row<4>(a, L, h, t);
-    else if (mm <= 8) softmax_row<8>(a, L, h, t);
-    else if (mm <= 12) softmax_row<12>(a, L, h, t);
-    else softmax_row<kSmMaxM>(a, L, h, t);
+    if (lane == 0) a.row_scale[row] = sum > 0.0f ? 1.0f / sum : 1.0f;
 }
 
 // G: query heads per workgroup, HG: per KV head (item unit = kv head * HG/G + part)
@@ -1143,7 +1160,8 @@ void wm_launch_attn_rows(const float *q, const wm_batch_tok *tok, uint32_t m, ui
     WM_SCORES_CASE(128, 1) WM_SCORES_CASE(128, 2) WM_SCORES_CASE(128, 4) WM_SCORES_CASE(128, 8)
     WM_SCORES_CASE(64, 1) WM_SCORES_CASE(64, 2) WM_SCORES_CASE(64, 4) WM_SCORES_CASE(64, 8)
 #undef WM_SCORES_CASE
-    hipLaunchKernelGGL(k_attn_softmax_rows, dim3(n_heads, m), dim3(kSmThreads), 0, s, a);
+    hipLaunchKernelGGL(k_attn_softmax_rows, dim3((n_heads + kSmRows - 1) / kSmRows, m), dim3(kSmRows * 64),
+                       0, s, a);
 #define WM_SV_CASE(HD, G)                                                                      \
     if (head_dim == HD && group == G)                                                          \
         hipLaunchKernelGGL((k_attn_sv_rows<HD, (G < kSvHeads ? G : kSvHeads), G>),             \

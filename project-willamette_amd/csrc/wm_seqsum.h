@@ -77,6 +77,78 @@ __host__ __device__ constexpr uint32_t seq_sum_padded(uint32_t n) {
 // is loaded twice.  The first kSeqLead terms, which move s through many
 // binades and (while s is small) hold most of the halfway cases, are added
 // one at a time straight from the registers.
+// One step: adds the 512 terms v (lane l holding terms 8l .. 8l+7 of the
+// step, 0 past the end) to s, which the step's first terms follow; `lead`
+// on the sum's first step.  v is consumed.  Every lane gets the same s.
+__device__ inline float seq_sum_step(float s, float (&v)[8], bool lead) {
+    const uint32_t lane = threadIdx.x & 63;
+    if (lead) {
+        // terms 0..127 sit in lanes 0-15; adding the zeros past n changes nothing
+#pragma unroll
+        for (int L = 0; L < kSeqLead / 8; L++)
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), L));
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = lane < kSeqLead / 8 ? 0.0f : v[j];
+    }
+    // Each restart zeroes at least one non-zero term, so a step ends after
+    // at most 513 passes; the bound is explicit all the same.
+    for (uint32_t pass = 0; pass <= kSeqBatch; pass++) {
+        if (s != s) return s;
+        const uint32_t bits = __float_as_uint(s);  // s >= +0
+        const uint32_t ef = bits >> 23;
+        const bool normal = ef - 1u < 254u;
+        const int sh = normal ? 150 - (int)ef : (ef == 0 ? 255 : -255);
+        const int N = normal ? (int)((bits & 0x7fffffu) | 0x800000u) : 0;
+        int p[8], rho[8];
+        bool bad[8];
+        int run = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float r = ldexpf(v[j], sh);    // a / ulp(s); exact unless < 2^-126
+            const bool fin = r < 0x1p22f;         // false for NaN, inf, huge
+            const float rr = fin ? r : 0.0f;
+            bad[j] = !fin || rr - floorf(rr) == 0.5f;  // halfway: parity decides
+            rho[j] = (int)rintf(rr);
+            run += rho[j];
+            p[j] = run;
+        }
+        const int incl = wave_incl_scan_i32(run);
+        const int excl = incl - run;
+        const int limit = (1 << 24) - 1 - N;  // N + prefix must stay below 2^24 - 1
+        int first = 8, before = 0;
+#pragma unroll
+        for (int j = 7; j >= 0; j--) {
+            // A term with increment 0 leaves N + prefix where it was, so it
+            // never crosses; hence offenders are never zero terms (a zero
+            // term is neither bad nor crossing), and every restart below
+            // consumes a non-zero term.
+            const bool off = bad[j] || (rho[j] > 0 && excl + p[j] >= limit);
+            first = off ? j : first;
+            before = off ? excl + (j ? p[j - 1] : 0) : before;
+        }
+        const uint64_t mask = __ballot(first < 8);
+        if (mask == 0) {
+            if (normal) s = ldexpf((float)(N + __builtin_amdgcn_readlane(incl, 63)), -sh);
+            break;
+        }
+        const int fl = __ffsll((unsigned long long)mask) - 1;
+        const int jl = __builtin_amdgcn_readlane(first, fl);
+        const int pre = __builtin_amdgcn_readlane(before, fl);
+        float vo = v[0];
+#pragma unroll
+        for (int j = 1; j < 8; j++) vo = j == jl ? v[j] : vo;
+        vo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vo), fl));
+        if (normal) s = ldexpf((float)(N + pre), -sh);  // the run before the offender
+        s = s + vo;                                      // the offender, by an ordinary add
+        const uint32_t done = 8 * (uint32_t)fl + (uint32_t)jl;  // last term now in s
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = 8 * lane + j <= done ? 0.0f : v[j];
+    }
+    return s;
+}
+
 // Continues the sum from s (itself a left-to-right sum of earlier terms,
 // so s >= +0 or NaN); a needs no alignment and is read only below n.
 __device__ inline float seq_sum_nonneg_from(float s, const float *a, uint32_t n) {
@@ -86,70 +158,8 @@ __device__ inline float seq_sum_nonneg_from(float s, const float *a, uint32_t n)
         float v[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) v[j] = base + j < n ? a[base + j] : 0.0f;
-        if (k == 0) {
-            // terms 0..127 sit in lanes 0-15; adding the zeros past n changes nothing
-#pragma unroll
-            for (int L = 0; L < kSeqLead / 8; L++)
-#pragma unroll
-                for (int j = 0; j < 8; j++)
-                    s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), L));
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = lane < kSeqLead / 8 ? 0.0f : v[j];
-        }
-        // Each restart zeroes at least one non-zero term, so a step ends after
-        // at most 513 passes; the bound is explicit all the same.
-        for (uint32_t pass = 0; pass <= kSeqBatch; pass++) {
-            if (s != s) return s;
-            const uint32_t bits = __float_as_uint(s);  // s >= +0
-            const uint32_t ef = bits >> 23;
-            const bool normal = ef - 1u < 254u;
-            const int sh = normal ? 150 - (int)ef : (ef == 0 ? 255 : -255);
-            const int N = normal ? (int)((bits & 0x7fffffu) | 0x800000u) : 0;
-            int p[8], rho[8];
-            bool bad[8];
-            int run = 0;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float r = ldexpf(v[j], sh);    // a / ulp(s); exact unless < 2^-126
-                const bool fin = r < 0x1p22f;         // false for NaN, inf, huge
-                const float rr = fin ? r : 0.0f;
-                bad[j] = !fin || rr - floorf(rr) == 0.5f;  // halfway: parity decides
-                rho[j] = (int)rintf(rr);
-                run += rho[j];
-                p[j] = run;
-            }
-            const int incl = wave_incl_scan_i32(run);
-            const int excl = incl - run;
-            const int limit = (1 << 24) - 1 - N;  // N + prefix must stay below 2^24 - 1
-            int first = 8, before = 0;
-#pragma unroll
-            for (int j = 7; j >= 0; j--) {
-                // A term with increment 0 leaves N + prefix where it was, so it
-                // never crosses; hence offenders are never zero terms (a zero
-                // term is neither bad nor crossing), and every restart below
-                // consumes a non-zero term.
-                const bool off = bad[j] || (rho[j] > 0 && excl + p[j] >= limit);
-                first = off ? j : first;
-                before = off ? excl + (j ? p[j - 1] : 0) : before;
-            }
-            const uint64_t mask = __ballot(first < 8);
-            if (mask == 0) {
-                if (normal) s = ldexpf((float)(N + __builtin_amdgcn_readlane(incl, 63)), -sh);
-                break;
-            }
-            const int fl = __ffsll((unsigned long long)mask) - 1;
-            const int jl = __builtin_amdgcn_readlane(first, fl);
-            const int pre = __builtin_amdgcn_readlane(before, fl);
-            float vo = v[0];
-#pragma unroll
-            for (int j = 1; j < 8; j++) vo = j == jl ? v[j] : vo;
-            vo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vo), fl));
-            if (normal) s = ldexpf((float)(N + pre), -sh);  // the run before the offender
-            s = s + vo;                                      // the offender, by an ordinary add
-            const uint32_t done = 8 * (uint32_t)fl + (uint32_t)jl;  // last term now in s
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = 8 * lane + j <= done ? 0.0f : v[j];
-        }
+        s = seq_sum_step(s, v, k == 0);
+        if (s != s) return s;
     }
     return s;
 }
