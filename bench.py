@@ -101,6 +101,20 @@ def role_bytes(cfg, n_past: int) -> dict:
     }
 
 
+def ffn_block(roles):
+    """The FFN block's time per layer from the gate_up and down roles, its
+    algorithmic bytes and HBM rate, and the time the same bytes take at 70 %
+    of the HBM peak."""
+    us = roles["gate_up"]["us_per_launch"] + roles["down"]["us_per_launch"]
+    nbytes = roles["gate_up"]["bytes_per_launch"] + roles["down"]["bytes_per_launch"]
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"us": round(us, 3), "bytes": int(nbytes), "gbps": round(gbps, 1),
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "us_at_70pct_hbm": round(nbytes / (0.7 * HBM_PEAK_GBPS * 1e9) * 1e6, 3),
+            "kernels": "k_i2s_fused<0, 1, 16, 3> (ffn_norm, gate, up) + "
+                       "k_i2s_fused<0, 1, 16, 7> (relu(gate)^2 * up, ffn_sub_norm, down)"}
+
+
 def decode_roles(ctx, wh, dev, dkv, cfg, reps: int):
     """Each per-layer role of the decode step just run, relaunched `reps`
     times back to back (layer 1, the cache's last position) and timed with
@@ -540,6 +554,10 @@ def main():
             "q6k_lm_head_128256x2560": {
                 k: {"us": round(v * 1000, 2), "gbps": round(gbps[k], 1),
                     "frac": round(gbps[k] / HBM_PEAK_GBPS, 4)} for k, v in lm.items()},
+            # the FFN block at M = 1 (ffn_norm with the residual add, gate and
+            # up 6912x2560, relu(gate)^2 * up, ffn_sub_norm, down 2560x6912):
+            # the gate_up and down launches of the decode step, timed above
+            "ffn_block_2560x6912_m1": ffn_block(roles),
             "i2s_2560x2560_rotated": {"gbps": round(mv_gbps, 1), "frac": round(mv_gbps / HBM_PEAK_GBPS, 4),
                                       "us_per_matvec": round(mv_ms * 1000 / copies, 3),
                                       "copies": copies},
