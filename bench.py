@@ -175,7 +175,11 @@ def lm_head_kernels(ctx, wh, hm, cfg, reps: int):
 
 def i2s_stream(ctx, wh, copies: int, reps: int):
     """i2_s 2560x2560 matvec over `copies` distinct device copies (rotated
-    through > 256 MB so the Infinity Cache cannot hold them), 64 per launch."""
+    through > 256 MB so the Infinity Cache cannot hold them), 64 per launch;
+    then one standalone call of wm_bitlinear_i2s_matvec_f32_dev per copy
+    (quantise, dots, finalise: three launches), back to back, each call on
+    the next copy.  Returns the stream's ms per launch, its bytes, and the
+    single call's ms."""
     seed = 0x5749_4C4C_0000_0001
     packed = wh.synth_i2s(seed, 1, 2560, 2560)
     ws = [ctx.upload_i2s(packed, 1.25, 2560, 2560) for _ in range(copies)]
@@ -188,10 +192,16 @@ def i2s_stream(ctx, wh, copies: int, reps: int):
     for _ in range(reps):
         ctx.check(wh.lib.wm_bitlinear_i2s_matvec_f32_multi_dev(ctx.h, arr, copies, x.ptr, y.ptr))
     ms = timer.stop_ms() / reps
+    single = wh.lib.wm_bitlinear_i2s_matvec_f32_dev
+    ctx.check(single(ctx.h, ws[0].h, x.ptr, y.ptr))
+    timer.start()
+    for w in ws:
+        ctx.check(single(ctx.h, w.h, x.ptr, y.ptr))
+    single_ms = timer.stop_ms() / copies
     per_matvec = 2560 * 640 + 4 + 2560 * 4 * 2  # weights + scale + x + y (f32)
     for w in ws:
         w.close()
-    return ms, per_matvec * copies
+    return ms, per_matvec * copies, single_ms
 
 
 INT8_MFMA_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
@@ -495,8 +505,9 @@ def main():
     gbps = {k: lm_bytes / (v / 1000.0) / 1e9 for k, v in lm.items()}
     log("lm-head: " + ", ".join(f"{k} {v * 1000:.1f} us ({gbps[k]:.0f} GB/s)" for k, v in lm.items()))
     copies = 320  # 320 x 1.64 MB = 524 MB > 256 MB Infinity Cache
-    mv_ms, mv_bytes = i2s_stream(ctx, wh, copies, reps=10)
+    mv_ms, mv_bytes, mv_single_ms = i2s_stream(ctx, wh, copies, reps=10)
     mv_gbps = mv_bytes / (mv_ms / 1000.0) / 1e9
+    mv_single_gbps = mv_bytes / copies / (mv_single_ms / 1000.0) / 1e9
     log(f"i2_s 2560x2560 x{copies}: {mv_ms * 1000 / copies:.2f} us/matvec, {mv_gbps:.0f} GB/s")
 
     batch = None
@@ -561,6 +572,10 @@ def main():
             "i2s_2560x2560_rotated": {"gbps": round(mv_gbps, 1), "frac": round(mv_gbps / HBM_PEAK_GBPS, 4),
                                       "us_per_matvec": round(mv_ms * 1000 / copies, 3),
                                       "copies": copies},
+            "i2s_2560x2560_single_call": {"us": round(mv_single_ms * 1000, 3),
+                                          "gbps": round(mv_single_gbps, 1),
+                                          "frac": round(mv_single_gbps / HBM_PEAK_GBPS, 4),
+                                          "launches": 3},
         },
         "ragged_batch": batch,
         "decode_effective_gbps": round(decode_gbps, 1),

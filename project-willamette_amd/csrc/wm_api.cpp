@@ -389,7 +389,21 @@ wm_status wm_bitlinear_i2s_matvec_f32_scalar(wm_ctx *ctx, const wm_tensor *w, co
 
 wm_status wm_bitlinear_i2s_matvec_f32_dev(wm_ctx *ctx, const wm_tensor *w, const float *d_input,
                                           float *d_output) {
-    return wm_bitlinear_i2s_matvec_f32_multi_dev(ctx, &w, 1, d_input, d_output);
+    // one tensor: its pointer and scale go in the kernels' arguments (the
+    // multi-copy path keeps a device table, uploaded again whenever the
+    // tensors change, which for a caller stepping through layers is every call)
+    if (!ctx || !w || !d_input || !d_output) return WM_E_ARG;
+    wm_status st = check_i2s(ctx, w);
+    if (st) return st;
+    void *scratch;
+    if ((st = wm_ctx_scratch(ctx, matvec_ws_bytes(w), &scratch))) return st;
+    uint8_t *act = (uint8_t *)scratch;
+    wm_act_meta *meta = (wm_act_meta *)(act + align256(w->in_dim));
+    int32_t *partial = (int32_t *)((uint8_t *)meta + 256);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    run_matvec(ctx, w, d_input, d_output, nullptr, act, meta, partial);
+    WM_HIP(ctx, hipGetLastError());
+    return WM_OK;
 }
 
 wm_status wm_bitlinear_i2s_matvec_f32_multi_dev(wm_ctx *ctx, const wm_tensor *const *ws,
