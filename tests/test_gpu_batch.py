@@ -140,6 +140,29 @@ def test_batch_decode_step_all_single_tokens(pair):
     run_case(cfg, dev, orm, prefill, new, seed=30)
 
 
+DENSE = bs.BitNetConfig(n_layers=2, n_embd=256, n_ff=384, n_heads=2, n_kv_heads=1, head_dim=128,
+                        vocab=500, context_length=4096)
+
+
+def test_batch_dense_softmax_long_rows(ctx):
+    """attn_q scaled down to 1e-6: every score is tiny and no softmax weight
+    underflows, so each row's exact exp sum crosses many binades and runs
+    over several 512-term steps with ragged tails (rows of 1 to ~3000
+    positions), every tile live; ragged batch against the oracle token by
+    token."""
+    hm = bs.make_host_model(DENSE, seed=43)
+    for hl in hm.layers:
+        hl.scales["attn_q"] = 1e-6
+    dev = bs.load_device_model(ctx, hm)
+    orm = OracleModel(hm)
+    rng = np.random.default_rng(12)
+    prefill = [2999, 1030, 511, 0, 64]
+    new = [[int(t) for t in rng.integers(0, DENSE.vocab, n)] for n in (3, 2, 4, 1, 6)]
+    run_case(DENSE, dev, orm, prefill, new, seed=50)
+    dev.close()
+    orm.close()
+
+
 def test_batch_over_64_tokens(pair):
     # more than one 64-token GEMM tile, tiles shared by several sequences
     cfg, hm, dev, orm = pair
