@@ -101,16 +101,45 @@ def role_bytes(cfg, n_past: int) -> dict:
     }
 
 
-def ffn_block(roles):
-    """The FFN block's time per layer from the gate_up and down roles, its
-    algorithmic bytes and HBM rate, and the time the same bytes take at 70 %
-    of the HBM peak."""
-    us = roles["gate_up"]["us_per_launch"] + roles["down"]["us_per_launch"]
-    nbytes = roles["gate_up"]["bytes_per_launch"] + roles["down"]["bytes_per_launch"]
-    gbps = nbytes / (us * 1e-6) / 1e9
-    return {"us": round(us, 3), "bytes": int(nbytes), "gbps": round(gbps, 1),
+FFN_BLOCK_BYTES = 13_329_408  # x, ffn_norm w, gate + up, ffn_sub_norm w, down, output (f32 / 2-bit)
+
+
+def ffn_block_stream(ctx, wh, bs, copies: int, reps: int):
+    """The FFN block at M = 1 as its own unit (wm_ffn_block_forward_dev:
+    ffn_norm, gate and up 6912x2560, relu(gate)^2 * up, ffn_sub_norm, down
+    2560x6912; two launches) over `copies` distinct weight sets rotated
+    through more than the 256 MB Infinity Cache, x ~ N(0, 1) straight into
+    ffn_norm.  Returns microseconds per block."""
+    E, F = 2560, 6912
+    seed = bs.master_seed(3)
+    g, u, d = wh.synth_i2s(seed, 1, E, F), wh.synth_i2s(seed, 2, E, F), wh.synth_i2s(seed, 3, F, E)
+    sc = wh.synth_uniform(seed, 4, 3, 0.5, 2.0)
+    sets = [(ctx.upload_i2s(g, float(sc[0]), E, F), ctx.upload_i2s(u, float(sc[1]), E, F),
+             ctx.upload_i2s(d, float(sc[2]), F, E)) for _ in range(copies)]
+    nw = ctx.to_device(wh.synth_uniform(seed, 5, E, 0.9, 1.1))
+    sw = ctx.to_device(wh.synth_uniform(seed, 6, F, 0.9, 1.1))
+    x = ctx.to_device(wh.synth_normal(seed, 7, E))
+    y = ctx.alloc(E * 4)
+    run = lambda t: ctx.check(wh.lib.wm_ffn_block_forward_dev(ctx.h, x.ptr, nw.ptr, t[0].h, t[1].h, t[2].h,
+                                                             sw.ptr, 1e-5, y.ptr))
+    for t in sets[:4]:
+        run(t)
+    timer = HipTimer(ctx.stream)
+    timer.start()
+    for i in range(reps):
+        for t in sets:
+            run(t)
+    us = timer.stop_ms() * 1000.0 / (reps * copies)
+    for t in sets:
+        for w in t:
+            w.close()
+    for b in (nw, sw, x, y):
+        b.free()
+    gbps = FFN_BLOCK_BYTES / (us * 1e-6) / 1e9
+    return {"us": round(us, 3), "bytes": FFN_BLOCK_BYTES, "gbps": round(gbps, 1),
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "us_at_70pct_hbm": round(nbytes / (0.7 * HBM_PEAK_GBPS * 1e9) * 1e6, 3),
+            "us_at_70pct_hbm": round(FFN_BLOCK_BYTES / (0.7 * HBM_PEAK_GBPS * 1e9) * 1e6, 3),
+            "copies": copies, "launches": 2,
             "kernels": "k_i2s_fused<0, 1, 16, 3> (ffn_norm, gate, up) + "
                        "k_i2s_fused<0, 1, 16, 7> (relu(gate)^2 * up, ffn_sub_norm, down)"}
 
@@ -277,24 +306,66 @@ def ragged_batch(ctx, wh, bs, dev, cfg, steps: int):
 
 def cpu_baseline(hm, cfg, n_tokens: int, threads: int):
     """The oracle (C restatement of the reference's x86 SSE2 path) on this
-    host: BitLinear single-threaded, lm-head rows over `threads` threads
-    (src/model/bitlinear_sse2.rs:329-340, src/model/lm_head.rs:87-88)."""
+    host, timed at the reference's own boundaries (cmd_bench_json,
+    src/main.rs:1301-1361): matvec_ms (layer 0's attn_q on the start token's
+    embedding, after one warm-up call), then per decode step
+    cached_forward_ms (forward_with_cache), lm_head_ms (compute_logits) and
+    argmax_ms, averaged over n_tokens steps of the bench workload (positions
+    1024..); plus the FFN block (ffn_block_forward on layer 0's tensors).
+    BitLinear single-threaded, lm-head rows over `threads` threads, as the
+    reference runs them (src/model/bitlinear_sse2.rs:329-340,
+    src/model/lm_head.rs:87-88)."""
     import bitnet_synth as bs
+    import oracle.oracle as orc
     from oracle.oracle_model import OracleModel
+    E, F, V = cfg.n_embd, cfg.n_ff, cfg.vocab
+    embd = hm.token_embd.reshape(V, -1)
+    L0 = hm.layers[0]
+    x = orc.q6k_dequantize_row(embd[START_TOKEN], E)
+    q = L0.packed["attn_q"], L0.scales["attn_q"]
+    orc.bitlinear_i8(q[0], q[1], E, E, x)
+    reps = 10
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        orc.bitlinear_i8(q[0], q[1], E, E, x)
+    matvec_ms = (time.perf_counter() - t0) * 1000.0 / reps
+    ffn_args = (x, L0.norms["ffn_norm"], L0.packed["ffn_gate"], L0.scales["ffn_gate"],
+                L0.packed["ffn_up"], L0.scales["ffn_up"], L0.packed["ffn_down"], L0.scales["ffn_down"],
+                L0.norms["ffn_sub_norm"], F, cfg.rms_eps)
+    orc.ffn_block(*ffn_args)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        orc.ffn_block(*ffn_args)
+    ffn_ms = (time.perf_counter() - t0) * 1000.0 / 3
     orm = OracleModel(hm, threads=threads)
     okv = orm.kv(cfg.context_length)
     k, v = bs.kv_prefill(cfg, bs.master_seed(4), PREFILL)
     okv.append_positions(k, v)
     del k, v
     tok, pos = START_TOKEN, PREFILL
-    t0 = time.perf_counter()
+    fwd = lm = am = 0.0
     for _ in range(n_tokens):
+        t0 = time.perf_counter()
         h = okv.forward(tok, pos)
-        _, tok = okv.logits_argmax(h)
+        t1 = time.perf_counter()
+        logits = orc.compute_logits(hm.token_embd, E, V, h, threads)
+        t2 = time.perf_counter()
+        tok = orc.argmax(logits)
+        t3 = time.perf_counter()
+        fwd, lm, am = fwd + (t1 - t0), lm + (t2 - t1), am + (t3 - t2)
         pos += 1
-    dt = time.perf_counter() - t0
     orm.close()
-    return n_tokens / dt, dt
+    b = {"matvec_ms": matvec_ms, "cached_forward_ms": fwd * 1000.0 / n_tokens,
+         "lm_head_ms": lm * 1000.0 / n_tokens, "argmax_ms": am * 1000.0 / n_tokens,
+         "ffn_block_ms": ffn_ms}
+    b["complete_token_ms"] = b["cached_forward_ms"] + b["lm_head_ms"] + b["argmax_ms"]
+    b["complete_tokens_per_second"] = 1000.0 / b["complete_token_ms"]
+    lm_bytes = V * (E // 256) * 210 + E * 4 + V * 4
+    gbps = {"i2s_2560x2560": 1_658_884 / (matvec_ms * 1e-3) / 1e9,
+            "q6k_lm_head_128256x2560": lm_bytes / (b["lm_head_ms"] * 1e-3) / 1e9,
+            "ffn_block_2560x6912": FFN_BLOCK_BYTES / (ffn_ms * 1e-3) / 1e9}
+    total_s = (matvec_ms * (reps + 1) + ffn_ms * 4) / 1000.0 + fwd + lm + am
+    return ({k: round(v, 4) for k, v in b.items()}, {k: round(v, 3) for k, v in gbps.items()}, total_s)
 
 
 def host_info():
@@ -436,7 +507,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=4)
-    ap.add_argument("--cpu-tokens", type=int, default=4)
+    ap.add_argument("--cpu-tokens", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batch", action="store_true", help="skip the ragged-batch measurement")
     ap.add_argument("--batch-steps", type=int, default=5)
@@ -510,6 +581,9 @@ def main():
     mv_single_gbps = mv_bytes / copies / (mv_single_ms / 1000.0) / 1e9
     log(f"i2_s 2560x2560 x{copies}: {mv_ms * 1000 / copies:.2f} us/matvec, {mv_gbps:.0f} GB/s")
 
+    ffn = ffn_block_stream(ctx, wh, bs, copies=40, reps=5)  # 40 x 13.3 MB = 533 MB
+    log(f"ffn block 2560x6912 (M = 1) x40: {ffn['us']:.2f} us/block, {ffn['gbps']:.0f} GB/s")
+
     batch = None
     if not args.no_batch:
         batch = ragged_batch(ctx, wh, bs, dev, cfg, args.batch_steps)
@@ -524,14 +598,17 @@ def main():
     cpu = None
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
-        cpu_tok_s, cpu_s = cpu_baseline(hm, cfg, args.cpu_tokens, threads)
-        cpu = {"value": round(cpu_tok_s, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-               "sample": f"{args.cpu_tokens} greedy tokens of the same workload (positions 1024..), "
-                         f"{cpu_s:.1f} s; BitLinear single-threaded, lm-head over {threads} threads",
+        bnd, cgbps, cpu_s = cpu_baseline(hm, cfg, args.cpu_tokens, threads)
+        cpu = {"value": bnd["complete_tokens_per_second"], "unit": "tok/s", "cores": threads,
+               "threads": {"bitlinear_forward_argmax": 1, "lm_head": threads}, "kind": "port",
+               "sample": f"{args.cpu_tokens} greedy decode steps of the same workload (positions "
+                         f"1024..) timed at cmd_bench_json's boundaries, plus 10 attn_q matvecs and "
+                         f"3 FFN blocks; {cpu_s:.1f} s of CPU time",
+               "boundaries": bnd, "derived_gbps": cgbps,
                "label": "C restatement of the reference's x86 SSE2 path (oracle/wm_oracle.c)",
                "host": host_info(),
                "compiler_flags": "gcc -O2 -ffp-contract=off -fno-fast-math (no -march=native)"}
-        log(f"cpu baseline: {cpu_tok_s:.3f} tok/s")
+        log("cpu baseline: " + ", ".join(f"{k} {v}" for k, v in bnd.items()))
 
     out = {
         "metric": METRIC,
@@ -565,10 +642,8 @@ def main():
             "q6k_lm_head_128256x2560": {
                 k: {"us": round(v * 1000, 2), "gbps": round(gbps[k], 1),
                     "frac": round(gbps[k] / HBM_PEAK_GBPS, 4)} for k, v in lm.items()},
-            # the FFN block at M = 1 (ffn_norm with the residual add, gate and
-            # up 6912x2560, relu(gate)^2 * up, ffn_sub_norm, down 2560x6912):
-            # the gate_up and down launches of the decode step, timed above
-            "ffn_block_2560x6912_m1": ffn_block(roles),
+            # the FFN block at M = 1 on its own inputs, over rotated weight copies
+            "ffn_block_2560x6912_m1": ffn,
             "i2s_2560x2560_rotated": {"gbps": round(mv_gbps, 1), "frac": round(mv_gbps / HBM_PEAK_GBPS, 4),
                                       "us_per_matvec": round(mv_ms * 1000 / copies, 3),
                                       "copies": copies},

@@ -165,6 +165,27 @@ wm_status wm_bitlinear_i2s_matmul_f32_dev(wm_ctx *ctx, const wm_tensor *w, const
 wm_status wm_bitlinear_i2s_matmul_f32(wm_ctx *ctx, const wm_tensor *w, const float *x,
                                       size_t x_len, uint32_t m, float *y, size_t y_len);
 
+/* ---- FFN block (src/model/ffn.rs) ------------------------------------ */
+
+/* ffn_block_forward (src/model/ffn.rs:73-136) for one token: RMSNorm of x
+ * (ffn_norm_weight, eps), the gate and up BitLinears, relu(gate)^2 * up,
+ * RMSNorm of that (ffn_sub_norm_weight, width n_ff), and the down BitLinear
+ * into output; no residual add.  n_embd = gate's in_dim, n_ff = gate's
+ * out_dim; up must be [n_embd, n_ff] and down [n_ff, n_embd].  The
+ * reference's length checks in its order: x_len, ffn_norm_len and output_len
+ * against n_embd, ffn_sub_norm_len against n_ff (WM_E_SHAPE).  Bit-identical
+ * to the reference: the norms' sums in its sequential order, the BitLinears
+ * exact. */
+wm_status wm_ffn_block_forward(wm_ctx *ctx, const float *x, size_t x_len, const float *ffn_norm_weight,
+                               size_t ffn_norm_len, const wm_tensor *gate, const wm_tensor *up,
+                               const wm_tensor *down, const float *ffn_sub_norm_weight,
+                               size_t ffn_sub_norm_len, float eps, float *output, size_t output_len);
+/* Device-pointer form (x, the two norm weights and output in device memory;
+ * the gate and up outputs in the context's scratch): two launches. */
+wm_status wm_ffn_block_forward_dev(wm_ctx *ctx, const float *d_x, const float *d_ffn_norm_weight,
+                                   const wm_tensor *gate, const wm_tensor *up, const wm_tensor *down,
+                                   const float *d_ffn_sub_norm_weight, float eps, float *d_output);
+
 /* ---- Q6_K / lm-head (src/model/q6_k.rs, lm_head.rs) ------------------ */
 
 /* Dequantise one row (src/model/q6_k.rs:59-69); embedding gather for a
@@ -342,7 +363,11 @@ wm_status wm_sampler_sample_dev(wm_sampler *s, const float *d_logits, size_t n, 
 /* generate_with_cache_and_sampler (src/model/generate.rs:195-277) on an
  * existing cache: observe the prompt, prefill it (batched), then up to
  * max_new sampled tokens (logits and sampling on the device), stopping at
- * `eos` (< 0: none) or any of stop_ids; each accepted id is observed. */
+ * `eos` (< 0: none) or any of stop_ids; each accepted id is observed.  On
+ * an error the cache goes back to its position at the call (the reference
+ * drops its own cache with the error) and *n_out is 0; the sampler keeps
+ * the ids it observed and its advanced rng, as the reference's caller-owned
+ * sampler does. */
 wm_status wm_generate_with_sampler(wm_model *m, wm_kv_cache *kv, const uint32_t *prompt,
                                    uint32_t n_prompt, uint32_t max_new, int64_t eos,
                                    const uint32_t *stop_ids, uint32_t n_stop, wm_sampler *s,

@@ -50,6 +50,8 @@ _SIGS = {
     "or_softmax_inplace": (None, _f32p, _sz),
     "or_relu_square_mul": (None, _f32p, _f32p, _sz, _f32p),
     "or_kv_quantise": (C.c_float, _f32p, _sz, _i8p),
+    "or_ffn_block_forward": (C.c_int, _f32p, _sz, _sz, _f32p, _u8p, C.c_float, _u8p, C.c_float,
+                             _u8p, C.c_float, _f32p, C.c_float, _f32p),
     "or_model_create": (_vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                         C.c_uint32, C.c_uint32, C.c_float, C.c_float),
     "or_model_destroy": (None, _vp),
@@ -182,6 +184,28 @@ def rms_norm(x, w, eps=1e-5):
     w = np.ascontiguousarray(w, dtype=np.float32)
     out = np.empty_like(x)
     lib.or_rms_norm(P(x, C.c_float), P(w, C.c_float), x.size, eps, P(out, C.c_float))
+    return out
+
+
+def ffn_block(x, ffn_norm_w, gate, gate_scale, up, up_scale, down, down_scale, ffn_sub_norm_w,
+              n_ff, eps=1e-5):
+    """ffn_block_forward (src/model/ffn.rs:73-136): n_embd = x.size; gate and
+    up are I2_S packed [n_embd -> n_ff], down [n_ff -> n_embd]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    E = x.size
+    nw = np.ascontiguousarray(ffn_norm_w, dtype=np.float32)
+    sw = np.ascontiguousarray(ffn_sub_norm_w, dtype=np.float32)
+    g, u, d = (np.ascontiguousarray(t, dtype=np.uint8) for t in (gate, up, down))
+    if nw.size != E or sw.size != n_ff or g.size < E // 4 * n_ff or u.size < E // 4 * n_ff \
+            or d.size < n_ff // 4 * E:
+        raise ValueError("ffn_block: length mismatch")
+    out = np.empty(E, dtype=np.float32)
+    rc = lib.or_ffn_block_forward(P(x, C.c_float), E, n_ff, P(nw, C.c_float), P(g, C.c_uint8),
+                                  C.c_float(gate_scale), P(u, C.c_uint8), C.c_float(up_scale),
+                                  P(d, C.c_uint8), C.c_float(down_scale), P(sw, C.c_float),
+                                  C.c_float(eps), P(out, C.c_float))
+    if rc:
+        raise ValueError(f"oracle ffn_block rejected input (rc={rc})")
     return out
 
 

@@ -681,6 +681,39 @@ static void attention_position_zero(or_model *m) {
     }
 }
 
+/* ffn_block_forward (src/model/ffn.rs:73-136): ffn_norm, the gate and up
+ * BitLinears, relu_square of gate then elementwise_mul with up, ffn_sub_norm
+ * (width n_ff) and the down BitLinear into out; no residual add.  The
+ * model's layer runs this same function (apply_ffn_block,
+ * src/model/cached_forward.rs:451-502, the same sequence).  xf (E), g, u,
+ * fused, fused_norm (F each) are scratch. */
+static int ffn_block(const or_lin *gate, const or_lin *up, const or_lin *down, const float *norm_w,
+                     const float *sub_norm_w, size_t E, size_t F, float eps, const float *x,
+                     float *xf, float *g, float *u, float *fused, float *fused_norm, float *out) {
+    int rc;
+    or_rms_norm(x, norm_w, E, eps, xf);
+    if ((rc = linear(gate, E, F, xf, g))) return rc;
+    if ((rc = linear(up, E, F, xf, u))) return rc;
+    or_relu_square_mul(g, u, F, fused);
+    or_rms_norm(fused, sub_norm_w, F, eps, fused_norm);
+    return linear(down, F, E, fused_norm, out);
+}
+
+int or_ffn_block_forward(const float *x, size_t n_embd, size_t n_ff, const float *ffn_norm_w,
+                         const uint8_t *gate, float gate_scale, const uint8_t *up, float up_scale,
+                         const uint8_t *down, float down_scale, const float *ffn_sub_norm_w,
+                         float eps, float *out) {
+    if (!x || !ffn_norm_w || !gate || !up || !down || !ffn_sub_norm_w || !out) return -2;
+    const or_lin lg = {gate, gate_scale}, lu = {up, up_scale}, ld = {down, down_scale};
+    float *buf = (float *)malloc((n_embd + 4 * n_ff) * sizeof(float));
+    if (!buf) return -5;
+    int rc = ffn_block(&lg, &lu, &ld, ffn_norm_w, ffn_sub_norm_w, n_embd, n_ff, eps, x, buf,
+                       buf + n_embd, buf + n_embd + n_ff, buf + n_embd + 2 * n_ff,
+                       buf + n_embd + 3 * n_ff, out);
+    free(buf);
+    return rc;
+}
+
 /* src/model/cached_forward.rs:308-415 + apply_ffn_block :451-502; with kv
  * NULL, transformer_block_forward_position_zero (src/model/block.rs:38-105):
  * the same layer at position 0 with attention_position_zero and no cache */
@@ -710,12 +743,9 @@ static int forward_one_layer(or_model *m, or_kv *kv, uint32_t l, uint32_t pos) {
     or_rms_norm(m->attn_out, L->attn_sub_norm, E, m->eps, m->sub);
     if ((rc = linear(&L->o, E, E, m->sub, m->wo))) return rc;
     for (size_t d = 0; d < E; d++) m->hidden[d] += m->wo[d];
-    or_rms_norm(m->hidden, L->ffn_norm, E, m->eps, m->xf);
-    if ((rc = linear(&L->gate, E, F, m->xf, m->gate))) return rc;
-    if ((rc = linear(&L->up, E, F, m->xf, m->up))) return rc;
-    or_relu_square_mul(m->gate, m->up, F, m->fused);
-    or_rms_norm(m->fused, L->ffn_sub_norm, F, m->eps, m->fused_norm);
-    if ((rc = linear(&L->down, F, E, m->fused_norm, m->down))) return rc;
+    if ((rc = ffn_block(&L->gate, &L->up, &L->down, L->ffn_norm, L->ffn_sub_norm, E, F, m->eps,
+                        m->hidden, m->xf, m->gate, m->up, m->fused, m->fused_norm, m->down)))
+        return rc;
     for (size_t d = 0; d < E; d++) m->hidden[d] += m->down[d];
     if (!finite_all(m->hidden, E)) return -3; /* cached_forward.rs:511-521 */
     return 0;
@@ -958,10 +988,16 @@ int or_sample(const or_sampling_params *p, uint64_t *state, const uint32_t *hist
     if (p->has_repetition_penalty)
         or_apply_repetition_penalty(buf, n, history, n_history, p->repetition_penalty);
     or_apply_temperature(buf, n, p->temperature);
-    if (p->has_top_k) or_apply_top_k(buf, n, p->top_k);
-    or_softmax_to_probs(buf, n, probs);
     int rc = 0;
-    if (p->has_top_p) {
+    /* top-k sorts only when 0 < k < n (sampler.rs:202-212); a NaN among the
+     * values it sorts leaves the k-th largest open (the comparator is then
+     * no order), so that case is refused, as NaN under top-p is */
+    if (p->has_top_k && p->top_k > 0 && p->top_k < n)
+        for (size_t i = 0; i < n && !rc; i++)
+            if (isnan(buf[i])) rc = -3;
+    if (p->has_top_k && !rc) or_apply_top_k(buf, n, p->top_k);
+    if (!rc) or_softmax_to_probs(buf, n, probs);
+    if (p->has_top_p && !rc) {
         if (p->top_p > 0.0f && p->top_p < 1.0f)
             for (size_t i = 0; i < n && !rc; i++)
                 if (isnan(probs[i])) rc = -3;

@@ -67,6 +67,12 @@ void or_rope_neox(float *x, size_t head_dim, size_t n_rot, uint32_t pos, float f
 void or_softmax_inplace(float *x, size_t n);
 /* src/model/ffn.rs:37-65: out = relu(gate)^2 * up */
 void or_relu_square_mul(const float *gate, const float *up, size_t n, float *out);
+/* src/model/ffn.rs:73-136: ffn_norm, gate/up (I2_S packed, in_dim n_embd,
+ * out_dim n_ff), relu^2 * up, ffn_sub_norm, down (in n_ff, out n_embd) */
+int or_ffn_block_forward(const float *x, size_t n_embd, size_t n_ff, const float *ffn_norm_w,
+                         const uint8_t *gate, float gate_scale, const uint8_t *up, float up_scale,
+                         const uint8_t *down, float down_scale, const float *ffn_sub_norm_w,
+                         float eps, float *out);
 /* src/model/kv_cache.rs:245-259: q + scale for one token; returns the scale */
 float or_kv_quantise(const float *x, size_t n, int8_t *q);
 /* src/model/cached_forward.rs:417-449: q[n_heads*head_dim] attends to n_past

@@ -1,6 +1,11 @@
 // Token sampling on the device (gfx950): Sampler::sample
 // (src/model/sampler.rs:133-196), bit-identical to the reference on the same
-// logits, parameters and xorshift64 state.
+// logits, parameters and xorshift64 state, with two cases the reference
+// leaves open: its top-k and top-p sorts are unstable, so equal values that
+// straddle the cut may come in any order there (here: index order, equal to
+// the reference whenever no such tie straddles the cut), and with NaN values
+// their comparator is not an order at all, so the kept set is unspecified
+// (here: an error, under top-k and top-p alike).
 //
 // The reference, on a copy of the logits:
 //   repetition penalty (:151-164)   each distinct history id once:
@@ -41,7 +46,7 @@ enum : uint32_t {
     SAMPLE_RUNNING = 0,
     SAMPLE_DONE = 1,         // id valid
     SAMPLE_NOT_POSITIVE = 2, // multinomial: total <= 0 or not finite (total valid)
-    SAMPLE_NAN_TOP_P = 3,    // NaN probabilities under top-p with 0 < p < 1
+    SAMPLE_NAN_ORDER = 3,    // NaN values to sort: top-k's logits, or top-p's probabilities
 };
 
 struct sample_state {
@@ -191,12 +196,18 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_pre(sample_args a) {
         }
         __syncthreads();
     }
+    int bad = 0;
     for (uint32_t i = tid; i < n; i += kSampleThreads) {
         float v = a.work[i];
         if (a.use_temp) v = v * a.inv_t;
         a.work[i] = v;
-        if (a.topk_mode == TOPK_THRESHOLD) a.keys[i] = order_key(v);
+        if (a.topk_mode == TOPK_THRESHOLD) {
+            a.keys[i] = order_key(v);
+            bad |= isnan(v);
+        }
     }
+    // a NaN among the values top-k sorts leaves the k-th largest unspecified
+    if (__syncthreads_or(bad) && tid == 0) a.st->status = SAMPLE_NAN_ORDER;
 }
 
 // Top-k mask, softmax_to_probs, and top-p's one-hot case or its sort keys.
@@ -243,7 +254,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample_probs(sample_args a) 
             a.keys[i] = order_key(v);
             a.vals[i] = i;
         }
-        if (__syncthreads_or(bad) && tid == 0) a.st->status = SAMPLE_NAN_TOP_P;
+        if (__syncthreads_or(bad) && tid == 0) a.st->status = SAMPLE_NAN_ORDER;
     }
 }
 
@@ -460,9 +471,11 @@ wm_status wm_sampler_run(wm_sampler *sp, const float *d_logits, uint32_t n, uint
         return wm_set_error(ctx, WM_E_PARSE,
                             "multinomial: probabilities do not sum to a positive finite value (%s)", v);
     }
-    if (st.status == SAMPLE_NAN_TOP_P)
+    if (st.status == SAMPLE_NAN_ORDER)
         return wm_set_error(ctx, WM_E_NONFINITE,
-                            "sample: NaN probabilities under top-p (their order is unspecified)");
+                            a.topp_mode == TOPP_CUT && a.topk_mode != TOPK_THRESHOLD
+                                ? "sample: NaN probabilities under top-p (their order is unspecified)"
+                                : "sample: NaN values under top-k or top-p (their order is unspecified)");
     if (st.status != SAMPLE_DONE) return wm_set_error(ctx, WM_E_STATE, "sample: did not finish");
     if (!greedy) sp->state = next_state;
     *out_id = st.id;

@@ -81,7 +81,8 @@ struct wm_model {
     float *k_new = nullptr, *v_new = nullptr;  // this token's K (after RoPE) and V
     float *proj_out = nullptr;  // O's, then down's f32 output (the next norm adds it to hidden)
     float *logits = nullptr, *scores = nullptr;
-    uint32_t *dscalars = nullptr;  // [0] token, [1] next token, [2] error flag, [4..5] K/V absmax
+    uint32_t *dscalars = nullptr;  // [0] token, [1] next token, [2] error flag, [3] greedy loop's
+                                   // position, [4..5] K/V absmax
     void *lm_work = nullptr;
     // ragged-batch workspace, grown on demand to b_cap tokens
     uint8_t *bws = nullptr;
@@ -1056,6 +1057,15 @@ wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *promp
         return wm_set_error(ctx, WM_E_NONFINITE, "forward_with_cache: non-finite hidden after layer %u",
                             failed_flag - 1);
     }
+    if (enq > done) {
+        // Steps queued past an EOS stop ran as well, and the error flag is
+        // cumulative: one of them (the EOS token's own step, say) may have
+        // raised it.  The steps kept were all found finite above, so the
+        // flag is cleared rather than left to fail the next call.
+        m->ring[0] = 0;
+        WM_HIP(ctx, hipMemcpyAsync(m->dscalars + 2, m->ring, 4, hipMemcpyHostToDevice, ctx->stream));
+        WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    }
     kv->pos = pos0 + done;
     *n_out = n;
     return WM_OK;
@@ -1166,6 +1176,15 @@ wm_status wm_generate_with_sampler(wm_model *m, wm_kv_cache *kv, const uint32_t 
         out_ids[n++] = next;
         wm_sampler_observe(s, next);
         if (step + 1 < max_new && (st = step_with_logits(m, kv, next))) break;
+    }
+    if (st) {
+        // The reference builds its cache inside the call and drops it with
+        // the error (generate.rs:237); here the cache is the caller's,
+        // so it goes back to where the call found it, as after a failed
+        // greedy generation.  The sampler is the caller's in both: its
+        // history and rng keep every id sampled before the error.
+        kv->pos = start;
+        n = 0;
     }
     *n_out = n;
     return st;

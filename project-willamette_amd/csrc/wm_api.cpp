@@ -406,6 +406,114 @@ wm_status wm_bitlinear_i2s_matvec_f32_dev(wm_ctx *ctx, const wm_tensor *w, const
     return WM_OK;
 }
 
+// ---------------------------------------------------------------------------
+// FFN block (ffn_block_forward, src/model/ffn.rs:73-136)
+// ---------------------------------------------------------------------------
+
+// The shapes the block needs: gate and up [n_embd -> n_ff], down [n_ff ->
+// n_embd], all I2_S of this context.  n_embd and n_ff come from gate.
+static wm_status check_ffn(wm_ctx *ctx, const wm_tensor *gate, const wm_tensor *up,
+                           const wm_tensor *down) {
+    wm_status st;
+    if ((st = check_i2s(ctx, gate)) || (st = check_i2s(ctx, up)) || (st = check_i2s(ctx, down)))
+        return st;
+    const uint64_t E = gate->in_dim, F = gate->out_dim;
+    if (up->in_dim != E || up->out_dim != F)
+        return wm_set_error(ctx, WM_E_SHAPE, "ffn_block_forward: ffn_up shape [%llu, %llu] != [%llu, %llu]",
+                            (unsigned long long)up->in_dim, (unsigned long long)up->out_dim,
+                            (unsigned long long)E, (unsigned long long)F);
+    if (down->in_dim != F || down->out_dim != E)
+        return wm_set_error(ctx, WM_E_SHAPE,
+                            "ffn_block_forward: ffn_down shape [%llu, %llu] != [%llu, %llu]",
+                            (unsigned long long)down->in_dim, (unsigned long long)down->out_dim,
+                            (unsigned long long)F, (unsigned long long)E);
+    return WM_OK;
+}
+
+// Two launches: ffn_norm + gate and up (each workgroup evaluates the norm
+// and its int8 codes itself), then relu(gate)^2 * up + ffn_sub_norm + down.
+// gu: 2 * n_ff floats of device scratch for the gate and up outputs.
+static wm_status run_ffn(wm_ctx *ctx, const float *d_x, const float *d_norm_w, const wm_tensor *gate,
+                         const wm_tensor *up, const wm_tensor *down, const float *d_sub_w, float eps,
+                         float *d_out, float *gu) {
+    const uint32_t F = (uint32_t)gate->out_dim;
+    wm_fused_norm fn{};
+    fn.x = d_x;
+    fn.w = d_norm_w;
+    fn.eps = eps;
+    const wm_i2s_desc gud[2] = {{(const uint8_t *)gate->d, gate->n_groups},
+                                {(const uint8_t *)up->d, up->n_groups}};
+    const float gus[2] = {gate->scale, up->scale};
+    float *guo[2] = {gu, gu + F};
+    wm_fused_norm dn{};
+    dn.x = gu;
+    dn.y = gu + F;
+    dn.relu2_mul = 1;
+    dn.w = d_sub_w;
+    dn.eps = eps;
+    const wm_i2s_desc dd = {(const uint8_t *)down->d, down->n_groups};
+    float *dout[1] = {d_out};
+    if (!wm_launch_i2s_fused(WM_FUSED_PLAIN, gud, gus, guo, 2, gate->n_chunks, 1, fn, nullptr, nullptr,
+                             0, 0, 0, nullptr, ctx->stream) ||
+        !wm_launch_i2s_fused(WM_FUSED_PLAIN, &dd, &down->scale, dout, 1, down->n_chunks, 1, dn, nullptr,
+                             nullptr, 0, 0, 0, nullptr, ctx->stream))
+        return wm_set_error(ctx, WM_E_SHAPE, "ffn_block_forward: no kernel for n_embd %llu, n_ff %llu",
+                            (unsigned long long)gate->in_dim, (unsigned long long)F);
+    WM_HIP(ctx, hipGetLastError());
+    return WM_OK;
+}
+
+wm_status wm_ffn_block_forward_dev(wm_ctx *ctx, const float *d_x, const float *d_ffn_norm_weight,
+                                   const wm_tensor *gate, const wm_tensor *up, const wm_tensor *down,
+                                   const float *d_ffn_sub_norm_weight, float eps, float *d_output) {
+    if (!ctx || !d_x || !d_ffn_norm_weight || !d_ffn_sub_norm_weight || !d_output) return WM_E_ARG;
+    wm_status st = check_ffn(ctx, gate, up, down);
+    if (st) return st;
+    void *scratch;
+    if ((st = wm_ctx_scratch(ctx, align256(gate->out_dim * 8), &scratch))) return st;
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    return run_ffn(ctx, d_x, d_ffn_norm_weight, gate, up, down, d_ffn_sub_norm_weight, eps, d_output,
+                   (float *)scratch);
+}
+
+wm_status wm_ffn_block_forward(wm_ctx *ctx, const float *x, size_t x_len, const float *ffn_norm_weight,
+                               size_t ffn_norm_len, const wm_tensor *gate, const wm_tensor *up,
+                               const wm_tensor *down, const float *ffn_sub_norm_weight,
+                               size_t ffn_sub_norm_len, float eps, float *output, size_t output_len) {
+    if (!ctx || !x || !ffn_norm_weight || !ffn_sub_norm_weight || !output) return WM_E_ARG;
+    wm_status st = check_ffn(ctx, gate, up, down);
+    if (st) return st;
+    const uint64_t E = gate->in_dim, F = gate->out_dim;
+    // the reference's checks, in its order (ffn.rs:87-114)
+    if (x_len != E)
+        return wm_set_error(ctx, WM_E_SHAPE, "ffn_block_forward: x.len()=%zu != n_embd=%llu", x_len,
+                            (unsigned long long)E);
+    if (ffn_norm_len != E)
+        return wm_set_error(ctx, WM_E_SHAPE, "ffn_block_forward: ffn_norm_weight.len()=%zu != n_embd=%llu",
+                            ffn_norm_len, (unsigned long long)E);
+    if (ffn_sub_norm_len != F)
+        return wm_set_error(ctx, WM_E_SHAPE,
+                            "ffn_block_forward: ffn_sub_norm_weight.len()=%zu != n_ff=%llu",
+                            ffn_sub_norm_len, (unsigned long long)F);
+    if (output_len != E)
+        return wm_set_error(ctx, WM_E_SHAPE, "ffn_block_forward: output.len()=%zu != n_embd=%llu",
+                            output_len, (unsigned long long)E);
+    WM_HIP(ctx, hipSetDevice(ctx->device));
+    const size_t eb = align256(E * 4), fb = align256(F * 4);
+    void *scratch;
+    if ((st = wm_ctx_scratch(ctx, 3 * eb + 3 * fb, &scratch))) return st;
+    uint8_t *b = (uint8_t *)scratch;
+    float *d_x = (float *)b, *d_nw = (float *)(b + eb), *d_out = (float *)(b + 2 * eb);
+    float *d_sw = (float *)(b + 3 * eb), *gu = (float *)(b + 3 * eb + fb);
+    WM_HIP(ctx, hipMemcpyAsync(d_x, x, E * 4, hipMemcpyHostToDevice, ctx->stream));
+    WM_HIP(ctx, hipMemcpyAsync(d_nw, ffn_norm_weight, E * 4, hipMemcpyHostToDevice, ctx->stream));
+    WM_HIP(ctx, hipMemcpyAsync(d_sw, ffn_sub_norm_weight, F * 4, hipMemcpyHostToDevice, ctx->stream));
+    if ((st = run_ffn(ctx, d_x, d_nw, gate, up, down, d_sw, eps, d_out, gu))) return st;
+    WM_HIP(ctx, hipMemcpyAsync(output, d_out, E * 4, hipMemcpyDeviceToHost, ctx->stream));
+    WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return WM_OK;
+}
+
 wm_status wm_bitlinear_i2s_matvec_f32_multi_dev(wm_ctx *ctx, const wm_tensor *const *ws,
                                                 uint32_t n_copies, const float *d_input,
                                                 float *d_outputs) {

@@ -364,7 +364,8 @@ struct wm_i2s_desc {
 struct wm_fused_norm {
     const float *x;         // the norm's input
     const float *y;         // nullable: residual, the norm runs on x + y
-    float *x_out;           // nullable: x + y written here (by one workgroup; never x itself)
+    float *x_out;           // nullable: x + y written here, each workgroup its contiguous share
+                            // (never x itself)
     const float *w;         // norm weight
     float eps;
     uint32_t *err_flag;     // nullable: set to layer_tag when x + y is not all finite

@@ -129,6 +129,9 @@ EXPORTS = {
     "wm_bitlinear_i2s_matvec_f32_debug": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p,
                                           C.c_size_t, _i8p, _f32p, _i32p),
     "wm_bitlinear_i2s_matvec_f32_dev": (C.c_int, _vp, _vp, _vp, _vp),
+    "wm_ffn_block_forward": (C.c_int, _vp, _vp, C.c_size_t, _vp, C.c_size_t, _vp, _vp, _vp, _vp,
+                             C.c_size_t, C.c_float, _vp, C.c_size_t),
+    "wm_ffn_block_forward_dev": (C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp),
     "wm_bitlinear_i2s_matvec_f32_scalar": (C.c_int, _vp, _vp, _f32p, C.c_size_t, _f32p, C.c_size_t),
     "wm_bitlinear_i2s_matvec_f32_scalar_dev": (C.c_int, _vp, _vp, _vp, _vp),
     "wm_bitlinear_i2s_matvec_f32_dev_noalloc": (C.c_int, _vp, _vp, _vp, _vp),
@@ -450,6 +453,20 @@ def bitlinear_i2s_matvec_f32(ctx: Context, w: Tensor, x: np.ndarray, debug: bool
                                                     _ptr(y, C.c_float), y.size, _ptr(act, C.c_int8),
                                                     C.byref(sc), _ptr(acc, C.c_int32)))
     return y, act, float(np.float32(sc.value)), acc
+
+
+def ffn_block_forward(ctx: Context, x, ffn_norm_weight, gate: Tensor, up: Tensor, down: Tensor,
+                      ffn_sub_norm_weight, eps: float = 1e-5) -> np.ndarray:
+    """ffn_block_forward (src/model/ffn.rs:73-136): ffn_norm, gate and up,
+    relu(gate)^2 * up, ffn_sub_norm, down; no residual add."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    nw = np.ascontiguousarray(ffn_norm_weight, dtype=np.float32)
+    sw = np.ascontiguousarray(ffn_sub_norm_weight, dtype=np.float32)
+    y = np.empty(gate.shape[0], dtype=np.float32)
+    ctx.check(lib.wm_ffn_block_forward(ctx.h, _ptr(x, C.c_float), x.size, _ptr(nw, C.c_float), nw.size,
+                                       gate.h, up.h, down.h, _ptr(sw, C.c_float), sw.size, eps,
+                                       _ptr(y, C.c_float), y.size))
+    return y
 
 
 def bitlinear_i2s_matvec_f32_scalar(ctx: Context, w: Tensor, x: np.ndarray) -> np.ndarray:

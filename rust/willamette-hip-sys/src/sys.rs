@@ -111,6 +111,8 @@ extern "C" {
     pub fn wm_bitlinear_i2s_matvec_f32_dev_noalloc(ctx: *mut wm_ctx, w: *const wm_tensor, d_input: *const f32, d_output: *mut f32) -> wm_status;
     pub fn wm_bitlinear_i2s_matmul_f32_dev(ctx: *mut wm_ctx, w: *const wm_tensor, d_x: *const f32, m: u32, d_y: *mut f32) -> wm_status;
     pub fn wm_bitlinear_i2s_matmul_f32(ctx: *mut wm_ctx, w: *const wm_tensor, x: *const f32, x_len: usize, m: u32, y: *mut f32, y_len: usize) -> wm_status;
+    pub fn wm_ffn_block_forward(ctx: *mut wm_ctx, x: *const f32, x_len: usize, ffn_norm_weight: *const f32, ffn_norm_len: usize, gate: *const wm_tensor, up: *const wm_tensor, down: *const wm_tensor, ffn_sub_norm_weight: *const f32, ffn_sub_norm_len: usize, eps: f32, output: *mut f32, output_len: usize) -> wm_status;
+    pub fn wm_ffn_block_forward_dev(ctx: *mut wm_ctx, d_x: *const f32, d_ffn_norm_weight: *const f32, gate: *const wm_tensor, up: *const wm_tensor, down: *const wm_tensor, d_ffn_sub_norm_weight: *const f32, eps: f32, d_output: *mut f32) -> wm_status;
     pub fn wm_q6k_dequantize_row(ctx: *mut wm_ctx, t: *const wm_tensor, row: u64, out: *mut f32, out_len: usize) -> wm_status;
     pub fn wm_compute_logits(ctx: *mut wm_ctx, token_embd: *const wm_tensor, hidden: *const f32, hidden_len: usize, logits: *mut f32, vocab: usize) -> wm_status;
     pub fn wm_logits_argmax(ctx: *mut wm_ctx, token_embd: *const wm_tensor, hidden: *const f32, hidden_len: usize, logits: *mut f32, argmax: *mut u32) -> wm_status;

@@ -89,6 +89,24 @@ class Mistakes:
     rope_pairs: str = "neox"     # "neox": (j, j + hd/2); "adjacent": (2j, 2j + 1)
     relu_square: bool = True     # relu(gate)^2 * up; False: relu(gate) * up
     rope_on_k: bool = True
+    ffn_sub_norm: bool = True    # ffn_sub_norm before down
+    gate_up_swapped: bool = False  # relu(up)^2 * gate
+
+
+def ffn_block(t_gate, s_gate, t_up, s_up, t_down, s_down, norm_w, sub_norm_w, eps, x,
+              mk: Mistakes | None = None) -> np.ndarray:
+    """ffn_block_forward (src/model/ffn.rs:73-136), no residual: ffn_norm ->
+    gate, up -> relu(gate)^2 * up -> ffn_sub_norm -> down."""
+    mk = mk or Mistakes()
+    xf = rms_norm(x, norm_w, eps)
+    g = bitlinear(t_gate, s_gate, xf)
+    u = bitlinear(t_up, s_up, xf)
+    if mk.gate_up_swapped:
+        g, u = u, g
+    r = np.maximum(g, 0.0)
+    f = (r * r if mk.relu_square else r) * u
+    fn = rms_norm(f, sub_norm_w, eps) if mk.ffn_sub_norm else f
+    return bitlinear(t_down, s_down, fn)
 
 
 class NpModel:
@@ -165,13 +183,9 @@ class NpModel:
         o = bitlinear(T["attn_output"], sc["attn_output"], a)
         if self.mk.o_residual:
             x = x + o
-        xf = rms_norm(x, nm["ffn_norm"], eps)
-        g = bitlinear(T["ffn_gate"], sc["ffn_gate"], xf)
-        u = bitlinear(T["ffn_up"], sc["ffn_up"], xf)
-        r = np.maximum(g, 0.0)
-        f = (r * r if self.mk.relu_square else r) * u
-        fn = rms_norm(f, nm["ffn_sub_norm"], eps)
-        return x + bitlinear(T["ffn_down"], sc["ffn_down"], fn), k, v
+        y = ffn_block(T["ffn_gate"], sc["ffn_gate"], T["ffn_up"], sc["ffn_up"], T["ffn_down"],
+                      sc["ffn_down"], nm["ffn_norm"], nm["ffn_sub_norm"], eps, x, self.mk)
+        return x + y, k, v
 
     def output(self, x: np.ndarray) -> np.ndarray:
         return rms_norm(x, self.hm.output_norm.astype(np.float64), self.cfg.rms_eps)

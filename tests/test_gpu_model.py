@@ -202,6 +202,58 @@ def test_greedy_nonfinite_step_with_steps_in_flight(ctx):
     orm.close()
 
 
+def _inf_embedding_model(cfg, seed, token):
+    """The host model with an infinite Q6_K d in block 0 of `token`'s
+    embedding row: the step that embeds it goes non-finite, and its tied
+    lm-head logit is +-inf."""
+    hm = bs.make_host_model(cfg, seed=seed)
+    row0 = token * (cfg.n_embd // 256) * 210
+    hm.token_embd.reshape(-1)[row0 + 208:row0 + 210] = [0x00, 0x7C]  # d = +inf (f16)
+    return hm
+
+
+def test_greedy_eos_clears_error_flag_of_steps_in_flight(ctx):
+    """Steps queued past an EOS stop still run.  Here the EOS token's own
+    embedding row has an infinite d, so the step queued behind the one that
+    produced EOS embeds it and raises the cumulative error flag.  The call
+    still returns the ids before EOS, and the next calls decode like the
+    oracle instead of failing with NonFinite."""
+    cfg = SMALL
+    for X in range(60, 400):  # an EOS id the greedy trajectory reaches after >= 2 ids
+        hm = _inf_embedding_model(cfg, 6, X)
+        orm = OracleModel(hm)
+        okv = orm.kv(cfg.context_length)
+        okv.forward(1, 0)
+        want = okv.greedy([2, 5], max_new=10, eos=X)
+        if 2 <= len(want) <= 7:
+            break
+        orm.close()
+    else:
+        pytest.fail("no EOS id in range")
+    print(f"eos id {X}, ids before it {want}", flush=True)
+    dev = bs.load_device_model(ctx, hm)
+    dkv = dev.kv_cache(cfg.context_length)
+    dkv.forward(1, 0)
+    assert dkv.greedy([2, 5], max_new=10, eos=X) == want
+    assert dkv.position == okv.position
+    # the flag left by the step past EOS must not fail these
+    assert dkv.greedy([3], max_new=6, eos=X) == okv.greedy([3], max_new=6, eos=X)
+    assert bits_equal(dkv.forward(4, dkv.position), okv.forward(4, okv.position))
+    # generate_with_sampler (greedy parameters: the same trajectory, no EOS)
+    # reaches X and fails on the step that embeds it: the cache goes back to
+    # where the call found it
+    dkv2 = dev.kv_cache(cfg.context_length)
+    dkv2.forward(1, 0)
+    with pytest.raises(wh.WillametteError) as e:
+        dkv2.generate_sampled([2, 5], 10, wh.Sampler(ctx, wh.SamplingParams.make(), 7))
+    assert e.value.kind == "NonFinite" and dkv2.position == 1
+    okv2 = orm.kv(cfg.context_length)
+    okv2.forward(1, 0)
+    assert bits_equal(dkv2.forward(3, 1), okv2.forward(3, 1))
+    dev.close()
+    orm.close()
+
+
 def test_zero_weight_model_closed_form(ctx):
     """tests/synthetic_model.rs analogue: all-zero ternary weights, unit norms,
     an all-ones embedding -> every BitLinear outputs 0, the hidden stays the

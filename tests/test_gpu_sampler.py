@@ -82,7 +82,8 @@ def test_sample_dev_logits_and_ties(ctx):
 
 
 @pytest.mark.parametrize("case", ["all_neg_inf", "top_k_zero", "nan_plain", "nan_top_p",
-                                  "nan_top_p_one_hot", "inf", "tiny_temperature", "empty"])
+                                  "nan_top_p_one_hot", "nan_top_k", "nan_top_k_all", "inf",
+                                  "tiny_temperature", "empty"])
 def test_sample_errors_match(ctx, case):
     logits = np.array([0.5, -1.0, 2.0, 0.25], np.float32)
     kw = dict(temperature=1.0)
@@ -95,6 +96,12 @@ def test_sample_errors_match(ctx, case):
     elif case == "nan_top_p":
         logits[1] = np.nan
         kw["top_p"] = 0.5
+    elif case == "nan_top_k":  # top-k sorts: a NaN leaves its k-th largest open
+        logits[1] = np.nan
+        kw["top_k"] = 2
+    elif case == "nan_top_k_all":  # k >= n sorts nothing: the NaN reaches the multinomial
+        logits[1] = np.nan
+        kw["top_k"] = 4
     elif case == "nan_top_p_one_hot":
         logits[:] = -np.inf
         kw["top_p"] = 0.0

@@ -20,6 +20,7 @@ import pytest
 import bitnet_synth as bs
 import np_bitnet as nb
 import oracle.oracle as orc
+import willamette_hip as wh
 from oracle.oracle_model import OracleModel
 
 f32 = np.float32
@@ -341,4 +342,78 @@ def test_position_zero_nonfinite_fails():
     orm = OracleModel(hm)
     with pytest.raises(RuntimeError):
         orm.forward_position_zero(1)
+    orm.close()
+
+
+# ---------------------------------------------------------------------------
+# the FFN block on its own (ffn_block_forward, src/model/ffn.rs:73-136)
+# ---------------------------------------------------------------------------
+
+FFN_MISTAKES = {
+    "relu_not_squared": nb.Mistakes(relu_square=False),
+    "no_ffn_sub_norm": nb.Mistakes(ffn_sub_norm=False),
+    "gate_up_swapped": nb.Mistakes(gate_up_swapped=True),
+}
+
+
+def ffn_inputs(E, F, seed):
+    """The FFN block's own inputs: I2_S gate/up [E -> F] and down [F -> E]
+    with uniform ternary codes, per-tensor scales ~U(0.5, 2), norm weights
+    ~U(0.9, 1.1), x ~N(0, 1) fed straight into ffn_norm."""
+    g, u, d = wh.synth_i2s(seed, 1, E, F), wh.synth_i2s(seed, 2, E, F), wh.synth_i2s(seed, 3, F, E)
+    sc = wh.synth_uniform(seed, 4, 3, 0.5, 2.0)
+    nw, sw = wh.synth_uniform(seed, 5, E, 0.9, 1.1), wh.synth_uniform(seed, 6, F, 0.9, 1.1)
+    return g, u, d, sc, nw, sw, wh.synth_normal(seed, 7, E)
+
+
+def ffn_twin(E, F, g, u, d, sc, nw, sw, x, mk=None):
+    return nb.ffn_block(nb.unpack_ternary(g, E, F), float(sc[0]), nb.unpack_ternary(u, E, F),
+                        float(sc[1]), nb.unpack_ternary(d, F, E), float(sc[2]),
+                        nw.astype(np.float64), sw.astype(np.float64), 1e-5, x.astype(np.float64), mk)
+
+
+@pytest.mark.parametrize("E,F", [(2560, 6912), (256, 384)], ids=["bitnet2b", "small"])
+def test_ffn_block_matches_float64_twin_and_catches_mistakes(E, F):
+    g, u, d, sc, nw, sw, x = ffn_inputs(E, F, bs.master_seed(3) + E)
+    y = orc.ffn_block(x, nw, g, sc[0], u, sc[1], d, sc[2], sw, F)
+    r = ffn_twin(E, F, g, u, d, sc, nw, sw, x)
+    assert np.abs(y - r).max() <= LAYER_TOL * np.abs(r).max()
+    for name, mk in FFN_MISTAKES.items():
+        bad = ffn_twin(E, F, g, u, d, sc, nw, sw, x, mk)
+        assert np.abs(bad - r).max() > 1000 * LAYER_TOL * np.abs(r).max(), name
+
+
+def test_ffn_block_zero_input_and_determinism():
+    """tests/ffn.rs: zero input gives exactly zero output (RMSNorm of zeros is
+    zeros, every quantiser sees absmax 0), and two calls agree bit for bit."""
+    E, F = 2560, 6912
+    g, u, d, sc, nw, sw, x = ffn_inputs(E, F, 11)
+    z = orc.ffn_block(np.zeros(E, np.float32), nw, g, sc[0], u, sc[1], d, sc[2], sw, F)
+    assert np.array_equal(z.view(np.uint32), np.zeros(E, np.uint32))
+    a = orc.ffn_block(x, nw, g, sc[0], u, sc[1], d, sc[2], sw, F)
+    b = orc.ffn_block(x, nw, g, sc[0], u, sc[1], d, sc[2], sw, F)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)) and np.all(np.isfinite(a))
+    assert np.count_nonzero(a) > E // 2
+
+
+def test_ffn_block_is_the_models_ffn():
+    """The model's layer runs the same block: a one-layer model whose
+    attention weights are all zero (codes 01) adds nothing before the FFN, so
+    its hidden after the layer is embedding + ffn_block(embedding)."""
+    cfg = bs.BitNetConfig(n_layers=1, n_embd=256, n_ff=384, n_heads=2, n_kv_heads=1, head_dim=128,
+                          vocab=50, context_length=8)
+    hm = bs.make_host_model(cfg, seed=77)
+    L = hm.layers[0]
+    for r in ("attn_q", "attn_k", "attn_v", "attn_output"):
+        L.packed[r][:] = 0x55
+    orm = OracleModel(hm)
+    okv = orm.kv(cfg.context_length)
+    _, tr = okv.forward(7, 0, trace=True)
+    x = nb.q6k_dequant(hm.token_embd.reshape(cfg.vocab, -1)[7], cfg.n_embd)[0].astype(np.float32)
+    y = orc.ffn_block(x, L.norms["ffn_norm"], L.packed["ffn_gate"], L.scales["ffn_gate"],
+                      L.packed["ffn_up"], L.scales["ffn_up"], L.packed["ffn_down"],
+                      L.scales["ffn_down"], L.norms["ffn_sub_norm"], cfg.n_ff, cfg.rms_eps)
+    # hidden += O (all zeros: turns a -0 of the embedding into +0), then += down
+    h = (x + np.zeros_like(x)) + y
+    assert np.array_equal(h.view(np.uint32), tr[0].view(np.uint32))
     orm.close()
