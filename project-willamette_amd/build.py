@@ -46,7 +46,11 @@ COMMON = [
 # The batched GEMM keeps its MFMA accumulators in VGPRs: with the compiler's
 # default (AGPRs) its wave-split-K loop copies them between the two register
 # files on every chunk.
-PER_FILE = {"k_batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# The fused matvecs take what their first loads need in their leading 16
+# argument dwords, which the hardware then preloads into SGPRs at wave
+# launch instead of each wave fetching them from memory.
+PER_FILE = {"k_batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+            "k_i2s.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
 def sources() -> list[Path]:

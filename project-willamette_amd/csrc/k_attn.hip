@@ -33,7 +33,10 @@ struct attn_args {
     // exactly as KVCache::append does; one workgroup of each writes the
     // cache row (kv_dim bytes) and its scale.
     const float *k_new, *v_new;
-    const uint32_t *kv_absmax;  // [2]: absmax of k_new, v_new (float bits), by the QKV matvec
+    // absmax of k_new and v_new (float bits) as the QKV matvec leaves them:
+    // slots whose maximum it is, k_new's [0, n), v_new's [stride, stride + n)
+    const uint32_t *kv_absmax;
+    uint32_t kv_absmax_n, kv_absmax_stride;
     // nullable: the token's position on the device (n_past = *pos_dev + 1,
     // for launches that are replayed at successive positions); the grid and
     // LDS are then sized for n_max, and a larger n_past launches nothing
@@ -55,6 +58,14 @@ __device__ __forceinline__ int8_t kv_q(float v, float absmax) {
     return kv_zero(absmax) ? (int8_t)0 : (int8_t)wm_round_clamp_i8(v * (127.0f / absmax));
 }
 __device__ __forceinline__ float kv_scale(float absmax) { return kv_zero(absmax) ? 0.0f : absmax / 127.0f; }
+// The absmax of k_new (which 0) or v_new (1) from its slots, in every lane
+// of the calling wave (the slots hold non-negative floats, no NaN).
+__device__ __forceinline__ float kv_absmax_of(const attn_args &a, uint32_t which) {
+    const uint32_t *sl = a.kv_absmax + which * a.kv_absmax_stride;
+    float m = 0.0f;
+    for (uint32_t i = threadIdx.x & 63; i < a.kv_absmax_n; i += 64) m = fmaxf(m, __uint_as_float(sl[i]));
+    return wm_wave_max_nonneg(m);
+}
 
 // scores[h][p] = (Σ_i q_h[i] * k_p[i]) * scale.  64 cached positions per
 // workgroup of 256 threads; grid (n_heads, ceil((n_past - 1) / 64) + 1).
@@ -78,7 +89,7 @@ __global__ __launch_bounds__(kScThreads) void k_attn_scores(attn_args a) {
     if (blockIdx.y > n_cached_blocks) return;
     const float *qh = a.q + (uint64_t)h * a.head_dim;
     if (blockIdx.y == n_cached_blocks) {
-        const float kabs = __uint_as_float(a.kv_absmax[0]);
+        const float kabs = kv_absmax_of(a, 0);
         const float ksn = kv_scale(kabs);
         for (uint32_t i = tid; i < a.head_dim; i += kScThreads) {
             const float kd = (float)kv_q(a.k_new[kvh * a.head_dim + i], kabs) * ksn;  // read_into
@@ -208,7 +219,7 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
     const uint32_t kvh = h / a.group;
     const int8_t *vseg = a.v_cache + kvh * a.head_dim + d0;
     const float *sc = a.scores + (uint64_t)h * a.score_stride;
-    const float vabs = __uint_as_float(a.kv_absmax[1]);
+    const float vabs = kv_absmax_of(a, 1);
     const bool v_writer = h == 0 && blockIdx.y == 0;
     if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
     // 1. the loads: thread t takes positions t + i * kSvThreads, its scores in
@@ -420,7 +431,8 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
                          const int8_t *v_cache, const float *v_scales, float *scores,
                          uint32_t score_stride, float *out, uint32_t n_heads, uint32_t n_kv_heads,
                          uint32_t head_dim, uint32_t n_past, float scale, const float *k_new,
-                         const float *v_new, const uint32_t *kv_absmax, hipStream_t s,
+                         const float *v_new, const uint32_t *kv_absmax, uint32_t kv_absmax_n,
+                         uint32_t kv_absmax_stride, hipStream_t s,
                          const uint32_t *pos_dev, uint32_t n_max) {
     // with pos_dev, n_past comes from the device and n_max bounds it
     const uint32_t nb = pos_dev ? n_max : n_past;
@@ -429,7 +441,8 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
         return false;
     const uint32_t kv_dim = n_kv_heads * head_dim;
     attn_args a{q, k_cache, k_scales, v_cache, v_scales, scores, out, n_past, kv_dim, head_dim,
-                n_heads / n_kv_heads, score_stride, scale, k_new, v_new, kv_absmax, pos_dev, nb};
+                n_heads / n_kv_heads, score_stride, scale, k_new, v_new, kv_absmax, kv_absmax_n,
+                kv_absmax_stride, pos_dev, nb};
     hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, (nb - 1 + 63) / 64 + 1), dim3(kScThreads), 0, s, a);
     const size_t npad = ((size_t)nb + 3) & ~(size_t)3;
     const size_t lds = (size_t)wm::seq_sum_padded(nb) * 4 + npad * (4 + 16) +

@@ -148,6 +148,33 @@ __device__ __forceinline__ void i2s_reduce(const i2s_round<RG> &R, const int *ac
             for (int q = 0; q < RG; q++)
                 dot_chunk(R.v[u][q], act_s + (c + u) * 16, acc16[q], acc4[q], acc1[q]);
 }
+// The same with KS lanes per row: lane sub-slice `sub` holds chunks
+// sub, sub + KS, sub + 2 KS, ... of the wave's slice (register u of round k:
+// chunk sub + KS (4k + u)); loads past the slice clamp to its last chunk and
+// their dots read a block of zero activations instead.
+template <int RG, int KS>
+__device__ __forceinline__ void i2s_issue_ks(i2s_round<RG> &R, const uint4 *const (&wp)[RG], uint32_t k,
+                                             uint32_t nc, uint32_t sub) {
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int q = 0; q < RG; q++)
+            R.v[u][q] = wm_load_stream(wp[q] + min(sub + KS * (4u * k + (uint32_t)u), nc - 1) * I2S_GROUP_ROWS);
+}
+template <int RG, int KS>
+__device__ __forceinline__ void i2s_reduce_ks(const i2s_round<RG> &R, const int *act_c0, const int *zeros,
+                                              uint32_t k, uint32_t cnt, uint32_t nc, uint32_t sub,
+                                              int (&acc16)[RG], int (&acc4)[RG], int (&acc1)[RG]) {
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        if ((uint32_t)u < cnt) {
+            const uint32_t j = sub + KS * (4u * k + (uint32_t)u);
+            const int *a = KS == 1 || j < nc ? act_c0 + j * 16 : zeros;
+#pragma unroll
+            for (int q = 0; q < RG; q++) dot_chunk(R.v[u][q], a, acc16[q], acc4[q], acc1[q]);
+        }
+}
+
 // The dots over chunks 0 .. nc-1, round 0 already issued into A (and round
 // 1 into B when b_issued, nc > 4): the next round's loads go out before the
 // current one is reduced, into the other register set (the loop body covers
@@ -234,13 +261,14 @@ __global__ __launch_bounds__(64) void k_i2s_partial(i2s_multi m, uint32_t n_chun
 // workgroup, and fused epilogues
 // --------------------------------------------------------------------------
 //
-// One workgroup per unit of UG 64-row groups.  It first issues its weights'
-// first round, then computes the input's RMSNorm and int8 quantisation
+// One workgroup per unit of UG 64-row groups, or KS workgroups per unit
+// each with 64 / KS rows of every group (KS lanes per row, below).  It first
+// issues its weights' first round, then computes the input's RMSNorm and int8 quantisation
 // itself (wm_norm.h, the same operations as k_rmsnorm_quant) straight into
 // LDS while those loads are in flight: every workgroup evaluates the same
 // norm, so their codes agree bit for bit, and the norm costs no launch and
 // no trip through memory.  Each workgroup writes its share of what the norm
-// leaves behind for later kernels (x + y), workgroup 0 the cleared slots.
+// leaves behind for later kernels (x + y).
 // Its W waves then split the chunks of K between them (wave w: chunks
 // [n_chunks*w/W, n_chunks*(w+1)/W)), each computing the unit's rows over its
 // slice exactly as k_i2s_partial does; the W partial dots meet in LDS (exact
@@ -254,144 +282,413 @@ __global__ __launch_bounds__(64) void k_i2s_partial(i2s_multi m, uint32_t n_chun
 //   WM_FUSED_ROPE    units are heads (UG = head_dim / 64 groups) of Q, K, V;
 //                    NEOX RoPE at `pos` on the tensors in rope_mask
 //                    (primitives.rs:285-345), then to out[t]
+// What the first loads of a launch need comes in the leading 14 argument
+// dwords, which the hardware preloads into SGPRs at wave launch (the file is
+// built with -amdgpu-kernarg-preload-count=16; the argument pointer takes
+// the other two user SGPRs): the norm's inputs, the tensors' weights, where
+// tensors 1 and 2 begin (units, 16 bits each), n_chunks and flags.
+// Everything else is in i2s_fused_args, read once the first loads are out,
+// so the norm covers that round trip.
+enum : uint32_t { FUSED_RELU2 = 1u << 16 };
 struct i2s_fused_args {
-    const uint8_t *w[WM_FUSED_MAX_TENSORS];
     float w_scale[WM_FUSED_MAX_TENSORS];
     float *out[WM_FUSED_MAX_TENSORS];
-    uint32_t unit_end[WM_FUSED_MAX_TENSORS];  // cumulative units per tensor
-    int n_tensors;
-    uint32_t n_chunks;
-    wm_fused_norm norm;                // the input's norm (n = n_chunks * 64)
+    float *x_out;       // nullable: x + y written here, each workgroup its share (never x itself)
+    float eps;
+    uint32_t *err_flag;  // nullable: set to layer_tag when x + y is not all finite
+    uint32_t layer_tag;
     const float *rope_cos, *rope_sin;  // [pos][n_rot/2]
     uint32_t pos, n_rot, rope_mask;
     const uint32_t *pos_dev;  // nullable: the position is read here instead of `pos`
-    uint32_t *absmax;  // ROPE: absmax of the outputs of tensors 1, 2 (float bits, nullable)
+    uint32_t *absmax;  // ROPE: absmax slots of the outputs of tensors 1, 2 (float bits, nullable)
+    uint32_t absmax_stride;  // tensor t's slots from absmax + (t - 1) * absmax_stride
 };
 
-template <int MODE, int UG, int W, int NP>  // NP >= ceil(n / (W * 64)): the norm's terms per thread
-__global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
-    // act [n_chunks*16 ints] | red [W][UG][64] | ys [UG*64] | squares [seq_sum_padded(n)]
+// Scalar arguments read from the argument struct, pinned in SGPRs where
+// they are read (a load the compiler moved to the first use would stall
+// there instead of under the norm).
+template <class T>
+__device__ __forceinline__ T pin_sgpr(T v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
+// KS: lanes per row.  A unit's rows are then split over KS workgroups of
+// R = 64 / KS rows of each of its groups, and lane l of a wave computes row
+// l % R over every KS-th chunk of the wave's slice from l / R on; the KS
+// partial dots of a row meet by lane exchange.
+template <int MODE, int UG, int W, int NP, int KS>  // NP: a power of two >= ceil(n / (W * 64))
+__global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const float *ny, const float *nw,
+                                                      const uint8_t *w0, const uint8_t *w1, const uint8_t *w2,
+                                                      uint32_t units01, uint32_t chunks_flags, i2s_fused_args a) {
+    // act [n_chunks*16 ints] | zeros [16] | red [W][UG][64] | ys [UG*64] | squares [seq_sum_padded(n)]
     extern __shared__ __align__(16) int smem[];
-    __shared__ wm::norm_lds<W> nl;
+    __shared__ wm::fused_norm_lds<W> nl;
+    constexpr int NR = (NP + 3) / 4;  // quantiser rounds: four chunks per round
     const uint32_t u = blockIdx.x;
-    int t = 0;
-#pragma unroll
-    for (int i = 1; i < WM_FUSED_MAX_TENSORS; i++)
-        if (i < a.n_tensors && u >= a.unit_end[i - 1]) t = i;
-    const uint32_t lu = u - (t ? a.unit_end[t - 1] : 0u);  // unit within its tensor
+    // this unit's tensor t (units [ue0, ue1) belong to tensor 1, from ue1 on
+    // to tensor 2) and its unit within the tensor
+    const uint32_t ue0 = units01 & 0xFFFFu, ue1 = units01 >> 16;
+    const uint32_t n_chunks = chunks_flags & 0xFFFFu;
+    const int t = u >= ue1 ? 2 : (u >= ue0 ? 1 : 0);
+    const uint8_t *wt = t == 2 ? w2 : (t == 1 ? w1 : w0);
+    const uint32_t lk = u - (t == 2 ? ue1 : (t == 1 ? ue0 : 0u));
+    constexpr uint32_t R = 64 / KS;  // rows per group of this workgroup
+    const uint32_t lu = lk / KS, h = lk % KS;  // the unit, and which R of each group's 64 rows
     const uint32_t wid = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const uint32_t lane = threadIdx.x & 63;
-    const uint32_t n_chunks = a.n_chunks;
-    const uint32_t c0 = n_chunks * wid / W, c1 = n_chunks * (wid + 1) / W, nc = c1 - c0;
+    const uint32_t sub = lane / R, row = h * R + lane % R;  // this lane's sub-slice and row
+    // With SPEC, wave 0 only walks the exact sum; waves 1..W-1 own the slices
+    // of K and quantise speculatively meanwhile (below).  NP bounds a wave's
+    // chunks, and SPEC needs them all resident (at most two rounds).
+    constexpr bool SPEC = W >= 2 && NP <= 8;
+    static_assert(KS == 1 || (SPEC && NP <= 4 * KS), "KS > 1: the speculating form, one register round");
+    constexpr uint32_t KW = SPEC ? W - 1 : W;  // waves with a slice of K
+    const uint32_t kw = SPEC ? (wid == 0 ? 0u : wid - 1) : wid;
+    const uint32_t c0 = n_chunks * kw / KW;
+    const uint32_t nc = SPEC && wid == 0 ? 0u : n_chunks * (kw + 1) / KW - c0;
     const uint64_t gstride = (uint64_t)n_chunks * I2S_GROUP_ROWS;  // uint4 per group
     const uint4 *wp[UG];
 #pragma unroll
     for (int q = 0; q < UG; q++) {
-        const int tq = MODE == WM_FUSED_GATEUP ? q : t;
+        const uint8_t *wq = MODE == WM_FUSED_GATEUP && q == 1 ? w1 : wt;
         const uint32_t g = MODE == WM_FUSED_GATEUP ? lu : lu * UG + q;
-        wp[q] = reinterpret_cast<const uint4 *>(a.w[tq]) + g * gstride + (uint64_t)c0 * I2S_GROUP_ROWS + lane;
+        wp[q] = reinterpret_cast<const uint4 *>(wq) + g * gstride + (uint64_t)c0 * I2S_GROUP_ROWS + row;
     }
     int *act_s = smem;
-    int *red = smem + n_chunks * 16;
+    int *zeros = smem + n_chunks * 16;  // the activations of a chunk past a lane's sub-slice
+    int *red = zeros + 16;
     float *ys = reinterpret_cast<float *>(red + W * UG * 64);
     float *sq = ys + UG * 64;
-    // The norm's inputs first, alone: they come back quickly while nothing
-    // else is queued (every workgroup's weight loads would otherwise be ahead
-    // of them in the memory system).  The first round of weights follows
-    // inside the exact sum, once its per-term work is done.
-    const wm_fused_norm &nm = a.norm;
     const uint32_t n = n_chunks * 64;
-    const bool first = blockIdx.x == 0;
-    float xv[NP], wv[NP], rv[NP];
-    wm::norm_load<NP, W * 64>(nm.x, nm.y, nm.w, n, xv, wv, rv);
-    wm::norm_prep<NP, W * 64>(nm.y != nullptr, n, nullptr, sq, xv, wv, rv, nm.relu2_mul != 0);
+    const bool relu2 = (chunks_flags & FUSED_RELU2) != 0, has_y = ny != nullptr;
+    // The norm's inputs first, in two layouts: the exact sum's (thread t:
+    // terms t*NP .. t*NP+NP-1; NP divides n, so a run lies wholly inside or
+    // wholly past the vector) and the quantiser's (fused_quads: four
+    // consecutive columns per lane and round, with their norm weights).
+    // Then the weights, whose loads are waited for only at the dots: the
+    // norm's waits are for loads issued before them.
+    const __amdgpu_buffer_rsrc_t rx = wm_rsrc(nx, n * 4), ry = wm_rsrc(has_y ? ny : nx, n * 4),
+                                 rw = wm_rsrc(nw, n * 4);
+    const uint32_t k0 = threadIdx.x * NP;
+    const bool sum_wave = wid * 64u * NP < n;  // wave-uniform: the wave holds terms
+    float xs[NP], ysum[NP];
+#pragma unroll
+    for (int j = 0; j < NP; j++) xs[j] = ysum[j] = 0.0f;
+    if (sum_wave) {
+        wm::buf_run<NP>(rx, k0 * 4, xs);
+        if (has_y) wm::buf_run<NP>(ry, k0 * 4, ysum);
+    }
+    wm::fused_quads<NR> Q;
+    float yq[NR][4];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const uint32_t off = Q.valid(r, c0, nc) ? wm::quad_col(r, c0) * 4 : n * 4;  // past the end: zeros
+        wm::buf_run<4>(rx, off, Q.v[r]);
+        wm::buf_run<4>(rw, off, Q.w[r]);
+        if (has_y) {
+            wm::buf_run<4>(ry, off, yq[r]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) yq[r][i] = 0.0f;
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
+    // (NP bounds the chunks per wave: at most 4 chunks, one round, when NP <= 4)
     i2s_round<UG> A, B;
-    // the epilogue's RoPE factors, fetched now rather than after the reduction
-    const uint32_t half = a.n_rot / 2;  // ROPE: at most 64 <= W * 64 pairs, one per thread
-    const bool rope = MODE == WM_FUSED_ROPE && ((a.rope_mask >> t) & 1u);
+    if (nc > 0) i2s_issue_ks<UG, KS>(A, wp, 0, nc, sub);
+    if constexpr (NP > 4 && KS == 1)
+        if (nc > 4) i2s_issue<UG>(B, wp, 4, nc);  // and the second round, if the slice has one
+    if (KS > 1 && threadIdx.x < 16) zeros[threadIdx.x] = 0;
+    __builtin_amdgcn_sched_barrier(0);
+    // The rest of the arguments, their round trip under the norm: read
+    // through their address plus a zero the compiler cannot see through, so
+    // the loads stay here instead of being hoisted above the first loads.
+    uint32_t zero;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+    const i2s_fused_args &ar =
+        *reinterpret_cast<const i2s_fused_args *>(reinterpret_cast<const char *>(&a) + zero);
+    const wm_fused_norm nm = {nx, ny, pin_sgpr(ar.x_out), nw, pin_sgpr(ar.eps), pin_sgpr(ar.err_flag),
+                              pin_sgpr(ar.layer_tag), chunks_flags & FUSED_RELU2};
+    const float ws0 = pin_sgpr(ar.w_scale[0]), w_scale1 = pin_sgpr(ar.w_scale[1]), ws2 = pin_sgpr(ar.w_scale[2]);
+    float *const o0 = pin_sgpr(ar.out[0]), *const o1 = pin_sgpr(ar.out[1]), *const o2 = pin_sgpr(ar.out[2]);
+    const float w_scale = t == 2 ? ws2 : (t == 1 ? w_scale1 : ws0);
+    float *const out_t = t == 2 ? o2 : (t == 1 ? o1 : o0);
+    const float *rope_cos = pin_sgpr(ar.rope_cos), *rope_sin = pin_sgpr(ar.rope_sin);
+    const uint32_t pos_arg = pin_sgpr(ar.pos), n_rot = pin_sgpr(ar.n_rot), rope_mask = pin_sgpr(ar.rope_mask);
+    const uint32_t *pos_dev = pin_sgpr(ar.pos_dev);
+    uint32_t *absmax = pin_sgpr(ar.absmax);
+    const uint32_t absmax_stride = pin_sgpr(ar.absmax_stride);
+    // the epilogue's RoPE factors
+    const uint32_t half = n_rot / 2;  // ROPE: at most 64 <= W * 64 pairs, one per thread
+    // this workgroup's pairs: all of the head's (KS = 1), else R, the pairs
+    // (h R + i, h R + i + 64) of a 128-wide rotation over UG = 2 groups
+    const uint32_t n_pairs = KS == 1 ? half : R, pair0 = KS == 1 ? 0u : h * R;
+    const bool rope = MODE == WM_FUSED_ROPE && ((rope_mask >> t) & 1u);
     float rc = 0.0f, rsn = 0.0f;
-    if (rope && threadIdx.x < half) {
-        const uint32_t pos = a.pos_dev ? *a.pos_dev : a.pos;
-        rc = a.rope_cos[(uint64_t)pos * half + threadIdx.x];
-        rsn = a.rope_sin[(uint64_t)pos * half + threadIdx.x];
+    if (rope && threadIdx.x < n_pairs) {
+        const uint32_t pos = pos_dev ? *pos_dev : pos_arg;
+        rc = rope_cos[(uint64_t)pos * half + pair0 + threadIdx.x];
+        rsn = rope_sin[(uint64_t)pos * half + pair0 + threadIdx.x];
     }
-    // the input's norm and int8 codes, into LDS (the weights stay in flight;
-    // no global memory access until the dots, so no wait the compiler places
-    // for one can wait on the weights)
-    float act_scale;
-    int asum;
-    {
-        // the first round of weights goes out once the sum's per-term work
-        // is done (data arriving during that work slows it), in flight
-        // during the record walk and the quantiser
-        const auto issue_first = [&]() {
-            __builtin_amdgcn_sched_barrier(0);
-            i2s_issue<UG>(A, wp, 0, nc);
-            if (nc > 4) i2s_issue<UG>(B, wp, 4, nc);  // and the second, if the slice has one
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        const float rsq = wm::norm_sum_rsqrt<NP, W * 64>(false, n, nm.eps, nullptr, 0, sq, nl, issue_first);
-        wm::norm_quant<NP, W * 64>(rsq, n, xv, wv, reinterpret_cast<uint8_t *>(act_s), nl,
-                                   act_scale, asum);
+    // x + y (hidden += the producing matvec's output), or with relu2
+    // relu(x)^2 * y (the FFN's gate x and up y, ffn.rs:37-65), the same f32
+    // operations in both layouts
+    const auto combine = [&](float x, float y) {
+        const float r = x > 0.0f ? x : 0.0f;
+        return relu2 ? (r * r) * y : (has_y ? x + y : x);
+    };
+    float v2[NP];
+#pragma unroll
+    for (int j = 0; j < NP; j++) {
+        const uint32_t k = k0 + (uint32_t)j;
+        const float v = combine(xs[j], ysum[j]);
+        v2[j] = k < n ? v * v : 0.0f;
     }
-    // What the norm leaves for later kernels, written once this workgroup's
-    // own work is done, each workgroup its contiguous share of the elements:
-    // x + y (the same f32 adds as above) with the non-finite check; and by
-    // workgroup 0 the cleared slots.
-    const auto finish = [&]() {
-        const uint32_t tid0 = threadIdx.x;
-        if (first && nm.clear2 && tid0 < 2) nm.clear2[tid0] = 0;
-        if (nm.x_out && nm.y) {
-            const uint32_t lo = (uint32_t)((uint64_t)n * blockIdx.x / gridDim.x);
-            const uint32_t hi = (uint32_t)((uint64_t)n * (blockIdx.x + 1) / gridDim.x);
-            bool nonfinite = false;
-            for (uint32_t j = lo + tid0; j < hi; j += W * 64) {
-                const float v = nm.x[j] + nm.y[j];
-                nm.x_out[j] = v;
+    // What the norm leaves for later kernels: x + y (the same f32 adds as
+    // the norm's, never relu2's combination), each workgroup its contiguous
+    // share of the elements, from the sum layout's registers, and whether
+    // it is all finite.
+    bool nonfinite = false;
+    if (nm.x_out && has_y) {
+        const uint32_t lo = (uint32_t)((uint64_t)n * blockIdx.x / gridDim.x);
+        const uint32_t hi = (uint32_t)((uint64_t)n * (blockIdx.x + 1) / gridDim.x);
+#pragma unroll
+        for (int j = 0; j < NP; j++) {
+            const uint32_t k = k0 + (uint32_t)j;
+            if (k >= lo && k < hi) {
+                const float v = xs[j] + ysum[j];
+                nm.x_out[k] = v;
                 nonfinite |= !isfinite(v);
             }
-            // every writer of this launch writes the same tag; a flag already
-            // raised by an earlier layer is kept
-            if (nonfinite && nm.err_flag && *nm.err_flag == 0) *nm.err_flag = nm.layer_tag;
         }
+    }
+    if (k0 < n) {  // the terms, for the sum's slow paths (a run lies wholly below n)
+        if constexpr (NP >= 4) {
+#pragma unroll
+            for (int j = 0; j < NP; j += 4)
+                *reinterpret_cast<float4 *>(sq + k0 + j) = make_float4(v2[j], v2[j + 1], v2[j + 2], v2[j + 3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < NP; j++) sq[k0 + j] = v2[j];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) Q.v[r][i] = combine(Q.v[r][i], yq[r][i]);
+    wm::fused_max_candidates<NR, W>(Q, c0, nc, nl);
+    uint8_t *const act8 = reinterpret_cast<uint8_t *>(act_s);
+    // the dots over this wave's slice, from the codes in act and the weights
+    // resident in A (and B): part[q] = Σ c a over the slice for group q
+    int part[UG];
+    const auto dots = [&]() {
+        int acc16[UG], acc4[UG], acc1[UG];
+#pragma unroll
+        for (int q = 0; q < UG; q++) acc16[q] = acc4[q] = acc1[q] = 0;
+        if (nc > 0) {
+            const uint32_t nk = (nc + KS - 1) / KS;  // chunk registers of the lanes with the most
+            i2s_reduce_ks<UG, KS>(A, act_s + c0 * 16, zeros, 0, min(nk, 4u), nc, sub, acc16, acc4, acc1);
+            if constexpr (NP > 4 && KS == 1)
+                if (nc > 4) i2s_reduce<UG>(B, act_s + c0 * 16, 4, nc - 4, acc16, acc4, acc1);
+        }
+#pragma unroll
+        for (int q = 0; q < UG; q++) part[q] = (acc16[q] >> 4) + (acc4[q] >> 2) + acc1[q];
     };
-    int acc16[UG], acc4[UG], acc1[UG];
+    // Speculation (waves 1..W-1 while wave 0 walks the exact sum): codes
+    // from the rsqrt of the float64 total of the squares, which is within a
+    // few ulps of the exact one, and their dots.  Afterwards only elements
+    // whose |y * inv| lies within the rsqrt's possible effect of a rounding
+    // boundary are redone exactly, and the difference in each such code
+    // corrected in the integer dot: the result is exactly the exact codes'.
+    uint32_t qw[NR];
+    float dist[NR][4];
+    int wave_asum = 0;
+    float rsq_s = 0.0f, max_s = 0.0f;
+    bool spec_ok = false;
+    wm::fused_cand_regs cand{};
+    wm::seq_sum_block_owned<NP, W * 64>(
+        v2, n, sq, &nl.seq, NP,
+        [&]() {
+            if (wid == 0) {
+                cand = wm::fused_cand_fetch<W>(nl);
+                if (SPEC) __builtin_amdgcn_s_setprio(3);  // the walk is the critical path
+            } else if (SPEC) {
+                rsq_s = nl.spec_rsq;
+                max_s = nl.spec_max;
+                spec_ok = max_s >= 0.0f;
+                if (spec_ok) {
+                    wave_asum = wm::fused_codes<NR, true>(Q, c0, nc, rsq_s, max_s, act8, qw, dist);
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    dots();
+                }
+            }
+        },
+        [&](float sum_sq) { wm::fused_publish<W>(sum_sq, n, nm.eps, cand, nl); },
+        [&]() {
+            // The speculation's rsqrt and max|y|, once, by the last wave (at
+            // these sizes it holds no terms of the sum and waits anyway):
+            // the rsqrt of the waves' float64 total, max|y| from the
+            // candidates, -1 where the candidate bound does not hold.
+            if (SPEC && wid == W - 1) {
+                double S = 0.0;
 #pragma unroll
-    for (int q = 0; q < UG; q++) acc16[q] = acc4[q] = acc1[q] = 0;
-    i2s_rounds<UG>(A, B, wp, nc, act_s + c0 * 16, acc16, acc4, acc1, nc > 4);
+                for (int i = 0; i < W; i++) S += nl.seq.dw[i];
+                const float r = wm::norm_rsq((float)S, n, nm.eps);
+                const wm::fused_cand_regs c = wm::fused_cand_fetch<W>(nl);
+                bool ok;
+                const float m = wm::fused_cand_max(c, r, ok);
+                if (lane == 0) {
+                    nl.spec_rsq = r;
+                    nl.spec_max = ok && r > 0.0f && r < 0x1p100f ? m : -1.0f;
+                }
+            }
+        });
+    if (SPEC && wid == 0) __builtin_amdgcn_s_setprio(0);
+    // the exact rsqrt and max|y| (wave 0); max|y| from every wave's own
+    // maximum when the candidates could not settle it
+    const float rsq = nl.rsq;
+    float max_abs = nl.maxabs;
+    const bool fallback = max_abs < 0.0f;  // the same in every wave
+    if (fallback) max_abs = wm::fused_block_max<NR, W>(Q, c0, nc, rsq, nl);
+    bool redo = !SPEC || !spec_ok || fallback;
+    if (!redo && (rsq != rsq_s || max_abs != max_s)) {
+        // |p - p'| <= |p'| (rho + 8u) with p = ((x r) w) inv, p' the same with
+        // r', inv' and rho = |(r / r')(M' / M) - 1| (eight roundings of at most
+        // u = 2^-24 between them), |p'| < 128; plus 2^-40 for a subnormal y.
+        const double rho = fabs(((double)rsq * (double)max_s) / ((double)rsq_s * (double)max_abs) - 1.0);
+        const float bound = (float)(128.0 * (rho + 9.0 * 0x1p-24) + 0x1p-40);
+        const float inv = 127.0f / max_abs;
+        int n_fix = 0;
 #pragma unroll
-    for (int q = 0; q < UG; q++)
-        red[(wid * UG + q) * 64 + lane] = (acc16[q] >> 4) + (acc4[q] >> 2) + acc1[q];
+        for (int r = 0; r < NR; r++) {
+            const bool ok = Q.valid(r, c0, nc);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint64_t m = __builtin_amdgcn_ballot_w64(ok && dist[r][i] <= bound);
+                while (m) {
+                    const int l = __builtin_ctzll(m);
+                    m &= m - 1;
+                    if (++n_fix > 16) break;
+                    // element (r, i) of lane l: its exact code and the change
+                    const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(Q.v[r][i]), l));
+                    const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(Q.w[r][i]), l));
+                    const int qs = (int)(int8_t)(uint8_t)(__builtin_amdgcn_readlane((int)qw[r], l) >> (8 * i));
+                    const int qe = wm_round_clamp_i8_fast(((v * rsq) * w) * inv);
+                    const int d = qe - qs;
+                    if (d != 0) {
+                        wave_asum += d;
+                        // the weight code of that column in this lane's row:
+                        // chunk u of the slice (register (u - sub) / KS of
+                        // the lanes of sub-slice u % KS; the others add 0),
+                        // byte b of the chunk (quarter b / 16 from the top
+                        // bit pair, gp = b % 16)
+                        const uint32_t u = 4u * (uint32_t)r + ((uint32_t)l >> 4), b = 4u * ((uint32_t)l & 15u) + (uint32_t)i;
+                        // The dword holding it, picked with masks the
+                        // compiler cannot see through (a select on u would
+                        // become an indexed access and put the resident
+                        // weights in scratch memory).
+                        const uint32_t g = (b & 15u) >> 2;
+                        constexpr int NK = NP > 4 && KS == 1 ? 8 : 4;
+                        uint32_t mk[NK][4];
+#pragma unroll
+                        for (int k = 0; k < NK; k++)
+#pragma unroll
+                            for (int j = 0; j < 4; j++) {
+                                mk[k][j] = u == sub + KS * (uint32_t)k && g == (uint32_t)j ? 0xFFFFFFFFu : 0u;
+                                asm volatile("" : "+v"(mk[k][j]));
+                            }
+#pragma unroll
+                        for (int q = 0; q < UG; q++) {
+                            uint32_t dw = 0;
+#pragma unroll
+                            for (int k = 0; k < NK; k++) {
+                                const uint4 ch = k < 4 ? A.v[k & 3][q] : B.v[k & 3][q];
+                                dw |= (ch.x & mk[k][0]) | (ch.y & mk[k][1]) | (ch.z & mk[k][2]) | (ch.w & mk[k][3]);
+                            }
+                            // part holds Σ c a (c = ternary + 1); Σ a is corrected apart
+                            const uint32_t code = (dw >> (8u * (b & 3u) + 6u - 2u * (b >> 4))) & 3u;
+                            part[q] += (int)code * d;
+                        }
+                    }
+                }
+            }
+        }
+        redo = n_fix > 16;  // too many to correct one by one
+    }
+    if (redo) {  // the codes and dots from the exact rsqrt and max|y|
+        wave_asum = wm::fused_codes<NR, false>(Q, c0, nc, rsq, max_abs, act8, qw, dist);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if constexpr (SPEC) {
+            dots();
+        } else {
+            int acc16[UG], acc4[UG], acc1[UG];
+#pragma unroll
+            for (int q = 0; q < UG; q++) acc16[q] = acc4[q] = acc1[q] = 0;
+            if constexpr (NP > 4)
+                i2s_rounds<UG>(A, B, wp, nc, act_s + c0 * 16, acc16, acc4, acc1, nc > 4);
+            else
+                i2s_reduce<UG>(A, act_s + c0 * 16, 0, nc, acc16, acc4, acc1);
+#pragma unroll
+            for (int q = 0; q < UG; q++) part[q] = (acc16[q] >> 4) + (acc4[q] >> 2) + acc1[q];
+        }
+    }
+    if (SPEC && wid == 0) {
+#pragma unroll
+        for (int q = 0; q < UG; q++) part[q] = 0;
+    }
+    const float act_scale = max_abs == 0.0f ? 1.0f : max_abs / 127.0f;
+    // At the end: the non-finite flag of x + y (every writer of this
+    // launch writes the same tag; a flag already raised by an earlier layer
+    // is kept).
+    const auto finish = [&]() {
+        if (nonfinite && nm.err_flag && *nm.err_flag == 0) *nm.err_flag = nm.layer_tag;
+    };
+    // this wave's share of Σ(c - 1) a = Σ c a - Σ a over its slice, each
+    // row's KS lanes summed first (lanes l, l ^ R, l ^ 2R, ...)
+#pragma unroll
+    for (int q = 0; q < UG; q++) {
+        int p = part[q];
+        if constexpr (KS >= 8) p += __shfl_xor(p, 8, 64);
+        if constexpr (KS >= 4) p += __shfl_xor(p, 16, 64);
+        if constexpr (KS >= 2) p += __shfl_xor(p, 32, 64);
+        if (lane < R) red[(wid * UG + q) * R + lane] = p - wave_asum;
+    }
     wm_sync_lds();
     const uint32_t tid = threadIdx.x;
     if (MODE == WM_FUSED_GATEUP) {
-        if (tid < 64) {
-            int dg = -asum, du = -asum;
+        if (tid < R) {
+            int dg = 0, du = 0;
 #pragma unroll
             for (int w = 0; w < W; w++) {
-                dg += red[(w * UG + 0) * 64 + tid];
-                du += red[(w * UG + 1) * 64 + tid];
+                dg += red[(w * UG + 0) * R + tid];
+                du += red[(w * UG + 1) * R + tid];
             }
-            const float g = (a.w_scale[0] * act_scale) * (float)dg;
-            const float up = (a.w_scale[1] * act_scale) * (float)du;
+            const float g = (w_scale * act_scale) * (float)dg;
+            const float up = (w_scale1 * act_scale) * (float)du;
             const float r = g > 0.0f ? g : 0.0f;
-            a.out[0][lu * 64 + tid] = (r * r) * up;
+            out_t[lu * 64 + h * R + tid] = (r * r) * up;
         }
         finish();
         return;
     }
-    float *out = a.out[t] + (uint64_t)lu * UG * 64;
-    for (uint32_t row = tid; row < UG * 64; row += W * 64) {
-        const uint32_t q = row >> 6, rr = row & 63;
-        int dot = -asum;
+    // the unit's outputs (row i of group q at out[64 q + i]); this workgroup
+    // holds rows h R .. h R + R - 1 of each group, ys[R q + i - h R]
+    float *out = out_t + (uint64_t)lu * UG * 64;
+    for (uint32_t idx = tid; idx < UG * R; idx += W * 64) {
+        const uint32_t q = idx / R, rr = idx % R;
+        int dot = 0;
 #pragma unroll
-        for (int w = 0; w < W; w++) dot += red[(w * UG + q) * 64 + rr];
-        const float y = (a.w_scale[t] * act_scale) * (float)dot;
+        for (int w = 0; w < W; w++) dot += red[(w * UG + q) * R + rr];
+        const float y = (w_scale * act_scale) * (float)dot;
         if (MODE == WM_FUSED_PLAIN) {
-            out[row] = y;
+            out[q * 64 + h * R + rr] = y;
         } else {
-            ys[row] = y;
+            ys[idx] = y;
         }
     }
     if (MODE == WM_FUSED_PLAIN) {
@@ -402,30 +699,33 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(i2s_fused_args a) {
     wm_sync_lds();
     float mx = 0.0f;  // |output| maximum, NaN never raising it
     if (rope) {
-        if (tid < half) {
-            const uint32_t j = tid;
-            const float x0 = ys[j], x1 = ys[j + half];
+        if (tid < n_pairs) {
+            const uint32_t j = pair0 + tid;  // the pair (j, j + half) of the head
+            const float x0 = ys[tid], x1 = ys[tid + (KS == 1 ? half : R)];
             const float r0 = x0 * rc - x1 * rsn, r1 = x0 * rsn + x1 * rc;
             out[j] = r0;
             out[j + half] = r1;
             mx = wm_max_nonan(wm_max_nonan(mx, fabsf(r0)), fabsf(r1));
         }
-        for (uint32_t j = a.n_rot + tid; j < UG * 64; j += W * 64) {
-            out[j] = ys[j];
-            mx = wm_max_nonan(mx, fabsf(ys[j]));
-        }
+        if constexpr (KS == 1)
+            for (uint32_t j = n_rot + tid; j < UG * 64; j += W * 64) {
+                out[j] = ys[j];
+                mx = wm_max_nonan(mx, fabsf(ys[j]));
+            }
     } else {
-        for (uint32_t j = tid; j < UG * 64; j += W * 64) {
-            out[j] = ys[j];
-            mx = wm_max_nonan(mx, fabsf(ys[j]));
+        for (uint32_t idx = tid; idx < UG * R; idx += W * 64) {
+            out[(idx / R) * 64 + h * R + idx % R] = ys[idx];
+            mx = wm_max_nonan(mx, fabsf(ys[idx]));
         }
     }
-    // KVCache::append needs each of K and V's absmax over all heads: the
-    // units publish theirs with an integer max of the float bits (non-negative
-    // floats order as their bits; the slots are cleared before the launch)
-    if (t >= 1 && a.absmax) {
+    // KVCache::append needs each of K and V's absmax over all heads: waves
+    // 0 and 1, which hold every output (at most 128 per workgroup), store
+    // their maxima to slots of their own (2 lk + wid), every launch; the
+    // consumer takes the maximum over the slots (no atomics: on a launch of
+    // a few hundred workgroups same-address atomics serialise)
+    if (t >= 1 && absmax && wid < 2) {
         mx = wm_wave_max_nonneg(mx);
-        if (lane == 0) atomicMax(a.absmax + (t - 1), __float_as_uint(mx));
+        if (lane == 0) absmax[(t - 1) * absmax_stride + 2 * lk + wid] = __float_as_uint(mx);
     }
     finish();
 }
@@ -616,13 +916,15 @@ void wm_launch_i2s_finalize(const int32_t *partial, uint32_t split, uint32_t row
 bool wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scales, float *const *outs,
                          int n_tensors, uint32_t n_chunks, uint32_t groups_per_unit,
                          const wm_fused_norm &norm, const float *rope_cos, const float *rope_sin,
-                         uint32_t pos, uint32_t n_rot, uint32_t rope_mask, uint32_t *absmax,
+                         uint32_t pos, uint32_t n_rot, uint32_t rope_mask, const wm_fused_absmax *absmax,
                          hipStream_t s, const uint32_t *pos_dev) {
+    if (n_tensors < 1 || n_tensors > WM_FUSED_MAX_TENSORS) return false;
     i2s_fused_args a{};
+    const uint8_t *wts[WM_FUSED_MAX_TENSORS] = {};
+    uint32_t unit_end[WM_FUSED_MAX_TENSORS] = {};
     uint32_t acc = 0;
-    a.n_tensors = n_tensors;
     for (int i = 0; i < n_tensors; i++) {
-        a.w[i] = descs[i].w;
+        wts[i] = descs[i].w;
         a.w_scale[i] = w_scales[i];
         a.out[i] = outs[i];
         // units: PLAIN one per group, ROPE one per head (UG groups), GATEUP one
@@ -630,48 +932,100 @@ bool wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
         const uint32_t units = mode == WM_FUSED_GATEUP ? (i == 0 ? descs[0].n_groups : 0)
                                                        : descs[i].n_groups / groups_per_unit;
         acc += units;
-        a.unit_end[i] = acc;
+        unit_end[i] = acc;
     }
-    if (mode == WM_FUSED_GATEUP) a.n_tensors = 1;  // units all belong to the pair
-    a.n_chunks = n_chunks;
-    a.norm = norm;
+    // the units of tensor 1 begin at ue0, those of tensor 2 at ue1 (past the
+    // grid: no such tensor; GATEUP's units all belong to the pair)
+    const bool pair = mode == WM_FUSED_GATEUP;
+    if (acc >= 0xFFFFu || n_chunks > 0xFFFFu) return false;  // 16-bit unit and chunk counts (again x KS below)
+    const uint32_t ue0 = !pair && n_tensors > 1 ? unit_end[0] : 0xFFFFu;
+    const uint32_t ue1 = !pair && n_tensors > 2 ? unit_end[1] : 0xFFFFu;
+    a.x_out = norm.x_out;
+    a.eps = norm.eps;
+    a.err_flag = norm.err_flag;
+    a.layer_tag = norm.layer_tag;
     a.rope_cos = rope_cos;
     a.rope_sin = rope_sin;
     a.pos = pos;
     a.pos_dev = pos_dev;
     a.n_rot = n_rot;
     a.rope_mask = rope_mask;
-    a.absmax = absmax;
+    a.absmax = absmax ? absmax->slots : nullptr;
+    a.absmax_stride = absmax ? absmax->stride : 0;
+    const uint32_t chunks_flags = n_chunks | (norm.relu2_mul ? FUSED_RELU2 : 0u);
     // Waves: as many as the chunks allow, up to 16 (the norm at the start is
     // latency-bound and runs best on the widest workgroup; each wave still
     // has its own chunks), rounded down to an instantiated count.
     int w = (int)(n_chunks < 16 ? n_chunks : 16);
-    static const int kWs[] = {16, 12, 10, 8, 6, 4, 2, 1};
+    static const int kWs[] = {16, 8, 4, 2, 1};
     for (int x : kWs)
         if (w >= x) { w = x; break; }
-    // the norm's terms per thread, rounded up to an instantiated bound (the
-    // exact sum's work grows with the bound; 3 and 7 are BitNet-2B's 2560 and
-    // 6912): at most 2 below 16 waves, at most 16 with 16 (n_chunks <= 256)
-    const uint32_t per = (n_chunks + (uint32_t)w - 1) / (uint32_t)w;
-    const int np = w == 16 && (per == 3 || per == 7) ? (int)per
-                                                     : (per <= 4 ? 4 : (per <= 8 ? 8 : 16));
+    // NP: the exact sum's terms per thread and the bound on a wave's chunks,
+    // a power of two (it then divides n, so no thread's run straddles the
+    // end).  With at least two waves and NP <= 8 the kernel speculates and
+    // spreads the chunks over waves 1..w-1; otherwise over all w waves.
+    const auto pow2 = [](uint32_t v) {
+        int p = 1;
+        while ((uint32_t)p < v) p *= 2;
+        return p;
+    };
+    int np = w >= 2 ? pow2((n_chunks + (uint32_t)w - 2) / (uint32_t)(w - 1)) : 1;
+    if (np > 8) np = 16;  // no speculation: ceil(n_chunks / w) <= 16 for n_chunks <= 256
+    // KS: lanes per row.  The units of a launch are few (a layer's 64-row
+    // groups), and each workgroup's dots run on one CU's four SIMDs, so a
+    // unit is split over KS workgroups while the grid stays within one
+    // workgroup per CU: each has 1/KS of the dots and the weight loads, and
+    // the norm (the same in every workgroup) costs no more.  The 16-wave
+    // speculating form only, PLAIN or whole-head ROPE (a 128-wide rotation
+    // over two groups, or none): a rotation pair then lies in one workgroup.
+    static const uint32_t n_cus = [] {
+        int dev = 0, c = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+            c = 256;
+        return (uint32_t)c;
+    }();
+    uint32_t ks = 1;
+    const bool ks_form = w == 16 && np <= 8 &&
+                         (mode == WM_FUSED_PLAIN ||
+                          (mode == WM_FUSED_ROPE && groups_per_unit == 2 && (rope_mask == 0 || n_rot == 128)));
+    if (ks_form)
+        while (ks < 8 && acc * ks * 2 <= n_cus) ks *= 2;
+    const uint32_t grid = acc * ks;
+    if (grid >= 0xFFFFu) return false;
+    const uint32_t units01 = (ue0 == 0xFFFFu ? ue0 : ue0 * ks) | (ue1 == 0xFFFFu ? ue1 : ue1 * ks) << 16;
+    if (absmax) {  // two slots per workgroup of tensors 1 and 2
+        uint32_t most = 0;
+        for (int i = 1; i < n_tensors; i++) most = std::max(most, 2 * (unit_end[i] - unit_end[i - 1]) * ks);
+        if (mode != WM_FUSED_ROPE || most > absmax->stride) return false;
+        *absmax->n_slots = most;
+    }
     const size_t sq_bytes = (size_t)wm::seq_sum_padded(n_chunks * 64) * 4;
-#define WM_FUSED_CASE(MODE, UG, W, NP)                                                             \
-    if (w == W && np == NP) {                                                                      \
-        const size_t lds = (size_t)n_chunks * 64 + (size_t)W * UG * 64 * 4 + (size_t)UG * 64 * 4 + \
-                           sq_bytes;                                                               \
-        hipLaunchKernelGGL((k_i2s_fused<MODE, UG, W, NP>), dim3(acc), dim3(W * 64), lds, s, a);    \
+#define WM_FUSED_CASE(MODE, UG, W, NP, KS)                                                         \
+    if (w == W && np == NP && ks == KS) {                                                          \
+        const size_t lds = (size_t)n_chunks * 64 + 64 + (size_t)W * UG * 64 * 4 +                  \
+                           (size_t)UG * 64 * 4 + sq_bytes;                                         \
+        hipLaunchKernelGGL((k_i2s_fused<MODE, UG, W, NP, KS>), dim3(grid), dim3(W * 64), lds, s,   \
+                           norm.x, norm.y, norm.w, wts[0], wts[1], wts[2], units01, chunks_flags, a); \
         return true;                                                                               \
     }
 #define WM_FUSED_WS(MODE, UG)                                                                      \
-    WM_FUSED_CASE(MODE, UG, 1, 4) WM_FUSED_CASE(MODE, UG, 2, 4) WM_FUSED_CASE(MODE, UG, 4, 4)      \
-    WM_FUSED_CASE(MODE, UG, 6, 4) WM_FUSED_CASE(MODE, UG, 8, 4) WM_FUSED_CASE(MODE, UG, 10, 4)     \
-    WM_FUSED_CASE(MODE, UG, 12, 4) WM_FUSED_CASE(MODE, UG, 16, 3) WM_FUSED_CASE(MODE, UG, 16, 4)   \
-    WM_FUSED_CASE(MODE, UG, 16, 7) WM_FUSED_CASE(MODE, UG, 16, 8) WM_FUSED_CASE(MODE, UG, 16, 16)
-    if (mode == WM_FUSED_PLAIN) { WM_FUSED_WS(WM_FUSED_PLAIN, 1) }
+    WM_FUSED_CASE(MODE, UG, 1, 1, 1) WM_FUSED_CASE(MODE, UG, 2, 2, 1) WM_FUSED_CASE(MODE, UG, 2, 4, 1) \
+    WM_FUSED_CASE(MODE, UG, 4, 2, 1) WM_FUSED_CASE(MODE, UG, 4, 4, 1) WM_FUSED_CASE(MODE, UG, 8, 2, 1) \
+    WM_FUSED_CASE(MODE, UG, 8, 4, 1) WM_FUSED_CASE(MODE, UG, 16, 2, 1)                               \
+    WM_FUSED_CASE(MODE, UG, 16, 4, 1) WM_FUSED_CASE(MODE, UG, 16, 8, 1)                              \
+    WM_FUSED_CASE(MODE, UG, 16, 16, 1)
+#define WM_FUSED_KS(MODE, UG)                                                                      \
+    WM_FUSED_CASE(MODE, UG, 16, 2, 2) WM_FUSED_CASE(MODE, UG, 16, 4, 2)                              \
+    WM_FUSED_CASE(MODE, UG, 16, 8, 2) WM_FUSED_CASE(MODE, UG, 16, 2, 4)                              \
+    WM_FUSED_CASE(MODE, UG, 16, 4, 4) WM_FUSED_CASE(MODE, UG, 16, 8, 4)                              \
+    WM_FUSED_CASE(MODE, UG, 16, 2, 8) WM_FUSED_CASE(MODE, UG, 16, 4, 8)                              \
+    WM_FUSED_CASE(MODE, UG, 16, 8, 8)
+    if (mode == WM_FUSED_PLAIN) { WM_FUSED_WS(WM_FUSED_PLAIN, 1) WM_FUSED_KS(WM_FUSED_PLAIN, 1) }
     else if (mode == WM_FUSED_GATEUP) { WM_FUSED_WS(WM_FUSED_GATEUP, 2) }
-    else if (groups_per_unit == 2) { WM_FUSED_WS(WM_FUSED_ROPE, 2) }
+    else if (groups_per_unit == 2) { WM_FUSED_WS(WM_FUSED_ROPE, 2) WM_FUSED_KS(WM_FUSED_ROPE, 2) }
     else if (groups_per_unit == 1) { WM_FUSED_WS(WM_FUSED_ROPE, 1) }
+#undef WM_FUSED_KS
 #undef WM_FUSED_WS
 #undef WM_FUSED_CASE
     return false;

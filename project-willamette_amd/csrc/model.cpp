@@ -31,8 +31,9 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
                          const int8_t *v_cache, const float *v_scales, float *scores,
                          uint32_t score_stride, float *out, uint32_t n_heads, uint32_t n_kv_heads,
                          uint32_t head_dim, uint32_t n_past, float scale, const float *k_new,
-                         const float *v_new, const uint32_t *kv_absmax, hipStream_t s,
-                         const uint32_t *pos_dev = nullptr, uint32_t n_max = 0);
+                         const float *v_new, const uint32_t *kv_absmax, uint32_t kv_absmax_n,
+                         uint32_t kv_absmax_stride, hipStream_t s, const uint32_t *pos_dev = nullptr,
+                         uint32_t n_max = 0);
 bool wm_launch_attention_position_zero(const float *q, const float *k_new, const float *v_new,
                                        float *out, uint32_t n_heads, uint32_t n_kv_heads,
                                        uint32_t head_dim, float scale, hipStream_t s);
@@ -82,7 +83,11 @@ struct wm_model {
     float *proj_out = nullptr;  // O's, then down's f32 output (the next norm adds it to hidden)
     float *logits = nullptr, *scores = nullptr;
     uint32_t *dscalars = nullptr;  // [0] token, [1] next token, [2] error flag, [3] greedy loop's
-                                   // position, [4..5] K/V absmax
+                                   // position
+    // this token's K/V absmax as the QKV launch leaves them (wm_fused_absmax):
+    // kv_absmax_stride slots each, kv_absmax_n of them written by every launch
+    uint32_t *kv_absmax = nullptr;
+    uint32_t kv_absmax_stride = 0, kv_absmax_n = 0;
     void *lm_work = nullptr;
     // ragged-batch workspace, grown on demand to b_cap tokens
     uint8_t *bws = nullptr;
@@ -174,13 +179,14 @@ bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, step_pos sp, float 
     const uint32_t E = c.n_embd, KV = m->kv_dim;
     const uint32_t n_chunks_e = E / I2S_CHUNK_COLS, n_chunks_f = c.n_ff / I2S_CHUNK_COLS;
     const float scale = 1.0f / sqrtf((float)c.head_dim);  // primitives.rs:354
-    // absmax of this token's K and V (float bits): zero at creation and after
-    // every O launch, raised by the QKV launch, read by attention
-    uint32_t *kv_absmax = m->dscalars + 4;
+    // absmax of this token's K and V: slots written by the QKV launch, whose
+    // maximum attention takes
+    const wm_fused_absmax kv_absmax{m->kv_absmax, m->kv_absmax_stride, &m->kv_absmax_n};
     const auto want = [&](int r) { return only == ROLE_ALL || only == r; };
     const dev_layer &L = m->layers[l];
     // attn_norm, on hidden + the previous layer's ffn_down, then Q, K, V
-    // (whole heads per workgroup, NEOX RoPE on Q and K at `pos`)
+    // (whole heads, or a head's rows split over a few workgroups; NEOX RoPE
+    // on Q and K at `pos`)
     wm_fused_norm an{};
     an.x = H[cur];
     an.w = L.attn_norm;
@@ -197,7 +203,7 @@ bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, step_pos sp, float 
     float *qkv_out[3] = {m->q, m->k_new, m->v_new};
     if (want(ROLE_QKV) &&
         !wm_launch_i2s_fused(WM_FUSED_ROPE, qkv, qkv_scales, qkv_out, 3, n_chunks_e, c.head_dim / 64,
-                             an, m->rope_cos, m->rope_sin, pos, c.n_rot, 0x3u, kv_absmax, s, sp.dev))
+                             an, m->rope_cos, m->rope_sin, pos, c.n_rot, 0x3u, &kv_absmax, s, sp.dev))
         return false;
     if (layer_trace_dev && l > 0)
         hipMemcpyAsync(layer_trace_dev + (size_t)(l - 1) * E, H[cur], (size_t)E * 4,
@@ -214,16 +220,16 @@ bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, step_pos sp, float 
             if (!wm_launch_attention(m->q, kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV,
                                      kv->vs + lay, m->scores, c.context_length, m->attn_out,
                                      c.n_heads, c.n_kv_heads, c.head_dim, pos + 1, scale, m->k_new,
-                                     m->v_new, kv_absmax, s, sp.dev, sp.n_max))
+                                     m->v_new, m->kv_absmax, m->kv_absmax_n, m->kv_absmax_stride, s,
+                                     sp.dev, sp.n_max))
                 return false;
         }
     }
-    // attn_sub_norm, then O (the launch also clears the K/V absmax slots)
+    // attn_sub_norm, then O
     wm_fused_norm sn{};
     sn.x = m->attn_out;
     sn.w = L.attn_sub_norm;
     sn.eps = c.rms_eps;
-    sn.clear2 = kv_absmax;
     wm_i2s_desc od = {L.o.w, L.o.n_groups};
     float *o_out[1] = {m->proj_out};
     if (want(ROLE_O) && !wm_launch_i2s_fused(WM_FUSED_PLAIN, &od, &L.o.scale, o_out, 1, n_chunks_e,
@@ -612,6 +618,7 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
         align256((size_t)c.vocab_size * 4),                       // logits
         align256((size_t)c.n_heads * c.context_length * 4),       // scores
         256,                                                      // device scalars
+        align256((size_t)2 * 16 * c.n_kv_heads * 4),              // K/V absmax slots
         align256(wm_q6k_logits_work_bytes(c.vocab_size, c.n_embd / Q6K_VALUES)),  // lm-head work
         align256(cs.size() * 4), align256(cs.size() * 4),         // rope tables
     };
@@ -628,6 +635,7 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
                       (void **)&m->final_hidden,
                       (void **)&m->k_new,    (void **)&m->v_new,    (void **)&m->proj_out,
                       (void **)&m->logits,   (void **)&m->scores,   (void **)&m->dscalars,
+                      (void **)&m->kv_absmax,
                       (void **)&m->lm_work,  (void **)&m->rope_cos, (void **)&m->rope_sin};
     static_assert(sizeof(slots) / sizeof(slots[0]) == sizeof(sizes) / sizeof(sizes[0]),
                   "one slot per workspace size");
@@ -635,6 +643,7 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
         *slots[i] = p;
         p += sizes[i];
     }
+    m->kv_absmax_stride = 16 * c.n_kv_heads;  // two per workgroup, at most 8 workgroups per head
     e = hipMemsetAsync(m->ws, 0, total, ctx->stream);
     if (e == hipSuccess)
         e = hipMemcpyAsync(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, ctx->stream);

@@ -350,7 +350,7 @@ void wm_launch_i2s_repack(const uint8_t *raw, uint8_t *out, uint32_t in_dim, uin
 void wm_launch_quantize_act(const float *x, uint32_t n, uint8_t *act, wm_act_meta *meta,
                             hipStream_t s);
 // Fused matvec modes (k_i2s_fused).
-constexpr int WM_FUSED_MAX_TENSORS = 4;
+constexpr int WM_FUSED_MAX_TENSORS = 3;
 enum { WM_FUSED_PLAIN = 0, WM_FUSED_GATEUP = 1, WM_FUSED_ROPE = 2 };
 
 // Partial dots over K splits (one launch covers up to WM_I2S_MAX_MULTI
@@ -370,7 +370,6 @@ struct wm_fused_norm {
     float eps;
     uint32_t *err_flag;     // nullable: set to layer_tag when x + y is not all finite
     uint32_t layer_tag;
-    uint32_t *clear2;       // nullable: two slots zeroed
     // nonzero: x is the gate projection and y the up projection of the FFN,
     // and the norm runs on relu(x)^2 * y (ffn.rs:37-65) instead of x + y
     uint32_t relu2_mul;
@@ -379,10 +378,19 @@ struct wm_fused_norm {
 // workgroup and a fused epilogue (mode WM_FUSED_*): rows of tensor i go to
 // outs[i] as f32; see k_i2s_fused.  groups_per_unit: 1, or head_dim / 64
 // for WM_FUSED_ROPE.
+// ROPE: where the launch leaves the absmax of tensors 1 and 2's outputs (K
+// and V), as slots whose maximum it is (float bits; every launch of one
+// shape writes the same slots): tensor t's at slots[(t - 1) * stride + i],
+// i < *n_slots, which the launch sets (false when they exceed the stride).
+struct wm_fused_absmax {
+    uint32_t *slots;
+    uint32_t stride;
+    uint32_t *n_slots;
+};
 bool wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scales, float *const *outs,
                          int n_tensors, uint32_t n_chunks, uint32_t groups_per_unit,
                          const wm_fused_norm &norm, const float *rope_cos, const float *rope_sin,
-                         uint32_t pos, uint32_t n_rot, uint32_t rope_mask, uint32_t *absmax,
+                         uint32_t pos, uint32_t n_rot, uint32_t rope_mask, const wm_fused_absmax *absmax,
                          hipStream_t s, const uint32_t *pos_dev = nullptr);
 void wm_launch_i2s_partial_table(const uint8_t *const *table, uint32_t n_tensors,
                                  uint32_t groups_per, uint32_t n_chunks, const uint8_t *act,

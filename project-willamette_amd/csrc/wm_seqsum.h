@@ -234,8 +234,6 @@ struct seq_block_scratch {
     int eaf[kSeqMaxWaves][kSeqWaveRecords];       // predicted binade after it
     uint32_t pi[kSeqMaxWaves][kSeqWaveRecords];   // wave's increments before it
     float val[kSeqMaxWaves][kSeqWaveRecords];     // the term
-    int first[64];  // walk: wave + 1 at the chunk lane of its first record, else 0
-    float2 step[64];  // walk: (segment increment, break term) of each step of a chunk
     float out;
 };
 
@@ -288,12 +286,20 @@ struct seq_no_hook {
 };
 
 // `before_walk` runs in every thread once the per-term work is done, while
-// wave 0 walks the records and the other waves wait (the fused matvecs issue
-// their weight loads there, so that the data does not arrive during the
-// per-term work).
-template <int MAXM, int NT, typename Hook = seq_no_hook>
-__device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const float *a,
-                                     seq_block_scratch *sc, const Hook &before_walk = Hook()) {
+// wave 0 walks the records and the other waves wait.  `after_walk(s)` runs
+// in wave 0 alone with the finished sum, before the barrier that hands it to
+// the other waves (work that only needs s can publish its result with it).
+struct seq_no_after {
+    __device__ void operator()(float) const {}
+};
+// `after_scan` runs in every thread right after the first barrier, when the
+// waves' float64 totals (sc->dw) are complete.
+template <int MAXM, int NT, typename Hook = seq_no_hook, typename After = seq_no_after,
+          typename Mid = seq_no_hook>
+__device__ __forceinline__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const float *a,
+                                     seq_block_scratch *sc, uint32_t m_run = 0,
+                                     const Hook &before_walk = Hook(), const After &after_walk = After(),
+                                     const Mid &after_scan = Mid()) {
     static_assert(NT % 64 == 0 && NT <= 64 * kSeqMaxWaves, "workgroup size");
     static_assert(MAXM >= 1 && MAXM <= 32, "terms per thread");
     constexpr int NW = NT / 64;
@@ -301,18 +307,27 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wid = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
     if (n == 0) return 0.0f;
-    const uint32_t m = (n + NT - 1) / NT;
+    // terms per thread: ceil(n / NT), or the caller's m_run (>= that, <= MAXM)
+    const uint32_t m = m_run ? m_run : (n + NT - 1) / NT;
     const uint32_t k0 = tid * m;
+    // A wave whose threads hold no terms (n below its first term) only takes
+    // part in the barriers: its total is 0 and it records no break.
+    const bool live = (uint64_t)wid * 64u * m < n;
     // 1. float64 prefix before this thread's first term
-    double loc = 0.0;
+    double inc = 0.0, ex = 0.0;
+    if (live) {
+        double loc = 0.0;
 #pragma unroll
-    for (int j = 0; j < MAXM; j++) loc += (double)v[j];
-    const double inc = wm_wave_scan_f64(loc);
-    // exclusive prefix: the inclusive scan one lane down
-    double ex = __shfl_up(inc, 1, 64);
-    if (lane == 0) ex = 0.0;
+        for (int j = 0; j < MAXM; j++) loc += (double)v[j];
+        inc = wm_wave_scan_f64(loc);
+        // exclusive prefix: the inclusive scan one lane down
+        ex = __shfl_up(inc, 1, 64);
+        if (lane == 0) ex = 0.0;
+    }
     if (lane == 63) sc->dw[wid] = inc;
     wm_sync_lds();
+    after_scan();
+  if (live) {
     // the waves before this one: lane w < wid holds wave w's total, and a
     // scan along row 0 (NW <= 16 lanes) leaves their sum in lane 15
     double dl = (lane < (uint32_t)NW && lane < wid) ? sc->dw[lane] : 0.0;
@@ -425,6 +440,10 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
         sc->wcnt[wid] = nb_inc;
         sc->wpi[wid] = pi_inc;
     }
+  } else if (lane == 63) {
+    sc->wcnt[wid] = 0;
+    sc->wpi[wid] = 0u;
+  }
     wm_sync_lds();
     before_walk();
     // 3. the walk over the breaks (wave 0)
@@ -435,41 +454,48 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
         if (__builtin_amdgcn_ballot_w64(wc > R) != 0) {
             s = seq_sum_nonneg_from(0.0f, a, n);
         } else {
+            // every wave's inclusive record count and increment total, as
+            // wave-uniform values (SGPRs)
             const int cinc = wm_wave_scan_i32(wc);
             const uint32_t winc = wave_scan_u32(wp);
-            const int cex = cinc - wc;        // first record of wave `lane`
-            const uint32_t wex = winc - wp;   // increments of the waves before it
-            const int nbrk = __builtin_amdgcn_readlane(cinc, 63);
-            const uint32_t pi_tot = (uint32_t)__builtin_amdgcn_readlane((int)winc, 63);
+            int cs[NW];
+            uint32_t ps[NW];
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                cs[w] = __builtin_amdgcn_readlane(cinc, w);
+                ps[w] = (uint32_t)__builtin_amdgcn_readlane((int)winc, w);
+            }
+            const int nbrk = cs[NW - 1];
+            const uint32_t pi_tot = ps[NW - 1];
             const int *idx = &sc->idx[0][0], *eafp = &sc->eaf[0][0];
             const uint32_t *pis = &sc->pi[0][0];
             const float *vals = &sc->val[0][0];
-            // record base - 1, carried from the previous chunk: its wave + 1,
-            // term index, binade after it, increments before it
-            int c_w = 0, c_t = -1, c_e = -1000, c_p = 0;
+            // record base - 1, carried from the previous chunk: term index,
+            // binade after it, increments before it
+            int c_t = -1, c_e = -1000, c_p = 0;
             for (int base = 0; base <= nbrk; base += 64) {
                 // lane l prepares step r = base + l: the segment between
                 // records r-1 and r, then record r's term (r == nbrk: the
                 // end; r > nbrk: a step that changes nothing)
                 const int r = base + (int)lane;
-                // the wave holding record r: every wave with records marks
-                // the lane of its first one, and a running maximum carries
-                // the mark forward (waves are in record order)
-                sc->first[lane] = 0;
-                if ((int)lane < NW && wc > 0 && cex >= base && cex < base + 64)
-                    sc->first[cex - base] = (int)lane + 1;
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                const int wr = max(wave_max_scan_nonneg(sc->first[lane]), c_w);
-                const int w = max(wr - 1, 0);
-                const int cw = __shfl(cex, w, 64);
-                const uint32_t wo = (uint32_t)__shfl((int)wex, w, 64);
-                int t1 = (int)n, e1 = -1000, cnt = 0;
+                // record r belongs to wave wr: the waves whose records all
+                // come before r are exactly those with cs[w] <= r (counts
+                // are non-decreasing), and the last of them gives the
+                // records and increments before wave wr
+                int wr = 0, cex = 0;
+                uint32_t wo = 0;
+#pragma unroll
+                for (int w = 0; w < NW; w++) {
+                    const bool before = cs[w] <= r;
+                    wr += before ? 1 : 0;
+                    cex = before ? cs[w] : cex;
+                    wo = before ? ps[w] : wo;
+                }
+                int t1 = (int)n, e1 = -1000;
                 uint32_t p1 = pi_tot;
                 float v1 = 0.0f;
                 if (r < nbrk) {
-                    const int f = w * R + (r - cw);
+                    const int f = wr * R + (r - cex);
                     t1 = idx[f];
                     e1 = eafp[f];
                     p1 = wo + pis[f];
@@ -478,12 +504,11 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
                 // record r - 1: the lane below's (lane 0: the carry)
                 const int t0 = wave_shr1(t1, c_t), e0 = wave_shr1(e1, c_e);
                 const uint32_t p0 = (uint32_t)wave_shr1((int)p1, c_p);
-                c_w = __builtin_amdgcn_readlane(wr, 63);
                 c_t = __builtin_amdgcn_readlane(t1, 63);
                 c_e = __builtin_amdgcn_readlane(e1, 63);
                 c_p = __builtin_amdgcn_readlane((int)p1, 63);
-                if (r <= nbrk) cnt = t1 - t0 - 1;  // terms in the segment
-                const uint32_t dl = p1 - p0;       // their increments
+                const int cnt = r <= nbrk ? t1 - t0 - 1 : 0;  // terms in the segment
+                const uint32_t dl = p1 - p0;                   // their increments
                 const int D = dl <= (1u << 24) ? (int)dl : (1 << 30);
                 const int here = min(64, nbrk + 1 - base);
                 // When step r's check holds (s normal in binade e, s >= 2^e,
@@ -502,28 +527,25 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
                 const float hi = seg ? (e_ok ? ldexpf(16777214.0f, e0 - 23) : -1.0f)
                                      : __int_as_float(0x7F800000);
                 const float s0 = s;
-                // The steps' (A, V) through LDS, read back by every lane as
-                // broadcasts: the chain then runs on vector registers with
-                // no lane reads between its adds.  Steps past `here` add
-                // +0 twice, which changes no running sum (never -0).
-                sc->step[lane] = make_float2(A, v1);
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                // s as a per-lane value, so the compiler keeps the chain on
-                // the vector unit (all lanes hold the same number)
+                // The chain, step u's operands read from lane u, four steps
+                // per round (a lane past `here` holds A = V = +0, which
+                // changes no running sum); s stays a per-lane value (all
+                // lanes hold the same number) so the adds run on the vector
+                // unit.
                 float sv;
                 asm volatile("v_mov_b32 %0, %1" : "=v"(sv) : "v"(s));
                 float s_in = 0.0f;
-                for (int g = 0; g < here; g += 16) {
-                    float2 st[16];
+                for (int u = 0; u < here; u += 4) {
+                    float Au[4], Vu[4];
 #pragma unroll
-                    for (int u = 0; u < 16; u++) st[u] = sc->step[g + u];
-                    const int lg = (int)lane - g;  // this lane's step within the block
+                    for (int k = 0; k < 4; k++) {
+                        Au[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(A), u + k));
+                        Vu[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v1), u + k));
+                    }
 #pragma unroll
-                    for (int u = 0; u < 16; u++) {
-                        s_in = lg == u ? sv : s_in;
-                        sv = (sv + st[u].x) + st[u].y;
+                    for (int k = 0; k < 4; k++) {
+                        s_in = (int)lane == u + k ? sv : s_in;
+                        sv = (sv + Au[k]) + Vu[k];
                     }
                 }
                 s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sv)));
@@ -553,6 +575,7 @@ __device__ float seq_sum_block_owned(const float (&v)[MAXM], uint32_t n, const f
             }
         }
         if (lane == 0) sc->out = s;
+        after_walk(s);
     }
     wm_sync_lds();
     return sc->out;
