@@ -206,8 +206,8 @@ def i2s_stream(ctx, wh, copies: int, reps: int):
     """i2_s 2560x2560 matvec over `copies` distinct device copies (rotated
     through > 256 MB so the Infinity Cache cannot hold them), 64 per launch;
     then one standalone call of wm_bitlinear_i2s_matvec_f32_dev per copy
-    (quantise, dots, finalise: three launches), back to back, each call on
-    the next copy.  Returns the stream's ms per launch, its bytes, and the
+    (one launch: k_i2s_matvec_one), back to back, each call on the next
+    copy.  Returns the stream's ms per launch, its bytes, and the
     single call's ms."""
     seed = 0x5749_4C4C_0000_0001
     packed = wh.synth_i2s(seed, 1, 2560, 2560)
@@ -650,7 +650,7 @@ def main():
             "i2s_2560x2560_single_call": {"us": round(mv_single_ms * 1000, 3),
                                           "gbps": round(mv_single_gbps, 1),
                                           "frac": round(mv_single_gbps / HBM_PEAK_GBPS, 4),
-                                          "launches": 3},
+                                          "launches": 1},
         },
         "ragged_batch": batch,
         "decode_effective_gbps": round(decode_gbps, 1),

@@ -730,6 +730,109 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
     finish();
 }
 
+// --------------------------------------------------------------------------
+// The standalone matvec in one launch (bitlinear_i2s_matvec_f32,
+// src/model/bitlinear.rs:67; the quantiser of bitlinear_sse2.rs:285-304 on
+// the raw input, then the ternary dots, bitlinear_sse2.rs:327-339).
+//
+// One workgroup per 64 / KS rows of a 64-row group (KS lanes per row, as in
+// k_i2s_fused).  Its W waves split the chunks of K between them (wave w:
+// chunks [n_chunks*w/W, n_chunks*(w+1)/W), at most NC); each wave loads its
+// slice of x in the quantiser's layout and its slice of the weights, the
+// workgroup takes max|x| (NaN never counted: an order-free maximum, so every
+// workgroup gets the same one), each wave quantises its own slice into LDS
+// and dots its rows over it, and the partial dots (exact integers) meet in
+// LDS.  Workgroup 0 also writes the codes (the permuted layout of
+// wm_act_perm) and the scale and Σq when asked.
+// --------------------------------------------------------------------------
+template <int W, int NC, int KS>
+__global__ __launch_bounds__(W * 64) void k_i2s_matvec_one(const float *x, const uint8_t *w, uint32_t n_chunks,
+                                                           uint32_t out_dim, float w_scale, float *y,
+                                                           int32_t *dot_out, uint8_t *act_out,
+                                                           wm_act_meta *meta_out) {
+    static_assert(NC <= 4 * KS, "one register round of chunks per lane");
+    // act [n_chunks*16 ints] | zeros [16] | red [W][64]
+    extern __shared__ __align__(16) int smem[];
+    __shared__ float wave_max[W];
+    __shared__ int wave_q[W];
+    constexpr int NR = (NC + 3) / 4;  // quantiser rounds: four chunks per round
+    constexpr uint32_t R = 64 / KS;
+    const uint32_t g = blockIdx.x / KS, h = blockIdx.x % KS;
+    const uint32_t wid = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t lane = threadIdx.x & 63, tid = threadIdx.x;
+    const uint32_t sub = lane / R, row = h * R + lane % R;
+    const uint32_t c0 = n_chunks * wid / W, nc = n_chunks * (wid + 1) / W - c0;
+    const uint32_t n = n_chunks * 64;
+    const uint4 *wp[1] = {reinterpret_cast<const uint4 *>(w) + ((uint64_t)g * n_chunks + c0) * I2S_GROUP_ROWS + row};
+    i2s_round<1> A;
+    if (nc > 0) i2s_issue_ks<1, KS>(A, wp, 0, nc, sub);
+    int *act_s = smem;
+    int *zeros = smem + n_chunks * 16;
+    int *red = zeros + 16;
+    uint8_t *const act8 = reinterpret_cast<uint8_t *>(act_s);
+    const __amdgpu_buffer_rsrc_t rx = wm_rsrc(x, n * 4);
+    wm::fused_quads<NR> Q;
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const uint32_t off = Q.valid(r, c0, nc) ? wm::quad_col(r, c0) * 4 : n * 4;  // past the end: zeros
+        wm::buf_run<4>(rx, off, Q.v[r]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) Q.w[r][i] = 1.0f;  // no norm: y = x exactly
+    }
+    if (KS > 1 && tid < 16) zeros[tid] = 0;
+    float m = 0.0f;
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+        if (Q.valid(r, c0, nc))
+#pragma unroll
+            for (int i = 0; i < 4; i++) m = wm_max_nonan(m, fabsf(Q.v[r][i]));
+    m = wm_wave_max_nonan(m);
+    if (lane == 0) wave_max[wid] = m;
+    wm_sync_lds();
+    float max_abs = wave_max[0];
+#pragma unroll
+    for (int i = 1; i < W; i++) max_abs = wm_max_nonan(max_abs, wave_max[i]);
+    uint32_t qw[NR];
+    float dist[NR][4];
+    const int wave_asum = wm::fused_codes<NR, false>(Q, c0, nc, 1.0f, max_abs, act8, qw, dist);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int acc16[1] = {0}, acc4[1] = {0}, acc1[1] = {0};
+    if (nc > 0)
+        i2s_reduce_ks<1, KS>(A, act_s + c0 * 16, zeros, 0, (nc + KS - 1) / KS, nc, sub, acc16, acc4, acc1);
+    int p = (acc16[0] >> 4) + (acc4[0] >> 2) + acc1[0];
+    if constexpr (KS >= 8) p += __shfl_xor(p, 8, 64);
+    if constexpr (KS >= 4) p += __shfl_xor(p, 16, 64);
+    if constexpr (KS >= 2) p += __shfl_xor(p, 32, 64);
+    if (lane < R) red[wid * R + lane] = p - wave_asum;  // Σ(c - 1) a over the wave's slice
+    if (lane == 0) wave_q[wid] = wave_asum;
+    wm_sync_lds();
+    const float act_scale = max_abs == 0.0f ? 1.0f : max_abs / 127.0f;
+    if (tid < R) {
+        int dot = 0;
+#pragma unroll
+        for (int i = 0; i < W; i++) dot += red[i * R + tid];
+        const uint32_t j = g * 64 + h * R + tid;
+        if (j < out_dim) {
+            y[j] = (w_scale * act_scale) * (float)dot;
+            if (dot_out) dot_out[j] = dot;
+        }
+    }
+    if (blockIdx.x == 0) {
+        if (act_out)
+            for (uint32_t i = tid; i < n_chunks * 16; i += W * 64)
+                reinterpret_cast<int *>(act_out)[i] = act_s[i];
+        if (meta_out && tid == 0) {
+            int q = 0;
+#pragma unroll
+            for (int i = 0; i < W; i++) q += wave_q[i];
+            meta_out->scale = act_scale;
+            meta_out->asum = q;
+        }
+    }
+}
+
 __global__ void k_i2s_finalize(const int32_t *__restrict__ partial, uint32_t split,
                                uint32_t rows_total, uint32_t row0, uint32_t out_dim,
                                float w_scale, const wm_act_meta *__restrict__ meta,
@@ -913,6 +1016,44 @@ void wm_launch_i2s_finalize(const int32_t *partial, uint32_t split, uint32_t row
 // The fused matvec over the units of `n_tensors` tensors (see k_i2s_fused).
 // Waves per workgroup: n_chunks / 4 (one 4-chunk round each), at most 16.
 // Returns false (and launches nothing) when no instantiation fits the shape.
+bool wm_launch_i2s_matvec_one(const uint8_t *w, uint32_t n_groups, uint32_t n_chunks, uint32_t out_dim,
+                              float w_scale, const float *x, float *y, int32_t *dot_out, uint8_t *act_out,
+                              wm_act_meta *meta_out, hipStream_t s) {
+    constexpr int W = 16;
+    // NC: a power of two >= ceil(n_chunks / W), at most 16 (n_chunks <= 256)
+    uint32_t nc = 1;
+    while (nc * W < n_chunks) nc *= 2;
+    if (nc > 16 || n_groups == 0 || n_chunks == 0) return false;
+    // KS: as many workgroups per group as keep the grid within one per CU
+    // (at least NC / 4: one register round of chunks per lane)
+    static const uint32_t n_cus = [] {
+        int dev = 0, c = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+            c = 256;
+        return (uint32_t)c;
+    }();
+    uint32_t ks = 1;
+    while (ks < 8 && (uint64_t)n_groups * ks * 2 <= n_cus) ks *= 2;
+    while (ks * 4 < nc) ks *= 2;
+    const uint64_t grid = (uint64_t)n_groups * ks;
+    if (grid > 0x7FFFFFFFu) return false;
+    const size_t lds = (size_t)n_chunks * 64 + 64 + (size_t)W * 64 * 4;
+#define WM_MV_CASE(NC, KS)                                                                         \
+    if (nc == NC && ks == KS) {                                                                    \
+        hipLaunchKernelGGL((k_i2s_matvec_one<W, NC, KS>), dim3((uint32_t)grid), dim3(W * 64), lds, s, x, w, \
+                           n_chunks, out_dim, w_scale, y, dot_out, act_out, meta_out);             \
+        return true;                                                                               \
+    }
+    WM_MV_CASE(1, 1) WM_MV_CASE(1, 2) WM_MV_CASE(1, 4) WM_MV_CASE(1, 8)
+    WM_MV_CASE(2, 1) WM_MV_CASE(2, 2) WM_MV_CASE(2, 4) WM_MV_CASE(2, 8)
+    WM_MV_CASE(4, 1) WM_MV_CASE(4, 2) WM_MV_CASE(4, 4) WM_MV_CASE(4, 8)
+    WM_MV_CASE(8, 2) WM_MV_CASE(8, 4) WM_MV_CASE(8, 8)
+    WM_MV_CASE(16, 4) WM_MV_CASE(16, 8)
+#undef WM_MV_CASE
+    return false;
+}
+
 bool wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scales, float *const *outs,
                          int n_tensors, uint32_t n_chunks, uint32_t groups_per_unit,
                          const wm_fused_norm &norm, const float *rope_cos, const float *rope_sin,

@@ -284,8 +284,17 @@ struct mv_ws {
 };
 
 
+// One launch where the shape allows (k_i2s_matvec_one, in_dim <= 16384),
+// else the quantiser, the split partial dots and their sum.  The codes and
+// the quantiser's scale land in act and meta when want_codes (the other
+// path always writes them).
 static void run_matvec(wm_ctx *ctx, const wm_tensor *w, const float *d_x, float *d_y,
-                       int32_t *d_dot, uint8_t *act, wm_act_meta *meta, int32_t *partial) {
+                       int32_t *d_dot, uint8_t *act, wm_act_meta *meta, int32_t *partial,
+                       bool want_codes) {
+    if (wm_launch_i2s_matvec_one((const uint8_t *)w->d, w->n_groups, w->n_chunks, (uint32_t)w->out_dim,
+                                 w->scale, d_x, d_y, d_dot, want_codes ? act : nullptr,
+                                 want_codes ? meta : nullptr, ctx->stream))
+        return;
     uint32_t split = wm_i2s_pick_split(w->n_groups, w->n_chunks);
     uint32_t rows_total = w->n_groups * I2S_GROUP_ROWS;
     wm_launch_quantize_act(d_x, (uint32_t)w->in_dim, act, meta, ctx->stream);
@@ -325,7 +334,7 @@ wm_status wm_bitlinear_i2s_matvec_f32_debug(wm_ctx *ctx, const wm_tensor *w, con
     wm_act_meta *meta = (wm_act_meta *)(act + align256(w->in_dim));
     int32_t *partial = (int32_t *)((uint8_t *)meta + 256);
     WM_HIP(ctx, hipMemcpyAsync(d_x, input, w->in_dim * 4, hipMemcpyHostToDevice, ctx->stream));
-    run_matvec(ctx, w, d_x, d_y, d_dot, act, meta, partial);
+    run_matvec(ctx, w, d_x, d_y, d_dot, act, meta, partial, act_out || act_scale);
     WM_HIP(ctx, hipGetLastError());
     WM_HIP(ctx, hipMemcpyAsync(output, d_y, w->out_dim * 4, hipMemcpyDeviceToHost, ctx->stream));
     if (acc_out)
@@ -401,7 +410,7 @@ wm_status wm_bitlinear_i2s_matvec_f32_dev(wm_ctx *ctx, const wm_tensor *w, const
     wm_act_meta *meta = (wm_act_meta *)(act + align256(w->in_dim));
     int32_t *partial = (int32_t *)((uint8_t *)meta + 256);
     WM_HIP(ctx, hipSetDevice(ctx->device));
-    run_matvec(ctx, w, d_input, d_output, nullptr, act, meta, partial);
+    run_matvec(ctx, w, d_input, d_output, nullptr, act, meta, partial, false);
     WM_HIP(ctx, hipGetLastError());
     return WM_OK;
 }

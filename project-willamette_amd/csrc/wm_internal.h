@@ -349,6 +349,12 @@ void wm_launch_i2s_repack(const uint8_t *raw, uint8_t *out, uint32_t in_dim, uin
 // Quantise f32 x[n] -> permuted int8 act + meta (one workgroup).
 void wm_launch_quantize_act(const float *x, uint32_t n, uint8_t *act, wm_act_meta *meta,
                             hipStream_t s);
+// The whole standalone matvec in one launch (k_i2s_matvec_one): y, and when
+// non-null the integer dots, the codes in the permuted layout and the
+// quantiser's scale and Σq.  False (nothing launched) for n_chunks > 256.
+bool wm_launch_i2s_matvec_one(const uint8_t *w, uint32_t n_groups, uint32_t n_chunks, uint32_t out_dim,
+                              float w_scale, const float *x, float *y, int32_t *dot_out, uint8_t *act_out,
+                              wm_act_meta *meta_out, hipStream_t s);
 // Fused matvec modes (k_i2s_fused).
 constexpr int WM_FUSED_MAX_TENSORS = 3;
 enum { WM_FUSED_PLAIN = 0, WM_FUSED_GATEUP = 1, WM_FUSED_ROPE = 2 };

@@ -32,8 +32,10 @@ def assert_parity(got, ref):
     assert same_bits(y, ry), "f32 outputs differ"
 
 
+# 16384 is the widest input the one-launch matvec takes (256 chunks of 64
+# columns); 16512 goes through the split quantise / dots / finalise path
 SHAPES = [(128, 1), (128, 3), (256, 100), (640, 65), (2560, 2560), (2560, 640), (2560, 6912),
-          (6912, 2560), (128, 64), (4096, 128)]
+          (6912, 2560), (128, 64), (4096, 128), (16384, 100), (16512, 70)]
 
 
 @pytest.mark.parametrize("in_dim,out_dim", SHAPES)
