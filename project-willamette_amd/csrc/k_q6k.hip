@@ -496,13 +496,24 @@ __device__ __forceinline__ void q6_bounded_accum(const q6_lane_blocks<CH> &v, ui
 template <int CH, bool PIPE>
 __global__ __launch_bounds__(kBoundedBlock) void k_q6k_bounded(
     const uint8_t *__restrict__ w, uint32_t n_blocks, uint32_t n_rows, uint32_t n_rowgroups,
-    const float *__restrict__ sigma, const uint8_t *__restrict__ prep, float *__restrict__ approx,
-    float *__restrict__ bound, float *__restrict__ wg_lb, float *__restrict__ wg_ub) {
+    const float *__restrict__ sigma, const uint8_t *__restrict__ prep, const float *__restrict__ hidden,
+    float *__restrict__ approx, float *__restrict__ bound, float *__restrict__ wg_lb,
+    float *__restrict__ wg_ub) {
     extern __shared__ __align__(16) q6k_xq xq[];  // [n_blocks][16]
     __shared__ float red[kBoundedBlock / 64], red2[kBoundedBlock / 64];
-    for (uint32_t i = threadIdx.x; i < n_blocks * 16 * 3; i += blockDim.x)
-        reinterpret_cast<int4 *>(xq)[i] = reinterpret_cast<const int4 *>(prep)[i];
-    const q6k_xhdr hdr = *reinterpret_cast<const q6k_xhdr *>(prep + q6k_xq_bytes(n_blocks));
+    __shared__ int redi[kBoundedBlock / 64];
+    // the fixed-point copy of the hidden vector: prepared (by the output
+    // norm), or made here from `hidden` by every workgroup (the same
+    // operations as k_q6k_xprep, so every workgroup gets the same copy; one
+    // launch fewer)
+    q6k_xhdr hdr;
+    if (prep) {
+        for (uint32_t i = threadIdx.x; i < n_blocks * 16 * 3; i += blockDim.x)
+            reinterpret_cast<int4 *>(xq)[i] = reinterpret_cast<const int4 *>(prep)[i];
+        hdr = *reinterpret_cast<const q6k_xhdr *>(prep + q6k_xq_bytes(n_blocks));
+    } else {
+        hdr = q6k_xprep_block(hidden, n_blocks, xq, red, redi);
+    }
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -641,7 +652,11 @@ __global__ __launch_bounds__(kBoundedBlock) void k_q6k_bounded(
 // for row 0, whose exact value the NaN rule reads) have their rows scanned;
 // the rows that qualify are recomputed in the exact order (4 per wave pass)
 // and their logits overwritten with the exact values; the first index of the
-// maximum among them is the reference's argmax.
+// maximum among them is the reference's argmax.  When a single row qualifies
+// on its own bounds (the usual case), it is the argmax and no row is
+// recomputed.  The global loads come in rounds: the workgroup bounds, the
+// listed workgroups' rows, and only when rows are rescored, the hidden
+// vector and their weights.
 constexpr int kSelectBlock = 1024;
 constexpr uint32_t kSelectCap = 2048;  // candidate rows held at once
 
@@ -652,77 +667,126 @@ __device__ __forceinline__ void q6_select(
     const float *__restrict__ wg_lb, const float *__restrict__ wg_ub, uint32_t n_wg,
     uint32_t *__restrict__ argmax_out, const wm_step_tail &tail) {
     extern __shared__ float xs[];  // [16][n_blocks*16 + 4]
-    __shared__ uint32_t wg_list[kBoundedMaxBlocks];
+    __shared__ uint32_t wg_r0[kBoundedMaxBlocks], wg_r1[kBoundedMaxBlocks];  // listed workgroups' rows
     __shared__ uint32_t cand[kSelectCap];
-    __shared__ uint32_t n_wg_list, n_cand;
+    __shared__ uint32_t n_wg_list, n_cand, n_real;
     __shared__ float red[kSelectBlock / 64];
     __shared__ argcand s_c[kSelectBlock / 64];
     __shared__ float s_f0;
+    __shared__ bool s_q0, s_fin0;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // the hidden vector in lane order (xs[L*stride + b*16 + s] = x at
-    // b*256 + h*128 + k*32 + band*16 + c*4 + l, L = 4k + l, s = 4*(2h+band) + c)
+    // The workgroup bounds first (n_wg <= kBoundedMaxBlocks = 2 per thread).
+    static_assert(kBoundedMaxBlocks <= 2 * kSelectBlock, "two workgroup bounds per thread");
     const uint32_t stride = xs_stride(n_blocks);
-    for (uint32_t j = tid; j < n_blocks * 256; j += blockDim.x) {
-        const uint32_t b = j >> 8, h = (j >> 7) & 1, k = (j >> 5) & 3, band = (j >> 4) & 1,
-                       c = (j >> 2) & 3, l = j & 3;
-        xs[(4 * k + l) * stride + b * 16 + (2 * h + band) * 4 + c] = hidden[j];
+    float lbv[2], ubv[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const uint32_t i = tid + (uint32_t)k * kSelectBlock;
+        lbv[k] = i < n_wg ? wg_lb[i] : -INFINITY;
+        ubv[k] = i < n_wg ? wg_ub[i] : -INFINITY;
     }
-    float m = -INFINITY;
-    for (uint32_t i = tid; i < n_wg; i += blockDim.x) m = wm_max_nonan(m, wg_lb[i]);
+    bool xs_ready = false;  // the hidden vector in lane order, loaded for the first rescoring
     if (tid == 0) {
         n_wg_list = 0;
         n_cand = 0;
+        n_real = 0;
     }
-    const float lb_max = wm_block_max_nonan(m, red);  // (also orders the writes above)
-    for (uint32_t i = tid; i < n_wg; i += blockDim.x)
-        if (i == 0 || !(wg_ub[i] < lb_max)) wg_list[atomicAdd(&n_wg_list, 1u)] = i;
+    const float lb_max = wm_block_max_nonan(wm_max_nonan(lbv[0], lbv[1]), red);  // (also orders the writes above)
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const uint32_t i = tid + (uint32_t)k * kSelectBlock;
+        if (i < n_wg && (i == 0 || !(ubv[k] < lb_max))) {
+            const uint32_t li = atomicAdd(&n_wg_list, 1u);
+            wg_r0[li] = (uint32_t)((uint64_t)i * n_rowgroups / n_wg) * Q6K_GROUP_ROWS;
+            wg_r1[li] = min((uint32_t)((uint64_t)(i + 1) * n_rowgroups / n_wg) * Q6K_GROUP_ROWS, n_rows);
+        }
+    }
     __syncthreads();
+    // The rows of the listed workgroups, all at once: flat index f = li *
+    // rpw + j is row r0(li) + j (rpw: the most rows a workgroup of the
+    // bounded pass has), in passes of kSelectCap so the list cannot overflow.
     const uint32_t n_list = n_wg_list;
+    const uint32_t rpw = (n_rowgroups + n_wg - 1) / n_wg * Q6K_GROUP_ROWS;
+    const uint32_t total = n_list * rpw;
     const uint32_t slot = lane >> 4, L = lane & 15;
     const float *xl = xs + L * stride;
     float best_v = -INFINITY;
     uint32_t best_i = 0xFFFFFFFFu;
-    for (uint32_t li = 0; li < n_list; li++) {
-        const uint32_t wgi = wg_list[li];
-        const uint32_t r0 = (uint32_t)((uint64_t)wgi * n_rowgroups / n_wg) * Q6K_GROUP_ROWS;
-        const uint32_t r1 = min((uint32_t)((uint64_t)(wgi + 1) * n_rowgroups / n_wg) * Q6K_GROUP_ROWS, n_rows);
-        for (uint32_t base = r0; base < r1; base += blockDim.x) {
-            const uint32_t row = base + tid;
-            if (row < r1 && (row == 0 || !(logits[row] + bound[row] < lb_max)))
-                cand[atomicAdd(&n_cand, 1u)] = row;
-            __syncthreads();
-            const uint32_t nc = n_cand;
-            // rescore once the list could overflow on the next pass, and at the end
-            const bool last = li + 1 == n_list && base + blockDim.x >= r1;
-            if (nc + blockDim.x > kSelectCap || (last && nc)) {
-                for (uint32_t c0 = wave * 4; c0 < nc; c0 += 4 * (kSelectBlock / 64)) {
-                    const uint32_t ci = min(c0 + slot, nc - 1);
-                    const uint32_t crow = cand[ci];
-                    const uint8_t *gbase =
-                        w + (uint64_t)(crow / Q6K_GROUP_ROWS) * q6k_group_bytes(n_blocks);
-                    const uint32_t rr = crow % Q6K_GROUP_ROWS;
-                    const q6_lane_offs o = q6_offs(n_blocks, rr, L);
-                    float acc = 0.0f;
-                    for (uint32_t b0 = 0; b0 < n_blocks; b0 += CH) {
-                        q6_lane_blocks<CH> v;
-                        q6_load_lane<CH>(v, gbase, b0, o);
-                        q6_exact_accum<CH>(v, b0, xl, acc);
-                    }
-                    const float dot = q6_combine(acc);
-                    if (L == 0 && c0 + slot < nc) {
-                        logits[crow] = dot;
-                        if (crow == 0) s_f0 = dot;
-                        if (cand_better(dot, crow, best_v, best_i)) {
-                            best_v = dot;
-                            best_i = crow;
-                        }
-                    }
-                }
-                __syncthreads();
-                if (tid == 0) n_cand = 0;
+    // thread 0: the id out, and the greedy loop's ring slot and position
+    const auto publish = [&](uint32_t id) {
+        *argmax_out = id;
+        if (tail.pos) {
+            const uint32_t p = *tail.pos;
+            if (tail.ring) {
+                uint32_t *slot = tail.ring + 2 * (p & tail.ring_mask);
+                slot[0] = id;
+                slot[1] = *tail.err_flag;
+                __threadfence_system();
             }
+            *tail.pos = p + 1;
+        }
+    };
+    for (uint32_t f0 = 0; f0 < total; f0 += kSelectCap) {
+        for (uint32_t f = f0 + tid; f < min(f0 + kSelectCap, total); f += blockDim.x) {
+            const uint32_t li = f / rpw;
+            const uint32_t row = wg_r0[li] + (f - li * rpw), r1 = wg_r1[li];
+            if (row < r1) {
+                const float a = logits[row], b = bound[row];
+                const bool q = !(a + b < lb_max);  // NaN qualifies
+                if (row == 0) {
+                    s_q0 = q;
+                    s_fin0 = isfinite(a) && isfinite(b);
+                }
+                if (q || row == 0) cand[atomicAdd(&n_cand, 1u)] = row;
+                if (q) atomicAdd(&n_real, 1u);
+            }
+        }
+        __syncthreads();
+        const uint32_t nc = n_cand;
+        // One row qualifying on its own bounds (all rows in this pass): it is
+        // the row attaining LB, whose logit is at least LB, and every other
+        // row's is below LB, so it is the argmax and nothing is rescored.
+        // Row 0 then only matters for the NaN rule, and finite bounds rule a
+        // NaN logit out.
+        if (total <= kSelectCap && n_real == 1 && s_fin0) {
+            if (tid == 0) publish((cand[0] == 0 && !s_q0) ? cand[nc - 1] : cand[0]);
+            return;
+        }
+        if (!xs_ready) {  // (uniform) xs[L*stride + b*16 + s] = x at b*256 + h*128 + k*32 +
+                          // band*16 + c*4 + l, L = 4k + l, s = 4*(2h+band) + c
+            for (uint32_t j = tid; j < n_blocks * 256; j += blockDim.x) {
+                const uint32_t b = j >> 8, h = (j >> 7) & 1, k = (j >> 5) & 3, band = (j >> 4) & 1,
+                               c = (j >> 2) & 3, l = j & 3;
+                xs[(4 * k + l) * stride + b * 16 + (2 * h + band) * 4 + c] = hidden[j];
+            }
+            xs_ready = true;
             __syncthreads();
         }
+        for (uint32_t c0 = wave * 4; c0 < nc; c0 += 4 * (kSelectBlock / 64)) {
+            const uint32_t ci = min(c0 + slot, nc - 1);
+            const uint32_t crow = cand[ci];
+            const uint8_t *gbase = w + (uint64_t)(crow / Q6K_GROUP_ROWS) * q6k_group_bytes(n_blocks);
+            const uint32_t rr = crow % Q6K_GROUP_ROWS;
+            const q6_lane_offs o = q6_offs(n_blocks, rr, L);
+            float acc = 0.0f;
+            for (uint32_t b0 = 0; b0 < n_blocks; b0 += CH) {
+                q6_lane_blocks<CH> v;
+                q6_load_lane<CH>(v, gbase, b0, o);
+                q6_exact_accum<CH>(v, b0, xl, acc);
+            }
+            const float dot = q6_combine(acc);
+            if (L == 0 && c0 + slot < nc) {
+                logits[crow] = dot;
+                if (crow == 0) s_f0 = dot;
+                if (cand_better(dot, crow, best_v, best_i)) {
+                    best_v = dot;
+                    best_i = crow;
+                }
+            }
+        }
+        __syncthreads();
+        if (tid == 0) n_cand = 0;
+        __syncthreads();
     }
     for (int o = 32; o > 0; o >>= 1) {
         float ov = __shfl_xor(best_v, o, 64);
@@ -740,18 +804,7 @@ __device__ __forceinline__ void q6_select(
             if (cand_better(s_c[i].v, s_c[i].i, bc.v, bc.i)) bc = s_c[i];
         // a NaN logit at index 0 wins (the reference's scan starts from
         // logits[0] and NaN compares false); all -inf/NaN keeps index 0
-        const uint32_t id = (s_f0 != s_f0 || bc.i == 0xFFFFFFFFu) ? 0u : bc.i;
-        *argmax_out = id;
-        if (tail.pos) {
-            const uint32_t p = *tail.pos;
-            if (tail.ring) {
-                uint32_t *slot = tail.ring + 2 * (p & tail.ring_mask);
-                slot[0] = id;
-                slot[1] = *tail.err_flag;
-                __threadfence_system();
-            }
-            *tail.pos = p + 1;
-        }
+        publish((s_f0 != s_f0 || bc.i == 0xFFFFFFFFu) ? 0u : bc.i);
     }
 }
 template <int CH>
@@ -1012,19 +1065,19 @@ uint32_t bounded_blocks_for(uint32_t n_rowgroups, size_t lds) {
 
 template <int CH>
 uint32_t launch_bounded_ch(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
-                           uint32_t n_rowgroups, const uint8_t *prep, float *approx, float *bound,
-                           float *wg_lb, float *wg_ub, hipStream_t s) {
+                           uint32_t n_rowgroups, const uint8_t *prep, const float *hidden, float *approx,
+                           float *bound, float *wg_lb, float *wg_ub, hipStream_t s) {
     const size_t lds = sizeof(q6k_xq) * 16 * n_blocks;
     const float *sigma = reinterpret_cast<const float *>(w + wm_q6k_sigma_offset(n_rowgroups, n_blocks));
     if (kPipelined) {
         const uint32_t blocks = bounded_blocks_for<CH, true>(n_rowgroups, lds);
         hipLaunchKernelGGL((k_q6k_bounded<CH, true>), dim3(blocks), dim3(kBoundedBlock), lds, s, w,
-                           n_blocks, n_rows, n_rowgroups, sigma, prep, approx, bound, wg_lb, wg_ub);
+                           n_blocks, n_rows, n_rowgroups, sigma, prep, hidden, approx, bound, wg_lb, wg_ub);
         return blocks;
     }
     const uint32_t blocks = bounded_blocks_for<CH, false>(n_rowgroups, lds);
     hipLaunchKernelGGL((k_q6k_bounded<CH, false>), dim3(blocks), dim3(kBoundedBlock), lds, s, w,
-                       n_blocks, n_rows, n_rowgroups, sigma, prep, approx, bound, wg_lb, wg_ub);
+                       n_blocks, n_rows, n_rowgroups, sigma, prep, hidden, approx, bound, wg_lb, wg_ub);
     return blocks;
 }
 
@@ -1038,9 +1091,8 @@ void launch_argmax_fast_ch(const uint8_t *w, uint32_t n_blocks, uint32_t n_rows,
     float *bound = reinterpret_cast<float *>(wb + lay.bound);
     float *wg_lb = reinterpret_cast<float *>(wb + lay.wg_lb);
     float *wg_ub = reinterpret_cast<float *>(wb + lay.wg_ub);
-    if (!prepared)
-        hipLaunchKernelGGL(k_q6k_xprep, dim3(1), dim3(256), 0, s, hidden, n_blocks, wb + lay.prep);
-    const uint32_t n_wg = launch_bounded_ch<CH>(w, n_blocks, n_rows, n_rowgroups, wb + lay.prep,
+    const uint32_t n_wg = launch_bounded_ch<CH>(w, n_blocks, n_rows, n_rowgroups,
+                                                prepared ? wb + lay.prep : nullptr, hidden,
                                                 logits, bound, wg_lb, wg_ub, s);
     const size_t lds = sizeof(float) * 16 * xs_stride(n_blocks);
     hipLaunchKernelGGL(k_q6k_select<CH>, dim3(1), dim3(kSelectBlock), lds, s, w, n_blocks, n_rows,
@@ -1240,8 +1292,8 @@ void wm_launch_q6k_bounded_only(const uint8_t *w, uint32_t n_blocks, uint32_t n_
         hipLaunchKernelGGL(k_q6k_xprep, dim3(1), dim3(256), 0, s, hidden, n_blocks, wb + lay.prep);
 #define WM_B_CASE(C)                                                                               \
     case C:                                                                                        \
-        launch_bounded_ch<C>(w, n_blocks, n_rows, n_rowgroups, wb + lay.prep, approx, bound_out,  \
-                             wg_lb, wg_ub, s);                                                     \
+        launch_bounded_ch<C>(w, n_blocks, n_rows, n_rowgroups, wb + lay.prep, hidden, approx,     \
+                             bound_out, wg_lb, wg_ub, s);                                          \
         break;
     switch (pick_ch(n_blocks)) {
         WM_B_CASE(10) WM_B_CASE(8) WM_B_CASE(5) WM_B_CASE(4) WM_B_CASE(2) default: WM_B_CASE(1)

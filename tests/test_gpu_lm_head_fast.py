@@ -3,9 +3,9 @@
 Bar: the returned id is the oracle's argmax (first index of the maximum,
 NaN rules) on every input, exactly.  That rests on one property, checked
 directly on every row: the bounded pass's value lies within its bound of the
-oracle's SSE2-order f32 logit, |approx - logit| <= bound.  The rows the
-rescoring step recomputes come back bit-identical to the oracle's logits
-(row 0 always, and the winning row).
+oracle's SSE2-order f32 logit, |approx - logit| <= bound.  When more than
+one row's bounds reach the largest lower bound, those rows are recomputed in
+the exact order; when a single row's do, it is the argmax as it stands.
 """
 import numpy as np
 import pytest
