@@ -151,15 +151,24 @@ __device__ __forceinline__ void i2s_reduce(const i2s_round<RG> &R, const int *ac
 // The same with KS lanes per row: lane sub-slice `sub` holds chunks
 // sub, sub + KS, sub + 2 KS, ... of the wave's slice (register u of round k:
 // chunk sub + KS (4k + u)); loads past the slice clamp to its last chunk and
-// their dots read a block of zero activations instead.
+// their dots read a block of zero activations instead.  Only the first cnt
+// registers (wave-uniform: the most any lane needs) are loaded, and with
+// KS > 1 only by the lanes whose chunk lies in the slice (the others hold
+// zeros): the CU's vector memory path moves every active lane's bytes, and
+// it is what the workgroup's first loads queue on.
 template <int RG, int KS>
 __device__ __forceinline__ void i2s_issue_ks(i2s_round<RG> &R, const uint4 *const (&wp)[RG], uint32_t k,
-                                             uint32_t nc, uint32_t sub) {
+                                             uint32_t nc, uint32_t sub, uint32_t cnt = 4) {
 #pragma unroll
-    for (int u = 0; u < 4; u++)
+    for (int u = 0; u < 4; u++) {
+        const uint32_t j = sub + KS * (4u * k + (uint32_t)u);
 #pragma unroll
-        for (int q = 0; q < RG; q++)
-            R.v[u][q] = wm_load_stream(wp[q] + min(sub + KS * (4u * k + (uint32_t)u), nc - 1) * I2S_GROUP_ROWS);
+        for (int q = 0; q < RG; q++) {
+            R.v[u][q] = make_uint4(0u, 0u, 0u, 0u);
+            if ((uint32_t)u < cnt && (KS == 1 || j < nc))
+                R.v[u][q] = wm_load_stream(wp[q] + min(j, nc - 1) * I2S_GROUP_ROWS);
+        }
+    }
 }
 template <int RG, int KS>
 __device__ __forceinline__ void i2s_reduce_ks(const i2s_round<RG> &R, const int *act_c0, const int *zeros,
@@ -343,10 +352,14 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
     // chunks, and SPEC needs them all resident (at most two rounds).
     constexpr bool SPEC = W >= 2 && NP <= 8;
     static_assert(KS == 1 || (SPEC && NP <= 4 * KS), "KS > 1: the speculating form, one register round");
+    // With SPEC the slices are NP chunks each (whole quantiser rounds, so
+    // every lane of a load has a column; the workgroup's first loads queue
+    // on the CU's vector memory path per instruction), from wave 1 on, as
+    // many waves as n_chunks needs; otherwise n_chunks spread over all W.
     constexpr uint32_t KW = SPEC ? W - 1 : W;  // waves with a slice of K
-    const uint32_t kw = SPEC ? (wid == 0 ? 0u : wid - 1) : wid;
-    const uint32_t c0 = n_chunks * kw / KW;
-    const uint32_t nc = SPEC && wid == 0 ? 0u : n_chunks * (kw + 1) / KW - c0;
+    const uint32_t kw = SPEC ? (wid == 0 ? KW : wid - 1) : wid;
+    const uint32_t c0 = SPEC ? min(kw * (uint32_t)NP, n_chunks) : n_chunks * kw / KW;
+    const uint32_t nc = SPEC ? min((uint32_t)NP, n_chunks - c0) : n_chunks * (kw + 1) / KW - c0;
     const uint64_t gstride = (uint64_t)n_chunks * I2S_GROUP_ROWS;  // uint4 per group
     const uint4 *wp[UG];
 #pragma unroll
@@ -362,41 +375,33 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
     float *sq = ys + UG * 64;
     const uint32_t n = n_chunks * 64;
     const bool relu2 = (chunks_flags & FUSED_RELU2) != 0, has_y = ny != nullptr;
-    // The norm's inputs first, in two layouts: the exact sum's (thread t:
-    // terms t*NP .. t*NP+NP-1; NP divides n, so a run lies wholly inside or
-    // wholly past the vector) and the quantiser's (fused_quads: four
-    // consecutive columns per lane and round, with their norm weights).
-    // Then the weights, whose loads are waited for only at the dots: the
-    // norm's waits are for loads issued before them.
+    // The norm's inputs first, once, in the quantiser's layout (fused_quads:
+    // four consecutive columns per lane and round, with their norm weights;
+    // the waves' slices cover the vector); the exact sum's layout (thread t:
+    // terms t*NP .. t*NP+NP-1) then comes from the squares in LDS.  Then the
+    // weights, whose loads are waited for only at the dots: the norm's waits
+    // are for loads issued before them.
     const __amdgpu_buffer_rsrc_t rx = wm_rsrc(nx, n * 4), ry = wm_rsrc(has_y ? ny : nx, n * 4),
                                  rw = wm_rsrc(nw, n * 4);
     const uint32_t k0 = threadIdx.x * NP;
-    const bool sum_wave = wid * 64u * NP < n;  // wave-uniform: the wave holds terms
-    float xs[NP], ysum[NP];
-#pragma unroll
-    for (int j = 0; j < NP; j++) xs[j] = ysum[j] = 0.0f;
-    if (sum_wave) {
-        wm::buf_run<NP>(rx, k0 * 4, xs);
-        if (has_y) wm::buf_run<NP>(ry, k0 * 4, ysum);
-    }
     wm::fused_quads<NR> Q;
     float yq[NR][4];
 #pragma unroll
     for (int r = 0; r < NR; r++) {
-        const uint32_t off = Q.valid(r, c0, nc) ? wm::quad_col(r, c0) * 4 : n * 4;  // past the end: zeros
-        wm::buf_run<4>(rx, off, Q.v[r]);
-        wm::buf_run<4>(rw, off, Q.w[r]);
-        if (has_y) {
-            wm::buf_run<4>(ry, off, yq[r]);
-        } else {
+        // (only the lanes whose chunk lies in the slice load)
 #pragma unroll
-            for (int i = 0; i < 4; i++) yq[r][i] = 0.0f;
+        for (int i = 0; i < 4; i++) Q.v[r][i] = Q.w[r][i] = yq[r][i] = 0.0f;
+        if (Q.valid(r, c0, nc)) {
+            const uint32_t off = wm::quad_col(r, c0) * 4;
+            wm::buf_run<4>(rx, off, Q.v[r]);
+            wm::buf_run<4>(rw, off, Q.w[r]);
+            if (has_y) wm::buf_run<4>(ry, off, yq[r]);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
     // (NP bounds the chunks per wave: at most 4 chunks, one round, when NP <= 4)
     i2s_round<UG> A, B;
-    if (nc > 0) i2s_issue_ks<UG, KS>(A, wp, 0, nc, sub);
+    if (nc > 0) i2s_issue_ks<UG, KS>(A, wp, 0, nc, sub, (nc + KS - 1) / KS);
     if constexpr (NP > 4 && KS == 1)
         if (nc > 4) i2s_issue<UG>(B, wp, 4, nc);  // and the second round, if the slice has one
     if (KS > 1 && threadIdx.x < 16) zeros[threadIdx.x] = 0;
@@ -438,46 +443,59 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
         const float r = x > 0.0f ? x : 0.0f;
         return relu2 ? (r * r) * y : (has_y ? x + y : x);
     };
-    float v2[NP];
-#pragma unroll
-    for (int j = 0; j < NP; j++) {
-        const uint32_t k = k0 + (uint32_t)j;
-        const float v = combine(xs[j], ysum[j]);
-        v2[j] = k < n ? v * v : 0.0f;
-    }
     // What the norm leaves for later kernels: x + y (the same f32 adds as
     // the norm's, never relu2's combination), each workgroup its contiguous
-    // share of the elements, from the sum layout's registers, and whether
-    // it is all finite.
+    // share of the elements, and whether it is all finite.
     bool nonfinite = false;
     if (nm.x_out && has_y) {
         const uint32_t lo = (uint32_t)((uint64_t)n * blockIdx.x / gridDim.x);
         const uint32_t hi = (uint32_t)((uint64_t)n * (blockIdx.x + 1) / gridDim.x);
 #pragma unroll
-        for (int j = 0; j < NP; j++) {
-            const uint32_t k = k0 + (uint32_t)j;
-            if (k >= lo && k < hi) {
-                const float v = xs[j] + ysum[j];
-                nm.x_out[k] = v;
-                nonfinite |= !isfinite(v);
-            }
+        for (int r = 0; r < NR; r++) {
+            const uint32_t col = wm::quad_col(r, c0);
+            if (Q.valid(r, c0, nc) && col + 4 > lo && col < hi)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float v = Q.v[r][i] + yq[r][i];
+                    if (col + i >= lo && col + i < hi) {
+                        nm.x_out[col + i] = v;
+                        nonfinite |= !isfinite(v);
+                    }
+                }
         }
     }
-    if (k0 < n) {  // the terms, for the sum's slow paths (a run lies wholly below n)
-        if constexpr (NP >= 4) {
+    // the squares to LDS in column order: the exact sum's terms (also read
+    // there by its slow paths)
 #pragma unroll
-            for (int j = 0; j < NP; j += 4)
-                *reinterpret_cast<float4 *>(sq + k0 + j) = make_float4(v2[j], v2[j + 1], v2[j + 2], v2[j + 3]);
-        } else {
-#pragma unroll
-            for (int j = 0; j < NP; j++) sq[k0 + j] = v2[j];
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < NR; r++)
+    for (int r = 0; r < NR; r++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) Q.v[r][i] = combine(Q.v[r][i], yq[r][i]);
+        if (Q.valid(r, c0, nc))
+            *reinterpret_cast<float4 *>(sq + wm::quad_col(r, c0)) =
+                make_float4(Q.v[r][0] * Q.v[r][0], Q.v[r][1] * Q.v[r][1], Q.v[r][2] * Q.v[r][2],
+                            Q.v[r][3] * Q.v[r][3]);
+    }
     wm::fused_max_candidates<NR, W>(Q, c0, nc, nl);
+    wm_sync_lds();
+    float v2[NP];  // this thread's run of terms (NP divides n: a run lies wholly inside or past it)
+    if (k0 < n) {
+        if constexpr (NP >= 4) {
+#pragma unroll
+            for (int j = 0; j < NP; j += 4) {
+                const float4 f = *reinterpret_cast<const float4 *>(sq + k0 + j);
+                v2[j] = f.x;
+                v2[j + 1] = f.y;
+                v2[j + 2] = f.z;
+                v2[j + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NP; j++) v2[j] = sq[k0 + j];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NP; j++) v2[j] = 0.0f;
+    }
     uint8_t *const act8 = reinterpret_cast<uint8_t *>(act_s);
     // the dots over this wave's slice, from the codes in act and the weights
     // resident in A (and B): part[q] = Σ c a over the slice for group q
@@ -765,7 +783,7 @@ __global__ __launch_bounds__(W * 64) void k_i2s_matvec_one(const float *x, const
     const uint32_t n = n_chunks * 64;
     const uint4 *wp[1] = {reinterpret_cast<const uint4 *>(w) + ((uint64_t)g * n_chunks + c0) * I2S_GROUP_ROWS + row};
     i2s_round<1> A;
-    if (nc > 0) i2s_issue_ks<1, KS>(A, wp, 0, nc, sub);
+    if (nc > 0) i2s_issue_ks<1, KS>(A, wp, 0, nc, sub, (nc + KS - 1) / KS);
     int *act_s = smem;
     int *zeros = smem + n_chunks * 16;
     int *red = zeros + 16;
