@@ -521,6 +521,7 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
     // corrected in the integer dot: the result is exactly the exact codes'.
     uint32_t qw[NR];
     float dist[NR][4];
+    float dmin = 1.0f;  // this lane's smallest dist (1: none)
     int wave_asum = 0;
     float rsq_s = 0.0f, max_s = 0.0f;
     bool spec_ok = false;
@@ -537,6 +538,11 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
                 spec_ok = max_s >= 0.0f;
                 if (spec_ok) {
                     wave_asum = wm::fused_codes<NR, true>(Q, c0, nc, rsq_s, max_s, act8, qw, dist);
+#pragma unroll
+                    for (int r = 0; r < NR; r++)
+                        if (Q.valid(r, c0, nc))
+#pragma unroll
+                            for (int i = 0; i < 4; i++) dmin = fminf(dmin, dist[r][i]);
                     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                     __builtin_amdgcn_wave_barrier();
                     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -580,8 +586,11 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
         const float bound = (float)(128.0 * (rho + 9.0 * 0x1p-24) + 0x1p-40);
         const float inv = 127.0f / max_abs;
         int n_fix = 0;
+        // (usually no element of the wave is that close: one test for all)
+        const bool any_close = __builtin_amdgcn_ballot_w64(dmin <= bound) != 0;
 #pragma unroll
         for (int r = 0; r < NR; r++) {
+            if (!any_close) break;
             const bool ok = Q.valid(r, c0, nc);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
