@@ -37,9 +37,9 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "i2_s/Q6_K matvec GB/s (% HBM peak) + decode tok/s, BitNet-2B shape, 1 GPU"
 # the kernel behind each role of the decode step (names as rocprofv3 prints them)
-ROLE_KERNEL = {"qkv": "k_i2s_fused<2, 2, 16, 3>", "attention": "k_attn_scores + k_attn_softmax_v<2>",
-               "o": "k_i2s_fused<0, 1, 16, 3>", "gate_up": "k_i2s_fused<0, 1, 16, 3>",
-               "down": "k_i2s_fused<0, 1, 16, 7>"}
+ROLE_KERNEL = {"qkv": "k_i2s_fused<2, 2, 16, 4, 8>", "attention": "k_attn_scores + k_attn_softmax_v<2>",
+               "o": "k_i2s_fused<0, 1, 16, 4, 4>", "gate_up": "k_i2s_fused<0, 1, 16, 4, 1>",
+               "down": "k_i2s_fused<0, 1, 16, 8, 4>"}
 HBM_PEAK_GBPS = 8000.0
 PREFILL, START_TOKEN = 1024, 15339
 
@@ -140,8 +140,8 @@ def ffn_block_stream(ctx, wh, bs, copies: int, reps: int):
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
             "us_at_70pct_hbm": round(FFN_BLOCK_BYTES / (0.7 * HBM_PEAK_GBPS * 1e9) * 1e6, 3),
             "copies": copies, "launches": 2,
-            "kernels": "k_i2s_fused<0, 1, 16, 3> (ffn_norm, gate, up) + "
-                       "k_i2s_fused<0, 1, 16, 7> (relu(gate)^2 * up, ffn_sub_norm, down)"}
+            "kernels": "k_i2s_fused<0, 1, 16, 4, 1> (ffn_norm, gate, up) + "
+                       "k_i2s_fused<0, 1, 16, 8, 4> (relu(gate)^2 * up, ffn_sub_norm, down)"}
 
 
 def decode_roles(ctx, wh, dev, dkv, cfg, reps: int):
