@@ -488,6 +488,22 @@ wm_status wm_debug_q6k_bounded_logits_dev(wm_ctx *ctx, const wm_tensor *token_em
 wm_status wm_debug_rerun_role(wm_model *m, wm_kv_cache *kv, uint32_t layer, uint32_t role,
                               uint32_t reps);
 
+/* No counterpart in the reference: a test hook for the norm-fused matvecs
+ * (every one launched on this context from now on).  They quantise
+ * speculatively from an approximate rsqrt and max|y| while the exact sum of
+ * squares runs, then correct the codes those could have changed; these bits
+ * force the rarer paths, whose results must still be exact:
+ *   WM_FUSED_DEBUG_SKEW_SMALL  the approximate max|y| off by 2^-12 (codes
+ *                              near a rounding boundary corrected one by one),
+ *   WM_FUSED_DEBUG_SKEW_LARGE  off by 2^-7 (too many: codes redone),
+ *   WM_FUSED_DEBUG_NO_CANDIDATES  max|y| from every wave's own maximum
+ *                              (the candidate lists treated as failed).
+ * 0 restores the normal behaviour. */
+#define WM_FUSED_DEBUG_SKEW_SMALL 1u
+#define WM_FUSED_DEBUG_SKEW_LARGE 2u
+#define WM_FUSED_DEBUG_NO_CANDIDATES 4u
+wm_status wm_debug_set_fused_flags(wm_ctx *ctx, uint32_t flags);
+
 /* ---- synthetic BitNet-shaped inputs (src/synth.rs) ------------------- */
 
 /* Counter-based SplitMix64 streams, identical on every host: value i of

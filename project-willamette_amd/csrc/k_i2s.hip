@@ -298,7 +298,14 @@ __global__ __launch_bounds__(64) void k_i2s_partial(i2s_multi m, uint32_t n_chun
 // tensors 1 and 2 begin (units, 16 bits each), n_chunks and flags.
 // Everything else is in i2s_fused_args, read once the first loads are out,
 // so the norm covers that round trip.
-enum : uint32_t { FUSED_RELU2 = 1u << 16 };
+enum : uint32_t {
+    FUSED_RELU2 = 1u << 16,
+    // test hooks (WM_FUSED_DEBUG_*): the speculation's max|y| skewed, the
+    // candidate lists treated as failed
+    FUSED_SKEW_SMALL = 1u << 17,
+    FUSED_SKEW_LARGE = 1u << 18,
+    FUSED_NO_CANDIDATES = 1u << 19
+};
 struct i2s_fused_args {
     float w_scale[WM_FUSED_MAX_TENSORS];
     float *out[WM_FUSED_MAX_TENSORS];
@@ -550,7 +557,9 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
                 }
             }
         },
-        [&](float sum_sq) { wm::fused_publish<W>(sum_sq, n, nm.eps, cand, nl); },
+        [&](float sum_sq) {
+            wm::fused_publish<W>(sum_sq, n, nm.eps, cand, nl, (chunks_flags & FUSED_NO_CANDIDATES) != 0);
+        },
         [&]() {
             // The speculation's rsqrt and max|y|, once, by the last wave (at
             // these sizes it holds no terms of the sum and waits anyway):
@@ -563,7 +572,11 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
                 const float r = wm::norm_rsq((float)S, n, nm.eps);
                 const wm::fused_cand_regs c = wm::fused_cand_fetch<W>(nl);
                 bool ok;
-                const float m = wm::fused_cand_max(c, r, ok);
+                float m = wm::fused_cand_max(c, r, ok);
+                // (test hooks: a skewed max|y| moves every code's p = y * 127 / max|y|;
+                // a skewed rsqrt alone would cancel in p)
+                if (chunks_flags & FUSED_SKEW_SMALL) m = m * (1.0f + 0x1p-12f);
+                if (chunks_flags & FUSED_SKEW_LARGE) m = m * (1.0f + 0x1p-7f);
                 if (lane == 0) {
                     nl.spec_rsq = r;
                     nl.spec_max = ok && r > 0.0f && r < 0x1p100f ? m : -1.0f;
@@ -1120,7 +1133,10 @@ bool wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
     a.rope_mask = rope_mask;
     a.absmax = absmax ? absmax->slots : nullptr;
     a.absmax_stride = absmax ? absmax->stride : 0;
-    const uint32_t chunks_flags = n_chunks | (norm.relu2_mul ? FUSED_RELU2 : 0u);
+    const uint32_t chunks_flags = n_chunks | (norm.relu2_mul ? FUSED_RELU2 : 0u) |
+                                  (norm.debug & WM_FUSED_DEBUG_SKEW_SMALL ? FUSED_SKEW_SMALL : 0u) |
+                                  (norm.debug & WM_FUSED_DEBUG_SKEW_LARGE ? FUSED_SKEW_LARGE : 0u) |
+                                  (norm.debug & WM_FUSED_DEBUG_NO_CANDIDATES ? FUSED_NO_CANDIDATES : 0u);
     // Waves: as many as the chunks allow, up to 16 (the norm at the start is
     // latency-bound and runs best on the widest workgroup; each wave still
     // has its own chunks), rounded down to an instantiated count.

@@ -188,6 +188,7 @@ bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, step_pos sp, float 
     // (whole heads, or a head's rows split over a few workgroups; NEOX RoPE
     // on Q and K at `pos`)
     wm_fused_norm an{};
+    an.debug = m->ctx->fused_debug;
     an.x = H[cur];
     an.w = L.attn_norm;
     an.eps = c.rms_eps;
@@ -227,6 +228,7 @@ bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, step_pos sp, float 
     }
     // attn_sub_norm, then O
     wm_fused_norm sn{};
+    sn.debug = m->ctx->fused_debug;
     sn.x = m->attn_out;
     sn.w = L.attn_sub_norm;
     sn.eps = c.rms_eps;
@@ -237,6 +239,7 @@ bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, step_pos sp, float 
         return false;
     // ffn_norm on hidden + wo_out, then gate and up (relu^2 * up)
     wm_fused_norm fn{};
+    fn.debug = m->ctx->fused_debug;
     fn.x = H[cur];
     fn.y = m->proj_out;
     fn.x_out = H[cur ^ 1];
@@ -256,6 +259,7 @@ bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, step_pos sp, float 
         return false;
     // ffn_sub_norm of relu(gate)^2 * up, then down
     wm_fused_norm dn{};
+    dn.debug = m->ctx->fused_debug;
     dn.x = m->h_ff;
     dn.y = m->h_up;
     dn.relu2_mul = 1;

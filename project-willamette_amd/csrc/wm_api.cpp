@@ -415,6 +415,14 @@ wm_status wm_bitlinear_i2s_matvec_f32_dev(wm_ctx *ctx, const wm_tensor *w, const
     return WM_OK;
 }
 
+wm_status wm_debug_set_fused_flags(wm_ctx *ctx, uint32_t flags) {
+    if (!ctx) return WM_E_ARG;
+    const uint32_t known = WM_FUSED_DEBUG_SKEW_SMALL | WM_FUSED_DEBUG_SKEW_LARGE | WM_FUSED_DEBUG_NO_CANDIDATES;
+    if (flags & ~known) return wm_set_error(ctx, WM_E_ARG, "set_fused_flags: unknown bits 0x%x", flags & ~known);
+    ctx->fused_debug = flags;
+    return WM_OK;
+}
+
 // ---------------------------------------------------------------------------
 // FFN block (ffn_block_forward, src/model/ffn.rs:73-136)
 // ---------------------------------------------------------------------------
@@ -447,6 +455,7 @@ static wm_status run_ffn(wm_ctx *ctx, const float *d_x, const float *d_norm_w, c
                          float *d_out, float *gu) {
     const uint32_t F = (uint32_t)gate->out_dim;
     wm_fused_norm fn{};
+    fn.debug = ctx->fused_debug;
     fn.x = d_x;
     fn.w = d_norm_w;
     fn.eps = eps;
@@ -455,6 +464,7 @@ static wm_status run_ffn(wm_ctx *ctx, const float *d_x, const float *d_norm_w, c
     const float gus[2] = {gate->scale, up->scale};
     float *guo[2] = {gu, gu + F};
     wm_fused_norm dn{};
+    dn.debug = ctx->fused_debug;
     dn.x = gu;
     dn.y = gu + F;
     dn.relu2_mul = 1;

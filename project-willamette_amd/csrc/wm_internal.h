@@ -43,6 +43,8 @@ struct wm_ctx {
     // Device address, on this context's device, of the file-scope scratch
     // array of wm_bitlinear_i2s_matvec_f32_dev_noalloc (wm_noalloc.hip).
     void *noalloc_scratch = nullptr;
+    // test hook: WM_FUSED_DEBUG_* bits for every fused matvec launched here
+    uint32_t fused_debug = 0;
 };
 
 // Objects created on a context keep their own device id: destroying them
@@ -379,6 +381,7 @@ struct wm_fused_norm {
     // nonzero: x is the gate projection and y the up projection of the FFN,
     // and the norm runs on relu(x)^2 * y (ffn.rs:37-65) instead of x + y
     uint32_t relu2_mul;
+    uint32_t debug;  // WM_FUSED_DEBUG_* (test hook), 0 normally
 };
 // Matvec that starts from its input's norm, with the K split inside each
 // workgroup and a fused epilogue (mode WM_FUSED_*): rows of tensor i go to

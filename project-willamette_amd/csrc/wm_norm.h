@@ -343,10 +343,11 @@ __device__ __forceinline__ float norm_rsq(float sum_sq, uint32_t n, float eps) {
 // candidate bound does not hold).
 template <int NW>
 __device__ __forceinline__ void fused_publish(float sum_sq, uint32_t n, float eps, const fused_cand_regs &c,
-                                              fused_norm_lds<NW> &L) {
+                                              fused_norm_lds<NW> &L, bool no_candidates = false) {
     const float rsq = norm_rsq(sum_sq, n, eps);
     bool ok;
     const float ya = fused_cand_max(c, rsq, ok);
+    ok = ok && !no_candidates;
     if ((threadIdx.x & 63) == 0) {
         L.rsq = rsq;
         L.maxabs = ok ? ya : -1.0f;

@@ -136,6 +136,7 @@ EXPORTS = {
     "wm_bitlinear_i2s_matvec_f32_scalar_dev": (C.c_int, _vp, _vp, _vp, _vp),
     "wm_bitlinear_i2s_matvec_f32_dev_noalloc": (C.c_int, _vp, _vp, _vp, _vp),
     "wm_debug_rerun_role": (C.c_int, _vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32),
+    "wm_debug_set_fused_flags": (C.c_int, _vp, C.c_uint32),
     "wm_bitlinear_i2s_matvec_f32_multi_dev": (C.c_int, _vp, C.POINTER(_vp), C.c_uint32, _vp, _vp),
     "wm_bitlinear_i2s_matmul_f32_dev": (C.c_int, _vp, _vp, _vp, C.c_uint32, _vp),
     "wm_bitlinear_i2s_matmul_f32": (C.c_int, _vp, _vp, _f32p, C.c_size_t, C.c_uint32, _f32p,

@@ -24,6 +24,9 @@ pub const WM_E_METADATA: wm_status = 12;
 pub const WM_E_BOUNDS: wm_status = 13;
 pub const WM_E_IO: wm_status = 14;
 pub const WM_E_NOT_IMPLEMENTED: wm_status = 15;
+pub const WM_FUSED_DEBUG_SKEW_SMALL: u32 = 1;
+pub const WM_FUSED_DEBUG_SKEW_LARGE: u32 = 2;
+pub const WM_FUSED_DEBUG_NO_CANDIDATES: u32 = 4;
 
 pub const WM_TYPE_I2S: c_int = 36;
 pub const WM_TYPE_Q6K: c_int = 14;
@@ -169,6 +172,7 @@ extern "C" {
     pub fn wm_debug_q6k_bounded_logits(ctx: *mut wm_ctx, token_embd: *const wm_tensor, hidden: *const f32, hidden_len: usize, approx: *mut f32, bound: *mut f32) -> wm_status;
     pub fn wm_debug_q6k_bounded_logits_dev(ctx: *mut wm_ctx, token_embd: *const wm_tensor, d_hidden: *const f32, d_approx: *mut f32, d_bound: *mut f32, reuse_prep: c_int) -> wm_status;
     pub fn wm_debug_rerun_role(m: *mut wm_model, kv: *mut wm_kv_cache, layer: u32, role: u32, reps: u32) -> wm_status;
+    pub fn wm_debug_set_fused_flags(ctx: *mut wm_ctx, flags: u32) -> wm_status;
     pub fn wm_synth_stream_seed(seed: u64, tag: u64) -> u64;
     pub fn wm_synth_i2s(seed: u64, tag: u64, packed: *mut u8, n_bytes: usize);
     pub fn wm_synth_normal(seed: u64, tag: u64, out: *mut f32, n: usize, sigma: f64);

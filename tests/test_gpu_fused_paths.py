@@ -1,0 +1,124 @@
+"""GPU parity of the norm-fused matvecs' rarer paths.
+
+The fused matvecs quantise speculatively from the rsqrt of the float64
+total of the squares while the exact sequential sum runs, then redo exactly
+the codes that the exact rsqrt and max|y| could change, or every code when
+too many could, or when max|y| cannot come from the candidate lists.  On
+ordinary inputs the first path almost always suffices; the test hook
+wm_debug_set_fused_flags forces the others (the approximate max|y| skewed
+by 2^-12 or 2^-7, the candidate lists treated as failed).  Bar: the same bits
+as without the hook, i.e. the oracle's: the FFN block (config 3's own
+inputs), small models' decode steps, and the BitNet-2B decode's first steps
+(ids and logits SHA-256 of tests/golden/bitnet2b_decode64.json).
+"""
+import hashlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import bitnet_synth as bs
+import oracle.oracle as orc
+import willamette_hip as wh
+from oracle.oracle_model import OracleModel
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+FLAGS = {"skew_small": 1, "skew_large": 2, "no_candidates": 4, "skew_small+no_candidates": 5}
+SMALL = bs.BitNetConfig(n_layers=2, n_embd=256, n_ff=512, n_heads=2, n_kv_heads=1, head_dim=128,
+                        vocab=1000, context_length=64)
+
+
+def same_bits(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+class fused_flags:
+    def __init__(self, ctx, flags):
+        self.ctx, self.flags = ctx, flags
+
+    def __enter__(self):
+        self.ctx.check(wh.lib.wm_debug_set_fused_flags(self.ctx.h, self.flags))
+
+    def __exit__(self, *exc):
+        self.ctx.check(wh.lib.wm_debug_set_fused_flags(self.ctx.h, 0))
+
+
+def test_unknown_flags_rejected(ctx):
+    with pytest.raises(wh.WillametteError) as e:
+        ctx.check(wh.lib.wm_debug_set_fused_flags(ctx.h, 8))
+    assert e.value.status == 6  # WM_E_ARG
+
+
+@pytest.mark.parametrize("name", list(FLAGS))
+def test_ffn_block_exact_on_forced_paths(ctx, name):
+    E, F = 2560, 6912
+    s = bs.master_seed(3)
+    g, u, d = wh.synth_i2s(s, 1, E, F), wh.synth_i2s(s, 2, E, F), wh.synth_i2s(s, 3, F, E)
+    sc = wh.synth_uniform(s, 4, 3, 0.5, 2.0)
+    nw, sw = wh.synth_uniform(s, 5, E, 0.9, 1.1), wh.synth_uniform(s, 6, F, 0.9, 1.1)
+    x = wh.synth_normal(s, 7, E)
+    tg, tu, td = (ctx.upload_i2s(g, float(sc[0]), E, F), ctx.upload_i2s(u, float(sc[1]), E, F),
+                  ctx.upload_i2s(d, float(sc[2]), F, E))
+    ref = orc.ffn_block(x, nw, g, sc[0], u, sc[1], d, sc[2], sw, F)
+    print(f"ffn block, flags {name}", flush=True)
+    with fused_flags(ctx, FLAGS[name]):
+        for f in (1.0, 1000.0, 1e-3):
+            xs = (x * np.float32(f)).astype(np.float32)
+            want = ref if f == 1.0 else orc.ffn_block(xs, nw, g, sc[0], u, sc[1], d, sc[2], sw, F)
+            assert same_bits(wh.ffn_block_forward(ctx, xs, nw, tg, tu, td, sw), want)
+
+
+@pytest.mark.parametrize("name", list(FLAGS))
+def test_small_model_decode_exact_on_forced_paths(ctx, name):
+    hm = bs.make_host_model(SMALL, seed=1234 + SMALL.n_layers)
+    dev, orm = bs.load_device_model(ctx, hm), OracleModel(hm)
+    dkv, okv = dev.kv_cache(SMALL.context_length), orm.kv(SMALL.context_length)
+    print(f"small model decode, flags {name}", flush=True)
+    with fused_flags(ctx, FLAGS[name]):
+        tok = 3
+        for pos in range(10):
+            h, logits, nxt = dkv.decode_step(tok, pos)
+            rh = okv.forward(tok, pos)
+            rlogits, rnxt = okv.logits_argmax(rh)
+            assert same_bits(h, rh) and same_bits(logits, rlogits) and nxt == rnxt, f"pos {pos}"
+            tok = nxt
+    dkv.close()
+    dev.close()
+    orm.close()
+
+
+@pytest.fixture(scope="module")
+def bitnet2b(ctx):
+    gold = json.loads((GOLDEN / "bitnet2b_decode64.json").read_text())
+    cfg = bs.BITNET_2B
+    seed = bs.master_seed(4)
+    hm = bs.make_host_model(cfg, seed)
+    dev = bs.load_device_model(ctx, hm)
+    k, v = bs.kv_prefill(cfg, seed, gold["prefill"])
+    dkv = dev.kv_cache(cfg.context_length)
+    dkv.append_positions(k, v)
+    del k, v, hm
+    yield gold, dkv
+    dkv.close()
+    dev.close()
+
+
+@pytest.mark.parametrize("name", list(FLAGS))
+def test_bitnet2b_decode_exact_on_forced_paths(ctx, bitnet2b, name):
+    """Every fused matvec of the BitNet-2B step on the forced path (QKV with
+    RoPE and split heads, O, gate/up, down): 6 steps, ids and logits."""
+    gold, dkv = bitnet2b
+    dkv.rollback(gold["prefill"])
+    tok, pos = gold["start_token"], gold["prefill"]
+    print(f"bitnet2b decode, flags {name}", flush=True)
+    with fused_flags(ctx, FLAGS[name]):
+        for step in range(6):
+            _, logits, nxt = dkv.decode_step(tok, pos)
+            assert hashlib.sha256(np.ascontiguousarray(logits, np.float32).tobytes()).hexdigest() == \
+                gold["logits_sha256"][step], f"step {step}"
+            assert nxt == gold["ids"][step]
+            tok, pos = nxt, pos + 1
