@@ -445,11 +445,16 @@ __device__ __forceinline__ float seq_sum_block_owned(const float (&v)[MAXM], uin
     sc->wpi[wid] = 0u;
   }
     wm_sync_lds();
-    before_walk();
-    // 3. the walk over the breaks (wave 0)
+    // 3. the walk over the breaks (wave 0), its first reads issued before
+    // the hook's (LDS answers a wave's reads in order)
+    int wc = 0;
+    uint32_t wp = 0u;
     if (wid == 0) {
-        const int wc = (int)lane < NW ? sc->wcnt[lane] : 0;
-        const uint32_t wp = (int)lane < NW ? sc->wpi[lane] : 0u;
+        wc = (int)lane < NW ? sc->wcnt[lane] : 0;
+        wp = (int)lane < NW ? sc->wpi[lane] : 0u;
+    }
+    before_walk();
+    if (wid == 0) {
         float s = 0.0f;
         if (__builtin_amdgcn_ballot_w64(wc > R) != 0) {
             s = seq_sum_nonneg_from(0.0f, a, n);
@@ -534,20 +539,36 @@ __device__ __forceinline__ float seq_sum_block_owned(const float (&v)[MAXM], uin
                 // unit.
                 float sv;
                 asm volatile("v_mov_b32 %0, %1" : "=v"(sv) : "v"(s));
-                float s_in = 0.0f;
-                for (int u = 0; u < here; u += 4) {
-                    float Au[4], Vu[4];
+                // The chain moves across the lanes: step u runs in lane u
+                // (its operands are that lane's A and V), and its output
+                // goes one lane up (a DPP shift) into lane u + 1 alone (a
+                // one-hot mask moving with it), so lane u ends holding the
+                // value s had entering step u.  No step needs a value
+                // broadcast through an SGPR (v_readlane, a compare's lane
+                // mask): on this part such a value reaches a VALU
+                // instruction ~35 cycles after it is written, and the
+                // broadcasts cost the walk more than its adds.
+                float cur = sv;  // lane 0: s entering step 0
+                uint32_t mk = lane == 1 ? 0xFFFFFFFFu : 0u;
+                // Eight steps per loop trip (a taken branch costs more than
+                // a step): the lanes past `here` hold A = V = +0 and are
+                // never checked, so the steps padded onto them change
+                // nothing; the last real step's output is kept as it passes.
+                // (`in` carries the chain: lane u + 1 of it holds step u's
+                // output; `cur` keeps each lane's own input, off the chain.)
+                float nxt = sv, in = sv, last = sv;
+                for (int u0 = 0; u0 < here; u0 += 8) {
 #pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        Au[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(A), u + k));
-                        Vu[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v1), u + k));
-                    }
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        s_in = (int)lane == u + k ? sv : s_in;
-                        sv = (sv + Au[k]) + Vu[k];
+                    for (int k = 0; k < 8; k++) {
+                        nxt = (in + A) + v1;  // lane u0 + k: step u0 + k
+                        in = __int_as_float(wave_shr1(__float_as_int(nxt), 0));
+                        cur = __uint_as_float((__float_as_uint(in) & mk) | (__float_as_uint(cur) & ~mk));
+                        mk = (uint32_t)wave_shr1((int)mk, 0);
+                        last = u0 + k == here - 1 ? nxt : last;
                     }
                 }
+                sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(last), here - 1));
+                const float s_in = cur;
                 s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sv)));
                 // lanes past `here` hold no step; a NaN s fails every check
                 const bool ok = (int)lane >= here || !seg || (s_in >= lo && s_in + A <= hi);
