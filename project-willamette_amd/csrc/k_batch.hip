@@ -651,58 +651,83 @@ struct attn_rows_args {
 constexpr int kScoreThreads = 256;  // positions per scores item, one per thread
 constexpr int kScoreTok = 8;        // tokens (of one sequence) per scores item
 
-// scores[t][h][p] for the kScoreTok tokens t0 .. t0+nt-1 of one sequence
-// (item blockIdx.x), the G query heads of the item's KV head and positions
-// p0 .. p0+255 below p1: thread p loads its K row once, dequantises it (read_into:
-// q8 * scale) and runs the nt*G chains Σ_i q[i] * k[i], each in dimension
-// order, then * (1/sqrt(head_dim)).  Positions past a token's own are
-// computed from rows other tokens of the batch have written and never read.
+// scores[t][h][p] for the NT tokens t0 .. t0+NT-1 of one sequence (item
+// it), the G query heads of the item's KV head and position p (this thread):
+// the thread loads its K row once, dequantises it (read_into: q8 * scale) and
+// runs the NT*G chains Σ_i q[i] * k[i], each in dimension order, then
+// * (1/sqrt(head_dim)).  The query values are the same for every lane and
+// are read as scalars.  Positions past a token's own are computed from rows
+// other tokens of the batch have written and never read.
+// Memory that no thread writes while the kernel runs, addressed so that the
+// compiler may read it through the scalar unit wherever the address is the
+// same for every lane.
+typedef const float __attribute__((address_space(4))) wm_const_f32;
+
+template <int HD, int G, int NT>
+__device__ __forceinline__ void scores_item(const int8_t *kp, float kscale, const float *qb,
+                                            uint64_t qstride, float *dst, uint64_t sstride,
+                                            float scale) {
+    float s[NT][G];
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+        for (int g = 0; g < G; g++) s[tt][g] = 0.0f;
+    // the next 16 codes are in flight while the current ones are used
+    int4 raw = *reinterpret_cast<const int4 *>(kp);
+#pragma unroll 1
+    for (int b = 0; b < HD / 16; b++) {
+        const int4 cur = raw;
+        if (b + 1 < HD / 16) raw = *reinterpret_cast<const int4 *>(kp + (b + 1) * 16);
+        float kd[16];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const uint32_t wd = e < 4 ? (uint32_t)cur.x : e < 8 ? (uint32_t)cur.y : e < 12 ? (uint32_t)cur.z : (uint32_t)cur.w;
+            kd[e] = (float)(int8_t)(wd >> (8 * (e & 3))) * kscale;  // read_into
+        }
+#pragma unroll
+        for (int tt = 0; tt < NT; tt++) {
+            const wm_const_f32 *qt = (const wm_const_f32 *)qb + (uint64_t)tt * qstride + b * 16;
+#pragma unroll
+            for (int g = 0; g < G; g++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) s[tt][g] = s[tt][g] + qt[g * HD + e] * kd[e];
+        }
+    }
+    // token tt, head g: dst[(tt * G + g) * sstride] (the token's rows follow
+    // its G heads' rows: n_heads rows per token, G of them this KV head's)
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+        for (int g = 0; g < G; g++) dst[(uint64_t)tt * qstride / HD * sstride + (uint64_t)g * sstride] = s[tt][g] * scale;
+}
+
+// One item per workgroup (blockIdx.x): its nt (1 .. kScoreTok) tokens and
+// positions p0 .. p0+255 below p1, one position per thread.
 template <int HD, int G>
 __global__ __launch_bounds__(kScoreThreads) void k_attn_scores_rows(attn_rows_args a) {
-    __shared__ __align__(16) float qs[kScoreTok][G][HD];
+    static_assert(kScoreTok == 8, "one case per token count");
     const wm_attn_item it = a.sc_items[blockIdx.x];
-    if (it.nt == 0) return;
-    const uint32_t kvh = it.unit, tid = threadIdx.x;
-    for (uint32_t i = tid; i < (uint32_t)(kScoreTok * G * HD); i += kScoreThreads) {
-        const uint32_t tt = i / (G * HD), r = i % (G * HD);
-        qs[tt][r / HD][r % HD] =
-            tt < it.nt ? a.q[(uint64_t)(it.t0 + tt) * a.n_heads * HD + (uint64_t)kvh * G * HD + r] : 0.0f;
-    }
-    __syncthreads();
-    const uint32_t p = it.p0 + tid;
-    if (p >= it.p1) return;
+    const uint32_t p = it.p0 + threadIdx.x;
+    if (it.nt == 0 || p >= it.p1) return;
+    const uint32_t kvh = it.unit;
     const wm_batch_tok tk = a.tok[it.t0];  // every token of the item: the same cache
     const uint64_t lay = (uint64_t)a.layer * tk.max_seq;
     const int8_t *kp = tk.k + (lay + p) * a.kv_dim + kvh * HD;
     const float kscale = tk.ks[lay + p];
-    float s[kScoreTok][G];
-#pragma unroll
-    for (int tt = 0; tt < kScoreTok; tt++)
-#pragma unroll
-        for (int g = 0; g < G; g++) s[tt][g] = 0.0f;
-#pragma unroll 1
-    for (int b = 0; b < HD / 16; b++) {
-        const int4 raw = *reinterpret_cast<const int4 *>(kp + b * 16);
-        float kd[16];
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const uint32_t wd = e < 4 ? (uint32_t)raw.x : e < 8 ? (uint32_t)raw.y : e < 12 ? (uint32_t)raw.z : (uint32_t)raw.w;
-            kd[e] = (float)(int8_t)(wd >> (8 * (e & 3))) * kscale;  // read_into
-        }
-#pragma unroll
-        for (int tt = 0; tt < kScoreTok; tt++)
-#pragma unroll
-            for (int g = 0; g < G; g++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) s[tt][g] = s[tt][g] + qs[tt][g][b * 16 + e] * kd[e];
+    const float *qb = a.q + (uint64_t)it.t0 * a.n_heads * HD + (uint64_t)kvh * G * HD;
+    const uint64_t qstride = (uint64_t)a.n_heads * HD;
+    float *dst = a.scores + ((uint64_t)it.t0 * a.n_heads + kvh * G) * a.score_stride + p;
+    const uint64_t ss = a.score_stride;
+    switch (it.nt) {
+        case 1: scores_item<HD, G, 1>(kp, kscale, qb, qstride, dst, ss, a.scale); break;
+        case 2: scores_item<HD, G, 2>(kp, kscale, qb, qstride, dst, ss, a.scale); break;
+        case 3: scores_item<HD, G, 3>(kp, kscale, qb, qstride, dst, ss, a.scale); break;
+        case 4: scores_item<HD, G, 4>(kp, kscale, qb, qstride, dst, ss, a.scale); break;
+        case 5: scores_item<HD, G, 5>(kp, kscale, qb, qstride, dst, ss, a.scale); break;
+        case 6: scores_item<HD, G, 6>(kp, kscale, qb, qstride, dst, ss, a.scale); break;
+        case 7: scores_item<HD, G, 7>(kp, kscale, qb, qstride, dst, ss, a.scale); break;
+        default: scores_item<HD, G, 8>(kp, kscale, qb, qstride, dst, ss, a.scale); break;
     }
-#pragma unroll
-    for (int tt = 0; tt < kScoreTok; tt++)
-        if ((uint32_t)tt < it.nt) {
-            float *dst = a.scores + ((uint64_t)(it.t0 + tt) * a.n_heads + kvh * G) * a.score_stride + p;
-#pragma unroll
-            for (int g = 0; g < G; g++) dst[(uint64_t)g * a.score_stride] = s[tt][g] * a.scale;
-        }
 }
 
 // out[t][h][d] = Σ_p w_h[p] * v_p[d] in position order (cached_forward.rs:
