@@ -739,8 +739,14 @@ __global__ __launch_bounds__(kScoreThreads) void k_attn_scores_rows(attn_rows_ar
 // loads in flight while the current one is summed) and the rows' weights; a
 // token's positions past its own get weight 0 (exact: a zero term leaves
 // the sum unchanged), so every tile runs in full.
+// The pass ends when its longest rows do (heads whose exps are non-zero
+// over the whole context, while most rows have one live tile), and what
+// such a row waits on is its waves' own work per tile; so each workgroup
+// takes one query head, although the heads of a KV group could share the
+// V dequantisation (BitNet-2B, 16 sequences: 133 us per layer with four
+// heads per workgroup, 99 with two, 90 with one).
 constexpr uint32_t kSvPos = 64;
-constexpr uint32_t kSvHeads = 4;  // query heads per workgroup (of one KV head's group)
+constexpr uint32_t kSvHeads = 1;  // query heads per workgroup (of one KV head's group)
 constexpr uint32_t kSvTok = 1;    // tokens per V item
 constexpr uint32_t kAttnTiles = 64;  // tiles of kSvPos positions per row (contexts <= 4096)
 
@@ -880,6 +886,43 @@ __global__ __launch_bounds__(kSmRows * 64) void k_attn_softmax_rows(attn_rows_ar
     if (lane == 0) a.row_scale[row] = sum > 0.0f ? 1.0f / sum : 1.0f;
 }
 
+// One group of 8 positions of a staged tile, as thread d reads it: the V
+// codes vt[q][d], the rows' scales and the C chains' weights.
+template <uint32_t C>
+struct sv_group {
+    int code[8];
+    float4 sc[2];
+    float4 w[C][2];
+};
+template <int HD, uint32_t C>
+__device__ __forceinline__ void sv_read(sv_group<C> &g, const int8_t (*vt)[HD], const float *vst,
+                                        const float (*wt)[kSvPos], uint32_t q0) {
+#pragma unroll
+    for (uint32_t j = 0; j < 8; j++) g.code[j] = vt[q0 + j][threadIdx.x];
+    g.sc[0] = *reinterpret_cast<const float4 *>(&vst[q0]);
+    g.sc[1] = *reinterpret_cast<const float4 *>(&vst[q0 + 4]);
+#pragma unroll
+    for (uint32_t c = 0; c < C; c++) {
+        g.w[c][0] = *reinterpret_cast<const float4 *>(&wt[c][q0]);
+        g.w[c][1] = *reinterpret_cast<const float4 *>(&wt[c][q0 + 4]);
+    }
+}
+// acc[c] += w * v for the group's positions in order (v = q8 * scale: read_into)
+template <uint32_t C>
+__device__ __forceinline__ void sv_sum(float (&acc)[C], const sv_group<C> &g) {
+    const float sc[8] = {g.sc[0].x, g.sc[0].y, g.sc[0].z, g.sc[0].w, g.sc[1].x, g.sc[1].y, g.sc[1].z, g.sc[1].w};
+    float v[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; j++) v[j] = (float)g.code[j] * sc[j];
+#pragma unroll
+    for (uint32_t c = 0; c < C; c++) {
+        const float w[8] = {g.w[c][0].x, g.w[c][0].y, g.w[c][0].z, g.w[c][0].w,
+                            g.w[c][1].x, g.w[c][1].y, g.w[c][1].z, g.w[c][1].w};
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) acc[c] = acc[c] + w[j] * v[j];
+    }
+}
+
 // G: query heads per workgroup, HG: per KV head (item unit = kv head * HG/G + part)
 template <int HD, int G, int HG>
 __global__ __launch_bounds__(HD) void k_attn_sv_rows(attn_rows_args a) {
@@ -955,20 +998,16 @@ __global__ __launch_bounds__(HD) void k_attn_sv_rows(attn_rows_args a) {
             sv_fetch<HD>(pr, vg, vsg, a.kv_dim, (uint32_t)__builtin_ctzll(mask) * kSvPos, n);
             wfetch((uint32_t)__builtin_ctzll(mask) * kSvPos);
         }
-#pragma unroll 2
-        for (uint32_t q = 0; q < kSvPos; q += 4) {
-            const float4 sc = *reinterpret_cast<const float4 *>(&vst[q]);
-            // read_into: q8 * scale
-            const float v0 = (float)vt[q][tid] * sc.x, v1 = (float)vt[q + 1][tid] * sc.y;
-            const float v2 = (float)vt[q + 2][tid] * sc.z, v3 = (float)vt[q + 3][tid] * sc.w;
+        // groups of 8 positions; a group's LDS reads are issued before the
+        // previous group is summed, so their latency overlaps that work
+        sv_group<C> ga, gb;
+        sv_read<HD, C>(ga, vt, vst, wt, 0);
 #pragma unroll
-            for (uint32_t c = 0; c < C; c++) {
-                const float4 w4 = *reinterpret_cast<const float4 *>(&wt[c][q]);
-                acc[c] = acc[c] + w4.x * v0;
-                acc[c] = acc[c] + w4.y * v1;
-                acc[c] = acc[c] + w4.z * v2;
-                acc[c] = acc[c] + w4.w * v3;
-            }
+        for (uint32_t q = 0; q < kSvPos; q += 16) {
+            sv_read<HD, C>(gb, vt, vst, wt, q + 8);
+            sv_sum<C>(acc, ga);
+            if (q + 16 < kSvPos) sv_read<HD, C>(ga, vt, vst, wt, q + 16);
+            sv_sum<C>(acc, gb);
         }
     }
 #pragma unroll
