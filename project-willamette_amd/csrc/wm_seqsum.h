@@ -54,6 +54,11 @@ __device__ __forceinline__ int wave_incl_scan_i32(int x) {
     return x;
 }
 
+// lane l - 1's value of x; lane 0 gets `first`
+__device__ __forceinline__ int wave_shr1(int x, int first) {
+    return __builtin_amdgcn_update_dpp(first, x, 0x138, 0xF, 0xF, false);  // wave_shr:1
+}
+
 // Terms handled per wave step (8 per lane).
 constexpr uint32_t kSeqBatch = 512;
 constexpr int kSeqLead = 128;  // leading terms added one by one
@@ -80,6 +85,17 @@ __host__ __device__ constexpr uint32_t seq_sum_padded(uint32_t n) {
 // One step: adds the 512 terms v (lane l holding terms 8l .. 8l+7 of the
 // step, 0 past the end) to s, which the step's first terms follow; `lead`
 // on the sum's first step.  v is consumed.  Every lane gets the same s.
+//
+// PARITY: halfway terms do not end a run.  Round-half-even takes a halfway
+// term a/u = k + 1/2 to the even one of N + k and N + k + 1, so its increment
+// is k + ((N + k) & 1) and the significand after it is even; the parity of
+// N before any term is therefore that of the increments since the last
+// halfway term (or since the run's start, plus N's own).  A segmented scan
+// of those parities over the wave (segments start at halfway terms) gives
+// every term its increment at once, and a run ends only at a crossing or a
+// huge or non-finite term.  For inputs with many halfway terms (squares of
+// values with few significant bits); without it, each one is a restart.
+template <bool PARITY = false>
 __device__ inline float seq_sum_step(float s, float (&v)[8], bool lead) {
     const uint32_t lane = threadIdx.x & 63;
     if (lead) {
@@ -104,13 +120,57 @@ __device__ inline float seq_sum_step(float s, float (&v)[8], bool lead) {
         int p[8], rho[8];
         bool bad[8];
         int run = 0;
+        if (!PARITY) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float r = ldexpf(v[j], sh);    // a / ulp(s); exact unless < 2^-126
+                const bool fin = r < 0x1p22f;         // false for NaN, inf, huge
+                const float rr = fin ? r : 0.0f;
+                bad[j] = !fin || rr - floorf(rr) == 0.5f;  // halfway: parity decides
+                rho[j] = (int)rintf(rr);
+            }
+        } else {
+            bool half[8];
+            // the lane's parity summary: bit 1 = it holds a halfway term,
+            // bit 0 = parity of the increments after its last one (of all
+            // of them when it holds none)
+            int x = 0;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float r = ldexpf(v[j], sh);
+                const bool fin = r < 0x1p22f;
+                const float rr = fin ? r : 0.0f;
+                half[j] = rr - floorf(rr) == 0.5f;
+                bad[j] = !fin;
+                rho[j] = half[j] ? (int)floorf(rr) : (int)rintf(rr);
+                x = half[j] ? 2 : x ^ (rho[j] & 1);
+            }
+            // inclusive segmented scan (a summary with bit 1 replaces what
+            // came before it; 0 is the identity), then one lane down
+            const auto comb = [](int left, int right) {
+                return (right & 2) ? right : ((left & 2) | ((left ^ right) & 1));
+            };
+            x = comb(wm_dpp<WM_DPP_ROW_SHR1, 0xF>(x), x);
+            x = comb(wm_dpp<WM_DPP_ROW_SHR2, 0xF>(x), x);
+            x = comb(wm_dpp<WM_DPP_ROW_SHR4, 0xF>(x), x);
+            x = comb(wm_dpp<WM_DPP_ROW_SHR8, 0xF>(x), x);
+            x = comb(wm_dpp<WM_DPP_ROW_BCAST15, 0xA>(x), x);
+            x = comb(wm_dpp<WM_DPP_ROW_BCAST31, 0xC>(x), x);
+            const int xe = wave_shr1(x, 0);
+            // parity of the significand before the lane's first term
+            int par = (xe & 2) ? (xe & 1) : ((N ^ xe) & 1);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                if (half[j]) {
+                    rho[j] += (par + rho[j]) & 1;  // to the even neighbour
+                    par = 0;
+                } else {
+                    par ^= rho[j] & 1;
+                }
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const float r = ldexpf(v[j], sh);    // a / ulp(s); exact unless < 2^-126
-            const bool fin = r < 0x1p22f;         // false for NaN, inf, huge
-            const float rr = fin ? r : 0.0f;
-            bad[j] = !fin || rr - floorf(rr) == 0.5f;  // halfway: parity decides
-            rho[j] = (int)rintf(rr);
             run += rho[j];
             p[j] = run;
         }
@@ -151,6 +211,7 @@ __device__ inline float seq_sum_step(float s, float (&v)[8], bool lead) {
 
 // Continues the sum from s (itself a left-to-right sum of earlier terms,
 // so s >= +0 or NaN); a needs no alignment and is read only below n.
+template <bool PARITY = false>
 __device__ inline float seq_sum_nonneg_from(float s, const float *a, uint32_t n) {
     const uint32_t lane = threadIdx.x & 63;
     for (uint32_t k = 0; k < n; k += kSeqBatch) {
@@ -158,7 +219,7 @@ __device__ inline float seq_sum_nonneg_from(float s, const float *a, uint32_t n)
         float v[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) v[j] = base + j < n ? a[base + j] : 0.0f;
-        s = seq_sum_step(s, v, k == 0);
+        s = seq_sum_step<PARITY>(s, v, k == 0);
         if (s != s) return s;
     }
     return s;
@@ -216,10 +277,13 @@ __device__ inline float seq_sum_nonneg(const float *a, uint32_t n) {
 // thread that computes its increments.
 //
 // With the squares of an RMSNorm (2560 or 6912 terms) a sum has about 18
-// breaks and a failed check in well under 1% of sums.  More than
-// kSeqWaveRecords breaks in one wave (adversarial inputs) send the whole sum
-// to the one-wave algorithm.
-constexpr int kSeqWaveRecords = 32;
+// breaks and a failed check in well under 1% of sums.  Squares of values
+// with few significant bits (Q6_K-dequantised embedding rows) put many
+// halfway terms among the first terms: up to ~75 breaks in the first wave of
+// a 512-thread sum of 2560 (a few rows in a hundred above 48).  More than
+// kSeqWaveRecords breaks in one wave send the whole sum to the one-wave
+// algorithm (with the parity scan, which takes halfway terms in its runs).
+constexpr int kSeqWaveRecords = 96;
 constexpr int kSeqMaxWaves = 16;
 
 // Increments are counted modulo 2^32: only differences over one segment are
@@ -256,10 +320,6 @@ __device__ __forceinline__ int wave_max_scan_nonneg(int x) {
     x = max(x, wm_dpp<WM_DPP_ROW_BCAST15, 0xA>(x));
     x = max(x, wm_dpp<WM_DPP_ROW_BCAST31, 0xC>(x));
     return x;
-}
-// lane l - 1's value of x; lane 0 gets `first`
-__device__ __forceinline__ int wave_shr1(int x, int first) {
-    return __builtin_amdgcn_update_dpp(first, x, 0x138, 0xF, 0xF, false);  // wave_shr:1
 }
 
 // the biased exponent field of a non-negative double: floor(log2 x) + 1023
@@ -457,7 +517,7 @@ __device__ __forceinline__ float seq_sum_block_owned(const float (&v)[MAXM], uin
     if (wid == 0) {
         float s = 0.0f;
         if (__builtin_amdgcn_ballot_w64(wc > R) != 0) {
-            s = seq_sum_nonneg_from(0.0f, a, n);
+            s = seq_sum_nonneg_from<true>(0.0f, a, n);
         } else {
             // every wave's inclusive record count and increment total, as
             // wave-uniform values (SGPRs)
@@ -587,7 +647,7 @@ __device__ __forceinline__ float seq_sum_block_owned(const float (&v)[MAXM], uin
                                 s = ldexpf((float)(N + Di), e - 23);
                             } else {  // the segment term by term
                                 const int tp = __builtin_amdgcn_readlane(t0, i);
-                                s = seq_sum_nonneg_from(s, a + tp + 1, (uint32_t)c);
+                                s = seq_sum_nonneg_from<true>(s, a + tp + 1, (uint32_t)c);
                             }
                         }
                         s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v1), i));

@@ -26,8 +26,45 @@ class PassCapReached(RuntimeError):
     pass
 
 
-def model_sum(a):
-    """Returns (sum, largest pass index used in any step)."""
+def _parity_increments(rr, half, N):
+    """Increments of one pass with halfway terms resolved (PARITY): lane
+    summaries (bit 1: the lane holds a halfway term; bit 0: parity of the
+    increments after its last one, or of all of them), their inclusive
+    segmented scan over the 64 lanes, one lane down, then each lane's terms
+    in order, as wm::seq_sum_step<true> does."""
+    rho = np.where(half, np.floor(rr), np.rint(rr)).astype(np.int64)
+    summ = np.zeros(LANES, np.int64)
+    for lane in range(LANES):
+        x = 0
+        for j in range(PER):
+            x = 2 if half[lane, j] else x ^ (int(rho[lane, j]) & 1)
+        summ[lane] = x
+
+    def comb(left, right):
+        return right if right & 2 else (left & 2) | ((left ^ right) & 1)
+
+    incl = [0] * LANES
+    acc = 0
+    for lane in range(LANES):
+        acc = comb(acc, int(summ[lane]))
+        incl[lane] = acc
+    out = rho.copy()
+    for lane in range(LANES):
+        xe = incl[lane - 1] if lane else 0
+        par = (xe & 1) if xe & 2 else ((N ^ xe) & 1)
+        for j in range(PER):
+            if half[lane, j]:
+                out[lane, j] += (par + int(rho[lane, j])) & 1
+                par = 0
+            else:
+                par ^= int(rho[lane, j]) & 1
+    return out
+
+
+def model_sum(a, parity=False, stats=None):
+    """Returns (sum, largest pass index used in any step).  parity: halfway
+    terms are resolved by the segmented parity scan instead of ending a run.
+    stats["passes"]: passes over all steps."""
     a = np.asarray(a, np.float32)
     n = a.size
     s = f32(0.0)
@@ -47,6 +84,8 @@ def model_sum(a):
             v[:LEAD // PER, :] = 0
         for ps in range(STEP + 1):
             max_pass = max(max_pass, ps)
+            if stats is not None:
+                stats["passes"] = stats.get("passes", 0) + 1
             if np.isnan(s):
                 return s, max_pass
             bits = int(np.array(s, np.float32).view(np.uint32))
@@ -58,8 +97,13 @@ def model_sum(a):
                 r = np.ldexp(v, sh).astype(np.float32)
             fin = r < f32(2.0 ** 22)
             rr = np.where(fin, r, f32(0)).astype(np.float32)
-            bad = (~fin) | ((rr - np.floor(rr)) == f32(0.5))
-            rho = np.rint(rr).astype(np.int64)
+            half = (rr - np.floor(rr)) == f32(0.5)
+            if parity:
+                bad = ~fin
+                rho = _parity_increments(rr, half, N)
+            else:
+                bad = (~fin) | half
+                rho = np.rint(rr).astype(np.int64)
             p = np.cumsum(rho, axis=1)
             incl = np.cumsum(p[:, -1])
             excl = incl - p[:, -1]
@@ -81,7 +125,7 @@ def model_sum(a):
     return s, max_pass
 
 
-WAVE_RECORDS = 32  # break records per wave the workgroup algorithm keeps (else: one-wave path)
+WAVE_RECORDS = 96  # break records per wave the workgroup algorithm keeps (else: one-wave path)
 BLOCK_THREADS = 1024
 
 
@@ -144,6 +188,7 @@ def model_block_sum(a, stats=None, nt=BLOCK_THREADS, start_prefix=None, near_rul
                 wave_pi[w] = wave_pi.get(w, 0) + int(np.rint(r))
     if stats is not None:
         stats["breaks"] = sum(len(r) for r in waves.values())
+        stats["max_wave_breaks"] = max((len(r) for r in waves.values()), default=0)
         stats["fallback_segments"] = 0
     if any(len(r) > WAVE_RECORDS for r in waves.values()):
         return model_sum(a)[0]
@@ -243,6 +288,88 @@ def test_model_fuzz():
             a[0] = f32(2 ** 24 - 1) * f32(2.0 ** rng.integers(-30, 0))
         got, _ = model_sum(a)
         assert same(got, sequential(a)), f"case {i} kind {kind} n {n}"
+
+
+@pytest.mark.parametrize("name,a", inputs(), ids=[c[0] for c in inputs()])
+def test_parity_model_matches_sequential(name, a):
+    got, max_pass = model_sum(a, parity=True)
+    assert same(got, sequential(a)), name
+    assert max_pass <= STEP
+
+
+def test_parity_model_fuzz():
+    rng = np.random.default_rng(12)
+    for i in range(300):
+        n = int(rng.integers(1, 2000))
+        sc = float(2.0 ** rng.integers(-20, 20))
+        kind = i % 3
+        if kind == 0:  # coarse grids: most terms are halfway at some binade
+            a = (rng.integers(0, 8, n) * sc).astype(np.float32)
+        elif kind == 1:
+            a = (rng.standard_normal(n) * sc).astype(np.float32) ** 2
+        else:
+            a = _q6k_like_squares(rng, n)
+        got, _ = model_sum(a, parity=True)
+        assert same(got, sequential(a)), f"case {i} kind {kind} n {n}"
+
+
+def _parity_sequential(rr, half, N):
+    """The increments of one pass evaluated term by term in sum order."""
+    out = np.zeros(rr.shape, np.int64)
+    par = N & 1
+    for t in range(rr.size):
+        lane, j = divmod(t, PER)
+        if half[lane, j]:
+            k = int(np.floor(rr[lane, j]))
+            out[lane, j] = k + ((par + k) & 1)
+            par = 0
+        else:
+            out[lane, j] = int(np.rint(rr[lane, j]))
+            par ^= int(out[lane, j]) & 1
+    return out
+
+
+def test_parity_scan_matches_term_by_term():
+    # the lane summaries and their segmented scan give every term the
+    # increment a term-by-term evaluation gives (halfway terms on the even
+    # neighbour of the running significand); sparse and dense halfway terms
+    rng = np.random.default_rng(13)
+    for i in range(200):
+        k = rng.integers(0, 9, (LANES, PER)).astype(np.float32)
+        half = rng.random((LANES, PER)) < [0.0, 0.02, 0.2, 0.6, 1.0][i % 5]
+        rr = np.where(half, k + f32(0.5), k).astype(np.float32)
+        N = int(rng.integers(1 << 23, 1 << 24))
+        assert (_parity_increments(rr, half, N) == _parity_sequential(rr, half, N)).all(), i
+
+
+def _q6k_like_squares(rng, n):
+    """Squares of Q6_K-dequantised values as the embedding rows hold them:
+    x = (d * sc) * q (d an f16 super-block scale, sc in [-32, 31] per 16
+    elements, q in [-32, 31]); their few significant bits put many squares
+    on halfway increments."""
+    x = np.empty(n, np.float32)
+    for b in range(0, n, 256):
+        d = np.float32(np.float16(abs(rng.standard_normal()) * 1e-3))
+        for c in range(b, min(b + 256, n), 16):
+            dd = np.float32(d * np.float32(rng.integers(-32, 32)))
+            q = rng.integers(-32, 32, min(16, n - c)).astype(np.float32)
+            x[c:c + 16] = (dd * q).astype(np.float32)
+    return (x * x).astype(np.float32)
+
+
+def test_parity_cuts_passes_on_embedding_squares():
+    # the rows of a step's first norm (some of them hold more than
+    # WAVE_RECORDS breaks in one wave of a 512-thread norm and go to the
+    # one-wave path): with halfway terms resolved in place a step needs far
+    # fewer passes
+    rng = np.random.default_rng(14)
+    plain, par = {}, {}
+    for _ in range(12):
+        a = _q6k_like_squares(rng, 2560)
+        got_p, _ = model_sum(a, parity=True, stats=par)
+        got, _ = model_sum(a, stats=plain)
+        assert same(got_p, sequential(a)) and same(got, sequential(a))
+    assert 2 * plain["passes"] >= 3 * par["passes"], (plain, par)
 
 
 def test_zero_increment_terms_never_end_a_run():
