@@ -37,7 +37,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "i2_s/Q6_K matvec GB/s (% HBM peak) + decode tok/s, BitNet-2B shape, 1 GPU"
 # the kernel behind each role of the decode step (names as rocprofv3 prints them)
-ROLE_KERNEL = {"qkv": "k_i2s_fused<2, 2, 16, 4, 8>", "attention": "k_attn_scores + k_attn_softmax_v<2>",
+ROLE_KERNEL = {"qkv": "k_i2s_fused<2, 2, 16, 4, 8>", "attention": "k_attn_decode<2>",
                "o": "k_i2s_fused<0, 1, 16, 4, 4>", "gate_up": "k_i2s_fused<0, 1, 16, 4, 1>",
                "down": "k_i2s_fused<0, 1, 16, 8, 4>"}
 HBM_PEAK_GBPS = 8000.0

@@ -497,11 +497,17 @@ wm_status wm_debug_rerun_role(wm_model *m, wm_kv_cache *kv, uint32_t layer, uint
  *                              near a rounding boundary corrected one by one),
  *   WM_FUSED_DEBUG_SKEW_LARGE  off by 2^-7 (too many: codes redone),
  *   WM_FUSED_DEBUG_NO_CANDIDATES  max|y| from every wave's own maximum
- *                              (the candidate lists treated as failed).
+ *                              (the candidate lists treated as failed),
+ *   WM_FUSED_DEBUG_ATTN_NO_WAIT   (below).
  * 0 restores the normal behaviour. */
 #define WM_FUSED_DEBUG_SKEW_SMALL 1u
 #define WM_FUSED_DEBUG_SKEW_LARGE 2u
 #define WM_FUSED_DEBUG_NO_CANDIDATES 4u
+/* Decode attention (one launch per layer) lets the workgroups that share a
+ * kv head wait for each other's scores; with this bit every such wait gives
+ * up at once, which must fail the step with WM_E_HIP and roll the cache
+ * back (never hang). */
+#define WM_FUSED_DEBUG_ATTN_NO_WAIT 8u
 wm_status wm_debug_set_fused_flags(wm_ctx *ctx, uint32_t flags);
 
 /* ---- synthetic BitNet-shaped inputs (src/synth.rs) ------------------- */

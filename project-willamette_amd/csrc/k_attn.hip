@@ -29,9 +29,8 @@ struct attn_args {
     uint32_t n_past, kv_dim, head_dim, group, score_stride;
     float scale;
     // This token's K (after RoPE) and V, [kv_dim] f32: position n_past - 1
-    // is not in the cache yet.  Each kernel quantises what it needs of them
-    // exactly as KVCache::append does; one workgroup of each writes the
-    // cache row (kv_dim bytes) and its scale.
+    // is not in the cache yet.  The kernel quantises what it needs of them
+    // exactly as KVCache::append does and writes the cache rows and scales.
     const float *k_new, *v_new;
     // absmax of k_new and v_new (float bits) as the QKV matvec leaves them:
     // slots whose maximum it is, k_new's [0, n), v_new's [stride, stride + n)
@@ -42,6 +41,17 @@ struct attn_args {
     // LDS are then sized for n_max, and a larger n_past launches nothing
     const uint32_t *pos_dev;
     uint32_t n_max;
+    // this launch's tag on its scores (never 0, and never the tag of an
+    // earlier launch whose words the scores buffer may still hold), the
+    // step's error flag and the value a failed wait raises it to
+    uint32_t tag;
+    uint32_t *err_flag;
+    uint32_t err_tag;
+    uint32_t gs;         // workgroups per kv head: group * head_dim / 16
+    uint32_t xstride;    // workgroup (g, j) has linear id j * xstride + g
+    uint32_t n_kv_heads;
+    uint32_t spin_limit; // polls before a wait gives up (0: at once, a test hook)
+    uint32_t sc_tile;    // positions per score tile: group * sc_tile <= kSvThreads
 };
 
 __device__ __forceinline__ uint32_t attn_n_past(const attn_args &a) {
@@ -67,86 +77,28 @@ __device__ __forceinline__ float kv_absmax_of(const attn_args &a, uint32_t which
     return wm_wave_max_nonneg(m);
 }
 
-// scores[h][p] = (Σ_i q_h[i] * k_p[i]) * scale.  64 cached positions per
-// workgroup of 256 threads; grid (n_heads, ceil((n_past - 1) / 64) + 1).
-// Wave w computes the products q_i * k_i of dims [w*hd/4, (w+1)*hd/4) for
-// the workgroup's 64 positions into LDS, then wave 0 adds each position's
-// products in order, one lane per position (the sum is a dependent chain;
-// the products are not, so four waves share them).  The last block of each
-// head scores position n_past - 1, whose K row is this token's k_new
-// quantised here exactly as KVCache::append does (head 0's also writes the
-// row to the cache).  It runs beside the cached blocks instead of after its
-// own loads.
-constexpr int kScThreads = 256;
-constexpr int kScStride = kMaxHeadDim + 4;  // floats per position row (16-byte rows, spread banks)
-__global__ __launch_bounds__(kScThreads) void k_attn_scores(attn_args a) {
-    __shared__ __align__(16) float prod[64 * kScStride];
-    const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const uint32_t n_past = attn_n_past(a);
-    if (n_past > a.n_max) return;
-    const uint32_t kvh = h / a.group, pnew = n_past - 1;
-    const uint32_t n_cached_blocks = (pnew + 63) / 64;  // the block after them scores pnew
-    if (blockIdx.y > n_cached_blocks) return;
-    const float *qh = a.q + (uint64_t)h * a.head_dim;
-    if (blockIdx.y == n_cached_blocks) {
-        const float kabs = kv_absmax_of(a, 0);
-        const float ksn = kv_scale(kabs);
-        for (uint32_t i = tid; i < a.head_dim; i += kScThreads) {
-            const float kd = (float)kv_q(a.k_new[kvh * a.head_dim + i], kabs) * ksn;  // read_into
-            prod[i] = qh[i] * kd;
-        }
-        if (h == 0) {
-            int8_t *k_row = const_cast<int8_t *>(a.k_cache) + (uint64_t)pnew * a.kv_dim;
-            for (uint32_t i = tid; i < a.kv_dim; i += kScThreads) k_row[i] = kv_q(a.k_new[i], kabs);
-            if (tid == 0) const_cast<float *>(a.k_scales)[pnew] = ksn;
-        }
-        wm_sync_lds();
-        if (tid == 0) {
-            float s = 0.0f;
-            for (uint32_t i = 0; i < a.head_dim; i += 4) {
-                const float4 f = *reinterpret_cast<const float4 *>(prod + i);
-                s = s + f.x; s = s + f.y; s = s + f.z; s = s + f.w;
-            }
-            a.scores[(uint64_t)h * a.score_stride + pnew] = s * a.scale;
-        }
-        return;
-    }
-    const uint32_t p = blockIdx.y * 64 + lane;
-    const bool live = p < pnew;
-    // this wave's 16-byte segments of the K row: hd/64 of them (2 or 1)
-    const uint32_t nseg = a.head_dim / 64, seg0 = wid * nseg;
-    const int8_t *kp = a.k_cache + (uint64_t)(live ? p : 0) * a.kv_dim + kvh * a.head_dim;
-    const float ksc = a.k_scales[live ? p : 0];
-    int4 raw[2];
-#pragma unroll
-    for (int b = 0; b < 2; b++)  // both loads in flight together
-        raw[b] = *reinterpret_cast<const int4 *>(kp + (seg0 + (b < (int)nseg ? b : 0)) * 16);
-    float *row = prod + lane * kScStride;
-#pragma unroll
-    for (int b = 0; b < 2; b++) {
-        if (b < (int)nseg) {
-            const int8_t *kb = reinterpret_cast<const int8_t *>(&raw[b]);
-            const uint32_t d0 = (seg0 + b) * 16;
-#pragma unroll
-            for (int t = 0; t < 16; t += 4) {
-                float4 f;
-                f.x = qh[d0 + t] * ((float)kb[t] * ksc);  // read_into: q as f32 * scale
-                f.y = qh[d0 + t + 1] * ((float)kb[t + 1] * ksc);
-                f.z = qh[d0 + t + 2] * ((float)kb[t + 2] * ksc);
-                f.w = qh[d0 + t + 3] * ((float)kb[t + 3] * ksc);
-                *reinterpret_cast<float4 *>(row + d0 + t) = f;
-            }
-        }
-    }
-    wm_sync_lds();
-    if (wid == 0 && live) {
-        float s = 0.0f;
-        for (uint32_t i = 0; i < a.head_dim; i += 4) {
-            const float4 f = *reinterpret_cast<const float4 *>(row + i);
-            s = s + f.x; s = s + f.y; s = s + f.z; s = s + f.w;
-        }
-        a.scores[(uint64_t)h * a.score_stride + p] = s * a.scale;
-    }
+// Scores cross from the workgroups that compute them to the workgroups
+// that use them inside one launch.  Each score is stored as one 64-bit word,
+// (tag << 32) | bits, by an agent-scope atomic store (relaxed): on gfx950
+// that goes through to the level every XCD's L2 agrees on, and a 64-bit
+// aligned store is seen whole or not at all.  The tag is the launch's own
+// (the host counts the launches), so a reader polls each of its scores with
+// agent-scope atomic loads until it carries this launch's tag: no arrival
+// counter, no fence, no L2 writeback or invalidation (__threadfence() or an
+// acquire fence cost several microseconds per launch here), and no wait
+// longer than the last score it needs.  A stale word can never pass for a
+// fresh one, so the tags carry the correctness; the agent scope only makes
+// the wait end.
+__device__ __forceinline__ void st_tagged(uint64_t *p, uint32_t tag, float v) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+// workgroup j of a kv head scores positions [p0_of(n, j, gs), p0_of(n, j + 1, gs))
+__device__ __forceinline__ uint32_t p0_of(uint32_t n, uint32_t j, uint32_t gs) {
+    return (uint32_t)((uint64_t)n * j / gs);
+}
+__device__ __forceinline__ uint64_t ld_tagged(const uint64_t *p) {
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 constexpr int kSvThreads = 1024;  // wave 0: the 16 chains; waves 1-15: products
@@ -156,24 +108,6 @@ constexpr int kSvStride = 244;     // floats per dim row of a product tile (16-b
 constexpr uint32_t kSvSerialSum = 64;  // longest exp list summed by one wave, one add at a time
 static_assert(kSvTile * (kSvDims / 4) == kSvThreads - 64, "one 4-dim unit per producer thread");
 
-// softmax over scores[h][0..n_past) then out[h][d] = Σ_p w_p * v_p[d] for
-// the 16 dimensions d0..d0+15 of head h.  Grid (n_heads, head_dim / 16).
-//
-// The workgroup first pulls its whole V slice (n_past x 16 int8: one
-// coalesced 16-byte load per position, 64 KB at 4096 positions) and the V
-// scales into LDS and its head's scores into registers, all loads in flight
-// at once.  All 16 waves then compute the softmax: max, exp, and the list of
-// positions whose exp is not exactly 0 (kept in position order; a zero term
-// changes neither the exp sum nor any output sum, so the reference's sums
-// over all positions equal the sums over this list).  The exp sum runs over
-// the list, left to right (one wave, one add at a time, for up to 64
-// terms; the workgroup's exact sum seq_sum_block_owned beyond), then the
-// normalisation.  Then,
-// tile by tile, waves 1-15 write products w_p * v_p[d] (4 dims of one listed
-// position per thread) while lanes 0-15 of wave 0 add the previous tile, one
-// chain per dimension, in position order.  Position n_past - 1 uses this
-// token's V, quantised from v_new (workgroup (0, 0) also writes the cache
-// row).
 // The largest of the workgroup's values (none of them NaN; -inf where a
 // thread has none), in every thread: a DPP reduction per wave (-inf fills
 // the lanes a shift leaves empty), one LDS exchange.  `red` is not in use
@@ -198,68 +132,223 @@ __device__ __forceinline__ float sv_block_max(float v, float *red) {
     return m;
 }
 
+// Decode attention for every head in one launch.  The gs = group *
+// head_dim / 16 workgroups of kv head g share its K and V rows:
+//
+// 1. Scores.  Workgroup (g, j) takes positions [j n / gs, (j + 1) n / gs)
+//    for all `group` query heads of g.  It loads those K rows once (one
+//    16-byte segment per thread, with its scale), dequantises them as
+//    read_into does, multiplies each value by every head's q into LDS, and
+//    each of its first group * np threads adds one chain
+//    s = (Σ_i q_h[i] * k_p[i]) * scale in order over i.  Position n - 1 is
+//    this token's k_new, quantised here exactly as KVCache::append does (its
+//    thread also writes the cache row segment, and kv head 0's the scale).
+//    The scores go out tagged with the launch's epoch (st_tagged).
+// 2. Workgroup (g, j) then serves query head g * group + j / (head_dim /
+//    16) and its 16 dimensions d0 = 16 (j % (head_dim / 16)): each thread
+//    polls its positions' scores until they carry this launch's tag, while
+//    its V slice (n x 16 int8: one 16-byte load per position) and the V
+//    scales come in.
+// 3. Softmax and V.  All 16 waves compute the softmax: max, exp, and the
+//    list of positions whose exp is not exactly 0 (kept in position order;
+//    a zero term changes neither the exp sum nor any output sum, so the
+//    reference's sums over all positions equal the sums over this list).
+//    The exp sum runs over the list, left to right (one wave, one add at a
+//    time, for up to 64 terms; the workgroup's exact sum
+//    seq_sum_block_owned beyond), then the normalisation.  Then, tile by
+//    tile, waves 1-15 write products w_p * v_p[d] (4 dims of one listed
+//    position per thread) while lanes 0-15 of wave 0 add the previous tile,
+//    one chain per dimension, in position order.  Position n - 1 uses this
+//    token's V, quantised from v_new (workgroup j = 0 of each kv head also
+//    writes the cache row segment, kv head 0's the scale).
+//
+// Every workgroup of the grid is resident at once (one per CU at most, far
+// fewer than the CUs), so every poll ends; it is bounded all the same.  K is
+// read once per launch and V once per XCD that serves its kv head (with
+// xstride 8, every workgroup of a kv head sits on one XCD: the dispatcher
+// deals linear workgroup ids to the 8 XCDs in turn).
 template <int MAXM>  // n_past <= MAXM * kSvThreads
-__global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
+__global__ __launch_bounds__(kSvThreads) void k_attn_decode(attn_args a) {
     extern __shared__ __align__(16) float sm[];
+    __shared__ float red[16];
+    __shared__ int wcnt[MAXM * 16];
+        __shared__ wm::seq_block_scratch seq_scratch;
+    __shared__ uint64_t exp_tab[32];
+    const uint32_t g = blockIdx.x % a.xstride, j = blockIdx.x / a.xstride;
+    if (g >= a.n_kv_heads) return;
     const uint32_t n = attn_n_past(a), pnew = n - 1;
     if (n > a.n_max) return;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wid = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6)), lane = tid & 63;
+    const uint32_t hd = a.head_dim, segs = hd / 16;
+    const uint32_t h = g * a.group + j / segs, d0 = (j % segs) * kSvDims;
+    if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
+
+    uint64_t *const scores64 = reinterpret_cast<uint64_t *>(a.scores);
+
+    // ---- phase 1: scores of positions [p0, p1) for the group's heads ----
+    const uint32_t p0 = p0_of(n, j, a.gs), p1 = p0_of(n, j + 1, a.gs);
+    const uint32_t pst = hd + 4;                  // floats per product row (spread banks)
+    float *qs = sm;                               // [group][hd]
+    float *qk = sm + a.group * hd;                // [group][sc_tile][pst] products
+    const int8_t *kseg = a.k_cache + g * hd;
+    const uint32_t row = tid / segs, sg = tid % segs;  // this thread's K row segment
+    for (uint32_t t0 = p0; t0 < p1; t0 += a.sc_tile) {
+        const uint32_t tp = min(a.sc_tile, p1 - t0);
+        const bool mine = row < tp, is_new = mine && t0 + row == pnew;
+        // the loads, all issued together: this thread's 16-byte K segment
+        // and its scale, or for the new position this token's k_new segment
+        // (and, in its wave, the absmax slots); q of the group's heads
+        uint32_t kw[4] = {0u, 0u, 0u, 0u};
+        float ksc = 0.0f;
+        float4 kn[4];
+        if (mine && !is_new) {
+            const int4 raw = *reinterpret_cast<const int4 *>(kseg + (uint64_t)(t0 + row) * a.kv_dim + sg * 16);
+            kw[0] = (uint32_t)raw.x; kw[1] = (uint32_t)raw.y; kw[2] = (uint32_t)raw.z; kw[3] = (uint32_t)raw.w;
+            ksc = a.k_scales[t0 + row];
+        }
+        if (is_new)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                kn[e] = *reinterpret_cast<const float4 *>(a.k_new + g * hd + sg * 16 + 4 * e);
+        if (t0 == p0)
+            for (uint32_t i = tid; i < a.group * hd / 4; i += kSvThreads)
+                reinterpret_cast<float4 *>(qs)[i] = reinterpret_cast<const float4 *>(a.q + (uint64_t)g * a.group * hd)[i];
+        // (the wave holding the new row computes k_new's absmax: uniform)
+        const bool new_wave = pnew >= t0 && pnew < t0 + tp && (pnew - t0) * segs / 64 == wid;
+        const float kabs = new_wave ? kv_absmax_of(a, 0) : 0.0f;
+        wm_sync_lds();
+        // this thread's 16 values of k_p (read_into: q as f32 * scale; the
+        // new row through KVCache::append's codes), times each head's q
+        if (mine) {
+            float kd[16];
+            if (is_new) {
+                const float ksn = kv_scale(kabs);
+                const float kv[16] = {kn[0].x, kn[0].y, kn[0].z, kn[0].w, kn[1].x, kn[1].y, kn[1].z, kn[1].w,
+                                      kn[2].x, kn[2].y, kn[2].z, kn[2].w, kn[3].x, kn[3].y, kn[3].z, kn[3].w};
+                uint32_t cw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int8_t c = kv_q(kv[e], kabs);
+                    cw[e / 4] |= (uint32_t)(uint8_t)c << (8 * (e % 4));
+                    kd[e] = (float)c * ksn;
+                }
+                // its workgroup writes the cache row segment, kv head 0's the scale
+                *reinterpret_cast<int4 *>(const_cast<int8_t *>(a.k_cache) + (uint64_t)pnew * a.kv_dim + g * hd +
+                                          sg * 16) = make_int4((int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3]);
+                if (g == 0 && sg == 0) const_cast<float *>(a.k_scales)[pnew] = ksn;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; e++) kd[e] = (float)(int8_t)(kw[e / 4] >> (8 * (e % 4))) * ksc;
+            }
+            for (uint32_t hh = 0; hh < a.group; hh++) {
+                const float *qr = qs + hh * hd + sg * 16;
+                float *dst = qk + (hh * a.sc_tile + row) * pst + sg * 16;
+#pragma unroll
+                for (int e = 0; e < 16; e += 4) {
+                    const float4 qv = *reinterpret_cast<const float4 *>(qr + e);
+                    *reinterpret_cast<float4 *>(dst + e) =
+                        make_float4(qv.x * kd[e], qv.y * kd[e + 1], qv.z * kd[e + 2], qv.w * kd[e + 3]);
+                }
+            }
+        }
+        wm_sync_lds();
+        // one chain per (head, position): s = Σ_i q_h[i] * k_p[i] in order
+        if (tid < a.group * tp) {
+            const uint32_t hh = tid / tp, pl = tid % tp;
+            const float *pr = qk + (hh * a.sc_tile + pl) * pst;
+            float s = 0.0f;
+            for (uint32_t i = 0; i < hd; i += 4) {
+                const float4 f = *reinterpret_cast<const float4 *>(pr + i);
+                s = s + f.x;
+                s = s + f.y;
+                s = s + f.z;
+                s = s + f.w;
+            }
+            st_tagged(scores64 + (uint64_t)(g * a.group + hh) * a.score_stride + t0 + pl, a.tag, s * a.scale);
+        }
+        if (t0 + a.sc_tile < p1) wm_sync_lds();
+    }
+
+    // ---- phase 2: this head's scores, once each carries the launch's tag ----
+    // The polls go out first, then the V slice and scales for phase 3
+    // (thread t takes positions t + i * kSvThreads, indices clamped so every
+    // load is unconditional) and this token's V.  A poll that never sees its tag gives up after
+    // spin_limit rounds and raises the error flag (the step then fails and
+    // is rolled back); spin_limit 0 (a test hook) gives up at once.
+    const uint32_t tag = a.tag;
+    const uint64_t *sc64 = scores64 + (uint64_t)h * a.score_stride;
+    uint64_t sw[MAXM];
+#pragma unroll
+    for (int i = 0; i < MAXM; i++) sw[i] = ld_tagged(sc64 + min(tid + (uint32_t)i * kSvThreads, n - 1));
+    const int8_t *vseg = a.v_cache + g * hd + d0;
+    uint32_t vr0[MAXM], vr1[MAXM], vr2[MAXM], vr3[MAXM];
+    float ss[MAXM];
+#pragma unroll
+    for (int i = 0; i < MAXM; i++) {
+        const uint32_t p = min(tid + (uint32_t)i * kSvThreads, n - 1);
+        const int4 t4 = *reinterpret_cast<const int4 *>(vseg + (uint64_t)p * a.kv_dim);
+        vr0[i] = t4.x; vr1[i] = t4.y; vr2[i] = t4.z; vr3[i] = t4.w;
+        ss[i] = a.v_scales[p];
+    }
+    // and this token's V: the workgroup's 16 values of v_new, and its absmax
+    // (every wave reduces the slots itself)
+    const float vnew = tid < kSvDims ? a.v_new[g * hd + d0 + tid] : 0.0f;
+    const float vabs = kv_absmax_of(a, 1);
+    {
+        uint32_t pending = 0;
+#pragma unroll
+        for (int i = 0; i < MAXM; i++) pending |= ((uint32_t)(sw[i] >> 32) != tag ? 1u : 0u) << i;
+        bool gave_up = a.spin_limit == 0;
+        for (uint32_t it = 0; pending && !gave_up; it++) {
+            if (it >= a.spin_limit) {
+                gave_up = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int i = 0; i < MAXM; i++)
+                if ((pending >> i) & 1u) {
+                    sw[i] = ld_tagged(sc64 + min(tid + (uint32_t)i * kSvThreads, n - 1));
+                    if ((uint32_t)(sw[i] >> 32) == tag) pending &= ~(1u << i);
+                }
+        }
+        if (gave_up && a.err_flag) atomicCAS(a.err_flag, 0u, a.err_tag);
+    }
+
+    // ---- phase 3: softmax over scores[h][0..n) and the V chains ----
     const uint32_t npad = (n + 3) & ~3u;
     float *cval = sm;                                     // [seq_sum_padded(n)] nonzero exps, then weights
     float *vsc = cval + wm::seq_sum_padded(n);            // [npad]
     int4 *vq = reinterpret_cast<int4 *>(vsc + npad);      // [npad] x 16 int8
     float *prod = reinterpret_cast<float *>(vq + npad);   // [2][kSvDims][kSvStride]
     uint16_t *cidx = reinterpret_cast<uint16_t *>(prod + 2 * kSvDims * kSvStride);  // [npad]
-    __shared__ float red[16];
-    __shared__ int wcnt[MAXM * 16];
-    __shared__ float ssum;
-    __shared__ wm::seq_block_scratch seq_scratch;
-    __shared__ uint64_t exp_tab[32];
-    const uint32_t h = blockIdx.x, d0 = blockIdx.y * kSvDims, tid = threadIdx.x;
-    const uint32_t wid = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6)), lane = tid & 63;
-    const uint32_t kvh = h / a.group;
-    const int8_t *vseg = a.v_cache + kvh * a.head_dim + d0;
-    const float *sc = a.scores + (uint64_t)h * a.score_stride;
-    const float vabs = kv_absmax_of(a, 1);
-    const bool v_writer = h == 0 && blockIdx.y == 0;
-    if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
-    // 1. the loads: thread t takes positions t + i * kSvThreads, its scores in
-    //    registers, the V slice and scales into LDS; indices clamped so that
-    //    every load is unconditional and all of them are in flight together
+    const bool v_writer = j == 0;
     float sv[MAXM];
     float m = -INFINITY;
-    {
-        int4 vr[MAXM];
-        float ss[MAXM];
 #pragma unroll
-        for (int i = 0; i < MAXM; i++) {
-            const uint32_t p = min(tid + (uint32_t)i * kSvThreads, n - 1);
-            vr[i] = *reinterpret_cast<const int4 *>(vseg + (uint64_t)p * a.kv_dim);
-            sv[i] = sc[p];
-            ss[i] = a.v_scales[p];
-        }
+    for (int i = 0; i < MAXM; i++) sv[i] = __uint_as_float((uint32_t)sw[i]);
 #pragma unroll
-        for (int i = 0; i < MAXM; i++) {
-            const uint32_t p = tid + (uint32_t)i * kSvThreads;
-            if (p < n) m = wm_max_nonan(m, sv[i]);
-            // the cache row of position n_past - 1 is stale (this token's V
-            // is written below, by other threads, with no barrier between):
-            // only the rows before it are copied
-            if (p < pnew) {
-                vq[p] = vr[i];
-                vsc[p] = ss[i];
-            }
+    for (int i = 0; i < MAXM; i++) {
+        const uint32_t p = tid + (uint32_t)i * kSvThreads;
+        if (p < n) m = wm_max_nonan(m, sv[i]);
+        // the cache row of position n - 1 is stale (this token's V is
+        // quantised below): only the rows before it are copied
+        if (p < pnew) {
+            vq[p] = make_int4(vr0[i], vr1[i], vr2[i], vr3[i]);
+            vsc[p] = ss[i];
         }
     }
-    // this token's V (position n_past - 1 is not in the cache yet)
+    // this token's V (position n - 1 is not in the cache yet)
     if (tid < kSvDims)
-        reinterpret_cast<int8_t *>(vq + pnew)[tid] = kv_q(a.v_new[kvh * a.head_dim + d0 + tid], vabs);
+        reinterpret_cast<int8_t *>(vq + pnew)[tid] = kv_q(vnew, vabs);
     if (tid == 0) vsc[pnew] = kv_scale(vabs);
-    // 2. softmax (attention.rs:45-73)
+    // softmax (attention.rs:45-73)
     // (the thread maxima are never NaN: a NaN score never wins above; a zero
     // maximum's sign, which the reduction order could change, does not reach
     // exp(s - max))
     const float mx = sv_block_max(m, red);
-    float *out = a.out + (uint64_t)h * a.head_dim + d0;
+    float *out = a.out + (uint64_t)h * hd + d0;
     if (!isfinite(mx)) {  // every weight becomes 0 -> output stays 0
         if (tid < kSvDims) out[tid] = 0.0f;
     } else {
@@ -294,35 +383,40 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
             }
         }
         wm_sync_lds();
-        // Σ exp left to right (attention.rs:63-66) over the compacted terms:
-        // up to kSvSerialSum by one wave, one add at a time; a longer list by
-        // the workgroup's exact sum (thread t takes terms t*m .. t*m+m-1)
-        float sum;
+        // Σ exp left to right (attention.rs:63-66) over the compacted terms.
         if (count <= kSvSerialSum) {
+            // Few terms (the usual case: most exps underflow to 0): wave 0
+            // alone finishes, lane k holding term k.  The sum one add at a
+            // time, w_k = e_k * (1 / sum), then per dimension d (lane d % 16)
+            // Σ_k w_k * v_k[d] in order.
             if (wid == 0) {
-                // 64 terms per step, one per lane; the next step's terms are
-                // read while this step's are added
+                const float ev = lane < count ? cval[lane] : 0.0f;
+                const uint32_t pv = lane < count ? (uint32_t)cidx[lane] : 0u;
                 float s;
                 asm volatile("v_mov_b32 %0, 0" : "=v"(s));
-                float v = lane < count ? cval[lane] : 0.0f;
-                for (uint32_t c = 0; c < count; c += 64) {
-                    const uint32_t nx = c + 64 + lane;
-                    const float vn = nx < count ? cval[nx] : 0.0f;
-                    const uint32_t here = count - c < 64u ? count - c : 64u;
-                    for (uint32_t k = 0; k < here; k++)
-                        s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)k));
-                    v = vn;
+                for (uint32_t k = 0; k < count; k++)
+                    s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), (int)k));
+                const float w = s > 0.0f ? ev * (1.0f / s) : ev;
+                float acc;
+                asm volatile("v_mov_b32 %0, 0" : "=v"(acc));
+                for (uint32_t k = 0; k < count; k++) {
+                    const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), (int)k));
+                    const uint32_t pk = (uint32_t)__builtin_amdgcn_readlane((int)pv, (int)k);
+                    const float vd = (float)reinterpret_cast<const int8_t *>(vq + pk)[lane & 15] * vsc[pk];  // read_into
+                    acc = acc + wk * vd;
                 }
-                if (lane == 0) ssum = s;
+                if (lane < kSvDims) out[lane] = acc;
             }
-            wm_sync_lds();
-            sum = ssum;
         } else {
+        // A longer list: the workgroup's exact sum (thread t takes terms
+        // t*m .. t*m+m-1), the normalisation, then the products by tiles.
+        float sum;
+        {
             float ev[MAXM];
             const uint32_t mm = (count + kSvThreads - 1) / kSvThreads, k0 = tid * mm;
 #pragma unroll
-            for (int j = 0; j < MAXM; j++)
-                ev[j] = ((uint32_t)j < mm && k0 + (uint32_t)j < count) ? cval[k0 + j] : 0.0f;
+            for (int jj = 0; jj < MAXM; jj++)
+                ev[jj] = ((uint32_t)jj < mm && k0 + (uint32_t)jj < count) ? cval[k0 + jj] : 0.0f;
             sum = wm::seq_sum_block_owned<MAXM, kSvThreads>(ev, count, cval, &seq_scratch);
         }
         if (sum > 0.0f) {
@@ -330,8 +424,8 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
             for (uint32_t k = tid; k < count; k += kSvThreads) cval[k] = cval[k] * inv;
         }
         wm_sync_lds();
-        // 3. products of tile t (waves 1-15) while wave 0 adds tile t - 1,
-        //    over the compacted positions in order
+        // products of tile t (waves 1-15) while wave 0 adds tile t - 1,
+        // over the compacted positions in order
         const uint32_t n_tiles = (count + kSvTile - 1) / kSvTile;
         const uint32_t pt = tid - 64, dq = pt / kSvTile, pl = pt % kSvTile;  // producer unit
         float acc = 0.0f;
@@ -373,15 +467,15 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
                         }
 #pragma unroll
                         for (int i = 0; i < kC; i++) {
-                            const float4 g = f[c4 & 1][i];
-                            acc = acc + g.x; acc = acc + g.y; acc = acc + g.z; acc = acc + g.w;
+                            const float4 gg = f[c4 & 1][i];
+                            acc = acc + gg.x; acc = acc + gg.y; acc = acc + gg.z; acc = acc + gg.w;
                         }
                     }
                 } else {
                     uint32_t q = 0;
                     for (; q + 4 <= tn; q += 4) {
-                        const float4 g = *reinterpret_cast<const float4 *>(src + q);
-                        acc = acc + g.x; acc = acc + g.y; acc = acc + g.z; acc = acc + g.w;
+                        const float4 gg = *reinterpret_cast<const float4 *>(src + q);
+                        acc = acc + gg.x; acc = acc + gg.y; acc = acc + gg.z; acc = acc + gg.w;
                     }
                     for (; q < tn; q++) acc = acc + src[q];
                 }
@@ -390,11 +484,12 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_softmax_v(attn_args a) {
         }
         if (wid == 0) __builtin_amdgcn_s_setprio(0);
         if (tid < kSvDims) out[tid] = acc;
+        }
     }
-    if (v_writer) {  // the cache row of position n_past - 1
-        int8_t *v_row = const_cast<int8_t *>(a.v_cache) + (uint64_t)pnew * a.kv_dim;
-        for (uint32_t i = tid; i < a.kv_dim; i += kSvThreads) v_row[i] = kv_q(a.v_new[i], vabs);
-        if (tid == 0) const_cast<float *>(a.v_scales)[pnew] = kv_scale(vabs);
+    if (v_writer) {  // kv head g's segment of the cache row of position n - 1
+        int8_t *v_row = const_cast<int8_t *>(a.v_cache) + (uint64_t)pnew * a.kv_dim + g * hd;
+        for (uint32_t i = tid; i < hd; i += kSvThreads) v_row[i] = kv_q(a.v_new[g * hd + i], vabs);
+        if (g == 0 && tid == 0) const_cast<float *>(a.v_scales)[pnew] = kv_scale(vabs);
     }
 }
 
@@ -424,34 +519,48 @@ __global__ __launch_bounds__(kMaxHeadDim) void k_attn_position_zero(const float 
 
 }  // namespace
 
-// Returns false (nothing launched) for a shape the kernels do not cover:
-// head_dim 64 or 128 (the scores kernel's four waves take head_dim / 64
-// 16-byte segments each), n_past in [1, 4096].
+// Returns false (nothing launched) for a shape the kernel does not cover:
+// head_dim 64 or 128, n_past in [1, 4096], n_heads a multiple of n_kv_heads
+// (at most 16 query heads per kv head).
+// `scores`: n_heads * score_stride 64-bit words (tagged scores), zero when
+// the model was created; `tag`: this launch's, 1 .. 2^32 - 1, a different
+// one for every launch on the buffer (a counter of launches).
 bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_scales,
                          const int8_t *v_cache, const float *v_scales, float *scores,
                          uint32_t score_stride, float *out, uint32_t n_heads, uint32_t n_kv_heads,
                          uint32_t head_dim, uint32_t n_past, float scale, const float *k_new,
                          const float *v_new, const uint32_t *kv_absmax, uint32_t kv_absmax_n,
-                         uint32_t kv_absmax_stride, hipStream_t s,
-                         const uint32_t *pos_dev, uint32_t n_max) {
+                         uint32_t kv_absmax_stride, uint32_t tag, uint32_t *err_flag,
+                         uint32_t err_tag, bool no_wait, hipStream_t s, const uint32_t *pos_dev,
+                         uint32_t n_max) {
     // with pos_dev, n_past comes from the device and n_max bounds it
     const uint32_t nb = pos_dev ? n_max : n_past;
-    if ((head_dim != 64 && head_dim != 128) || nb == 0 || nb > 4 * kSvThreads ||
-        nb > score_stride)
+    if ((head_dim != 64 && head_dim != 128) || nb == 0 || nb > 4 * kSvThreads || nb > score_stride ||
+        n_kv_heads == 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 16 || tag == 0)
         return false;
-    const uint32_t kv_dim = n_kv_heads * head_dim;
-    attn_args a{q, k_cache, k_scales, v_cache, v_scales, scores, out, n_past, kv_dim, head_dim,
-                n_heads / n_kv_heads, score_stride, scale, k_new, v_new, kv_absmax, kv_absmax_n,
-                kv_absmax_stride, pos_dev, nb};
-    hipLaunchKernelGGL(k_attn_scores, dim3(n_heads, (nb - 1 + 63) / 64 + 1), dim3(kScThreads), 0, s, a);
+    const uint32_t kv_dim = n_kv_heads * head_dim, group = n_heads / n_kv_heads;
+    const uint32_t gs = group * head_dim / kSvDims;
+    // kv head g's workgroups at linear ids g, g + 8, g + 16, ... (at most 8
+    // kv heads): all on one XCD, which then fetches its K and V rows once
+    const uint32_t xstride = n_kv_heads <= 8 ? 8u : n_kv_heads;
+    // positions per score tile: one chain per thread, one K segment per
+    // thread, and the products of the group's heads within 128 KiB of LDS
+    const uint32_t pst = head_dim + 4;
+    const uint32_t sc_tile = min(min((uint32_t)kSvThreads / group, (uint32_t)kSvThreads / (head_dim / 16)),
+                                 (uint32_t)((128u * 1024u / 4u - group * head_dim) / (group * pst)));
+    attn_args a{q, k_cache, k_scales, v_cache, v_scales, scores, out, n_past, kv_dim, head_dim, group,
+                score_stride, scale, k_new, v_new, kv_absmax, kv_absmax_n, kv_absmax_stride, pos_dev, nb,
+                tag, err_flag, err_tag, gs, xstride, n_kv_heads, no_wait ? 0u : (1u << 16), sc_tile};
     const size_t npad = ((size_t)nb + 3) & ~(size_t)3;
-    const size_t lds = (size_t)wm::seq_sum_padded(nb) * 4 + npad * (4 + 16) +
-                       (size_t)2 * kSvDims * kSvStride * 4 + npad * 2;
-    const dim3 grid(n_heads, head_dim / kSvDims);
+    const size_t lds_sv = (size_t)wm::seq_sum_padded(nb) * 4 + npad * (4 + 16) +
+                          (size_t)2 * kSvDims * kSvStride * 4 + npad * 2;
+    const size_t lds_sc = ((size_t)group * head_dim + (size_t)group * sc_tile * pst) * 4;
+    const size_t lds = lds_sv > lds_sc ? lds_sv : lds_sc;
+    const dim3 grid(xstride * gs);
     if (nb <= 2 * kSvThreads)
-        hipLaunchKernelGGL(k_attn_softmax_v<2>, grid, dim3(kSvThreads), lds, s, a);
+        hipLaunchKernelGGL(k_attn_decode<2>, grid, dim3(kSvThreads), lds, s, a);
     else  // nb <= 4096, the models' context limit
-        hipLaunchKernelGGL(k_attn_softmax_v<4>, grid, dim3(kSvThreads), lds, s, a);
+        hipLaunchKernelGGL(k_attn_decode<4>, grid, dim3(kSvThreads), lds, s, a);
     return true;
 }
 

@@ -27,12 +27,15 @@ bool wm_launch_rmsnorm_quant(float *x, const float *res_y, const float *w, uint3
                              uint8_t *act, wm_act_meta *meta_out, float *y_out,
                              uint32_t *err_flag, uint32_t layer_tag, void *q6k_prep,
                              uint32_t *clear2, hipStream_t s);
+// decode attention's tag in the step's error flag (above any layer tag)
+constexpr uint32_t kAttnWaitFlag = 0x80000000u;
 bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_scales,
                          const int8_t *v_cache, const float *v_scales, float *scores,
                          uint32_t score_stride, float *out, uint32_t n_heads, uint32_t n_kv_heads,
                          uint32_t head_dim, uint32_t n_past, float scale, const float *k_new,
                          const float *v_new, const uint32_t *kv_absmax, uint32_t kv_absmax_n,
-                         uint32_t kv_absmax_stride, hipStream_t s, const uint32_t *pos_dev = nullptr,
+                         uint32_t kv_absmax_stride, uint32_t tag, uint32_t *err_flag,
+                         uint32_t err_tag, bool no_wait, hipStream_t s, const uint32_t *pos_dev = nullptr,
                          uint32_t n_max = 0);
 bool wm_launch_attention_position_zero(const float *q, const float *k_new, const float *v_new,
                                        float *out, uint32_t n_heads, uint32_t n_kv_heads,
@@ -84,6 +87,9 @@ struct wm_model {
     float *logits = nullptr, *scores = nullptr;
     uint32_t *dscalars = nullptr;  // [0] token, [1] next token, [2] error flag, [3] greedy loop's
                                    // position
+    // the tag of the last decode attention launch (k_attn.hip): every launch
+    // takes the next one, 1 .. 2^32 - 1
+    uint32_t attn_tag = 0;
     // this token's K/V absmax as the QKV launch leaves them (wm_fused_absmax):
     // kv_absmax_stride slots each, kv_absmax_n of them written by every launch
     uint32_t *kv_absmax = nullptr;
@@ -171,6 +177,13 @@ struct step_pos {
     uint32_t n_max;
 };
 
+// The tag for the next decode attention launch on m's scores buffer: the
+// launches are counted, skipping 0 (the tag of the zeroed buffer).
+uint32_t next_attn_tag(wm_model *m) {
+    m->attn_tag = m->attn_tag == 0xFFFFFFFFu ? 1u : m->attn_tag + 1u;
+    return m->attn_tag;
+}
+
 bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, step_pos sp, float *const H[2],
                    int &cur, float *layer_trace_dev, int only = ROLE_ALL) {
     const uint32_t pos = sp.pos;
@@ -221,7 +234,9 @@ bool enqueue_layer(wm_model *m, wm_kv_cache *kv, uint32_t l, step_pos sp, float 
             if (!wm_launch_attention(m->q, kv->k + lay * KV, kv->ks + lay, kv->v + lay * KV,
                                      kv->vs + lay, m->scores, c.context_length, m->attn_out,
                                      c.n_heads, c.n_kv_heads, c.head_dim, pos + 1, scale, m->k_new,
-                                     m->v_new, m->kv_absmax, m->kv_absmax_n, m->kv_absmax_stride, s,
+                                     m->v_new, m->kv_absmax, m->kv_absmax_n, m->kv_absmax_stride,
+                                     next_attn_tag(m), m->dscalars + 2, kAttnWaitFlag | (l + 1),
+                                     (m->ctx->fused_debug & WM_FUSED_DEBUG_ATTN_NO_WAIT) != 0, s,
                                      sp.dev, sp.n_max))
                 return false;
         }
@@ -319,6 +334,17 @@ wm_status check_step(wm_model *m, wm_kv_cache *kv, uint32_t token, uint32_t pos)
     return WM_OK;
 }
 
+// The step's error flag (dscalars[2]): layer + 1 of the first non-finite
+// residual stream (the fused matvecs raise it), or kAttnWaitFlag | (layer +
+// 1) when decode attention's workgroups gave up waiting for each other (a
+// bounded wait that does not end in practice: every workgroup is resident).
+wm_status step_flag_error(wm_ctx *ctx, const char *what, uint32_t flag) {
+    if (flag & kAttnWaitFlag)
+        return wm_set_error(ctx, WM_E_HIP, "%s: attention workgroups stopped waiting at layer %u", what,
+                            (flag & ~kAttnWaitFlag) - 1);
+    return wm_set_error(ctx, WM_E_NONFINITE, "%s: non-finite hidden after layer %u", what, flag - 1);
+}
+
 // After the step: read the error flag; on a non-finite hidden the cache is
 // rolled back (cached_forward.rs:256-259) and the flag cleared.
 wm_status finish_step(wm_model *m, wm_kv_cache *kv, uint32_t pos, bool *failed) {
@@ -332,8 +358,7 @@ wm_status finish_step(wm_model *m, wm_kv_cache *kv, uint32_t pos, bool *failed) 
         WM_HIP(ctx, hipMemcpyAsync(m->dscalars + 2, &zero, 4, hipMemcpyHostToDevice, ctx->stream));
         WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
         kv->pos = pos;
-        return wm_set_error(ctx, WM_E_NONFINITE, "forward_with_cache: non-finite hidden after layer %u",
-                            flag - 1);
+        return step_flag_error(ctx, "forward_with_cache", flag);
     }
     kv->pos = pos + 1;
     return WM_OK;
@@ -620,7 +645,7 @@ wm_status wm_model_create(wm_ctx *ctx, const wm_model_config *cfg, wm_model **ou
         align256((size_t)m->kv_dim * 4), align256((size_t)m->kv_dim * 4),  // k_new, v_new
         align256((size_t)E * 4),                                  // proj_out
         align256((size_t)c.vocab_size * 4),                       // logits
-        align256((size_t)c.n_heads * c.context_length * 4),       // scores
+        align256((size_t)c.n_heads * c.context_length * 8),       // decode attention's tagged scores
         256,                                                      // device scalars
         align256((size_t)2 * 16 * c.n_kv_heads * 4),              // K/V absmax slots
         align256(wm_q6k_logits_work_bytes(c.vocab_size, c.n_embd / Q6K_VALUES)),  // lm-head work
@@ -1067,8 +1092,7 @@ wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *promp
         WM_HIP(ctx, hipMemcpyAsync(m->dscalars + 2, m->ring, 4, hipMemcpyHostToDevice, ctx->stream));
         WM_HIP(ctx, hipStreamSynchronize(ctx->stream));
         kv->pos = start;
-        return wm_set_error(ctx, WM_E_NONFINITE, "forward_with_cache: non-finite hidden after layer %u",
-                            failed_flag - 1);
+        return step_flag_error(ctx, "forward_with_cache", failed_flag);
     }
     if (enq > done) {
         // Steps queued past an EOS stop ran as well, and the error flag is

@@ -49,7 +49,7 @@ class fused_flags:
 
 def test_unknown_flags_rejected(ctx):
     with pytest.raises(wh.WillametteError) as e:
-        ctx.check(wh.lib.wm_debug_set_fused_flags(ctx.h, 8))
+        ctx.check(wh.lib.wm_debug_set_fused_flags(ctx.h, 16))
     assert e.value.status == 6  # WM_E_ARG
 
 
@@ -122,3 +122,43 @@ def test_bitnet2b_decode_exact_on_forced_paths(ctx, bitnet2b, name):
                 gold["logits_sha256"][step], f"step {step}"
             assert nxt == gold["ids"][step]
             tok, pos = nxt, pos + 1
+
+
+ATTN_NO_WAIT = 8
+
+
+def test_attention_wait_gives_up_without_hanging(ctx):
+    """Decode attention's workgroups of a kv head meet once their scores are
+    out (a bounded wait).  With the hook every wait gives up at once: the
+    step must fail (WM_E_HIP, the layer named), leave the cache where it
+    was, and the following steps must be the oracle's bit for bit (the
+    arrival counters stay consistent after a failed launch)."""
+    hm = bs.make_host_model(SMALL, seed=77)
+    dev, orm = bs.load_device_model(ctx, hm), OracleModel(hm)
+    dkv, okv = dev.kv_cache(SMALL.context_length), orm.kv(SMALL.context_length)
+    tok = 5
+    for pos in range(3):
+        h, _, nxt = dkv.decode_step(tok, pos)
+        assert same_bits(h, okv.forward(tok, pos)), f"pos {pos}"
+        tok = nxt
+    print("attention wait hook: failing step at position 3", flush=True)
+    with fused_flags(ctx, ATTN_NO_WAIT):
+        with pytest.raises(wh.WillametteError) as e:
+            dkv.decode_step(tok, 3)
+    assert e.value.status == 5 and "attention workgroups stopped waiting" in str(e.value)
+    assert dkv.position == 3
+    for pos in range(3, 8):
+        h, logits, nxt = dkv.decode_step(tok, pos)
+        rh = okv.forward(tok, pos)
+        rlogits, rnxt = okv.logits_argmax(rh)
+        assert same_bits(h, rh) and same_bits(logits, rlogits) and nxt == rnxt, f"pos {pos}"
+        tok = nxt
+    print("attention wait hook: greedy with every wait failing", flush=True)
+    before = dkv.position
+    with fused_flags(ctx, ATTN_NO_WAIT):
+        with pytest.raises(wh.WillametteError) as e:
+            dkv.greedy([tok], 4)
+    assert e.value.status == 5 and dkv.position == before
+    dkv.close()
+    dev.close()
+    orm.close()
