@@ -162,3 +162,29 @@ def test_attention_wait_gives_up_without_hanging(ctx):
     dkv.close()
     dev.close()
     orm.close()
+
+
+MEDIUM = bs.BitNetConfig(n_layers=2, n_embd=1024, n_ff=1536, n_heads=8, n_kv_heads=2, head_dim=128,
+                         vocab=1000, context_length=64)
+
+
+@pytest.mark.parametrize("name", ["none"] + list(FLAGS))
+def test_medium_model_decode_exact(ctx, name):
+    """A 1024 / 1536 model (8 query heads over 2 kv heads; 16-wave fused
+    matvecs with 8 lanes per row for Q/K/V, O and down): decode steps
+    bit-exact against the oracle, on the fused matvecs' forced paths too."""
+    hm = bs.make_host_model(MEDIUM, seed=4321)
+    dev, orm = bs.load_device_model(ctx, hm), OracleModel(hm)
+    dkv, okv = dev.kv_cache(MEDIUM.context_length), orm.kv(MEDIUM.context_length)
+    print(f"medium model decode, flags {name}", flush=True)
+    with fused_flags(ctx, FLAGS.get(name, 0)):
+        tok = 9
+        for pos in range(8):
+            h, logits, nxt = dkv.decode_step(tok, pos)
+            rh = okv.forward(tok, pos)
+            rlogits, rnxt = okv.logits_argmax(rh)
+            assert same_bits(h, rh) and same_bits(logits, rlogits) and nxt == rnxt, f"pos {pos}"
+            tok = nxt
+    dkv.close()
+    dev.close()
+    orm.close()
