@@ -537,7 +537,6 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
         v2, n, sq, &nl.seq, NP,
         [&]() {
             if (wid == 0) {
-                cand = wm::fused_cand_fetch<W>(nl);
                 if (SPEC) __builtin_amdgcn_s_setprio(3);  // the walk is the critical path
             } else if (SPEC) {
                 rsq_s = nl.spec_rsq;
@@ -561,6 +560,14 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
             wm::fused_publish<W>(sum_sq, n, nm.eps, cand, nl, (chunks_flags & FUSED_NO_CANDIDATES) != 0);
         },
         [&]() {
+            // Wave 0's copy of the candidate lists (complete since before the
+            // sum), read here, ahead of the other waves' dots, which keep
+            // LDS busy while wave 0 walks the sum, and reduced as far as it
+            // goes without the rsqrt.
+            if (wid == 0) {
+                cand = wm::fused_cand_fetch<W>(nl);
+                wm::fused_cand_prep(cand);
+            }
             // The speculation's rsqrt and max|y|, once, by the last wave (at
             // these sizes it holds no terms of the sum and waits anyway):
             // the rsqrt of the waves' float64 total, max|y| from the
@@ -570,7 +577,8 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
 #pragma unroll
                 for (int i = 0; i < W; i++) S += nl.seq.dw[i];
                 const float r = wm::norm_rsq((float)S, n, nm.eps);
-                const wm::fused_cand_regs c = wm::fused_cand_fetch<W>(nl);
+                wm::fused_cand_regs c = wm::fused_cand_fetch<W>(nl);
+                wm::fused_cand_prep(c);
                 bool ok;
                 float m = wm::fused_cand_max(c, r, ok);
                 // (test hooks: a skewed max|y| moves every code's p = y * 127 / max|y|;

@@ -294,6 +294,10 @@ __device__ __forceinline__ void fused_max_candidates(const fused_quads<NR> &Q, u
 struct fused_cand_regs {
     float m, cv, cw, cm;
     int n, bad, cn;
+    // what does not depend on the rsqrt (fused_cand_prep): the largest p, the
+    // lists' flags, and whether this lane's slot is a candidate
+    float M;
+    bool flags, use;
 };
 template <int NW>
 __device__ __forceinline__ fused_cand_regs fused_cand_fetch(const fused_norm_lds<NW> &L) {
@@ -307,7 +311,17 @@ __device__ __forceinline__ fused_cand_regs fused_cand_fetch(const fused_norm_lds
     c.cw = L.cand_w[wq][j];
     c.cm = w < NW ? L.cand_m[wq] : 0.0f;
     c.cn = w < NW ? L.cand_n[wq] - j : 0;  // > 0: slot j holds a candidate
+    c.M = 0.0f;
+    c.flags = true;
+    c.use = false;
     return c;
+}
+
+// The part of fused_cand_max that does not depend on the rsqrt, ahead of it.
+__device__ __forceinline__ void fused_cand_prep(fused_cand_regs &c) {
+    c.M = wm_wave_max_nonneg(c.m);
+    c.flags = __builtin_amdgcn_ballot_w64(c.n > kCandSlots || c.bad != 0) != 0;
+    c.use = c.cn > 0 && c.cm >= c.M * (1.0f - 0x1p-19f);
 }
 
 // max|y| for a given rsqrt from the candidate lists (every lane gets it),
@@ -323,13 +337,11 @@ __device__ __forceinline__ fused_cand_regs fused_cand_fetch(const fused_norm_lds
 // rounding, times |w| <= 2^60 at most: below 2^-88, against a gap of at
 // least 2^-20 |y_k| >= 2^-80 once max|y| >= 2^-60 and M >= 2^-100.  Those
 // are the conditions checked.
+// (c has been through fused_cand_prep)
 __device__ __forceinline__ float fused_cand_max(const fused_cand_regs &c, float rsq, bool &ok) {
-    const float M = wm_wave_max_nonneg(c.m);
-    const bool flags = __builtin_amdgcn_ballot_w64(c.n > kCandSlots || c.bad != 0) != 0;
-    const bool use = c.cn > 0 && c.cm >= M * (1.0f - 0x1p-19f);
     const float yy = c.cv * rsq * c.cw;  // out = x * rsqrt * weight
-    const float ya = wm_wave_max_nonneg(use ? fabsf(yy) : 0.0f);
-    ok = !flags && M >= 0x1p-100f && ya >= 0x1p-60f;
+    const float ya = wm_wave_max_nonneg(c.use ? fabsf(yy) : 0.0f);
+    ok = !c.flags && c.M >= 0x1p-100f && ya >= 0x1p-60f;
     return ya;
 }
 

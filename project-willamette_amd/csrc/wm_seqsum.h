@@ -592,43 +592,38 @@ __device__ __forceinline__ float seq_sum_block_owned(const float (&v)[MAXM], uin
                 const float hi = seg ? (e_ok ? ldexpf(16777214.0f, e0 - 23) : -1.0f)
                                      : __int_as_float(0x7F800000);
                 const float s0 = s;
-                // The chain, step u's operands read from lane u, four steps
-                // per round (a lane past `here` holds A = V = +0, which
-                // changes no running sum); s stays a per-lane value (all
-                // lanes hold the same number) so the adds run on the vector
-                // unit.
+                // (s is kept as a per-lane value, the same in every lane,
+                // so the adds run on the vector unit)
                 float sv;
                 asm volatile("v_mov_b32 %0, %1" : "=v"(sv) : "v"(s));
                 // The chain moves across the lanes: step u runs in lane u
                 // (its operands are that lane's A and V), and its output
-                // goes one lane up (a DPP shift) into lane u + 1 alone (a
-                // one-hot mask moving with it), so lane u ends holding the
-                // value s had entering step u.  No step needs a value
-                // broadcast through an SGPR (v_readlane, a compare's lane
-                // mask): on this part such a value reaches a VALU
-                // instruction ~35 cycles after it is written, and the
-                // broadcasts cost the walk more than its adds.
-                float cur = sv;  // lane 0: s entering step 0
-                uint32_t mk = lane == 1 ? 0xFFFFFFFFu : 0u;
+                // goes one lane up (a DPP shift; lane 0 is fed s, the value
+                // entering step 0).  Every lane recomputes its step on every
+                // round, but a lane's input stops changing once the lane
+                // below has run its step, and so does its output: after
+                // round u, lanes 0..u hold their final outputs, and in the
+                // end lane u's input is the value s had entering step u.
+                // Three dependent instructions a step (two adds, the
+                // shift), and no step needs a value broadcast through an
+                // SGPR (v_readlane, a compare's lane mask): on this part
+                // such a value reaches a VALU instruction ~35 cycles after
+                // it is written, and the broadcasts cost the walk more than
+                // its adds.
                 // Eight steps per loop trip (a taken branch costs more than
-                // a step): the lanes past `here` hold A = V = +0 and are
-                // never checked, so the steps padded onto them change
-                // nothing; the last real step's output is kept as it passes.
-                // (`in` carries the chain: lane u + 1 of it holds step u's
-                // output; `cur` keeps each lane's own input, off the chain.)
-                float nxt = sv, in = sv, last = sv;
+                // a step): the lanes past `here` hold A = V = +0 and pass
+                // their input on unchanged.
+                const int svb = __float_as_int(sv);
+                float in = sv, nxt = sv;
                 for (int u0 = 0; u0 < here; u0 += 8) {
 #pragma unroll
                     for (int k = 0; k < 8; k++) {
-                        nxt = (in + A) + v1;  // lane u0 + k: step u0 + k
-                        in = __int_as_float(wave_shr1(__float_as_int(nxt), 0));
-                        cur = __uint_as_float((__float_as_uint(in) & mk) | (__float_as_uint(cur) & ~mk));
-                        mk = (uint32_t)wave_shr1((int)mk, 0);
-                        last = u0 + k == here - 1 ? nxt : last;
+                        nxt = (in + A) + v1;  // lane u: step u, once the steps below have run
+                        in = __int_as_float(wave_shr1(__float_as_int(nxt), svb));
                     }
                 }
-                sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(last), here - 1));
-                const float s_in = cur;
+                sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(nxt), here - 1));
+                const float s_in = in;
                 s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sv)));
                 // lanes past `here` hold no step; a NaN s fails every check
                 const bool ok = (int)lane >= here || !seg || (s_in >= lo && s_in + A <= hi);
