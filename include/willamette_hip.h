@@ -498,7 +498,7 @@ wm_status wm_debug_rerun_role(wm_model *m, wm_kv_cache *kv, uint32_t layer, uint
  *   WM_FUSED_DEBUG_SKEW_LARGE  off by 2^-7 (too many: codes redone),
  *   WM_FUSED_DEBUG_NO_CANDIDATES  max|y| from every wave's own maximum
  *                              (the candidate lists treated as failed),
- *   WM_FUSED_DEBUG_ATTN_NO_WAIT   (below).
+ *   WM_FUSED_DEBUG_ATTN_NO_WAIT, WM_FUSED_DEBUG_ATTN_LOOSE_COUNT   (below).
  * 0 restores the normal behaviour. */
 #define WM_FUSED_DEBUG_SKEW_SMALL 1u
 #define WM_FUSED_DEBUG_SKEW_LARGE 2u
@@ -508,6 +508,13 @@ wm_status wm_debug_rerun_role(wm_model *m, wm_kv_cache *kv, uint32_t layer, uint
  * up at once, which must fail the step with WM_E_HIP and roll the cache
  * back (never hang). */
 #define WM_FUSED_DEBUG_ATTN_NO_WAIT 8u
+/* The greedy loop's steps read their position from the device, and each
+ * attention launch is sized for the count the host expects, with which its
+ * first loads go out before the device word arrives.  With this bit the
+ * launches are sized for up to 9 more positions than the step has: the
+ * kernel then starts its scores again with the device's count, and the ids
+ * must be the same. */
+#define WM_FUSED_DEBUG_ATTN_LOOSE_COUNT 16u
 wm_status wm_debug_set_fused_flags(wm_ctx *ctx, uint32_t flags);
 
 /* ---- synthetic BitNet-shaped inputs (src/synth.rs) ------------------- */

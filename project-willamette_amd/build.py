@@ -46,11 +46,12 @@ COMMON = [
 # The batched GEMM keeps its MFMA accumulators in VGPRs: with the compiler's
 # default (AGPRs) its wave-split-K loop copies them between the two register
 # files on every chunk.
-# The fused matvecs take what their first loads need in their leading 16
-# argument dwords, which the hardware then preloads into SGPRs at wave
-# launch instead of each wave fetching them from memory.
+# The fused matvecs and decode attention take what their first loads need in
+# their leading 16 argument dwords, which the hardware then preloads into
+# SGPRs at wave launch instead of each wave fetching them from memory.
 PER_FILE = {"k_batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-            "k_i2s.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
+            "k_i2s.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+            "k_attn.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
 def sources() -> list[Path]:

@@ -18,45 +18,39 @@
 
 namespace {
 
+// What the scores need first (the query, the K cache, this token's K, the
+// geometry and the position) comes in the kernel's leading 14 argument
+// dwords, which the hardware preloads into SGPRs at wave launch (the file is
+// built with -amdgpu-kernarg-preload-count=16): six pointers, then
+//   geom  = group | n_kv_heads << 8 | kv_absmax_n << 16
+//   shape = (head_dim == 128) | sc_tile << 1 | nb << 12
+// where sc_tile is the positions per score tile (group * sc_tile <=
+// kSvThreads) and nb the position count the launch is sized for: n_past, or
+// with pos_dev the count the host expects the device word to give.  The rest
+// is read from this struct once the first loads are out.
 struct attn_args {
-    const float *q;          // [n_heads][head_dim]
-    const int8_t *k_cache;   // this layer: [max_seq][kv_dim]
-    const float *k_scales;   // [max_seq]
-    const int8_t *v_cache;
-    const float *v_scales;
+    const int8_t *v_cache;   // this layer: [max_seq][kv_dim]
+    const float *v_scales;   // [max_seq]
     float *scores;           // [n_heads][score_stride]
     float *out;              // [n_heads][head_dim]
-    uint32_t n_past, kv_dim, head_dim, group, score_stride;
+    uint32_t score_stride;
     float scale;
-    // This token's K (after RoPE) and V, [kv_dim] f32: position n_past - 1
-    // is not in the cache yet.  The kernel quantises what it needs of them
-    // exactly as KVCache::append does and writes the cache rows and scales.
-    const float *k_new, *v_new;
-    // absmax of k_new and v_new (float bits) as the QKV matvec leaves them:
-    // slots whose maximum it is, k_new's [0, n), v_new's [stride, stride + n)
-    const uint32_t *kv_absmax;
-    uint32_t kv_absmax_n, kv_absmax_stride;
-    // nullable: the token's position on the device (n_past = *pos_dev + 1,
-    // for launches that are replayed at successive positions); the grid and
-    // LDS are then sized for n_max, and a larger n_past launches nothing
-    const uint32_t *pos_dev;
-    uint32_t n_max;
+    // This token's V, [kv_dim] f32 (its K comes as an argument): position
+    // n_past - 1 is not in the cache yet.  The kernel quantises what it needs
+    // of k_new and v_new exactly as KVCache::append does and writes the cache
+    // rows and scales.
+    const float *v_new;
+    // v_new's absmax slots begin at kv_absmax + kv_absmax_stride (k_new's at
+    // kv_absmax; kv_absmax_n of each)
+    uint32_t kv_absmax_stride;
     // this launch's tag on its scores (never 0, and never the tag of an
     // earlier launch whose words the scores buffer may still hold), the
     // step's error flag and the value a failed wait raises it to
     uint32_t tag;
     uint32_t *err_flag;
     uint32_t err_tag;
-    uint32_t gs;         // workgroups per kv head: group * head_dim / 16
-    uint32_t xstride;    // workgroup (g, j) has linear id j * xstride + g
-    uint32_t n_kv_heads;
     uint32_t spin_limit; // polls before a wait gives up (0: at once, a test hook)
-    uint32_t sc_tile;    // positions per score tile: group * sc_tile <= kSvThreads
 };
-
-__device__ __forceinline__ uint32_t attn_n_past(const attn_args &a) {
-    return a.pos_dev ? *a.pos_dev + 1 : a.n_past;
-}
 
 constexpr uint32_t kMaxHeadDim = 128;
 
@@ -68,12 +62,12 @@ __device__ __forceinline__ int8_t kv_q(float v, float absmax) {
     return kv_zero(absmax) ? (int8_t)0 : (int8_t)wm_round_clamp_i8(v * (127.0f / absmax));
 }
 __device__ __forceinline__ float kv_scale(float absmax) { return kv_zero(absmax) ? 0.0f : absmax / 127.0f; }
-// The absmax of k_new (which 0) or v_new (1) from its slots, in every lane
-// of the calling wave (the slots hold non-negative floats, no NaN).
-__device__ __forceinline__ float kv_absmax_of(const attn_args &a, uint32_t which) {
-    const uint32_t *sl = a.kv_absmax + which * a.kv_absmax_stride;
+// The absmax of a vector from its n slots (as the QKV matvec leaves them:
+// non-negative floats, no NaN, whose maximum it is), in every lane of the
+// calling wave.
+__device__ __forceinline__ float kv_absmax_of(const uint32_t *sl, uint32_t n) {
     float m = 0.0f;
-    for (uint32_t i = threadIdx.x & 63; i < a.kv_absmax_n; i += 64) m = fmaxf(m, __uint_as_float(sl[i]));
+    for (uint32_t i = threadIdx.x & 63; i < n; i += 64) m = fmaxf(m, __uint_as_float(sl[i]));
     return wm_wave_max_nonneg(m);
 }
 
@@ -167,34 +161,54 @@ __device__ __forceinline__ float sv_block_max(float v, float *red) {
 // read once per launch and V once per XCD that serves its kv head (with
 // xstride 8, every workgroup of a kv head sits on one XCD: the dispatcher
 // deals linear workgroup ids to the 8 XCDs in turn).
+//
+// q [n_heads][head_dim], k_cache and k_scales (this layer's [max_seq][kv_dim]
+// codes and [max_seq] scales), k_new (this token's K after RoPE, [kv_dim]
+// f32), kv_absmax (the absmax slots) and pos_dev (nullable: the token's
+// position on the device, n_past = *pos_dev + 1, for steps the host queues
+// ahead; a count above nb launches nothing) lead the arguments; geom and
+// shape are packed as described at attn_args.
 template <int MAXM>  // n_past <= MAXM * kSvThreads
-__global__ __launch_bounds__(kSvThreads) void k_attn_decode(attn_args a) {
+__global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, const int8_t *k_cache,
+                                                            const float *k_scales, const float *k_new,
+                                                            const uint32_t *kv_absmax, const uint32_t *pos_dev,
+                                                            uint32_t geom, uint32_t shape, attn_args a) {
     extern __shared__ __align__(16) float sm[];
     __shared__ float red[16];
     __shared__ int wcnt[MAXM * 16];
-        __shared__ wm::seq_block_scratch seq_scratch;
+    __shared__ wm::seq_block_scratch seq_scratch;
     __shared__ uint64_t exp_tab[32];
-    const uint32_t g = blockIdx.x % a.xstride, j = blockIdx.x / a.xstride;
-    if (g >= a.n_kv_heads) return;
-    const uint32_t n = attn_n_past(a), pnew = n - 1;
-    if (n > a.n_max) return;
+    const uint32_t group = geom & 0xFFu, n_kv_heads = (geom >> 8) & 0xFFu, kv_absmax_n = geom >> 16;
+    const uint32_t hd = (shape & 1u) ? 128u : 64u, segs = hd / 16;
+    const uint32_t sc_tile = (shape >> 1) & 0x7FFu, nb = shape >> 12;
+    const uint32_t gs = group * segs, kv_dim = n_kv_heads * hd;
+    // workgroup (g, j) has linear id j * xstride + g
+    const uint32_t xstride = n_kv_heads <= 8 ? 8u : n_kv_heads;
+    const uint32_t g = blockIdx.x % xstride, j = blockIdx.x / xstride;
+    if (g >= n_kv_heads) return;
+    // The position count.  Phase 1's loads go out for the launch's count nb
+    // while the device word is still on its way; where the word gives
+    // another count, phase 1 starts again with it (before any store).
+    const uint32_t nd = pos_dev ? *pos_dev + 1 : nb;
+    uint32_t n = nb, pnew = nb - 1;
     const uint32_t tid = threadIdx.x;
     const uint32_t wid = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6)), lane = tid & 63;
-    const uint32_t hd = a.head_dim, segs = hd / 16;
-    const uint32_t h = g * a.group + j / segs, d0 = (j % segs) * kSvDims;
+    const uint32_t h = g * group + j / segs, d0 = (j % segs) * kSvDims;
     if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
 
     uint64_t *const scores64 = reinterpret_cast<uint64_t *>(a.scores);
 
     // ---- phase 1: scores of positions [p0, p1) for the group's heads ----
-    const uint32_t p0 = p0_of(n, j, a.gs), p1 = p0_of(n, j + 1, a.gs);
     const uint32_t pst = hd + 4;                  // floats per product row (spread banks)
     float *qs = sm;                               // [group][hd]
-    float *qk = sm + a.group * hd;                // [group][sc_tile][pst] products
-    const int8_t *kseg = a.k_cache + g * hd;
+    float *qk = sm + group * hd;                  // [group][sc_tile][pst] products
+    const int8_t *kseg = k_cache + g * hd;
     const uint32_t row = tid / segs, sg = tid % segs;  // this thread's K row segment
-    for (uint32_t t0 = p0; t0 < p1; t0 += a.sc_tile) {
-        const uint32_t tp = min(a.sc_tile, p1 - t0);
+    for (bool settled = false; !settled;) {
+    settled = true;
+    const uint32_t p0 = p0_of(n, j, gs), p1 = p0_of(n, j + 1, gs);
+    for (uint32_t t0 = p0; t0 < p1; t0 += sc_tile) {
+        const uint32_t tp = min(sc_tile, p1 - t0);
         const bool mine = row < tp, is_new = mine && t0 + row == pnew;
         // the loads, all issued together: this thread's 16-byte K segment
         // and its scale, or for the new position this token's k_new segment
@@ -203,20 +217,24 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(attn_args a) {
         float ksc = 0.0f;
         float4 kn[4];
         if (mine && !is_new) {
-            const int4 raw = *reinterpret_cast<const int4 *>(kseg + (uint64_t)(t0 + row) * a.kv_dim + sg * 16);
+            const int4 raw = *reinterpret_cast<const int4 *>(kseg + (uint64_t)(t0 + row) * kv_dim + sg * 16);
             kw[0] = (uint32_t)raw.x; kw[1] = (uint32_t)raw.y; kw[2] = (uint32_t)raw.z; kw[3] = (uint32_t)raw.w;
-            ksc = a.k_scales[t0 + row];
+            ksc = k_scales[t0 + row];
         }
         if (is_new)
 #pragma unroll
             for (int e = 0; e < 4; e++)
-                kn[e] = *reinterpret_cast<const float4 *>(a.k_new + g * hd + sg * 16 + 4 * e);
+                kn[e] = *reinterpret_cast<const float4 *>(k_new + g * hd + sg * 16 + 4 * e);
         if (t0 == p0)
-            for (uint32_t i = tid; i < a.group * hd / 4; i += kSvThreads)
-                reinterpret_cast<float4 *>(qs)[i] = reinterpret_cast<const float4 *>(a.q + (uint64_t)g * a.group * hd)[i];
+            for (uint32_t i = tid; i < group * hd / 4; i += kSvThreads)
+                reinterpret_cast<float4 *>(qs)[i] = reinterpret_cast<const float4 *>(q + (uint64_t)g * group * hd)[i];
+        if (t0 == p0 && nd != n) {  // uniform: the whole workgroup starts again
+            settled = false;
+            break;
+        }
         // (the wave holding the new row computes k_new's absmax: uniform)
         const bool new_wave = pnew >= t0 && pnew < t0 + tp && (pnew - t0) * segs / 64 == wid;
-        const float kabs = new_wave ? kv_absmax_of(a, 0) : 0.0f;
+        const float kabs = new_wave ? kv_absmax_of(kv_absmax, kv_absmax_n) : 0.0f;
         wm_sync_lds();
         // this thread's 16 values of k_p (read_into: q as f32 * scale; the
         // new row through KVCache::append's codes), times each head's q
@@ -234,16 +252,16 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(attn_args a) {
                     kd[e] = (float)c * ksn;
                 }
                 // its workgroup writes the cache row segment, kv head 0's the scale
-                *reinterpret_cast<int4 *>(const_cast<int8_t *>(a.k_cache) + (uint64_t)pnew * a.kv_dim + g * hd +
+                *reinterpret_cast<int4 *>(const_cast<int8_t *>(k_cache) + (uint64_t)pnew * kv_dim + g * hd +
                                           sg * 16) = make_int4((int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3]);
-                if (g == 0 && sg == 0) const_cast<float *>(a.k_scales)[pnew] = ksn;
+                if (g == 0 && sg == 0) const_cast<float *>(k_scales)[pnew] = ksn;
             } else {
 #pragma unroll
                 for (int e = 0; e < 16; e++) kd[e] = (float)(int8_t)(kw[e / 4] >> (8 * (e % 4))) * ksc;
             }
-            for (uint32_t hh = 0; hh < a.group; hh++) {
+            for (uint32_t hh = 0; hh < group; hh++) {
                 const float *qr = qs + hh * hd + sg * 16;
-                float *dst = qk + (hh * a.sc_tile + row) * pst + sg * 16;
+                float *dst = qk + (hh * sc_tile + row) * pst + sg * 16;
 #pragma unroll
                 for (int e = 0; e < 16; e += 4) {
                     const float4 qv = *reinterpret_cast<const float4 *>(qr + e);
@@ -254,9 +272,9 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(attn_args a) {
         }
         wm_sync_lds();
         // one chain per (head, position): s = Σ_i q_h[i] * k_p[i] in order
-        if (tid < a.group * tp) {
+        if (tid < group * tp) {
             const uint32_t hh = tid / tp, pl = tid % tp;
-            const float *pr = qk + (hh * a.sc_tile + pl) * pst;
+            const float *pr = qk + (hh * sc_tile + pl) * pst;
             float s = 0.0f;
             for (uint32_t i = 0; i < hd; i += 4) {
                 const float4 f = *reinterpret_cast<const float4 *>(pr + i);
@@ -265,9 +283,16 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(attn_args a) {
                 s = s + f.z;
                 s = s + f.w;
             }
-            st_tagged(scores64 + (uint64_t)(g * a.group + hh) * a.score_stride + t0 + pl, a.tag, s * a.scale);
+            st_tagged(scores64 + (uint64_t)(g * group + hh) * a.score_stride + t0 + pl, a.tag, s * a.scale);
         }
-        if (t0 + a.sc_tile < p1) wm_sync_lds();
+        if (t0 + sc_tile < p1) wm_sync_lds();
+    }
+    if (p0 >= p1 && nd != n) settled = false;  // no positions here: nothing was loaded
+    if (!settled) {
+        if (nd == 0 || nd > nb) return;  // a count the launch is not sized for
+        n = nd;
+        pnew = nd - 1;
+    }
     }
 
     // ---- phase 2: this head's scores, once each carries the launch's tag ----
@@ -287,14 +312,14 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(attn_args a) {
 #pragma unroll
     for (int i = 0; i < MAXM; i++) {
         const uint32_t p = min(tid + (uint32_t)i * kSvThreads, n - 1);
-        const int4 t4 = *reinterpret_cast<const int4 *>(vseg + (uint64_t)p * a.kv_dim);
+        const int4 t4 = *reinterpret_cast<const int4 *>(vseg + (uint64_t)p * kv_dim);
         vr0[i] = t4.x; vr1[i] = t4.y; vr2[i] = t4.z; vr3[i] = t4.w;
         ss[i] = a.v_scales[p];
     }
     // and this token's V: the workgroup's 16 values of v_new, and its absmax
     // (every wave reduces the slots itself)
     const float vnew = tid < kSvDims ? a.v_new[g * hd + d0 + tid] : 0.0f;
-    const float vabs = kv_absmax_of(a, 1);
+    const float vabs = kv_absmax_of(kv_absmax + a.kv_absmax_stride, kv_absmax_n);
     {
         uint32_t pending = 0;
 #pragma unroll
@@ -328,6 +353,9 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(attn_args a) {
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < MAXM; i++) sv[i] = __uint_as_float((uint32_t)sw[i]);
+    // These arrays overlap phase 1's products, and a thread's own scores can
+    // all come from other workgroups while this one's chains still read them.
+    wm_sync_lds();
 #pragma unroll
     for (int i = 0; i < MAXM; i++) {
         const uint32_t p = tid + (uint32_t)i * kSvThreads;
@@ -487,7 +515,7 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(attn_args a) {
         }
     }
     if (v_writer) {  // kv head g's segment of the cache row of position n - 1
-        int8_t *v_row = const_cast<int8_t *>(a.v_cache) + (uint64_t)pnew * a.kv_dim + g * hd;
+        int8_t *v_row = const_cast<int8_t *>(a.v_cache) + (uint64_t)pnew * kv_dim + g * hd;
         for (uint32_t i = tid; i < hd; i += kSvThreads) v_row[i] = kv_q(a.v_new[g * hd + i], vabs);
         if (g == 0 && tid == 0) const_cast<float *>(a.v_scales)[pnew] = kv_scale(vabs);
     }
@@ -533,12 +561,14 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
                          uint32_t kv_absmax_stride, uint32_t tag, uint32_t *err_flag,
                          uint32_t err_tag, bool no_wait, hipStream_t s, const uint32_t *pos_dev,
                          uint32_t n_max) {
-    // with pos_dev, n_past comes from the device and n_max bounds it
+    // with pos_dev, n_past comes from the device and n_max bounds it; the
+    // score loads go out for n_max before the device word arrives, so a
+    // count other than n_max costs the kernel a second start of its scores
     const uint32_t nb = pos_dev ? n_max : n_past;
     if ((head_dim != 64 && head_dim != 128) || nb == 0 || nb > 4 * kSvThreads || nb > score_stride ||
         n_kv_heads == 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 16 || tag == 0)
         return false;
-    const uint32_t kv_dim = n_kv_heads * head_dim, group = n_heads / n_kv_heads;
+    const uint32_t group = n_heads / n_kv_heads;
     const uint32_t gs = group * head_dim / kSvDims;
     // kv head g's workgroups at linear ids g, g + 8, g + 16, ... (at most 8
     // kv heads): all on one XCD, which then fetches its K and V rows once
@@ -548,9 +578,11 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
     const uint32_t pst = head_dim + 4;
     const uint32_t sc_tile = min(min((uint32_t)kSvThreads / group, (uint32_t)kSvThreads / (head_dim / 16)),
                                  (uint32_t)((128u * 1024u / 4u - group * head_dim) / (group * pst)));
-    attn_args a{q, k_cache, k_scales, v_cache, v_scales, scores, out, n_past, kv_dim, head_dim, group,
-                score_stride, scale, k_new, v_new, kv_absmax, kv_absmax_n, kv_absmax_stride, pos_dev, nb,
-                tag, err_flag, err_tag, gs, xstride, n_kv_heads, no_wait ? 0u : (1u << 16), sc_tile};
+    if (n_kv_heads > 255 || kv_absmax_n > 0xFFFFu) return false;
+    const uint32_t geom = group | n_kv_heads << 8 | kv_absmax_n << 16;
+    const uint32_t shape = (head_dim == 128 ? 1u : 0u) | sc_tile << 1 | nb << 12;
+    attn_args a{v_cache, v_scales, scores, out, score_stride, scale, v_new, kv_absmax_stride,
+                tag, err_flag, err_tag, no_wait ? 0u : (1u << 16)};
     const size_t npad = ((size_t)nb + 3) & ~(size_t)3;
     const size_t lds_sv = (size_t)wm::seq_sum_padded(nb) * 4 + npad * (4 + 16) +
                           (size_t)2 * kSvDims * kSvStride * 4 + npad * 2;
@@ -558,9 +590,11 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
     const size_t lds = lds_sv > lds_sc ? lds_sv : lds_sc;
     const dim3 grid(xstride * gs);
     if (nb <= 2 * kSvThreads)
-        hipLaunchKernelGGL(k_attn_decode<2>, grid, dim3(kSvThreads), lds, s, a);
+        hipLaunchKernelGGL(k_attn_decode<2>, grid, dim3(kSvThreads), lds, s, q, k_cache, k_scales, k_new,
+                           kv_absmax, pos_dev, geom, shape, a);
     else  // nb <= 4096, the models' context limit
-        hipLaunchKernelGGL(k_attn_decode<4>, grid, dim3(kSvThreads), lds, s, a);
+        hipLaunchKernelGGL(k_attn_decode<4>, grid, dim3(kSvThreads), lds, s, q, k_cache, k_scales, k_new,
+                           kv_absmax, pos_dev, geom, shape, a);
     return true;
 }
 

@@ -1047,9 +1047,13 @@ wm_status wm_greedy_generate(wm_model *m, wm_kv_cache *kv, const uint32_t *promp
     const uint32_t n_steps = max_new ? max_new : 1;
     const wm_step_tail tail{m->dscalars + 3, m->ring_dev, m->dscalars + 2, kRing - 1};
     // step k at position pos0 + k: the kernels read the position from the
-    // device, and the host sizes the attention launches for it
+    // device, and the host sizes the attention launches for it (a test hook
+    // sizes them for a few positions more)
+    const bool loose = (ctx->fused_debug & WM_FUSED_DEBUG_ATTN_LOOSE_COUNT) != 0;
     const auto enqueue_step = [&](uint32_t k) -> bool {
-        if (!enqueue_forward(m, kv, step_pos{0, m->dscalars + 3, pos0 + k + 1}, nullptr, m->dscalars + 1))
+        const uint32_t n_exp = pos0 + k + 1;
+        const uint32_t n_max = loose ? std::min(n_exp + 9u, std::min(m->cfg.context_length, 4096u)) : n_exp;
+        if (!enqueue_forward(m, kv, step_pos{0, m->dscalars + 3, n_max}, nullptr, m->dscalars + 1))
             return false;
         wm_launch_q6k_argmax_fast(m->embd, m->embd_blocks, m->cfg.vocab_size, m->embd_rowgroups,
                                   m->final_hidden, m->logits, m->dscalars + 1, m->lm_work, true,

@@ -418,7 +418,7 @@ wm_status wm_bitlinear_i2s_matvec_f32_dev(wm_ctx *ctx, const wm_tensor *w, const
 wm_status wm_debug_set_fused_flags(wm_ctx *ctx, uint32_t flags) {
     if (!ctx) return WM_E_ARG;
     const uint32_t known = WM_FUSED_DEBUG_SKEW_SMALL | WM_FUSED_DEBUG_SKEW_LARGE | WM_FUSED_DEBUG_NO_CANDIDATES |
-                           WM_FUSED_DEBUG_ATTN_NO_WAIT;
+                           WM_FUSED_DEBUG_ATTN_NO_WAIT | WM_FUSED_DEBUG_ATTN_LOOSE_COUNT;
     if (flags & ~known) return wm_set_error(ctx, WM_E_ARG, "set_fused_flags: unknown bits 0x%x", flags & ~known);
     ctx->fused_debug = flags;
     return WM_OK;

@@ -28,6 +28,7 @@ pub const WM_FUSED_DEBUG_SKEW_SMALL: u32 = 1;
 pub const WM_FUSED_DEBUG_SKEW_LARGE: u32 = 2;
 pub const WM_FUSED_DEBUG_NO_CANDIDATES: u32 = 4;
 pub const WM_FUSED_DEBUG_ATTN_NO_WAIT: u32 = 8;
+pub const WM_FUSED_DEBUG_ATTN_LOOSE_COUNT: u32 = 16;
 
 pub const WM_TYPE_I2S: c_int = 36;
 pub const WM_TYPE_Q6K: c_int = 14;

@@ -49,7 +49,7 @@ class fused_flags:
 
 def test_unknown_flags_rejected(ctx):
     with pytest.raises(wh.WillametteError) as e:
-        ctx.check(wh.lib.wm_debug_set_fused_flags(ctx.h, 16))
+        ctx.check(wh.lib.wm_debug_set_fused_flags(ctx.h, 32))
     assert e.value.status == 6  # WM_E_ARG
 
 
@@ -159,6 +159,32 @@ def test_attention_wait_gives_up_without_hanging(ctx):
         with pytest.raises(wh.WillametteError) as e:
             dkv.greedy([tok], 4)
     assert e.value.status == 5 and dkv.position == before
+    dkv.close()
+    dev.close()
+    orm.close()
+
+
+ATTN_LOOSE_COUNT = 16
+
+
+@pytest.mark.parametrize("cfg_name", ["small", "medium"])
+def test_attention_restarts_scores_on_the_device_count(ctx, cfg_name):
+    """The greedy loop sizes each attention launch for the count the host
+    expects, and the kernel's first loads go out for it before the device's
+    position arrives.  With the hook the launches are sized for up to 9
+    positions more, so every launch starts its scores again with the
+    device's count (and workgroups with no positions under the host's count
+    get some): the ids must still be the oracle's, and the cache ends where
+    the oracle's does."""
+    cfg = SMALL if cfg_name == "small" else MEDIUM
+    hm = bs.make_host_model(cfg, seed=606)
+    dev, orm = bs.load_device_model(ctx, hm), OracleModel(hm)
+    dkv, okv = dev.kv_cache(cfg.context_length), orm.kv(cfg.context_length)
+    print(f"attention loose count, {cfg_name}", flush=True)
+    with fused_flags(ctx, ATTN_LOOSE_COUNT):
+        ids = dkv.greedy([3, 1, 4], max_new=20)
+    assert ids == okv.greedy([3, 1, 4], max_new=20) and len(ids) == 20
+    assert dkv.position == okv.position
     dkv.close()
     dev.close()
     orm.close()
