@@ -64,11 +64,23 @@ __device__ __forceinline__ int8_t kv_q(float v, float absmax) {
 __device__ __forceinline__ float kv_scale(float absmax) { return kv_zero(absmax) ? 0.0f : absmax / 127.0f; }
 // The absmax of a vector from its n slots (as the QKV matvec leaves them:
 // non-negative floats, no NaN, whose maximum it is), in every lane of the
-// calling wave.
-__device__ __forceinline__ float kv_absmax_of(const uint32_t *sl, uint32_t n) {
-    float m = 0.0f;
-    for (uint32_t i = threadIdx.x & 63; i < n; i += 64) m = fmaxf(m, __uint_as_float(sl[i]));
+// calling wave: the loads of the first 128 slots (kv_absmax_first, issued
+// where the caller has other loads in flight), then the rest and the wave's
+// maximum (kv_absmax_finish).
+struct kv_absmax_part {
+    float m0, m1;
+};
+__device__ __forceinline__ kv_absmax_part kv_absmax_first(const uint32_t *sl, uint32_t n) {
+    const uint32_t l = threadIdx.x & 63;
+    return {l < n ? __uint_as_float(sl[l]) : 0.0f, l + 64 < n ? __uint_as_float(sl[l + 64]) : 0.0f};
+}
+__device__ __forceinline__ float kv_absmax_finish(kv_absmax_part f, const uint32_t *sl, uint32_t n) {
+    float m = fmaxf(f.m0, f.m1);
+    for (uint32_t i = (threadIdx.x & 63) + 128; i < n; i += 64) m = fmaxf(m, __uint_as_float(sl[i]));
     return wm_wave_max_nonneg(m);
+}
+__device__ __forceinline__ float kv_absmax_of(const uint32_t *sl, uint32_t n) {
+    return kv_absmax_finish(kv_absmax_first(sl, n), sl, n);
 }
 
 // Scores cross from the workgroups that compute them to the workgroups
@@ -132,9 +144,10 @@ __device__ __forceinline__ float sv_block_max(float v, float *red) {
 // 1. Scores.  Workgroup (g, j) takes positions [j n / gs, (j + 1) n / gs)
 //    for all `group` query heads of g.  It loads those K rows once (one
 //    16-byte segment per thread, with its scale), dequantises them as
-//    read_into does, multiplies each value by every head's q into LDS, and
-//    each of its first group * np threads adds one chain
-//    s = (Σ_i q_h[i] * k_p[i]) * scale in order over i.  Position n - 1 is
+//    read_into does into LDS rows, and each of its first group * np threads
+//    forms one chain s = (Σ_i q_h[i] * k_p[i]) * scale, each product and add
+//    in order over i (q from LDS, read by every thread of a head at once).
+//    Position n - 1 is
 //    this token's k_new, quantised here exactly as KVCache::append does (its
 //    thread also writes the cache row segment, and kv head 0's the scale).
 //    The scores go out tagged with the launch's epoch (st_tagged).
@@ -187,21 +200,21 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
     const uint32_t g = blockIdx.x % xstride, j = blockIdx.x / xstride;
     if (g >= n_kv_heads) return;
     // The position count.  Phase 1's loads go out for the launch's count nb
-    // while the device word is still on its way; where the word gives
-    // another count, phase 1 starts again with it (before any store).
-    const uint32_t nd = pos_dev ? *pos_dev + 1 : nb;
+    // before the device word is read (each read sits where it is needed, so
+    // that the wait for it comes after them); where the word gives another
+    // count, phase 1 starts again with it (before any store).
     uint32_t n = nb, pnew = nb - 1;
+    const auto dev_count_differs = [&]() { return pos_dev && *pos_dev + 1 != n; };
     const uint32_t tid = threadIdx.x;
     const uint32_t wid = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6)), lane = tid & 63;
     const uint32_t h = g * group + j / segs, d0 = (j % segs) * kSvDims;
-    if (tid < 32) exp_tab[tid] = wm::kExp2Tab[tid];
 
     uint64_t *const scores64 = reinterpret_cast<uint64_t *>(a.scores);
 
     // ---- phase 1: scores of positions [p0, p1) for the group's heads ----
-    const uint32_t pst = hd + 4;                  // floats per product row (spread banks)
+    const uint32_t pst = hd + 4;                  // floats per K row in LDS (spread banks)
     float *qs = sm;                               // [group][hd]
-    float *qk = sm + group * hd;                  // [group][sc_tile][pst] products
+    float *kdl = sm + group * hd;                 // [sc_tile][pst] dequantised K rows
     const int8_t *kseg = k_cache + g * hd;
     const uint32_t row = tid / segs, sg = tid % segs;  // this thread's K row segment
     for (bool settled = false; !settled;) {
@@ -225,19 +238,26 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
 #pragma unroll
             for (int e = 0; e < 4; e++)
                 kn[e] = *reinterpret_cast<const float4 *>(k_new + g * hd + sg * 16 + 4 * e);
-        if (t0 == p0)
-            for (uint32_t i = tid; i < group * hd / 4; i += kSvThreads)
-                reinterpret_cast<float4 *>(qs)[i] = reinterpret_cast<const float4 *>(q + (uint64_t)g * group * hd)[i];
-        if (t0 == p0 && nd != n) {  // uniform: the whole workgroup starts again
+        // (group * hd / 4 <= 512 float4 of q: one per thread at most)
+        const bool q_mine = t0 == p0 && tid < group * hd / 4;
+        float4 qv4;
+        if (q_mine) qv4 = reinterpret_cast<const float4 *>(q + (uint64_t)g * group * hd)[tid];
+        // (the wave holding the new row computes k_new's absmax: uniform)
+        const bool new_wave = pnew >= t0 && pnew < t0 + tp && (pnew - t0) * segs / 64 == wid;
+        kv_absmax_part kpart{0.0f, 0.0f};
+        if (new_wave) kpart = kv_absmax_first(kv_absmax, kv_absmax_n);
+        if (t0 == p0 && dev_count_differs()) {  // uniform: the whole workgroup starts again
             settled = false;
             break;
         }
-        // (the wave holding the new row computes k_new's absmax: uniform)
-        const bool new_wave = pnew >= t0 && pnew < t0 + tp && (pnew - t0) * segs / 64 == wid;
-        const float kabs = new_wave ? kv_absmax_of(kv_absmax, kv_absmax_n) : 0.0f;
+        // (the slots are combined only now, so that their wait is not ahead
+        // of the device word's load)
+        asm volatile("" : "+v"(kpart.m0), "+v"(kpart.m1));
+        if (q_mine) reinterpret_cast<float4 *>(qs)[tid] = qv4;
+        const float kabs = new_wave ? kv_absmax_finish(kpart, kv_absmax, kv_absmax_n) : 0.0f;
         wm_sync_lds();
         // this thread's 16 values of k_p (read_into: q as f32 * scale; the
-        // new row through KVCache::append's codes), times each head's q
+        // new row through KVCache::append's codes), into the tile's rows
         if (mine) {
             float kd[16];
             if (is_new) {
@@ -259,36 +279,63 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
 #pragma unroll
                 for (int e = 0; e < 16; e++) kd[e] = (float)(int8_t)(kw[e / 4] >> (8 * (e % 4))) * ksc;
             }
-            for (uint32_t hh = 0; hh < group; hh++) {
-                const float *qr = qs + hh * hd + sg * 16;
-                float *dst = qk + (hh * sc_tile + row) * pst + sg * 16;
+            float *dst = kdl + row * pst + sg * 16;
 #pragma unroll
-                for (int e = 0; e < 16; e += 4) {
-                    const float4 qv = *reinterpret_cast<const float4 *>(qr + e);
-                    *reinterpret_cast<float4 *>(dst + e) =
-                        make_float4(qv.x * kd[e], qv.y * kd[e + 1], qv.z * kd[e + 2], qv.w * kd[e + 3]);
-                }
-            }
+            for (int e = 0; e < 16; e += 4)
+                *reinterpret_cast<float4 *>(dst + e) = make_float4(kd[e], kd[e + 1], kd[e + 2], kd[e + 3]);
         }
         wm_sync_lds();
+        // (the struct's fields the stores use are in by now; taking them
+        // here leaves no scalar load outstanding in the chains' loop, whose
+        // waits can then count its LDS reads)
+        const uint32_t sc_stride = a.score_stride, sc_tag = a.tag;
+        const float sc_scale = a.scale;
+        asm volatile("" ::"s"(sc_stride), "s"(sc_tag), "s"(sc_scale));
         // one chain per (head, position): s = Σ_i q_h[i] * k_p[i] in order
         if (tid < group * tp) {
             const uint32_t hh = tid / tp, pl = tid % tp;
-            const float *pr = qk + (hh * sc_tile + pl) * pst;
+            const float *kr = kdl + pl * pst, *qr = qs + hh * hd;
+            // 16 terms per step (four float4 of k_p, four of q_h), the next
+            // step's reads issued before this step's products and adds, into
+            // two buffers in turn (hd is 64 or 128: 4 or 8 steps)
             float s = 0.0f;
-            for (uint32_t i = 0; i < hd; i += 4) {
-                const float4 f = *reinterpret_cast<const float4 *>(pr + i);
-                s = s + f.x;
-                s = s + f.y;
-                s = s + f.z;
-                s = s + f.w;
+            float4 ka[4], qa[4], kb[4], qb[4];
+            const auto add16 = [&](const float4 (&k)[4], const float4 (&qq)[4]) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    s = s + qq[c].x * k[c].x;
+                    s = s + qq[c].y * k[c].y;
+                    s = s + qq[c].z * k[c].z;
+                    s = s + qq[c].w * k[c].w;
+                }
+            };
+            const auto read16 = [&](float4 (&k)[4], float4 (&qq)[4], uint32_t i) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    k[c] = *reinterpret_cast<const float4 *>(kr + i + 4 * c);
+                    qq[c] = *reinterpret_cast<const float4 *>(qr + i + 4 * c);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the adds that follow
+            };
+            // (a read past the row's end rereads its last 16 values, unused:
+            // every read is unconditional, so each wait is for one buffer)
+            read16(ka, qa, 0);
+#pragma unroll 1
+            for (uint32_t i = 16;; i += 32) {
+                read16(kb, qb, min(i, hd - 16));
+                add16(ka, qa);
+                if (i >= hd) break;
+                read16(ka, qa, min(i + 16, hd - 16));
+                add16(kb, qb);
+                if (i + 16 >= hd) break;
             }
-            st_tagged(scores64 + (uint64_t)(g * group + hh) * a.score_stride + t0 + pl, a.tag, s * a.scale);
+            st_tagged(scores64 + (uint64_t)(g * group + hh) * sc_stride + t0 + pl, sc_tag, s * sc_scale);
         }
         if (t0 + sc_tile < p1) wm_sync_lds();
     }
-    if (p0 >= p1 && nd != n) settled = false;  // no positions here: nothing was loaded
+    if (p0 >= p1 && dev_count_differs()) settled = false;  // no positions here: nothing was loaded
     if (!settled) {
+        const uint32_t nd = *pos_dev + 1;
         if (nd == 0 || nd > nb) return;  // a count the launch is not sized for
         n = nd;
         pnew = nd - 1;
@@ -319,6 +366,9 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
     // and this token's V: the workgroup's 16 values of v_new, and its absmax
     // (every wave reduces the slots itself)
     const float vnew = tid < kSvDims ? a.v_new[g * hd + d0 + tid] : 0.0f;
+    // expf's table, into LDS at phase 3 (loaded here, after phase 1's loads,
+    // so that no wait for it comes ahead of them)
+    const uint64_t exp_word = tid < 32 ? wm::kExp2Tab[tid] : 0u;
     const float vabs = kv_absmax_of(kv_absmax + a.kv_absmax_stride, kv_absmax_n);
     {
         uint32_t pending = 0;
@@ -353,7 +403,8 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < MAXM; i++) sv[i] = __uint_as_float((uint32_t)sw[i]);
-    // These arrays overlap phase 1's products, and a thread's own scores can
+    if (tid < 32) exp_tab[tid] = exp_word;
+    // These arrays overlap phase 1's K rows, and a thread's own scores can
     // all come from other workgroups while this one's chains still read them.
     wm_sync_lds();
 #pragma unroll
@@ -574,10 +625,10 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
     // kv heads): all on one XCD, which then fetches its K and V rows once
     const uint32_t xstride = n_kv_heads <= 8 ? 8u : n_kv_heads;
     // positions per score tile: one chain per thread, one K segment per
-    // thread, and the products of the group's heads within 128 KiB of LDS
+    // thread, and the tile's dequantised K rows within 128 KiB of LDS
     const uint32_t pst = head_dim + 4;
     const uint32_t sc_tile = min(min((uint32_t)kSvThreads / group, (uint32_t)kSvThreads / (head_dim / 16)),
-                                 (uint32_t)((128u * 1024u / 4u - group * head_dim) / (group * pst)));
+                                 (uint32_t)((128u * 1024u / 4u - group * head_dim) / pst));
     if (n_kv_heads > 255 || kv_absmax_n > 0xFFFFu) return false;
     const uint32_t geom = group | n_kv_heads << 8 | kv_absmax_n << 16;
     const uint32_t shape = (head_dim == 128 ? 1u : 0u) | sc_tile << 1 | nb << 12;
@@ -586,7 +637,7 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
     const size_t npad = ((size_t)nb + 3) & ~(size_t)3;
     const size_t lds_sv = (size_t)wm::seq_sum_padded(nb) * 4 + npad * (4 + 16) +
                           (size_t)2 * kSvDims * kSvStride * 4 + npad * 2;
-    const size_t lds_sc = ((size_t)group * head_dim + (size_t)group * sc_tile * pst) * 4;
+    const size_t lds_sc = ((size_t)group * head_dim + (size_t)sc_tile * pst) * 4;
     const size_t lds = lds_sv > lds_sc ? lds_sv : lds_sc;
     const dim3 grid(xstride * gs);
     if (nb <= 2 * kSvThreads)
