@@ -169,11 +169,12 @@ __device__ __forceinline__ float sv_block_max(float v, float *red) {
 //    token's V, quantised from v_new (workgroup j = 0 of each kv head also
 //    writes the cache row segment, kv head 0's the scale).
 //
-// Every workgroup of the grid is resident at once (one per CU at most, far
-// fewer than the CUs), so every poll ends; it is bounded all the same.  K is
-// read once per launch and V once per XCD that serves its kv head (with
-// xstride 8, every workgroup of a kv head sits on one XCD: the dispatcher
-// deals linear workgroup ids to the 8 XCDs in turn).
+// Every workgroup of the grid is resident at once (one per CU, at most 32
+// per XCD, which the launcher checks), so every poll ends; it is bounded all
+// the same.  K is read once per launch, and V once per XCD that serves one
+// of its kv head's query heads: a query head's workgroups, which together
+// read whole V lines, sit on one XCD, and the query heads are dealt to the
+// 8 XCDs in turn (so that the XCDs share the work evenly).
 //
 // q [n_heads][head_dim], k_cache and k_scales (this layer's [max_seq][kv_dim]
 // codes and [max_seq] scales), k_new (this token's K after RoPE, [kv_dim]
@@ -195,10 +196,14 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
     const uint32_t hd = (shape & 1u) ? 128u : 64u, segs = hd / 16;
     const uint32_t sc_tile = (shape >> 1) & 0x7FFu, nb = shape >> 12;
     const uint32_t gs = group * segs, kv_dim = n_kv_heads * hd;
-    // workgroup (g, j) has linear id j * xstride + g
-    const uint32_t xstride = n_kv_heads <= 8 ? 8u : n_kv_heads;
-    const uint32_t g = blockIdx.x % xstride, j = blockIdx.x / xstride;
-    if (g >= n_kv_heads) return;
+    // Query head qh's segs workgroups (its 16-dimension slices, which
+    // together read whole V lines) sit on one XCD, qh mod 8: the dispatcher
+    // deals linear ids to the 8 XCDs in turn, and qh = 8k + x takes the ids
+    // (k * segs + s) * 8 + x for its slices s.
+    const uint32_t x8 = blockIdx.x % 8, slot = blockIdx.x / 8;
+    const uint32_t qh = (slot / segs) * 8 + x8;
+    if (qh >= group * n_kv_heads) return;
+    const uint32_t g = qh / group, j = (qh % group) * segs + slot % segs;
     // The position count.  Phase 1's loads go out for the launch's count nb
     // before the device word is read (each read sits where it is needed, so
     // that the wait for it comes after them); where the word gives another
@@ -404,24 +409,9 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
 #pragma unroll
     for (int i = 0; i < MAXM; i++) sv[i] = __uint_as_float((uint32_t)sw[i]);
     if (tid < 32) exp_tab[tid] = exp_word;
-    // These arrays overlap phase 1's K rows, and a thread's own scores can
-    // all come from other workgroups while this one's chains still read them.
-    wm_sync_lds();
 #pragma unroll
-    for (int i = 0; i < MAXM; i++) {
-        const uint32_t p = tid + (uint32_t)i * kSvThreads;
-        if (p < n) m = wm_max_nonan(m, sv[i]);
-        // the cache row of position n - 1 is stale (this token's V is
-        // quantised below): only the rows before it are copied
-        if (p < pnew) {
-            vq[p] = make_int4(vr0[i], vr1[i], vr2[i], vr3[i]);
-            vsc[p] = ss[i];
-        }
-    }
-    // this token's V (position n - 1 is not in the cache yet)
-    if (tid < kSvDims)
-        reinterpret_cast<int8_t *>(vq + pnew)[tid] = kv_q(vnew, vabs);
-    if (tid == 0) vsc[pnew] = kv_scale(vabs);
+    for (int i = 0; i < MAXM; i++)
+        if (tid + (uint32_t)i * kSvThreads < n) m = wm_max_nonan(m, sv[i]);
     // softmax (attention.rs:45-73)
     // (the thread maxima are never NaN: a NaN score never wins above; a zero
     // maximum's sign, which the reduction order could change, does not reach
@@ -431,6 +421,24 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
     if (!isfinite(mx)) {  // every weight becomes 0 -> output stays 0
         if (tid < kSvDims) out[tid] = 0.0f;
     } else {
+        // The V slice and scales into LDS.  These arrays overlap phase 1's K
+        // rows: the barrier in sv_block_max is the first after which no
+        // chain of this workgroup still reads them (a thread's own scores
+        // can all come from other workgroups before its chains end).
+#pragma unroll
+        for (int i = 0; i < MAXM; i++) {
+            const uint32_t p = tid + (uint32_t)i * kSvThreads;
+            // the cache row of position n - 1 is stale (this token's V is
+            // quantised below): only the rows before it are copied
+            if (p < pnew) {
+                vq[p] = make_int4(vr0[i], vr1[i], vr2[i], vr3[i]);
+                vsc[p] = ss[i];
+            }
+        }
+        // this token's V (position n - 1 is not in the cache yet)
+        if (tid < kSvDims)
+            reinterpret_cast<int8_t *>(vq + pnew)[tid] = kv_q(vnew, vabs);
+        if (tid == 0) vsc[pnew] = kv_scale(vabs);
         // exp(v - max) (attention.rs:62), then the positions whose exp is not
         // exactly 0, compacted in position order: a zero exp adds nothing to
         // the sum (s + 0 = s for every s the sum can hold), its weight
@@ -620,10 +628,11 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
         n_kv_heads == 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 16 || tag == 0)
         return false;
     const uint32_t group = n_heads / n_kv_heads;
-    const uint32_t gs = group * head_dim / kSvDims;
-    // kv head g's workgroups at linear ids g, g + 8, g + 16, ... (at most 8
-    // kv heads): all on one XCD, which then fetches its K and V rows once
-    const uint32_t xstride = n_kv_heads <= 8 ? 8u : n_kv_heads;
+    // each query head's head_dim / 16 workgroups on one XCD, the heads dealt
+    // to the 8 XCDs in turn; every workgroup must be resident at once (one
+    // per CU, 32 CUs per XCD), since they wait for each other's scores
+    const uint32_t segs = head_dim / kSvDims, per_xcd = segs * ((n_heads + 7) / 8);
+    if (per_xcd > 32) return false;
     // positions per score tile: one chain per thread, one K segment per
     // thread, and the tile's dequantised K rows within 128 KiB of LDS
     const uint32_t pst = head_dim + 4;
@@ -639,7 +648,7 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
                           (size_t)2 * kSvDims * kSvStride * 4 + npad * 2;
     const size_t lds_sc = ((size_t)group * head_dim + (size_t)sc_tile * pst) * 4;
     const size_t lds = lds_sv > lds_sc ? lds_sv : lds_sc;
-    const dim3 grid(xstride * gs);
+    const dim3 grid(8 * per_xcd);
     if (nb <= 2 * kSvThreads)
         hipLaunchKernelGGL(k_attn_decode<2>, grid, dim3(kSvThreads), lds, s, q, k_cache, k_scales, k_new,
                            kv_absmax, pos_dev, geom, shape, a);
