@@ -24,8 +24,8 @@ namespace {
 // built with -amdgpu-kernarg-preload-count=16): six pointers, then
 //   geom  = group | n_kv_heads << 8 | kv_absmax_n << 16
 //   shape = (head_dim == 128) | sc_tile << 1 | nb << 12
-// where sc_tile is the positions per score tile (group * sc_tile <=
-// kSvThreads) and nb the position count the launch is sized for: n_past, or
+// where sc_tile is the positions per score tile (group * ceil(sc_tile / 64)
+// <= 16 waves) and nb the position count the launch is sized for: n_past, or
 // with pos_dev the count the host expects the device word to give.  The rest
 // is read from this struct once the first loads are out.
 struct attn_args {
@@ -296,9 +296,12 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
         const uint32_t sc_stride = a.score_stride, sc_tag = a.tag;
         const float sc_scale = a.scale;
         asm volatile("" ::"s"(sc_stride), "s"(sc_tag), "s"(sc_scale));
-        // one chain per (head, position): s = Σ_i q_h[i] * k_p[i] in order
-        if (tid < group * tp) {
-            const uint32_t hh = tid / tp, pl = tid % tp;
+        // one chain per (head, position): s = Σ_i q_h[i] * k_p[i] in order.
+        // Wave w takes head w % group and positions 64 (w / group) + lane:
+        // the chains spread over the SIMDs, and a wave's q reads are one
+        // address (group * ceil(sc_tile / 64) <= 16 waves).
+        const uint32_t hh = wid % group, pl = (wid / group) * 64 + lane;
+        if (pl < tp) {
             const float *kr = kdl + pl * pst, *qr = qs + hh * hd;
             // 16 terms per step (four float4 of k_p, four of q_h), the next
             // step's reads issued before this step's products and adds, into
@@ -633,10 +636,11 @@ bool wm_launch_attention(const float *q, const int8_t *k_cache, const float *k_s
     // per CU, 32 CUs per XCD), since they wait for each other's scores
     const uint32_t segs = head_dim / kSvDims, per_xcd = segs * ((n_heads + 7) / 8);
     if (per_xcd > 32) return false;
-    // positions per score tile: one chain per thread, one K segment per
-    // thread, and the tile's dequantised K rows within 128 KiB of LDS
+    // positions per score tile: each head's chains on waves of their own
+    // (64 positions a wave, 16 waves), one K segment per thread, and the
+    // tile's dequantised K rows within 128 KiB of LDS
     const uint32_t pst = head_dim + 4;
-    const uint32_t sc_tile = min(min((uint32_t)kSvThreads / group, (uint32_t)kSvThreads / (head_dim / 16)),
+    const uint32_t sc_tile = min(min(64u * (16u / group), (uint32_t)kSvThreads / (head_dim / 16)),
                                  (uint32_t)((128u * 1024u / 4u - group * head_dim) / pst));
     if (n_kv_heads > 255 || kv_absmax_n > 0xFFFFu) return false;
     const uint32_t geom = group | n_kv_heads << 8 | kv_absmax_n << 16;
