@@ -260,9 +260,10 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
         asm volatile("" : "+v"(kpart.m0), "+v"(kpart.m1));
         if (q_mine) reinterpret_cast<float4 *>(qs)[tid] = qv4;
         const float kabs = new_wave ? kv_absmax_finish(kpart, kv_absmax, kv_absmax_n) : 0.0f;
-        wm_sync_lds();
         // this thread's 16 values of k_p (read_into: q as f32 * scale; the
-        // new row through KVCache::append's codes), into the tile's rows
+        // new row through KVCache::append's codes), into the tile's rows (q
+        // and the rows are read after the barrier below; the rows of the
+        // tile before were last read before the barrier that ends it)
         if (mine) {
             float kd[16];
             if (is_new) {
