@@ -100,8 +100,10 @@ __device__ __forceinline__ void st_tagged(uint64_t *p, uint32_t tag, float v) {
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 // workgroup j of a kv head scores positions [p0_of(n, j, gs), p0_of(n, j + 1, gs))
+// (n <= 4096 and j <= gs <= 256: n * j fits 32 bits, so the division is a
+// 32-bit one, which the first loads' addresses wait for)
 __device__ __forceinline__ uint32_t p0_of(uint32_t n, uint32_t j, uint32_t gs) {
-    return (uint32_t)((uint64_t)n * j / gs);
+    return n * j / gs;
 }
 __device__ __forceinline__ uint64_t ld_tagged(const uint64_t *p) {
     return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -193,7 +195,7 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
     __shared__ wm::seq_block_scratch seq_scratch;
     __shared__ uint64_t exp_tab[32];
     const uint32_t group = geom & 0xFFu, n_kv_heads = (geom >> 8) & 0xFFu, kv_absmax_n = geom >> 16;
-    const uint32_t hd = (shape & 1u) ? 128u : 64u, segs = hd / 16;
+    const uint32_t hd = (shape & 1u) ? 128u : 64u, segs = hd / 16, segs_log2 = (shape & 1u) ? 3u : 2u;
     const uint32_t sc_tile = (shape >> 1) & 0x7FFu, nb = shape >> 12;
     const uint32_t gs = group * segs, kv_dim = n_kv_heads * hd;
     // Query head qh's segs workgroups (its 16-dimension slices, which
@@ -201,9 +203,9 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
     // deals linear ids to the 8 XCDs in turn, and qh = 8k + x takes the ids
     // (k * segs + s) * 8 + x for its slices s.
     const uint32_t x8 = blockIdx.x % 8, slot = blockIdx.x / 8;
-    const uint32_t qh = (slot / segs) * 8 + x8;
+    const uint32_t qh = (slot >> segs_log2) * 8 + x8;
     if (qh >= group * n_kv_heads) return;
-    const uint32_t g = qh / group, j = (qh % group) * segs + slot % segs;
+    const uint32_t g = qh / group, j = (qh % group) * segs + (slot & (segs - 1));
     // The position count.  Phase 1's loads go out for the launch's count nb
     // before the device word is read (each read sits where it is needed, so
     // that the wait for it comes after them); where the word gives another
@@ -212,7 +214,7 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
     const auto dev_count_differs = [&]() { return pos_dev && *pos_dev + 1 != n; };
     const uint32_t tid = threadIdx.x;
     const uint32_t wid = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6)), lane = tid & 63;
-    const uint32_t h = g * group + j / segs, d0 = (j % segs) * kSvDims;
+    const uint32_t h = qh, d0 = (slot & (segs - 1)) * kSvDims;
 
     uint64_t *const scores64 = reinterpret_cast<uint64_t *>(a.scores);
 
@@ -221,7 +223,7 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
     float *qs = sm;                               // [group][hd]
     float *kdl = sm + group * hd;                 // [sc_tile][pst] dequantised K rows
     const int8_t *kseg = k_cache + g * hd;
-    const uint32_t row = tid / segs, sg = tid % segs;  // this thread's K row segment
+    const uint32_t row = tid >> segs_log2, sg = tid & (segs - 1);  // this thread's K row segment
     for (bool settled = false; !settled;) {
     settled = true;
     const uint32_t p0 = p0_of(n, j, gs), p1 = p0_of(n, j + 1, gs);
@@ -248,7 +250,7 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
         float4 qv4;
         if (q_mine) qv4 = reinterpret_cast<const float4 *>(q + (uint64_t)g * group * hd)[tid];
         // (the wave holding the new row computes k_new's absmax: uniform)
-        const bool new_wave = pnew >= t0 && pnew < t0 + tp && (pnew - t0) * segs / 64 == wid;
+        const bool new_wave = pnew >= t0 && pnew < t0 + tp && ((pnew - t0) << segs_log2) / 64 == wid;
         kv_absmax_part kpart{0.0f, 0.0f};
         if (new_wave) kpart = kv_absmax_first(kv_absmax, kv_absmax_n);
         if (t0 == p0 && dev_count_differs()) {  // uniform: the whole workgroup starts again
