@@ -456,7 +456,14 @@ __global__ __launch_bounds__(kSvThreads) void k_attn_decode(const float *q, cons
 #pragma unroll
         for (int i = 0; i < MAXM; i++) {
             const uint32_t p = tid + (uint32_t)i * kSvThreads;
-            e[i] = p < n ? wm::expf_glibc(sv[i] - mx, exp_tab) : 0.0f;
+            // expf_glibc returns +0 below -0x1.9fe368p6 (its first branch), so
+            // only the lanes at or above it (or NaN) evaluate it, and a wave
+            // with none of them skips it (most exps underflow here)
+            const float x = sv[i] - mx;
+            const bool ev = p < n && !(x < -0x1.9fe368p6f);
+            e[i] = 0.0f;
+            if (__builtin_amdgcn_ballot_w64(ev))  // (uniform)
+                if (ev) e[i] = wm::expf_glibc(x, exp_tab);
             mask[i] = __builtin_amdgcn_ballot_w64(e[i] != 0.0f);
             if (lane == 0) wcnt[i * 16 + wid] = __builtin_popcountll(mask[i]);
         }

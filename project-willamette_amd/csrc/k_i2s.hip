@@ -455,8 +455,9 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
     // share of the elements, and whether it is all finite.
     bool nonfinite = false;
     if (nm.x_out && has_y) {
-        const uint32_t lo = (uint32_t)((uint64_t)n * blockIdx.x / gridDim.x);
-        const uint32_t hi = (uint32_t)((uint64_t)n * (blockIdx.x + 1) / gridDim.x);
+        // (n * gridDim.x fits 32 bits: the launcher rejects grids where not)
+        const uint32_t lo = n * blockIdx.x / gridDim.x;
+        const uint32_t hi = n * (blockIdx.x + 1) / gridDim.x;
 #pragma unroll
         for (int r = 0; r < NR; r++) {
             const uint32_t col = wm::quad_col(r, c0);
@@ -1191,6 +1192,8 @@ bool wm_launch_i2s_fused(int mode, const wm_i2s_desc *descs, const float *w_scal
         while (ks < 8 && acc * ks * 2 <= n_cus) ks *= 2;
     const uint32_t grid = acc * ks;
     if (grid >= 0xFFFFu) return false;
+    // (each workgroup's share of x_out is split in 32-bit arithmetic)
+    if ((uint64_t)n_chunks * I2S_CHUNK_COLS * grid >= (1ull << 32)) return false;
     const uint32_t units01 = (ue0 == 0xFFFFu ? ue0 : ue0 * ks) | (ue1 == 0xFFFFu ? ue1 : ue1 * ks) << 16;
     if (absmax) {  // two slots per workgroup of tensors 1 and 2
         uint32_t most = 0;
