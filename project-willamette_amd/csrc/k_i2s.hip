@@ -320,14 +320,6 @@ struct i2s_fused_args {
     uint32_t absmax_stride;  // tensor t's slots from absmax + (t - 1) * absmax_stride
 };
 
-// Scalar arguments read from the argument struct, pinned in SGPRs where
-// they are read (a load the compiler moved to the first use would stall
-// there instead of under the norm).
-template <class T>
-__device__ __forceinline__ T pin_sgpr(T v) {
-    asm volatile("" : "+s"(v));
-    return v;
-}
 
 // KS: lanes per row.  A unit's rows are then split over KS workgroups of
 // R = 64 / KS rows of each of its groups, and lane l of a wave computes row
@@ -420,17 +412,26 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
     asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
     const i2s_fused_args &ar =
         *reinterpret_cast<const i2s_fused_args *>(reinterpret_cast<const char *>(&a) + zero);
-    const wm_fused_norm nm = {nx, ny, pin_sgpr(ar.x_out), nw, pin_sgpr(ar.eps), pin_sgpr(ar.err_flag),
-                              pin_sgpr(ar.layer_tag), chunks_flags & FUSED_RELU2};
-    const float ws0 = pin_sgpr(ar.w_scale[0]), w_scale1 = pin_sgpr(ar.w_scale[1]), ws2 = pin_sgpr(ar.w_scale[2]);
-    float *const o0 = pin_sgpr(ar.out[0]), *const o1 = pin_sgpr(ar.out[1]), *const o2 = pin_sgpr(ar.out[2]);
+    float *x_out = ar.x_out, eps = ar.eps;
+    uint32_t *err_flag = ar.err_flag, layer_tag = ar.layer_tag;
+    float ws0 = ar.w_scale[0], w_scale1 = ar.w_scale[1], ws2 = ar.w_scale[2];
+    float *o0 = ar.out[0], *o1 = ar.out[1], *o2 = ar.out[2];
+    const float *rope_cos = ar.rope_cos, *rope_sin = ar.rope_sin;
+    uint32_t pos_arg = ar.pos, n_rot = ar.n_rot, rope_mask = ar.rope_mask;
+    const uint32_t *pos_dev = ar.pos_dev;
+    uint32_t *absmax = ar.absmax;
+    uint32_t absmax_stride = ar.absmax_stride;
+    // Pinned in SGPRs here (a load the compiler moved to the first use would
+    // stall there instead of under the norm), all by one asm: the loads go
+    // out together and meet one wait (an asm per value made a chain of round
+    // trips, each load issued after the previous value's wait).
+    asm volatile(""
+                 : "+s"(x_out), "+s"(eps), "+s"(err_flag), "+s"(layer_tag), "+s"(ws0), "+s"(w_scale1), "+s"(ws2),
+                   "+s"(o0), "+s"(o1), "+s"(o2), "+s"(rope_cos), "+s"(rope_sin), "+s"(pos_arg), "+s"(n_rot),
+                   "+s"(rope_mask), "+s"(pos_dev), "+s"(absmax), "+s"(absmax_stride));
+    const wm_fused_norm nm = {nx, ny, x_out, nw, eps, err_flag, layer_tag, chunks_flags & FUSED_RELU2};
     const float w_scale = t == 2 ? ws2 : (t == 1 ? w_scale1 : ws0);
     float *const out_t = t == 2 ? o2 : (t == 1 ? o1 : o0);
-    const float *rope_cos = pin_sgpr(ar.rope_cos), *rope_sin = pin_sgpr(ar.rope_sin);
-    const uint32_t pos_arg = pin_sgpr(ar.pos), n_rot = pin_sgpr(ar.n_rot), rope_mask = pin_sgpr(ar.rope_mask);
-    const uint32_t *pos_dev = pin_sgpr(ar.pos_dev);
-    uint32_t *absmax = pin_sgpr(ar.absmax);
-    const uint32_t absmax_stride = pin_sgpr(ar.absmax_stride);
     // the epilogue's RoPE factors
     const uint32_t half = n_rot / 2;  // ROPE: at most 64 <= W * 64 pairs, one per thread
     // this workgroup's pairs: all of the head's (KS = 1), else R, the pairs
