@@ -459,18 +459,28 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
         // (n * gridDim.x fits 32 bits: the launcher rejects grids where not)
         const uint32_t lo = n * blockIdx.x / gridDim.x;
         const uint32_t hi = n * (blockIdx.x + 1) / gridDim.x;
+        // the sums first, then the stores through a global pointer: a store
+        // between two of them made the next wait for the inputs also wait
+        // for that store (a flat store counts with the loads)
+        float xs[NR][4];
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) xs[r][i] = Q.v[r][i] + yq[r][i];
+            // (formed here, not sunk into the stores' branches below)
+            asm volatile("" : "+v"(xs[r][0]), "+v"(xs[r][1]), "+v"(xs[r][2]), "+v"(xs[r][3]));
+        }
+        __attribute__((address_space(1))) float *const xo = (__attribute__((address_space(1))) float *)nm.x_out;
 #pragma unroll
         for (int r = 0; r < NR; r++) {
             const uint32_t col = wm::quad_col(r, c0);
             if (Q.valid(r, c0, nc) && col + 4 > lo && col < hi)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float v = Q.v[r][i] + yq[r][i];
+                for (int i = 0; i < 4; i++)
                     if (col + i >= lo && col + i < hi) {
-                        nm.x_out[col + i] = v;
-                        nonfinite |= !isfinite(v);
+                        xo[col + i] = xs[r][i];
+                        nonfinite |= !isfinite(xs[r][i]);
                     }
-                }
         }
     }
     // the squares to LDS in column order: the exact sum's terms (also read
