@@ -440,9 +440,13 @@ __global__ __launch_bounds__(W * 64) void k_i2s_fused(const float *nx, const flo
     const bool rope = MODE == WM_FUSED_ROPE && ((rope_mask >> t) & 1u);
     float rc = 0.0f, rsn = 0.0f;
     if (rope && threadIdx.x < n_pairs) {
-        const uint32_t pos = pos_dev ? *pos_dev : pos_arg;
-        rc = rope_cos[(uint64_t)pos * half + pair0 + threadIdx.x];
-        rsn = rope_sin[(uint64_t)pos * half + pair0 + threadIdx.x];
+        // (through global pointers: a flat load would also count with the
+        // LDS operations, and the norm's barriers would wait for it)
+        using gu32 = __attribute__((address_space(1))) const uint32_t;
+        using gf32 = __attribute__((address_space(1))) const float;
+        const uint32_t pos = pos_dev ? *(gu32 *)pos_dev : pos_arg;
+        rc = ((gf32 *)rope_cos)[(uint64_t)pos * half + pair0 + threadIdx.x];
+        rsn = ((gf32 *)rope_sin)[(uint64_t)pos * half + pair0 + threadIdx.x];
     }
     // x + y (hidden += the producing matvec's output), or with relu2
     // relu(x)^2 * y (the FFN's gate x and up y, ffn.rs:37-65), the same f32
