@@ -20,10 +20,13 @@ const FLAGS: &[&str] = &[
 ];
 
 /// Extra flags of single sources (as PER_FILE in build.py): the batched GEMM
-/// keeps its MFMA accumulators in VGPRs.
+/// keeps its MFMA accumulators in VGPRs; the fused matvecs and decode
+/// attention take what their first loads need in their leading 16 argument
+/// dwords, preloaded into SGPRs at wave launch.
 fn per_file(name: &str) -> &'static [&'static str] {
     match name {
         "k_batch.hip" => &["-mllvm", "-amdgpu-mfma-vgpr-form"],
+        "k_i2s.hip" | "k_attn.hip" => &["-mllvm", "-amdgpu-kernarg-preload-count=16"],
         _ => &[],
     }
 }
